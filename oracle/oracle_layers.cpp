@@ -1,0 +1,539 @@
+// oracle_layers.cpp - the verify step's layers on the CPU: the dense SwiGLU MLP, the MoE block, gated attention with
+// the causal chain or a draft tree, and the whole forward pass of a batch (verify_n / verify_keep).
+//
+// TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the HIP path, never part of it.
+//
+// Pinning (tests/test_oracle_layers.py): the reference's Model does not build without a real pack, so these
+// compositions are pinned by reduction to the pinned primitives (oracle_core.cpp) plus invariants the reference
+// states: verify logits equal one-token-at-a-time logits bit for bit (model.hpp:189-193); attention bits do not
+// depend on the block size up to the merge (model.cpp:3799-3804) and equal a float64 softmax within fp32 rounding;
+// a tree row equals the chain over its ancestors; verify + keep equals a verify of the kept prefix. The MoE block is
+// checked against a brute-force restatement (every expert computed densely, the unpicked ones weighted 0).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <vector>
+
+#include "oracle.h"
+#include "oracle_internal.hpp"
+
+namespace orc {
+
+namespace {
+
+std::vector<float *> row_ptrs(float *base, int n, size_t stride) {
+    std::vector<float *> v(static_cast<size_t>(n));
+    for (int t = 0; t < n; ++t) v[static_cast<size_t>(t)] = base + static_cast<size_t>(t) * stride;
+    return v;
+}
+std::vector<const float *> crow_ptrs(const float *base, int n, size_t stride) {
+    std::vector<const float *> v(static_cast<size_t>(n));
+    for (int t = 0; t < n; ++t) v[static_cast<size_t>(t)] = base + static_cast<size_t>(t) * stride;
+    return v;
+}
+
+// down(silu(gate h) * up h) for n tokens, gate and up separate matrices (the shared expert, model.cpp:4279-4296;
+// the dense MLP, :4126-4146)
+void swiglu_mlp(const uint8_t *gate, const uint8_t *up, const uint8_t *down, float gg, float gu, float gd, int H, int F,
+                int n, const float *h, int mode, float *out) {
+    std::vector<float> g(static_cast<size_t>(n) * F), u(static_cast<size_t>(n) * F);
+    const auto hs = crow_ptrs(h, n, static_cast<size_t>(H));
+    auto gs = row_ptrs(g.data(), n, static_cast<size_t>(F));
+    auto us = row_ptrs(u.data(), n, static_cast<size_t>(F));
+    matmul(gate, F, H, gg, n, hs.data(), gs.data(), mode);
+    matmul(up, F, H, gu, n, hs.data(), us.data(), mode);
+    for (size_t i = 0; i < g.size(); ++i) g[i] = silu(g[i]) * u[i];
+    const auto ms = crow_ptrs(g.data(), n, static_cast<size_t>(F));
+    auto os = row_ptrs(out, n, static_cast<size_t>(H));
+    matmul(down, H, F, gd, n, ms.data(), os.data(), mode);
+}
+
+}  // namespace
+
+// The MoE block of model.cpp:4123-4587 for n tokens (no residual). Each pick is computed whole, as one expert alone
+// (every path of the reference gives these bits, model.cpp:4305-4308): gate_up h, silu(gate) * up, down.
+void moe_layer(const orc_moe_weights &w, int n, const float *h, const float *router_logits, int mode, float *out,
+               int *ids_out, float *wts_out, float *gate_out) {
+    const int H = w.H, E = w.E, K = w.K, F = w.F;
+    std::vector<float> logits(static_cast<size_t>(n) * E);
+    if (router_logits) {
+        std::copy(router_logits, router_logits + static_cast<size_t>(n) * E, logits.begin());
+    } else {
+        const auto hs = crow_ptrs(h, n, static_cast<size_t>(H));
+        auto ls = row_ptrs(logits.data(), n, static_cast<size_t>(E));
+        par(E, 16, [&](int64_t a, int64_t b) { bf16_rows(w.router, H, n, hs.data(), ls.data(), a, b); });
+    }
+    std::vector<int> ids(static_cast<size_t>(n) * K);
+    std::vector<float> wts(static_cast<size_t>(n) * K);
+    for (int t = 0; t < n; ++t)
+        route_topk(logits.data() + static_cast<size_t>(t) * E, E, K, ids.data() + static_cast<size_t>(t) * K,
+                   wts.data() + static_cast<size_t>(t) * K);
+    const size_t gu_bytes = static_cast<size_t>(2 * F) * q4_row_bytes(H);
+    const size_t blk_bytes = gu_bytes + static_cast<size_t>(H) * q4_row_bytes(F);
+    std::vector<float> eout(static_cast<size_t>(n) * K * H);
+    std::vector<float> ga(static_cast<size_t>(2 * F));
+    for (int t = 0; t < n; ++t)
+        for (int k = 0; k < K; ++k) {
+            const int e = ids[static_cast<size_t>(t * K + k)];
+            const uint8_t *blk = w.experts + static_cast<size_t>(e) * blk_bytes;
+            const float *ht = h + static_cast<size_t>(t) * H;
+            float *gp = ga.data();
+            matmul(blk, 2 * F, H, w.expert_globals[2 * e], 1, &ht, &gp, mode);   // [gate F | up F]
+            for (int i = 0; i < F; ++i) ga[static_cast<size_t>(i)] = silu(ga[static_cast<size_t>(i)]) * ga[static_cast<size_t>(F + i)];
+            const float *mp = ga.data();
+            float *yp = eout.data() + (static_cast<size_t>(t) * K + static_cast<size_t>(k)) * H;
+            matmul(blk + gu_bytes, H, F, w.expert_globals[2 * e + 1], 1, &mp, &yp, mode);
+        }
+    std::vector<float> sh(static_cast<size_t>(n) * H);
+    swiglu_mlp(w.sh_gate, w.sh_up, w.sh_down, w.sh_globals[0], w.sh_globals[1], w.sh_globals[2], H, w.SF, n, h, mode,
+               sh.data());
+    // per token: sigmoid(bf16 gate . h) times the shared expert, then the routed outputs in rank order
+    for (int t = 0; t < n; ++t) {
+        const float *ht = h + static_cast<size_t>(t) * H;
+        float gs = 0.0f;
+        for (int i = 0; i < H; ++i) gs += bf16_to_f32(w.shared_gate[i]) * ht[i];
+        gs = sigmoid(gs);
+        if (gate_out) gate_out[t] = gs;
+        float *o = out + static_cast<size_t>(t) * H;
+        const float *shv = sh.data() + static_cast<size_t>(t) * H;
+        for (int i = 0; i < H; ++i) o[i] = gs * shv[i];
+        for (int k = 0; k < K; ++k) {
+            const float wk = wts[static_cast<size_t>(t * K + k)];
+            if (wk == 0.0f) continue;
+            const float *y = eout.data() + (static_cast<size_t>(t) * K + static_cast<size_t>(k)) * H;
+            for (int i = 0; i < H; ++i) o[i] += wk * y[i];
+        }
+    }
+    if (ids_out) std::copy(ids.begin(), ids.end(), ids_out);
+    if (wts_out) std::copy(wts.begin(), wts.end(), wts_out);
+}
+
+// ---------------------------------------------------------------- the model
+struct Layer {
+    std::vector<float> in_norm, post_norm, q_norm, k_norm;
+    std::vector<uint8_t> q, k, v, o, experts, sh_gate, sh_up, sh_down;
+    float gq = 1, gk = 1, gv = 1, go = 1, gsg = 1, gsu = 1, gsd = 1;
+    std::vector<float> expert_globals;   // [E][2]
+    std::vector<uint16_t> router, shared_gate, kv;   // kv: [2][max_ctx][nkv * hd] fp16
+};
+
+}  // namespace orc
+
+struct orc_model {
+    orc_config c{};
+    std::vector<uint8_t> embed, lm_head;
+    float g_embed = 1, g_lm = 1;
+    std::vector<float> final_norm, inv_freq;
+    std::vector<orc::Layer> layers;
+    int pos = 0, last_n = 0, last_pos = 0;
+    double t_layers = 0, t_head = 0;
+};
+
+namespace orc {
+namespace {
+
+size_t expert_block_bytes(const orc_config &c) {   // pack.cpp:329-333
+    return static_cast<size_t>(2 * c.moe_ff) * q4_row_bytes(c.hidden) +
+           static_cast<size_t>(c.hidden) * q4_row_bytes(c.moe_ff);
+}
+
+// depth of each row of a draft tree (chain when parents is null)
+std::vector<int> depths(const int32_t *parents, int n) {
+    std::vector<int> d(static_cast<size_t>(n), 0);
+    for (int i = 0; i < n; ++i) d[static_cast<size_t>(i)] = parents ? (parents[i] < 0 ? 0 : d[static_cast<size_t>(parents[i])] + 1) : i;
+    return d;
+}
+
+// visible[i][j]: row j is row i or one of its ancestors (chain: j <= i)
+std::vector<char> ancestry(const int32_t *parents, int n) {
+    std::vector<char> a(static_cast<size_t>(n) * n, 0);
+    for (int i = 0; i < n; ++i) {
+        if (!parents) {
+            for (int j = 0; j <= i; ++j) a[static_cast<size_t>(i) * n + j] = 1;
+            continue;
+        }
+        for (int j = i; j >= 0; j = parents[j]) a[static_cast<size_t>(i) * n + j] = 1;
+    }
+    return a;
+}
+
+// Model::attention + attend + attend_heads (model.cpp:3690-4019) for the n rows at slots pos.., rotary positions
+// pos + depth. KV in fp16 (attend<_Float16>). h: the in-norm's output; mix: o_proj's.
+void attention(const orc_model &m, Layer &L, int n, const float *h, int pos, const int32_t *parents, int mode,
+               float *mix) {
+    const auto &c = m.c;
+    const int H = c.hidden, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim, half = c.rope_dim / 2;
+    const size_t kv_row = static_cast<size_t>(nkv) * hd, qw = static_cast<size_t>(nh) * 2 * hd;
+    std::vector<float> qs(static_cast<size_t>(n) * qw), ks(static_cast<size_t>(n) * kv_row),
+        vs(static_cast<size_t>(n) * kv_row);
+    const auto hs = crow_ptrs(h, n, static_cast<size_t>(H));
+    {
+        auto qp = row_ptrs(qs.data(), n, qw);
+        auto kp = row_ptrs(ks.data(), n, kv_row);
+        auto vp = row_ptrs(vs.data(), n, kv_row);
+        matmul(L.q.data(), static_cast<int64_t>(qw), H, L.gq, n, hs.data(), qp.data(), mode);
+        matmul(L.k.data(), static_cast<int64_t>(kv_row), H, L.gk, n, hs.data(), kp.data(), mode);
+        matmul(L.v.data(), static_cast<int64_t>(kv_row), H, L.gv, n, hs.data(), vp.data(), mode);
+    }
+    const std::vector<int> dep = depths(parents, n);
+    std::vector<float> cosv(static_cast<size_t>(half)), sinv(static_cast<size_t>(half));
+    auto rope = [&](float *x) {
+        for (int i = 0; i < half; ++i) {
+            const float x1 = x[i], x2 = x[i + half];
+            x[i] = x1 * cosv[static_cast<size_t>(i)] - x2 * sinv[static_cast<size_t>(i)];
+            x[i + half] = x2 * cosv[static_cast<size_t>(i)] + x1 * sinv[static_cast<size_t>(i)];
+        }
+    };
+    for (int t = 0; t < n; ++t) {
+        const int p = pos + dep[static_cast<size_t>(t)];   // text: the three M-RoPE streams are one (model.cpp:1746-1760)
+        for (int i = 0; i < half; ++i) {
+            const float f = static_cast<float>(p) * m.inv_freq[static_cast<size_t>(i)];
+            cosv[static_cast<size_t>(i)] = std::cos(f);
+            sinv[static_cast<size_t>(i)] = std::sin(f);
+        }
+        for (int hh = 0; hh < nh; ++hh) {
+            float *q = qs.data() + static_cast<size_t>(t) * qw + static_cast<size_t>(hh) * 2 * hd;
+            rmsnorm(q, L.q_norm.data(), q, hd, c.eps, true);
+            rope(q);
+        }
+        for (int kh = 0; kh < nkv; ++kh) {
+            float *k = ks.data() + static_cast<size_t>(t) * kv_row + static_cast<size_t>(kh) * hd;
+            rmsnorm(k, L.k_norm.data(), k, hd, c.eps, true);
+            rope(k);
+        }
+    }
+    uint16_t *K = L.kv.data(), *V = L.kv.data() + static_cast<size_t>(c.max_ctx) * kv_row;
+    for (int t = 0; t < n; ++t)
+        for (size_t i = 0; i < kv_row; ++i) {
+            K[static_cast<size_t>(pos + t) * kv_row + i] = f32_to_f16(ks[static_cast<size_t>(t) * kv_row + i]);
+            V[static_cast<size_t>(pos + t) * kv_row + i] = f32_to_f16(vs[static_cast<size_t>(t) * kv_row + i]);
+        }
+    const std::vector<char> vis = ancestry(parents, n);
+    const int group = nh / nkv, blk = c.attn_block;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    std::vector<float> core(static_cast<size_t>(n) * nh * hd);
+    par(static_cast<int64_t>(n) * nh, 1, [&](int64_t i0, int64_t i1) {
+        std::vector<float> sc, part, o(static_cast<size_t>(hd));
+        std::vector<int> slots;
+        for (int64_t it = i0; it < i1; ++it) {
+            const int t = static_cast<int>(it / nh), hh = static_cast<int>(it % nh), kh = hh / group;
+            const float *q = qs.data() + static_cast<size_t>(t) * qw + static_cast<size_t>(hh) * 2 * hd;
+            const float *gate = q + hd;
+            const int last = pos + t;
+            const int nb = last / blk + 1;
+            part.assign(static_cast<size_t>(nb) * (hd + 2), 0.0f);
+            for (int b = 0; b < nb; ++b) {
+                slots.clear();
+                for (int s = b * blk; s < std::min(last + 1, (b + 1) * blk); ++s)
+                    if (s < pos || vis[static_cast<size_t>(t) * n + (s - pos)]) slots.push_back(s);
+                float mx = -std::numeric_limits<float>::infinity();
+                sc.resize(slots.size());
+                for (size_t p = 0; p < slots.size(); ++p) {
+                    const uint16_t *k = K + static_cast<size_t>(slots[p]) * kv_row + static_cast<size_t>(kh) * hd;
+                    float acc[8] = {};
+                    for (int i = 0; i < hd; i += 8)
+                        for (int j = 0; j < 8; ++j) acc[j] += q[i + j] * f16_to_f32(k[i + j]);
+                    const float dot = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+                    const float sv = dot * scale;
+                    sc[p] = sv;
+                    mx = std::max(mx, sv);
+                }
+                float sum = 0.0f;
+                for (size_t p = 0; p < slots.size(); ++p) {
+                    sc[p] = std::exp(sc[p] - mx);
+                    sum += sc[p];
+                }
+                float *dst = part.data() + static_cast<size_t>(b) * (hd + 2);
+                dst[hd] = mx;
+                dst[hd + 1] = sum;
+                for (int i = 0; i < hd; i += 8) {
+                    float acc[8] = {};
+                    for (size_t p = 0; p < slots.size(); ++p) {
+                        const uint16_t *v = V + static_cast<size_t>(slots[p]) * kv_row + static_cast<size_t>(kh) * hd + i;
+                        for (int j = 0; j < 8; ++j) acc[j] += sc[p] * f16_to_f32(v[j]);
+                    }
+                    std::memcpy(dst + i, acc, sizeof acc);
+                }
+            }
+            float sum = part[static_cast<size_t>(hd) + 1];
+            if (nb == 1) {
+                std::copy(part.begin(), part.begin() + hd, o.begin());
+            } else {
+                float mx = -std::numeric_limits<float>::infinity();
+                for (int b = 0; b < nb; ++b) mx = std::max(mx, part[static_cast<size_t>(b) * (hd + 2) + hd]);
+                std::fill(o.begin(), o.end(), 0.0f);
+                sum = 0.0f;
+                for (int b = 0; b < nb; ++b) {
+                    const float *pp = part.data() + static_cast<size_t>(b) * (hd + 2);
+                    const float f = std::exp(pp[hd] - mx);
+                    sum += pp[hd + 1] * f;
+                    for (int j = 0; j < hd; ++j) o[static_cast<size_t>(j)] += pp[j] * f;
+                }
+            }
+            const float inv = 1.0f / sum;
+            float *out = core.data() + (static_cast<size_t>(t) * nh + hh) * hd;
+            for (int j = 0; j < hd; ++j) out[j] = o[static_cast<size_t>(j)] * inv * sigmoid(gate[j]);
+        }
+    });
+    const auto cr = crow_ptrs(core.data(), n, static_cast<size_t>(nh) * hd);
+    auto ms = row_ptrs(mix, n, static_cast<size_t>(H));
+    matmul(L.o.data(), H, static_cast<int64_t>(nh) * hd, L.go, n, cr.data(), ms.data(), mode);
+}
+
+orc_moe_weights moe_view(const orc_model &m, const Layer &L) {
+    orc_moe_weights w{};
+    w.H = m.c.hidden, w.E = m.c.n_experts, w.K = m.c.top_k, w.F = m.c.moe_ff, w.SF = m.c.shared_ff;
+    w.experts = L.experts.data();
+    w.expert_globals = L.expert_globals.data();
+    w.sh_gate = L.sh_gate.data(), w.sh_up = L.sh_up.data(), w.sh_down = L.sh_down.data();
+    w.sh_globals[0] = L.gsg, w.sh_globals[1] = L.gsu, w.sh_globals[2] = L.gsd;
+    w.shared_gate = L.shared_gate.data();
+    w.router = L.router.data();
+    return w;
+}
+
+uint64_t tensor_seed(uint64_t seed, int kind, int layer, int expert) {
+    return orc_hash(seed, (static_cast<uint64_t>(kind) << 48) | (static_cast<uint64_t>(layer) << 24) |
+                              static_cast<uint64_t>(expert));
+}
+
+float fill_q4(std::vector<uint8_t> &dst, int64_t rows, int64_t cols, uint64_t seed, float sigma, int fast) {
+    dst.resize(static_cast<size_t>(rows) * q4_row_bytes(cols));
+    if (fast) {
+        const int64_t nb = cols / 16;
+        const size_t rb = q4_row_bytes(cols);
+        par(rows, 64, [&](int64_t a, int64_t b) {
+            for (int64_t r = a; r < b; ++r) {
+                uint8_t *row = dst.data() + static_cast<size_t>(r) * rb;
+                for (int64_t i = 0; i < nb * 8; ++i) row[i] = static_cast<uint8_t>(orc_hash(seed, static_cast<uint64_t>(r * rb + i)));
+                for (int64_t i = 0; i < nb; ++i)
+                    row[nb * 8 + i] = static_cast<uint8_t>(0x30 + orc_hash(seed ^ 1, static_cast<uint64_t>(r * nb + i)) % 25);
+            }
+        });
+        return 1.0f / 448.0f;
+    }
+    std::vector<float> w(static_cast<size_t>(rows) * cols);
+    orc_fill_normal(seed, static_cast<int64_t>(w.size()), 0.0f, sigma, w.data());
+    const float s2 = orc_q4_global(w.data(), static_cast<int64_t>(w.size()));
+    orc_q4_pack(w.data(), rows, cols, s2, dst.data());
+    return s2;
+}
+
+void fill_f32(std::vector<float> &dst, size_t n, uint64_t seed, float sigma) {
+    dst.resize(n);
+    orc_fill_normal(seed, static_cast<int64_t>(n), 0.0f, sigma, dst.data());
+}
+
+void fill_bf16(std::vector<uint16_t> &dst, size_t n, uint64_t seed, float sigma) {
+    std::vector<float> f(n);
+    orc_fill_normal(seed, static_cast<int64_t>(n), 0.0f, sigma, f.data());
+    dst.resize(n);
+    for (size_t i = 0; i < n; ++i) dst[i] = f32_to_bf16(f[i]);
+}
+
+}  // namespace
+}  // namespace orc
+
+using namespace orc;
+
+extern "C" {
+
+void orc_ffn_swiglu(const uint8_t *gate, const uint8_t *up, const uint8_t *down, float g_gate, float g_up,
+                    float g_down, int H, int F, int M, const uint16_t *x_f16, int mode, float *y) {
+    std::vector<float> x(static_cast<size_t>(M) * H);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = f16_to_f32(x_f16[i]);
+    swiglu_mlp(gate, up, down, g_gate, g_up, g_down, H, F, M, x.data(), mode, y);
+}
+
+void orc_moe_layer(const orc_moe_weights *w, int M, const float *h, const float *router_logits, int mode, float *out,
+                   int *ids, float *wts, float *gate) {
+    moe_layer(*w, M, h, router_logits, mode, out, ids, wts, gate);
+}
+
+orc_model *orc_model_create(const orc_config *cfg) {
+    auto m = std::make_unique<orc_model>();
+    m->c = *cfg;
+    if (m->c.attn_block <= 0) m->c.attn_block = 1024;
+    const auto &c = m->c;
+    const int half = c.rope_dim / 2;
+    m->inv_freq.resize(static_cast<size_t>(half));
+    for (int i = 0; i < half; ++i)   // model.cpp:739-740
+        m->inv_freq[static_cast<size_t>(i)] =
+            1.0f / std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(c.rope_dim));
+    m->layers.resize(static_cast<size_t>(c.n_layers));
+    return m.release();
+}
+
+void orc_model_free(orc_model *m) { delete m; }
+
+void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma, int ctx, int fast) {
+    const auto &c = m->c;
+    const int H = c.hidden, E = c.n_experts, F = c.moe_ff, SF = c.shared_ff, nh = c.n_heads, nkv = c.n_kv_heads,
+              hd = c.head_dim;
+    m->g_embed = fill_q4(m->embed, c.vocab, H, tensor_seed(seed, ORC_EMBED, 0, 0), sigma, fast);
+    m->g_lm = fill_q4(m->lm_head, c.vocab, H, tensor_seed(seed, ORC_LM_HEAD, 0, 0), sigma, fast);
+    fill_f32(m->final_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_FINAL_NORM, 0, 0), 0.02f);
+    const size_t kv_row = static_cast<size_t>(nkv) * hd;
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer &L = m->layers[static_cast<size_t>(l)];
+        fill_f32(L.in_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_IN_NORM, l, 0), 0.02f);
+        fill_f32(L.post_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_POST_NORM, l, 0), 0.02f);
+        fill_f32(L.q_norm, static_cast<size_t>(hd), tensor_seed(seed, ORC_Q_NORM, l, 0), 0.02f);
+        fill_f32(L.k_norm, static_cast<size_t>(hd), tensor_seed(seed, ORC_K_NORM, l, 0), 0.02f);
+        L.gq = fill_q4(L.q, static_cast<int64_t>(nh) * 2 * hd, H, tensor_seed(seed, ORC_Q, l, 0), sigma, fast);
+        L.gk = fill_q4(L.k, static_cast<int64_t>(kv_row), H, tensor_seed(seed, ORC_K, l, 0), sigma, fast);
+        L.gv = fill_q4(L.v, static_cast<int64_t>(kv_row), H, tensor_seed(seed, ORC_V, l, 0), sigma, fast);
+        L.go = fill_q4(L.o, H, static_cast<int64_t>(nh) * hd, tensor_seed(seed, ORC_O, l, 0), sigma, fast);
+        fill_bf16(L.router, static_cast<size_t>(E) * H, tensor_seed(seed, ORC_ROUTER, l, 0), router_sigma);
+        fill_bf16(L.shared_gate, static_cast<size_t>(H), tensor_seed(seed, ORC_SHARED_GATE, l, 0), sigma);
+        const size_t eb = expert_block_bytes(c), gu = static_cast<size_t>(2 * F) * q4_row_bytes(H);
+        L.experts.resize(eb * static_cast<size_t>(E));
+        L.expert_globals.resize(static_cast<size_t>(2 * E));
+        std::vector<uint8_t> tmp;
+        for (int e = 0; e < E; ++e) {
+            L.expert_globals[static_cast<size_t>(2 * e)] =
+                fill_q4(tmp, 2 * F, H, tensor_seed(seed, ORC_EXPERT, l, 2 * e), sigma, fast);
+            std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e));
+            L.expert_globals[static_cast<size_t>(2 * e + 1)] =
+                fill_q4(tmp, H, F, tensor_seed(seed, ORC_EXPERT, l, 2 * e + 1), sigma, fast);
+            std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e + gu));
+        }
+        L.gsg = fill_q4(L.sh_gate, SF, H, tensor_seed(seed, ORC_SH_GATE, l, 0), sigma, fast);
+        L.gsu = fill_q4(L.sh_up, SF, H, tensor_seed(seed, ORC_SH_UP, l, 0), sigma, fast);
+        L.gsd = fill_q4(L.sh_down, H, SF, tensor_seed(seed, ORC_SH_DOWN, l, 0), sigma, fast);
+        L.kv.assign(2 * static_cast<size_t>(c.max_ctx) * kv_row, 0);
+        if (ctx > 0) {
+            std::vector<float> f(static_cast<size_t>(ctx) * kv_row);
+            for (int kvi = 0; kvi < 2; ++kvi) {
+                orc_fill_normal(tensor_seed(seed, ORC_KV, l, kvi), static_cast<int64_t>(f.size()), 0.0f, 1.0f, f.data());
+                uint16_t *dst = L.kv.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
+                for (size_t i = 0; i < f.size(); ++i) dst[i] = f32_to_f16(f[i]);
+            }
+        }
+    }
+    m->pos = ctx;
+}
+
+uint8_t *orc_model_tensor(orc_model *m, int kind, int layer, int expert, int64_t *bytes, float *globals) {
+    auto ret = [&](auto &vec, float g0, float g1) -> uint8_t * {
+        if (bytes) *bytes = static_cast<int64_t>(vec.size() * sizeof(vec[0]));
+        if (globals) globals[0] = g0, globals[1] = g1;
+        return reinterpret_cast<uint8_t *>(vec.data());
+    };
+    if (kind == ORC_EMBED) return ret(m->embed, m->g_embed, 0);
+    if (kind == ORC_LM_HEAD) return ret(m->lm_head, m->g_lm, 0);
+    if (kind == ORC_FINAL_NORM) return ret(m->final_norm, 0, 0);
+    if (layer < 0 || layer >= m->c.n_layers) return nullptr;
+    Layer &L = m->layers[static_cast<size_t>(layer)];
+    switch (kind) {
+    case ORC_IN_NORM: return ret(L.in_norm, 0, 0);
+    case ORC_POST_NORM: return ret(L.post_norm, 0, 0);
+    case ORC_Q: return ret(L.q, L.gq, 0);
+    case ORC_K: return ret(L.k, L.gk, 0);
+    case ORC_V: return ret(L.v, L.gv, 0);
+    case ORC_O: return ret(L.o, L.go, 0);
+    case ORC_Q_NORM: return ret(L.q_norm, 0, 0);
+    case ORC_K_NORM: return ret(L.k_norm, 0, 0);
+    case ORC_ROUTER: return ret(L.router, 0, 0);
+    case ORC_SHARED_GATE: return ret(L.shared_gate, 0, 0);
+    case ORC_SH_GATE: return ret(L.sh_gate, L.gsg, 0);
+    case ORC_SH_UP: return ret(L.sh_up, L.gsu, 0);
+    case ORC_SH_DOWN: return ret(L.sh_down, L.gsd, 0);
+    case ORC_KV: return ret(L.kv, 0, 0);
+    case ORC_EXPERT: {
+        if (expert < 0 || expert >= m->c.n_experts) return nullptr;
+        const size_t eb = expert_block_bytes(m->c);
+        if (bytes) *bytes = static_cast<int64_t>(eb);
+        if (globals)
+            globals[0] = L.expert_globals[static_cast<size_t>(2 * expert)],
+            globals[1] = L.expert_globals[static_cast<size_t>(2 * expert + 1)];
+        return L.experts.data() + eb * static_cast<size_t>(expert);
+    }
+    default: return nullptr;
+    }
+}
+
+void orc_model_set_position(orc_model *m, int pos) { m->pos = pos; }
+int orc_model_position(const orc_model *m) { return m->pos; }
+
+int orc_model_verify(orc_model *m, const int32_t *tokens, int n, const int32_t *parents, int mode, float *logits,
+                     int32_t *route_ids) {
+    const auto &c = m->c;
+    const int H = c.hidden;
+    if (n <= 0 || m->pos + n > c.max_ctx) return -1;
+    for (int t = 0; t < n; ++t)
+        if (tokens[t] < 0 || tokens[t] >= c.vocab) return -1;
+    if (parents) {
+        if (parents[0] != -1) return -1;
+        for (int i = 1; i < n; ++i)
+            if (parents[i] < 0 || parents[i] >= i) return -1;
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<float> x(static_cast<size_t>(n) * H), h(static_cast<size_t>(n) * H), mix(static_cast<size_t>(n) * H);
+    for (int t = 0; t < n; ++t)   // the embeddings: dequantized rows (pack.cpp:356-366)
+        orc_dequant_rows(m->embed.data() + static_cast<size_t>(tokens[t]) * q4_row_bytes(H), 1, H, m->g_embed,
+                         x.data() + static_cast<size_t>(t) * H);
+    std::vector<int> ids(static_cast<size_t>(n) * c.top_k);
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer &L = m->layers[static_cast<size_t>(l)];
+        for (int t = 0; t < n; ++t)
+            rmsnorm(x.data() + static_cast<size_t>(t) * H, L.in_norm.data(), h.data() + static_cast<size_t>(t) * H, H,
+                    c.eps, true);
+        attention(*m, L, n, h.data(), m->pos, parents, mode, mix.data());
+        for (int t = 0; t < n; ++t) {
+            float *xr = x.data() + static_cast<size_t>(t) * H;
+            const float *mr = mix.data() + static_cast<size_t>(t) * H;
+            for (int i = 0; i < H; ++i) xr[i] += mr[i];
+            rmsnorm(xr, L.post_norm.data(), h.data() + static_cast<size_t>(t) * H, H, c.eps, true);
+        }
+        const orc_moe_weights w = moe_view(*m, L);
+        moe_layer(w, n, h.data(), nullptr, mode, mix.data(), ids.data(), nullptr, nullptr);
+        if (route_ids)
+            std::copy(ids.begin(), ids.end(), route_ids + static_cast<size_t>(l) * n * c.top_k);
+        for (size_t i = 0; i < x.size(); ++i) x[i] += mix[i];
+    }
+    const auto t1 = std::chrono::steady_clock::now();
+    for (int t = 0; t < n; ++t)
+        rmsnorm(x.data() + static_cast<size_t>(t) * H, m->final_norm.data(), h.data() + static_cast<size_t>(t) * H, H,
+                c.eps, true);
+    const auto hs = crow_ptrs(h.data(), n, static_cast<size_t>(H));
+    auto ls = row_ptrs(logits, n, static_cast<size_t>(c.vocab));
+    matmul(m->lm_head.data(), c.vocab, H, m->g_lm, n, hs.data(), ls.data(), mode);
+    const auto t2 = std::chrono::steady_clock::now();
+    m->t_layers = std::chrono::duration<double>(t1 - t0).count();
+    m->t_head = std::chrono::duration<double>(t2 - t1).count();
+    m->last_pos = m->pos;
+    m->last_n = n;
+    m->pos += n;
+    return 0;
+}
+
+int orc_model_keep(orc_model *m, int kept, const int32_t *path) {
+    if (kept < 1 || kept > m->last_n || m->pos != m->last_pos + m->last_n) return -1;
+    const auto &c = m->c;
+    const size_t kv_row = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
+    if (path) {
+        for (int j = 0; j < kept; ++j)
+            if (path[j] < 0 || path[j] >= m->last_n || (j > 0 && path[j] <= path[j - 1])) return -1;
+        for (auto &L : m->layers)
+            for (int kvi = 0; kvi < 2; ++kvi) {
+                uint16_t *base = L.kv.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
+                for (int j = 0; j < kept; ++j)
+                    if (path[j] != j)
+                        std::memmove(base + static_cast<size_t>(m->last_pos + j) * kv_row,
+                                     base + static_cast<size_t>(m->last_pos + path[j]) * kv_row, kv_row * 2);
+            }
+    }
+    m->pos = m->last_pos + kept;
+    return 0;
+}
+
+void orc_model_last_times(const orc_model *m, double *t_layers, double *t_head) {
+    if (t_layers) *t_layers = m->t_layers;
+    if (t_head) *t_head = m->t_head;
+}
+
+}  // extern "C"

@@ -1,0 +1,310 @@
+"""numpy bindings of the CPU oracle (liboracle.so) and of the reference built from its sources (_ref/libgeode_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker or the timed CPU baseline. The product (geode_amd) never imports this module.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libgeode_ref.so")
+
+_c = ctypes
+_P = _c.c_void_p
+
+
+def _ptr(a):
+    return a.ctypes.data_as(_P) if a is not None else None
+
+
+def q4_row_bytes(cols):
+    return cols // 16 * 9
+
+
+class Config(_c.Structure):
+    _fields_ = [(n, _c.c_int) for n in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff",
+                                        "n_heads", "n_kv_heads", "head_dim", "rope_dim")] + \
+               [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int), ("attn_block", _c.c_int)]
+
+
+class MoeWeights(_c.Structure):
+    _fields_ = [("H", _c.c_int), ("E", _c.c_int), ("K", _c.c_int), ("F", _c.c_int), ("SF", _c.c_int),
+                ("experts", _P), ("expert_globals", _P), ("sh_gate", _P), ("sh_up", _P), ("sh_down", _P),
+                ("sh_globals", _c.c_float * 3), ("shared_gate", _P), ("router", _P)]
+
+
+# tensor kinds, numbered as in oracle.h and include/geode_verify.h
+EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, Q, K, V, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, SH_GATE, \
+    SH_UP, SH_DOWN, KV = range(18)
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError("oracle/liboracle.so is not built (run __graft_entry__.build())")
+    lib = _c.CDLL(LIB_PATH)
+    sig = {
+        "orc_hash": (_c.c_uint64, [_c.c_uint64, _c.c_uint64]),
+        "orc_fill_normal": (None, [_c.c_uint64, _c.c_int64, _c.c_float, _c.c_float, _P]),
+        "orc_fill_uniform": (None, [_c.c_uint64, _c.c_int64, _P]),
+        "orc_f32_to_f16": (_c.c_uint16, [_c.c_float]),
+        "orc_f16_to_f32": (_c.c_float, [_c.c_uint16]),
+        "orc_f32_to_bf16": (_c.c_uint16, [_c.c_float]),
+        "orc_set_threads": (None, [_c.c_int]),
+        "orc_threads": (_c.c_int, []),
+        "orc_e4m3_value": (_c.c_float, [_c.c_uint8]),
+        "orc_e4m3_byte": (_c.c_uint8, [_c.c_float]),
+        "orc_q4_block": (None, [_P, _c.c_float, _P, _P]),
+        "orc_q4_global": (_c.c_float, [_P, _c.c_int64]),
+        "orc_q4_pack": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P]),
+        "orc_dequant_rows": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P]),
+        "orc_matvec_rows": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P, _P]),
+        "orc_quantize_activation": (None, [_P, _c.c_int64, _P, _P, _P]),
+        "orc_matvec_rows_q": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P, _P, _P]),
+        "orc_matvec_bf16": (None, [_P, _c.c_int64, _c.c_int64, _c.c_int, _P, _P]),
+        "orc_rmsnorm": (None, [_P, _P, _P, _c.c_int, _c.c_float, _c.c_int]),
+        "orc_route_topk": (None, [_P, _c.c_int, _c.c_int, _P, _P]),
+        "orc_ffn_swiglu": (None, [_P, _P, _P, _c.c_float, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _c.c_int, _P,
+                                  _c.c_int, _P]),
+        "orc_moe_layer": (None, [_c.POINTER(MoeWeights), _c.c_int, _P, _P, _c.c_int, _P, _P, _P, _P]),
+        "orc_model_create": (_P, [_c.POINTER(Config)]),
+        "orc_model_free": (None, [_P]),
+        "orc_model_tensor": (_P, [_P, _c.c_int, _c.c_int, _c.c_int, _c.POINTER(_c.c_int64), _P]),
+        "orc_model_fill": (None, [_P, _c.c_uint64, _c.c_float, _c.c_float, _c.c_int, _c.c_int]),
+        "orc_model_set_position": (None, [_P, _c.c_int]),
+        "orc_model_position": (_c.c_int, [_P]),
+        "orc_model_verify": (_c.c_int, [_P, _P, _c.c_int, _P, _c.c_int, _P, _P]),
+        "orc_model_keep": (_c.c_int, [_P, _c.c_int, _P]),
+        "orc_model_last_times": (None, [_P, _P, _P]),
+        "orc_sample": (_c.c_int, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _c.c_double]),
+        "orc_sample_seeded": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_uint64, _c.c_int, _P]),
+        "orc_accept_match": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _P,
+                                        _P, _P]),
+        "orc_accept_textbook": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _P, _P,
+                                           _c.c_float, _P]),
+        "orc_nucleus_probs": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def load_ref():
+    """The reference's own functions (oracle/_ref), or None where they were not built (e.g. on the GPU box)."""
+    if not os.path.exists(REF_PATH):
+        return None
+    r = _c.CDLL(REF_PATH)
+    sig = {
+        "ref_e4m3_value": (_c.c_float, [_c.c_uint8]),
+        "ref_e4m3_byte": (_c.c_uint8, [_c.c_float]),
+        "ref_q4_block": (None, [_P, _c.c_float, _P, _P]),
+        "ref_dequant_rows": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P]),
+        "ref_matvec_rows": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P, _P]),
+        "ref_quantize_activation": (None, [_P, _c.c_int64, _P, _P, _P]),
+        "ref_matvec_rows_q": (None, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P, _P]),
+        "ref_matvec_bf16_multi": (None, [_P, _c.c_int64, _c.c_int64, _c.c_int, _P, _P]),
+        "ref_rmsnorm": (None, [_P, _P, _P, _c.c_int, _c.c_float, _c.c_int]),
+        "ref_sample_seeded": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_uint64, _c.c_int, _P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(r, name)
+        f.restype = res
+        f.argtypes = args
+    return r
+
+
+# ---------------------------------------------------------------- numpy wrappers
+def normal(seed, n, sigma=1.0, mean=0.0):
+    out = np.empty(int(n), np.float32)
+    lib.orc_fill_normal(seed, int(n), mean, sigma, _ptr(out))
+    return out
+
+
+def uniform(seed, n):
+    out = np.empty(int(n), np.float32)
+    lib.orc_fill_uniform(seed, int(n), _ptr(out))
+    return out
+
+
+def f32_to_f16_bits(x):
+    x = np.ascontiguousarray(x, np.float32)
+    return np.array([lib.orc_f32_to_f16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def q4_pack(w):
+    """fp32 [rows, cols] -> (pack-layout bytes [rows, cols/16*9], global s2)"""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    s2 = lib.orc_q4_global(_ptr(w), w.size)
+    out = np.empty((rows, q4_row_bytes(cols)), np.uint8)
+    lib.orc_q4_pack(_ptr(w), rows, cols, s2, _ptr(out))
+    return out, s2
+
+
+def q4_random(seed, rows, cols, sigma=0.02):
+    return q4_pack(normal(seed, rows * cols, sigma).reshape(rows, cols))
+
+
+def dequant(wq, cols, g):
+    rows = wq.shape[0]
+    out = np.empty((rows, cols), np.float32)
+    lib.orc_dequant_rows(_ptr(np.ascontiguousarray(wq)), rows, cols, g, _ptr(out))
+    return out
+
+
+def matvec(wq, cols, g, x):
+    rows = wq.shape[0]
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    lib.orc_matvec_rows(_ptr(np.ascontiguousarray(wq)), rows, cols, g, _ptr(x), _ptr(y))
+    return y
+
+
+def quantize_activation(x):
+    x = np.ascontiguousarray(x, np.float32)
+    cols = x.size
+    q = np.empty(cols, np.int8)
+    s = np.empty(cols // 16, np.float32)
+    b = np.empty(cols // 16, np.int32)
+    lib.orc_quantize_activation(_ptr(x), cols, _ptr(q), _ptr(s), _ptr(b))
+    return q, s, b
+
+
+def matvec_q(wq, cols, g, x):
+    q, s, _ = quantize_activation(x)
+    rows = wq.shape[0]
+    y = np.empty(rows, np.float32)
+    lib.orc_matvec_rows_q(_ptr(np.ascontiguousarray(wq)), rows, cols, g, _ptr(q), _ptr(s), _ptr(y))
+    return y
+
+
+def matvec_bf16(w, x):
+    w = np.ascontiguousarray(w, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = w.shape
+    n = x.shape[0]
+    y = np.empty((n, rows), np.float32)
+    lib.orc_matvec_bf16(_ptr(w), rows, cols, n, _ptr(x), _ptr(y))
+    return y
+
+
+def rmsnorm(x, w, eps=1e-6, zero_centered=True):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib.orc_rmsnorm(_ptr(x), _ptr(np.ascontiguousarray(w, np.float32)) if w is not None else None, _ptr(out), x.size,
+                    eps, int(zero_centered))
+    return out
+
+
+def route_topk(logits, K):
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(K, np.int32)
+    w = np.empty(K, np.float32)
+    lib.orc_route_topk(_ptr(logits), logits.size, K, _ptr(ids), _ptr(w))
+    return ids, w
+
+
+def ffn_swiglu(gate, up, down, gg, gu, gd, H, F, x_f16, mode=0):
+    M = x_f16.shape[0]
+    y = np.empty((M, H), np.float32)
+    lib.orc_ffn_swiglu(_ptr(gate), _ptr(up), _ptr(down), gg, gu, gd, H, F, M,
+                       _ptr(np.ascontiguousarray(x_f16, np.uint16)), mode, _ptr(y))
+    return y
+
+
+def sample(logits, temperature, top_p, top_k=0, cap=1024, u=0.5):
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib.orc_sample(_ptr(logits), logits.size, temperature, top_p, top_k, cap, u)
+
+
+def nucleus_probs(logits, temperature, top_p):
+    logits = np.ascontiguousarray(logits, np.float32)
+    p = np.empty(logits.size, np.float64)
+    lib.orc_nucleus_probs(_ptr(logits), logits.size, temperature, top_p, _ptr(p))
+    return p
+
+
+def accept_textbook(target, draft, temperature, top_p, greedy, u_draft, u_acc, u_res):
+    target = np.ascontiguousarray(target, np.float32)
+    draft = np.ascontiguousarray(draft, np.float32)
+    k, V = draft.shape
+    out = np.empty(k + 1, np.int32)
+    n = lib.orc_accept_textbook(_ptr(target), _ptr(draft), V, k, temperature, top_p, int(greedy),
+                                _ptr(np.ascontiguousarray(u_draft, np.float32)),
+                                _ptr(np.ascontiguousarray(u_acc, np.float32)), float(u_res), _ptr(out))
+    return out[:n]
+
+
+def accept_match(logits, batch, temperature, top_p, top_k=0, cap=1024, u=None):
+    logits = np.ascontiguousarray(logits, np.float32)
+    n, V = logits.shape
+    u = np.ascontiguousarray(u if u is not None else np.full(n, 0.5), np.float64)
+    out = np.empty(n, np.int32)
+    kept = _c.c_int(0)
+    cnt = lib.orc_accept_match(_ptr(logits), V, _ptr(np.ascontiguousarray(batch, np.int32)), n, temperature, top_p,
+                               top_k, cap, _ptr(u), _ptr(out), _c.byref(kept))
+    return out[:cnt], kept.value
+
+
+class Model:
+    """The oracle's whole model (orc_model_*): host-side weights in the pack layout."""
+
+    def __init__(self, cfg: dict, seed=1, sigma=0.02, router_sigma=0.0221, ctx=0, fast=False):
+        self.cfg = dict(cfg)
+        c = Config(**{k: cfg[k] for k, _ in Config._fields_ if k in cfg})
+        if "attn_block" not in cfg:
+            c.attn_block = 1024
+        self._c = c
+        self.h = lib.orc_model_create(_c.byref(c))
+        lib.orc_model_fill(self.h, seed, sigma, router_sigma, ctx, int(fast))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.orc_model_free(self.h)
+            self.h = None
+
+    def tensor(self, kind, layer=0, expert=0):
+        """(numpy uint8 view of the bytes, globals[2])"""
+        nb = _c.c_int64(0)
+        g = np.zeros(2, np.float32)
+        p = lib.orc_model_tensor(self.h, kind, layer, expert, _c.byref(nb), _ptr(g))
+        if not p:
+            raise KeyError((kind, layer, expert))
+        buf = (_c.c_uint8 * nb.value).from_address(p)
+        return np.frombuffer(buf, np.uint8), g
+
+    @property
+    def position(self):
+        return lib.orc_model_position(self.h)
+
+    @position.setter
+    def position(self, p):
+        lib.orc_model_set_position(self.h, p)
+
+    def verify(self, tokens, parents=None, mode=0, route=False):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        n = tokens.size
+        logits = np.empty((n, self.cfg["vocab"]), np.float32)
+        par = np.ascontiguousarray(parents, np.int32) if parents is not None else None
+        ids = np.empty((self.cfg["n_layers"], n, self.cfg["top_k"]), np.int32) if route else None
+        rc = lib.orc_model_verify(self.h, _ptr(tokens), n, _ptr(par), mode, _ptr(logits), _ptr(ids))
+        if rc != 0:
+            raise ValueError("orc_model_verify failed")
+        return (logits, ids) if route else logits
+
+    def keep(self, kept, path=None):
+        p = np.ascontiguousarray(path, np.int32) if path is not None else None
+        if lib.orc_model_keep(self.h, kept, _ptr(p)) != 0:
+            raise ValueError("orc_model_keep failed")
+
+    def last_times(self):
+        a, b = _c.c_double(0), _c.c_double(0)
+        lib.orc_model_last_times(self.h, _c.byref(a), _c.byref(b))
+        return a.value, b.value
