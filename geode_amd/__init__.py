@@ -1,0 +1,243 @@
+"""geode_amd: Geode's speculative-decoding verify step on MI355X (gfx950), behind the C ABI of libgeode_verify.so.
+
+This module is the Python host side over that ABI (ctypes; numpy for host arrays). It loads the in-tree library
+and fails loudly when it is missing: there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgeode_verify.so")
+
+_c = ctypes
+_P = _c.c_void_p
+
+
+class GvQ4(_c.Structure):
+    _fields_ = [("codes", _P), ("scales", _P), ("rows", _c.c_int64), ("cols", _c.c_int64), ("lanes", _c.c_int32),
+                ("steps", _c.c_int32), ("global_", _c.c_float)]
+
+
+class GvModelConfig(_c.Structure):
+    _fields_ = [(n, _c.c_int32) for n in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff",
+                                          "n_heads", "n_kv_heads", "head_dim", "rope_dim")] + \
+               [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int32), ("max_rows", _c.c_int32)]
+
+
+# tensor kinds of gv_model_adopt
+EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, QKV, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, \
+    SHARED_EXPERT, KV = 0, 1, 2, 3, 4, 5, 8, 9, 10, 11, 12, 13, 14, 17
+
+# every symbol include/geode_verify.h declares, with its signature
+SIGNATURES = {
+    "gv_last_error": (_c.c_char_p, []),
+    "gv_init": (_c.c_int, [_c.c_int]),
+    "gv_device_count": (_c.c_int, []),
+    "gv_malloc": (_P, [_c.c_size_t]),
+    "gv_free": (_c.c_int, [_P]),
+    "gv_memcpy_h2d": (_c.c_int, [_P, _P, _c.c_size_t]),
+    "gv_memcpy_d2h": (_c.c_int, [_P, _P, _c.c_size_t]),
+    "gv_memcpy_d2d": (_c.c_int, [_P, _P, _c.c_size_t]),
+    "gv_memset": (_c.c_int, [_P, _c.c_int, _c.c_size_t]),
+    "gv_synchronize": (_c.c_int, []),
+    "gv_event_record": (_c.c_int, []),
+    "gv_event_elapsed_ms": (_c.c_float, [_c.c_int, _c.c_int]),
+    "gv_q4_device_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64]),
+    "gv_q4_from_pack": (_c.c_int, [_P, _c.c_int64, _c.c_int64, _c.c_float, _P, _c.POINTER(GvQ4)]),
+    "gv_q4_dequant": (_c.c_int, [_c.POINTER(GvQ4), _P]),
+    "gv_q4_pack": (_c.c_int, [_P, _c.c_int64, _c.c_int64, _P, _P]),
+    "gv_act_bytes": (_c.c_size_t, [_c.c_int64]),
+    "gv_quantize": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _P, _c.c_float, _P, _P]),
+    "gv_gemv_q4": (_c.c_int, [_c.POINTER(GvQ4), _P, _c.c_int, _P, _c.c_int64, _c.c_int]),
+    "gv_ffn_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int]),
+    "gv_ffn_swiglu": (_c.c_int, [_c.POINTER(GvQ4), _c.POINTER(GvQ4), _c.POINTER(GvQ4), _c.c_int, _P, _P, _P]),
+    "gv_open": (_P, [_c.c_int, _c.c_char_p, _c.c_int]),
+    "gv_close": (None, [_P]),
+    "gv_adopt_q4": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int64, _c.c_size_t, _c.c_float]),
+    "gv_gemm": (_c.c_int, [_P, _c.c_int, _c.c_int, _P, _P]),
+    "gv_mlp": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int, _c.c_int, _P, _P]),
+    "gv_model_create": (_P, [_c.POINTER(GvModelConfig), _c.c_char_p, _c.c_int]),
+    "gv_model_free": (None, [_P]),
+    "gv_model_adopt": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64, _P]),
+    "gv_model_randomize": (_c.c_int, [_P, _c.c_uint64, _c.c_float, _c.c_float, _c.c_int]),
+    "gv_model_set_position": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_position": (_c.c_int, [_P]),
+    "gv_verify": (_c.c_int, [_P, _P, _c.c_int, _P, _P]),
+    "gv_verify_keep": (_c.c_int, [_P, _c.c_int, _P]),
+    "gv_model_logits": (_P, [_P]),
+    "gv_model_route_ids": (_c.c_int, [_P, _P]),
+}
+
+
+class GeodeError(RuntimeError):
+    pass
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise GeodeError(f"{LIB_PATH} is not built: run `python -m geode_amd.build` (no CPU fallback exists)")
+    lib = _c.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def check(rc, what=""):
+    if rc != 0:
+        raise GeodeError(f"{what}: {lib.gv_last_error().decode()}")
+
+
+def init(device=0):
+    check(lib.gv_init(device), "gv_init")
+
+
+class DeviceBuffer:
+    """Device memory owned from Python (gv_malloc / gv_free)."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib.gv_malloc(max(1, self.nbytes))
+        if not self.ptr:
+            raise GeodeError(f"gv_malloc({nbytes}): {lib.gv_last_error().decode()}")
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a, offset=0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib.gv_memcpy_h2d(_c.c_void_p(self.ptr + offset), a.ctypes.data_as(_P), a.nbytes), "h2d")
+
+    def download(self, dtype, shape, offset=0):
+        out = np.empty(shape, dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib.gv_memcpy_d2h(out.ctypes.data_as(_P), _c.c_void_p(self.ptr + offset), out.nbytes), "d2h")
+        return out
+
+    def zero(self):
+        check(lib.gv_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def __int__(self):
+        return self.ptr
+
+    def free(self):
+        if self.ptr:
+            lib.gv_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Q4Matrix:
+    """A q4 matrix resident on the device in the kernels' layout (from pack-layout bytes)."""
+
+    def __init__(self, pack_bytes, rows, cols, global_):
+        pack = np.ascontiguousarray(pack_bytes, np.uint8).reshape(rows, cols // 16 * 9)
+        staging = DeviceBuffer.from_array(pack)
+        self.buf = DeviceBuffer(lib.gv_q4_device_bytes(rows, cols))
+        self.desc = GvQ4()
+        check(lib.gv_q4_from_pack(staging.ptr, rows, cols, global_, self.buf.ptr, _c.byref(self.desc)),
+              "gv_q4_from_pack")
+        check(lib.gv_synchronize(), "sync")
+        staging.free()
+        self.rows, self.cols = rows, cols
+
+    def ref(self):
+        return _c.byref(self.desc)
+
+    def dequant(self):
+        out = DeviceBuffer(self.rows * self.cols * 4)
+        check(lib.gv_q4_dequant(self.ref(), out.ptr), "gv_q4_dequant")
+        return out.download(np.float32, (self.rows, self.cols))
+
+
+def act_bytes(cols):
+    return lib.gv_act_bytes(cols)
+
+
+def gemv(w: Q4Matrix, x: np.ndarray, accumulate_into=None):
+    """y = W x for x [M, cols] fp32 (host), on the int8 path; returns y [M, rows]."""
+    x = np.ascontiguousarray(x, np.float32)
+    M = x.shape[0]
+    dx = DeviceBuffer.from_array(x)
+    act = DeviceBuffer(M * act_bytes(w.cols))
+    check(lib.gv_quantize(dx.ptr, w.cols, M, w.cols, None, 0.0, act.ptr, None), "gv_quantize")
+    y = DeviceBuffer(M * w.rows * 4)
+    if accumulate_into is not None:
+        y.upload(np.ascontiguousarray(accumulate_into, np.float32))
+    check(lib.gv_gemv_q4(w.ref(), act.ptr, M, y.ptr, w.rows, int(accumulate_into is not None)), "gv_gemv_q4")
+    return y.download(np.float32, (M, w.rows))
+
+
+class VerifyModel:
+    """A whole model on the device and the verify contract: verify(tokens, parents) then keep(kept, path), as
+    Model::verify_n / verify_keep (engine/src/model.cpp:1483-1634)."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = dict(cfg)
+        c = GvModelConfig(**{k: cfg[k] for k, _ in GvModelConfig._fields_})
+        err = _c.create_string_buffer(512)
+        self.h = lib.gv_model_create(_c.byref(c), err, 512)
+        if not self.h:
+            raise GeodeError(f"gv_model_create: {err.value.decode()}")
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib.gv_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def adopt(self, kind, data, layer=0, expert=0, globals_=None):
+        data = np.ascontiguousarray(data)
+        g = np.ascontiguousarray(globals_ if globals_ is not None else [0.0], np.float32)
+        check(lib.gv_model_adopt(self.h, kind, layer, expert, data.ctypes.data_as(_P), data.nbytes,
+                                 g.ctypes.data_as(_P)), f"gv_model_adopt({kind}, {layer}, {expert})")
+
+    def randomize(self, seed, sigma=0.02, router_sigma=0.0221, ctx=0):
+        check(lib.gv_model_randomize(self.h, seed, sigma, router_sigma, ctx), "gv_model_randomize")
+
+    @property
+    def position(self):
+        return lib.gv_model_position(self.h)
+
+    @position.setter
+    def position(self, p):
+        check(lib.gv_model_set_position(self.h, p), "gv_model_set_position")
+
+    def verify(self, tokens, parents=None, want_logits=True):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        n = tokens.size
+        par = np.ascontiguousarray(parents, np.int32) if parents is not None else None
+        out = np.empty((n, self.cfg["vocab"]), np.float32) if want_logits else None
+        check(lib.gv_verify(self.h, tokens.ctypes.data_as(_P), n, par.ctypes.data_as(_P) if par is not None else None,
+                            out.ctypes.data_as(_P) if out is not None else None), "gv_verify")
+        return out
+
+    def keep(self, kept, path=None):
+        p = np.ascontiguousarray(path, np.int32) if path is not None else None
+        check(lib.gv_verify_keep(self.h, kept, p.ctypes.data_as(_P) if p is not None else None), "gv_verify_keep")
+
+    def route_ids(self, n):
+        out = np.empty((self.cfg["n_layers"], n, self.cfg["top_k"]), np.int32)
+        check(lib.gv_model_route_ids(self.h, out.ctypes.data_as(_P)), "gv_model_route_ids")
+        return out

@@ -1,0 +1,59 @@
+// kernels.hpp - host-side launchers of the gfx950 kernels (namespace gv); the C ABI (capi.hip) sits on these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace gv {
+
+constexpr int kMaxRows = 32;   // rows (tokens) a skinny product takes at once
+
+// Where a product's results go: y[t * ldy + row] = acc x global (the global of the row's segment: a fused matrix
+// of parts, e.g. q | k | v, keeps each part's own), or += when accumulate (the residual add).
+struct GemvOut {
+    float *y = nullptr;
+    int64_t ldy = 0;
+    int accumulate = 0;
+    int nseg = 1;
+    int64_t seg_end[4] = {0, 0, 0, 0};
+    float seg_global[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    __device__ inline void put(int64_t row, int t, float v) const {
+        float g = seg_global[0];
+        for (int s = 1; s < nseg; ++s)
+            if (row >= seg_end[s - 1]) g = seg_global[s];
+        const float r = v * g;
+        float *p = y + t * ldy + row;
+        if (accumulate) *p += r;
+        else *p = r;
+    }
+};
+
+inline GemvOut gemv_out(float *y, int64_t ldy, float global, int accumulate = 0) {
+    GemvOut o;
+    o.y = y;
+    o.ldy = ldy;
+    o.accumulate = accumulate;
+    o.nseg = 1;
+    o.seg_end[0] = INT64_MAX;
+    o.seg_global[0] = global;
+    return o;
+}
+
+int q4_init_constants();
+int q4_from_pack(const uint8_t *pack_dev, int64_t rows, int64_t cols, float global, uint8_t *codes, uint8_t *scales,
+                 Q4 &out, hipStream_t st);
+int q4_dequant(const Q4 &w, float *out, hipStream_t st);
+int q4_pack(const float *w, int64_t rows, int64_t cols, unsigned int *scratch_u32, uint8_t *out, float *global_out,
+            hipStream_t st);
+int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, uint8_t *act,
+                 int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st);
+int gemv_q4(const Q4 &w, const uint8_t *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st);
+
+// elementwise helpers (misc.hip)
+int f16_to_f32(const uint16_t *x, int64_t n, float *y, hipStream_t st);
+int swiglu(const float *g, const float *u, int64_t n, float *m, hipStream_t st);
+int fill_normal(uint64_t seed, int64_t n, float sigma, float *out, hipStream_t st);
+
+}  // namespace gv

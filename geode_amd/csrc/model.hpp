@@ -1,0 +1,78 @@
+// model.hpp - the verify step's device state: weights in the kernels' layout, the fp16 KV cache, per-step
+// parameters and scratch. The C ABI (gv_model_*, gv_verify*) is in model.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "../../include/geode_verify.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace gv {
+
+// Per verify: the rows' tokens, their KV slots (pos + i) and rotary positions (pos + depth), and which earlier rows
+// each row sees (bit j of vis[i]: row j is row i or one of its ancestors; a chain sees every earlier row).
+struct StepParams {
+    int pos;
+    int M;
+    int tokens[kMaxRows];
+    int depth[kMaxRows];
+    uint32_t vis[kMaxRows];
+};
+
+// Routing of one layer, written by the route kernel: slots are the distinct experts picked (ascending, the shared
+// expert last, index E), each with its picks (token, rank), picks ordered by (expert, token, rank).
+struct RouteState {
+    int n_slots;
+    int n_picks;
+    int slot_expert[kMaxRows * 16 + 1];
+    int slot_start[kMaxRows * 16 + 1];
+    int slot_count[kMaxRows * 16 + 1];
+    int pick_token[kMaxRows * 17];
+    int pick_of[kMaxRows * 17];   // [t][k] for k < K the routed pick, [t][K] the shared expert's
+    float weight[kMaxRows * 16];  // [t][k]
+    float gate[kMaxRows];         // sigmoid of the shared expert's gate
+};
+
+struct LayerW {
+    Q4 qkv;   // [nh*2*hd (q | gate per head) + nkv*hd (k) + nkv*hd (v)] x H, three globals
+    float g_q = 1, g_k = 1, g_v = 1;
+    Q4 o;     // H x nh*hd
+    float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    uint16_t *router = nullptr;   // bf16 [E + 1][H]: the router's rows, then the shared expert's gate
+    uint8_t *gu_codes = nullptr, *gu_scales = nullptr;   // [E + 1] experts' gate_up (the shared one last)
+    uint8_t *dn_codes = nullptr, *dn_scales = nullptr;   // [E + 1] experts' down
+    float *expert_globals = nullptr;                     // [E + 1][3]: gate half, up half, down
+    uint16_t *kv = nullptr;                              // [2][max_ctx][nkv * hd] fp16
+};
+
+struct Model {
+    gv_model_config c{};
+    int E1 = 0;   // experts + the shared one
+    size_t gu_code_stride = 0, gu_scale_stride = 0, dn_code_stride = 0, dn_scale_stride = 0;
+    Q4 embed, lm_head;
+    float *final_norm = nullptr;
+    std::vector<LayerW> layers;
+    std::vector<void *> allocs;
+    float *rope_cos = nullptr, *rope_sin = nullptr;   // [max_ctx + kMaxRows][rope_dim / 2], the host's cosf/sinf
+    int kv_blocks = 0;                                // attention blocks of kAttnBlock positions
+    // scratch
+    StepParams *sp = nullptr;
+    RouteState *route = nullptr;   // [n_layers]
+    float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *q_out = nullptr, *core = nullptr, *rlogits = nullptr;
+    float *parts = nullptr, *gu_out = nullptr, *y = nullptr, *logits = nullptr;
+    uint8_t *act_h = nullptr, *act_core = nullptr, *act_m = nullptr;
+    int32_t *route_ids = nullptr;   // [n_layers][max_rows][K]
+    uint16_t *kv_all = nullptr;
+    // host side
+    int pos = 0, last_pos = 0, last_n = 0;
+    StepParams host_sp{};
+    int max_slots = 0, max_picks = 0;
+};
+
+constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
+
+}  // namespace gv

@@ -1,0 +1,154 @@
+/* geode_verify.h - libgeode_verify.so: Geode's speculative-decoding verify step on one MI355X (gfx950).
+ *
+ * A C ABI with no HIP or torch type in it: plain pointers, sizes, int status (0 = done, nonzero = failed, the
+ * reason in gv_last_error()). It stands where the reference engine calls its accelerator backends: the NPU
+ * plugin's C ABI (npu/host/npu_api.h), which the engine dlopen()s and binds into Model::Npu's function table
+ * (engine/src/model.cpp:2255-2394, engine/src/model.hpp:682-797), and the Adreno backend's decode calls
+ * (engine/src/gpu8.hpp:116-192) under Model::verify_n / verify_keep (engine/src/model.cpp:1483-1634).
+ *
+ * Threading: one host thread drives the library at a time (engine/include/geode/geode.h:6-8). Every call is
+ * enqueued on the library's stream; calls that return host data wait for it.
+ *
+ * q4 matrices come in the pack's row layout (engine/src/kernels.hpp:22-26; npu/host/npu_api.h:31-34): per row
+ * cols/2 code bytes (value 2j in the low nibble of byte j; levels 1 3 .. 15 for codes 0..7, -1 .. -15 for 8..15)
+ * then cols/16 E4M3 scale bytes; value = level x E4M3(scale) x global.
+ */
+#ifndef GEODE_VERIFY_H
+#define GEODE_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ run time
+ * (no reference counterpart: the device, its memory and stream; the reference's OpenCL/FastRPC equivalents are
+ * engine/src/opencl.cpp and npu/host/npu_api.h's gnpu_open) */
+const char *gv_last_error(void);
+/* Makes the device current and creates the library's stream (idempotent). 0 when done. */
+int gv_init(int device);
+int gv_device_count(void);
+void *gv_malloc(size_t bytes); /* device memory, NULL on failure */
+int gv_free(void *p);
+int gv_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int gv_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int gv_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int gv_memset(void *dst, int value, size_t bytes);
+int gv_synchronize(void);
+/* milliseconds between two points of the library's stream: gv_event_record returns an id */
+int gv_event_record(void);
+float gv_event_elapsed_ms(int start, int stop);
+
+/* ------------------------------------------------------------------ the q4 format on the device */
+typedef struct gv_q4 {
+    const uint8_t *codes;  /* device: affine nibbles in the step-major tile layout */
+    const uint8_t *scales; /* device: E4M3 bytes grouped per lane */
+    int64_t rows, cols;
+    int32_t lanes, steps;
+    float global;
+} gv_q4;
+
+/* Device bytes a rows x cols q4 matrix takes (the same 4.5 bits a weight as the pack). */
+size_t gv_q4_device_bytes(int64_t rows, int64_t cols);
+/* The pack layout at pack_dev (device) into the device layout at dst (gv_q4_device_bytes of device memory):
+ * a lossless permutation of the same bytes. Replaces the reference's load-time re-layouts to_quad / to_tile8
+ * (engine/src/kernels.cpp:946-991). */
+int gv_q4_from_pack(const uint8_t *pack_dev, int64_t rows, int64_t cols, float global, void *dst, gv_q4 *out);
+/* out[rows][cols] fp32 (device) = the dequantized weights, bit for bit dequant_row's (engine/src/kernels.cpp:1214) */
+int gv_q4_dequant(const gv_q4 *w, float *out);
+/* The RTN packer on the device: w[rows][cols] fp32 -> pack layout, global = max|w| x 1.25 / (15 x 448); bit for
+ * bit q4_block / e4m3_byte (engine/src/yue2_q4.cpp:72-114, :332-358). global_out: device float. */
+int gv_q4_pack(const float *w_dev, int64_t rows, int64_t cols, uint8_t *pack_out_dev, float *global_out_dev);
+
+/* ------------------------------------------------------------------ activations and products (device pointers) */
+/* Bytes of one token's int8 activations for cols inputs. */
+size_t gv_act_bytes(int64_t cols);
+/* act[t] = quantize_activation(x[t]) (engine/src/kernels.cpp:1254-1295) for M tokens (x rows ldx floats apart);
+ * with norm_w, x is first RMSNorm'ed with weight (1 + w) (engine/src/kernels.cpp:1520-1529) and the normalized
+ * rows go to h_out when it is not NULL. */
+int gv_quantize(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, uint8_t *act,
+                float *h_out);
+/* y[t][r] (= or +=) W act[t] for M <= 32 tokens: the int8 path of matvec_rows_q_multi (engine/src/kernels.cpp:
+ * 1304-1420; the integer block sums bit for bit, the fp32 sum in another order). */
+int gv_gemv_q4(const gv_q4 *w, const uint8_t *act, int M, float *y, int64_t ldy, int accumulate);
+/* C1: y[t] = down(silu(gate x[t]) * up x[t]) for M fp16 rows x (device), the dense MLP of Model::moe
+ * (engine/src/model.cpp:4126-4146) on the int8 path. ws: device scratch of gv_ffn_workspace_bytes. */
+size_t gv_ffn_workspace_bytes(int64_t hidden, int64_t ff, int M);
+int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16, float *y,
+                  void *ws);
+
+/* ------------------------------------------------------------------ the NPU plugin's calls, on this GPU
+ * The same names' meaning as npu/host/npu_api.h (gnpu_open / gnpu_adopt_q4 / gnpu_gemm / gnpu_mlp): a handle,
+ * matrices adopted in the pack layout (copied to the device), products on host rows. */
+typedef struct gv_ctx gv_ctx;
+gv_ctx *gv_open(int device, char *err, int err_len);                                    /* npu_api.h:16 */
+void gv_close(gv_ctx *g);                                                                /* npu_api.h:30 */
+int gv_adopt_q4(gv_ctx *g, const uint8_t *data, int64_t rows, int64_t cols, size_t row_bytes, float global); /* :34 */
+int gv_gemm(gv_ctx *g, int id, int n, const float *const *xs, float *const *ys);       /* npu_api.h:44 */
+int gv_mlp(gv_ctx *g, int gate, int up, int n_down, const int *downs, int act, int n, const float *const *xs,
+           float *const *ys);                                                            /* npu_api.h:66 */
+
+/* ------------------------------------------------------------------ the verify step
+ * A whole model resident on the device and the reference's verify contract (engine/src/model.hpp:189-205):
+ * gv_verify = Model::verify_n (engine/src/model.cpp:1483-1592), gv_verify_keep = Model::verify_keep
+ * (engine/src/model.cpp:1594-1634). Per layer: RMSNorm, gated attention with q/k RMSNorm and partial RoPE over an
+ * fp16 KV cache (engine/src/model.cpp:3690-4019), RMSNorm, the MoE block (router, top-k, experts, sigmoid-gated
+ * shared expert, combine; engine/src/model.cpp:4123-4587); then the final norm and lm_head. Products on the
+ * reference's int8 path (quantize_activation + matvec_rows_q). */
+typedef struct gv_model_config {
+    int32_t hidden, vocab, n_layers, n_experts, top_k, moe_ff, shared_ff;
+    int32_t n_heads, n_kv_heads, head_dim, rope_dim;
+    float rope_theta, eps;
+    int32_t max_ctx;  /* KV positions the cache holds */
+    int32_t max_rows; /* rows a verify takes at most (<= 32) */
+} gv_model_config;
+
+/* tensor kinds for gv_model_adopt (numbered as the CPU oracle's) */
+enum {
+    GV_EMBED = 0,         /* q4 [vocab x hidden], globals[0] */
+    GV_LM_HEAD = 1,       /* q4 [vocab x hidden], globals[0] */
+    GV_FINAL_NORM = 2,    /* f32 [hidden] */
+    GV_IN_NORM = 3,       /* f32 [hidden] */
+    GV_POST_NORM = 4,     /* f32 [hidden] */
+    GV_QKV = 5,           /* q4 rows of q [n_heads x (query hd | gate hd)], then k, then v; globals[3] */
+    GV_O = 8,             /* q4 [hidden x n_heads*hd], globals[0] */
+    GV_Q_NORM = 9,        /* f32 [hd] */
+    GV_K_NORM = 10,       /* f32 [hd] */
+    GV_ROUTER = 11,       /* bf16 [n_experts x hidden] */
+    GV_SHARED_GATE = 12,  /* bf16 [hidden] */
+    GV_EXPERT = 13,       /* the pack's expert block: q4 gate_up [2ff x hidden] then down [hidden x ff];
+                             globals[0] gate_up, globals[1] down (engine/src/pack.cpp:329-333) */
+    GV_SHARED_EXPERT = 14,/* q4 gate [ff x hidden], up [ff x hidden], down [hidden x ff]; globals[3] */
+    GV_KV = 17            /* fp16 [2][n_positions][n_kv_heads*hd]: K then V of positions 0.. */
+};
+
+typedef struct gv_model gv_model;
+gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len);
+void gv_model_free(gv_model *m);
+/* A tensor from host memory (bytes: its size, checked). */
+int gv_model_adopt(gv_model *m, int kind, int layer, int expert, const void *data, int64_t bytes,
+                   const float *globals);
+/* Every tensor seeded on the device: N(0, sigma) weights through the RTN packer, the router N(0, router_sigma) in
+ * bf16, norms N(0, 0.02), the KV cache's first ctx positions N(0, 1) in fp16; the position becomes ctx. */
+int gv_model_randomize(gv_model *m, uint64_t seed, float sigma, float router_sigma, int ctx);
+int gv_model_set_position(gv_model *m, int pos);
+int gv_model_position(const gv_model *m);
+/* verify_n: n rows at KV slots pos.. . parents NULL: a chain (row i sees rows 0..i); else a draft tree in BFS
+ * order, parents[0] = -1, parents[i] < i (row i sees the context, its ancestors and itself; rotary position
+ * pos + depth). logits (host, [n][vocab]) may be NULL: they stay on the device (gv_model_logits). The position
+ * advances by n. */
+int gv_verify(gv_model *m, const int32_t *tokens, int n, const int32_t *parents, float *logits);
+/* verify_keep: the first kept rows stay (a tree: path[0..kept) of row indices, path[0] = 0, ascending; their
+ * keys and values move to slots pos..pos+kept-1); the position becomes the verify's start plus kept. */
+int gv_verify_keep(gv_model *m, int kept, const int32_t *path);
+const float *gv_model_logits(const gv_model *m); /* device [max_rows][vocab] of the last verify */
+/* the last verify's routed experts, host [n_layers][n][top_k] */
+int gv_model_route_ids(const gv_model *m, int32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEODE_VERIFY_H */

@@ -1,0 +1,119 @@
+"""GPU parity of the whole verify step (C4's family at small shapes) against the oracle on the same seeded inputs:
+logits within 1e-2 (max error over max |logit|) of the reference's default int8 CPU path, routed experts
+identical, greedy tokens identical away from near-ties; chain and tree; verify + keep equal to a verify of the kept
+prefix."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+from model_helpers import SMALL, SMALL_ROUTER_SIGMA, adopt_oracle_model, near_tie_rows, rel_err, tree_parents
+
+pytestmark = pytest.mark.gpu
+
+CTX = 100
+
+
+@pytest.fixture(scope="module")
+def gv():
+    import geode_amd
+
+    geode_amd.init(0)
+    return geode_amd
+
+
+@pytest.fixture(scope="module")
+def models(gv):
+    om = po.Model(SMALL, seed=7, router_sigma=SMALL_ROUTER_SIGMA, ctx=CTX)
+    gm = gv.VerifyModel(SMALL)
+    adopt_oracle_model(gm, om, CTX)
+    return om, gm
+
+
+def _check(om_logits, gm_logits, om_ids, gm_ids):
+    err = rel_err(gm_logits, om_logits)
+    assert err <= 1e-2, f"logits max error {err:.3e}"
+    same_route = np.mean(om_ids == gm_ids)
+    assert same_route == 1.0, f"routing agrees on {same_route:.4f} of picks"
+    ties = near_tie_rows(om_logits, 2 * np.abs(gm_logits - om_logits).max())
+    for r in range(om_logits.shape[0]):
+        if r not in ties:
+            assert np.argmax(gm_logits[r]) == np.argmax(om_logits[r]), f"greedy token differs at row {r}"
+
+
+@pytest.mark.parametrize("n", [1, 2, 5])
+def test_chain_verify(models, n):
+    om, gm = models
+    om.position = CTX
+    gm.position = CTX
+    toks = (np.arange(n) * 37 + 11) % SMALL["vocab"]
+    ol, oids = om.verify(toks, route=True)
+    gl = gm.verify(toks)
+    _check(ol, gl, oids, gm.route_ids(n))
+
+
+def test_tree_verify(models):
+    om, gm = models
+    parents = tree_parents((4, 3))   # 17 rows: the root, 4 children, 12 grandchildren
+    n = parents.size
+    toks = (np.arange(n) * 53 + 5) % SMALL["vocab"]
+    om.position = CTX
+    gm.position = CTX
+    ol, oids = om.verify(toks, parents=parents, route=True)
+    gl = gm.verify(toks, parents=parents)
+    _check(ol, gl, oids, gm.route_ids(n))
+
+
+def test_tree_row_equals_chain_of_its_ancestors(models):
+    """a tree row's logits equal those of the chain through its ancestors (same positions): on the GPU"""
+    _, gm = models
+    parents = tree_parents((4, 3))
+    toks = (np.arange(parents.size) * 53 + 5) % SMALL["vocab"]
+    gm.position = CTX
+    tl = gm.verify(toks, parents=parents)
+    for node in (1, 4, 5, 16):
+        path = [node]
+        while parents[path[-1]] >= 0:
+            path.append(int(parents[path[-1]]))
+        path = path[::-1]
+        gm.position = CTX
+        cl = gm.verify(toks[path])
+        assert rel_err(tl[node], cl[-1]) <= 1e-5
+
+
+def test_keep_then_verify(models):
+    """verify 5, keep 2, verify 3 more == verify the 2 kept + the 3 new at once (oracle and GPU agree throughout)"""
+    om, gm = models
+    toks = np.array([3, 99, 200, 7, 401], np.int32)
+    nxt = np.array([45, 46, 47], np.int32)
+    for m in (om, gm):
+        m.position = CTX
+    om.verify(toks)
+    gm.verify(toks)
+    om.keep(2)
+    gm.keep(2)
+    assert gm.position == CTX + 2
+    ol = om.verify(nxt)
+    gl = gm.verify(nxt)
+    assert rel_err(gl, ol) <= 1e-2
+    gm.position = CTX
+    whole = gm.verify(np.concatenate([toks[:2], nxt]))
+    assert rel_err(gl, whole[2:]) <= 1e-5
+
+
+def test_tree_keep_compacts_kv(models):
+    om, gm = models
+    parents = tree_parents((4, 3))
+    toks = (np.arange(parents.size) * 29 + 1) % SMALL["vocab"]
+    path = np.array([0, 2, 9], np.int32)   # root -> its 2nd child -> a grandchild under it
+    assert parents[2] == 0 and parents[9] == 2
+    for m in (om, gm):
+        m.position = CTX
+        m.verify(toks, parents=parents)
+        m.keep(3, path)
+    nxt = np.array([17, 18], np.int32)
+    ol = om.verify(nxt)
+    gl = gm.verify(nxt)
+    assert rel_err(gl, ol) <= 1e-2
+    gm.position = CTX
+    chain = gm.verify(np.concatenate([toks[path], nxt]))
+    assert rel_err(gl, chain[3:]) <= 1e-5
