@@ -1,0 +1,234 @@
+"""Benchmark of the speculative-decoding verify step on one MI355X (the driver's contract: one JSON line).
+
+Workload (the metric's config): the full 40-layer 35B-A3B-shape verify step, gated
+attention (16 query heads, 2 KV heads, head_dim 256, RoPE theta 1e7) plus the MoE (256 experts, top-8 softmax
+routing, 1 shared expert, ff 512), vocab 151,936, q4 weights seeded on the device (N(0, 0.02) through the RTN
+packer), an fp16 KV cache of 8,192 context positions N(0, 1). A step verifies k = 4 chained drafts plus the last
+token (M = 5 rows): every layer, the final norm and lm_head, logits left on the device. The drafts are the target
+model's own greedy continuation, so a greedy sample-and-match accepts all of them (5 tokens emitted a step).
+
+    python bench.py [--steps K] [--warmup W] [--tree] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+C4 = dict(hidden=2048, vocab=151936, n_layers=40, n_experts=256, top_k=8, moe_ff=512, shared_ff=512, n_heads=16,
+          n_kv_heads=2, head_dim=256, rope_dim=64, rope_theta=1e7, eps=1e-6, max_ctx=8192 + 64, max_rows=17)
+CTX = 8192
+SEED = 20261201
+PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s
+Q4_ROW = lambda cols: cols // 16 * 9   # noqa: E731  bytes of a q4 row (engine/src/kernels.cpp:900-902)
+
+
+def tree_parents():
+    """the draft tree of configs[3]: 16 nodes under the root, branching 4 then 3 (17 rows)"""
+    parents, frontier = [-1], [0]
+    for b in (4, 3):
+        nxt = []
+        for p in frontier:
+            for _ in range(b):
+                parents.append(p)
+                nxt.append(len(parents) - 1)
+        frontier = nxt
+    return np.array(parents, np.int32)
+
+
+def algorithmic_bytes(cls, c, M, uniq_per_layer, ctx):
+    """bytes a launch of kernel class cls must move at least (weights and KV read once, activations ignored when
+    small), per launch; uniq_per_layer: distinct routed experts of each layer counted from the run"""
+    H, F, V = c["hidden"], c["moe_ff"], c["vocab"]
+    nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+    L = c["n_layers"]
+    gu, dn = 2 * F * Q4_ROW(H), H * Q4_ROW(F)
+    if cls == "moe_up":
+        return sum((u + 1) * gu for u in uniq_per_layer) / L
+    if cls == "moe_down":
+        return sum((u + 1) * dn for u in uniq_per_layer) / L
+    if cls == "qkv":
+        return (nh * 2 * hd + 2 * nkv * hd) * Q4_ROW(H)
+    if cls == "o_proj":
+        return H * Q4_ROW(nh * hd)
+    if cls == "lm_head":
+        return V * Q4_ROW(H)
+    if cls == "attention":
+        return 2 * nkv * (ctx + M) * hd * 2
+    if cls == "router":
+        return (c["n_experts"] + 1) * H * 2
+    return None
+
+
+def step_bytes(c, M, uniq_per_layer, ctx):
+    """algorithmic bytes of one whole verify step (BASELINE.md section 2 / SURVEY.md 8(d))"""
+    tot = 0
+    for u in uniq_per_layer:
+        tot += algorithmic_bytes("qkv", c, M, [u], ctx) + algorithmic_bytes("o_proj", c, M, [u], ctx)
+        tot += algorithmic_bytes("router", c, M, [u], ctx) + 2 * c["hidden"] * 4 + 2 * c["head_dim"] * 4
+        tot += (u + 1) * (2 * c["moe_ff"] * Q4_ROW(c["hidden"]) + c["hidden"] * Q4_ROW(c["moe_ff"]))
+        tot += algorithmic_bytes("attention", c, M, [u], ctx)
+    tot += algorithmic_bytes("lm_head", c, M, [0], ctx) + M * c["hidden"] * 4
+    return tot
+
+
+def cpu_baseline(M, threads):
+    """The oracle (the reference's CPU arithmetic restated, int8 path) on the host cores: a bounded sample of the
+    same workload, 1 of the 40 layers plus the final norm and lm_head at full shapes (timing-only random q4
+    bytes); the step time is extrapolated as t_head + 40 x t_layer."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+
+    po.lib.orc_set_threads(threads)
+    cfg = dict(C4)
+    cfg["n_layers"] = 1
+    om = po.Model(cfg, seed=SEED, ctx=CTX, fast=True)
+    toks = (np.arange(M) * 1000 + 7).astype(np.int32)
+    best = None
+    t_start = time.time()
+    reps = 0
+    while reps < 2 or (time.time() - t_start < 10 and reps < 5):
+        om.position = CTX
+        om.verify(toks)
+        tl, th = om.last_times()
+        est = th + C4["n_layers"] * tl
+        best = est if best is None else min(best, est)
+        reps += 1
+    return {"value": M / best, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"1 of 40 layers + final norm + lm_head at full shapes, M={M}, ctx {CTX}, int8 path, "
+                      f"best of {reps}; step = t_head + 40 x t_layer = {best * 1e3:.1f} ms"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--tree", action="store_true", help="verify the 17-row draft tree instead of the k=4 chain")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the verify step on one GPU only: the step of one sequence does not shard "
+              "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import geode_amd as g
+
+    g.init(0)
+    M = 17 if args.tree else 5
+    parents = tree_parents() if args.tree else None
+    m = g.VerifyModel(C4)
+    t0 = time.time()
+    m.randomize(SEED, 0.02, 0.0221, CTX)
+    g.check(g.lib.gv_synchronize())
+    t_init = time.time() - t0
+
+    # the drafts: the model's own greedy continuation of a token (each verified alone, then rolled back)
+    toks = [7]
+    m.position = CTX
+    for i in range(M - 1):
+        lg = m.verify(np.array([toks[-1]], np.int32))
+        toks.append(int(np.argmax(lg[0])))
+    toks = np.array(toks, np.int32)
+    if args.tree:   # a tree's first child of each node follows the chain, the rest other tokens
+        toks = np.array([(7 + 1000 * i) % C4["vocab"] for i in range(M)], np.int32)
+
+    def step():
+        m.position = CTX
+        m.verify(toks, parents, want_logits=False)
+
+    for _ in range(args.warmup):
+        step()
+    g.check(g.lib.gv_synchronize())
+    e0 = g.lib.gv_event_record()
+    for _ in range(args.steps):
+        step()
+    e1 = g.lib.gv_event_record()
+    ms = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+
+    # acceptance of the last step's logits: greedy sample-and-match (engine/src/geode.cpp:331-350)
+    m.position = CTX
+    logits = m.verify(toks, parents)
+    route = m.route_ids(M)
+    uniq = [len(np.unique(route[l])) for l in range(C4["n_layers"])]
+    if not args.tree:
+        emitted = 1
+        for i in range(M - 1):
+            if int(np.argmax(logits[i])) != int(toks[i + 1]):
+                break
+            emitted += 1
+    else:
+        emitted = 1
+        node = 0
+        while True:
+            y = int(np.argmax(logits[node]))
+            kids = [j for j in range(M) if parents[j] == node and toks[j] == y]
+            if not kids:
+                break
+            node = kids[0]
+            emitted += 1
+
+    # per kernel class: the summed event time over some timed steps; the dominant one gets the roofline
+    per_class = {}
+    for cls, name in enumerate(g.KERNEL_CLASSES):
+        m.time_kernel(cls)
+        for _ in range(3):
+            step()
+        tms, n = m.kernel_time()
+        per_class[name] = (tms / 3, n // 3)
+    m.time_kernel(-1)
+    dom = max((k for k in per_class if algorithmic_bytes(k, C4, M, uniq, CTX)), key=lambda k: per_class[k][0])
+    m.time_kernel(g.KERNEL_CLASSES.index(dom))
+    for _ in range(args.steps):
+        step()
+    dms, dn = m.kernel_time()
+    m.time_kernel(-1)
+    dom_avg_s = dms / dn / 1e3
+    dom_bytes = algorithmic_bytes(dom, C4, M, uniq, CTX)
+    achieved = dom_bytes / dom_avg_s
+
+    steps_s = 1e3 / ms
+    sbytes = step_bytes(C4, M, uniq, CTX)
+    out = {
+        "metric": "verify-step tok/s, 35B-A3B-shape MoE k=4; HBM GB/s vs peak",
+        "value": steps_s * emitted,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": ("C4 full 40-layer 35B-A3B-shape verify step, " +
+                                ("draft tree 16 nodes (4,3) + root, M=17" if args.tree else "chain k=4, M=5") +
+                                f", ctx {CTX}, vocab 151936, q4 weights, fp16 KV, int8-path products"),
+                   "rows": M, "tokens_emitted_per_step": emitted, "acceptance": "greedy sample-and-match on the "
+                   "step's logits; drafts = the target's own greedy chain" if not args.tree else "greedy tree walk"},
+        "verify_steps_per_s": steps_s,
+        "verified_rows_per_s": steps_s * M,
+        "step_hbm_gbs": sbytes / (ms / 1e3) / 1e9,
+        "step_roofline_frac": sbytes / (ms / 1e3) / PEAK_HBM,
+        "step_bytes": sbytes,
+        "distinct_experts_per_layer": float(np.mean(uniq)),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
+                     "bytes_per_launch": dom_bytes, "avg_launch_us": dom_avg_s * 1e6},
+        "kernel_ms_per_step": {k: round(v[0], 4) for k, v in per_class.items()},
+        "init_s": t_init,
+    }
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        out["cpu_baseline"] = cpu_baseline(M, threads)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

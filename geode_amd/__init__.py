@@ -68,7 +68,13 @@ SIGNATURES = {
     "gv_verify_keep": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_model_logits": (_P, [_P]),
     "gv_model_route_ids": (_c.c_int, [_P, _P]),
+    "gv_model_time_kernel": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
 }
+
+# kernel classes of a verify step (gv_model_time_kernel)
+KERNEL_CLASSES = ["embed", "quantize", "qkv", "rope_kv", "attention", "attn_merge", "o_proj", "router", "route",
+                  "moe_up", "swiglu", "moe_down", "combine", "lm_head"]
 
 
 class GeodeError(RuntimeError):
@@ -86,16 +92,30 @@ def _load():
     return lib
 
 
-lib = _load()
+_LIB = None
+
+
+def _lib():
+    """the loaded library (on first use: importing this package, e.g. for geode_amd.build, loads nothing)"""
+    global _LIB
+    if _LIB is None:
+        _LIB = _load()
+    return _LIB
+
+
+def __getattr__(name):   # geode_amd.lib
+    if name == "lib":
+        return _lib()
+    raise AttributeError(name)
 
 
 def check(rc, what=""):
     if rc != 0:
-        raise GeodeError(f"{what}: {lib.gv_last_error().decode()}")
+        raise GeodeError(f"{what}: {_lib().gv_last_error().decode()}")
 
 
 def init(device=0):
-    check(lib.gv_init(device), "gv_init")
+    check(_lib().gv_init(device), "gv_init")
 
 
 class DeviceBuffer:
@@ -103,9 +123,9 @@ class DeviceBuffer:
 
     def __init__(self, nbytes):
         self.nbytes = int(nbytes)
-        self.ptr = lib.gv_malloc(max(1, self.nbytes))
+        self.ptr = _lib().gv_malloc(max(1, self.nbytes))
         if not self.ptr:
-            raise GeodeError(f"gv_malloc({nbytes}): {lib.gv_last_error().decode()}")
+            raise GeodeError(f"gv_malloc({nbytes}): {_lib().gv_last_error().decode()}")
 
     @classmethod
     def from_array(cls, a):
@@ -117,23 +137,23 @@ class DeviceBuffer:
     def upload(self, a, offset=0):
         a = np.ascontiguousarray(a)
         assert offset + a.nbytes <= self.nbytes
-        check(lib.gv_memcpy_h2d(_c.c_void_p(self.ptr + offset), a.ctypes.data_as(_P), a.nbytes), "h2d")
+        check(_lib().gv_memcpy_h2d(_c.c_void_p(self.ptr + offset), a.ctypes.data_as(_P), a.nbytes), "h2d")
 
     def download(self, dtype, shape, offset=0):
         out = np.empty(shape, dtype)
         assert offset + out.nbytes <= self.nbytes
-        check(lib.gv_memcpy_d2h(out.ctypes.data_as(_P), _c.c_void_p(self.ptr + offset), out.nbytes), "d2h")
+        check(_lib().gv_memcpy_d2h(out.ctypes.data_as(_P), _c.c_void_p(self.ptr + offset), out.nbytes), "d2h")
         return out
 
     def zero(self):
-        check(lib.gv_memset(self.ptr, 0, self.nbytes), "memset")
+        check(_lib().gv_memset(self.ptr, 0, self.nbytes), "memset")
 
     def __int__(self):
         return self.ptr
 
     def free(self):
         if self.ptr:
-            lib.gv_free(self.ptr)
+            _lib().gv_free(self.ptr)
             self.ptr = None
 
     def __del__(self):
@@ -149,11 +169,11 @@ class Q4Matrix:
     def __init__(self, pack_bytes, rows, cols, global_):
         pack = np.ascontiguousarray(pack_bytes, np.uint8).reshape(rows, cols // 16 * 9)
         staging = DeviceBuffer.from_array(pack)
-        self.buf = DeviceBuffer(lib.gv_q4_device_bytes(rows, cols))
+        self.buf = DeviceBuffer(_lib().gv_q4_device_bytes(rows, cols))
         self.desc = GvQ4()
-        check(lib.gv_q4_from_pack(staging.ptr, rows, cols, global_, self.buf.ptr, _c.byref(self.desc)),
+        check(_lib().gv_q4_from_pack(staging.ptr, rows, cols, global_, self.buf.ptr, _c.byref(self.desc)),
               "gv_q4_from_pack")
-        check(lib.gv_synchronize(), "sync")
+        check(_lib().gv_synchronize(), "sync")
         staging.free()
         self.rows, self.cols = rows, cols
 
@@ -162,12 +182,12 @@ class Q4Matrix:
 
     def dequant(self):
         out = DeviceBuffer(self.rows * self.cols * 4)
-        check(lib.gv_q4_dequant(self.ref(), out.ptr), "gv_q4_dequant")
+        check(_lib().gv_q4_dequant(self.ref(), out.ptr), "gv_q4_dequant")
         return out.download(np.float32, (self.rows, self.cols))
 
 
 def act_bytes(cols):
-    return lib.gv_act_bytes(cols)
+    return _lib().gv_act_bytes(cols)
 
 
 def gemv(w: Q4Matrix, x: np.ndarray, accumulate_into=None):
@@ -176,11 +196,11 @@ def gemv(w: Q4Matrix, x: np.ndarray, accumulate_into=None):
     M = x.shape[0]
     dx = DeviceBuffer.from_array(x)
     act = DeviceBuffer(M * act_bytes(w.cols))
-    check(lib.gv_quantize(dx.ptr, w.cols, M, w.cols, None, 0.0, act.ptr, None), "gv_quantize")
+    check(_lib().gv_quantize(dx.ptr, w.cols, M, w.cols, None, 0.0, act.ptr, None), "gv_quantize")
     y = DeviceBuffer(M * w.rows * 4)
     if accumulate_into is not None:
         y.upload(np.ascontiguousarray(accumulate_into, np.float32))
-    check(lib.gv_gemv_q4(w.ref(), act.ptr, M, y.ptr, w.rows, int(accumulate_into is not None)), "gv_gemv_q4")
+    check(_lib().gv_gemv_q4(w.ref(), act.ptr, M, y.ptr, w.rows, int(accumulate_into is not None)), "gv_gemv_q4")
     return y.download(np.float32, (M, w.rows))
 
 
@@ -192,13 +212,13 @@ class VerifyModel:
         self.cfg = dict(cfg)
         c = GvModelConfig(**{k: cfg[k] for k, _ in GvModelConfig._fields_})
         err = _c.create_string_buffer(512)
-        self.h = lib.gv_model_create(_c.byref(c), err, 512)
+        self.h = _lib().gv_model_create(_c.byref(c), err, 512)
         if not self.h:
             raise GeodeError(f"gv_model_create: {err.value.decode()}")
 
     def close(self):
         if getattr(self, "h", None):
-            lib.gv_model_free(self.h)
+            _lib().gv_model_free(self.h)
             self.h = None
 
     def __del__(self):
@@ -210,34 +230,44 @@ class VerifyModel:
     def adopt(self, kind, data, layer=0, expert=0, globals_=None):
         data = np.ascontiguousarray(data)
         g = np.ascontiguousarray(globals_ if globals_ is not None else [0.0], np.float32)
-        check(lib.gv_model_adopt(self.h, kind, layer, expert, data.ctypes.data_as(_P), data.nbytes,
+        check(_lib().gv_model_adopt(self.h, kind, layer, expert, data.ctypes.data_as(_P), data.nbytes,
                                  g.ctypes.data_as(_P)), f"gv_model_adopt({kind}, {layer}, {expert})")
 
     def randomize(self, seed, sigma=0.02, router_sigma=0.0221, ctx=0):
-        check(lib.gv_model_randomize(self.h, seed, sigma, router_sigma, ctx), "gv_model_randomize")
+        check(_lib().gv_model_randomize(self.h, seed, sigma, router_sigma, ctx), "gv_model_randomize")
 
     @property
     def position(self):
-        return lib.gv_model_position(self.h)
+        return _lib().gv_model_position(self.h)
 
     @position.setter
     def position(self, p):
-        check(lib.gv_model_set_position(self.h, p), "gv_model_set_position")
+        check(_lib().gv_model_set_position(self.h, p), "gv_model_set_position")
 
     def verify(self, tokens, parents=None, want_logits=True):
         tokens = np.ascontiguousarray(tokens, np.int32)
         n = tokens.size
         par = np.ascontiguousarray(parents, np.int32) if parents is not None else None
         out = np.empty((n, self.cfg["vocab"]), np.float32) if want_logits else None
-        check(lib.gv_verify(self.h, tokens.ctypes.data_as(_P), n, par.ctypes.data_as(_P) if par is not None else None,
+        check(_lib().gv_verify(self.h, tokens.ctypes.data_as(_P), n, par.ctypes.data_as(_P) if par is not None else None,
                             out.ctypes.data_as(_P) if out is not None else None), "gv_verify")
         return out
 
     def keep(self, kept, path=None):
         p = np.ascontiguousarray(path, np.int32) if path is not None else None
-        check(lib.gv_verify_keep(self.h, kept, p.ctypes.data_as(_P) if p is not None else None), "gv_verify_keep")
+        check(_lib().gv_verify_keep(self.h, kept, p.ctypes.data_as(_P) if p is not None else None), "gv_verify_keep")
+
+    def time_kernel(self, cls):
+        """events around every launch of kernel class cls (an index into KERNEL_CLASSES; -1 off) from now on"""
+        check(_lib().gv_model_time_kernel(self.h, cls), "gv_model_time_kernel")
+
+    def kernel_time(self):
+        """(summed ms, launches) of the timed class since time_kernel"""
+        ms, n = _c.c_float(0), _c.c_int(0)
+        check(_lib().gv_model_kernel_time(self.h, _c.byref(ms), _c.byref(n)), "gv_model_kernel_time")
+        return ms.value, n.value
 
     def route_ids(self, n):
         out = np.empty((self.cfg["n_layers"], n, self.cfg["top_k"]), np.int32)
-        check(lib.gv_model_route_ids(self.h, out.ctypes.data_as(_P)), "gv_model_route_ids")
+        check(_lib().gv_model_route_ids(self.h, out.ctypes.data_as(_P)), "gv_model_route_ids")
         return out

@@ -58,15 +58,26 @@ __device__ inline double block_sum_double(double v, double *red) {
     return r;
 }
 
+// The device KV cache of one layer: K [nkv][slots][hd] and V [nkv][slots / 64][hd][64] in fp16 (V transposed in
+// blocks of kAttnBlock positions, so that the MFMA operands of both products are contiguous loads).
+__device__ __host__ inline int64_t k_index(int64_t slots, int hd, int kh, int64_t slot, int d) {
+    return (static_cast<int64_t>(kh) * slots + slot) * hd + d;
+}
+__device__ __host__ inline int64_t v_index(int64_t slots, int hd, int nkv, int kh, int64_t slot, int d) {
+    return static_cast<int64_t>(nkv) * slots * hd +
+           ((static_cast<int64_t>(kh) * (slots / kAttnBlock) + slot / kAttnBlock) * hd + d) * kAttnBlock + slot % kAttnBlock;
+}
+
 // Per (row, head): the query heads' and key heads' RMSNorm(1 + w) then partial RoPE on the first rope_dim dims
 // (pairs i, i + half; model.cpp:3714-3733, rotary position pos + depth), the keys and values appended to the fp16
-// cache at slot pos + row (static_cast<_Float16>: round to nearest even). Query heads go to q_out [M][nh][hd].
+// cache at slot pos + row (static_cast<_Float16>: round to nearest even). Query heads go to q_out as two fp16
+// arrays [M][nh][hd], hi then lo (hi + lo = the fp32 query to 2^-22), the MFMA operands of the scores.
 __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ qkv, int64_t ldq, int nh, int nkv, int hd,
                                                       int half, const float *__restrict__ q_norm,
                                                       const float *__restrict__ k_norm, float eps,
                                                       const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                                                      const StepParams *__restrict__ sp, float *__restrict__ q_out,
-                                                      uint16_t *__restrict__ kv, int max_ctx) {
+                                                      const StepParams *__restrict__ sp, _Float16 *__restrict__ q_out,
+                                                      _Float16 *__restrict__ kv, int64_t slots) {
     const int t = blockIdx.x, head = blockIdx.y, i = threadIdx.x;
     if (t >= sp->M) return;
     __shared__ double red[256];
@@ -92,7 +103,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
     }
     const float xv = i < hd ? src[i] : 0.0f;
     if (kind == 2) {
-        if (i < hd) kv[(static_cast<int64_t>(max_ctx) + slot) * kv_row + kh * hd + i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(xv));
+        if (i < hd) kv[v_index(slots, hd, nkv, kh, slot, i)] = static_cast<_Float16>(xv);
         return;
     }
     const double ss = block_sum_double(static_cast<double>(xv) * static_cast<double>(xv), red);
@@ -110,131 +121,162 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
         const float c = cos_t[static_cast<int64_t>(p) * half + j], s = sin_t[static_cast<int64_t>(p) * half + j];
         out = __fadd_rn(__fmul_rn(v[i], c), __fmul_rn(v[j], s));
     }
-    if (kind == 0) q_out[(static_cast<int64_t>(t) * nh + head) * hd + i] = out;
-    else kv[static_cast<int64_t>(slot) * kv_row + kh * hd + i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(out));
+    if (kind == 0) {   // the query as two halves, hi + lo, for near-fp32 scores from fp16 products
+        const int64_t qo = (static_cast<int64_t>(t) * nh + head) * hd + i;
+        const _Float16 hi = static_cast<_Float16>(out);
+        q_out[qo] = hi;
+        q_out[qo + static_cast<int64_t>(sp->M) * nh * hd] = static_cast<_Float16>(out - static_cast<float>(hi));
+    } else {
+        kv[k_index(slots, hd, kh, slot, i)] = static_cast<_Float16>(out);
+    }
 }
 
-// Split-KV attention (flash decoding over blocks of kAttnBlock positions): a workgroup per (block, KV head) takes the
-// group of query heads that share the KV head for every row; scores q.k / sqrt(hd) (eight partial sums in the
-// reference's order, model.cpp:3927-3948), masked to the context plus the row's visible rows, the block's maximum,
-// exp(score - max), their sum and the weighted values: parts [M][nh][blocks][hd + 2] (model.cpp:3990-4018).
-__global__ __launch_bounds__(256) void attn_part_kernel(const float *__restrict__ q_out, const uint16_t *__restrict__ kv,
-                                                        int max_ctx, int nh, int nkv, int hd,
-                                                        const StepParams *__restrict__ sp, float *__restrict__ parts,
-                                                        int nb_max) {
-    extern __shared__ uint4 lds_u4[];
-    const int b = blockIdx.x, kh = blockIdx.y;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+// Split-KV attention on the matrix cores: a wave per (16 queries, block of 64 positions, KV head); the queries of a
+// KV head are its query heads x the rows. S^T = K Q^T (v_mfma_f32_16x16x32_f16: fp16 keys, the queries as hi + lo
+// fp16 halves, fp32 sums), masked to the context plus each row's visible rows, then per query the block's
+// maximum, the weights exp(s - max) and their sum; O^T = V^T P^T with the weights as hi + lo halves. Writes the block's
+// partial (weighted values, max, sum) as attend_heads does per block (model.cpp:3894-4018); attn_merge joins them.
+__global__ __launch_bounds__(64) void attn_mfma_kernel(const _Float16 *__restrict__ q16, const _Float16 *__restrict__ kv,
+                                                       int64_t slots, int nh, int nkv, int hd,
+                                                       const StepParams *__restrict__ sp, float *__restrict__ parts,
+                                                       int nb_max) {
+    const int qt = blockIdx.x, b = blockIdx.y, kh = blockIdx.z;
     const int pos = sp->pos, M = sp->M, total = pos + M;
-    const int s0 = b * kAttnBlock;
-    if (s0 >= total) return;
-    const int ns = min(kAttnBlock, total - s0);
     const int group = nh / nkv, NQ = group * M;
-    const int64_t kv_row = static_cast<int64_t>(nkv) * hd;
-    uint16_t *Kt = reinterpret_cast<uint16_t *>(lds_u4);
-    uint16_t *Vt = Kt + kAttnBlock * hd;
-    float *Qc = reinterpret_cast<float *>(Vt + kAttnBlock * hd);   // [16][hd]
-    float *Sc = Qc + 16 * hd;                                       // [16][kAttnBlock]
-    for (int idx = threadIdx.x; idx < ns * hd; idx += blockDim.x) {
-        const int s = idx / hd, d = idx % hd;
-        Kt[idx] = kv[static_cast<int64_t>(s0 + s) * kv_row + kh * hd + d];
-        Vt[idx] = kv[(static_cast<int64_t>(max_ctx) + s0 + s) * kv_row + kh * hd + d];
+    const int s0 = b * kAttnBlock;
+    if (s0 >= total || qt * 16 >= NQ) return;
+    const int l = threadIdx.x, lq = l % 16, lg = l / 16;
+    const int qi = qt * 16 + lq;
+    const bool qvalid = qi < NQ;
+    const int tq = qvalid ? qi / group : 0, hq = kh * group + (qvalid ? qi % group : 0);
+    const int nch = hd / 32;
+    // the queries as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query lq
+    half8 qb[8], ql[8];
+    const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+        const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        const int64_t qo = (static_cast<int64_t>(tq) * nh + hq) * hd + ch * 32 + 8 * lg;
+        qb[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qo) : z;
+        ql[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
     }
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(hd)));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int qc = 0; qc < NQ; qc += 16) {
-        const int nq = min(16, NQ - qc);
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < nq * hd; idx += blockDim.x) {
-            const int j = idx / hd, d = idx % hd, qi = qc + j;
-            const int t = qi / group, h = kh * group + qi % group;
-            Qc[idx] = q_out[(static_cast<int64_t>(t) * nh + h) * hd + d];
-        }
-        __syncthreads();
-        for (int pr = threadIdx.x; pr < nq * ns; pr += blockDim.x) {
-            const int j = pr / ns, s = pr % ns, slot = s0 + s, t = (qc + j) / group;
-            const bool visible = slot < pos || ((sp->vis[t] >> (slot - pos)) & 1u);
-            float sv = -__builtin_inff();
-            if (visible) {
-                float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                const float *q = Qc + j * hd;
-                const uint16_t *k = Kt + s * hd;
-                for (int d = 0; d < hd; d += 8)
+    const uint32_t vis = qvalid ? sp->vis[tq] : 0u;
+    float sc[4][4];
+    float mx = -__builtin_inff();
 #pragma unroll
-                    for (int u = 0; u < 8; ++u)
-                        acc[u] = __fadd_rn(acc[u], __fmul_rn(q[d + u], static_cast<float>(__builtin_bit_cast(_Float16, k[d + u]))));
-                const float dot = __fadd_rn(__fadd_rn(__fadd_rn(acc[0], acc[4]), __fadd_rn(acc[1], acc[5])),
-                                            __fadd_rn(__fadd_rn(acc[2], acc[6]), __fadd_rn(acc[3], acc[7])));
-                sv = __fmul_rn(dot, scale);
-            }
-            Sc[j * kAttnBlock + s] = sv;
+    for (int pt = 0; pt < 4; ++pt) {
+        float4v c = {0, 0, 0, 0};
+        const _Float16 *krow = kv + k_index(slots, hd, kh, s0 + pt * 16 + lq, 8 * lg);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) {
+            if (ch >= nch) break;
+            const half8 a = *reinterpret_cast<const half8 *>(krow + ch * 32);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ch], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ch], c, 0, 0, 0);
         }
-        __syncthreads();
-        __shared__ float ml[16][2];
-        for (int j = wave; j < nq; j += 4) {
-            const float sv = lane < ns ? Sc[j * kAttnBlock + lane] : -__builtin_inff();
-            const float mx = wave_max(sv);
-            const float e = (sv == -__builtin_inff()) ? 0.0f : expf(__fsub_rn(sv, mx));
-            float l = e;
-            for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-            if (lane < ns) Sc[j * kAttnBlock + lane] = e;
-            if (lane == 0) {
-                ml[j][0] = mx;
-                ml[j][1] = l;
-            }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {   // S^T[position pt*16 + 4 lg + r][query lq]
+            const int slot = s0 + pt * 16 + 4 * lg + r;
+            const bool ok = qvalid && slot < total && (slot < pos || ((vis >> (slot - pos)) & 1u));
+            sc[pt][r] = ok ? c[r] * scale : -__builtin_inff();
+            mx = fmaxf(mx, sc[pt][r]);
         }
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < nq * hd; idx += blockDim.x) {
-            const int j = idx / hd, d = idx % hd, qi = qc + j;
-            const int t = qi / group, h = kh * group + qi % group;
-            float o = 0.0f;
-            for (int s = 0; s < ns; ++s)
-                o = __builtin_fmaf(Sc[j * kAttnBlock + s], static_cast<float>(__builtin_bit_cast(_Float16, Vt[s * hd + d])), o);
-            float *dst = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max + b) * (hd + 2);
-            dst[d] = o;
-            if (d == 0) {
-                dst[hd] = ml[j][0];
-                dst[hd + 1] = ml[j][1];
-            }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float lsum = 0.0f;
+    half4 pe[4], pl[4];   // the weights as hi + lo halves
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float e = sc[pt][r] == -__builtin_inff() ? 0.0f : expf(sc[pt][r] - mx);
+            const _Float16 eh = static_cast<_Float16>(e);
+            pe[pt][r] = eh;
+            pl[pt][r] = static_cast<_Float16>(e - static_cast<float>(eh));
+            lsum += e;
         }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    // P^T operands of the two 32-position chunks: k-slot j < 4 is position 32 kc + 4 lg + j, j >= 4 is
+    // 32 kc + 16 + 4 lg + j - 4; the V^T operands take the same positions
+    half8 pb[2], pbl[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            pb[kc][j] = pe[2 * kc][j];
+            pb[kc][4 + j] = pe[2 * kc + 1][j];
+            pbl[kc][j] = pl[2 * kc][j];
+            pbl[kc][4 + j] = pl[2 * kc + 1][j];
+        }
+    float *dst = parts + ((static_cast<int64_t>(tq) * nh + hq) * nb_max + b) * (hd + 2);
+    const _Float16 *vblk = kv + v_index(slots, hd, nkv, kh, s0, 0);   // [hd][64] of this block
+    for (int dt = 0; dt < hd / 16; ++dt) {
+        float4v c = {0, 0, 0, 0};
+        const _Float16 *vrow = vblk + static_cast<int64_t>(dt * 16 + lq) * kAttnBlock;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
+            const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
+            const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[kc], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pbl[kc], c, 0, 0, 0);
+        }
+        // O^T[dim dt*16 + 4 lg + r][query lq]
+        if (qvalid) *reinterpret_cast<float4 *>(dst + dt * 16 + 4 * lg) = make_float4(c[0], c[1], c[2], c[3]);
+    }
+    if (qvalid && lg == 0) {
+        dst[hd] = mx;
+        dst[hd + 1] = lsum;
     }
 }
 
 // The blocks joined per (row, head): exp(block max - max), the sums, 1 / sum, times sigmoid(gate)
-// (model.cpp:3830-3855); the row's core then quantized for o_proj.
+// (model.cpp:3830-3855). A workgroup per (row, head); the blocks' weights computed once.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ parts, const float *__restrict__ qkv,
                                                          int64_t ldq, int nh, int hd, int nb_max,
-                                                         const StepParams *__restrict__ sp, float *__restrict__ core,
-                                                         uint8_t *__restrict__ act_core, int64_t act_stride) {
-    extern __shared__ uint4 lds_u4[];
-    float *row = reinterpret_cast<float *>(lds_u4);
-    const int t = blockIdx.x;
+                                                         const StepParams *__restrict__ sp, float *__restrict__ core) {
+    __shared__ float fw[1024];
+    __shared__ float lsum;
+    const int t = blockIdx.x, h = blockIdx.y;
     if (t >= sp->M) return;
     const int nbw = (sp->pos + sp->M + kAttnBlock - 1) / kAttnBlock;
-    for (int idx = threadIdx.x; idx < nh * hd; idx += blockDim.x) {
-        const int h = idx / hd, d = idx % hd;
-        const float *base = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max) * (hd + 2);
+    const float *base = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max) * (hd + 2);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave == 0) {
         float mx = -__builtin_inff();
-        for (int b = 0; b < nbw; ++b) mx = fmaxf(mx, base[b * (hd + 2) + hd]);
-        float o = 0.0f, l = 0.0f;
-        for (int b = 0; b < nbw; ++b) {
-            const float *pb = base + b * (hd + 2);
-            const float f = pb[hd] == -__builtin_inff() ? 0.0f : expf(__fsub_rn(pb[hd], mx));
-            l = __fadd_rn(l, __fmul_rn(pb[hd + 1], f));
-            o = __fadd_rn(o, __fmul_rn(pb[d], f));
+        for (int b = lane; b < nbw; b += 64) mx = fmaxf(mx, base[b * (hd + 2) + hd]);
+        mx = wave_max(mx);
+        float l = 0.0f;
+        for (int b = lane; b < nbw; b += 64) {
+            const float mb = base[b * (hd + 2) + hd];
+            const float f = mb == -__builtin_inff() ? 0.0f : expf(__fsub_rn(mb, mx));
+            fw[b] = f;
+            l = __builtin_fmaf(base[b * (hd + 2) + hd + 1], f, l);
         }
-        const float gate = qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + d];
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate)));
-        const float val = __fmul_rn(__fmul_rn(o, __fdiv_rn(1.0f, l)), sig);
-        row[idx] = val;
-        core[static_cast<int64_t>(t) * nh * hd + idx] = val;
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        if (lane == 0) lsum = l;
     }
     __syncthreads();
-    quantize_row(row, nh * hd, act_core + t * act_stride);
+    const float inv = __fdiv_rn(1.0f, lsum);
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float o = 0.0f;
+        for (int b = 0; b < nbw; ++b) o = __builtin_fmaf(base[b * (hd + 2) + d], fw[b], o);
+        const float gate = qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + d];
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate)));
+        core[(static_cast<int64_t>(t) * nh + h) * hd + d] = __fmul_rn(__fmul_rn(o, inv), sig);
+    }
 }
 
 // Router logits: bf16 rows [E + 1][H] (the shared expert's gate row last) times the post-norm rows, eight partial
 // sums per row in the reference's fixed order (bf16_row_dots, kernels.cpp:1446-1483). A wave per row, its lanes
-// 8 tokens x 8 partial sums.
+// 8 tokens x 8 partial sums; loads in chunks of 32 columns ahead of the sequential sums.
 __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict__ w, int E1, int H,
                                                      const float *__restrict__ h, const StepParams *__restrict__ sp,
                                                      float *__restrict__ logits) {
@@ -245,104 +287,136 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     const uint16_t *row = w + static_cast<int64_t>(r) * H;
     for (int t0 = 0; t0 < M; t0 += 8) {
         const int t = t0 + lane / 8, j = lane % 8;
+        const bool live = t < M;
+        const float *x = h + static_cast<int64_t>(live ? t : 0) * H;
         float acc = 0.0f;
-        if (t < M) {
-            const float *x = h + static_cast<int64_t>(t) * H;
-            for (int c = 0; c < H; c += 8) {
-                const float wf = __uint_as_float(static_cast<uint32_t>(row[c + j]) << 16);
-                acc = __fadd_rn(acc, __fmul_rn(wf, x[c + j]));
+        for (int c0 = 0; c0 < H; c0 += 256) {
+            float wf[32], xv[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                wf[u] = __uint_as_float(static_cast<uint32_t>(row[c0 + u * 8 + j]) << 16);
+                xv[u] = x[c0 + u * 8 + j];
             }
+#pragma unroll
+            for (int u = 0; u < 32; ++u) acc = __fadd_rn(acc, __fmul_rn(wf[u], xv[u]));
         }
         const float s = __fadd_rn(acc, __shfl_down(acc, 4, 64));          // lanes j < 4: a_j + a_{j+4}
         const float s2 = __fadd_rn(s, __shfl_down(s, 1, 64));             // j = 0: s0 + s1, j = 2: s2 + s3
         const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));           // j = 0: (s0 + s1) + (s2 + s3)
-        if (j == 0 && t < M) logits[static_cast<int64_t>(t) * E1 + r] = s3;
+        if (j == 0 && live) logits[static_cast<int64_t>(t) * E1 + r] = s3;
     }
 }
 
 // The route (route_topk, model.cpp:4021-4065): softmax over the experts (max, expf, the sum in index order, divide),
 // the top K by probability with ties to the lower index, the weights p / (their sum in rank order); the shared
-// expert's gate sigmoid(logit); then the slots (distinct experts ascending, the shared one last) and their picks.
-__global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ logits, int E, int K,
+// expert's gate sigmoid(logit); then the slots (distinct experts ascending, the shared one last) and their picks
+// ordered by (expert, token, rank), each pick placed by counting, so the order never depends on timing.
+__global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ logits, int E, int K,
                                                     const StepParams *__restrict__ sp, RouteState *__restrict__ rs,
                                                     int32_t *__restrict__ ids_out) {
     __shared__ float p[kMaxRows][256];
     __shared__ int ids[kMaxRows * 16];
-    __shared__ int cursor[257];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ int cnt[257], start[257], slot_of[257];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int M = sp->M, E1 = E + 1;
-    for (int t = wave; t < M; t += 4) {
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
+    for (int t = wave; t < M; t += waves) {
         const float *lg = logits + static_cast<int64_t>(t) * E1;
+        float v[4];
         float mx = -__builtin_inff();
-        for (int e = lane; e < E; e += 64) mx = fmaxf(mx, lg[e]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            v[i] = e < E ? lg[e] : -__builtin_inff();
+            mx = fmaxf(mx, v[i]);
+        }
         mx = wave_max(mx);
-        for (int e = lane; e < E; e += 64) p[t][e] = expf(__fsub_rn(lg[e], mx));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E) p[t][e] = expf(__fsub_rn(v[i], mx));
+        }
         __builtin_amdgcn_wave_barrier();
         float sum = 0.0f;
-        if (lane == 0)
-            for (int e = 0; e < E; ++e) sum = __fadd_rn(sum, p[t][e]);
+        if (lane == 0) {   // index order, as the reference; four values a load
+            int e = 0;
+            for (; e + 4 <= E; e += 4) {
+                const float4 v4 = *reinterpret_cast<const float4 *>(&p[t][e]);
+                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4.x), v4.y), v4.z), v4.w);
+            }
+            for (; e < E; ++e) sum = __fadd_rn(sum, p[t][e]);
+        }
         sum = __shfl(sum, 0, 64);
-        for (int e = lane; e < E; e += 64) p[t][e] = __fdiv_rn(p[t][e], sum);
-        __builtin_amdgcn_wave_barrier();
-        float top = 0.0f;
-        float pk[16];
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            pv[i] = e < E ? __fdiv_rn(p[t][e], sum) : -1.0f;
+        }
+        float top = 0.0f, mine = 0.0f;
         for (int k = 0; k < K; ++k) {
             float bv = -1.0f;
             int bi = E;
-            for (int e = lane; e < E; e += 64) {
-                bool taken = false;
-                for (int q = 0; q < k; ++q) taken |= ids[t * 16 + q] == e;
-                const float v = p[t][e];
-                if (!taken && (v > bv || (v == bv && e < bi))) bv = v, bi = e;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = lane + 64 * i;
+                if (pv[i] > bv || (pv[i] == bv && e < bi)) bv = pv[i], bi = e;
             }
             for (int o = 32; o > 0; o >>= 1) {
                 const float ov = __shfl_xor(bv, o, 64);
                 const int oi = __shfl_xor(bi, o, 64);
                 if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (lane + 64 * i == bi) pv[i] = -1.0f;   // taken
+            if (lane == k) mine = bv;
             if (lane == 0) ids[t * 16 + k] = bi;
-            __builtin_amdgcn_wave_barrier();
-            pk[k] = bv;
-            top = __fadd_rn(top, bv);
+            top = __fadd_rn(top, bv);   // rank order
         }
         if (lane < K) {
-            float mine = 0.0f;
-            for (int k = 0; k < K; ++k)
-                if (k == lane) mine = pk[k];
             rs->weight[t * K + lane] = __fdiv_rn(mine, top);
             ids_out[t * K + lane] = ids[t * 16 + lane];
         }
         if (lane == 0) rs->gate[t] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[E])));
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
-    for (int e = 0; e <= E; ++e) cursor[e] = 0;
-    for (int t = 0; t < M; ++t)
-        for (int k = 0; k < K; ++k) ++cursor[ids[t * 16 + k]];
-    cursor[E] = M;
-    int u = 0, run = 0;
-    for (int e = 0; e <= E; ++e) {
-        const int c = cursor[e];
-        cursor[e] = run;
-        if (c > 0) {
-            rs->slot_expert[u] = e;
-            rs->slot_start[u] = run;
-            rs->slot_count[u] = c;
-            ++u;
+    // counts per expert (the shared expert, E, once per row)
+    for (int i = threadIdx.x; i < M * K; i += blockDim.x) atomicAdd(&cnt[ids[(i / K) * 16 + i % K]], 1);
+    if (threadIdx.x == 0) cnt[E] = M;
+    __syncthreads();
+    if (threadIdx.x == 0) {   // exclusive scans over 257 counters: starts and slot numbers
+        int run = 0, u = 0;
+        for (int e = 0; e <= E; ++e) {
+            start[e] = run;
+            slot_of[e] = cnt[e] > 0 ? u : -1;
+            run += cnt[e];
+            u += cnt[e] > 0;
         }
-        run += c;
+        rs->n_slots = u;
+        rs->n_picks = run;
     }
-    rs->n_slots = u;
-    rs->n_picks = run;
-    for (int t = 0; t < M; ++t) {
-        for (int k = 0; k < K; ++k) {
-            const int pk_ = cursor[ids[t * 16 + k]]++;
-            rs->pick_token[pk_] = t;
-            rs->pick_of[t * (K + 1) + k] = pk_;
+    __syncthreads();
+    for (int e = threadIdx.x; e <= E; e += blockDim.x)
+        if (slot_of[e] >= 0) {
+            rs->slot_expert[slot_of[e]] = e;
+            rs->slot_start[slot_of[e]] = start[e];
+            rs->slot_count[slot_of[e]] = cnt[e];
         }
-        const int ps = cursor[E]++;
-        rs->pick_token[ps] = t;
-        rs->pick_of[t * (K + 1) + K] = ps;
+    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
+    for (int i = threadIdx.x; i < M * (K + 1); i += blockDim.x) {
+        const int t = i / (K + 1), k = i % (K + 1);
+        const int e = k < K ? ids[t * 16 + k] : E;
+        int before = 0;
+        if (k < K) {
+            for (int t2 = 0; t2 < t; ++t2)
+                for (int k2 = 0; k2 < K; ++k2) before += ids[t2 * 16 + k2] == e;
+        } else {
+            before = t;
+        }
+        const int pk = start[e] + before;
+        rs->pick_token[pk] = t;
+        rs->pick_of[t * (K + 1) + k] = pk;
     }
 }
 
@@ -407,36 +481,51 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
     quantize_row(m, F, act_m + static_cast<int64_t>(p) * (F / 32) * kActChunkBytes);
 }
 
-// x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365)
+// x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365); a workgroup per
+// (row, 256 columns)
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K,
                                                       const RouteState *__restrict__ rs,
                                                       const StepParams *__restrict__ sp, float *__restrict__ x) {
-    const int t = blockIdx.x;
-    if (t >= sp->M) return;
+    const int t = blockIdx.x, i = blockIdx.y * blockDim.x + threadIdx.x;
+    if (t >= sp->M || i >= H) return;
     const float gs = rs->gate[t];
-    const float *sh = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + K]) * H;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        float o = __fmul_rn(gs, sh[i]);
-        for (int k = 0; k < K; ++k) {
-            const float wk = rs->weight[t * K + k];
-            if (wk == 0.0f) continue;
-            o = __fadd_rn(o, __fmul_rn(wk, y[static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + i]));
-        }
-        x[static_cast<int64_t>(t) * H + i] = __fadd_rn(x[static_cast<int64_t>(t) * H + i], o);
+    float o = __fmul_rn(gs, y[static_cast<int64_t>(rs->pick_of[t * (K + 1) + K]) * H + i]);
+    for (int k = 0; k < K; ++k) {
+        const float wk = rs->weight[t * K + k];
+        if (wk == 0.0f) continue;
+        o = __fadd_rn(o, __fmul_rn(wk, y[static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + i]));
+    }
+    x[static_cast<int64_t>(t) * H + i] = __fadd_rn(x[static_cast<int64_t>(t) * H + i], o);
+}
+
+// verify_keep of a tree: the kept path's keys and values moved to the kept slots in every layer; a thread per
+// (layer, KV head, dim)
+__global__ void kv_compact_kernel(_Float16 *kv_all, int n_layers, int nkv, int hd, int64_t slots, int pos, int kept,
+                                  const int *__restrict__ path) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(n_layers) * nkv * hd) return;
+    const int l = static_cast<int>(i / (static_cast<int64_t>(nkv) * hd)), kh = static_cast<int>((i / hd) % nkv);
+    const int d = static_cast<int>(i % hd);
+    _Float16 *kv = kv_all + static_cast<int64_t>(l) * 2 * nkv * slots * hd;
+    for (int j = 1; j < kept; ++j) {   // ascending: path[j] >= j, so no source is overwritten before it is read
+        if (path[j] == j) continue;
+        kv[k_index(slots, hd, kh, pos + j, d)] = kv[k_index(slots, hd, kh, pos + path[j], d)];
+        kv[v_index(slots, hd, nkv, kh, pos + j, d)] = kv[v_index(slots, hd, nkv, kh, pos + path[j], d)];
     }
 }
 
-// verify_keep of a tree: the kept path's KV rows moved to the kept slots in every layer
-__global__ void kv_compact_kernel(uint16_t *kv_all, int n_layers, int max_ctx, int64_t kv_row, int pos, int kept,
-                                  const int *__restrict__ path) {
+// positions [0, n) of the reference's layout ([K, V][position][nkv * hd], fp32 here) into the device layout
+__global__ void kv_from_rows_kernel(const float *__restrict__ src, int n, int nkv, int hd, int64_t slots,
+                                    _Float16 *__restrict__ kv) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t per_layer = 2 * kv_row;
-    if (i >= n_layers * per_layer) return;
-    const int l = static_cast<int>(i / per_layer), kvi = static_cast<int>((i % per_layer) / kv_row);
-    const int64_t d = i % kv_row;
-    uint16_t *base = kv_all + (static_cast<int64_t>(l) * 2 + kvi) * max_ctx * kv_row;
-    for (int j = 1; j < kept; ++j)   // ascending: path[j] >= j, so no source is overwritten before it is read
-        if (path[j] != j) base[(pos + j) * kv_row + d] = base[(pos + path[j]) * kv_row + d];
+    const int64_t kv_row = static_cast<int64_t>(nkv) * hd;
+    if (i >= 2 * n * kv_row) return;
+    const int which = static_cast<int>(i / (n * kv_row));
+    const int p = static_cast<int>((i / kv_row) % n);
+    const int kh = static_cast<int>((i % kv_row) / hd), d = static_cast<int>(i % hd);
+    const _Float16 v = static_cast<_Float16>(src[i]);
+    if (which == 0) kv[k_index(slots, hd, kh, p, d)] = v;
+    else kv[v_index(slots, hd, nkv, kh, p, d)] = v;
 }
 
 __global__ void f32_to_bf16_kernel(const float *__restrict__ x, int64_t n, uint16_t *__restrict__ y) {
@@ -514,40 +603,112 @@ GemvOut qkv_out(const Model &m, const LayerW &L) {
     return o;
 }
 
+// events around the launches of the timed kernel class
+struct Tick {
+    Model &m;
+    int cls;
+    hipStream_t st;
+    bool on;
+    Tick(Model &mm, int c, hipStream_t s) : m(mm), cls(c), st(s), on(mm.timed_class == c) { mark(); }
+    ~Tick() { mark(); }
+    void mark() {
+        if (!on) return;
+        if (m.events_used == m.events.size()) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) {
+                on = false;
+                return;
+            }
+            m.events.push_back(e);
+        }
+        (void)hipEventRecord(m.events[m.events_used++], st);
+    }
+};
+
 int run_layers(Model &m, int M, hipStream_t st) {
     const auto &c = m.c;
     const int H = c.hidden, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     const int64_t abH = static_cast<int64_t>(act_bytes(H)), abC = static_cast<int64_t>(act_bytes(static_cast<int64_t>(nh) * hd));
-    const size_t lds_attn = (2 * static_cast<size_t>(kAttnBlock) * hd) * 2 + 16 * static_cast<size_t>(hd) * 4 +
-                            16 * static_cast<size_t>(kAttnBlock) * 4;
-    static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&attn_part_kernel), lds_attn, granted) != 0) return -1;
-    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x);
+    {
+        Tick tk(m, GV_K_EMBED, st);
+        hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x);
+    }
     for (int l = 0; l < c.n_layers; ++l) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
-        if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
-        if (gemv_q4(L.qkv, m.act_h, abH, M, qkv_out(m, L), st) != 0) return -1;
-        hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
-                           c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q_out, L.kv,
-                           c.max_ctx);
-        hipLaunchKernelGGL(attn_part_kernel, dim3(m.kv_blocks, nkv), dim3(256), lds_attn, st, m.q_out, L.kv, c.max_ctx,
-                           nh, nkv, hd, m.sp, m.parts, m.kv_blocks);
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(M), dim3(256), static_cast<size_t>(nh) * hd * 4, st, m.parts,
-                           m.qkv_out, L.qkv.rows, nh, hd, m.kv_blocks, m.sp, m.core, m.act_core, abC);
-        if (gemv_q4(L.o, m.act_core, abC, M, gemv_out(m.x, H, L.o.global, 1), st) != 0) return -1;
-        if (quantize_act(m.x, H, M, H, L.post_norm, c.eps, m.act_h, abH, m.h, H, st) != 0) return -1;
-        hipLaunchKernelGGL(router_kernel, dim3((m.E1 + 3) / 4), dim3(256), 0, st, L.router, m.E1, H, m.h, m.sp,
-                           m.rlogits);
-        hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
-                           m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
-        if (moe_products(m, L, M, true, st) != 0) return -1;
-        hipLaunchKernelGGL(swiglu_quant_kernel, dim3(m.max_picks), dim3(256), static_cast<size_t>(c.moe_ff) * 4, st,
-                           m.gu_out, c.moe_ff, m.route + l, m.act_m);
-        if (moe_products(m, L, M, false, st) != 0) return -1;
-        hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, m.route + l, m.sp, m.x);
+        {
+            Tick tk(m, GV_K_QUANT, st);
+            if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_QKV, st);
+            if (gemv_q4(L.qkv, m.act_h, abH, M, qkv_out(m, L), st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_ROPE, st);
+            hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
+                               c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
+                               m.slots);
+        }
+        const int qtiles = (nh / nkv * M + 15) / 16;
+        {
+            Tick tk(m, GV_K_ATTN, st);
+            hipLaunchKernelGGL(attn_mfma_kernel, dim3(qtiles, m.kv_blocks, nkv), dim3(64), 0, st, m.q16, L.kv, m.slots, nh,
+                               nkv, hd, m.sp, m.parts, m.kv_blocks);
+        }
+        {
+            Tick tk(m, GV_K_MERGE, st);
+            hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
+                               m.kv_blocks, m.sp, m.core);
+        }
+        {
+            Tick tk(m, GV_K_QUANT, st);
+            if (quantize_act(m.core, nh * hd, M, nh * hd, nullptr, 0.0f, m.act_core, abC, nullptr, 0, st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_O, st);
+            if (gemv_q4(L.o, m.act_core, abC, M, gemv_out(m.x, H, L.o.global, 1), st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_QUANT, st);
+            if (quantize_act(m.x, H, M, H, L.post_norm, c.eps, m.act_h, abH, m.h, H, st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_ROUTER, st);
+            hipLaunchKernelGGL(router_kernel, dim3((m.E1 + 3) / 4), dim3(256), 0, st, L.router, m.E1, H, m.h, m.sp,
+                               m.rlogits);
+        }
+        {
+            Tick tk(m, GV_K_ROUTE, st);
+            hipLaunchKernelGGL(route_kernel, dim3(1), dim3(1024), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
+        }
+        {
+            Tick tk(m, GV_K_MOE_UP, st);
+            if (moe_products(m, L, M, true, st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_SWIGLU, st);
+            hipLaunchKernelGGL(swiglu_quant_kernel, dim3(m.max_picks), dim3(256), static_cast<size_t>(c.moe_ff) * 4, st,
+                               m.gu_out, c.moe_ff, m.route + l, m.act_m);
+        }
+        {
+            Tick tk(m, GV_K_MOE_DOWN, st);
+            if (moe_products(m, L, M, false, st) != 0) return -1;
+        }
+        {
+            Tick tk(m, GV_K_COMBINE, st);
+            hipLaunchKernelGGL(combine_kernel, dim3(M, (H + 255) / 256), dim3(256), 0, st, m.y, H, c.top_k, m.route + l,
+                               m.sp, m.x);
+        }
     }
-    if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
-    if (gemv_q4(m.lm_head, m.act_h, abH, M, gemv_out(m.logits, c.vocab, m.lm_head.global), st) != 0) return -1;
+    {
+            Tick tk(m, GV_K_QUANT, st);
+            if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
+        }
+    {
+            Tick tk(m, GV_K_LM_HEAD, st);
+            if (gemv_q4(m.lm_head, m.act_h, abH, M, gemv_out(m.logits, c.vocab, m.lm_head.global), st) != 0) return -1;
+        }
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -630,8 +791,9 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     if (c.hidden <= 0 || c.hidden % 256 != 0) return fail("hidden must be a positive multiple of 256");
     if (c.moe_ff <= 0 || c.moe_ff % 64 != 0 || c.shared_ff != c.moe_ff)
         return fail("moe_ff must be a positive multiple of 64 and shared_ff equal to it");
-    if (c.head_dim <= 0 || c.head_dim > 256 || c.head_dim % 8 != 0 || c.rope_dim > c.head_dim || c.rope_dim % 2)
-        return fail("head_dim must be a multiple of 8 up to 256, rope_dim even and <= head_dim");
+    if (c.head_dim <= 0 || c.head_dim > 256 || c.head_dim % 32 != 0 || c.rope_dim > c.head_dim || c.rope_dim % 2)
+        return fail("head_dim must be a multiple of 32 up to 256, rope_dim even and <= head_dim");
+    if ((c.max_ctx + kAttnBlock - 1) / kAttnBlock > 1024) return fail("max_ctx at most 65536 positions");
     if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0 || (c.n_heads * c.head_dim) % 256 != 0)
         return fail("n_heads must be a multiple of n_kv_heads, n_heads x head_dim a multiple of 256");
     if (c.n_experts <= 0 || c.n_experts > 256 || c.top_k <= 0 || c.top_k > 16 || c.top_k > c.n_experts)
@@ -650,7 +812,9 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     const int64_t kv_row = nkv * hd;
     bool ok = alloc_q4(m, m.embed, V, H) && alloc_q4(m, m.lm_head, V, H);
     ok = ok && (m.final_norm = static_cast<float *>(dalloc(m, H * 4)));
-    m.kv_all = static_cast<uint16_t *>(dalloc(m, static_cast<size_t>(c.n_layers) * 2 * c.max_ctx * kv_row * 2));
+    m.slots = (static_cast<int64_t>(c.max_ctx) + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
+    const size_t kv_layer = 2 * static_cast<size_t>(nkv) * m.slots * hd;   // halves
+    m.kv_all = static_cast<_Float16 *>(dalloc(m, static_cast<size_t>(c.n_layers) * kv_layer * 2));
     ok = ok && m.kv_all;
     m.layers.resize(static_cast<size_t>(c.n_layers));
     for (int l = 0; ok && l < c.n_layers; ++l) {
@@ -668,7 +832,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         if (!ok) break;
         L.gu_codes = gu, L.gu_scales = gu + m.gu_code_stride * m.E1;
         L.dn_codes = dn, L.dn_scales = dn + m.dn_code_stride * m.E1;
-        L.kv = m.kv_all + static_cast<size_t>(l) * 2 * c.max_ctx * kv_row;
+        L.kv = m.kv_all + static_cast<size_t>(l) * kv_layer;
     }
     const int Mx = c.max_rows, K = c.top_k;
     m.max_slots = std::min(c.n_experts, Mx * K) + 1;
@@ -679,7 +843,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     ok = ok && (m.x = static_cast<float *>(dalloc(m, Mx * H * 4)));
     ok = ok && (m.h = static_cast<float *>(dalloc(m, Mx * H * 4)));
     ok = ok && (m.qkv_out = static_cast<float *>(dalloc(m, Mx * qkv_rows(c) * 4)));
-    ok = ok && (m.q_out = static_cast<float *>(dalloc(m, Mx * nh * hd * 4)));
+    ok = ok && (m.q16 = static_cast<_Float16 *>(dalloc(m, 2 * Mx * nh * hd * 2)));
     ok = ok && (m.core = static_cast<float *>(dalloc(m, Mx * nh * hd * 4)));
     ok = ok && (m.rlogits = static_cast<float *>(dalloc(m, Mx * m.E1 * 4)));
     ok = ok && (m.parts = static_cast<float *>(dalloc(m, static_cast<size_t>(Mx) * nh * m.kv_blocks * (hd + 2) * 4)));
@@ -713,7 +877,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         (hipMemcpy(m.rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
          hipMemcpy(m.rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess))
         return fail("gv_model_create: rope table copy failed");
-    if (hipMemset(m.kv_all, 0, static_cast<size_t>(c.n_layers) * 2 * c.max_ctx * kv_row * 2) != hipSuccess)
+    if (hipMemset(m.kv_all, 0, static_cast<size_t>(c.n_layers) * kv_layer * 2) != hipSuccess)
         return fail("gv_model_create: memset failed");
     return g.release();
 }
@@ -787,10 +951,17 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
         const int64_t kv_row = nkv * hd;
         GV_REQUIRE(bytes % (2 * kv_row * 2) == 0 && bytes / (2 * kv_row * 2) <= c.max_ctx, "gv_model_adopt: kv size");
         const int64_t n = bytes / (2 * kv_row * 2);
-        for (int kvi = 0; kvi < 2; ++kvi)
-            GV_CHECK_HIP(hipMemcpy(L->kv + static_cast<size_t>(kvi) * c.max_ctx * kv_row,
-                                   static_cast<const uint8_t *>(data) + kvi * n * kv_row * 2,
-                                   static_cast<size_t>(n * kv_row * 2), hipMemcpyHostToDevice));
+        std::vector<float> f(static_cast<size_t>(2 * n * kv_row));
+        const auto *hsrc = static_cast<const uint16_t *>(data);
+        for (size_t i = 0; i < f.size(); ++i) f[i] = static_cast<float>(__builtin_bit_cast(_Float16, hsrc[i]));
+        float *dsrc = nullptr;
+        GV_CHECK_HIP(hipMalloc(&dsrc, f.size() * 4 + 4));
+        GV_CHECK_HIP(hipMemcpy(dsrc, f.data(), f.size() * 4, hipMemcpyHostToDevice));
+        hipLaunchKernelGGL(kv_from_rows_kernel, dim3(static_cast<unsigned>((f.size() + 255) / 256)), dim3(256), 0,
+                           stream(), dsrc, static_cast<int>(n), static_cast<int>(nkv), static_cast<int>(hd), m.slots, L->kv);
+        GV_CHECK_HIP(hipGetLastError());
+        GV_CHECK_HIP(hipStreamSynchronize(stream()));
+        GV_CHECK_HIP(hipFree(dsrc));
         return 0;
     }
     default: set_error("gv_model_adopt: unknown tensor kind"); return -1;
@@ -897,13 +1068,12 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
             }
             (void)gd;
         }
-        if (ctx > 0) {
-            for (int kvi = 0; kvi < 2; ++kvi) {
-                rc |= fill_normal(tseed(GV_KV, l, kvi), static_cast<int64_t>(ctx) * kv_row, 1.0f, wf, st);
-                hipLaunchKernelGGL(f32_to_f16_kernel, dim3(static_cast<unsigned>((ctx * kv_row + 255) / 256)), dim3(256), 0,
-                                   st, wf, static_cast<int64_t>(ctx) * kv_row,
-                                   L.kv + static_cast<size_t>(kvi) * c.max_ctx * kv_row);
-            }
+        if (ctx > 0) {   // K then V of positions [0, ctx) in the reference's row layout, then the device's
+            for (int kvi = 0; kvi < 2; ++kvi)
+                rc |= fill_normal(tseed(GV_KV, l, kvi), static_cast<int64_t>(ctx) * kv_row, 1.0f,
+                                  wf + static_cast<int64_t>(kvi) * ctx * kv_row, st);
+            hipLaunchKernelGGL(kv_from_rows_kernel, dim3(static_cast<unsigned>((2 * ctx * kv_row + 255) / 256)), dim3(256),
+                               0, st, wf, ctx, static_cast<int>(nkv), static_cast<int>(hd), m.slots, L.kv);
         }
     }
     (void)hipStreamSynchronize(st);
@@ -972,10 +1142,9 @@ int gv_verify_keep(gv_model *g, int kept, const int32_t *path) {
         for (int j = 1; j < kept; ++j) GV_REQUIRE(path[j] > path[j - 1] && path[j] < m.last_n, "gv_verify_keep: path");
         int *dpath = reinterpret_cast<int *>(m.rlogits);   // scratch: free between verifies
         GV_CHECK_HIP(hipMemcpyAsync(dpath, path, static_cast<size_t>(kept) * 4, hipMemcpyHostToDevice, stream()));
-        const int64_t kv_row = static_cast<int64_t>(m.c.n_kv_heads) * m.c.head_dim;
-        const int64_t n = static_cast<int64_t>(m.c.n_layers) * 2 * kv_row;
+        const int64_t n = static_cast<int64_t>(m.c.n_layers) * m.c.n_kv_heads * m.c.head_dim;
         hipLaunchKernelGGL(kv_compact_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream(),
-                           m.kv_all, m.c.n_layers, m.c.max_ctx, kv_row, m.last_pos, kept, dpath);
+                           m.kv_all, m.c.n_layers, m.c.n_kv_heads, m.c.head_dim, m.slots, m.last_pos, kept, dpath);
         GV_CHECK_HIP(hipGetLastError());
         GV_CHECK_HIP(hipStreamSynchronize(stream()));
     }
@@ -985,6 +1154,29 @@ int gv_verify_keep(gv_model *g, int kept, const int32_t *path) {
 }
 
 const float *gv_model_logits(const gv_model *g) { return g ? g->m.logits : nullptr; }
+
+int gv_model_time_kernel(gv_model *g, int cls) {
+    GV_REQUIRE(g && cls < GV_K_COUNT, "gv_model_time_kernel: bad class");
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    g->m.timed_class = cls;
+    g->m.events_used = 0;
+    return 0;
+}
+
+int gv_model_kernel_time(gv_model *g, float *total_ms, int *launches) {
+    GV_REQUIRE(g && total_ms && launches, "gv_model_kernel_time: null pointer");
+    Model &m = g->m;
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    float sum = 0.0f;
+    for (size_t i = 0; i + 1 < m.events_used; i += 2) {
+        float ms = 0.0f;
+        GV_CHECK_HIP(hipEventElapsedTime(&ms, m.events[i], m.events[i + 1]));
+        sum += ms;
+    }
+    *total_ms = sum;
+    *launches = static_cast<int>(m.events_used / 2);
+    return 0;
+}
 
 int gv_model_route_ids(const gv_model *g, int32_t *out) {
     GV_REQUIRE(g && out && g->m.last_n > 0, "gv_model_route_ids: no verify yet");

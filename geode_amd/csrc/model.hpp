@@ -46,7 +46,7 @@ struct LayerW {
     uint8_t *gu_codes = nullptr, *gu_scales = nullptr;   // [E + 1] experts' gate_up (the shared one last)
     uint8_t *dn_codes = nullptr, *dn_scales = nullptr;   // [E + 1] experts' down
     float *expert_globals = nullptr;                     // [E + 1][3]: gate half, up half, down
-    uint16_t *kv = nullptr;                              // [2][max_ctx][nkv * hd] fp16
+    _Float16 *kv = nullptr;   // K [nkv][slots][hd], then V [nkv][slots / 64][hd][64] (model.hip: k_index, v_index)
 };
 
 struct Model {
@@ -62,13 +62,18 @@ struct Model {
     // scratch
     StepParams *sp = nullptr;
     RouteState *route = nullptr;   // [n_layers]
-    float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *q_out = nullptr, *core = nullptr, *rlogits = nullptr;
+    float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *core = nullptr, *rlogits = nullptr;
+    _Float16 *q16 = nullptr;   // [max_rows][nh][hd]: the rotated queries
     float *parts = nullptr, *gu_out = nullptr, *y = nullptr, *logits = nullptr;
     uint8_t *act_h = nullptr, *act_core = nullptr, *act_m = nullptr;
     int32_t *route_ids = nullptr;   // [n_layers][max_rows][K]
-    uint16_t *kv_all = nullptr;
+    _Float16 *kv_all = nullptr;
+    int64_t slots = 0;   // KV positions a layer holds: max_ctx rounded up to whole attention blocks
     // host side
     int pos = 0, last_pos = 0, last_n = 0;
+    int timed_class = -1;
+    std::vector<hipEvent_t> events;   // pairs around the timed class's launches
+    size_t events_used = 0;
     StepParams host_sp{};
     int max_slots = 0, max_picks = 0;
 };

@@ -147,6 +147,18 @@ const float *gv_model_logits(const gv_model *m); /* device [max_rows][vocab] of 
 /* the last verify's routed experts, host [n_layers][n][top_k] */
 int gv_model_route_ids(const gv_model *m, int32_t *out);
 
+/* kernel classes of a verify step, for gv_model_time_kernel */
+enum {
+    GV_K_EMBED = 0, GV_K_QUANT = 1, GV_K_QKV = 2, GV_K_ROPE = 3, GV_K_ATTN = 4, GV_K_MERGE = 5, GV_K_O = 6,
+    GV_K_ROUTER = 7, GV_K_ROUTE = 8, GV_K_MOE_UP = 9, GV_K_SWIGLU = 10, GV_K_MOE_DOWN = 11, GV_K_COMBINE = 12,
+    GV_K_LM_HEAD = 13, GV_K_COUNT = 14
+};
+/* From now on, every launch of kernel class cls is bracketed by events on the library's stream (cls < 0: off);
+ * gv_model_kernel_time waits and returns their summed milliseconds and launches since (no reference counterpart:
+ * the reference's per-kernel timing is GEODE_GPU8_PROF, engine/src/gpu8.cpp:195). */
+int gv_model_time_kernel(gv_model *m, int cls);
+int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
+
 #ifdef __cplusplus
 }
 #endif
