@@ -205,15 +205,15 @@ size_t gv_act_bytes(int64_t cols) { return act_bytes(cols); }
 int gv_quantize(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, uint8_t *act,
                 float *h_out) {
     if (ensure_init() != 0) return -1;
-    return quantize_act(x, ldx, M, cols, norm_w, eps, act, static_cast<int64_t>(act_bytes(cols)), h_out, cols,
+    return quantize_act(x, ldx, M, cols, norm_w, eps, 0, reinterpret_cast<_Float16 *>(act), act_halves(cols), h_out, cols,
                         stream());
 }
 
 int gv_gemv_q4(const gv_q4 *w, const uint8_t *act, int M, float *y, int64_t ldy, int accumulate) {
     if (ensure_init() != 0) return -1;
     GV_REQUIRE(w && act && y, "gv_gemv_q4: null pointer");
-    return gemv_q4(to_q4(*w), act, static_cast<int64_t>(act_bytes(w->cols)), M, gemv_out(y, ldy, w->global, accumulate),
-                   stream());
+    return gemv_q4(to_q4(*w), reinterpret_cast<const _Float16 *>(act), act_halves(w->cols), M,
+                   gemv_out(y, ldy, w->global, accumulate), stream());
 }
 
 size_t gv_ffn_workspace_bytes(int64_t hidden, int64_t ff, int M) {
@@ -232,15 +232,15 @@ int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, 
     float *g = x + static_cast<size_t>(M) * H;
     float *u = g + static_cast<size_t>(M) * F;
     float *m = u + static_cast<size_t>(M) * F;
-    uint8_t *act = reinterpret_cast<uint8_t *>(m + static_cast<size_t>(M) * F);
+    _Float16 *act = reinterpret_cast<_Float16 *>(m + static_cast<size_t>(M) * F);
     hipStream_t st = stream();
     if (f16_to_f32(x_f16, static_cast<int64_t>(M) * H, x, st) != 0) return -1;
-    const int64_t ab_h = static_cast<int64_t>(act_bytes(H)), ab_f = static_cast<int64_t>(act_bytes(F));
-    if (quantize_act(x, H, M, static_cast<int>(H), nullptr, 0.0f, act, ab_h, nullptr, 0, st) != 0) return -1;
+    const int64_t ab_h = act_halves(H), ab_f = act_halves(F);
+    if (quantize_act(x, H, M, static_cast<int>(H), nullptr, 0.0f, 0, act, ab_h, nullptr, 0, st) != 0) return -1;
     if (gemv_q4(to_q4(*gate), act, ab_h, M, gemv_out(g, F, gate->global), st) != 0) return -1;
     if (gemv_q4(to_q4(*up), act, ab_h, M, gemv_out(u, F, up->global), st) != 0) return -1;
     if (swiglu(g, u, static_cast<int64_t>(M) * F, m, st) != 0) return -1;
-    if (quantize_act(m, F, M, static_cast<int>(F), nullptr, 0.0f, act, ab_f, nullptr, 0, st) != 0) return -1;
+    if (quantize_act(m, F, M, static_cast<int>(F), nullptr, 0.0f, 0, act, ab_f, nullptr, 0, st) != 0) return -1;
     return gemv_q4(to_q4(*down), act, ab_f, M, gemv_out(y, H, down->global), st);
 }
 
@@ -282,8 +282,8 @@ gv_ctx *gv_open(int device, char *err, int err_len) {
 void gv_close(gv_ctx *g) { delete g; }
 
 int gv_adopt_q4(gv_ctx *g, const uint8_t *data, int64_t rows, int64_t cols, size_t row_bytes, float global) {
-    if (!g || !data || rows <= 0 || cols % 32 != 0 || row_bytes != static_cast<size_t>(cols / 16) * 9) {
-        set_error("gv_adopt_q4: bad arguments (rows > 0, cols a multiple of 32, the pack's row bytes)");
+    if (!g || !data || rows <= 0 || cols % 128 != 0 || row_bytes != static_cast<size_t>(cols / 16) * 9) {
+        set_error("gv_adopt_q4: bad arguments (rows > 0, cols a multiple of 128, the pack's row bytes)");
         return -1;
     }
     const size_t pack = static_cast<size_t>(rows) * row_bytes;
@@ -317,14 +317,14 @@ int gv_gemm(gv_ctx *g, int id, int n, const float *const *xs, float *const *ys) 
         auto *base = static_cast<uint8_t *>(g->io.get(xb + yb + static_cast<size_t>(m) * act_bytes(q.cols)));
         GV_REQUIRE(base, "gv_gemm: out of device memory");
         float *x = reinterpret_cast<float *>(base), *y = reinterpret_cast<float *>(base + xb);
-        uint8_t *act = base + xb + yb;
+        _Float16 *act = reinterpret_cast<_Float16 *>(base + xb + yb);
         for (int t = 0; t < m; ++t)
             GV_CHECK_HIP(hipMemcpyAsync(x + static_cast<size_t>(t) * q.cols, xs[t0 + t], q.cols * 4,
                                         hipMemcpyHostToDevice, st));
-        if (quantize_act(x, q.cols, m, static_cast<int>(q.cols), nullptr, 0.0f, act,
-                         static_cast<int64_t>(act_bytes(q.cols)), nullptr, 0, st) != 0)
+        if (quantize_act(x, q.cols, m, static_cast<int>(q.cols), nullptr, 0.0f, 0, act, act_halves(q.cols), nullptr, 0,
+                         st) != 0)
             return -1;
-        if (gemv_q4(q, act, static_cast<int64_t>(act_bytes(q.cols)), m, gemv_out(y, q.rows, q.global), st) != 0)
+        if (gemv_q4(q, act, act_halves(q.cols), m, gemv_out(y, q.rows, q.global), st) != 0)
             return -1;
         for (int t = 0; t < m; ++t)
             GV_CHECK_HIP(hipMemcpyAsync(ys[t0 + t], y + static_cast<size_t>(t) * q.rows, q.rows * 4,
@@ -360,19 +360,19 @@ int gv_mlp(gv_ctx *g, int gate, int up, int n_down, const int *downs, int act, i
         GV_REQUIRE(base, "gv_mlp: out of device memory");
         float *x = base, *gg = x + static_cast<size_t>(m) * H, *uu = gg + static_cast<size_t>(m) * F,
               *mm = uu + static_cast<size_t>(m) * F, *y = mm + static_cast<size_t>(m) * F;
-        auto *a = reinterpret_cast<uint8_t *>(y + static_cast<size_t>(m) * drows);
+        auto *a = reinterpret_cast<_Float16 *>(y + static_cast<size_t>(m) * drows);
         for (int t = 0; t < m; ++t)
             GV_CHECK_HIP(hipMemcpyAsync(x + static_cast<size_t>(t) * H, xs[t0 + t], H * 4, hipMemcpyHostToDevice, st));
-        const int64_t abh = static_cast<int64_t>(act_bytes(H));
-        if (quantize_act(x, H, m, static_cast<int>(H), nullptr, 0.0f, a, abh, nullptr, 0, st) != 0) return -1;
+        const int64_t abh = act_halves(H);
+        if (quantize_act(x, H, m, static_cast<int>(H), nullptr, 0.0f, 0, a, abh, nullptr, 0, st) != 0) return -1;
         if (gemv_q4(qg, a, abh, m, gemv_out(gg, F, qg.global), st) != 0) return -1;
         if (gemv_q4(qu, a, abh, m, gemv_out(uu, F, qu.global), st) != 0) return -1;
         if (swiglu(gg, uu, static_cast<int64_t>(m) * F, mm, st) != 0) return -1;
         int64_t c0 = 0;
         for (int j = 0; j < n_down; ++j) {   // each part's results added (npu_api.h:62-65)
             const Q4 &qd = g->mats[static_cast<size_t>(downs[j])].q;
-            const int64_t ab = static_cast<int64_t>(act_bytes(qd.cols));
-            if (quantize_act(mm + c0, F, m, static_cast<int>(qd.cols), nullptr, 0.0f, a, ab, nullptr, 0, st) != 0)
+            const int64_t ab = act_halves(qd.cols);
+            if (quantize_act(mm + c0, F, m, static_cast<int>(qd.cols), nullptr, 0.0f, 0, a, ab, nullptr, 0, st) != 0)
                 return -1;
             if (gemv_q4(qd, a, ab, m, gemv_out(y, drows, qd.global, j > 0), st) != 0) return -1;
             c0 += qd.cols;

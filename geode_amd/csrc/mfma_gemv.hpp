@@ -1,0 +1,239 @@
+// mfma_gemv.hpp - the skinny products on the matrix cores (v_mfma_f32_16x16x32_f16).
+//
+// y[t][r] = sum_k W[r][k] x[t][k] for up to 32 rows t of activations. The weights are the q4 matrix's exact values
+// level x E4M3(scale) (at most 8 significant bits: exact in fp16), made in registers from the nibbles; global is
+// applied to the fp32 sums. The activations are staged as two fp16 halves hi + lo of their fp32 value (hi + lo =
+// the value to 2^-22), so each product is two MFMAs and the result is the fp32 one up to summation order. On the
+// int8 path (the reference's default, matvec_rows_q_ref in engine/src/kernels.cpp:1304-1322) the activation value
+// is its int8 code times its block scale, q x (amax / 127): the same products as the integer block sums times the
+// block scales.
+//
+// The q4 layout of these kernels ("tiles"): rows in tiles of 16, K in super-chunks of 128 values. A tile's
+// super-chunk is 1 KB of codes: lane l (row l % 16, k-group g = l / 16) has 16 bytes = the pack's code words
+// 16 sc + 4 j + g (j = 0..3: the 32-value chunks of the super-chunk, 8 values of the k-group each), nibbles remapped
+// to the affine order (level = 2c' - 15) and placed for decode8 (tile_word); then 128 bytes of E4M3 scales, byte
+// (r * 2 + g / 2) * 4 + j = the block of chunk j that k-group g falls in. One load instruction of a wave reads the
+// 1 KB whole.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace gv {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+constexpr int kTileR = 16;    // rows a tile
+constexpr int kSuperK = 128;  // values a super-chunk
+
+__host__ __device__ inline int64_t tiles_rows(int64_t rows) { return (rows + kTileR - 1) / kTileR; }
+inline size_t tq4_code_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * kTileR * (cols / 2); }
+inline size_t tq4_scale_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * kTileR * (cols / 16); }
+
+// The activations' layout for these kernels: per row, per 32-value chunk c and k-group g, 8 hi halves then 8 lo
+// halves (32 bytes) of values 32c + 8g + (0 4 1 5 2 6 3 7), the order the nibble pairs come out in.
+inline size_t act16_row_bytes(int64_t cols) { return static_cast<size_t>(cols) * 4; }
+
+// 16 values (block b of a row) into the row's operands: the int8 path's q x (amax / 127) (quantize_activation,
+// engine/src/kernels.cpp:1254-1295, bit for bit) unless exact, then hi + lo halves at their slots
+__device__ inline void act16_block(float (&v)[16], int b, _Float16 *ar, bool exact) {
+    if (!exact) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        const float s = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int q = min(max(static_cast<int>(rintf(__fmul_rn(v[i], qi))), -127), 127);
+            v[i] = __fmul_rn(static_cast<float>(q), s);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {   // value k = 16 b + i: chunk k / 32, k-group (k % 32) / 8, slot of k % 8
+        const int k = b * 16 + i, u = k % 8;
+        const int slot = u < 4 ? 2 * u : 2 * (u - 4) + 1;
+        _Float16 *p = ar + (static_cast<int64_t>(k / 32) * 4 + (k % 32) / 8) * 16;
+        const _Float16 hi = static_cast<_Float16>(v[i]);
+        p[slot] = hi;
+        p[8 + slot] = static_cast<_Float16>(v[i] - static_cast<float>(hi));
+    }
+}
+
+// a row of cols values (any memory) into its operands, the workgroup's threads over its blocks
+__device__ inline void act16_row(const float *v, int cols, _Float16 *ar, bool exact) {
+    for (int b = threadIdx.x; b < cols / 16; b += blockDim.x) {
+        float blk[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) blk[i] = v[b * 16 + i];
+        act16_block(blk, b, ar, exact);
+    }
+}
+
+// Where a code word's nibbles sit. decode8 makes the A operand's pairs (v_i, v_i+4), i = 0..3, from 4 views of the
+// word (itself, << 4, >> 4, rotated right by 8); in view i the pair's nibbles sit at bits 6..9 and 22..25. tile_word
+// places the 8 affine codes of a word (nibble i = value i) so, untile_word takes them back.
+__host__ __device__ inline uint32_t tile_word(uint32_t a) {
+    uint32_t p[4];
+    for (int i = 0; i < 4; ++i) p[i] = (((a >> (4 * i)) & 15u) << 6) | (((a >> (4 * i + 16)) & 15u) << 22);
+    return p[0] | (p[1] >> 4) | (p[2] << 4) | (p[3] << 8) | (p[3] >> 24);
+}
+__host__ __device__ inline uint32_t untile_word(uint32_t w) {
+    const uint32_t d[4] = {w, w << 4, w >> 4, (w >> 8) | (w << 24)};
+    uint32_t a = 0;
+    for (int i = 0; i < 4; ++i) a |= (((d[i] >> 6) & 15u) << (4 * i)) | (((d[i] >> 22) & 15u) << (4 * i + 16));
+    return a;
+}
+
+// code word wi (values 8 wi .. 8 wi + 7) of row r of a tile-layout matrix: the 8 affine codes (nibble i = value i)
+// and the block's scale byte
+__device__ inline void tq4_word(const Q4 &w, int64_t r, int64_t wi, uint32_t &word, uint32_t &scale) {
+    const int64_t T = r / kTileR, rr = r % kTileR, nsc = w.cols / kSuperK;
+    const int64_t sc = wi / 16, j = (wi % 16) / 4, g = wi % 4;
+    const int64_t blk = T * nsc + sc;
+    word = untile_word(*reinterpret_cast<const uint32_t *>(w.codes + blk * 1024 + (rr + 16 * g) * 16 + j * 4));
+    scale = w.scales[blk * 128 + (rr * 2 + g / 2) * 4 + j];
+}
+
+// The scale table: per E4M3 byte, the fp16 pairs (e4 / 32, -47 e4). With a nibble c' at bits 6..9 of the fp16
+// 1024.0 (0x6400), v = 1024 + 64 c' and fma(v, e4 / 32, -47 e4) = (2 c' - 15) e4 = level x E4M3, exactly: v x e4 / 32
+// is exact inside the fma, -47 e4 has at most 10 significant bits, and the result at most 8 (all E4M3 values,
+// subnormals included, stay fp16 normals here).
+__device__ inline void fill_e4m3_table(uint2 *tab) {
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+        const float e = e4m3_to_f32(static_cast<uint32_t>(b));
+        const uint32_t m = __builtin_bit_cast(uint16_t, static_cast<_Float16>(e * 0.03125f));
+        const uint32_t c = __builtin_bit_cast(uint16_t, static_cast<_Float16>(-47.0f * e));
+        tab[b] = make_uint2(m | (m << 16), c | (c << 16));
+    }
+}
+
+// (x & mask) | magic in one instruction (mask from a scalar register, magic from a vector one)
+__device__ inline uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
+    return r;
+}
+
+// 8 weights of one code word as the A operand, level x E4M3 each in fp16: pairs (v_i, v_i+4), i = 0..3
+__device__ inline h8 decode8(uint32_t w, uint2 sc, uint32_t magic) {
+    const uint32_t d[4] = {w, w << 4, w >> 4, __builtin_amdgcn_alignbit(w, w, 8)};
+    const h2 m = __builtin_bit_cast(h2, sc.x), c = __builtin_bit_cast(h2, sc.y);
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2 v = __builtin_bit_cast(h2, and_or(d[i], 0x03C003C0u, magic));
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, m, c));
+    }
+    return __builtin_bit_cast(h8, make_uint4(r[0], r[1], r[2], r[3]));
+}
+
+// One workgroup's share of a product: its waves split the K range [sc0, sc0 + waves KW / 4) super-chunks (wave w:
+// chunks [w KW, (w + 1) KW) of it) of row tiles [t0, t1), a tile at a time with the next one's loads in flight;
+// nsc = super-chunks a row. act(j) gives local row j's activation row (act16 layout, whole row) or nullptr, put(row,
+// j, v) takes the fp32 sum (before global). part: LDS of (t1 - t0) * waves * NTT KB for the waves' partial sums,
+// added once at the end (waves > 1); tab: fill_e4m3_table's.
+template <int KW, int NTT, typename ActFn, typename PutFn>
+__device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, int64_t rows,
+                                  int nsc, int sc0, int64_t t0, int64_t t1, int M, ActFn act, PutFn put, f4 *part,
+                                  const uint2 *tab) {
+    const int W = blockDim.x / 64;
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
+    // the activations of this wave's K range, resident for all the tiles
+    h8 bh[KW][NTT], bl[KW][NTT];
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) {
+        const int j = tt * 16 + lq;
+        const _Float16 *ar = j < M ? act(j) : nullptr;
+#pragma unroll
+        for (int c = 0; c < KW; ++c) {
+            const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (ar) {
+                const _Float16 *p = ar + ((static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg) * 16;
+                bh[c][tt] = *reinterpret_cast<const h8 *>(p);
+                bl[c][tt] = *reinterpret_cast<const h8 *>(p + 8);
+            } else {
+                bh[c][tt] = z;
+                bl[c][tt] = z;
+            }
+        }
+    }
+    constexpr int NS = KW / 4;   // super-chunks a wave takes
+    const uint32_t magic = 0x64006400u;
+    const int nt = static_cast<int>(t1 - t0);
+    const uint8_t *cbase = codes + (t0 * nsc + sc0 + w * NS) * 1024 + l * 16;
+    const uint8_t *sbase = scales + (t0 * nsc + sc0 + w * NS) * 128 + (lq * 2 + lg / 2) * 4;
+    const int64_t tstride = static_cast<int64_t>(nsc);
+    auto load = [&](int i, uint4 (&cw)[NS], uint32_t (&sw)[NS]) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const u4v v = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(cbase + (i * tstride + s) * 1024));
+            cw[s] = make_uint4(v.x, v.y, v.z, v.w);
+            sw[s] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(sbase + (i * tstride + s) * 128));
+        }
+    };
+    auto tile = [&](int i, const uint4 (&cw)[NS], const uint32_t (&sw)[NS]) {
+        f4 acc[NTT], acl[NTT];   // the hi and lo products apart: two independent MFMA chains
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) acc[tt] = acl[tt] = f4{0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const uint32_t words[4] = {cw[s].x, cw[s].y, cw[s].z, cw[s].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const h8 a = decode8(words[j], tab[(sw[s] >> (8 * j)) & 0xFFu], magic);
+                const int c = s * 4 + j;
+#pragma unroll
+                for (int tt = 0; tt < NTT; ++tt) {
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh[c][tt], acc[tt], 0, 0, 0);
+                    acl[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl[c][tt], acl[tt], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) acc[tt] += acl[tt];
+        if (W > 1) {
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) part[((i * W + w) * NTT + tt) * 64 + l] = acc[tt];
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) {
+                const int j = tt * 16 + lq;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = (t0 + i) * kTileR + 4 * lg + r;
+                    if (j < M && row < rows) put(row, j, acc[tt][r]);
+                }
+            }
+        }
+    };
+    uint4 ca[NS], cb[NS];
+    uint32_t sa[NS], sb[NS];
+    load(0, ca, sa);
+    for (int i = 0; i < nt; i += 2) {
+        if (i + 1 < nt) load(i + 1, cb, sb);
+        tile(i, ca, sa);
+        if (i + 1 >= nt) break;
+        if (i + 2 < nt) load(i + 2, ca, sa);
+        tile(i + 1, cb, sb);
+    }
+    // the waves' partial sums added in wave order, each output by one thread
+    if (W > 1) {
+        __syncthreads();
+        for (int o = threadIdx.x; o < nt * NTT * 64; o += blockDim.x) {
+            const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+            f4 sum = part[((i * W + 0) * NTT + tt) * 64 + ll];
+            for (int w2 = 1; w2 < W; ++w2) sum += part[((i * W + w2) * NTT + tt) * 64 + ll];
+            const int j = tt * 16 + ll % 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = (t0 + i) * kTileR + 4 * (ll / 16) + r;
+                if (j < M && row < rows) put(row, j, sum[r]);
+            }
+        }
+    }
+}
+
+}  // namespace gv

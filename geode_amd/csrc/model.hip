@@ -15,7 +15,7 @@
 #include <string>
 #include <vector>
 
-#include "gemv_core.hpp"
+#include "mfma_gemv.hpp"
 #include "model.hpp"
 
 namespace gv {
@@ -29,20 +29,13 @@ __global__ void embed_kernel(Q4 w, const StepParams *__restrict__ sp, float *__r
     const int t = blockIdx.x;
     if (t >= sp->M) return;
     const int64_t r = sp->tokens[t];
-    const int nch = static_cast<int>(w.cols / 32), groups = q4_groups(w.steps);
-    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
-        const uint4 cw = *reinterpret_cast<const uint4 *>(w.codes + q4_code_offset(w.rows, w.cols, w.S, r, c));
-        const uint8_t *sd = w.scales + q4_scale_offset(w.rows, w.S, groups, r, c);
-        const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
-        float *o = x + static_cast<int64_t>(t) * w.cols + c * 32;
-        for (int j = 0; j < 2; ++j) {
-            const float s = __fmul_rn(e4m3_to_f32(sd[j]), w.global);
-            for (int q = 0; q < 2; ++q)
-                for (int b = 0; b < 8; ++b) {
-                    const int cp = static_cast<int>((words[2 * j + q] >> (4 * b)) & 15u);
-                    o[16 * j + 8 * q + b] = __fmul_rn(static_cast<float>(2 * cp - 15), s);
-                }
-        }
+    for (int64_t wi = threadIdx.x; wi < w.cols / 8; wi += blockDim.x) {   // the row's code words (tile layout)
+        uint32_t word, sb;
+        tq4_word(w, r, wi, word, sb);
+        const float s = __fmul_rn(e4m3_to_f32(sb), w.global);
+        float *o = x + static_cast<int64_t>(t) * w.cols + wi * 8;
+        for (int b = 0; b < 8; ++b)
+            o[b] = __fmul_rn(static_cast<float>(2 * static_cast<int>((word >> (4 * b)) & 15u) - 15), s);
     }
 }
 
@@ -420,54 +413,47 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
     }
 }
 
-// The experts' products, a workgroup per (slot, row tile): UP takes gate_up [2F x H] against the post-norm rows of
-// the slot's tokens, DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each pick's rows go to out.
-template <int S, int R, int MT, bool UP>
-__global__ __launch_bounds__(256) void moe_gemv_kernel(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
-                                                       size_t code_stride, size_t scale_stride, int64_t rows,
-                                                       int64_t cols, int steps, const float *__restrict__ globals,
-                                                       int half_rows, const uint8_t *__restrict__ act,
-                                                       const RouteState *__restrict__ rs, float *__restrict__ out) {
-    constexpr int G = 64 / S;
-    constexpr int WROWS = G * R;
-    extern __shared__ uint4 lds_u4[];
-    uint8_t *lds = reinterpret_cast<uint8_t *>(lds_u4);
+// The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
+// the post-norm rows of the slot's tokens, DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each
+// pick's rows go to out [pick][rows].
+template <int KW, int NTT, int WMAX, bool UP>
+__global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
+                                                        size_t code_stride, size_t scale_stride, int64_t rows, int K,
+                                                        const float *__restrict__ globals, int half_rows,
+                                                        const _Float16 *__restrict__ act, int64_t act_stride,
+                                                        const RouteState *__restrict__ rs, float *__restrict__ out,
+                                                        int tiles_per_wg) {
+    extern __shared__ f4 part_lds[];
+    __shared__ uint2 tab[256];
+    fill_e4m3_table(tab);
+    __syncthreads();
     const int u = blockIdx.x;
     if (u >= rs->n_slots) return;
     const int e = rs->slot_expert[u], start = rs->slot_start[u], cnt = rs->slot_count[u];
-    const int64_t abytes = (cols / 32) * kActChunkBytes;
-    for (int64_t i = static_cast<int64_t>(threadIdx.x) * 16; i < cnt * abytes; i += static_cast<int64_t>(blockDim.x) * 16) {
-        const int64_t j = i / abytes, o = i % abytes;
-        const int64_t src_row = UP ? rs->pick_token[start + j] : start + j;
-        *reinterpret_cast<uint4 *>(lds + i) = *reinterpret_cast<const uint4 *>(act + src_row * abytes + o);
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane / S, k = lane % S;
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * WROWS;
-    if (row0 >= rows) return;
-    float acc[R][MT];
-    gemv_wave<S, R, MT>(codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride,
-                        rows, cols, steps, row0, lds, abytes, cnt, g, k, acc);
-    gemv_reduce<S, R, MT>(acc, cnt);
-    if (k != 0) return;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        const int64_t row = row0 + i * G + g;
-        if (row >= rows) continue;
-        const float gl = UP ? (row < half_rows ? globals[e * 3] : globals[e * 3 + 1]) : globals[e * 3 + 2];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            if (t >= cnt) break;
-            out[static_cast<int64_t>(start + t) * rows + row] = acc[i][t] * gl;
-        }
-    }
+    const int64_t ntiles = tiles_rows(rows);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * tiles_per_wg;
+    const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
+    if (t0 >= ntiles) return;
+    const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
+    mfma_tiles<KW, NTT>(
+        codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
+        K / kSuperK, 0, t0, t1,
+        cnt,
+        [&](int j) {
+            const int64_t src = UP ? rs->pick_token[start + j] : start + j;
+            return act + src * act_stride;
+        },
+        [&](int64_t row, int j, float v) {
+            const float gl = UP ? (row < half_rows ? g0 : g1) : g2;
+            out[static_cast<int64_t>(start + j) * rows + row] = v * gl;
+        },
+        part_lds, tab);
 }
 
 // per pick: silu(gate) * up (kernels.hpp:141), quantized for down
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restrict__ gu, int F,
                                                            const RouteState *__restrict__ rs,
-                                                           uint8_t *__restrict__ act_m) {
+                                                           _Float16 *__restrict__ act_m) {
     extern __shared__ uint4 lds_u4[];
     float *m = reinterpret_cast<float *>(lds_u4);
     const int p = blockIdx.x;
@@ -478,7 +464,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
         m[i] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), row[F + i]);
     }
     __syncthreads();
-    quantize_row(m, F, act_m + static_cast<int64_t>(p) * (F / 32) * kActChunkBytes);
+    act16_row(m, F, act_m + static_cast<int64_t>(p) * act_halves(F), false);
 }
 
 // x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365); a workgroup per
@@ -544,47 +530,43 @@ __global__ void f32_to_f16_kernel(const float *__restrict__ x, int64_t n, uint16
 // ---------------------------------------------------------------- launches
 namespace {
 
-template <int S, int R, int MT, bool UP>
-int launch_moe(const Model &m, const LayerW &L, int M, hipStream_t st) {
-    constexpr int WROWS = (64 / S) * R;
+template <int KW, int NTT, int WMAX, bool UP>
+int launch_moe(const Model &m, const LayerW &L, int waves, hipStream_t st) {
     const int64_t H = m.c.hidden, F = m.c.moe_ff;
     const int64_t rows = UP ? 2 * F : H, cols = UP ? H : F;
-    const int steps = static_cast<int>(cols / (32 * S));
-    const int tiles = static_cast<int>((rows + 4 * WROWS - 1) / (4 * WROWS));
-    const size_t lds = static_cast<size_t>(M) * act_bytes(cols);
+    const int64_t ntiles = tiles_rows(rows);
+    // ~8 workgroups a slot, the waves' partial sums within 48 KB of LDS
+    const int64_t cap = waves > 1 ? std::max(1, 48 / (waves * NTT)) : 64;
+    const int per = static_cast<int>(std::min<int64_t>(cap, (ntiles + 7) / 8));
+    const int tiles = static_cast<int>((ntiles + per - 1) / per);
+    const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&moe_gemv_kernel<S, R, MT, UP>), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL((moe_gemv_kernel<S, R, MT, UP>), dim3(m.max_slots, tiles), dim3(256), lds, st,
+    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 64 * 1024, granted) != 0)
+        return -1;
+    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(m.max_slots, tiles), dim3(64 * waves), lds, st,
                        UP ? L.gu_codes : L.dn_codes, UP ? L.gu_scales : L.dn_scales,
-                       UP ? m.gu_code_stride : m.dn_code_stride, UP ? m.gu_scale_stride : m.dn_scale_stride, rows, cols,
-                       steps, L.expert_globals, static_cast<int>(F), UP ? m.act_h : m.act_m, m.route + (&L - &m.layers[0]),
-                       UP ? m.gu_out : m.y);
+                       UP ? m.gu_code_stride : m.dn_code_stride, UP ? m.gu_scale_stride : m.dn_scale_stride, rows,
+                       static_cast<int>(cols), L.expert_globals, static_cast<int>(F), UP ? m.act_h : m.act_m,
+                       act_halves(cols), m.route + (&L - &m.layers[0]), UP ? m.gu_out : m.y, per);
     return 0;
 }
 
-template <int S, bool UP>
-int moe_dispatch(const Model &m, const LayerW &L, int M, hipStream_t st) {
-    if (M <= 1) return launch_moe<S, 1, 1, UP>(m, L, M, st);
-    if (M <= 2) return launch_moe<S, 1, 2, UP>(m, L, M, st);
-    if (M <= 4) return launch_moe<S, 1, 4, UP>(m, L, M, st);
-    if (M <= 8) return launch_moe<S, 1, 8, UP>(m, L, M, st);
-    if (M <= 16) return launch_moe<S, 1, 16, UP>(m, L, M, st);
-    return launch_moe<S, 1, 32, UP>(m, L, M, st);
+template <bool UP>
+int moe_launch(const Model &m, const LayerW &L, int ntt, int kw, int waves, hipStream_t st) {
+    if (ntt == 1) {
+        if (kw == 16) return launch_moe<16, 1, 8, UP>(m, L, waves, st);
+        if (kw == 8) return launch_moe<8, 1, 8, UP>(m, L, waves, st);
+        return launch_moe<4, 1, 8, UP>(m, L, waves, st);
+    }
+    if (kw == 8) return launch_moe<8, 2, 8, UP>(m, L, waves, st);
+    return launch_moe<4, 2, 8, UP>(m, L, waves, st);
 }
 
 int moe_products(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
-    const int S = q4_lanes_for(up ? m.c.hidden : m.c.moe_ff);
-    switch (S * 2 + (up ? 1 : 0)) {
-    case 2: return moe_dispatch<1, false>(m, L, M, st);
-    case 3: return moe_dispatch<1, true>(m, L, M, st);
-    case 4: return moe_dispatch<2, false>(m, L, M, st);
-    case 5: return moe_dispatch<2, true>(m, L, M, st);
-    case 8: return moe_dispatch<4, false>(m, L, M, st);
-    case 9: return moe_dispatch<4, true>(m, L, M, st);
-    case 16: return moe_dispatch<8, false>(m, L, M, st);
-    case 17: return moe_dispatch<8, true>(m, L, M, st);
-    default: set_error("moe: unsupported width"); return -1;
-    }
+    const int ntt = M <= 16 ? 1 : 2;
+    int waves, kw;
+    GV_REQUIRE(mfma_split(up ? m.c.hidden : m.c.moe_ff, ntt, waves, kw), "moe: K too wide for one launch");
+    return up ? moe_launch<true>(m, L, ntt, kw, waves, st) : moe_launch<false>(m, L, ntt, kw, waves, st);
 }
 
 GemvOut qkv_out(const Model &m, const LayerW &L) {
@@ -628,7 +610,7 @@ struct Tick {
 int run_layers(Model &m, int M, hipStream_t st) {
     const auto &c = m.c;
     const int H = c.hidden, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
-    const int64_t abH = static_cast<int64_t>(act_bytes(H)), abC = static_cast<int64_t>(act_bytes(static_cast<int64_t>(nh) * hd));
+    const int64_t abH = act_halves(H), abC = act_halves(static_cast<int64_t>(nh) * hd);
     {
         Tick tk(m, GV_K_EMBED, st);
         hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x);
@@ -637,7 +619,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
         {
             Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
+            if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, 0, m.act_h, abH, nullptr, 0, st) != 0) return -1;
         }
         {
             Tick tk(m, GV_K_QKV, st);
@@ -662,7 +644,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
         }
         {
             Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.core, nh * hd, M, nh * hd, nullptr, 0.0f, m.act_core, abC, nullptr, 0, st) != 0) return -1;
+            if (quantize_act(m.core, nh * hd, M, nh * hd, nullptr, 0.0f, 0, m.act_core, abC, nullptr, 0, st) != 0) return -1;
         }
         {
             Tick tk(m, GV_K_O, st);
@@ -670,7 +652,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
         }
         {
             Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, L.post_norm, c.eps, m.act_h, abH, m.h, H, st) != 0) return -1;
+            if (quantize_act(m.x, H, M, H, L.post_norm, c.eps, 0, m.act_h, abH, m.h, H, st) != 0) return -1;
         }
         {
             Tick tk(m, GV_K_ROUTER, st);
@@ -703,7 +685,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
     }
     {
             Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
+            if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, 0, m.act_h, abH, nullptr, 0, st) != 0) return -1;
         }
     {
             Tick tk(m, GV_K_LM_HEAD, st);
@@ -727,8 +709,6 @@ bool alloc_q4(Model &m, Q4 &q, int64_t rows, int64_t cols) {
     q.scales = p + q4_code_bytes(rows, cols);
     q.rows = rows;
     q.cols = cols;
-    q.S = q4_lanes_for(cols);
-    q.steps = static_cast<int>(cols / (32 * q.S));
     return true;
 }
 
@@ -788,18 +768,24 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         set_error(msg);
         return nullptr;
     };
-    if (c.hidden <= 0 || c.hidden % 256 != 0) return fail("hidden must be a positive multiple of 256");
-    if (c.moe_ff <= 0 || c.moe_ff % 64 != 0 || c.shared_ff != c.moe_ff)
-        return fail("moe_ff must be a positive multiple of 64 and shared_ff equal to it");
+    if (c.hidden <= 0 || c.hidden % 128 != 0) return fail("hidden must be a positive multiple of 128");
+    if (c.moe_ff <= 0 || c.moe_ff % 128 != 0 || c.shared_ff != c.moe_ff)
+        return fail("moe_ff must be a positive multiple of 128 and shared_ff equal to it");
     if (c.head_dim <= 0 || c.head_dim > 256 || c.head_dim % 32 != 0 || c.rope_dim > c.head_dim || c.rope_dim % 2)
         return fail("head_dim must be a multiple of 32 up to 256, rope_dim even and <= head_dim");
     if ((c.max_ctx + kAttnBlock - 1) / kAttnBlock > 1024) return fail("max_ctx at most 65536 positions");
-    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0 || (c.n_heads * c.head_dim) % 256 != 0)
-        return fail("n_heads must be a multiple of n_kv_heads, n_heads x head_dim a multiple of 256");
+    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0 || (c.n_heads * c.head_dim) % 128 != 0)
+        return fail("n_heads must be a multiple of n_kv_heads, n_heads x head_dim a multiple of 128");
     if (c.n_experts <= 0 || c.n_experts > 256 || c.top_k <= 0 || c.top_k > 16 || c.top_k > c.n_experts)
         return fail("1 <= top_k <= 16, top_k <= n_experts <= 256");
     if (c.max_rows <= 0 || c.max_rows > kMaxRows) return fail("max_rows must be 1..32");
     if (c.vocab <= 0 || c.n_layers <= 0 || c.max_ctx <= c.max_rows) return fail("vocab, n_layers, max_ctx");
+    {
+        int waves, kw;
+        const int ntt = c.max_rows <= 16 ? 1 : 2;
+        if (!mfma_split(c.hidden, ntt, waves, kw) || !mfma_split(c.moe_ff, ntt, waves, kw))
+            return fail("the expert products take hidden and moe_ff up to 4096 (2048 when max_rows > 16)");
+    }
     auto g = std::make_unique<gv_model>();
     Model &m = g->m;
     m.c = c;
@@ -850,9 +836,9 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     ok = ok && (m.gu_out = static_cast<float *>(dalloc(m, static_cast<size_t>(m.max_picks) * 2 * F * 4)));
     ok = ok && (m.y = static_cast<float *>(dalloc(m, static_cast<size_t>(m.max_picks) * H * 4)));
     ok = ok && (m.logits = static_cast<float *>(dalloc(m, static_cast<size_t>(Mx) * V * 4)));
-    ok = ok && (m.act_h = static_cast<uint8_t *>(dalloc(m, Mx * act_bytes(H))));
-    ok = ok && (m.act_core = static_cast<uint8_t *>(dalloc(m, Mx * act_bytes(nh * hd))));
-    ok = ok && (m.act_m = static_cast<uint8_t *>(dalloc(m, m.max_picks * act_bytes(F))));
+    ok = ok && (m.act_h = static_cast<_Float16 *>(dalloc(m, Mx * act_bytes(H))));
+    ok = ok && (m.act_core = static_cast<_Float16 *>(dalloc(m, Mx * act_bytes(nh * hd))));
+    ok = ok && (m.act_m = static_cast<_Float16 *>(dalloc(m, m.max_picks * act_bytes(F))));
     ok = ok && (m.route_ids = static_cast<int32_t *>(dalloc(m, static_cast<size_t>(c.n_layers) * Mx * K * 4)));
     const int half = c.rope_dim / 2;
     const int npos = c.max_ctx + kMaxRows;

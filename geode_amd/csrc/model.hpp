@@ -65,7 +65,7 @@ struct Model {
     float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *core = nullptr, *rlogits = nullptr;
     _Float16 *q16 = nullptr;   // [max_rows][nh][hd]: the rotated queries
     float *parts = nullptr, *gu_out = nullptr, *y = nullptr, *logits = nullptr;
-    uint8_t *act_h = nullptr, *act_core = nullptr, *act_m = nullptr;
+    _Float16 *act_h = nullptr, *act_core = nullptr, *act_m = nullptr;   // the products' operands (act16)
     int32_t *route_ids = nullptr;   // [n_layers][max_rows][K]
     _Float16 *kv_all = nullptr;
     int64_t slots = 0;   // KV positions a layer holds: max_ctx rounded up to whole attention blocks

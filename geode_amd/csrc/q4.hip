@@ -6,11 +6,11 @@
 //   q4_block / e4m3_byte   yue2_q4.cpp:72-114       the packer's candidates and choice, bit for bit
 //   quantize_activation    kernels.cpp:1254-1295   amax / 127 per 16 values, lrint, clamp +-127, bit for bit
 //   rmsnorm                kernels.cpp:1520-1529   double sum of squares, 1 / sqrt(float(ss / n) + eps), x inv (1 + w)
-//   matvec_rows_q_ref      kernels.cpp:1304-1322   integer block sums (exact), block scale e4m3 x act scale, fp32
-//                                                  accumulation (here per k-lane then a fixed xor tree)
+//   matvec_rows_q_ref      kernels.cpp:1304-1322   the int8 path's products: exact weights x (q x act scale) on the
+//                                                  matrix cores, fp32 sums (mfma_gemv.hpp)
 #include "common.hpp"
-#include "gemv_core.hpp"
 #include "kernels.hpp"
+#include "mfma_gemv.hpp"
 
 namespace gv {
 
@@ -24,71 +24,64 @@ __device__ inline uint32_t affine_nibbles(uint32_t w) {
 }
 }  // namespace
 
-__global__ void q4_from_pack_kernel(const uint8_t *__restrict__ pack, int64_t rows, int64_t cols, int S, int groups,
-                                   uint8_t *__restrict__ codes, uint8_t *__restrict__ scales) {
-    const int64_t nch = cols / 32;
+// one thread per (row, 8-value code word): the pack's word w of row r into the tile layout (mfma_gemv.hpp)
+__global__ void q4_from_pack_kernel(const uint8_t *__restrict__ pack, int64_t rows, int64_t cols,
+                                    uint8_t *__restrict__ codes, uint8_t *__restrict__ scales) {
+    const int64_t nw = cols / 8;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= rows * nch) return;
-    const int64_t r = i / nch, c = i % nch;
+    if (i >= rows * nw) return;
+    const int64_t r = i / nw, wi = i % nw;
     const size_t rb = static_cast<size_t>(cols / 16) * 9;
     const uint8_t *row = pack + static_cast<size_t>(r) * rb;
-    const uint4 w = *reinterpret_cast<const uint4 *>(row + c * 16);
-    uint4 o;
-    o.x = affine_nibbles(w.x);
-    o.y = affine_nibbles(w.y);
-    o.z = affine_nibbles(w.z);
-    o.w = affine_nibbles(w.w);
-    *reinterpret_cast<uint4 *>(codes + q4_code_offset(rows, cols, S, r, c)) = o;
-    uint8_t *sd = scales + q4_scale_offset(rows, S, groups, r, c);
-    sd[0] = row[cols / 2 + 2 * c];
-    sd[1] = row[cols / 2 + 2 * c + 1];
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(row + wi * 4);
+    const int64_t T = r / kTileR, rr = r % kTileR, nsc = cols / kSuperK;
+    const int64_t sc = wi / 16, j = (wi % 16) / 4, g = wi % 4;   // word 16 sc + 4 j + g
+    const int64_t blk = T * nsc + sc;
+    *reinterpret_cast<uint32_t *>(codes + blk * 1024 + (rr + 16 * g) * 16 + j * 4) = tile_word(affine_nibbles(w));
+    if (g % 2 == 0)   // the block of (chunk j, k-groups g, g + 1): pack scale 8 sc + 2 j + g / 2
+        scales[blk * 128 + (rr * 2 + g / 2) * 4 + j] = row[cols / 2 + 8 * sc + 2 * j + g / 2];
 }
 
 int q4_from_pack(const uint8_t *pack_dev, int64_t rows, int64_t cols, float global, uint8_t *codes, uint8_t *scales,
                  Q4 &out, hipStream_t st) {
-    GV_REQUIRE(rows > 0 && cols > 0 && cols % 32 == 0, "q4: cols must be a positive multiple of 32");
-    const int S = q4_lanes_for(cols);
-    GV_REQUIRE(cols % (32 * S) == 0, "q4: cols must be a multiple of 32 x the k-lanes");
-    const int steps = static_cast<int>(cols / (32 * S)), groups = q4_groups(steps);
-    if (groups * 8 != steps) GV_CHECK_HIP(hipMemsetAsync(scales, 0, q4_scale_bytes(rows, cols), st));
-    const int64_t n = rows * (cols / 32);
+    GV_REQUIRE(rows > 0 && cols > 0 && cols % kSuperK == 0, "q4: cols must be a positive multiple of 128");
+    if (rows % kTileR != 0) {   // the last tile's missing rows: zero codes and scales (their sums are discarded)
+        const int64_t T = rows / kTileR, nsc = cols / kSuperK;
+        GV_CHECK_HIP(hipMemsetAsync(codes + T * nsc * 1024, 0, nsc * 1024, st));
+        GV_CHECK_HIP(hipMemsetAsync(scales + T * nsc * 128, 0, nsc * 128, st));
+    }
+    const int64_t n = rows * (cols / 8);
     hipLaunchKernelGGL(q4_from_pack_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, pack_dev,
-                       rows, cols, S, groups, codes, scales);
+                       rows, cols, codes, scales);
     GV_CHECK_HIP(hipGetLastError());
     out.codes = codes;
     out.scales = scales;
     out.rows = rows;
     out.cols = cols;
-    out.S = S;
-    out.steps = steps;
+    out.S = 0;
+    out.steps = 0;
     out.global = global;
     return 0;
 }
 
 // ---------------------------------------------------------------- dequant (kernels.cpp:1214-1228)
 __global__ void q4_dequant_kernel(Q4 w, float *__restrict__ out) {
-    const int64_t nch = w.cols / 32;
+    const int64_t nw = w.cols / 8;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= w.rows * nch) return;
-    const int64_t r = i / nch, c = i % nch;
-    const uint4 cw = *reinterpret_cast<const uint4 *>(w.codes + q4_code_offset(w.rows, w.cols, w.S, r, c));
-    const uint8_t *sd = w.scales + q4_scale_offset(w.rows, w.S, q4_groups(w.steps), r, c);
-    const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
-    float *o = out + r * w.cols + c * 32;
-    for (int j = 0; j < 2; ++j) {
-        const float s = __fmul_rn(e4m3_to_f32(sd[j]), w.global);   // E4M3 x global, then level x that
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t wd = words[2 * j + q];
-            for (int b = 0; b < 8; ++b) {
-                const int cp = static_cast<int>((wd >> (4 * b)) & 15u);
-                o[16 * j + 8 * q + b] = __fmul_rn(static_cast<float>(2 * cp - 15), s);
-            }
-        }
+    if (i >= w.rows * nw) return;
+    const int64_t r = i / nw, wi = i % nw;
+    uint32_t word, sb;
+    tq4_word(w, r, wi, word, sb);
+    const float s = __fmul_rn(e4m3_to_f32(sb), w.global);   // E4M3 x global, then level x that
+    float *o = out + r * w.cols + wi * 8;
+    for (int b = 0; b < 8; ++b) {
+        const int cp = static_cast<int>((word >> (4 * b)) & 15u);
+        o[b] = __fmul_rn(static_cast<float>(2 * cp - 15), s);
     }
 }
 
 int q4_dequant(const Q4 &w, float *out, hipStream_t st) {
-    const int64_t n = w.rows * (w.cols / 32);
+    const int64_t n = w.rows * (w.cols / 8);
     hipLaunchKernelGGL(q4_dequant_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, w, out);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
@@ -202,11 +195,12 @@ int q4_pack(const float *w, int64_t rows, int64_t cols, unsigned int *scratch_u3
 }
 
 // ---------------------------------------------------------------- activations
-// One workgroup per token: optional RMSNorm (kernels.cpp:1520-1529), then the int8 blocks in the products' layout
-// (common.hpp), and optionally the normalized fp32 row (the router's and the shared gate's input).
+// One workgroup per row: optional RMSNorm (kernels.cpp:1520-1529), then the products' fp16 hi + lo operands
+// (mfma_gemv.hpp) of either the int8 path's values q x (amax / 127) (quantize_activation, kernels.cpp:1254-1295,
+// bit for bit) or the exact fp32 values; optionally the normalized fp32 row too (the router's input).
 __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restrict__ x, int64_t ldx, int cols,
-                                                           const float *__restrict__ norm_w, float eps,
-                                                           uint8_t *__restrict__ act, int64_t act_stride,
+                                                           const float *__restrict__ norm_w, float eps, int exact,
+                                                           _Float16 *__restrict__ act, int64_t act_stride,
                                                            float *__restrict__ h_out, int64_t ldh) {
     const int t = blockIdx.x;
     const float *xr = x + t * ldx;
@@ -227,119 +221,111 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
         __syncthreads();
         inv = inv_s;
     }
-    uint8_t *ar = act + t * act_stride;
+    _Float16 *ar = act + t * act_stride;
     for (int b = threadIdx.x; b < cols / 16; b += 256) {
         float v[16];
-        float amax = 0.0f;
         for (int i = 0; i < 16; ++i) {
             const int c = b * 16 + i;
             float y = xr[c];
             if (norm_w) y = __fmul_rn(__fmul_rn(y, inv), __fadd_rn(1.0f, norm_w[c]));
             v[i] = y;
-            amax = fmaxf(amax, fabsf(y));
         }
         if (h_out)
             for (int i = 0; i < 16; ++i) h_out[t * ldh + b * 16 + i] = v[i];
-        const float s = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-        int sum = 0;
-        uint32_t dw[4] = {0, 0, 0, 0};   // word 0: even, odd; word 1: even, odd
-        for (int i = 0; i < 16; ++i) {
-            const int q = min(max(static_cast<int>(rintf(__fmul_rn(v[i], qi))), -127), 127);
-            sum += q;
-            const int word = i / 8, within = i % 8;
-            dw[2 * word + (within & 1)] |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * (within >> 1));
-        }
-        const int c = b / 2, j = b % 2;
-        uint8_t *chunk = ar + static_cast<size_t>(c) * kActChunkBytes;
-        *reinterpret_cast<uint4 *>(chunk + 16 * j) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
-        reinterpret_cast<float *>(chunk + 32)[j] = s;
-        reinterpret_cast<int *>(chunk + 40)[j] = -15 * sum;
+        act16_block(v, b, ar, exact != 0);
     }
 }
 
-int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, uint8_t *act,
-                 int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st) {
+int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, int exact,
+                 _Float16 *act, int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st) {
     GV_REQUIRE(cols % 32 == 0 && M > 0, "quantize_act: cols must be a multiple of 32");
-    hipLaunchKernelGGL(quantize_act_kernel, dim3(M), dim3(256), 0, st, x, ldx, cols, norm_w, eps, act, act_stride,
-                       h_out, ldh);
+    hipLaunchKernelGGL(quantize_act_kernel, dim3(M), dim3(256), 0, st, x, ldx, cols, norm_w, eps, exact, act,
+                       act_stride, h_out, ldh);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-// ---------------------------------------------------------------- the skinny GEMM (gemv_core.hpp)
-template <int S, int R, int MT>
-__global__ __launch_bounds__(256) void gemv_q4_kernel(Q4 w, const uint8_t *__restrict__ act, int64_t act_stride,
-                                                      int M, GemvOut out) {
-    constexpr int G = 64 / S;
-    constexpr int WROWS = G * R;
-    extern __shared__ uint4 lds_u4[];
-    uint8_t *lds = reinterpret_cast<uint8_t *>(lds_u4);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane / S, k = lane % S;
-    const int64_t abytes = (w.cols / 32) * kActChunkBytes;
-    load_acts(lds, act, act_stride, abytes, M);
+// ---------------------------------------------------------------- the skinny GEMM (mfma_gemv.hpp)
+// WMAX: the most waves a launch of the instance takes (8: a budget of 256 VGPRs a lane)
+template <int KW, int NTT, int WMAX>
+__global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16 *__restrict__ act,
+                                                            int64_t act_stride, int M, int sc0, int tiles_per_wg,
+                                                            GemvOut out) {
+    extern __shared__ f4 part_lds[];
+    __shared__ uint2 tab[256];
+    fill_e4m3_table(tab);
     __syncthreads();
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * WROWS;
-    if (row0 >= w.rows) return;
-    float acc[R][MT];
-    gemv_wave<S, R, MT>(w.codes, w.scales, w.rows, w.cols, w.steps, row0, lds, abytes, M, g, k, acc);
-    gemv_reduce<S, R, MT>(acc, M);
-    if (k != 0) return;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        const int64_t row = row0 + i * G + g;
-        if (row >= w.rows) continue;
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            if (t >= M) break;
-            out.put(row, t, acc[i][t]);
-        }
-    }
+    const int64_t ntiles = tiles_rows(w.rows);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
+    const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
+    if (t0 >= ntiles) return;
+    mfma_tiles<KW, NTT>(
+        w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, t0, t1, M,
+        [&](int j) { return act + j * act_stride; }, [&](int64_t row, int j, float v) { out.put(row, j, v); },
+        part_lds, tab);
 }
 
-template <int S, int R, int MT>
-static int launch_gemv(const Q4 &w, const uint8_t *act, int64_t act_stride, int M, const GemvOut &out,
-                       hipStream_t st) {
-    constexpr int WROWS = (64 / S) * R;
-    const int64_t wg = (w.rows + 4 * WROWS - 1) / (4 * WROWS);
-    const size_t lds = static_cast<size_t>(M) * act_bytes(w.cols);
+int mfma_split(int64_t K, int ntt, int &waves, int &kw) {
+    const int chunks = static_cast<int>(K / 32);
+    kw = ntt == 1 ? 16 : 8;
+    while (kw > 4 && (chunks % kw || chunks / kw < 2)) kw /= 2;
+    waves = chunks / kw;
+    return K % kSuperK == 0 && waves >= 1 && waves <= 8;
+}
+
+// tiles a workgroup: ~1024 workgroups when the matrix has the tiles, the waves' partial sums within 48 KB of LDS
+inline int64_t tiles_per_wg(int64_t ntiles, int waves, int ntt) {
+    const int64_t cap = waves > 1 ? std::max(1, 48 / (waves * ntt)) : 64;
+    return std::min<int64_t>(cap, std::max<int64_t>(1, (ntiles + 1023) / 1024));
+}
+
+template <int KW, int NTT, int WMAX>
+static int launch_gemv(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, int sc0, int waves,
+                       const GemvOut &out, hipStream_t st) {
+    const int64_t ntiles = tiles_rows(w.rows);
+    const int64_t per = tiles_per_wg(ntiles, waves, NTT);
+    const int64_t wg = (ntiles + per - 1) / per;
+    const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<S, R, MT>), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL((gemv_q4_kernel<S, R, MT>), dim3(static_cast<unsigned>(wg)), dim3(256), lds, st, w, act,
-                       act_stride, M, out);
+    if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX>), 64 * 1024, granted) != 0) return -1;
+    hipLaunchKernelGGL((gemv_q4_kernel<KW, NTT, WMAX>), dim3(static_cast<unsigned>(wg)), dim3(64 * waves), lds, st, w,
+                       act, act_stride, M, sc0, static_cast<int>(per), out);
     return 0;
 }
 
-template <int S, int R>
-static int dispatch_mt(const Q4 &w, const uint8_t *act, int64_t act_stride, int M, const GemvOut &out,
-                       hipStream_t st) {
-    if (M <= 1) return launch_gemv<S, R, 1>(w, act, act_stride, M, out, st);
-    if (M <= 2) return launch_gemv<S, R, 2>(w, act, act_stride, M, out, st);
-    if (M <= 4) return launch_gemv<S, R, 4>(w, act, act_stride, M, out, st);
-    if (M <= 8) return launch_gemv<S, R, 8>(w, act, act_stride, M, out, st);
-    if (M <= 16) return launch_gemv<S, (R > 2 ? 2 : R), 16>(w, act, act_stride, M, out, st);
-    return launch_gemv<S, 1, 32>(w, act, act_stride, M, out, st);
+// one launch over super-chunks [sc0, sc0 + n) of every row
+static int gemv_range(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, int ntt, int sc0, int n,
+                      const GemvOut &out, hipStream_t st) {
+    int waves, kw;
+    if (!mfma_split(static_cast<int64_t>(n) * kSuperK, ntt, waves, kw)) {
+        set_error("gemv_q4: no split of this K range");
+        return -1;
+    }
+    if (ntt == 1) {
+        if (kw == 16) return launch_gemv<16, 1, 8>(w, act, act_stride, M, sc0, waves, out, st);
+        if (kw == 8) return launch_gemv<8, 1, 8>(w, act, act_stride, M, sc0, waves, out, st);
+        return launch_gemv<4, 1, 8>(w, act, act_stride, M, sc0, waves, out, st);
+    }
+    if (kw == 8) return launch_gemv<8, 2, 8>(w, act, act_stride, M, sc0, waves, out, st);
+    return launch_gemv<4, 2, 8>(w, act, act_stride, M, sc0, waves, out, st);
 }
 
-int gemv_q4(const Q4 &w, const uint8_t *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st) {
-    GV_REQUIRE(M >= 1 && M <= kMaxRows, "gemv_q4: 1 <= M <= 32 tokens");
-    GV_REQUIRE(static_cast<size_t>(M) * act_bytes(w.cols) <= 160 * 1024, "gemv_q4: activations exceed LDS");
-    // rows a lane: as many as keep >= 512 workgroups (a large matrix takes 4, a small one 1)
-    const int64_t G = 64 / w.S;
-    const int R = w.rows >= 512 * 4 * G * 4 ? 4 : w.rows >= 512 * 4 * G * 2 ? 2 : 1;
-    int rc;
-    switch (w.S * 8 + R) {
-    case 1 * 8 + 1: case 1 * 8 + 2: case 1 * 8 + 4: rc = dispatch_mt<1, 1>(w, act, act_stride, M, out, st); break;
-    case 2 * 8 + 1: rc = dispatch_mt<2, 1>(w, act, act_stride, M, out, st); break;
-    case 2 * 8 + 2: case 2 * 8 + 4: rc = dispatch_mt<2, 2>(w, act, act_stride, M, out, st); break;
-    case 4 * 8 + 1: rc = dispatch_mt<4, 1>(w, act, act_stride, M, out, st); break;
-    case 4 * 8 + 2: case 4 * 8 + 4: rc = dispatch_mt<4, 2>(w, act, act_stride, M, out, st); break;
-    case 8 * 8 + 1: rc = dispatch_mt<8, 1>(w, act, act_stride, M, out, st); break;
-    case 8 * 8 + 2: rc = dispatch_mt<8, 2>(w, act, act_stride, M, out, st); break;
-    case 8 * 8 + 4: rc = dispatch_mt<8, 4>(w, act, act_stride, M, out, st); break;
-    default: set_error("gemv_q4: unsupported k-lane count"); return -1;
+int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st) {
+    GV_REQUIRE(M >= 1 && M <= kMaxRows, "gemv_q4: 1 <= M <= 32 rows");
+    GV_REQUIRE(w.cols % kSuperK == 0, "gemv_q4: cols must be a multiple of 128");
+    const int ntt = M <= 16 ? 1 : 2;
+    const int nsc = static_cast<int>(w.cols / kSuperK);
+    // K ranges whose activations fit the waves' registers: one launch up to 4096 (2048 for 17..32 rows) values,
+    // later ranges adding to the first's sums
+    for (int sc0 = 0, part = 0; sc0 < nsc; ++part) {
+        int n = std::min(nsc - sc0, ntt == 1 ? 32 : 16);
+        int waves, kw;
+        while (n > 1 && !mfma_split(static_cast<int64_t>(n) * kSuperK, ntt, waves, kw)) --n;
+        GemvOut o = out;
+        if (part > 0) o.accumulate = 1;
+        if (gemv_range(w, act, act_stride, M, ntt, sc0, n, o, st) != 0) return -1;
+        sc0 += n;
     }
-    if (rc != 0) return rc;
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }

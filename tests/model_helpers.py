@@ -4,7 +4,7 @@ import numpy as np
 import pyoracle as po
 
 # a small model of the C4 family (gated attention + MoE), quick for the oracle
-SMALL = dict(hidden=256, vocab=512, n_layers=2, n_experts=16, top_k=4, moe_ff=64, shared_ff=64, n_heads=4,
+SMALL = dict(hidden=256, vocab=512, n_layers=2, n_experts=16, top_k=4, moe_ff=128, shared_ff=128, n_heads=4,
              n_kv_heads=2, head_dim=64, rope_dim=16, rope_theta=1e7, eps=1e-6, max_ctx=160, max_rows=17)
 # router sigma giving unit-std router logits for unit-RMS inputs
 SMALL_ROUTER_SIGMA = 1.0 / np.sqrt(SMALL["hidden"])

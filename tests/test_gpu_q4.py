@@ -1,5 +1,6 @@
-"""GPU parity of the q4 path (C ABI) against the oracle: dequant and the packer bit for bit, activation quantization
-bit for bit, the int8 skinny GEMM within fp32 summation order, the C1 dense SwiGLU MLP within 1e-2."""
+"""GPU parity of the q4 path (C ABI) against the oracle: dequant and the packer bit for bit, the int8 activation codes
+bit for bit, the skinny products (matrix cores) within fp32 summation order of the int8 path, the C1 dense SwiGLU
+MLP within 1e-2."""
 import numpy as np
 import pytest
 
@@ -20,7 +21,7 @@ def _u32(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 64), (300, 256), (256, 512), (1024, 2048), (520, 6144)])
+@pytest.mark.parametrize("rows,cols", [(64, 128), (300, 256), (256, 512), (1024, 2048), (520, 6144)])
 def test_dequant_bit_exact(gv, rows, cols):
     wq, s2 = po.q4_random(11 + rows, rows, cols)
     m = gv.Q4Matrix(wq, rows, cols, s2)
@@ -30,10 +31,11 @@ def test_dequant_bit_exact(gv, rows, cols):
 
 
 def test_dequant_every_code_and_scale(gv):
-    # every code byte with every finite scale byte: rows of 32 values, 2 blocks, scales 0..0x7E
-    rows, cols = 127, 32
-    codes = np.tile(np.arange(16, dtype=np.uint8) * 17, 1)[None, :].repeat(rows, 0)  # both nibbles equal
-    scales = np.stack([np.arange(127, dtype=np.uint8), np.arange(127, dtype=np.uint8)[::-1]], 1)
+    # every code byte with every finite scale byte: rows of 128 values, 8 blocks, scales 0..0x7E
+    rows, cols = 127, 128
+    codes = np.tile(np.arange(16, dtype=np.uint8) * 17, 4)[None, :].repeat(rows, 0)  # both nibbles equal
+    sc = np.arange(127, dtype=np.uint8)
+    scales = np.stack([sc, sc[::-1], (sc + 7) % 127, (sc + 50) % 127, sc, sc[::-1], (sc * 3) % 127, (sc + 99) % 127], 1)
     pack = np.concatenate([codes, scales], 1)
     m = gv.Q4Matrix(pack, rows, cols, 0.37)
     assert np.array_equal(_u32(m.dequant()), _u32(po.dequant(pack, cols, 0.37)))
@@ -53,6 +55,18 @@ def test_packer_bit_exact(gv, rows, cols):
     assert np.array_equal(got, want)
 
 
+def _act16_values(raw, cols):
+    """the products' operands (per 32-value chunk and 8-value group: 8 hi then 8 lo halves, values in the order
+    0 4 1 5 2 6 3 7) back to one fp64 value per column"""
+    h = raw.reshape(cols // 32, 4, 2, 8).astype(np.float64)
+    v = h[:, :, 0, :] + h[:, :, 1, :]
+    order = [0, 4, 1, 5, 2, 6, 3, 7]
+    out = np.empty((cols // 32, 4, 8))
+    for slot, u in enumerate(order):
+        out[:, :, u] = v[:, :, slot]
+    return out.reshape(cols)
+
+
 @pytest.mark.parametrize("norm", [False, True])
 def test_quantize_bit_exact(gv, norm):
     M, cols = 5, 2048
@@ -63,25 +77,21 @@ def test_quantize_bit_exact(gv, norm):
     act = gv.DeviceBuffer(M * gv.act_bytes(cols))
     h = gv.DeviceBuffer(M * cols * 4)
     gv.check(gv.lib.gv_quantize(dx.ptr, cols, M, cols, dw.ptr if norm else None, 1e-6, act.ptr, h.ptr), "quantize")
-    raw = act.download(np.uint8, (M, cols // 32, 48))
+    raw = act.download(np.float16, (M, cols * 2))
     hh = h.download(np.float32, (M, cols))
     for t in range(M):
         xt = po.rmsnorm(x[t], w) if norm else x[t]
-        assert np.array_equal(_u32(hh[t]), _u32(xt))
-        q, s, b = po.quantize_activation(xt)
-        qb = raw[t, :, :32].reshape(cols // 32, 4, 2, 4)  # chunk, word, even/odd, 4 values
-        got_q = np.empty((cols // 32, 4, 8), np.int8)
-        got_q[:, :, 0::2] = qb[:, :, 0, :].view(np.int8)
-        got_q[:, :, 1::2] = qb[:, :, 1, :].view(np.int8)
-        assert np.array_equal(got_q.reshape(-1), q)
-        sc = raw[t, :, 32:40].copy().view(np.float32).reshape(-1)
-        corr = raw[t, :, 40:48].copy().view(np.int32).reshape(-1)
-        assert np.array_equal(_u32(sc), _u32(s))
-        assert np.array_equal(corr, -15 * b)
+        assert np.array_equal(_u32(hh[t]), _u32(xt))          # the RMSNorm bit for bit
+        q, s, _ = po.quantize_activation(xt)
+        val = _act16_values(raw[t], cols)
+        srep = np.repeat(s.astype(np.float64), 16)
+        assert np.array_equal(np.rint(val / np.where(srep > 0, srep, 1)).astype(np.int64), q)   # the int8 codes
+        want = (q.astype(np.float32) * np.repeat(s, 16)).astype(np.float64)                   # q x scale in fp32
+        assert np.abs(val - want).max() <= 2.0 ** -21 * np.abs(want).max()                    # as hi + lo halves
 
 
-@pytest.mark.parametrize("rows,cols,M", [(64, 64, 1), (256, 256, 3), (1024, 2048, 5), (2048, 512, 5),
-                                          (2048, 4096, 17), (9216, 2048, 5), (600, 2048, 32)])
+@pytest.mark.parametrize("rows,cols,M", [(64, 128, 1), (256, 256, 3), (1024, 2048, 5), (2048, 512, 5),
+                                          (2048, 4096, 17), (9216, 2048, 5), (600, 2048, 32), (8192, 6144, 16)])
 def test_gemv_int8_path(gv, rows, cols, M):
     wq, s2 = po.q4_random(31 + rows + cols, rows, cols)
     m = gv.Q4Matrix(wq, rows, cols, s2)
