@@ -205,7 +205,7 @@ size_t gv_act_bytes(int64_t cols) { return act_bytes(cols); }
 int gv_quantize(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, uint8_t *act,
                 float *h_out) {
     if (ensure_init() != 0) return -1;
-    return quantize_act(x, ldx, M, cols, norm_w, eps, 0, reinterpret_cast<_Float16 *>(act), act_halves(cols), h_out, cols,
+    return quantize_act(x, ldx, M, cols, norm_w, eps, reinterpret_cast<_Float16 *>(act), act_halves(cols), h_out, cols,
                         stream());
 }
 
@@ -236,11 +236,11 @@ int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, 
     hipStream_t st = stream();
     if (f16_to_f32(x_f16, static_cast<int64_t>(M) * H, x, st) != 0) return -1;
     const int64_t ab_h = act_halves(H), ab_f = act_halves(F);
-    if (quantize_act(x, H, M, static_cast<int>(H), nullptr, 0.0f, 0, act, ab_h, nullptr, 0, st) != 0) return -1;
+    if (quantize_act(x, H, M, static_cast<int>(H), nullptr, 0.0f, act, ab_h, nullptr, 0, st) != 0) return -1;
     if (gemv_q4(to_q4(*gate), act, ab_h, M, gemv_out(g, F, gate->global), st) != 0) return -1;
     if (gemv_q4(to_q4(*up), act, ab_h, M, gemv_out(u, F, up->global), st) != 0) return -1;
     if (swiglu(g, u, static_cast<int64_t>(M) * F, m, st) != 0) return -1;
-    if (quantize_act(m, F, M, static_cast<int>(F), nullptr, 0.0f, 0, act, ab_f, nullptr, 0, st) != 0) return -1;
+    if (quantize_act(m, F, M, static_cast<int>(F), nullptr, 0.0f, act, ab_f, nullptr, 0, st) != 0) return -1;
     return gemv_q4(to_q4(*down), act, ab_f, M, gemv_out(y, H, down->global), st);
 }
 
@@ -321,7 +321,7 @@ int gv_gemm(gv_ctx *g, int id, int n, const float *const *xs, float *const *ys) 
         for (int t = 0; t < m; ++t)
             GV_CHECK_HIP(hipMemcpyAsync(x + static_cast<size_t>(t) * q.cols, xs[t0 + t], q.cols * 4,
                                         hipMemcpyHostToDevice, st));
-        if (quantize_act(x, q.cols, m, static_cast<int>(q.cols), nullptr, 0.0f, 0, act, act_halves(q.cols), nullptr, 0,
+        if (quantize_act(x, q.cols, m, static_cast<int>(q.cols), nullptr, 0.0f, act, act_halves(q.cols), nullptr, 0,
                          st) != 0)
             return -1;
         if (gemv_q4(q, act, act_halves(q.cols), m, gemv_out(y, q.rows, q.global), st) != 0)
@@ -364,7 +364,7 @@ int gv_mlp(gv_ctx *g, int gate, int up, int n_down, const int *downs, int act, i
         for (int t = 0; t < m; ++t)
             GV_CHECK_HIP(hipMemcpyAsync(x + static_cast<size_t>(t) * H, xs[t0 + t], H * 4, hipMemcpyHostToDevice, st));
         const int64_t abh = act_halves(H);
-        if (quantize_act(x, H, m, static_cast<int>(H), nullptr, 0.0f, 0, a, abh, nullptr, 0, st) != 0) return -1;
+        if (quantize_act(x, H, m, static_cast<int>(H), nullptr, 0.0f, a, abh, nullptr, 0, st) != 0) return -1;
         if (gemv_q4(qg, a, abh, m, gemv_out(gg, F, qg.global), st) != 0) return -1;
         if (gemv_q4(qu, a, abh, m, gemv_out(uu, F, qu.global), st) != 0) return -1;
         if (swiglu(gg, uu, static_cast<int64_t>(m) * F, mm, st) != 0) return -1;
@@ -372,7 +372,7 @@ int gv_mlp(gv_ctx *g, int gate, int up, int n_down, const int *downs, int act, i
         for (int j = 0; j < n_down; ++j) {   // each part's results added (npu_api.h:62-65)
             const Q4 &qd = g->mats[static_cast<size_t>(downs[j])].q;
             const int64_t ab = act_halves(qd.cols);
-            if (quantize_act(mm + c0, F, m, static_cast<int>(qd.cols), nullptr, 0.0f, 0, a, ab, nullptr, 0, st) != 0)
+            if (quantize_act(mm + c0, F, m, static_cast<int>(qd.cols), nullptr, 0.0f, a, ab, nullptr, 0, st) != 0)
                 return -1;
             if (gemv_q4(qd, a, ab, m, gemv_out(y, drows, qd.global, j > 0), st) != 0) return -1;
             c0 += qd.cols;

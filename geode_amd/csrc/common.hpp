@@ -75,9 +75,55 @@ __device__ inline T wave_sum_xor(T v, int width) {
     return v;
 }
 
+// y as two fp16 halves, hi = y rounded to fp16 and lo = (y - hi) rounded, so hi + lo = y to 2^-22 relative. The
+// empty asm pins y as a computed fp32 value: without it the compiler may fold the product that made y into the
+// conversion (one rounding, v_fma_mix) for one use of hi and not for another, and hi + lo is then off by an ulp.
+__device__ inline void split_f16(float y, _Float16 &hi, _Float16 &lo) {
+    asm volatile("" : "+v"(y));
+    hi = static_cast<_Float16>(y);
+    lo = static_cast<_Float16>(y - static_cast<float>(hi));
+}
+
+// DPP lane moves within 16-lane rows (quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror = 0x141,
+// row_mirror = 0x140): full-rate VALU, no LDS crossbar round trip
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ inline double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), CTRL, 0xF, 0xF, false);
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), CTRL, 0xF, 0xF,
+                                                    false);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// the sum over the wave's 64 lanes, the same bits in every lane: pairs, quads, 8s and 16s of lanes in rows, then the
+// rows' sums (0 + 16) + (32 + 48)
+__device__ inline double wave_sum(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    auto lane_d = [&](int l) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), l);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), l);
+        return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    return (lane_d(0) + lane_d(16)) + (lane_d(32) + lane_d(48));
+}
+
+// the maximum over the wave's 64 lanes, in every lane (a uniform value)
 __device__ inline float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    auto lane_f = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+    return fmaxf(fmaxf(lane_f(0), lane_f(16)), fmaxf(lane_f(32), lane_f(48)));
 }
 
 }  // namespace gv

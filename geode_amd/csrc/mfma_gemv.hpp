@@ -33,42 +33,100 @@ __host__ __device__ inline int64_t tiles_rows(int64_t rows) { return (rows + kTi
 inline size_t tq4_code_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * kTileR * (cols / 2); }
 inline size_t tq4_scale_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * kTileR * (cols / 16); }
 
-// The activations' layout for these kernels: per row, per 32-value chunk c and k-group g, 8 hi halves then 8 lo
-// halves (32 bytes) of values 32c + 8g + (0 4 1 5 2 6 3 7), the order the nibble pairs come out in.
+// The activations' layout for these kernels: per row, per k-group g (values 8 g .. 8 g + 7; chunk g / 4, k-group g % 4
+// of it), 8 hi halves then 8 lo halves (32 bytes) of values 8 g + (0 4 1 5 2 6 3 7), the order the nibble pairs come
+// out in.
 inline size_t act16_row_bytes(int64_t cols) { return static_cast<size_t>(cols) * 4; }
 
-// 16 values (block b of a row) into the row's operands: the int8 path's q x (amax / 127) (quantize_activation,
-// engine/src/kernels.cpp:1254-1295, bit for bit) unless exact, then hi + lo halves at their slots
-__device__ inline void act16_block(float (&v)[16], int b, _Float16 *ar, bool exact) {
-    if (!exact) {
-        float amax = 0.0f;
+// One k-group's operands: v = values 8 g .. 8 g + 7 of a row, the int8 path's q x (amax / 127) (quantize_activation,
+// engine/src/kernels.cpp:1254-1295, bit for bit) written as hi + lo halves at the group's 32 bytes. The 16-value
+// block is the groups g and g ^ 1, held by lanes l and l ^ 1: every lane of the wave calls this (live = false: a lane
+// past the row's end, which stores nothing).
+__device__ inline void act16_group(const float (&v)[8], int g, bool live, _Float16 *ar) {
+    float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        const float s = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    if (!live) return;
+    const float s = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    h8 hi, lo;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int q = min(max(static_cast<int>(rintf(__fmul_rn(v[i], qi))), -127), 127);
-            v[i] = __fmul_rn(static_cast<float>(q), s);
-        }
+    for (int i = 0; i < 8; ++i) {   // slot of value i: (0 4 1 5 2 6 3 7)
+        const int q = min(max(static_cast<int>(rintf(__fmul_rn(v[i], qi))), -127), 127);
+        const float y = __fmul_rn(static_cast<float>(q), s);
+        const int slot = i < 4 ? 2 * i : 2 * (i - 4) + 1;
+        _Float16 yh, yl;
+        split_f16(y, yh, yl);
+        hi[slot] = yh;
+        lo[slot] = yl;
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {   // value k = 16 b + i: chunk k / 32, k-group (k % 32) / 8, slot of k % 8
-        const int k = b * 16 + i, u = k % 8;
-        const int slot = u < 4 ? 2 * u : 2 * (u - 4) + 1;
-        _Float16 *p = ar + (static_cast<int64_t>(k / 32) * 4 + (k % 32) / 8) * 16;
-        const _Float16 hi = static_cast<_Float16>(v[i]);
-        p[slot] = hi;
-        p[8 + slot] = static_cast<_Float16>(v[i] - static_cast<float>(hi));
-    }
+    h8 *p = reinterpret_cast<h8 *>(ar + static_cast<int64_t>(g) * 16);
+    p[0] = hi;
+    p[1] = lo;
 }
 
-// a row of cols values (any memory) into its operands, the workgroup's threads over its blocks
-__device__ inline void act16_row(const float *v, int cols, _Float16 *ar, bool exact) {
-    for (int b = threadIdx.x; b < cols / 16; b += blockDim.x) {
-        float blk[16];
+// A row of cols (a multiple of 16, at most 32 blockDim) values into its operands, optionally RMSNorm(1 + w) first
+// (rmsnorm's arithmetic: the double sum of squares, inv = 1 / sqrt(float(ss / n) + eps), x inv (1 + w)) and the
+// normalized fp32 row to h (if not null). The whole workgroup takes the row, thread i the 8-value groups i, i +
+// blockDim, ... (up to 4), loaded once; red: LDS of 16 x 8 doubles (unused without norm_w). x may be any readable
+// memory (global or LDS), 16-byte aligned.
+__device__ inline void norm_quant_row(const float *x, int cols, const float *norm_w, float eps, _Float16 *ar, float *h,
+                                      double (*red)[8]) {
+    const int ng = cols / 8, nthr = blockDim.x;
+    float v[4][8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) blk[i] = v[b * 16 + i];
-        act16_block(blk, b, ar, exact);
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * nthr;
+        float4 a = make_float4(0, 0, 0, 0), b = a;
+        if (g < ng) {
+            a = *reinterpret_cast<const float4 *>(x + g * 8);
+            b = *reinterpret_cast<const float4 *>(x + g * 8 + 4);
+        }
+        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[q][i] = t[i];
+    }
+    if (norm_w) {
+        float w1[4][8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int g = threadIdx.x + q * nthr;
+            float4 a = make_float4(0, 0, 0, 0), b = a;
+            if (g < ng) {
+                a = *reinterpret_cast<const float4 *>(norm_w + g * 8);
+                b = *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4);
+            }
+            const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w1[q][i] = __fadd_rn(1.0f, t[i]);
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += static_cast<double>(v[q][i]) * static_cast<double>(v[q][i]);
+        ss = wave_sum(ss);
+        __syncthreads();   // red may still be read by an earlier call
+        if (threadIdx.x % 64 == 0) red[threadIdx.x / 64][0] = ss;
+        __syncthreads();
+        double tot = 0.0;
+        for (int w = 0; w < nthr / 64; ++w) tot += red[w][0];
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(cols)), eps)));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[q][i] = __fmul_rn(__fmul_rn(v[q][i], inv), w1[q][i]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (q * nthr >= ng) break;   // uniform: no lane has a group from here on
+        const int g = threadIdx.x + q * nthr;
+        const bool live = g < ng;
+        if (h && live) {
+            *reinterpret_cast<float4 *>(h + g * 8) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+            *reinterpret_cast<float4 *>(h + g * 8 + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+        }
+        act16_group(v[q], g, live, ar);
     }
 }
 

@@ -116,9 +116,10 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
     }
     if (kind == 0) {   // the query as two halves, hi + lo, for near-fp32 scores from fp16 products
         const int64_t qo = (static_cast<int64_t>(t) * nh + head) * hd + i;
-        const _Float16 hi = static_cast<_Float16>(out);
+        _Float16 hi, lo;
+        split_f16(out, hi, lo);
         q_out[qo] = hi;
-        q_out[qo + static_cast<int64_t>(sp->M) * nh * hd] = static_cast<_Float16>(out - static_cast<float>(hi));
+        q_out[qo + static_cast<int64_t>(sp->M) * nh * hd] = lo;
     } else {
         kv[k_index(slots, hd, kh, slot, i)] = static_cast<_Float16>(out);
     }
@@ -128,175 +129,370 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
-// Split-KV attention on the matrix cores: a wave per (16 queries, block of 64 positions, KV head); the queries of a
-// KV head are its query heads x the rows. S^T = K Q^T (v_mfma_f32_16x16x32_f16: fp16 keys, the queries as hi + lo
-// fp16 halves, fp32 sums), masked to the context plus each row's visible rows, then per query the block's
-// maximum, the weights exp(s - max) and their sum; O^T = V^T P^T with the weights as hi + lo halves. Writes the block's
-// partial (weighted values, max, sum) as attend_heads does per block (model.cpp:3894-4018); attn_merge joins them.
-__global__ __launch_bounds__(64) void attn_mfma_kernel(const _Float16 *__restrict__ q16, const _Float16 *__restrict__ kv,
-                                                       int64_t slots, int nh, int nkv, int hd,
-                                                       const StepParams *__restrict__ sp, float *__restrict__ parts,
-                                                       int nb_max) {
-    const int qt = blockIdx.x, b = blockIdx.y, kh = blockIdx.z;
+// Split-KV attention on the matrix cores: a workgroup (4 waves) per (block of 64 positions, KV head), the block's
+// keys [64][hd] and values [hd][64] staged in LDS by all its threads (positions past the context as zeros), then a
+// wave per 16 queries of the KV head (its query heads x the rows). S^T = K Q^T (v_mfma_f32_16x16x32_f16: fp16 keys,
+// the queries as hi + lo fp16 halves, fp32 sums), masked to the context plus each row's visible rows, then per query
+// the block's maximum, the weights exp(s - max) and their sum; O^T = V^T P^T with the weights as hi + lo halves.
+// Writes the block's partial (weighted values, max, sum) as attend_heads does per block (model.cpp:3894-4018);
+// attn_merge joins them.
+__host__ __device__ inline int attn_k_ld(int hd) { return hd + 8; }   // halves a staged key row (bank spread)
+constexpr int kAttnVld = kAttnBlock + 8;                              // halves a staged value row
+inline size_t attn_lds(int hd) { return (static_cast<size_t>(kAttnBlock) * attn_k_ld(hd) + hd * kAttnVld) * 2; }
+
+__global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restrict__ q16,
+                                                         const _Float16 *__restrict__ kv, int64_t slots, int nh,
+                                                         int nkv, int hd, const StepParams *__restrict__ sp,
+                                                         float *__restrict__ parts, int nb_max) {
+    extern __shared__ _Float16 lds_h[];
+    const int b = blockIdx.x, kh = blockIdx.y;
     const int pos = sp->pos, M = sp->M, total = pos + M;
-    const int group = nh / nkv, NQ = group * M;
     const int s0 = b * kAttnBlock;
-    if (s0 >= total || qt * 16 >= NQ) return;
-    const int l = threadIdx.x, lq = l % 16, lg = l / 16;
-    const int qi = qt * 16 + lq;
-    const bool qvalid = qi < NQ;
-    const int tq = qvalid ? qi / group : 0, hq = kh * group + (qvalid ? qi % group : 0);
-    const int nch = hd / 32;
-    // the queries as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query lq
-    half8 qb[8], ql[8];
-    const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
-#pragma unroll
-    for (int ch = 0; ch < 8; ++ch) {
-        const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-        const int64_t qo = (static_cast<int64_t>(tq) * nh + hq) * hd + ch * 32 + 8 * lg;
-        qb[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qo) : z;
-        ql[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
+    if (s0 >= total) return;
+    const int kld = attn_k_ld(hd);
+    _Float16 *ks = lds_h, *vs = lds_h + kAttnBlock * kld;
+    {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load
+        const _Float16 *kg = kv + k_index(slots, hd, kh, s0, 0);
+        const _Float16 *vg = kv + v_index(slots, hd, nkv, kh, s0, 0);
+        const int kpr = hd / 8;   // loads a key row
+        for (int i = threadIdx.x; i < kAttnBlock * kpr; i += blockDim.x) {
+            const int r = i / kpr, c = i % kpr;
+            const uint4 v = s0 + r < total ? *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8)
+                                           : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(ks + r * kld + c * 8) = v;
+        }
+        for (int i = threadIdx.x; i < hd * (kAttnBlock / 8); i += blockDim.x) {
+            const int d = i / (kAttnBlock / 8), c = i % (kAttnBlock / 8);
+            uint4 v = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(d) * kAttnBlock + c * 8);
+            const int lim = total - s0 - c * 8;   // positions of this load inside the context
+            if (lim < 8) {
+                uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                for (int k = 0; k < 4; ++k) {
+                    if (2 * k >= lim) u[k] = 0;
+                    else if (2 * k + 1 >= lim) u[k] &= 0xFFFFu;
+                }
+                v = make_uint4(u[0], u[1], u[2], u[3]);
+            }
+            *reinterpret_cast<uint4 *>(vs + d * kAttnVld + c * 8) = v;
+        }
     }
+    __syncthreads();
+    const int group = nh / nkv, NQ = group * M, nqt = (NQ + 15) / 16;
+    const int wave = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
+    const int nch = hd / 32;
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(hd)));
-    const uint32_t vis = qvalid ? sp->vis[tq] : 0u;
-    float sc[4][4];
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-        float4v c = {0, 0, 0, 0};
-        const _Float16 *krow = kv + k_index(slots, hd, kh, s0 + pt * 16 + lq, 8 * lg);
+    const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
+    for (int qt = wave; qt < nqt; qt += 4) {
+        const int qi = qt * 16 + lq;
+        const bool qvalid = qi < NQ;
+        const int tq = qvalid ? qi / group : 0, hq = kh * group + (qvalid ? qi % group : 0);
+        // the queries as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query lq
+        half8 qb[8], ql[8];
 #pragma unroll
         for (int ch = 0; ch < 8; ++ch) {
-            if (ch >= nch) break;
-            const half8 a = *reinterpret_cast<const half8 *>(krow + ch * 32);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ch], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ch], c, 0, 0, 0);
+            const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            const int64_t qo = (static_cast<int64_t>(tq) * nh + hq) * hd + ch * 32 + 8 * lg;
+            qb[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qo) : z;
+            ql[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
         }
+        const uint32_t vis = qvalid ? sp->vis[tq] : 0u;
+        float sc[4][4];
+        float mx = -__builtin_inff();
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {   // S^T[position pt*16 + 4 lg + r][query lq]
-            const int slot = s0 + pt * 16 + 4 * lg + r;
-            const bool ok = qvalid && slot < total && (slot < pos || ((vis >> (slot - pos)) & 1u));
-            sc[pt][r] = ok ? c[r] * scale : -__builtin_inff();
-            mx = fmaxf(mx, sc[pt][r]);
+        for (int pt = 0; pt < 4; ++pt) {
+            float4v c = {0, 0, 0, 0};
+            const _Float16 *krow = ks + (pt * 16 + lq) * kld + 8 * lg;
+#pragma unroll
+            for (int ch = 0; ch < 8; ++ch) {
+                if (ch >= nch) break;
+                const half8 a = *reinterpret_cast<const half8 *>(krow + ch * 32);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ch], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ch], c, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {   // S^T[position pt*16 + 4 lg + r][query lq]
+                const int slot = s0 + pt * 16 + 4 * lg + r;
+                const bool ok = qvalid && slot < total && (slot < pos || ((vis >> (slot - pos)) & 1u));
+                sc[pt][r] = ok ? c[r] * scale : -__builtin_inff();
+                mx = fmaxf(mx, sc[pt][r]);
+            }
         }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    float lsum = 0.0f;
-    half4 pe[4], pl[4];   // the weights as hi + lo halves
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float lsum = 0.0f;
+        half4 pe[4], pl[4];   // the weights as hi + lo halves
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt)
+        for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float e = sc[pt][r] == -__builtin_inff() ? 0.0f : expf(sc[pt][r] - mx);
-            const _Float16 eh = static_cast<_Float16>(e);
-            pe[pt][r] = eh;
-            pl[pt][r] = static_cast<_Float16>(e - static_cast<float>(eh));
-            lsum += e;
+            for (int r = 0; r < 4; ++r) {
+                const float e = sc[pt][r] == -__builtin_inff() ? 0.0f : expf(sc[pt][r] - mx);
+                _Float16 eh, el;
+                split_f16(e, eh, el);
+                pe[pt][r] = eh;
+                pl[pt][r] = el;
+                lsum += e;
+            }
+        lsum += __shfl_xor(lsum, 16, 64);
+        lsum += __shfl_xor(lsum, 32, 64);
+        // P^T operands of the two 32-position chunks: k-slot j < 4 is position 32 kc + 4 lg + j, j >= 4 is
+        // 32 kc + 16 + 4 lg + j - 4; the V^T operands take the same positions
+        half8 pb[2], pbl[2];
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pb[kc][j] = pe[2 * kc][j];
+                pb[kc][4 + j] = pe[2 * kc + 1][j];
+                pbl[kc][j] = pl[2 * kc][j];
+                pbl[kc][4 + j] = pl[2 * kc + 1][j];
+            }
+        float *dst = parts + ((static_cast<int64_t>(tq) * nh + hq) * nb_max + b) * (hd + 2);
+        for (int dt = 0; dt < hd / 16; ++dt) {
+            float4v c = {0, 0, 0, 0};
+            const _Float16 *vrow = vs + (dt * 16 + lq) * kAttnVld;
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
+                const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
+                const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[kc], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pbl[kc], c, 0, 0, 0);
+            }
+            // O^T[dim dt*16 + 4 lg + r][query lq]
+            if (qvalid) *reinterpret_cast<float4 *>(dst + dt * 16 + 4 * lg) = make_float4(c[0], c[1], c[2], c[3]);
         }
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    // P^T operands of the two 32-position chunks: k-slot j < 4 is position 32 kc + 4 lg + j, j >= 4 is
-    // 32 kc + 16 + 4 lg + j - 4; the V^T operands take the same positions
-    half8 pb[2], pbl[2];
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            pb[kc][j] = pe[2 * kc][j];
-            pb[kc][4 + j] = pe[2 * kc + 1][j];
-            pbl[kc][j] = pl[2 * kc][j];
-            pbl[kc][4 + j] = pl[2 * kc + 1][j];
+        if (qvalid && lg == 0) {
+            dst[hd] = mx;
+            dst[hd + 1] = lsum;
         }
-    float *dst = parts + ((static_cast<int64_t>(tq) * nh + hq) * nb_max + b) * (hd + 2);
-    const _Float16 *vblk = kv + v_index(slots, hd, nkv, kh, s0, 0);   // [hd][64] of this block
-    for (int dt = 0; dt < hd / 16; ++dt) {
-        float4v c = {0, 0, 0, 0};
-        const _Float16 *vrow = vblk + static_cast<int64_t>(dt * 16 + lq) * kAttnBlock;
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
-            const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
-            const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[kc], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pbl[kc], c, 0, 0, 0);
-        }
-        // O^T[dim dt*16 + 4 lg + r][query lq]
-        if (qvalid) *reinterpret_cast<float4 *>(dst + dt * 16 + 4 * lg) = make_float4(c[0], c[1], c[2], c[3]);
-    }
-    if (qvalid && lg == 0) {
-        dst[hd] = mx;
-        dst[hd + 1] = lsum;
     }
 }
 
 // The blocks joined per (row, head): exp(block max - max), the sums, 1 / sum, times sigmoid(gate)
-// (model.cpp:3830-3855). A workgroup per (row, head); the blocks' weights computed once.
+// (model.cpp:3830-3855), then the row's operands for the output projection (the int8 path, act16 layout). A
+// workgroup (4 waves) per (row, head): the blocks' weights once, then wave w adds the blocks b = w mod 4, four dims
+// a lane, and the waves' sums are added in order.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ parts, const float *__restrict__ qkv,
                                                          int64_t ldq, int nh, int hd, int nb_max,
-                                                         const StepParams *__restrict__ sp, float *__restrict__ core) {
+                                                         const StepParams *__restrict__ sp,
+                                                         _Float16 *__restrict__ act, int64_t act_stride) {
     __shared__ float fw[1024];
-    __shared__ float lsum;
+    __shared__ float red[2][4];
+    __shared__ float4 osum[4][64];
     const int t = blockIdx.x, h = blockIdx.y;
     if (t >= sp->M) return;
     const int nbw = (sp->pos + sp->M + kAttnBlock - 1) / kAttnBlock;
-    const float *base = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max) * (hd + 2);
+    const int ld = hd + 2;
+    const float *base = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max) * ld;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (wave == 0) {
-        float mx = -__builtin_inff();
-        for (int b = lane; b < nbw; b += 64) mx = fmaxf(mx, base[b * (hd + 2) + hd]);
-        mx = wave_max(mx);
-        float l = 0.0f;
-        for (int b = lane; b < nbw; b += 64) {
-            const float mb = base[b * (hd + 2) + hd];
-            const float f = mb == -__builtin_inff() ? 0.0f : expf(__fsub_rn(mb, mx));
-            fw[b] = f;
-            l = __builtin_fmaf(base[b * (hd + 2) + hd + 1], f, l);
-        }
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-        if (lane == 0) lsum = l;
-    }
+    float mx = -__builtin_inff();
+    for (int b = threadIdx.x; b < nbw; b += 256) mx = fmaxf(mx, base[b * ld + hd]);
+    mx = wave_max(mx);
+    if (lane == 0) red[0][wave] = mx;
     __syncthreads();
-    const float inv = __fdiv_rn(1.0f, lsum);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float o = 0.0f;
-        for (int b = 0; b < nbw; ++b) o = __builtin_fmaf(base[b * (hd + 2) + d], fw[b], o);
-        const float gate = qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + d];
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate)));
-        core[(static_cast<int64_t>(t) * nh + h) * hd + d] = __fmul_rn(__fmul_rn(o, inv), sig);
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float l = 0.0f;
+    for (int b = threadIdx.x; b < nbw; b += 256) {
+        const float mb = base[b * ld + hd];
+        const float f = mb == -__builtin_inff() ? 0.0f : expf(__fsub_rn(mb, mx));
+        fw[b] = f;
+        l = __builtin_fmaf(base[b * ld + hd + 1], f, l);
+    }
+    l = static_cast<float>(wave_sum(static_cast<double>(l)));
+    if (lane == 0) red[1][wave] = l;
+    __syncthreads();
+    const float inv = __fdiv_rn(1.0f, ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3]);
+    // wave w: blocks w, w + 4, ...; lane: dims 4 lane .. 4 lane + 3 (hd / 4 lanes)
+    float4 o = make_float4(0, 0, 0, 0);
+    if (lane * 4 < hd) {
+        int b = wave;
+        for (; b + 12 < nbw; b += 16) {   // four blocks' loads ahead of their sums
+            float4 v[4];
+            float f[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v[u] = *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4);
+                f[u] = fw[b + 4 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                o.x = __builtin_fmaf(v[u].x, f[u], o.x);
+                o.y = __builtin_fmaf(v[u].y, f[u], o.y);
+                o.z = __builtin_fmaf(v[u].z, f[u], o.z);
+                o.w = __builtin_fmaf(v[u].w, f[u], o.w);
+            }
+        }
+        for (; b < nbw; b += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(base + b * ld + lane * 4);
+            const float f = fw[b];
+            o.x = __builtin_fmaf(v.x, f, o.x);
+            o.y = __builtin_fmaf(v.y, f, o.y);
+            o.z = __builtin_fmaf(v.z, f, o.z);
+            o.w = __builtin_fmaf(v.w, f, o.w);
+        }
+    }
+    osum[wave][lane] = o;
+    __syncthreads();
+    // the gated output, 8 dims (one k-group of the projection's operands) a lane of wave 0
+    if (wave == 0) {
+        const int g = lane, ng = hd / 8;
+        const bool live = g < ng;
+        float v[8];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int li = live ? 2 * g + half : 0;
+            float4 s4 = osum[0][li];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) {
+                const float4 a = osum[w][li];
+                s4.x += a.x, s4.y += a.y, s4.z += a.z, s4.w += a.w;
+            }
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 8 * g + 4 * half + i;
+                const float gate = live ? qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + d] : 0.0f;
+                const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate)));
+                v[4 * half + i] = __fmul_rn(__fmul_rn(sv[i], inv), sig);
+            }
+        }
+        act16_group(v, h * ng + g, live, act + static_cast<int64_t>(t) * act_stride);
     }
 }
 
-// Router logits: bf16 rows [E + 1][H] (the shared expert's gate row last) times the post-norm rows, eight partial
-// sums per row in the reference's fixed order (bf16_row_dots, kernels.cpp:1446-1483). A wave per row, its lanes
-// 8 tokens x 8 partial sums; loads in chunks of 32 columns ahead of the sequential sums.
+// The post-attention RMSNorm and the router logits. A workgroup takes 4 rows of the router ([E + 1][H] bf16, the
+// shared expert's gate row last; one a wave) and the tokens in groups of router_tokens(H). Every load is issued
+// first (the rows, the residual rows, the norm weights); the sums of squares, 1 / RMS and x inv (1 + w) (rmsnorm's
+// arithmetic) then come from registers, workgroup b also writing token b's operands for the experts' products, and
+// the normalized rows and the router rows (as fp32) go to LDS for the sums. Each logit is eight partial sums in the
+// reference's fixed order (bf16_row_dots, kernels.cpp:1446-1483), a lane per (token, partial).
+constexpr int kRouterRows = 4;
+__host__ __device__ inline int router_tokens(int H) { return H <= 2048 ? 8 : 4; }
+inline size_t router_lds(int H) {
+    return static_cast<size_t>(router_tokens(H)) * (H + 8) * 4 + static_cast<size_t>(kRouterRows) * H * 4;
+}
+
+template <int GPT>   // 8-value groups a thread takes per row: 1 for H <= 2048, 2 up to 4096
 __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict__ w, int E1, int H,
-                                                     const float *__restrict__ h, const StepParams *__restrict__ sp,
-                                                     float *__restrict__ logits) {
+                                                     const float *__restrict__ x, const float *__restrict__ norm_w,
+                                                     float eps, const StepParams *__restrict__ sp,
+                                                     float *__restrict__ logits, _Float16 *__restrict__ act,
+                                                     int64_t act_stride) {
+    constexpr int TG = GPT == 1 ? 8 : 4;
+    extern __shared__ float lds_f[];
+    __shared__ double red[4][TG];
+    const int ldh = H + 8;
+    float *hs = lds_f;                 // [TG][ldh] the normalized rows
+    float *ws = hs + TG * ldh;         // [4][H] the router rows as fp32
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = blockIdx.x * 4 + wave;
-    if (r >= E1) return;
-    const int M = sp->M;
-    const uint16_t *row = w + static_cast<int64_t>(r) * H;
-    for (int t0 = 0; t0 < M; t0 += 8) {
-        const int t = t0 + lane / 8, j = lane % 8;
-        const bool live = t < M;
-        const float *x = h + static_cast<int64_t>(live ? t : 0) * H;
-        float acc = 0.0f;
-        for (int c0 = 0; c0 < H; c0 += 256) {
-            float wf[32], xv[32];
+    const int M = sp->M, r0 = blockIdx.x * kRouterRows;
+    // the workgroup's router rows: 4 x H bf16, 8 a load (H / 256 loads a thread)
+    uint4 wr[GPT * 4];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                wf[u] = __uint_as_float(static_cast<uint32_t>(row[c0 + u * 8 + j]) << 16);
-                xv[u] = x[c0 + u * 8 + j];
+    for (int k = 0; k < GPT * 4; ++k) {
+        const int i = threadIdx.x + k * 256, rr = i / (H / 8), c8 = i % (H / 8);
+        wr[k] = i < 4 * (H / 8) && r0 + rr < E1
+                    ? *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(r0 + rr) * H + c8 * 8)
+                    : make_uint4(0, 0, 0, 0);
+    }
+    float nw[GPT][8];
+#pragma unroll
+    for (int q = 0; q < GPT; ++q) {
+        const int g = threadIdx.x + q * 256;
+        const float4 a = g < H / 8 ? *reinterpret_cast<const float4 *>(norm_w + g * 8) : make_float4(0, 0, 0, 0);
+        const float4 b = g < H / 8 ? *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4) : make_float4(0, 0, 0, 0);
+        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);
+    }
+    bool wrote_w = false;
+    for (int t0 = 0; t0 < M; t0 += TG) {
+        const int nt = min(TG, M - t0);
+        float xv[TG][GPT][8];
+#pragma unroll
+        for (int tt = 0; tt < TG; ++tt)
+#pragma unroll
+            for (int q = 0; q < GPT; ++q) {
+                float4 a = make_float4(0, 0, 0, 0), b = a;
+                if (tt < nt && threadIdx.x + q * 256 < H / 8) {
+                    const float *src = x + static_cast<int64_t>(t0 + tt) * H + (threadIdx.x + q * 256) * 8;
+                    a = *reinterpret_cast<const float4 *>(src);
+                    b = *reinterpret_cast<const float4 *>(src + 4);
+                }
+                const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv[tt][q][i] = t[i];
+            }
+        // 1 / RMS per row: the thread's squares, the wave sums, the waves' in order
+        __syncthreads();   // the previous group's sums are done with hs and red
+#pragma unroll
+        for (int tt = 0; tt < TG; ++tt) {
+            double ss = 0.0;
+#pragma unroll
+            for (int q = 0; q < GPT; ++q)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += static_cast<double>(xv[tt][q][i]) * static_cast<double>(xv[tt][q][i]);
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave][tt] = ss;
+        }
+        if (!wrote_w) {   // the router rows to LDS as fp32
+#pragma unroll
+            for (int k = 0; k < GPT * 4; ++k) {
+                const int i = threadIdx.x + k * 256;
+                if (i >= 4 * (H / 8)) break;
+                const uint32_t u[4] = {wr[k].x, wr[k].y, wr[k].z, wr[k].w};
+                float *d = ws + (i / (H / 8)) * H + (i % (H / 8)) * 8;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    d[2 * h] = __uint_as_float(u[h] << 16);
+                    d[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
+                }
+            }
+            wrote_w = true;
+        }
+        __syncthreads();
+        const int tq = static_cast<int>(blockIdx.x) - t0;
+#pragma unroll
+        for (int tt = 0; tt < TG; ++tt) {
+            if (tt >= nt) break;
+            const double tot = ((red[0][tt] + red[1][tt]) + red[2][tt]) + red[3][tt];
+            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(H)), eps)));
+#pragma unroll
+            for (int q = 0; q < GPT; ++q) {
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(xv[tt][q][i], inv), nw[q][i]);
+                const int g = threadIdx.x + q * 256;
+                const bool live = g < H / 8;
+                if (live) {
+                    *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                }
+                if (tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(blockIdx.x) * act_stride);
+            }
+        }
+        __syncthreads();
+        const int tt = lane / 8, j = lane % 8;
+        const int ra = r0 + wave;
+        if (ra >= E1) continue;
+        const float *hr = hs + (tt < nt ? tt : 0) * ldh;
+        const float *wrow = ws + wave * H;
+        float a0 = 0.0f;
+        for (int c0 = j; c0 < H; c0 += 8 * 16) {   // 16 steps' operands read ahead of their sums
+            float hv[16], wv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                hv[u] = hr[c0 + 8 * u];
+                wv[u] = wrow[c0 + 8 * u];
             }
 #pragma unroll
-            for (int u = 0; u < 32; ++u) acc = __fadd_rn(acc, __fmul_rn(wf[u], xv[u]));
+            for (int u = 0; u < 16; ++u) a0 = __fadd_rn(a0, __fmul_rn(wv[u], hv[u]));
         }
-        const float s = __fadd_rn(acc, __shfl_down(acc, 4, 64));          // lanes j < 4: a_j + a_{j+4}
-        const float s2 = __fadd_rn(s, __shfl_down(s, 1, 64));             // j = 0: s0 + s1, j = 2: s2 + s3
-        const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));           // j = 0: (s0 + s1) + (s2 + s3)
-        if (j == 0 && live) logits[static_cast<int64_t>(t) * E1 + r] = s3;
+        // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7))
+        const float s1 = __fadd_rn(a0, __shfl_down(a0, 4, 64));
+        const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
+        const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
+        if (j == 0 && tt < nt) logits[static_cast<int64_t>(t0 + tt) * E1 + ra] = s3;
     }
 }
 
@@ -331,15 +527,19 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
         }
         __builtin_amdgcn_wave_barrier();
         float sum = 0.0f;
-        if (lane == 0) {   // index order, as the reference; four values a load
+        if (lane == 0) {   // index order, as the reference; 64 values read ahead of their sums
             int e = 0;
-            for (; e + 4 <= E; e += 4) {
-                const float4 v4 = *reinterpret_cast<const float4 *>(&p[t][e]);
-                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4.x), v4.y), v4.z), v4.w);
+            for (; e + 64 <= E; e += 64) {
+                float4 v4[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v4[u] = *reinterpret_cast<const float4 *>(&p[t][e + 4 * u]);
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4[u].x), v4[u].y), v4[u].z), v4[u].w);
             }
             for (; e < E; ++e) sum = __fadd_rn(sum, p[t][e]);
         }
-        sum = __shfl(sum, 0, 64);
+        sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
         float pv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -347,18 +547,13 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
             pv[i] = e < E ? __fdiv_rn(p[t][e], sum) : -1.0f;
         }
         float top = 0.0f, mine = 0.0f;
-        for (int k = 0; k < K; ++k) {
-            float bv = -1.0f;
+        for (int k = 0; k < K; ++k) {   // the largest left, ties to the lowest index: a wave max, then ballots
+            const float bv = wave_max(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])));
             int bi = E;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = lane + 64 * i;
-                if (pv[i] > bv || (pv[i] == bv && e < bi)) bv = pv[i], bi = e;
-            }
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
-                if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+            for (int i = 3; i >= 0; --i) {
+                const uint64_t hit = __ballot(pv[i] == bv);
+                if (hit) bi = 64 * i + __builtin_ctzll(hit);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -378,16 +573,24 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
     for (int i = threadIdx.x; i < M * K; i += blockDim.x) atomicAdd(&cnt[ids[(i / K) * 16 + i % K]], 1);
     if (threadIdx.x == 0) cnt[E] = M;
     __syncthreads();
-    if (threadIdx.x == 0) {   // exclusive scans over 257 counters: starts and slot numbers
-        int run = 0, u = 0;
-        for (int e = 0; e <= E; ++e) {
-            start[e] = run;
-            slot_of[e] = cnt[e] > 0 ? u : -1;
-            run += cnt[e];
-            u += cnt[e] > 0;
+    {   // exclusive scans over the E + 1 counters (starts, slot numbers): waves of 64, then the waves' totals
+        __shared__ int wtot[2][5];
+        const int e = threadIdx.x;
+        const int c = e <= E ? cnt[e] : 0, u = c > 0;
+        int ic = c, iu = u;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
+            if (lane >= o) ic += pc, iu += pu;
         }
-        rs->n_slots = u;
-        rs->n_picks = run;
+        if (lane == 63 && wave < 5) wtot[0][wave] = ic, wtot[1][wave] = iu;
+        __syncthreads();
+        if (e <= E) {
+            int bc = 0, bu = 0;
+            for (int w2 = 0; w2 < wave; ++w2) bc += wtot[0][w2], bu += wtot[1][w2];
+            start[e] = bc + ic - c;
+            slot_of[e] = u ? bu + iu - u : -1;
+            if (e == E) rs->n_slots = bu + iu, rs->n_picks = bc + ic;
+        }
     }
     __syncthreads();
     for (int e = threadIdx.x; e <= E; e += blockDim.x)
@@ -422,7 +625,7 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
                                                         const float *__restrict__ globals, int half_rows,
                                                         const _Float16 *__restrict__ act, int64_t act_stride,
                                                         const RouteState *__restrict__ rs, float *__restrict__ out,
-                                                        int tiles_per_wg) {
+                                                        int tiles_per_wg, int E1, int max_picks) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
     fill_e4m3_table(tab);
@@ -430,6 +633,7 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
     const int u = blockIdx.x;
     if (u >= rs->n_slots) return;
     const int e = rs->slot_expert[u], start = rs->slot_start[u], cnt = rs->slot_count[u];
+    if (e < 0 || e >= E1 || cnt < 1 || cnt > kMaxRows || start < 0 || start + cnt > max_picks) return;   // no slot
     const int64_t ntiles = tiles_rows(rows);
     const int64_t t0 = static_cast<int64_t>(blockIdx.y) * tiles_per_wg;
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
@@ -464,7 +668,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
         m[i] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), row[F + i]);
     }
     __syncthreads();
-    act16_row(m, F, act_m + static_cast<int64_t>(p) * act_halves(F), false);
+    norm_quant_row(m, F, nullptr, 0.0f, act_m + static_cast<int64_t>(p) * act_halves(F), nullptr, nullptr);
 }
 
 // x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365); a workgroup per
@@ -547,7 +751,8 @@ int launch_moe(const Model &m, const LayerW &L, int waves, hipStream_t st) {
                        UP ? L.gu_codes : L.dn_codes, UP ? L.gu_scales : L.dn_scales,
                        UP ? m.gu_code_stride : m.dn_code_stride, UP ? m.gu_scale_stride : m.dn_scale_stride, rows,
                        static_cast<int>(cols), L.expert_globals, static_cast<int>(F), UP ? m.act_h : m.act_m,
-                       act_halves(cols), m.route + (&L - &m.layers[0]), UP ? m.gu_out : m.y, per);
+                       act_halves(cols), m.route + (&L - &m.layers[0]), UP ? m.gu_out : m.y, per, m.E1,
+                       m.max_picks);
     return 0;
 }
 
@@ -619,7 +824,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
         {
             Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, 0, m.act_h, abH, nullptr, 0, st) != 0) return -1;
+            if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
         }
         {
             Tick tk(m, GV_K_QKV, st);
@@ -631,33 +836,36 @@ int run_layers(Model &m, int M, hipStream_t st) {
                                c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
                                m.slots);
         }
-        const int qtiles = (nh / nkv * M + 15) / 16;
         {
             Tick tk(m, GV_K_ATTN, st);
-            hipLaunchKernelGGL(attn_mfma_kernel, dim3(qtiles, m.kv_blocks, nkv), dim3(64), 0, st, m.q16, L.kv, m.slots, nh,
-                               nkv, hd, m.sp, m.parts, m.kv_blocks);
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel), attn_lds(hd), granted) != 0) return -1;
+            hipLaunchKernelGGL(attn_block_kernel, dim3(m.kv_blocks, nkv), dim3(256), attn_lds(hd), st, m.q16, L.kv,
+                               m.slots, nh, nkv, hd, m.sp, m.parts, m.kv_blocks);
         }
         {
             Tick tk(m, GV_K_MERGE, st);
             hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
-                               m.kv_blocks, m.sp, m.core);
-        }
-        {
-            Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.core, nh * hd, M, nh * hd, nullptr, 0.0f, 0, m.act_core, abC, nullptr, 0, st) != 0) return -1;
+                               m.kv_blocks, m.sp, m.act_core, abC);
         }
         {
             Tick tk(m, GV_K_O, st);
             if (gemv_q4(L.o, m.act_core, abC, M, gemv_out(m.x, H, L.o.global, 1), st) != 0) return -1;
         }
         {
-            Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, L.post_norm, c.eps, 0, m.act_h, abH, m.h, H, st) != 0) return -1;
-        }
-        {
             Tick tk(m, GV_K_ROUTER, st);
-            hipLaunchKernelGGL(router_kernel, dim3((m.E1 + 3) / 4), dim3(256), 0, st, L.router, m.E1, H, m.h, m.sp,
-                               m.rlogits);
+            const int wgs = std::max((m.E1 + kRouterRows - 1) / kRouterRows, M);
+            if (H <= 2048) {
+                static int granted = 0;
+                if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
+                hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
+                                   L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+            } else {
+                static int granted = 0;
+                if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
+                hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
+                                   L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+            }
         }
         {
             Tick tk(m, GV_K_ROUTE, st);
@@ -685,7 +893,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
     }
     {
             Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, 0, m.act_h, abH, nullptr, 0, st) != 0) return -1;
+            if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
         }
     {
             Tick tk(m, GV_K_LM_HEAD, st);
@@ -795,7 +1003,6 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     m.gu_scale_stride = q4_scale_bytes(2 * F, H);
     m.dn_code_stride = q4_code_bytes(H, F);
     m.dn_scale_stride = q4_scale_bytes(H, F);
-    const int64_t kv_row = nkv * hd;
     bool ok = alloc_q4(m, m.embed, V, H) && alloc_q4(m, m.lm_head, V, H);
     ok = ok && (m.final_norm = static_cast<float *>(dalloc(m, H * 4)));
     m.slots = (static_cast<int64_t>(c.max_ctx) + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
@@ -827,10 +1034,8 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     ok = ok && (m.sp = static_cast<StepParams *>(dalloc(m, sizeof(StepParams))));
     ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * c.n_layers)));
     ok = ok && (m.x = static_cast<float *>(dalloc(m, Mx * H * 4)));
-    ok = ok && (m.h = static_cast<float *>(dalloc(m, Mx * H * 4)));
     ok = ok && (m.qkv_out = static_cast<float *>(dalloc(m, Mx * qkv_rows(c) * 4)));
     ok = ok && (m.q16 = static_cast<_Float16 *>(dalloc(m, 2 * Mx * nh * hd * 2)));
-    ok = ok && (m.core = static_cast<float *>(dalloc(m, Mx * nh * hd * 4)));
     ok = ok && (m.rlogits = static_cast<float *>(dalloc(m, Mx * m.E1 * 4)));
     ok = ok && (m.parts = static_cast<float *>(dalloc(m, static_cast<size_t>(Mx) * nh * m.kv_blocks * (hd + 2) * 4)));
     ok = ok && (m.gu_out = static_cast<float *>(dalloc(m, static_cast<size_t>(m.max_picks) * 2 * F * 4)));

@@ -62,7 +62,7 @@ struct Model {
     // scratch
     StepParams *sp = nullptr;
     RouteState *route = nullptr;   // [n_layers]
-    float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *core = nullptr, *rlogits = nullptr;
+    float *x = nullptr, *qkv_out = nullptr, *rlogits = nullptr;
     _Float16 *q16 = nullptr;   // [max_rows][nh][hd]: the rotated queries
     float *parts = nullptr, *gu_out = nullptr, *y = nullptr, *logits = nullptr;
     _Float16 *act_h = nullptr, *act_core = nullptr, *act_m = nullptr;   // the products' operands (act16)

@@ -194,53 +194,23 @@ int q4_pack(const float *w, int64_t rows, int64_t cols, unsigned int *scratch_u3
     return 0;
 }
 
-// ---------------------------------------------------------------- activations
-// One workgroup per row: optional RMSNorm (kernels.cpp:1520-1529), then the products' fp16 hi + lo operands
-// (mfma_gemv.hpp) of either the int8 path's values q x (amax / 127) (quantize_activation, kernels.cpp:1254-1295,
-// bit for bit) or the exact fp32 values; optionally the normalized fp32 row too (the router's input).
+// Rows of activations into the products' operands (mfma_gemv.hpp: act16 layout, the int8 path's values), optionally
+// RMSNorm first and the normalized fp32 rows out; a workgroup per row.
 __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restrict__ x, int64_t ldx, int cols,
-                                                           const float *__restrict__ norm_w, float eps, int exact,
+                                                           const float *__restrict__ norm_w, float eps,
                                                            _Float16 *__restrict__ act, int64_t act_stride,
                                                            float *__restrict__ h_out, int64_t ldh) {
+    __shared__ double red[16][8];
     const int t = blockIdx.x;
-    const float *xr = x + t * ldx;
-    __shared__ double red[256];
-    __shared__ float inv_s;
-    float inv = 1.0f;
-    if (norm_w) {
-        double ss = 0.0;
-        for (int i = threadIdx.x; i < cols; i += 256) ss += static_cast<double>(xr[i]) * static_cast<double>(xr[i]);
-        red[threadIdx.x] = ss;
-        __syncthreads();
-        for (int o = 128; o > 0; o >>= 1) {
-            if (static_cast<int>(threadIdx.x) < o) red[threadIdx.x] += red[threadIdx.x + o];
-            __syncthreads();
-        }
-        if (threadIdx.x == 0)
-            inv_s = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(red[0] / static_cast<double>(cols)), eps)));
-        __syncthreads();
-        inv = inv_s;
-    }
-    _Float16 *ar = act + t * act_stride;
-    for (int b = threadIdx.x; b < cols / 16; b += 256) {
-        float v[16];
-        for (int i = 0; i < 16; ++i) {
-            const int c = b * 16 + i;
-            float y = xr[c];
-            if (norm_w) y = __fmul_rn(__fmul_rn(y, inv), __fadd_rn(1.0f, norm_w[c]));
-            v[i] = y;
-        }
-        if (h_out)
-            for (int i = 0; i < 16; ++i) h_out[t * ldh + b * 16 + i] = v[i];
-        act16_block(v, b, ar, exact != 0);
-    }
+    norm_quant_row(x + t * ldx, cols, norm_w, eps, act + t * act_stride, h_out ? h_out + t * ldh : nullptr, red);
 }
 
-int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, int exact,
-                 _Float16 *act, int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st) {
-    GV_REQUIRE(cols % 32 == 0 && M > 0, "quantize_act: cols must be a multiple of 32");
-    hipLaunchKernelGGL(quantize_act_kernel, dim3(M), dim3(256), 0, st, x, ldx, cols, norm_w, eps, exact, act,
-                       act_stride, h_out, ldh);
+int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, _Float16 *act,
+                 int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st) {
+    GV_REQUIRE(cols % 16 == 0 && cols <= 8192 && M > 0, "quantize_act: cols must be a multiple of 16, at most 8192");
+    GV_REQUIRE(ldx % 4 == 0 && (!h_out || ldh % 4 == 0), "quantize_act: row strides must keep 16-byte alignment");
+    hipLaunchKernelGGL(quantize_act_kernel, dim3(M), dim3(256), 0, st, x, ldx, cols, norm_w, eps, act, act_stride,
+                       h_out, ldh);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
