@@ -151,29 +151,40 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
     if (s0 >= total) return;
     const int kld = attn_k_ld(hd);
     _Float16 *ks = lds_h, *vs = lds_h + kAttnBlock * kld;
-    {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load
+    {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load, every load of
+        // the thread issued before the first store (hd / 32 <= 8 of each)
         const _Float16 *kg = kv + k_index(slots, hd, kh, s0, 0);
         const _Float16 *vg = kv + v_index(slots, hd, nkv, kh, s0, 0);
         const int kpr = hd / 8;   // loads a key row
-        for (int i = threadIdx.x; i < kAttnBlock * kpr; i += blockDim.x) {
+        const int nl = hd / 32;   // loads a thread of each
+        uint4 kr[8], vr[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (u >= nl) break;
+            const int i = threadIdx.x + u * 256;
             const int r = i / kpr, c = i % kpr;
-            const uint4 v = s0 + r < total ? *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8)
-                                           : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4 *>(ks + r * kld + c * 8) = v;
+            kr[u] = s0 + r < total ? *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8)
+                                   : make_uint4(0, 0, 0, 0);
+            vr[u] = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(i) * 8);
         }
-        for (int i = threadIdx.x; i < hd * (kAttnBlock / 8); i += blockDim.x) {
-            const int d = i / (kAttnBlock / 8), c = i % (kAttnBlock / 8);
-            uint4 v = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(d) * kAttnBlock + c * 8);
-            const int lim = total - s0 - c * 8;   // positions of this load inside the context
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (u >= nl) break;
+            const int i = threadIdx.x + u * 256;
+            const int r = i / kpr, c = i % kpr;
+            *reinterpret_cast<uint4 *>(ks + r * kld + c * 8) = kr[u];
+            const int d = i / (kAttnBlock / 8), cv = i % (kAttnBlock / 8);
+            uint4 v = vr[u];
+            const int lim = total - s0 - cv * 8;   // positions of this load inside the context
             if (lim < 8) {
-                uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                uint32_t w[4] = {v.x, v.y, v.z, v.w};
                 for (int k = 0; k < 4; ++k) {
-                    if (2 * k >= lim) u[k] = 0;
-                    else if (2 * k + 1 >= lim) u[k] &= 0xFFFFu;
+                    if (2 * k >= lim) w[k] = 0;
+                    else if (2 * k + 1 >= lim) w[k] &= 0xFFFFu;
                 }
-                v = make_uint4(u[0], u[1], u[2], u[3]);
+                v = make_uint4(w[0], w[1], w[2], w[3]);
             }
-            *reinterpret_cast<uint4 *>(vs + d * kAttnVld + c * 8) = v;
+            *reinterpret_cast<uint4 *>(vs + d * kAttnVld + cv * 8) = v;
         }
     }
     __syncthreads();
@@ -196,27 +207,31 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             ql[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
         }
         const uint32_t vis = qvalid ? sp->vis[tq] : 0u;
+        // the four 16-position tiles' scores, hi and lo products apart: eight independent MFMA chains
+        float4v ch_[4], cl_[4];
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) ch_[pt] = cl_[pt] = float4v{0, 0, 0, 0};
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) {
+            if (ch >= nch) break;
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+                const half8 a = *reinterpret_cast<const half8 *>(ks + (pt * 16 + lq) * kld + 8 * lg + ch * 32);
+                ch_[pt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ch], ch_[pt], 0, 0, 0);
+                cl_[pt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ch], cl_[pt], 0, 0, 0);
+            }
+        }
         float sc[4][4];
         float mx = -__builtin_inff();
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
-            float4v c = {0, 0, 0, 0};
-            const _Float16 *krow = ks + (pt * 16 + lq) * kld + 8 * lg;
-#pragma unroll
-            for (int ch = 0; ch < 8; ++ch) {
-                if (ch >= nch) break;
-                const half8 a = *reinterpret_cast<const half8 *>(krow + ch * 32);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ch], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ch], c, 0, 0, 0);
-            }
+        for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {   // S^T[position pt*16 + 4 lg + r][query lq]
                 const int slot = s0 + pt * 16 + 4 * lg + r;
                 const bool ok = qvalid && slot < total && (slot < pos || ((vis >> (slot - pos)) & 1u));
-                sc[pt][r] = ok ? c[r] * scale : -__builtin_inff();
+                sc[pt][r] = ok ? (ch_[pt][r] + cl_[pt][r]) * scale : -__builtin_inff();
                 mx = fmaxf(mx, sc[pt][r]);
             }
-        }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         float lsum = 0.0f;
@@ -247,19 +262,28 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
                 pbl[kc][4 + j] = pl[2 * kc + 1][j];
             }
         float *dst = parts + ((static_cast<int64_t>(tq) * nh + hq) * nb_max + b) * (hd + 2);
-        for (int dt = 0; dt < hd / 16; ++dt) {
-            float4v c = {0, 0, 0, 0};
-            const _Float16 *vrow = vs + (dt * 16 + lq) * kAttnVld;
+        for (int dt0 = 0; dt0 < hd / 16; dt0 += 4) {   // four 16-dim tiles at a time, hi and lo apart
+            float4v oh[4], ol[4];
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
-                const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
-                const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[kc], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pbl[kc], c, 0, 0, 0);
-            }
+            for (int k = 0; k < 4; ++k) oh[k] = ol[k] = float4v{0, 0, 0, 0};
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const _Float16 *vrow = vs + ((dt0 + k) * 16 + lq) * kAttnVld;
+                    const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
+                    const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
+                    const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    oh[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[kc], oh[k], 0, 0, 0);
+                    ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pbl[kc], ol[k], 0, 0, 0);
+                }
             // O^T[dim dt*16 + 4 lg + r][query lq]
-            if (qvalid) *reinterpret_cast<float4 *>(dst + dt * 16 + 4 * lg) = make_float4(c[0], c[1], c[2], c[3]);
+            if (qvalid)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4v c = oh[k] + ol[k];
+                    *reinterpret_cast<float4 *>(dst + (dt0 + k) * 16 + 4 * lg) = make_float4(c[0], c[1], c[2], c[3]);
+                }
         }
         if (qvalid && lg == 0) {
             dst[hd] = mx;
@@ -306,13 +330,30 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     float4 o = make_float4(0, 0, 0, 0);
     if (lane * 4 < hd) {
         int b = wave;
-        for (; b + 12 < nbw; b += 16) {   // four blocks' loads ahead of their sums
+        for (; b + 60 < nbw; b += 64) {   // sixteen blocks' loads ahead of their sums
+            float4 v[16];
+            float f[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                v[u] = *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4);
+                f[u] = fw[b + 4 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                o.x = __builtin_fmaf(v[u].x, f[u], o.x);
+                o.y = __builtin_fmaf(v[u].y, f[u], o.y);
+                o.z = __builtin_fmaf(v[u].z, f[u], o.z);
+                o.w = __builtin_fmaf(v[u].w, f[u], o.w);
+            }
+        }
+        for (; b < nbw; b += 16) {   // the rest, four at a time
             float4 v[4];
             float f[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                v[u] = *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4);
-                f[u] = fw[b + 4 * u];
+                const bool in = b + 4 * u < nbw;
+                v[u] = in ? *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4) : make_float4(0, 0, 0, 0);
+                f[u] = in ? fw[b + 4 * u] : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -321,14 +362,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
                 o.z = __builtin_fmaf(v[u].z, f[u], o.z);
                 o.w = __builtin_fmaf(v[u].w, f[u], o.w);
             }
-        }
-        for (; b < nbw; b += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(base + b * ld + lane * 4);
-            const float f = fw[b];
-            o.x = __builtin_fmaf(v.x, f, o.x);
-            o.y = __builtin_fmaf(v.y, f, o.y);
-            o.z = __builtin_fmaf(v.z, f, o.z);
-            o.w = __builtin_fmaf(v.w, f, o.w);
         }
     }
     osum[wave][lane] = o;
