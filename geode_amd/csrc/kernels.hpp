@@ -54,6 +54,7 @@ int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const G
 // the waves a product's K (a multiple of 128) splits over and the 32-value chunks each takes, for ntt 16-row tiles
 // of activations; 0 when one launch cannot take K (more than 8 waves)
 int mfma_split(int64_t K, int ntt, int &waves, int &kw);
+int64_t tiles_per_wg(int64_t ntiles, int waves, int ntt);
 
 // elementwise helpers (misc.hip)
 int f16_to_f32(const uint16_t *x, int64_t n, float *y, hipStream_t st);

@@ -65,27 +65,13 @@ __device__ inline void act16_group(const float (&v)[8], int g, bool live, _Float
     p[1] = lo;
 }
 
-// A row of cols (a multiple of 16, at most 32 blockDim) values into its operands, optionally RMSNorm(1 + w) first
-// (rmsnorm's arithmetic: the double sum of squares, inv = 1 / sqrt(float(ss / n) + eps), x inv (1 + w)) and the
-// normalized fp32 row to h (if not null). The whole workgroup takes the row, thread i the 8-value groups i, i +
-// blockDim, ... (up to 4), loaded once; red: LDS of 16 x 8 doubles (unused without norm_w). x may be any readable
-// memory (global or LDS), 16-byte aligned.
-__device__ inline void norm_quant_row(const float *x, int cols, const float *norm_w, float eps, _Float16 *ar, float *h,
-                                      double (*red)[8]) {
+// A row of cols (a multiple of 16, at most 32 blockDim) values, held in registers, into its operands: thread i has
+// the 8-value groups i, i + blockDim, ... (up to 4; zeros past the row), optionally RMSNorm(1 + w) first (rmsnorm's
+// arithmetic, engine/src/kernels.cpp:1520-1529: the double sum of squares, inv = 1 / sqrt(float(ss / n) + eps), x inv
+// (1 + w)) and the normalized fp32 row to h (if not null). The whole workgroup calls this; red: LDS of 16 doubles.
+__device__ inline void norm_quant_regs(float (&v)[4][8], int cols, const float *norm_w, float eps, _Float16 *ar,
+                                       float *h, double *red) {
     const int ng = cols / 8, nthr = blockDim.x;
-    float v[4][8];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int g = threadIdx.x + q * nthr;
-        float4 a = make_float4(0, 0, 0, 0), b = a;
-        if (g < ng) {
-            a = *reinterpret_cast<const float4 *>(x + g * 8);
-            b = *reinterpret_cast<const float4 *>(x + g * 8 + 4);
-        }
-        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[q][i] = t[i];
-    }
     if (norm_w) {
         float w1[4][8];
 #pragma unroll
@@ -107,10 +93,10 @@ __device__ inline void norm_quant_row(const float *x, int cols, const float *nor
             for (int i = 0; i < 8; ++i) ss += static_cast<double>(v[q][i]) * static_cast<double>(v[q][i]);
         ss = wave_sum(ss);
         __syncthreads();   // red may still be read by an earlier call
-        if (threadIdx.x % 64 == 0) red[threadIdx.x / 64][0] = ss;
+        if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = ss;
         __syncthreads();
         double tot = 0.0;
-        for (int w = 0; w < nthr / 64; ++w) tot += red[w][0];
+        for (int w = 0; w < nthr / 64; ++w) tot += red[w];
         const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(cols)), eps)));
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -128,6 +114,26 @@ __device__ inline void norm_quant_row(const float *x, int cols, const float *nor
         }
         act16_group(v[q], g, live, ar);
     }
+}
+
+// norm_quant_regs of a row in memory (global or LDS, 16-byte aligned), loaded once
+__device__ inline void norm_quant_row(const float *x, int cols, const float *norm_w, float eps, _Float16 *ar, float *h,
+                                      double *red) {
+    const int ng = cols / 8;
+    float v[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * blockDim.x;
+        float4 a = make_float4(0, 0, 0, 0), b = a;
+        if (g < ng) {
+            a = *reinterpret_cast<const float4 *>(x + g * 8);
+            b = *reinterpret_cast<const float4 *>(x + g * 8 + 4);
+        }
+        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[q][i] = t[i];
+    }
+    norm_quant_regs(v, cols, norm_w, eps, ar, h, red);
 }
 
 // Where a code word's nibbles sit. decode8 makes the A operand's pairs (v_i, v_i+4), i = 0..3, from 4 views of the
@@ -189,35 +195,17 @@ __device__ inline h8 decode8(uint32_t w, uint2 sc, uint32_t magic) {
 }
 
 // One workgroup's share of a product: its waves split the K range [sc0, sc0 + waves KW / 4) super-chunks (wave w:
-// chunks [w KW, (w + 1) KW) of it) of row tiles [t0, t1), a tile at a time with the next one's loads in flight;
-// nsc = super-chunks a row. act(j) gives local row j's activation row (act16 layout, whole row) or nullptr, put(row,
+// chunks [w KW, (w + 1) KW) of it) of row tiles [t0, t1), a tile at a time with the next two tiles' loads in flight;
+// nsc = super-chunks a row. act(j) gives local row j's activation row (act16 layout, whole row; any j < M), put(row,
 // j, v) takes the fp32 sum (before global). part: LDS of (t1 - t0) * waves * NTT KB for the waves' partial sums,
-// added once at the end (waves > 1); tab: fill_e4m3_table's.
+// added once at the end (waves > 1); tab: LDS for fill_e4m3_table, filled here (every thread of the workgroup calls
+// this) while the first loads are in flight.
 template <int KW, int NTT, typename ActFn, typename PutFn>
 __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, int64_t rows,
                                   int nsc, int sc0, int64_t t0, int64_t t1, int M, ActFn act, PutFn put, f4 *part,
-                                  const uint2 *tab) {
+                                  uint2 *tab) {
     const int W = blockDim.x / 64;
     const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
-    // the activations of this wave's K range, resident for all the tiles
-    h8 bh[KW][NTT], bl[KW][NTT];
-#pragma unroll
-    for (int tt = 0; tt < NTT; ++tt) {
-        const int j = tt * 16 + lq;
-        const _Float16 *ar = j < M ? act(j) : nullptr;
-#pragma unroll
-        for (int c = 0; c < KW; ++c) {
-            const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (ar) {
-                const _Float16 *p = ar + ((static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg) * 16;
-                bh[c][tt] = *reinterpret_cast<const h8 *>(p);
-                bl[c][tt] = *reinterpret_cast<const h8 *>(p + 8);
-            } else {
-                bh[c][tt] = z;
-                bl[c][tt] = z;
-            }
-        }
-    }
     constexpr int NS = KW / 4;   // super-chunks a wave takes
     const uint32_t magic = 0x64006400u;
     const int nt = static_cast<int>(t1 - t0);
@@ -232,6 +220,31 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             sw[s] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(sbase + (i * tstride + s) * 128));
         }
     };
+    // the first two tiles' weights (HBM, the longest wait) first
+    uint4 ca[NS], cb[NS], cc[NS];
+    uint32_t sa[NS], sb[NS], sc[NS];
+    load(0, ca, sa);
+    if (nt > 1) load(1, cb, sb);
+    // the activations of this wave's K range, resident for all the tiles (rows past M: row M - 1's, then zeros)
+    h8 bh[KW][NTT], bl[KW][NTT];
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) {
+        const int j = tt * 16 + lq;
+        const _Float16 *ar = act(j < M ? j : M - 1);
+#pragma unroll
+        for (int c = 0; c < KW; ++c) {
+            const _Float16 *p = ar + ((static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg) * 16;
+            bh[c][tt] = *reinterpret_cast<const h8 *>(p);
+            bl[c][tt] = *reinterpret_cast<const h8 *>(p + 8);
+        }
+    }
+    fill_e4m3_table(tab);
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt)
+        if (tt * 16 + lq >= M)
+#pragma unroll
+            for (int c = 0; c < KW; ++c) bh[c][tt] = bl[c][tt] = h8{0, 0, 0, 0, 0, 0, 0, 0};
     auto tile = [&](int i, const uint4 (&cw)[NS], const uint32_t (&sw)[NS]) {
         f4 acc[NTT], acl[NTT];   // the hi and lo products apart: two independent MFMA chains
 #pragma unroll
@@ -267,15 +280,16 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             }
         }
     };
-    uint4 ca[NS], cb[NS];
-    uint32_t sa[NS], sb[NS];
-    load(0, ca, sa);
-    for (int i = 0; i < nt; i += 2) {
-        if (i + 1 < nt) load(i + 1, cb, sb);
+    // a ring of three tiles' loads: two in flight while one is computed
+    for (int i = 0; i < nt; i += 3) {
+        if (i + 2 < nt) load(i + 2, cc, sc);
         tile(i, ca, sa);
         if (i + 1 >= nt) break;
-        if (i + 2 < nt) load(i + 2, ca, sa);
+        if (i + 3 < nt) load(i + 3, ca, sa);
         tile(i + 1, cb, sb);
+        if (i + 2 >= nt) break;
+        if (i + 4 < nt) load(i + 4, cb, sb);
+        tile(i + 2, cc, sc);
     }
     // the waves' partial sums added in wave order, each output by one thread
     if (W > 1) {

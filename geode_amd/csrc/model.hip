@@ -24,31 +24,34 @@ hipStream_t stream();
 int ensure_init();
 
 // ---------------------------------------------------------------- kernels
-// the rows' embeddings: dequant_row of the embedding matrix (pack.cpp:356-366), bit for bit
-__global__ void embed_kernel(Q4 w, const StepParams *__restrict__ sp, float *__restrict__ x) {
+// the rows' embeddings: dequant_row of the embedding matrix (pack.cpp:356-366), bit for bit, to x; then the first
+// layer's input RMSNorm and its operands (norm_quant_regs). A workgroup (256 threads) per row.
+__global__ __launch_bounds__(256) void embed_kernel(Q4 w, const StepParams *__restrict__ sp, float *__restrict__ x,
+                                                    const float *__restrict__ norm_w, float eps,
+                                                    _Float16 *__restrict__ act, int64_t act_stride) {
+    __shared__ double red[16];
     const int t = blockIdx.x;
     if (t >= sp->M) return;
     const int64_t r = sp->tokens[t];
-    for (int64_t wi = threadIdx.x; wi < w.cols / 8; wi += blockDim.x) {   // the row's code words (tile layout)
+    const int ng = static_cast<int>(w.cols / 8);
+    float v[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * blockDim.x;   // the row's code word g (tile layout)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) v[q][b] = 0.0f;
+        if (g >= ng) continue;
         uint32_t word, sb;
-        tq4_word(w, r, wi, word, sb);
+        tq4_word(w, r, g, word, sb);
         const float s = __fmul_rn(e4m3_to_f32(sb), w.global);
-        float *o = x + static_cast<int64_t>(t) * w.cols + wi * 8;
+#pragma unroll
         for (int b = 0; b < 8; ++b)
-            o[b] = __fmul_rn(static_cast<float>(2 * static_cast<int>((word >> (4 * b)) & 15u) - 15), s);
+            v[q][b] = __fmul_rn(static_cast<float>(2 * static_cast<int>((word >> (4 * b)) & 15u) - 15), s);
+        float *o = x + static_cast<int64_t>(t) * w.cols + g * 8;
+        *reinterpret_cast<float4 *>(o) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+        *reinterpret_cast<float4 *>(o + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
     }
-}
-
-__device__ inline double block_sum_double(double v, double *red) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-        if (static_cast<int>(threadIdx.x) < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const double r = red[0];
-    __syncthreads();
-    return r;
+    norm_quant_regs(v, ng * 8, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
 }
 
 // The device KV cache of one layer: K [nkv][slots][hd] and V [nkv][slots / 64][hd][64] in fp16 (V transposed in
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
                                                       _Float16 *__restrict__ kv, int64_t slots) {
     const int t = blockIdx.x, head = blockIdx.y, i = threadIdx.x;
     if (t >= sp->M) return;
-    __shared__ double red[256];
+    __shared__ double red[4];
     __shared__ float v[256];
     const int64_t kv_row = static_cast<int64_t>(nkv) * hd;
     const int slot = sp->pos + t;
@@ -99,7 +102,10 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
         if (i < hd) kv[v_index(slots, hd, nkv, kh, slot, i)] = static_cast<_Float16>(xv);
         return;
     }
-    const double ss = block_sum_double(static_cast<double>(xv) * static_cast<double>(xv), red);
+    double ss = wave_sum(static_cast<double>(xv) * static_cast<double>(xv));
+    if (i % 64 == 0) red[i / 64] = ss;
+    __syncthreads();
+    ss = ((red[0] + red[1]) + red[2]) + red[3];
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(ss / static_cast<double>(hd)), eps)));
     if (i < hd) v[i] = __fmul_rn(__fmul_rn(xv, inv), __fadd_rn(1.0f, nw[i]));
     __syncthreads();
@@ -661,8 +667,6 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
                                                         int tiles_per_wg, int E1, int max_picks) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
-    fill_e4m3_table(tab);
-    __syncthreads();
     const int u = blockIdx.x;
     if (u >= rs->n_slots) return;
     const int e = rs->slot_expert[u], start = rs->slot_start[u], cnt = rs->slot_count[u];
@@ -708,17 +712,47 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
 // (row, 256 columns)
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K,
                                                       const RouteState *__restrict__ rs,
-                                                      const StepParams *__restrict__ sp, float *__restrict__ x) {
-    const int t = blockIdx.x, i = blockIdx.y * blockDim.x + threadIdx.x;
-    if (t >= sp->M || i >= H) return;
+                                                      const StepParams *__restrict__ sp, float *__restrict__ x,
+                                                      const float *__restrict__ norm_w, float eps,
+                                                      _Float16 *__restrict__ act, int64_t act_stride) {
+    __shared__ double red[16];
+    const int t = blockIdx.x;
+    if (t >= sp->M) return;
+    const int ng = H / 8;
     const float gs = rs->gate[t];
-    float o = __fmul_rn(gs, y[static_cast<int64_t>(rs->pick_of[t * (K + 1) + K]) * H + i]);
-    for (int k = 0; k < K; ++k) {
-        const float wk = rs->weight[t * K + k];
-        if (wk == 0.0f) continue;
-        o = __fadd_rn(o, __fmul_rn(wk, y[static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + i]));
+    const float *ysh = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + K]) * H;
+    float v[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * blockDim.x;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[q][i] = 0.0f;
+        if (g >= ng) continue;
+        float o[8];
+        {
+            const float4 a = *reinterpret_cast<const float4 *>(ysh + g * 8), b = *reinterpret_cast<const float4 *>(ysh + g * 8 + 4);
+            const float yv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = __fmul_rn(gs, yv[i]);
+        }
+        for (int k = 0; k < K; ++k) {   // rank order
+            const float wk = rs->weight[t * K + k];
+            if (wk == 0.0f) continue;
+            const float *yk = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + g * 8;
+            const float4 a = *reinterpret_cast<const float4 *>(yk), b = *reinterpret_cast<const float4 *>(yk + 4);
+            const float yv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(o[i], __fmul_rn(wk, yv[i]));
+        }
+        float *xr = x + static_cast<int64_t>(t) * H + g * 8;
+        const float4 a = *reinterpret_cast<const float4 *>(xr), b = *reinterpret_cast<const float4 *>(xr + 4);
+        const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[q][i] = __fadd_rn(xv[i], o[i]);
+        *reinterpret_cast<float4 *>(xr) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+        *reinterpret_cast<float4 *>(xr + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
     }
-    x[static_cast<int64_t>(t) * H + i] = __fadd_rn(x[static_cast<int64_t>(t) * H + i], o);
+    norm_quant_regs(v, H, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
 }
 
 // verify_keep of a tree: the kept path's keys and values moved to the kept slots in every layer; a thread per
@@ -767,20 +801,23 @@ __global__ void f32_to_f16_kernel(const float *__restrict__ x, int64_t n, uint16
 // ---------------------------------------------------------------- launches
 namespace {
 
+// the slots a step of M rows can have: its distinct experts (at most M K) and the shared one
+inline int moe_slots(const Model &m, int M) { return std::min(m.max_slots, std::min(m.c.n_experts, M * m.c.top_k) + 1); }
+
 template <int KW, int NTT, int WMAX, bool UP>
-int launch_moe(const Model &m, const LayerW &L, int waves, hipStream_t st) {
+int launch_moe(const Model &m, const LayerW &L, int M, int waves, hipStream_t st) {
     const int64_t H = m.c.hidden, F = m.c.moe_ff;
     const int64_t rows = UP ? 2 * F : H, cols = UP ? H : F;
     const int64_t ntiles = tiles_rows(rows);
-    // ~8 workgroups a slot, the waves' partial sums within 48 KB of LDS
-    const int64_t cap = waves > 1 ? std::max(1, 48 / (waves * NTT)) : 64;
-    const int per = static_cast<int>(std::min<int64_t>(cap, (ntiles + 7) / 8));
+    const int slots = moe_slots(m, M);
+    // the slots' tiles over about as many workgroups as the chip holds at once
+    const int per = static_cast<int>(tiles_per_wg(ntiles * slots, waves, NTT));
     const int tiles = static_cast<int>((ntiles + per - 1) / per);
     const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 64 * 1024, granted) != 0)
+    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 76 * 1024, granted) != 0)
         return -1;
-    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(m.max_slots, tiles), dim3(64 * waves), lds, st,
+    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(slots, tiles), dim3(64 * waves), lds, st,
                        UP ? L.gu_codes : L.dn_codes, UP ? L.gu_scales : L.dn_scales,
                        UP ? m.gu_code_stride : m.dn_code_stride, UP ? m.gu_scale_stride : m.dn_scale_stride, rows,
                        static_cast<int>(cols), L.expert_globals, static_cast<int>(F), UP ? m.act_h : m.act_m,
@@ -790,21 +827,21 @@ int launch_moe(const Model &m, const LayerW &L, int waves, hipStream_t st) {
 }
 
 template <bool UP>
-int moe_launch(const Model &m, const LayerW &L, int ntt, int kw, int waves, hipStream_t st) {
+int moe_launch(const Model &m, const LayerW &L, int M, int ntt, int kw, int waves, hipStream_t st) {
     if (ntt == 1) {
-        if (kw == 16) return launch_moe<16, 1, 8, UP>(m, L, waves, st);
-        if (kw == 8) return launch_moe<8, 1, 8, UP>(m, L, waves, st);
-        return launch_moe<4, 1, 8, UP>(m, L, waves, st);
+        if (kw == 16) return launch_moe<16, 1, 8, UP>(m, L, M, waves, st);
+        if (kw == 8) return launch_moe<8, 1, 8, UP>(m, L, M, waves, st);
+        return launch_moe<4, 1, 8, UP>(m, L, M, waves, st);
     }
-    if (kw == 8) return launch_moe<8, 2, 8, UP>(m, L, waves, st);
-    return launch_moe<4, 2, 8, UP>(m, L, waves, st);
+    if (kw == 8) return launch_moe<8, 2, 8, UP>(m, L, M, waves, st);
+    return launch_moe<4, 2, 8, UP>(m, L, M, waves, st);
 }
 
 int moe_products(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
     const int ntt = M <= 16 ? 1 : 2;
     int waves, kw;
     GV_REQUIRE(mfma_split(up ? m.c.hidden : m.c.moe_ff, ntt, waves, kw), "moe: K too wide for one launch");
-    return up ? moe_launch<true>(m, L, ntt, kw, waves, st) : moe_launch<false>(m, L, ntt, kw, waves, st);
+    return up ? moe_launch<true>(m, L, M, ntt, kw, waves, st) : moe_launch<false>(m, L, M, ntt, kw, waves, st);
 }
 
 GemvOut qkv_out(const Model &m, const LayerW &L) {
@@ -851,14 +888,11 @@ int run_layers(Model &m, int M, hipStream_t st) {
     const int64_t abH = act_halves(H), abC = act_halves(static_cast<int64_t>(nh) * hd);
     {
         Tick tk(m, GV_K_EMBED, st);
-        hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x);
+        hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x, m.layers[0].in_norm, c.eps,
+                           m.act_h, abH);
     }
     for (int l = 0; l < c.n_layers; ++l) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
-        {
-            Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, L.in_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
-        }
         {
             Tick tk(m, GV_K_QKV, st);
             if (gemv_q4(L.qkv, m.act_h, abH, M, qkv_out(m, L), st) != 0) return -1;
@@ -911,7 +945,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
         }
         {
             Tick tk(m, GV_K_SWIGLU, st);
-            hipLaunchKernelGGL(swiglu_quant_kernel, dim3(m.max_picks), dim3(256), static_cast<size_t>(c.moe_ff) * 4, st,
+            hipLaunchKernelGGL(swiglu_quant_kernel, dim3(M * (c.top_k + 1)), dim3(256), static_cast<size_t>(c.moe_ff) * 4, st,
                                m.gu_out, c.moe_ff, m.route + l, m.act_m);
         }
         {
@@ -920,18 +954,16 @@ int run_layers(Model &m, int M, hipStream_t st) {
         }
         {
             Tick tk(m, GV_K_COMBINE, st);
-            hipLaunchKernelGGL(combine_kernel, dim3(M, (H + 255) / 256), dim3(256), 0, st, m.y, H, c.top_k, m.route + l,
-                               m.sp, m.x);
+            // the residual add, then the next layer's input RMSNorm (the final norm after the last) and its operands
+            const float *next_norm = l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm : m.final_norm;
+            hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, m.route + l, m.sp, m.x,
+                               next_norm, c.eps, m.act_h, abH);
         }
     }
     {
-            Tick tk(m, GV_K_QUANT, st);
-            if (quantize_act(m.x, H, M, H, m.final_norm, c.eps, m.act_h, abH, nullptr, 0, st) != 0) return -1;
-        }
-    {
-            Tick tk(m, GV_K_LM_HEAD, st);
-            if (gemv_q4(m.lm_head, m.act_h, abH, M, gemv_out(m.logits, c.vocab, m.lm_head.global), st) != 0) return -1;
-        }
+        Tick tk(m, GV_K_LM_HEAD, st);
+        if (gemv_q4(m.lm_head, m.act_h, abH, M, gemv_out(m.logits, c.vocab, m.lm_head.global), st) != 0) return -1;
+    }
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }

@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
                                                            const float *__restrict__ norm_w, float eps,
                                                            _Float16 *__restrict__ act, int64_t act_stride,
                                                            float *__restrict__ h_out, int64_t ldh) {
-    __shared__ double red[16][8];
+    __shared__ double red[16];
     const int t = blockIdx.x;
     norm_quant_row(x + t * ldx, cols, norm_w, eps, act + t * act_stride, h_out ? h_out + t * ldh : nullptr, red);
 }
@@ -223,8 +223,6 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
                                                             GemvOut out) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
-    fill_e4m3_table(tab);
-    __syncthreads();
     const int64_t ntiles = tiles_rows(w.rows);
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
@@ -243,10 +241,12 @@ int mfma_split(int64_t K, int ntt, int &waves, int &kw) {
     return K % kSuperK == 0 && waves >= 1 && waves <= 8;
 }
 
-// tiles a workgroup: ~1024 workgroups when the matrix has the tiles, the waves' partial sums within 48 KB of LDS
-inline int64_t tiles_per_wg(int64_t ntiles, int waves, int ntt) {
-    const int64_t cap = waves > 1 ? std::max(1, 48 / (waves * ntt)) : 64;
-    return std::min<int64_t>(cap, std::max<int64_t>(1, (ntiles + 1023) / 1024));
+// tiles a workgroup: about as many workgroups as the chip holds at once (2 waves a SIMD at these kernels' register
+// use: 512 / waves workgroups), the waves' partial sums within 76 KB of LDS (two workgroups a CU)
+int64_t tiles_per_wg(int64_t ntiles, int waves, int ntt) {
+    const int64_t resident = 256 * std::max(1, 8 / waves);
+    const int64_t cap = waves > 1 ? std::max(1, 76 / (waves * ntt)) : 64;
+    return std::min<int64_t>(cap, std::max<int64_t>(1, (ntiles + resident - 1) / resident));
 }
 
 template <int KW, int NTT, int WMAX>
@@ -257,7 +257,7 @@ static int launch_gemv(const Q4 &w, const _Float16 *act, int64_t act_stride, int
     const int64_t wg = (ntiles + per - 1) / per;
     const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX>), 64 * 1024, granted) != 0) return -1;
+    if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX>), 76 * 1024, granted) != 0) return -1;
     hipLaunchKernelGGL((gemv_q4_kernel<KW, NTT, WMAX>), dim3(static_cast<unsigned>(wg)), dim3(64 * waves), lds, st, w,
                        act, act_stride, M, sc0, static_cast<int>(per), out);
     return 0;
