@@ -70,6 +70,7 @@ SIGNATURES = {
     "gv_model_route_ids": (_c.c_int, [_P, _P]),
     "gv_model_time_kernel": (_c.c_int, [_P, _c.c_int]),
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
+    "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
 }
 
 # kernel classes of a verify step (gv_model_time_kernel)
@@ -266,6 +267,12 @@ class VerifyModel:
         ms, n = _c.c_float(0), _c.c_int(0)
         check(_lib().gv_model_kernel_time(self.h, _c.byref(ms), _c.byref(n)), "gv_model_kernel_time")
         return ms.value, n.value
+
+    def replay(self, cls, layer=0, reps=20):
+        """mean ms of kernel class cls of one layer, launched reps times back to back on the last verify's state"""
+        ms = _c.c_float(0)
+        check(_lib().gv_model_replay(self.h, cls, layer, reps, _c.byref(ms)), "gv_model_replay")
+        return ms.value
 
     def route_ids(self, n):
         out = np.empty((self.cfg["n_layers"], n, self.cfg["top_k"]), np.int32)

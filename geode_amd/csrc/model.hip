@@ -735,14 +735,26 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = __fmul_rn(gs, yv[i]);
         }
-        for (int k = 0; k < K; ++k) {   // rank order
-            const float wk = rs->weight[t * K + k];
-            if (wk == 0.0f) continue;
-            const float *yk = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + g * 8;
-            const float4 a = *reinterpret_cast<const float4 *>(yk), b = *reinterpret_cast<const float4 *>(yk + 4);
-            const float yv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        for (int k0 = 0; k0 < K; k0 += 8) {   // rank order; eight picks' loads ahead of their sums
+            float4 ya[8], yb[8];
+            float wk[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(o[i], __fmul_rn(wk, yv[i]));
+            for (int u = 0; u < 8; ++u) {
+                const int k = k0 + u;
+                wk[u] = k < K ? rs->weight[t * K + k] : 0.0f;
+                if (k < K) {
+                    const float *yk = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + g * 8;
+                    ya[u] = *reinterpret_cast<const float4 *>(yk);
+                    yb[u] = *reinterpret_cast<const float4 *>(yk + 4);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (k0 + u >= K || wk[u] == 0.0f) continue;
+                const float yv[8] = {ya[u].x, ya[u].y, ya[u].z, ya[u].w, yb[u].x, yb[u].y, yb[u].z, yb[u].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(o[i], __fmul_rn(wk[u], yv[i]));
+            }
         }
         float *xr = x + static_cast<int64_t>(t) * H + g * 8;
         const float4 a = *reinterpret_cast<const float4 *>(xr), b = *reinterpret_cast<const float4 *>(xr + 4);
@@ -882,88 +894,87 @@ struct Tick {
     }
 };
 
-int run_layers(Model &m, int M, hipStream_t st) {
+// One kernel class of layer l (the embedding and lm_head: l ignored) for M rows; the verify step is these in order.
+int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     const auto &c = m.c;
     const int H = c.hidden, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     const int64_t abH = act_halves(H), abC = act_halves(static_cast<int64_t>(nh) * hd);
-    {
-        Tick tk(m, GV_K_EMBED, st);
+    LayerW &L = m.layers[static_cast<size_t>(l)];
+    Tick tk(m, cls, st);
+    switch (cls) {
+    case GV_K_EMBED:
         hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x, m.layers[0].in_norm, c.eps,
                            m.act_h, abH);
+        return 0;
+    case GV_K_QKV:
+        return gemv_q4(L.qkv, m.act_h, abH, M, qkv_out(m, L), st);
+    case GV_K_ROPE:
+        hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
+                           c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
+                           m.slots);
+        return 0;
+    case GV_K_ATTN: {
+        static int granted = 0;
+        if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel), attn_lds(hd), granted) != 0) return -1;
+        hipLaunchKernelGGL(attn_block_kernel, dim3(m.kv_blocks, nkv), dim3(256), attn_lds(hd), st, m.q16, L.kv,
+                           m.slots, nh, nkv, hd, m.sp, m.parts, m.kv_blocks);
+        return 0;
     }
-    for (int l = 0; l < c.n_layers; ++l) {
-        LayerW &L = m.layers[static_cast<size_t>(l)];
-        {
-            Tick tk(m, GV_K_QKV, st);
-            if (gemv_q4(L.qkv, m.act_h, abH, M, qkv_out(m, L), st) != 0) return -1;
-        }
-        {
-            Tick tk(m, GV_K_ROPE, st);
-            hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
-                               c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
-                               m.slots);
-        }
-        {
-            Tick tk(m, GV_K_ATTN, st);
+    case GV_K_MERGE:
+        hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
+                           m.kv_blocks, m.sp, m.act_core, abC);
+        return 0;
+    case GV_K_O:   // the residual add is the product's accumulate
+        return gemv_q4(L.o, m.act_core, abC, M, gemv_out(m.x, H, L.o.global, 1), st);
+    case GV_K_ROUTER: {
+        const int wgs = std::max((m.E1 + kRouterRows - 1) / kRouterRows, M);
+        if (H <= 2048) {
             static int granted = 0;
-            if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel), attn_lds(hd), granted) != 0) return -1;
-            hipLaunchKernelGGL(attn_block_kernel, dim3(m.kv_blocks, nkv), dim3(256), attn_lds(hd), st, m.q16, L.kv,
-                               m.slots, nh, nkv, hd, m.sp, m.parts, m.kv_blocks);
+            if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
+            hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
+                               L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+        } else {
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
+            hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
+                               L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
         }
-        {
-            Tick tk(m, GV_K_MERGE, st);
-            hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
-                               m.kv_blocks, m.sp, m.act_core, abC);
-        }
-        {
-            Tick tk(m, GV_K_O, st);
-            if (gemv_q4(L.o, m.act_core, abC, M, gemv_out(m.x, H, L.o.global, 1), st) != 0) return -1;
-        }
-        {
-            Tick tk(m, GV_K_ROUTER, st);
-            const int wgs = std::max((m.E1 + kRouterRows - 1) / kRouterRows, M);
-            if (H <= 2048) {
-                static int granted = 0;
-                if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
-                hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
-                                   L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
-            } else {
-                static int granted = 0;
-                if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
-                hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
-                                   L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
-            }
-        }
-        {
-            Tick tk(m, GV_K_ROUTE, st);
-            hipLaunchKernelGGL(route_kernel, dim3(1), dim3(1024), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
-                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
-        }
-        {
-            Tick tk(m, GV_K_MOE_UP, st);
-            if (moe_products(m, L, M, true, st) != 0) return -1;
-        }
-        {
-            Tick tk(m, GV_K_SWIGLU, st);
-            hipLaunchKernelGGL(swiglu_quant_kernel, dim3(M * (c.top_k + 1)), dim3(256), static_cast<size_t>(c.moe_ff) * 4, st,
-                               m.gu_out, c.moe_ff, m.route + l, m.act_m);
-        }
-        {
-            Tick tk(m, GV_K_MOE_DOWN, st);
-            if (moe_products(m, L, M, false, st) != 0) return -1;
-        }
-        {
-            Tick tk(m, GV_K_COMBINE, st);
-            // the residual add, then the next layer's input RMSNorm (the final norm after the last) and its operands
-            const float *next_norm = l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm : m.final_norm;
-            hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, m.route + l, m.sp, m.x,
-                               next_norm, c.eps, m.act_h, abH);
-        }
+        return 0;
     }
-    {
-        Tick tk(m, GV_K_LM_HEAD, st);
-        if (gemv_q4(m.lm_head, m.act_h, abH, M, gemv_out(m.logits, c.vocab, m.lm_head.global), st) != 0) return -1;
+    case GV_K_ROUTE:
+        hipLaunchKernelGGL(route_kernel, dim3(1), dim3(1024), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
+                           m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
+        return 0;
+    case GV_K_MOE_UP:
+        return moe_products(m, L, M, true, st);
+    case GV_K_SWIGLU:
+        hipLaunchKernelGGL(swiglu_quant_kernel, dim3(M * (c.top_k + 1)), dim3(256), static_cast<size_t>(c.moe_ff) * 4,
+                           st, m.gu_out, c.moe_ff, m.route + l, m.act_m);
+        return 0;
+    case GV_K_MOE_DOWN:
+        return moe_products(m, L, M, false, st);
+    case GV_K_COMBINE: {   // the residual add, then the next layer's input RMSNorm (after the last: the final norm)
+        const float *next_norm = l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm : m.final_norm;
+        hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, m.route + l, m.sp, m.x,
+                           next_norm, c.eps, m.act_h, abH);
+        return 0;
     }
+    case GV_K_LM_HEAD:
+        return gemv_q4(m.lm_head, m.act_h, abH, M, gemv_out(m.logits, c.vocab, m.lm_head.global), st);
+    default:
+        return 0;
+    }
+}
+
+constexpr int kLayerClasses[] = {GV_K_QKV,    GV_K_ROPE,   GV_K_ATTN,   GV_K_MERGE,     GV_K_O,      GV_K_ROUTER,
+                                 GV_K_ROUTE,  GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN, GV_K_COMBINE};
+
+int run_layers(Model &m, int M, hipStream_t st) {
+    if (launch_class(m, GV_K_EMBED, 0, M, st) != 0) return -1;
+    for (int l = 0; l < m.c.n_layers; ++l)
+        for (int cls : kLayerClasses)
+            if (launch_class(m, cls, l, M, st) != 0) return -1;
+    if (launch_class(m, GV_K_LM_HEAD, 0, M, st) != 0) return -1;
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -1416,6 +1427,37 @@ int gv_model_time_kernel(gv_model *g, int cls) {
     GV_CHECK_HIP(hipStreamSynchronize(stream()));
     g->m.timed_class = cls;
     g->m.events_used = 0;
+    return 0;
+}
+
+int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_launch) {
+    GV_REQUIRE(g && ms_per_launch && cls >= 0 && cls < GV_K_COUNT && cls != GV_K_QUANT && reps >= 1,
+               "gv_model_replay: bad arguments");
+    Model &m = g->m;
+    GV_REQUIRE(layer >= 0 && layer < m.c.n_layers, "gv_model_replay: no such layer");
+    GV_REQUIRE(m.last_n > 0, "gv_model_replay: no verify yet");
+    const hipStream_t st = stream();
+    const int saved = m.timed_class;
+    m.timed_class = -1;
+    // the step's row count and position as the last verify left them
+    m.host_sp.pos = m.last_pos;
+    GV_CHECK_HIP(hipMemcpyAsync(m.sp, &m.host_sp, sizeof(StepParams), hipMemcpyHostToDevice, st));
+    if (launch_class(m, cls, layer, m.last_n, st) != 0) return -1;   // warm
+    hipEvent_t e0, e1;
+    GV_CHECK_HIP(hipEventCreate(&e0));
+    GV_CHECK_HIP(hipEventCreate(&e1));
+    GV_CHECK_HIP(hipEventRecord(e0, st));
+    int rc = 0;
+    for (int i = 0; i < reps && rc == 0; ++i) rc = launch_class(m, cls, layer, m.last_n, st);
+    GV_CHECK_HIP(hipEventRecord(e1, st));
+    GV_CHECK_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    GV_CHECK_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    m.timed_class = saved;
+    if (rc != 0) return -1;
+    *ms_per_launch = ms / reps;
     return 0;
 }
 

@@ -158,6 +158,11 @@ enum {
  * the reference's per-kernel timing is GEODE_GPU8_PROF, engine/src/gpu8.cpp:195). */
 int gv_model_time_kernel(gv_model *m, int cls);
 int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
+/* Launch kernel class cls of layer `layer` (ignored for GV_K_EMBED / GV_K_LM_HEAD) reps times back to back on the
+ * last verify's rows and return the mean milliseconds a launch; a measurement aid with no reference counterpart.
+ * The kernels run on the state the last verify left; classes that accumulate (GV_K_O, GV_K_COMBINE) change it, so
+ * verify again before trusting the model's state. */
+int gv_model_replay(gv_model *m, int cls, int layer, int reps, float *ms_per_launch);
 
 #ifdef __cplusplus
 }
