@@ -71,6 +71,12 @@ SIGNATURES = {
     "gv_model_time_kernel": (_c.c_int, [_P, _c.c_int]),
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
+    "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
+                                  _P, _P]),
+    "gv_accept_match": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
+                                   _c.c_int, _P, _P, _P]),
+    "gv_accept_textbook": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
+                                      _P, _P, _c.c_float, _P]),
 }
 
 # kernel classes of a verify step (gv_model_time_kernel)
@@ -203,6 +209,54 @@ def gemv(w: Q4Matrix, x: np.ndarray, accumulate_into=None):
         y.upload(np.ascontiguousarray(accumulate_into, np.float32))
     check(_lib().gv_gemv_q4(w.ref(), act.ptr, M, y.ptr, w.rows, int(accumulate_into is not None)), "gv_gemv_q4")
     return y.download(np.float32, (M, w.rows))
+
+
+def _dev_rows(x):
+    """(device buffer or pointer, ld) of a float32 [rows][V] array (uploaded) or an existing device pointer"""
+    if isinstance(x, np.ndarray):
+        x = np.ascontiguousarray(x, np.float32)
+        buf = DeviceBuffer.from_array(x)
+        return buf, buf.ptr, x.shape[-1]
+    raise TypeError("expected a float32 [rows][V] numpy array")
+
+
+def sample_rows(logits, temperature, top_p=1.0, top_k=0, cap=1024, u=None):
+    """Sampler::sample of each row (engine/src/sampler.cpp:16-50) on the GPU with injected uniforms u[r]"""
+    buf, ptr, V = _dev_rows(logits)
+    rows = logits.shape[0]
+    uu = np.ascontiguousarray(u if u is not None else np.zeros(rows), np.float64)
+    out = np.empty(rows, np.int32)
+    check(_lib().gv_sample_rows(ptr, V, rows, V, temperature, top_p, top_k, cap, uu.ctypes.data_as(_P),
+                                out.ctypes.data_as(_P)), "gv_sample_rows")
+    return out
+
+
+def accept_match(logits, batch, temperature, top_p=1.0, top_k=0, cap=1024, u=None):
+    """sample-and-match over a verified chain (engine/src/geode.cpp:318-374): (emitted tokens, kept rows)"""
+    buf, ptr, V = _dev_rows(logits)
+    n = logits.shape[0]
+    b = np.ascontiguousarray(batch, np.int32)
+    uu = np.ascontiguousarray(u if u is not None else np.zeros(n), np.float64)
+    out = np.empty(n, np.int32)
+    kept = _c.c_int(0)
+    rc = _lib().gv_accept_match(ptr, V, V, b.ctypes.data_as(_P), n, temperature, top_p, top_k, cap,
+                                uu.ctypes.data_as(_P), out.ctypes.data_as(_P), _c.byref(kept))
+    check(-1 if rc < 0 else 0, "gv_accept_match")
+    return out[:rc].copy(), kept.value
+
+
+def accept_textbook(target, draft, temperature, top_p, greedy, u_draft=None, u_acc=None, u_res=0.0):
+    """the textbook rule (Leviathan et al. 2023, Alg. 1) on the GPU: the emitted tokens"""
+    tb, tp, V = _dev_rows(target)
+    db, dp, _ = _dev_rows(draft)
+    k = draft.shape[0]
+    ud = np.ascontiguousarray(u_draft if u_draft is not None else np.zeros(k), np.float32)
+    ua = np.ascontiguousarray(u_acc if u_acc is not None else np.zeros(k), np.float32)
+    out = np.empty(k + 1, np.int32)
+    rc = _lib().gv_accept_textbook(tp, dp, V, V, k, temperature, top_p, 1 if greedy else 0, ud.ctypes.data_as(_P),
+                                   ua.ctypes.data_as(_P), float(u_res), out.ctypes.data_as(_P))
+    check(-1 if rc < 0 else 0, "gv_accept_textbook")
+    return out[:rc].copy()
 
 
 class VerifyModel:

@@ -56,6 +56,10 @@ int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const G
 int mfma_split(int64_t K, int ntt, int &waves, int &kw);
 int64_t tiles_per_wg(int64_t ntiles, int waves, int ntt);
 
+// the library's stream and lazy device set-up (capi.hip)
+hipStream_t stream();
+int ensure_init();
+
 // elementwise helpers (misc.hip)
 int f16_to_f32(const uint16_t *x, int64_t n, float *y, hipStream_t st);
 int swiglu(const float *g, const float *u, int64_t n, float *m, hipStream_t st);

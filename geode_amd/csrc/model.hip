@@ -20,8 +20,6 @@
 
 namespace gv {
 
-hipStream_t stream();
-int ensure_init();
 
 // ---------------------------------------------------------------- kernels
 // the rows' embeddings: dequant_row of the embedding matrix (pack.cpp:356-366), bit for bit, to x; then the first

@@ -164,6 +164,30 @@ int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
  * verify again before trusting the model's state. */
 int gv_model_replay(gv_model *m, int cls, int layer, int reps, float *ms_per_launch);
 
+/* ------------------------------------------------------------------ sampling and acceptance (C2)
+ * Rows of logits in device memory (ld floats apart, e.g. gv_model_logits'), uniforms and results on the host.
+ * The double sums of the sampler run as parallel scans and expf is the device's: a sampled index can differ from
+ * the reference's only when a uniform or top_p falls within ~1e-15 (relative) of a boundary. */
+
+/* Sampler::sample (engine/src/sampler.cpp:16-50) of each row with its injected uniform u[r] in [0, 1) standing for
+ * uniform_real_distribution<double>(0, kept): T <= 0 the first argmax; else the top_k candidates (else the top
+ * `cap`, 1024 in the reference; cap 0 with top_p < 1: the whole vocabulary), ties to the lower index. rows <= 64. */
+int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float temperature, float top_p, int top_k,
+                   int cap, const double *u, int32_t *out);
+/* Sample-and-match over a verified chain (engine/src/geode.cpp:318-374): batch = [tok, d1..d_{n-1}]; row i sampled
+ * with u[i]; a draft stands while row i samples exactly it. out: the stood drafts then the first sampled token that
+ * is no draft; returns their count (or -1), *kept = the rows that stay (verify_keep's argument). n <= 32. */
+int gv_accept_match(const float *logits, int64_t ld, int V, const int32_t *batch, int n, float temperature,
+                    float top_p, int top_k, int cap, const double *u, int32_t *out, int *kept);
+/* The textbook rule (Leviathan et al. 2023, Alg. 1; no reference counterpart: the reference accepts by
+ * sample-and-match). p_i, q_i = the full-vocabulary top-p nucleus of target row i / draft row i at temperature T.
+ * Draft i: greedy: argmax q_i, accepted iff argmax p_i equals it; else d_i ~ q_i by u_draft[i], accepted iff
+ * u_acc[i] q_i(d_i) < p_i(d_i). At the first rejection a token from max(0, p_i - q_i) by inverse CDF in index order
+ * (u_res); when all k stand, a bonus token from p_k (u_res). target [k+1][ld], draft [k][ld]; k <= 31. out: the
+ * accepted drafts then the extra token; returns their count (or -1). */
+int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int V, int k, float temperature,
+                       float top_p, int greedy, const float *u_draft, const float *u_acc, float u_res, int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif
