@@ -71,6 +71,7 @@ SIGNATURES = {
     "gv_model_time_kernel": (_c.c_int, [_P, _c.c_int]),
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
+    "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
                                   _P, _P]),
     "gv_accept_match": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
@@ -327,6 +328,20 @@ class VerifyModel:
         ms = _c.c_float(0)
         check(_lib().gv_model_replay(self.h, cls, layer, reps, _c.byref(ms)), "gv_model_replay")
         return ms.value
+
+    def moe(self, layer, h, router_logits=None):
+        """one MoE block on rows h [M][hidden] (C3): (out [M][hidden] without the residual, ids, weights)"""
+        h = np.ascontiguousarray(h, np.float32)
+        M = h.shape[0]
+        K, H = self.cfg["top_k"], self.cfg["hidden"]
+        lg = np.ascontiguousarray(router_logits, np.float32) if router_logits is not None else None
+        out = np.empty((M, H), np.float32)
+        ids = np.empty((M, K), np.int32)
+        wts = np.empty((M, K), np.float32)
+        check(_lib().gv_model_moe(self.h, layer, h.ctypes.data_as(_P), M, lg.ctypes.data_as(_P) if lg is not None
+                                  else None, out.ctypes.data_as(_P), ids.ctypes.data_as(_P), wts.ctypes.data_as(_P)),
+              "gv_model_moe")
+        return out, ids, wts
 
     def route_ids(self, n):
         out = np.empty((self.cfg["n_layers"], n, self.cfg["top_k"]), np.int32)

@@ -397,7 +397,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     }
 }
 
-// The post-attention RMSNorm and the router logits. A workgroup takes 4 rows of the router ([E + 1][H] bf16, the
+// The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A
+// workgroup takes 4 rows of the router ([E + 1][H] bf16, the
 // shared expert's gate row last; one a wave) and the tokens in groups of router_tokens(H). Every load is issued
 // first (the rows, the residual rows, the norm weights); the sums of squares, 1 / RMS and x inv (1 + w) (rmsnorm's
 // arithmetic) then come from registers, workgroup b also writing token b's operands for the experts' products, and
@@ -436,11 +437,12 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
 #pragma unroll
     for (int q = 0; q < GPT; ++q) {
         const int g = threadIdx.x + q * 256;
-        const float4 a = g < H / 8 ? *reinterpret_cast<const float4 *>(norm_w + g * 8) : make_float4(0, 0, 0, 0);
-        const float4 b = g < H / 8 ? *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4) : make_float4(0, 0, 0, 0);
+        const bool ld = norm_w && g < H / 8;
+        const float4 a = ld ? *reinterpret_cast<const float4 *>(norm_w + g * 8) : make_float4(0, 0, 0, 0);
+        const float4 b = ld ? *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4) : make_float4(0, 0, 0, 0);
         const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);
+        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);   // no norm: 1, and inv = 1 below
     }
     bool wrote_w = false;
     for (int t0 = 0; t0 < M; t0 += TG) {
@@ -493,7 +495,9 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
         for (int tt = 0; tt < TG; ++tt) {
             if (tt >= nt) break;
             const double tot = ((red[0][tt] + red[1][tt]) + red[2][tt]) + red[3][tt];
-            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(H)), eps)));
+            const float inv =
+                norm_w ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(H)), eps)))
+                       : 1.0f;
 #pragma unroll
             for (int q = 0; q < GPT; ++q) {
                 float v[8];
@@ -930,12 +934,12 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
-                               L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+                               m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
-                               L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+                               m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
         }
         return 0;
     }
@@ -952,7 +956,9 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     case GV_K_MOE_DOWN:
         return moe_products(m, L, M, false, st);
     case GV_K_COMBINE: {   // the residual add, then the next layer's input RMSNorm (after the last: the final norm)
-        const float *next_norm = l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm : m.final_norm;
+        const float *next_norm = m.moe_only                ? nullptr
+                                 : l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm
+                                                      : m.final_norm;
         hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, m.route + l, m.sp, m.x,
                            next_norm, c.eps, m.act_h, abH);
         return 0;
@@ -1456,6 +1462,44 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
     m.timed_class = saved;
     if (rc != 0) return -1;
     *ms_per_launch = ms / reps;
+    return 0;
+}
+
+int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *router_logits, float *out,
+                 int32_t *ids, float *weights) {
+    GV_REQUIRE(g && h && out, "gv_model_moe: null pointer");
+    Model &m = g->m;
+    const auto &c = m.c;
+    GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_moe: no such layer");
+    GV_REQUIRE(M >= 1 && M <= c.max_rows, "gv_model_moe: 1 <= M <= max_rows");
+    const int H = c.hidden, E = c.n_experts, K = c.top_k;
+    const hipStream_t st = stream();
+    StepParams &sp = m.host_sp;
+    std::memset(&sp, 0, sizeof sp);
+    sp.pos = m.pos;
+    sp.M = M;
+    GV_CHECK_HIP(hipMemcpyAsync(m.sp, &sp, sizeof sp, hipMemcpyHostToDevice, st));
+    GV_CHECK_HIP(hipMemcpyAsync(m.x, h, static_cast<size_t>(M) * H * 4, hipMemcpyHostToDevice, st));
+    m.moe_only = true;
+    int rc = launch_class(m, GV_K_ROUTER, layer, M, st);   // the shared expert's gate logit and the operands
+    if (rc == 0 && router_logits)                          // the routed logits as given
+        rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, router_logits, static_cast<size_t>(E) * 4,
+                              static_cast<size_t>(E) * 4, M, hipMemcpyHostToDevice, st) == hipSuccess ? 0 : -1;
+    for (int cls : {GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN})
+        if (rc == 0) rc = launch_class(m, cls, layer, M, st);
+    if (rc == 0) rc = hipMemsetAsync(m.x, 0, static_cast<size_t>(M) * H * 4, st) == hipSuccess ? 0 : -1;
+    if (rc == 0) rc = launch_class(m, GV_K_COMBINE, layer, M, st);   // the block's output, no residual
+    m.moe_only = false;
+    GV_REQUIRE(rc == 0, std::string("gv_model_moe: ") + last_error());
+    GV_CHECK_HIP(hipMemcpyAsync(out, m.x, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToHost, st));
+    if (ids)
+        GV_CHECK_HIP(hipMemcpyAsync(ids, m.route_ids + static_cast<int64_t>(layer) * c.max_rows * K,
+                                    static_cast<size_t>(M) * K * 4, hipMemcpyDeviceToHost, st));
+    if (weights)
+        GV_CHECK_HIP(hipMemcpyAsync(weights, m.route[layer].weight, static_cast<size_t>(M) * K * 4,
+                                    hipMemcpyDeviceToHost, st));
+    GV_CHECK_HIP(hipStreamSynchronize(st));
+    m.last_n = 0;   // the step's state is this block's, not a verify's
     return 0;
 }
 

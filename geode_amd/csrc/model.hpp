@@ -72,6 +72,7 @@ struct Model {
     // host side
     int pos = 0, last_pos = 0, last_n = 0;
     int timed_class = -1;
+    bool moe_only = false;   // gv_model_moe: the router takes the rows as they are, the combine no next norm
     std::vector<hipEvent_t> events;   // pairs around the timed class's launches
     size_t events_used = 0;
     StepParams host_sp{};

@@ -219,6 +219,35 @@ def ffn_swiglu(gate, up, down, gg, gu, gd, H, F, x_f16, mode=0):
     return y
 
 
+def moe_layer(model, layer, h, router_logits=None, mode=0):
+    """orc_moe_layer on the oracle model's layer weights: (out [M][H] without the residual, ids, weights)"""
+    c = model.cfg
+    H, E, K, F = c["hidden"], c["n_experts"], c["top_k"], c["moe_ff"]
+    blocks, globs = [], []
+    for e in range(E):
+        b, g = model.tensor(EXPERT, layer, e)
+        blocks.append(b)
+        globs.append(np.asarray(g[:2], np.float32))
+    experts = np.ascontiguousarray(np.concatenate(blocks))
+    eg = np.ascontiguousarray(np.concatenate(globs), np.float32)
+    sg, gsg = model.tensor(SH_GATE, layer)
+    su, gsu = model.tensor(SH_UP, layer)
+    sd, gsd = model.tensor(SH_DOWN, layer)
+    shared_gate = np.ascontiguousarray(model.tensor(SHARED_GATE, layer)[0])
+    router = np.ascontiguousarray(model.tensor(ROUTER, layer)[0])
+    w = MoeWeights(H, E, K, F, c["shared_ff"], _ptr(experts), _ptr(eg), _ptr(sg), _ptr(su), _ptr(sd),
+                   (_c.c_float * 3)(gsg[0], gsu[0], gsd[0]), _ptr(shared_gate), _ptr(router))
+    h = np.ascontiguousarray(h, np.float32)
+    M = h.shape[0]
+    out = np.empty((M, H), np.float32)
+    ids = np.empty((M, K), np.int32)
+    wts = np.empty((M, K), np.float32)
+    lg = np.ascontiguousarray(router_logits, np.float32) if router_logits is not None else None
+    lib.orc_moe_layer(_c.byref(w), M, _ptr(h), _ptr(lg) if lg is not None else None, mode, _ptr(out), _ptr(ids),
+                      _ptr(wts), None)
+    return out, ids, wts
+
+
 def sample(logits, temperature, top_p, top_k=0, cap=1024, u=0.5):
     logits = np.ascontiguousarray(logits, np.float32)
     return lib.orc_sample(_ptr(logits), logits.size, temperature, top_p, top_k, cap, u)

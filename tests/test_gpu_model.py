@@ -117,3 +117,25 @@ def test_tree_keep_compacts_kv(models):
     gm.position = CTX
     chain = gm.verify(np.concatenate([toks[path], nxt]))
     assert rel_err(gl, chain[3:]) <= 1e-5
+
+
+@pytest.mark.parametrize("M,given", [(5, True), (17, True), (5, False)])
+def test_moe_block(models, M, given):
+    """C3: one MoE block on fp16-valued rows (routed logits given as N(0, 1), or the layer's router): the block's
+    output within 1e-2 of the oracle's int8 path (max error over max |out|), the routed experts and weights"""
+    om, gm = models
+    E = SMALL["n_experts"]
+    h = np.array([po.lib.orc_f16_to_f32(po.lib.orc_f32_to_f16(float(v))) for v in po.normal(91 + M, M * SMALL["hidden"], 1.0)],
+                 np.float32).reshape(M, SMALL["hidden"])
+    lg = po.normal(92 + M, M * E, 1.0).reshape(M, E) if given else None
+    want, wids, wwts = po.moe_layer(om, 1, h, lg)
+    got, gids, gwts = gm.moe(1, h, lg)
+    assert np.array_equal(gids, wids)
+    assert np.abs(gwts - wwts).max() <= 1e-6
+    assert rel_err(got, want) <= 1e-2, f"max error {rel_err(got, want):.3e}"
+    # and the verify state still works afterwards
+    om.position = CTX
+    gm.position = CTX
+    toks = np.array([3, 4], np.int32)
+    ol, oids = om.verify(toks, route=True)
+    _check(ol, gm.verify(toks), oids, gm.route_ids(2))
