@@ -537,10 +537,71 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     }
 }
 
-// The route (route_topk, model.cpp:4021-4065): softmax over the experts (max, expf, the sum in index order, divide),
-// the top K by probability with ties to the lower index, the weights p / (their sum in rank order); the shared
-// expert's gate sigmoid(logit); then the slots (distinct experts ascending, the shared one last) and their picks
-// ordered by (expert, token, rank), each pick placed by counting, so the order never depends on timing.
+// route_topk (model.cpp:4021-4065) of one row by one wave: softmax over the E experts (max, expf, the sum in index
+// order, divide), the top K by probability with ties to the lower index (a wave max, then ballots), the weights
+// p / (their sum in rank order) to w[0..K), the ids to ids[0..K) (lane 0), the shared expert's gate sigmoid(lg[E])
+// to *gate. p: this wave's E floats of LDS.
+__device__ inline void route_row(const float *__restrict__ lg, int E, int K, float *p, int *ids, float *w,
+                                 float *gate) {
+    const int lane = threadIdx.x & 63;
+    float v[4];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = e < E ? lg[e] : -__builtin_inff();
+        mx = fmaxf(mx, v[i]);
+    }
+    mx = wave_max(mx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E) p[e] = expf(__fsub_rn(v[i], mx));
+    }
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    if (lane == 0) {   // index order, as the reference; 64 values read ahead of their sums
+        int e = 0;
+        for (; e + 64 <= E; e += 64) {
+            float4 v4[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v4[u] = *reinterpret_cast<const float4 *>(&p[e + 4 * u]);
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4[u].x), v4[u].y), v4[u].z), v4[u].w);
+        }
+        for (; e < E; ++e) sum = __fadd_rn(sum, p[e]);
+    }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        pv[i] = e < E ? __fdiv_rn(p[e], sum) : -1.0f;
+    }
+    float top = 0.0f, mine = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const float bv = wave_max(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])));
+        int bi = E;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            const uint64_t hit = __ballot(pv[i] == bv);
+            if (hit) bi = 64 * i + __builtin_ctzll(hit);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (lane + 64 * i == bi) pv[i] = -1.0f;   // taken
+        if (lane == k) mine = bv;
+        if (lane == 0) ids[k] = bi;
+        top = __fadd_rn(top, bv);   // rank order
+    }
+    if (lane < K) w[lane] = __fdiv_rn(mine, top);
+    if (lane == 0 && gate) *gate = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[E])));
+}
+
+// The route of the step's rows (route_row each); then the slots (distinct experts ascending, the shared one last)
+// and their picks ordered by (expert, token, rank), each pick placed by counting, so the order never depends on
+// timing.
 __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ logits, int E, int K,
                                                     const StepParams *__restrict__ sp, RouteState *__restrict__ rs,
                                                     int32_t *__restrict__ ids_out) {
@@ -551,63 +612,8 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
     const int M = sp->M, E1 = E + 1;
     for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
     for (int t = wave; t < M; t += waves) {
-        const float *lg = logits + static_cast<int64_t>(t) * E1;
-        float v[4];
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
-            v[i] = e < E ? lg[e] : -__builtin_inff();
-            mx = fmaxf(mx, v[i]);
-        }
-        mx = wave_max(mx);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
-            if (e < E) p[t][e] = expf(__fsub_rn(v[i], mx));
-        }
-        __builtin_amdgcn_wave_barrier();
-        float sum = 0.0f;
-        if (lane == 0) {   // index order, as the reference; 64 values read ahead of their sums
-            int e = 0;
-            for (; e + 64 <= E; e += 64) {
-                float4 v4[16];
-#pragma unroll
-                for (int u = 0; u < 16; ++u) v4[u] = *reinterpret_cast<const float4 *>(&p[t][e + 4 * u]);
-#pragma unroll
-                for (int u = 0; u < 16; ++u)
-                    sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4[u].x), v4[u].y), v4[u].z), v4[u].w);
-            }
-            for (; e < E; ++e) sum = __fadd_rn(sum, p[t][e]);
-        }
-        sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
-        float pv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
-            pv[i] = e < E ? __fdiv_rn(p[t][e], sum) : -1.0f;
-        }
-        float top = 0.0f, mine = 0.0f;
-        for (int k = 0; k < K; ++k) {   // the largest left, ties to the lowest index: a wave max, then ballots
-            const float bv = wave_max(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])));
-            int bi = E;
-#pragma unroll
-            for (int i = 3; i >= 0; --i) {
-                const uint64_t hit = __ballot(pv[i] == bv);
-                if (hit) bi = 64 * i + __builtin_ctzll(hit);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i == bi) pv[i] = -1.0f;   // taken
-            if (lane == k) mine = bv;
-            if (lane == 0) ids[t * 16 + k] = bi;
-            top = __fadd_rn(top, bv);   // rank order
-        }
-        if (lane < K) {
-            rs->weight[t * K + lane] = __fdiv_rn(mine, top);
-            ids_out[t * K + lane] = ids[t * 16 + lane];
-        }
-        if (lane == 0) rs->gate[t] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[E])));
+        route_row(logits + static_cast<int64_t>(t) * E1, E, K, p[t], &ids[t * 16], rs->weight + t * K, rs->gate + t);
+        if (lane < K) ids_out[t * K + lane] = ids[t * 16 + lane];
     }
     __syncthreads();
     // counts per expert (the shared expert, E, once per row)
@@ -665,13 +671,13 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
                                                         size_t code_stride, size_t scale_stride, int64_t rows, int K,
                                                         const float *__restrict__ globals, int half_rows,
                                                         const _Float16 *__restrict__ act, int64_t act_stride,
-                                                        const RouteState *__restrict__ rs, float *__restrict__ out,
+                                                        const Slots sl, float *__restrict__ out,
                                                         int tiles_per_wg, int E1, int max_picks) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
     const int u = blockIdx.x;
-    if (u >= rs->n_slots) return;
-    const int e = rs->slot_expert[u], start = rs->slot_start[u], cnt = rs->slot_count[u];
+    if (u >= *sl.n_slots) return;
+    const int e = sl.expert[u], start = sl.start[u], cnt = sl.count[u];
     if (e < 0 || e >= E1 || cnt < 1 || cnt > kMaxRows || start < 0 || start + cnt > max_picks) return;   // no slot
     const int64_t ntiles = tiles_rows(rows);
     const int64_t t0 = static_cast<int64_t>(blockIdx.y) * tiles_per_wg;
@@ -683,7 +689,7 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
         K / kSuperK, 0, t0, t1,
         cnt,
         [&](int j) {
-            const int64_t src = UP ? rs->pick_token[start + j] : start + j;
+            const int64_t src = UP ? sl.pick_token[start + j] : start + j;
             return act + src * act_stride;
         },
         [&](int64_t row, int j, float v) {
@@ -695,12 +701,12 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
 
 // per pick: silu(gate) * up (kernels.hpp:141), quantized for down
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restrict__ gu, int F,
-                                                           const RouteState *__restrict__ rs,
+                                                           const int *__restrict__ n_picks,
                                                            _Float16 *__restrict__ act_m) {
     extern __shared__ uint4 lds_u4[];
     float *m = reinterpret_cast<float *>(lds_u4);
     const int p = blockIdx.x;
-    if (p >= rs->n_picks) return;
+    if (p >= *n_picks) return;
     const float *row = gu + static_cast<int64_t>(p) * 2 * F;
     for (int i = threadIdx.x; i < F; i += blockDim.x) {
         const float x = row[i];
@@ -712,17 +718,15 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
 
 // x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365); a workgroup per
 // (row, 256 columns)
-__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K,
-                                                      const RouteState *__restrict__ rs,
-                                                      const StepParams *__restrict__ sp, float *__restrict__ x,
-                                                      const float *__restrict__ norm_w, float eps,
-                                                      _Float16 *__restrict__ act, int64_t act_stride) {
+__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K, const MixView mix,
+                                                      int M, float *__restrict__ x, const float *__restrict__ norm_w,
+                                                      float eps, _Float16 *__restrict__ act, int64_t act_stride) {
     __shared__ double red[16];
     const int t = blockIdx.x;
-    if (t >= sp->M) return;
+    if (t >= M) return;
     const int ng = H / 8;
-    const float gs = rs->gate[t];
-    const float *ysh = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + K]) * H;
+    const float gs = mix.gate[t];
+    const float *ysh = y + static_cast<int64_t>(mix.pick_of[t * (K + 1) + K]) * H;
     float v[4][8];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -743,9 +747,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int k = k0 + u;
-                wk[u] = k < K ? rs->weight[t * K + k] : 0.0f;
+                wk[u] = k < K ? mix.weight[t * K + k] : 0.0f;
                 if (k < K) {
-                    const float *yk = y + static_cast<int64_t>(rs->pick_of[t * (K + 1) + k]) * H + g * 8;
+                    const float *yk = y + static_cast<int64_t>(mix.pick_of[t * (K + 1) + k]) * H + g * 8;
                     ya[u] = *reinterpret_cast<const float4 *>(yk);
                     yb[u] = *reinterpret_cast<const float4 *>(yk + 4);
                 }
@@ -766,7 +770,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
         *reinterpret_cast<float4 *>(xr) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
         *reinterpret_cast<float4 *>(xr + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
     }
-    norm_quant_regs(v, H, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
+    if (act) norm_quant_regs(v, H, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
 }
 
 // verify_keep of a tree: the kept path's keys and values moved to the kept slots in every layer; a thread per
@@ -818,44 +822,187 @@ namespace {
 // the slots a step of M rows can have: its distinct experts (at most M K) and the shared one
 inline int moe_slots(const Model &m, int M) { return std::min(m.max_slots, std::min(m.c.n_experts, M * m.c.top_k) + 1); }
 
+// One launch of the experts' products over a slot list
+struct MoeArgs {
+    const uint8_t *codes, *scales;
+    size_t code_stride, scale_stride;
+    int64_t rows, cols;
+    const float *globals;
+    int F;
+    const _Float16 *act;   // UP: the rows' operands, by pick_token; DOWN: the picks' (SwiGLU) operands, by pick
+    Slots sl;
+    float *out;            // [pick][rows]
+    int slots;             // a bound on the slot count (the grid)
+    int E1, max_picks;
+};
+
 template <int KW, int NTT, int WMAX, bool UP>
-int launch_moe(const Model &m, const LayerW &L, int M, int waves, hipStream_t st) {
-    const int64_t H = m.c.hidden, F = m.c.moe_ff;
-    const int64_t rows = UP ? 2 * F : H, cols = UP ? H : F;
-    const int64_t ntiles = tiles_rows(rows);
-    const int slots = moe_slots(m, M);
+int launch_moe_raw(const MoeArgs &a, int waves, hipStream_t st) {
+    const int64_t ntiles = tiles_rows(a.rows);
     // the slots' tiles over about as many workgroups as the chip holds at once
-    const int per = static_cast<int>(tiles_per_wg(ntiles * slots, waves, NTT));
+    const int per = static_cast<int>(tiles_per_wg(ntiles * a.slots, waves, NTT));
     const int tiles = static_cast<int>((ntiles + per - 1) / per);
     const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
     static int granted = 0;
     if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 76 * 1024, granted) != 0)
         return -1;
-    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(slots, tiles), dim3(64 * waves), lds, st,
-                       UP ? L.gu_codes : L.dn_codes, UP ? L.gu_scales : L.dn_scales,
-                       UP ? m.gu_code_stride : m.dn_code_stride, UP ? m.gu_scale_stride : m.dn_scale_stride, rows,
-                       static_cast<int>(cols), L.expert_globals, static_cast<int>(F), UP ? m.act_h : m.act_m,
-                       act_halves(cols), m.route + (&L - &m.layers[0]), UP ? m.gu_out : m.y, per, m.E1,
-                       m.max_picks);
+    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(a.slots, tiles), dim3(64 * waves), lds, st, a.codes,
+                       a.scales, a.code_stride, a.scale_stride, a.rows, static_cast<int>(a.cols), a.globals, a.F, a.act,
+                       act_halves(a.cols), a.sl, a.out, per, a.E1, a.max_picks);
+    GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
 template <bool UP>
-int moe_launch(const Model &m, const LayerW &L, int M, int ntt, int kw, int waves, hipStream_t st) {
+int moe_launch(const MoeArgs &a, int ntt, int kw, int waves, hipStream_t st) {
     if (ntt == 1) {
-        if (kw == 16) return launch_moe<16, 1, 8, UP>(m, L, M, waves, st);
-        if (kw == 8) return launch_moe<8, 1, 8, UP>(m, L, M, waves, st);
-        return launch_moe<4, 1, 8, UP>(m, L, M, waves, st);
+        if (kw == 16) return launch_moe_raw<16, 1, 8, UP>(a, waves, st);
+        if (kw == 8) return launch_moe_raw<8, 1, 8, UP>(a, waves, st);
+        return launch_moe_raw<4, 1, 8, UP>(a, waves, st);
     }
-    if (kw == 8) return launch_moe<8, 2, 8, UP>(m, L, M, waves, st);
-    return launch_moe<4, 2, 8, UP>(m, L, M, waves, st);
+    if (kw == 8) return launch_moe_raw<8, 2, 8, UP>(a, waves, st);
+    return launch_moe_raw<4, 2, 8, UP>(a, waves, st);
+}
+
+// the experts' products of layer L: gate|up (up) or down, over slots of at most `rows_max` rows each
+int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float16 *act, const Slots &sl, float *out,
+            int slots, int max_picks, hipStream_t st) {
+    const int64_t H = m.c.hidden, F = m.c.moe_ff;
+    const int ntt = rows_max <= 16 ? 1 : 2;
+    int waves, kw;
+    GV_REQUIRE(mfma_split(up ? H : F, ntt, waves, kw), "moe: K too wide for one launch");
+    MoeArgs a{up ? L.gu_codes : L.dn_codes,
+              up ? L.gu_scales : L.dn_scales,
+              up ? m.gu_code_stride : m.dn_code_stride,
+              up ? m.gu_scale_stride : m.dn_scale_stride,
+              up ? 2 * F : H,
+              up ? H : F,
+              L.expert_globals,
+              static_cast<int>(F),
+              act,
+              sl,
+              out,
+              slots,
+              m.E1,
+              max_picks};
+    return up ? moe_launch<true>(a, ntt, kw, waves, st) : moe_launch<false>(a, ntt, kw, waves, st);
 }
 
 int moe_products(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
-    const int ntt = M <= 16 ? 1 : 2;
-    int waves, kw;
-    GV_REQUIRE(mfma_split(up ? m.c.hidden : m.c.moe_ff, ntt, waves, kw), "moe: K too wide for one launch");
-    return up ? moe_launch<true>(m, L, M, ntt, kw, waves, st) : moe_launch<false>(m, L, M, ntt, kw, waves, st);
+    return moe_run(m, L, up, M, up ? m.act_h : m.act_m, route_slots(m.route + (&L - &m.layers[0])),
+                   up ? m.gu_out : m.y, moe_slots(m, M), m.max_picks, st);
+}
+
+// ---------------------------------------------------------------- prefill MoE (C5): many rows
+// the shared expert's gate logit of each row: the bf16 row . h in the router's eight-sum order; a wave a row
+__global__ __launch_bounds__(256) void gate_rows_kernel(const uint16_t *__restrict__ wrow, int H,
+                                                        const float *__restrict__ h, int M, float *__restrict__ logits,
+                                                        int E1) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= M) return;
+    const float *hr = h + static_cast<int64_t>(t) * H;
+    float a = 0.0f;
+    if (lane < 8)
+        for (int c0 = lane; c0 < H; c0 += 8 * 16) {
+            float hv[16], wv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                hv[u] = hr[c0 + 8 * u];
+                wv[u] = __uint_as_float(static_cast<uint32_t>(wrow[c0 + 8 * u]) << 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) a = __fadd_rn(a, __fmul_rn(wv[u], hv[u]));
+        }
+    const float s1 = __fadd_rn(a, __shfl_down(a, 4, 64));   // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7))
+    const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
+    const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
+    if (lane == 0) logits[static_cast<int64_t>(t) * E1 + E1 - 1] = s3;
+}
+
+// route_topk of every row (route_row), a wave a row
+__global__ __launch_bounds__(256) void route_rows_kernel(const float *__restrict__ logits, int E, int K, int M,
+                                                         int *__restrict__ ids, float *__restrict__ w,
+                                                         float *__restrict__ gate) {
+    __shared__ float p[4][256];
+    const int wave = threadIdx.x >> 6, t = blockIdx.x * 4 + wave;
+    if (t >= M) return;
+    route_row(logits + static_cast<int64_t>(t) * (E + 1), E, K, p[wave], ids + static_cast<int64_t>(t) * K,
+              w + static_cast<int64_t>(t) * K, gate + t);
+}
+
+// The picks per expert (the shared one, E, takes every row), their starts, and the slots: each expert's picks in
+// runs of at most 32 (the products' row tiles), experts ascending. One workgroup of 1024 threads (E + 1 <= 257).
+__global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids, int M, int K, int E,
+                                                     int *__restrict__ start_out, int *__restrict__ n_slots,
+                                                     int *__restrict__ slot_expert, int *__restrict__ slot_start,
+                                                     int *__restrict__ slot_count, int *__restrict__ n_picks) {
+    __shared__ int cnt[257], start[257], sbase[257];
+    __shared__ int wt[2][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e <= E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < M * K; i += blockDim.x) atomicAdd(&cnt[ids[i]], 1);
+    if (tid == 0) cnt[E] = M;
+    __syncthreads();
+    const int c = tid <= E ? cnt[tid] : 0, ns = (c + 31) / 32;
+    int ic = c, is = ns;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int pc = __shfl_up(ic, o, 64), ps = __shfl_up(is, o, 64);
+        if (lane >= o) ic += pc, is += ps;
+    }
+    if (lane == 63) wt[0][wave] = ic, wt[1][wave] = is;
+    __syncthreads();
+    if (tid <= E) {
+        int bc = 0, bs = 0;
+        for (int w2 = 0; w2 < wave; ++w2) bc += wt[0][w2], bs += wt[1][w2];
+        start[tid] = bc + ic - c;
+        sbase[tid] = bs + is - ns;
+        start_out[tid] = bc + ic - c;
+        if (tid == E) *n_slots = bs + is, *n_picks = bc + ic;
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += blockDim.x)
+        for (int j = 0; 32 * j < cnt[e]; ++j) {
+            const int u = sbase[e] + j;
+            slot_expert[u] = e;
+            slot_start[u] = start[e] + 32 * j;
+            slot_count[u] = min(32, cnt[e] - 32 * j);
+        }
+}
+
+// The picks of expert blockIdx.x in (token, rank) order, by ordered compaction over ids [M][K]: their rows and,
+// per (row, rank), where the pick went; the shared expert (E) takes row t at start + t.
+__global__ __launch_bounds__(256) void fill_picks_kernel(const int *__restrict__ ids, int M, int K, int E,
+                                                         const int *__restrict__ start, int *__restrict__ pick_token,
+                                                         int *__restrict__ pick_of) {
+    __shared__ int wt[4];
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int s0 = start[e];
+    if (e == E) {
+        for (int t = tid; t < M; t += blockDim.x) {
+            pick_token[s0 + t] = t;
+            pick_of[t * (K + 1) + K] = s0 + t;
+        }
+        return;
+    }
+    int base = 0;
+    for (int c0 = 0; c0 < M * K; c0 += blockDim.x) {
+        const int i = c0 + tid;
+        const bool match = i < M * K && ids[i] == e;
+        const uint64_t b = __ballot(match);
+        const int rank = __popcll(b & ((1ull << lane) - 1ull));
+        if (lane == 0) wt[wave] = __popcll(b);
+        __syncthreads();
+        int wb = base;
+        for (int w2 = 0; w2 < wave; ++w2) wb += wt[w2];
+        if (match) {
+            const int p = s0 + wb + rank, t = i / K, k = i % K;
+            pick_token[p] = t;
+            pick_of[t * (K + 1) + k] = p;
+        }
+        base += wt[0] + wt[1] + wt[2] + wt[3];
+        __syncthreads();
+    }
 }
 
 GemvOut qkv_out(const Model &m, const LayerW &L) {
@@ -951,7 +1098,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         return moe_products(m, L, M, true, st);
     case GV_K_SWIGLU:
         hipLaunchKernelGGL(swiglu_quant_kernel, dim3(M * (c.top_k + 1)), dim3(256), static_cast<size_t>(c.moe_ff) * 4,
-                           st, m.gu_out, c.moe_ff, m.route + l, m.act_m);
+                           st, m.gu_out, c.moe_ff, &m.route[l].n_picks, m.act_m);
         return 0;
     case GV_K_MOE_DOWN:
         return moe_products(m, L, M, false, st);
@@ -959,7 +1106,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         const float *next_norm = m.moe_only                ? nullptr
                                  : l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm
                                                       : m.final_norm;
-        hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, m.route + l, m.sp, m.x,
+        hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, route_mix(m.route + l), M, m.x,
                            next_norm, c.eps, m.act_h, abH);
         return 0;
     }
@@ -980,6 +1127,83 @@ int run_layers(Model &m, int M, hipStream_t st) {
             if (launch_class(m, cls, l, M, st) != 0) return -1;
     if (launch_class(m, GV_K_LM_HEAD, 0, M, st) != 0) return -1;
     GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+// the prefill buffers for M rows (kept for later calls; regrown when M is larger)
+int prefill_alloc(Model &m, int M) {
+    Prefill &pf = m.pf;
+    if (pf.cap >= M) return 0;
+    for (void *p : pf.allocs) (void)hipFree(p);
+    pf.allocs.clear();
+    const int cap = (M + 511) / 512 * 512;
+    const auto &c = m.c;
+    const int64_t H = c.hidden, F = c.moe_ff, E1 = m.E1, K = c.top_k;
+    pf.max_picks = cap * (c.top_k + 1);
+    pf.max_slots = static_cast<int>(E1 + pf.max_picks / 32 + 1);
+    bool ok = true;
+    auto get = [&](size_t bytes) -> void * {
+        void *p = nullptr;
+        if (!ok || hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+            ok = false;
+            return nullptr;
+        }
+        pf.allocs.push_back(p);
+        return p;
+    };
+    pf.h = static_cast<float *>(get(cap * H * 4));
+    pf.logits = static_cast<float *>(get(cap * E1 * 4));
+    pf.gate = static_cast<float *>(get(cap * 4));
+    pf.w = static_cast<float *>(get(cap * K * 4));
+    pf.ids = static_cast<int *>(get(cap * K * 4));
+    pf.cnt = static_cast<int *>(get(E1 * 4));
+    pf.start = static_cast<int *>(get(E1 * 4));
+    pf.n_slots = static_cast<int *>(get(4));
+    pf.n_picks = static_cast<int *>(get(4));
+    pf.slot_expert = static_cast<int *>(get(static_cast<size_t>(pf.max_slots) * 4));
+    pf.slot_start = static_cast<int *>(get(static_cast<size_t>(pf.max_slots) * 4));
+    pf.slot_count = static_cast<int *>(get(static_cast<size_t>(pf.max_slots) * 4));
+    pf.pick_token = static_cast<int *>(get(static_cast<size_t>(pf.max_picks) * 4));
+    pf.pick_of = static_cast<int *>(get(cap * (K + 1) * 4));
+    pf.act = static_cast<_Float16 *>(get(cap * act_bytes(H)));
+    pf.gu = static_cast<float *>(get(static_cast<size_t>(pf.max_picks) * 2 * F * 4));
+    pf.act_m = static_cast<_Float16 *>(get(static_cast<size_t>(pf.max_picks) * act_bytes(F)));
+    pf.y = static_cast<float *>(get(static_cast<size_t>(pf.max_picks) * H * 4));
+    pf.out = static_cast<float *>(get(cap * H * 4));
+    GV_REQUIRE(ok, "prefill MoE: out of device memory");
+    pf.cap = cap;
+    return 0;
+}
+
+// The MoE block of layer `layer` on the M rows in pf.h with the routed logits in pf.logits [M][E + 1] (column E
+// filled here: the shared expert's gate logit): route each row, group the picks by expert (runs of at most 32),
+// the experts' products, SwiGLU, down, and the combine into pf.out (no residual).
+int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
+    const auto &c = m.c;
+    const int H = c.hidden, E = c.n_experts, K = c.top_k, F = c.moe_ff;
+    Prefill &pf = m.pf;
+    LayerW &L = m.layers[static_cast<size_t>(layer)];
+    if (quantize_act(pf.h, H, M, H, nullptr, 0.0f, pf.act, act_halves(H), nullptr, 0, st) != 0) return -1;
+    const int wg4 = (M + 3) / 4;
+    hipLaunchKernelGGL(gate_rows_kernel, dim3(wg4), dim3(256), 0, st, L.router + static_cast<int64_t>(E) * H, H, pf.h,
+                       M, pf.logits, m.E1);
+    hipLaunchKernelGGL(route_rows_kernel, dim3(wg4), dim3(256), 0, st, pf.logits, E, K, M, pf.ids, pf.w, pf.gate);
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, pf.start, pf.n_slots,
+                       pf.slot_expert, pf.slot_start, pf.slot_count, pf.n_picks);
+    hipLaunchKernelGGL(fill_picks_kernel, dim3(m.E1), dim3(256), 0, st, pf.ids, M, K, E, pf.start, pf.pick_token,
+                       pf.pick_of);
+    GV_CHECK_HIP(hipGetLastError());
+    const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks};
+    const int picks = M * (K + 1);
+    if (moe_run(m, L, true, 32, pf.act, sl, pf.gu, pf.max_slots, picks, st) != 0) return -1;
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(picks), dim3(256), static_cast<size_t>(F) * 4, st, pf.gu, F,
+                       pf.n_picks, pf.act_m);
+    if (moe_run(m, L, false, 32, pf.act_m, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
+    GV_CHECK_HIP(hipMemsetAsync(pf.out, 0, static_cast<size_t>(M) * H * 4, st));
+    hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M,
+                       pf.out, nullptr, 0.0f, nullptr, 0);
+    GV_CHECK_HIP(hipGetLastError());
+    pf.M = M;
     return 0;
 }
 
@@ -1157,6 +1381,7 @@ void gv_model_free(gv_model *g) {
     if (!g) return;
     (void)hipStreamSynchronize(stream());
     for (void *p : g->m.allocs) (void)hipFree(p);
+    for (void *p : g->m.pf.allocs) (void)hipFree(p);
     delete g;
 }
 
@@ -1471,9 +1696,25 @@ int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *rou
     Model &m = g->m;
     const auto &c = m.c;
     GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_moe: no such layer");
-    GV_REQUIRE(M >= 1 && M <= c.max_rows, "gv_model_moe: 1 <= M <= max_rows");
+    GV_REQUIRE(M >= 1 && M <= 16384, "gv_model_moe: 1 <= M <= 16384");
     const int H = c.hidden, E = c.n_experts, K = c.top_k;
     const hipStream_t st = stream();
+    if (M > c.max_rows) {   // prefill: the routed logits given, the experts' grouped products
+        GV_REQUIRE(router_logits, "gv_model_moe: more rows than max_rows need the routed logits given");
+        if (prefill_alloc(m, M) != 0) return -1;
+        Prefill &pf = m.pf;
+        GV_CHECK_HIP(hipMemcpyAsync(pf.h, h, static_cast<size_t>(M) * H * 4, hipMemcpyHostToDevice, st));
+        GV_CHECK_HIP(hipMemcpy2DAsync(pf.logits, static_cast<size_t>(m.E1) * 4, router_logits,
+                                      static_cast<size_t>(E) * 4, static_cast<size_t>(E) * 4, M,
+                                      hipMemcpyHostToDevice, st));
+        if (moe_prefill(m, layer, M, st) != 0) return -1;
+        GV_CHECK_HIP(hipMemcpyAsync(out, pf.out, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToHost, st));
+        if (ids) GV_CHECK_HIP(hipMemcpyAsync(ids, pf.ids, static_cast<size_t>(M) * K * 4, hipMemcpyDeviceToHost, st));
+        if (weights)
+            GV_CHECK_HIP(hipMemcpyAsync(weights, pf.w, static_cast<size_t>(M) * K * 4, hipMemcpyDeviceToHost, st));
+        GV_CHECK_HIP(hipStreamSynchronize(st));
+        return 0;
+    }
     StepParams &sp = m.host_sp;
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;

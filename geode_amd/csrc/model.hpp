@@ -37,6 +37,21 @@ struct RouteState {
     float gate[kMaxRows];         // sigmoid of the shared expert's gate
 };
 
+// Expert slots in device memory: slot u is expert[u]'s run of count[u] picks from start[u]; pick p's row is
+// pick_token[p]. The decode step's come from its RouteState, the prefill's from its own buffers.
+struct Slots {
+    const int *n_slots, *expert, *start, *count, *pick_token, *n_picks;
+};
+inline Slots route_slots(const RouteState *rs) {   // member addresses of a device struct (no host access)
+    return Slots{&rs->n_slots, rs->slot_expert, rs->slot_start, rs->slot_count, rs->pick_token, &rs->n_picks};
+}
+// What the combine reads: the shared gate [M], the routed weights [M][K], the picks of each row [M][K + 1]
+struct MixView {
+    const float *gate, *weight;
+    const int *pick_of;
+};
+inline MixView route_mix(const RouteState *rs) { return MixView{rs->gate, rs->weight, rs->pick_of}; }
+
 struct LayerW {
     Q4 qkv;   // [nh*2*hd (q | gate per head) + nkv*hd (k) + nkv*hd (v)] x H, three globals
     float g_q = 1, g_k = 1, g_v = 1;
@@ -47,6 +62,17 @@ struct LayerW {
     uint8_t *dn_codes = nullptr, *dn_scales = nullptr;   // [E + 1] experts' down
     float *expert_globals = nullptr;                     // [E + 1][3]: gate half, up half, down
     _Float16 *kv = nullptr;   // K [nkv][slots][hd], then V [nkv][slots / 64][hd][64] (model.hip: k_index, v_index)
+};
+
+// The prefill MoE's buffers (C5: many rows), allocated for `cap` rows on first use
+struct Prefill {
+    int cap = 0, M = 0;
+    float *h = nullptr, *logits = nullptr, *gate = nullptr, *w = nullptr, *gu = nullptr, *y = nullptr, *out = nullptr;
+    int *ids = nullptr, *cnt = nullptr, *start = nullptr, *n_slots = nullptr, *n_picks = nullptr;
+    int *slot_expert = nullptr, *slot_start = nullptr, *slot_count = nullptr, *pick_token = nullptr, *pick_of = nullptr;
+    _Float16 *act = nullptr, *act_m = nullptr;
+    int max_slots = 0, max_picks = 0;
+    std::vector<void *> allocs;
 };
 
 struct Model {
@@ -73,6 +99,7 @@ struct Model {
     int pos = 0, last_pos = 0, last_n = 0;
     int timed_class = -1;
     bool moe_only = false;   // gv_model_moe: the router takes the rows as they are, the combine no next norm
+    Prefill pf;
     std::vector<hipEvent_t> events;   // pairs around the timed class's launches
     size_t events_used = 0;
     StepParams host_sp{};
