@@ -8,6 +8,7 @@ token (M = 5 rows): every layer, the final norm and lm_head, logits left on the 
 model's own greedy continuation, so a greedy sample-and-match accepts all of them (5 tokens emitted a step).
 
     python bench.py [--steps K] [--warmup W] [--tree] [--no-cpu]
+    python bench.py --config c2|c3|c5      (the acceptance rules; one MoE block at M = 5 or 512)
 """
 import argparse
 import json
@@ -104,6 +105,92 @@ def cpu_baseline(M, threads):
                       f"best of {reps}; step = t_head + 40 x t_layer = {best * 1e3:.1f} ms"}
 
 
+def bench_moe_block(g, M, reps):
+    """C3 (M = 5) / C5 (M = 512): one MoE block at the configs' shapes (256 experts + the shared one, hidden 2048,
+    ff 512), rows fp16-valued N(0, 1), routed logits N(0, 1) given; device time of the block re-run on its staged
+    inputs (gv_model_moe_replay)"""
+    cfg = dict(C4)
+    cfg["n_layers"] = 1
+    m = g.VerifyModel(cfg)
+    m.randomize(SEED, 0.02, 0.0221, 0)
+    rng = np.random.default_rng(SEED + M)
+    h = rng.standard_normal((M, cfg["hidden"])).astype(np.float16).astype(np.float32)
+    lg = rng.standard_normal((M, cfg["n_experts"])).astype(np.float32)
+    out, ids, _ = m.moe(0, h, lg)
+    touched = len(np.unique(ids))
+    ms = m.moe_replay(reps)
+    blk = 2 * cfg["moe_ff"] * Q4_ROW(cfg["hidden"]) + cfg["hidden"] * Q4_ROW(cfg["moe_ff"])   # 1,769,472 B
+    byts = (touched + 1) * blk + (M * cfg["hidden"] * (2 + 4) if M > cfg["max_rows"] else 0)
+    flops = 2.0 * 3 * cfg["hidden"] * cfg["moe_ff"] * M * (cfg["top_k"] + 1)
+    m.close()
+    return ms, touched, byts, flops
+
+
+def bench_c2(g, trials):
+    """C2: target logits [5 x V] ~ N(0, 3), draft [4 x V] = target rows 0..3 + N(0, 0.5), T 0.7, top-p 0.95; the
+    textbook rule per trial (seeded uniforms), stochastic and greedy, and sample-and-match of the 5 rows; logits
+    resident on the device, the time of each API call (device work and the result copy)"""
+    import ctypes as C
+    V, k = C4["vocab"], 4
+    rng = np.random.default_rng(SEED)
+    target = (rng.standard_normal((k + 1, V)) * 3).astype(np.float32)
+    draft = (target[:k] + rng.standard_normal((k, V)) * 0.5).astype(np.float32)
+    dt, dd = g.DeviceBuffer.from_array(target), g.DeviceBuffer.from_array(draft)
+    out = np.empty(k + 1, np.int32)
+    res = {}
+    for name, greedy in (("textbook_stochastic", 0), ("textbook_greedy", 1)):
+        times, emitted = [], []
+        for t in range(trials):
+            r = np.random.default_rng(SEED + t)
+            ud, ua = r.random(k).astype(np.float32), r.random(k).astype(np.float32)
+            t0 = time.perf_counter()
+            n = g.lib.gv_accept_textbook(dt.ptr, dd.ptr, V, V, k, 0.7, 0.95, greedy, ud.ctypes.data_as(C.c_void_p),
+                                         ua.ctypes.data_as(C.c_void_p), float(r.random()),
+                                         out.ctypes.data_as(C.c_void_p))
+            times.append(time.perf_counter() - t0)
+            g.check(-1 if n < 0 else 0, "gv_accept_textbook")
+            emitted.append(n)
+        res[name] = {"us_per_trial": float(np.median(times[2:]) * 1e6), "mean_tokens": float(np.mean(emitted))}
+    batch = np.array([7, 1, 2, 3, 4], np.int32)
+    kept = C.c_int(0)
+    times = []
+    for t in range(trials):
+        u = np.random.default_rng(SEED + 7 * t).random(k + 1)
+        t0 = time.perf_counter()
+        n = g.lib.gv_accept_match(dt.ptr, V, V, batch.ctypes.data_as(C.c_void_p), k + 1, 0.7, 0.95, 0, 1024,
+                                  u.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), C.byref(kept))
+        times.append(time.perf_counter() - t0)
+        g.check(-1 if n < 0 else 0, "gv_accept_match")
+    res["sample_and_match"] = {"us_per_step": float(np.median(times[2:]) * 1e6)}
+    return res
+
+
+def main_config(args):
+    import geode_amd as g
+
+    g.init(0)
+    if args.config in ("c3", "c5"):
+        M = 5 if args.config == "c3" else 512
+        ms, touched, byts, flops = bench_moe_block(g, M, 20 if M > 5 else 100)
+        out = {"metric": f"{args.config.upper()} MoE block: HBM GB/s vs peak", "value": byts / (ms / 1e3) / 1e9,
+               "unit": "GB/s", "n_gpus": 1, "steps": 20 if M > 5 else 100, "warmup": 1, "ms_per_step": ms,
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+               "config": {"workload": f"{args.config.upper()}: one MoE block, 256 experts + shared, hidden 2048, ff 512, "
+                                      f"top-8, M={M}, routed logits N(0,1) given"},
+               "experts_touched": touched, "bytes_per_block": byts, "tflops": flops / (ms / 1e3) / 1e12,
+               "roofline": {"bound": "hbm", "achieved": byts / (ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9,
+                            "unit": "GB/s", "frac": byts / (ms / 1e3) / PEAK_HBM, "traffic": None}}
+    else:
+        r = bench_c2(g, 40)
+        out = {"metric": "C2 acceptance: microseconds per trial", "value": r["textbook_stochastic"]["us_per_trial"],
+               "unit": "us/trial", "n_gpus": 1, "steps": 40, "warmup": 2, "higher_is_better": False,
+               "scaling": "weak", "vs_baseline": None, "dtype": "f32/f64", "data": "synthetic",
+               "config": {"workload": "C2: k=4, V=151936, T=0.7, top-p 0.95, textbook rule (stochastic), logits "
+                                      "device-resident; per API call incl. the result copy"}, "detail": r,
+               "bytes_per_trial": 9 * C4["vocab"] * 4}
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,11 +198,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--tree", action="store_true", help="verify the 17-row draft tree instead of the k=4 chain")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--config", choices=["c4", "c2", "c3", "c5"], default="c4",
+                    help="c4 (default): the verify step; c2 / c3 / c5: the acceptance rules / one MoE block")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the verify step on one GPU only: the step of one sequence does not shard "
               "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.config != "c4":
+        main_config(args)
+        return
 
     import geode_amd as g
 

@@ -72,6 +72,7 @@ SIGNATURES = {
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
+    "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
                                   _P, _P]),
     "gv_accept_match": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
@@ -342,6 +343,12 @@ class VerifyModel:
                                   else None, out.ctypes.data_as(_P), ids.ctypes.data_as(_P), wts.ctypes.data_as(_P)),
               "gv_model_moe")
         return out, ids, wts
+
+    def moe_replay(self, reps=20):
+        """mean ms of the last moe() block re-run on its device-staged inputs (device work only)"""
+        ms = _c.c_float(0)
+        check(_lib().gv_model_moe_replay(self.h, reps, _c.byref(ms)), "gv_model_moe_replay")
+        return ms.value
 
     def route_ids(self, n):
         out = np.empty((self.cfg["n_layers"], n, self.cfg["top_k"]), np.int32)

@@ -1690,6 +1690,34 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
     return 0;
 }
 
+}  // extern "C"
+
+namespace gv {
+// The MoE block of layer `layer` on the M rows staged in pf.h (and the routed logits in pf.logits when given):
+// the verify step's kernels for M <= max_rows (the router without a norm, the combine into a zeroed x), the
+// prefill path beyond; the output in pf.out (M > max_rows) or m.x.
+int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
+    const auto &c = m.c;
+    const int H = c.hidden, E = c.n_experts;
+    if (M > c.max_rows) return moe_prefill(m, layer, M, st);
+    Prefill &pf = m.pf;
+    GV_CHECK_HIP(hipMemcpyAsync(m.x, pf.h, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToDevice, st));
+    m.moe_only = true;
+    int rc = launch_class(m, GV_K_ROUTER, layer, M, st);   // the shared expert's gate logit and the operands
+    if (rc == 0 && given)                                  // the routed logits as given
+        rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, pf.logits, static_cast<size_t>(m.E1) * 4,
+                              static_cast<size_t>(E) * 4, M, hipMemcpyDeviceToDevice, st) == hipSuccess ? 0 : -1;
+    for (int cls : {GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN})
+        if (rc == 0) rc = launch_class(m, cls, layer, M, st);
+    if (rc == 0) rc = hipMemsetAsync(m.x, 0, static_cast<size_t>(M) * H * 4, st) == hipSuccess ? 0 : -1;
+    if (rc == 0) rc = launch_class(m, GV_K_COMBINE, layer, M, st);   // the block's output, no residual
+    m.moe_only = false;
+    return rc;
+}
+}  // namespace gv
+
+extern "C" {
+
 int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *router_logits, float *out,
                  int32_t *ids, float *weights) {
     GV_REQUIRE(g && h && out, "gv_model_moe: null pointer");
@@ -1697,50 +1725,59 @@ int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *rou
     const auto &c = m.c;
     GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_moe: no such layer");
     GV_REQUIRE(M >= 1 && M <= 16384, "gv_model_moe: 1 <= M <= 16384");
+    GV_REQUIRE(M <= c.max_rows || router_logits, "gv_model_moe: more rows than max_rows need the routed logits");
     const int H = c.hidden, E = c.n_experts, K = c.top_k;
     const hipStream_t st = stream();
-    if (M > c.max_rows) {   // prefill: the routed logits given, the experts' grouped products
-        GV_REQUIRE(router_logits, "gv_model_moe: more rows than max_rows need the routed logits given");
-        if (prefill_alloc(m, M) != 0) return -1;
-        Prefill &pf = m.pf;
-        GV_CHECK_HIP(hipMemcpyAsync(pf.h, h, static_cast<size_t>(M) * H * 4, hipMemcpyHostToDevice, st));
-        GV_CHECK_HIP(hipMemcpy2DAsync(pf.logits, static_cast<size_t>(m.E1) * 4, router_logits,
-                                      static_cast<size_t>(E) * 4, static_cast<size_t>(E) * 4, M,
-                                      hipMemcpyHostToDevice, st));
-        if (moe_prefill(m, layer, M, st) != 0) return -1;
-        GV_CHECK_HIP(hipMemcpyAsync(out, pf.out, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToHost, st));
-        if (ids) GV_CHECK_HIP(hipMemcpyAsync(ids, pf.ids, static_cast<size_t>(M) * K * 4, hipMemcpyDeviceToHost, st));
-        if (weights)
-            GV_CHECK_HIP(hipMemcpyAsync(weights, pf.w, static_cast<size_t>(M) * K * 4, hipMemcpyDeviceToHost, st));
-        GV_CHECK_HIP(hipStreamSynchronize(st));
-        return 0;
-    }
+    if (prefill_alloc(m, M) != 0) return -1;
+    Prefill &pf = m.pf;
     StepParams &sp = m.host_sp;
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;
-    sp.M = M;
+    sp.M = std::min(M, c.max_rows);
     GV_CHECK_HIP(hipMemcpyAsync(m.sp, &sp, sizeof sp, hipMemcpyHostToDevice, st));
-    GV_CHECK_HIP(hipMemcpyAsync(m.x, h, static_cast<size_t>(M) * H * 4, hipMemcpyHostToDevice, st));
-    m.moe_only = true;
-    int rc = launch_class(m, GV_K_ROUTER, layer, M, st);   // the shared expert's gate logit and the operands
-    if (rc == 0 && router_logits)                          // the routed logits as given
-        rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, router_logits, static_cast<size_t>(E) * 4,
-                              static_cast<size_t>(E) * 4, M, hipMemcpyHostToDevice, st) == hipSuccess ? 0 : -1;
-    for (int cls : {GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN})
-        if (rc == 0) rc = launch_class(m, cls, layer, M, st);
-    if (rc == 0) rc = hipMemsetAsync(m.x, 0, static_cast<size_t>(M) * H * 4, st) == hipSuccess ? 0 : -1;
-    if (rc == 0) rc = launch_class(m, GV_K_COMBINE, layer, M, st);   // the block's output, no residual
-    m.moe_only = false;
-    GV_REQUIRE(rc == 0, std::string("gv_model_moe: ") + last_error());
-    GV_CHECK_HIP(hipMemcpyAsync(out, m.x, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToHost, st));
+    GV_CHECK_HIP(hipMemcpyAsync(pf.h, h, static_cast<size_t>(M) * H * 4, hipMemcpyHostToDevice, st));
+    if (router_logits)
+        GV_CHECK_HIP(hipMemcpy2DAsync(pf.logits, static_cast<size_t>(m.E1) * 4, router_logits,
+                                      static_cast<size_t>(E) * 4, static_cast<size_t>(E) * 4, M,
+                                      hipMemcpyHostToDevice, st));
+    GV_REQUIRE(moe_block(m, layer, M, router_logits != nullptr, st) == 0,
+               std::string("gv_model_moe: ") + last_error());
+    pf.M = M;
+    pf.given = router_logits != nullptr;
+    pf.layer = layer;
+    const bool big = M > c.max_rows;
+    GV_CHECK_HIP(hipMemcpyAsync(out, big ? pf.out : m.x, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToHost, st));
     if (ids)
-        GV_CHECK_HIP(hipMemcpyAsync(ids, m.route_ids + static_cast<int64_t>(layer) * c.max_rows * K,
+        GV_CHECK_HIP(hipMemcpyAsync(ids, big ? pf.ids : m.route_ids + static_cast<int64_t>(layer) * c.max_rows * K,
                                     static_cast<size_t>(M) * K * 4, hipMemcpyDeviceToHost, st));
     if (weights)
-        GV_CHECK_HIP(hipMemcpyAsync(weights, m.route[layer].weight, static_cast<size_t>(M) * K * 4,
+        GV_CHECK_HIP(hipMemcpyAsync(weights, big ? pf.w : m.route[layer].weight, static_cast<size_t>(M) * K * 4,
                                     hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
     m.last_n = 0;   // the step's state is this block's, not a verify's
+    return 0;
+}
+
+int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
+    GV_REQUIRE(g && ms_per_block && reps >= 1, "gv_model_moe_replay: bad arguments");
+    Model &m = g->m;
+    GV_REQUIRE(m.pf.M > 0, "gv_model_moe_replay: no gv_model_moe call to replay");
+    const hipStream_t st = stream();
+    if (moe_block(m, m.pf.layer, m.pf.M, m.pf.given, st) != 0) return -1;   // warm
+    hipEvent_t e0, e1;
+    GV_CHECK_HIP(hipEventCreate(&e0));
+    GV_CHECK_HIP(hipEventCreate(&e1));
+    GV_CHECK_HIP(hipEventRecord(e0, st));
+    int rc = 0;
+    for (int i = 0; i < reps && rc == 0; ++i) rc = moe_block(m, m.pf.layer, m.pf.M, m.pf.given, st);
+    GV_CHECK_HIP(hipEventRecord(e1, st));
+    GV_CHECK_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    GV_CHECK_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc != 0) return -1;
+    *ms_per_block = ms / reps;
     return 0;
 }
 

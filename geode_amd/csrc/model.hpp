@@ -66,7 +66,8 @@ struct LayerW {
 
 // The prefill MoE's buffers (C5: many rows), allocated for `cap` rows on first use
 struct Prefill {
-    int cap = 0, M = 0;
+    int cap = 0, M = 0, layer = 0;   // M, layer: the last gv_model_moe call's (for the replay)
+    bool given = false;
     float *h = nullptr, *logits = nullptr, *gate = nullptr, *w = nullptr, *gu = nullptr, *y = nullptr, *out = nullptr;
     int *ids = nullptr, *cnt = nullptr, *start = nullptr, *n_slots = nullptr, *n_picks = nullptr;
     int *slot_expert = nullptr, *slot_start = nullptr, *slot_count = nullptr, *pick_token = nullptr, *pick_of = nullptr;

@@ -164,12 +164,17 @@ int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
  * verify again before trusting the model's state. */
 int gv_model_replay(gv_model *m, int cls, int layer, int reps, float *ms_per_launch);
 
-/* C3: one MoE block of layer `layer` (Model::moe, engine/src/model.cpp:4123-4587; route_topk :4021-4065, combine
- * :4554-4585) on M rows h [M][hidden] fp32 (host), the routed logits given [M][n_experts] (C3) or NULL (the layer's
- * bf16 router); the shared expert's gate from the layer's shared_gate row. out [M][hidden] = the block's output
- * without the residual; ids / weights [M][top_k] (may be NULL). The int8 path. Leaves no verify to keep. */
+/* C3 / C5: one MoE block of layer `layer` (Model::moe, engine/src/model.cpp:4123-4587; route_topk :4021-4065,
+ * combine :4554-4585; the prefill's expert-grouped products :4484-4543) on M rows h [M][hidden] fp32 (host), the
+ * routed logits given [M][n_experts] or NULL (the layer's bf16 router; only for M <= max_rows); the shared
+ * expert's gate from the layer's shared_gate row. M <= max_rows runs the verify step's kernels, more rows (up to
+ * 16384) the prefill path: the picks grouped by expert in runs of at most 32 rows. out [M][hidden] = the block's
+ * output without the residual; ids / weights [M][top_k] (may be NULL). The int8 path. Leaves no verify to keep. */
 int gv_model_moe(gv_model *m, int layer, const float *h, int M, const float *router_logits, float *out,
                  int32_t *ids, float *weights);
+/* Re-run the last gv_model_moe call's block on its device-staged rows and logits reps times back to back and return
+ * the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */
+int gv_model_moe_replay(gv_model *m, int reps, float *ms_per_block);
 
 /* ------------------------------------------------------------------ sampling and acceptance (C2)
  * Rows of logits in device memory (ld floats apart, e.g. gv_model_logits'), uniforms and results on the host.
