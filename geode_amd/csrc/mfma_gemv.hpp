@@ -42,16 +42,12 @@ inline size_t act16_row_bytes(int64_t cols) { return static_cast<size_t>(cols) *
 // engine/src/kernels.cpp:1254-1295, bit for bit) written as hi + lo halves at the group's 32 bytes. The 16-value
 // block is the groups g and g ^ 1, held by lanes l and l ^ 1: every lane of the wave calls this (live = false: a lane
 // past the row's end, which stores nothing).
-__device__ inline void act16_group(const float (&v)[8], int g, bool live, _Float16 *ar) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    if (!live) return;
+// 8 values of a 16-value block with the block's amax into their operands: q x (amax / 127) as hi + lo halves in
+// the slot order (0 4 1 5 2 6 3 7)
+__device__ inline void act16_operands(const float (&v)[8], float amax, h8 &hi, h8 &lo) {
     const float s = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    h8 hi, lo;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {   // slot of value i: (0 4 1 5 2 6 3 7)
+    for (int i = 0; i < 8; ++i) {
         const int q = min(max(static_cast<int>(rintf(__fmul_rn(v[i], qi))), -127), 127);
         const float y = __fmul_rn(static_cast<float>(q), s);
         const int slot = i < 4 ? 2 * i : 2 * (i - 4) + 1;
@@ -60,6 +56,20 @@ __device__ inline void act16_group(const float (&v)[8], int g, bool live, _Float
         hi[slot] = yh;
         lo[slot] = yl;
     }
+}
+
+__device__ inline float amax8(const float (&v)[8]) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
+    return a;
+}
+
+__device__ inline void act16_group(const float (&v)[8], int g, bool live, _Float16 *ar) {
+    const float amax = fmaxf(amax8(v), __shfl_xor(amax8(v), 1, 64));
+    if (!live) return;
+    h8 hi, lo;
+    act16_operands(v, amax, hi, lo);
     h8 *p = reinterpret_cast<h8 *>(ar + static_cast<int64_t>(g) * 16);
     p[0] = hi;
     p[1] = lo;
@@ -194,15 +204,22 @@ __device__ inline h8 decode8(uint32_t w, uint2 sc, uint32_t magic) {
     return __builtin_bit_cast(h8, make_uint4(r[0], r[1], r[2], r[3]));
 }
 
+// the operands of k-group g of an act16 row
+__device__ inline void load_act16(const _Float16 *ar, int64_t g, h8 &hi, h8 &lo) {
+    const _Float16 *p = ar + g * 16;
+    hi = *reinterpret_cast<const h8 *>(p);
+    lo = *reinterpret_cast<const h8 *>(p + 8);
+}
+
 // One workgroup's share of a product: its waves split the K range [sc0, sc0 + waves KW / 4) super-chunks (wave w:
 // chunks [w KW, (w + 1) KW) of it) of row tiles [t0, t1), a tile at a time with the next two tiles' loads in flight;
-// nsc = super-chunks a row. act(j) gives local row j's activation row (act16 layout, whole row; any j < M), put(row,
-// j, v) takes the fp32 sum (before global). part: LDS of (t1 - t0) * waves * NTT KB for the waves' partial sums,
+// nsc = super-chunks a row. bload(j, g, hi, lo) gives local row j's operands of k-group g (any j < M; every lane
+// calls it, j and g uniform in the lane's 16-lane group), put(row, j, v) takes the fp32 sum (before global). part: LDS of (t1 - t0) * waves * NTT KB for the waves' partial sums,
 // added once at the end (waves > 1); tab: LDS for fill_e4m3_table, filled here (every thread of the workgroup calls
 // this) while the first loads are in flight.
-template <int KW, int NTT, typename ActFn, typename PutFn>
+template <int KW, int NTT, typename BFn, typename PutFn>
 __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, int64_t rows,
-                                  int nsc, int sc0, int64_t t0, int64_t t1, int M, ActFn act, PutFn put, f4 *part,
+                                  int nsc, int sc0, int64_t t0, int64_t t1, int M, BFn bload, PutFn put, f4 *part,
                                   uint2 *tab) {
     const int W = blockDim.x / 64;
     const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
@@ -230,13 +247,9 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
         const int j = tt * 16 + lq;
-        const _Float16 *ar = act(j < M ? j : M - 1);
 #pragma unroll
-        for (int c = 0; c < KW; ++c) {
-            const _Float16 *p = ar + ((static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg) * 16;
-            bh[c][tt] = *reinterpret_cast<const h8 *>(p);
-            bl[c][tt] = *reinterpret_cast<const h8 *>(p + 8);
-        }
+        for (int c = 0; c < KW; ++c)
+            bload(j < M ? j : M - 1, (static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg, bh[c][tt], bl[c][tt]);
     }
     fill_e4m3_table(tab);
     __syncthreads();

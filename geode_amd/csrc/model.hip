@@ -397,6 +397,153 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     }
 }
 
+// route_topk (model.cpp:4021-4065) of one row by one wave: softmax over the E experts (max, expf, the sum in index
+// order, divide), the top K by probability with ties to the lower index (a wave max, then ballots), the weights
+// p / (their sum in rank order) to w[0..K), the ids to ids[0..K) (lane 0), the shared expert's gate sigmoid(lg[E])
+// to *gate. p: this wave's E floats of LDS.
+__device__ inline void route_row(const float *__restrict__ lg, int E, int K, float *p, int *ids, float *w,
+                                 float *gate) {
+    const int lane = threadIdx.x & 63;
+    float v[4];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = e < E ? lg[e] : -__builtin_inff();
+        mx = fmaxf(mx, v[i]);
+    }
+    mx = wave_max(mx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E) p[e] = expf(__fsub_rn(v[i], mx));
+    }
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    if (lane == 0) {   // index order, as the reference; 64 values read ahead of their sums
+        int e = 0;
+        for (; e + 64 <= E; e += 64) {
+            float4 v4[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v4[u] = *reinterpret_cast<const float4 *>(&p[e + 4 * u]);
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4[u].x), v4[u].y), v4[u].z), v4[u].w);
+        }
+        for (; e < E; ++e) sum = __fadd_rn(sum, p[e]);
+    }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        pv[i] = e < E ? __fdiv_rn(p[e], sum) : -1.0f;
+    }
+    float top = 0.0f, mine = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const float bv = wave_max(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])));
+        int bi = E;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            const uint64_t hit = __ballot(pv[i] == bv);
+            if (hit) bi = 64 * i + __builtin_ctzll(hit);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (lane + 64 * i == bi) pv[i] = -1.0f;   // taken
+        if (lane == k) mine = bv;
+        if (lane == 0) ids[k] = bi;
+        top = __fadd_rn(top, bv);   // rank order
+    }
+    if (lane < K) w[lane] = __fdiv_rn(mine, top);
+    if (lane == 0 && gate) *gate = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[E])));
+}
+
+// The route of the step's rows (route_row each); then the slots (distinct experts ascending, the shared one last)
+// and their picks ordered by (expert, token, rank), each pick placed by counting, so the order never depends on
+// timing. The whole workgroup (blockDim a multiple of 64, at least 256) calls this; LDS: p [M][256], ids [M][16],
+// cnt / start / slot_of [E + 1], wtot [2][16].
+struct RouteLds {
+    float (*p)[256];
+    int *ids, *cnt, *start, *slot_of;
+    int (*wtot)[16];
+};
+
+__device__ inline void route_all(const float *__restrict__ logits, int E, int K, int M, RouteState *__restrict__ rs,
+                                 int32_t *__restrict__ ids_out, const RouteLds &r) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    const int E1 = E + 1;
+    for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0;
+    for (int t = wave; t < M; t += waves) {
+        route_row(logits + static_cast<int64_t>(t) * E1, E, K, r.p[t], &r.ids[t * 16], rs->weight + t * K,
+                  rs->gate + t);
+        if (lane < K) ids_out[t * K + lane] = r.ids[t * 16 + lane];
+    }
+    __syncthreads();
+    // counts per expert (the shared expert, E, once per row)
+    for (int i = tid; i < M * K; i += blockDim.x) atomicAdd(&r.cnt[r.ids[(i / K) * 16 + i % K]], 1);
+    if (tid == 0) r.cnt[E] = M;
+    __syncthreads();
+    {   // exclusive scans over the E + 1 counters (starts, slot numbers): two a thread, waves, the waves' totals
+        const int e0 = 2 * tid, e1 = e0 + 1;
+        const int c0 = e0 <= E ? r.cnt[e0] : 0, c1 = e1 <= E ? r.cnt[e1] : 0;
+        const int u0 = c0 > 0, u1 = c1 > 0;
+        int ic = c0 + c1, iu = u0 + u1;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
+            if (lane >= o) ic += pc, iu += pu;
+        }
+        if (lane == 63) r.wtot[0][wave] = ic, r.wtot[1][wave] = iu;
+        __syncthreads();
+        int bc = 0, bu = 0;
+        for (int w2 = 0; w2 < wave; ++w2) bc += r.wtot[0][w2], bu += r.wtot[1][w2];
+        const int xc = bc + ic - (c0 + c1), xu = bu + iu - (u0 + u1);   // exclusive, before e0
+        if (e0 <= E) {
+            r.start[e0] = xc;
+            r.slot_of[e0] = u0 ? xu : -1;
+            if (e0 == E) rs->n_slots = xu + u0, rs->n_picks = xc + c0;
+        }
+        if (e1 <= E) {
+            r.start[e1] = xc + c0;
+            r.slot_of[e1] = u1 ? xu + u0 : -1;
+            if (e1 == E) rs->n_slots = xu + u0 + u1, rs->n_picks = xc + c0 + c1;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += blockDim.x)
+        if (r.slot_of[e] >= 0) {
+            rs->slot_expert[r.slot_of[e]] = e;
+            rs->slot_start[r.slot_of[e]] = r.start[e];
+            rs->slot_count[r.slot_of[e]] = r.cnt[e];
+        }
+    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
+    for (int i = tid; i < M * (K + 1); i += blockDim.x) {
+        const int t = i / (K + 1), k = i % (K + 1);
+        const int e = k < K ? r.ids[t * 16 + k] : E;
+        int before = 0;
+        if (k < K) {
+            for (int t2 = 0; t2 < t; ++t2)
+                for (int k2 = 0; k2 < K; ++k2) before += r.ids[t2 * 16 + k2] == e;
+        } else {
+            before = t;
+        }
+        const int pk = r.start[e] + before;
+        rs->pick_token[pk] = t;
+        rs->pick_of[t * (K + 1) + k] = pk;
+    }
+}
+
+// the route alone (rows' logits given after the router: the MoE block entry point)
+__global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ logits, int E, int K,
+                                                    const StepParams *__restrict__ sp, RouteState *__restrict__ rs,
+                                                    int32_t *__restrict__ ids_out) {
+    __shared__ float p[kMaxRows][256];
+    __shared__ int ids[kMaxRows * 16];
+    __shared__ int cnt[257], start[257], slot_of[257];
+    __shared__ int wtot[2][16];
+    route_all(logits, E, K, sp->M, rs, ids_out, RouteLds{p, ids, cnt, start, slot_of, wtot});
+}
+
 // The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A
 // workgroup takes 4 rows of the router ([E + 1][H] bf16, the
 // shared expert's gate row last; one a wave) and the tokens in groups of router_tokens(H). Every load is issued
@@ -406,8 +553,11 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
 // reference's fixed order (bf16_row_dots, kernels.cpp:1446-1483), a lane per (token, partial).
 constexpr int kRouterRows = 4;
 __host__ __device__ inline int router_tokens(int H) { return H <= 2048 ? 8 : 4; }
+// the route's LDS in the router's tail: p [kMaxRows][256], ids [kMaxRows][16], cnt / start / slot_of [257]
+constexpr size_t kRouteLds = (static_cast<size_t>(kMaxRows) * 256 + kMaxRows * 16 + 3 * 260) * 4;
 inline size_t router_lds(int H) {
-    return static_cast<size_t>(router_tokens(H)) * (H + 8) * 4 + static_cast<size_t>(kRouterRows) * H * 4;
+    return std::max(static_cast<size_t>(router_tokens(H)) * (H + 8) * 4 + static_cast<size_t>(kRouterRows) * H * 4,
+                    kRouteLds);
 }
 
 template <int GPT>   // 8-value groups a thread takes per row: 1 for H <= 2048, 2 up to 4096
@@ -415,7 +565,9 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
                                                      const float *__restrict__ x, const float *__restrict__ norm_w,
                                                      float eps, const StepParams *__restrict__ sp,
                                                      float *__restrict__ logits, _Float16 *__restrict__ act,
-                                                     int64_t act_stride) {
+                                                     int64_t act_stride, int route, int E, int K,
+                                                     RouteState *__restrict__ rs, int32_t *__restrict__ ids_out,
+                                                     int *__restrict__ counter) {
     constexpr int TG = GPT == 1 ? 8 : 4;
     extern __shared__ float lds_f[];
     __shared__ double red[4][TG];
@@ -535,132 +687,21 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
         const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
         if (j == 0 && tt < nt) logits[static_cast<int64_t>(t0 + tt) * E1 + ra] = s3;
     }
-}
-
-// route_topk (model.cpp:4021-4065) of one row by one wave: softmax over the E experts (max, expf, the sum in index
-// order, divide), the top K by probability with ties to the lower index (a wave max, then ballots), the weights
-// p / (their sum in rank order) to w[0..K), the ids to ids[0..K) (lane 0), the shared expert's gate sigmoid(lg[E])
-// to *gate. p: this wave's E floats of LDS.
-__device__ inline void route_row(const float *__restrict__ lg, int E, int K, float *p, int *ids, float *w,
-                                 float *gate) {
-    const int lane = threadIdx.x & 63;
-    float v[4];
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        v[i] = e < E ? lg[e] : -__builtin_inff();
-        mx = fmaxf(mx, v[i]);
-    }
-    mx = wave_max(mx);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E) p[e] = expf(__fsub_rn(v[i], mx));
-    }
-    __builtin_amdgcn_wave_barrier();
-    float sum = 0.0f;
-    if (lane == 0) {   // index order, as the reference; 64 values read ahead of their sums
-        int e = 0;
-        for (; e + 64 <= E; e += 64) {
-            float4 v4[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v4[u] = *reinterpret_cast<const float4 *>(&p[e + 4 * u]);
-#pragma unroll
-            for (int u = 0; u < 16; ++u)
-                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4[u].x), v4[u].y), v4[u].z), v4[u].w);
-        }
-        for (; e < E; ++e) sum = __fadd_rn(sum, p[e]);
-    }
-    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
-    float pv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        pv[i] = e < E ? __fdiv_rn(p[e], sum) : -1.0f;
-    }
-    float top = 0.0f, mine = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const float bv = wave_max(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])));
-        int bi = E;
-#pragma unroll
-        for (int i = 3; i >= 0; --i) {
-            const uint64_t hit = __ballot(pv[i] == bv);
-            if (hit) bi = 64 * i + __builtin_ctzll(hit);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (lane + 64 * i == bi) pv[i] = -1.0f;   // taken
-        if (lane == k) mine = bv;
-        if (lane == 0) ids[k] = bi;
-        top = __fadd_rn(top, bv);   // rank order
-    }
-    if (lane < K) w[lane] = __fdiv_rn(mine, top);
-    if (lane == 0 && gate) *gate = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[E])));
-}
-
-// The route of the step's rows (route_row each); then the slots (distinct experts ascending, the shared one last)
-// and their picks ordered by (expert, token, rank), each pick placed by counting, so the order never depends on
-// timing.
-__global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ logits, int E, int K,
-                                                    const StepParams *__restrict__ sp, RouteState *__restrict__ rs,
-                                                    int32_t *__restrict__ ids_out) {
-    __shared__ float p[kMaxRows][256];
-    __shared__ int ids[kMaxRows * 16];
-    __shared__ int cnt[257], start[257], slot_of[257];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const int M = sp->M, E1 = E + 1;
-    for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
-    for (int t = wave; t < M; t += waves) {
-        route_row(logits + static_cast<int64_t>(t) * E1, E, K, p[t], &ids[t * 16], rs->weight + t * K, rs->gate + t);
-        if (lane < K) ids_out[t * K + lane] = ids[t * 16 + lane];
-    }
+    if (!route) return;
+    // the last workgroup to finish routes the rows (the others' logits made visible by their fences)
+    __shared__ int s_last;
+    __shared__ int wtot[2][16];
+    __threadfence();
     __syncthreads();
-    // counts per expert (the shared expert, E, once per row)
-    for (int i = threadIdx.x; i < M * K; i += blockDim.x) atomicAdd(&cnt[ids[(i / K) * 16 + i % K]], 1);
-    if (threadIdx.x == 0) cnt[E] = M;
+    if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == static_cast<int>(gridDim.x) - 1;
     __syncthreads();
-    {   // exclusive scans over the E + 1 counters (starts, slot numbers): waves of 64, then the waves' totals
-        __shared__ int wtot[2][5];
-        const int e = threadIdx.x;
-        const int c = e <= E ? cnt[e] : 0, u = c > 0;
-        int ic = c, iu = u;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
-            if (lane >= o) ic += pc, iu += pu;
-        }
-        if (lane == 63 && wave < 5) wtot[0][wave] = ic, wtot[1][wave] = iu;
-        __syncthreads();
-        if (e <= E) {
-            int bc = 0, bu = 0;
-            for (int w2 = 0; w2 < wave; ++w2) bc += wtot[0][w2], bu += wtot[1][w2];
-            start[e] = bc + ic - c;
-            slot_of[e] = u ? bu + iu - u : -1;
-            if (e == E) rs->n_slots = bu + iu, rs->n_picks = bc + ic;
-        }
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e <= E; e += blockDim.x)
-        if (slot_of[e] >= 0) {
-            rs->slot_expert[slot_of[e]] = e;
-            rs->slot_start[slot_of[e]] = start[e];
-            rs->slot_count[slot_of[e]] = cnt[e];
-        }
-    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
-    for (int i = threadIdx.x; i < M * (K + 1); i += blockDim.x) {
-        const int t = i / (K + 1), k = i % (K + 1);
-        const int e = k < K ? ids[t * 16 + k] : E;
-        int before = 0;
-        if (k < K) {
-            for (int t2 = 0; t2 < t; ++t2)
-                for (int k2 = 0; k2 < K; ++k2) before += ids[t2 * 16 + k2] == e;
-        } else {
-            before = t;
-        }
-        const int pk = start[e] + before;
-        rs->pick_token[pk] = t;
-        rs->pick_of[t * (K + 1) + k] = pk;
-    }
+    if (!s_last) return;
+    __threadfence();
+    if (threadIdx.x == 0) *counter = 0;   // ready for the next launch
+    float(*p)[256] = reinterpret_cast<float(*)[256]>(lds_f);
+    int *ids = reinterpret_cast<int *>(lds_f + kMaxRows * 256);
+    int *cnt = ids + kMaxRows * 16, *start = cnt + 260, *slot_of = start + 260;
+    route_all(logits, E, K, M, rs, ids_out, RouteLds{p, ids, cnt, start, slot_of, wtot});
 }
 
 // The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
@@ -671,8 +712,9 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
                                                         size_t code_stride, size_t scale_stride, int64_t rows, int K,
                                                         const float *__restrict__ globals, int half_rows,
                                                         const _Float16 *__restrict__ act, int64_t act_stride,
-                                                        const Slots sl, float *__restrict__ out,
-                                                        int tiles_per_wg, int E1, int max_picks) {
+                                                        const float *__restrict__ gu, const Slots sl,
+                                                        float *__restrict__ out, int tiles_per_wg, int E1,
+                                                        int max_picks) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
     const int u = blockIdx.x;
@@ -688,9 +730,10 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
         codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
         K / kSuperK, 0, t0, t1,
         cnt,
-        [&](int j) {
+        [&](int j, int64_t g, h8 &hi, h8 &lo) {
+            // UP: the row's act16 operands; DOWN: the pick's SwiGLU operands
             const int64_t src = UP ? sl.pick_token[start + j] : start + j;
-            return act + src * act_stride;
+            load_act16(act + src * act_stride, g, hi, lo);
         },
         [&](int64_t row, int j, float v) {
             const float gl = UP ? (row < half_rows ? g0 : g1) : g2;
@@ -829,7 +872,8 @@ struct MoeArgs {
     int64_t rows, cols;
     const float *globals;
     int F;
-    const _Float16 *act;   // UP: the rows' operands, by pick_token; DOWN: the picks' (SwiGLU) operands, by pick
+    const _Float16 *act;   // UP: the rows' operands, by pick_token
+    const float *gu;       // DOWN: the picks' gate|up products (their SwiGLU quantized on the fly)
     Slots sl;
     float *out;            // [pick][rows]
     int slots;             // a bound on the slot count (the grid)
@@ -848,7 +892,7 @@ int launch_moe_raw(const MoeArgs &a, int waves, hipStream_t st) {
         return -1;
     hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(a.slots, tiles), dim3(64 * waves), lds, st, a.codes,
                        a.scales, a.code_stride, a.scale_stride, a.rows, static_cast<int>(a.cols), a.globals, a.F, a.act,
-                       act_halves(a.cols), a.sl, a.out, per, a.E1, a.max_picks);
+                       act_halves(a.cols), a.gu, a.sl, a.out, per, a.E1, a.max_picks);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -865,8 +909,8 @@ int moe_launch(const MoeArgs &a, int ntt, int kw, int waves, hipStream_t st) {
 }
 
 // the experts' products of layer L: gate|up (up) or down, over slots of at most `rows_max` rows each
-int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float16 *act, const Slots &sl, float *out,
-            int slots, int max_picks, hipStream_t st) {
+int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float16 *act, const float *gu,
+            const Slots &sl, float *out, int slots, int max_picks, hipStream_t st) {
     const int64_t H = m.c.hidden, F = m.c.moe_ff;
     const int ntt = rows_max <= 16 ? 1 : 2;
     int waves, kw;
@@ -880,6 +924,7 @@ int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float
               L.expert_globals,
               static_cast<int>(F),
               act,
+              gu,
               sl,
               out,
               slots,
@@ -889,7 +934,7 @@ int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float
 }
 
 int moe_products(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
-    return moe_run(m, L, up, M, up ? m.act_h : m.act_m, route_slots(m.route + (&L - &m.layers[0])),
+    return moe_run(m, L, up, M, up ? m.act_h : m.act_m, m.gu_out, route_slots(m.route + (&L - &m.layers[0])),
                    up ? m.gu_out : m.y, moe_slots(m, M), m.max_picks, st);
 }
 
@@ -1081,12 +1126,16 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
-                               m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+                               m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
+                               m.route_in_router ? 1 : 0, c.n_experts, c.top_k, m.route + l,
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
-                               m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH);
+                               m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
+                               m.route_in_router ? 1 : 0, c.n_experts, c.top_k, m.route + l,
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter);
         }
         return 0;
     }
@@ -1117,7 +1166,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     }
 }
 
-constexpr int kLayerClasses[] = {GV_K_QKV,    GV_K_ROPE,   GV_K_ATTN,   GV_K_MERGE,     GV_K_O,      GV_K_ROUTER,
+constexpr int kLayerClasses[] = {GV_K_QKV,    GV_K_ROPE,  GV_K_ATTN,   GV_K_MERGE,  GV_K_O,       GV_K_ROUTER,
                                  GV_K_ROUTE,  GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN, GV_K_COMBINE};
 
 int run_layers(Model &m, int M, hipStream_t st) {
@@ -1195,10 +1244,10 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     GV_CHECK_HIP(hipGetLastError());
     const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks};
     const int picks = M * (K + 1);
-    if (moe_run(m, L, true, 32, pf.act, sl, pf.gu, pf.max_slots, picks, st) != 0) return -1;
+    if (moe_run(m, L, true, 32, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st) != 0) return -1;
     hipLaunchKernelGGL(swiglu_quant_kernel, dim3(picks), dim3(256), static_cast<size_t>(F) * 4, st, pf.gu, F,
                        pf.n_picks, pf.act_m);
-    if (moe_run(m, L, false, 32, pf.act_m, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
+    if (moe_run(m, L, false, 32, pf.act_m, pf.gu, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
     GV_CHECK_HIP(hipMemsetAsync(pf.out, 0, static_cast<size_t>(M) * H * 4, st));
     hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M,
                        pf.out, nullptr, 0.0f, nullptr, 0);
@@ -1337,6 +1386,8 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     m.kv_blocks = (c.max_ctx + kAttnBlock - 1) / kAttnBlock;
     ok = ok && (m.sp = static_cast<StepParams *>(dalloc(m, sizeof(StepParams))));
     ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * c.n_layers)));
+    ok = ok && (m.counter = static_cast<int *>(dalloc(m, 64)));
+    ok = ok && hipMemset(m.counter, 0, 64) == hipSuccess;
     ok = ok && (m.x = static_cast<float *>(dalloc(m, Mx * H * 4)));
     ok = ok && (m.qkv_out = static_cast<float *>(dalloc(m, Mx * qkv_rows(c) * 4)));
     ok = ok && (m.q16 = static_cast<_Float16 *>(dalloc(m, 2 * Mx * nh * hd * 2)));

@@ -100,6 +100,8 @@ struct Model {
     int pos = 0, last_pos = 0, last_n = 0;
     int timed_class = -1;
     bool moe_only = false;   // gv_model_moe: the router takes the rows as they are, the combine no next norm
+    bool route_in_router = false;  // the router's last workgroup routes (off: route_kernel; on measured slower)
+    int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
     Prefill pf;
     std::vector<hipEvent_t> events;   // pairs around the timed class's launches
     size_t events_used = 0;

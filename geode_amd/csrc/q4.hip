@@ -229,7 +229,8 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     if (t0 >= ntiles) return;
     mfma_tiles<KW, NTT>(
         w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, t0, t1, M,
-        [&](int j) { return act + j * act_stride; }, [&](int64_t row, int j, float v) { out.put(row, j, v); },
+        [&](int j, int64_t g, h8 &hi, h8 &lo) { load_act16(act + j * act_stride, g, hi, lo); },
+        [&](int64_t row, int j, float v) { out.put(row, j, v); },
         part_lds, tab);
 }
 
