@@ -242,6 +242,14 @@ def main():
         step()
     e1 = g.lib.gv_event_record()
     ms = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+    # the same steps as plain launches (no graph), for comparison
+    m.set_graphs(False)
+    e0 = g.lib.gv_event_record()
+    for _ in range(args.steps):
+        step()
+    e1 = g.lib.gv_event_record()
+    ms_direct = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+    m.set_graphs(True)
 
     # acceptance of the last step's logits: greedy sample-and-match (engine/src/geode.cpp:331-350)
     m.position = CTX
@@ -308,6 +316,7 @@ def main():
                    "rows": M, "tokens_emitted_per_step": emitted, "acceptance": "greedy sample-and-match on the "
                    "step's logits; drafts = the target's own greedy chain" if not args.tree else "greedy tree walk"},
         "verify_steps_per_s": steps_s,
+        "ms_per_step_without_graphs": ms_direct,
         "verified_rows_per_s": steps_s * M,
         "step_hbm_gbs": sbytes / (ms / 1e3) / 1e9,
         "step_roofline_frac": sbytes / (ms / 1e3) / PEAK_HBM,

@@ -71,6 +71,7 @@ SIGNATURES = {
     "gv_model_time_kernel": (_c.c_int, [_P, _c.c_int]),
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
+    "gv_model_set_graphs": (_c.c_int, [_P, _c.c_int]),
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
@@ -323,6 +324,10 @@ class VerifyModel:
         ms, n = _c.c_float(0), _c.c_int(0)
         check(_lib().gv_model_kernel_time(self.h, _c.byref(ms), _c.byref(n)), "gv_model_kernel_time")
         return ms.value, n.value
+
+    def set_graphs(self, on):
+        """the verify step as one HIP graph per row count (default) or plain launches"""
+        check(_lib().gv_model_set_graphs(self.h, 1 if on else 0), "gv_model_set_graphs")
 
     def replay(self, cls, layer=0, reps=20):
         """mean ms of kernel class cls of one layer, launched reps times back to back on the last verify's state"""

@@ -1179,6 +1179,32 @@ int run_layers(Model &m, int M, hipStream_t st) {
     return 0;
 }
 
+// the verify step's launches: replayed from the row count's graph when there is one (captured on the second step of
+// that row count, so the first runs the launches directly and sets every kernel's attributes)
+int run_step(Model &m, int M, hipStream_t st) {
+    if (!m.use_graphs || m.timed_class >= 0 || !m.seen[M]) {
+        m.seen[M] = true;
+        return run_layers(m, M, st);
+    }
+    hipGraphExec_t &ge = m.graphs[M];
+    if (!ge) {
+        hipGraph_t graph = nullptr;
+        GV_CHECK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        const int rc = run_layers(m, M, st);
+        const hipError_t e = hipStreamEndCapture(st, &graph);
+        if (rc != 0 || e != hipSuccess || !graph) {
+            if (graph) (void)hipGraphDestroy(graph);
+            set_error(std::string("verify: graph capture failed: ") + (rc != 0 ? last_error() : hipGetErrorString(e)));
+            return -1;
+        }
+        const hipError_t ie = hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        GV_REQUIRE(ie == hipSuccess, std::string("verify: graph instantiate failed: ") + hipGetErrorString(ie));
+    }
+    GV_CHECK_HIP(hipGraphLaunch(ge, st));
+    return 0;
+}
+
 // the prefill buffers for M rows (kept for later calls; regrown when M is larger)
 int prefill_alloc(Model &m, int M) {
     Prefill &pf = m.pf;
@@ -1431,6 +1457,8 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
 void gv_model_free(gv_model *g) {
     if (!g) return;
     (void)hipStreamSynchronize(stream());
+    for (auto &ge : g->m.graphs)
+        if (ge) (void)hipGraphExecDestroy(ge);
     for (void *p : g->m.allocs) (void)hipFree(p);
     for (void *p : g->m.pf.allocs) (void)hipFree(p);
     delete g;
@@ -1668,7 +1696,7 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     }
     hipStream_t st = stream();
     GV_CHECK_HIP(hipMemcpyAsync(m.sp, &sp, sizeof sp, hipMemcpyHostToDevice, st));
-    if (run_layers(m, n, st) != 0) return -1;
+    if (run_step(m, n, st) != 0) return -1;
     if (logits) {
         GV_CHECK_HIP(hipMemcpyAsync(logits, m.logits, static_cast<size_t>(n) * c.vocab * 4, hipMemcpyDeviceToHost, st));
         GV_CHECK_HIP(hipStreamSynchronize(st));
@@ -1829,6 +1857,12 @@ int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
     (void)hipEventDestroy(e1);
     if (rc != 0) return -1;
     *ms_per_block = ms / reps;
+    return 0;
+}
+
+int gv_model_set_graphs(gv_model *g, int on) {
+    GV_REQUIRE(g, "gv_model_set_graphs: null model");
+    g->m.use_graphs = on != 0;
     return 0;
 }
 

@@ -104,6 +104,11 @@ struct Model {
     int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
     Prefill pf;
     std::vector<hipEvent_t> events;   // pairs around the timed class's launches
+    // the verify step as a HIP graph per row count (captured on its second use; the step's parameters are read
+    // from device memory, so one graph serves every position, token set and tree)
+    bool use_graphs = true;
+    hipGraphExec_t graphs[kMaxRows + 1] = {};
+    bool seen[kMaxRows + 1] = {};
     size_t events_used = 0;
     StepParams host_sp{};
     int max_slots = 0, max_picks = 0;

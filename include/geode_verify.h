@@ -156,6 +156,9 @@ enum {
 /* From now on, every launch of kernel class cls is bracketed by events on the library's stream (cls < 0: off);
  * gv_model_kernel_time waits and returns their summed milliseconds and launches since (no reference counterpart:
  * the reference's per-kernel timing is GEODE_GPU8_PROF, engine/src/gpu8.cpp:195). */
+/* The verify step runs as one HIP graph per row count (captured on the second step of that count and replayed
+ * after; every step parameter lives in device memory). on = 0: plain launches (no reference counterpart). */
+int gv_model_set_graphs(gv_model *m, int on);
 int gv_model_time_kernel(gv_model *m, int cls);
 int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
 /* Launch kernel class cls of layer `layer` (ignored for GV_K_EMBED / GV_K_LM_HEAD) reps times back to back on the

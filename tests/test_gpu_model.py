@@ -155,3 +155,25 @@ def test_moe_prefill(models, M):
     assert np.array_equal(gids, wids)
     assert np.abs(gwts - wwts).max() <= 1e-6
     assert rel_err(got, want) <= 1e-2, f"max error {rel_err(got, want):.3e}"
+
+
+def test_graph_replays_match_direct_launches(models):
+    """the step's HIP graph (captured on the second step of a row count) replayed several times, with direct steps
+    and other row counts in between: every replay's logits and routing equal the direct launches' bit for bit"""
+    om, gm = models
+    toks = np.array([21, 22, 23, 24, 25], np.int32)
+
+    def step(n, graphs):
+        gm.set_graphs(graphs)
+        gm.position = CTX
+        lg = gm.verify(toks[:n])
+        return lg, gm.route_ids(n)
+
+    want, wids = step(5, False)
+    for rep in range(4):
+        got, ids = step(5, True)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}"
+        assert np.array_equal(ids, wids)
+        other, _ = step(2, rep % 2 == 0)   # another row count, graphs on and off, between the replays
+        assert np.array_equal(other.view(np.uint32), step(2, False)[0].view(np.uint32))
+    gm.set_graphs(True)
