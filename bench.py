@@ -26,6 +26,11 @@ C4 = dict(hidden=2048, vocab=151936, n_layers=40, n_experts=256, top_k=8, moe_ff
 CTX = 8192
 SEED = 20261201
 PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s
+COPY_BYTES = 256 << 20
+# HBM bytes a launch of the dominant kernel moves, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes (KiB a dispatch)
+# scaled by what the same counters read for a copy of known size (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000); the
+# commands and figures are in profiles/moe_up_c4_m5_traffic.md
+PROFILED_TRAFFIC = {"moe_up": (22444.5 * 2.000 + 180.0 * 1.000) * 1024}
 Q4_ROW = lambda cols: cols // 16 * 9   # noqa: E731  bytes of a q4 row (engine/src/kernels.cpp:900-902)
 
 
@@ -165,6 +170,25 @@ def bench_c2(g, trials):
     return res
 
 
+def calibrate_copy(args):
+    """a device-to-device vector copy of COPY_BYTES, three times: a kernel whose HBM traffic is known (COPY_BYTES read
+    and COPY_BYTES written per launch), for scaling the FETCH_SIZE / WRITE_SIZE counters of a profile"""
+    import geode_amd as g
+
+    g.init(0)
+    src, dst = g.lib.gv_malloc(COPY_BYTES), g.lib.gv_malloc(COPY_BYTES)
+    g.check(g.lib.gv_memset(src, 1, COPY_BYTES))
+    g.check(g.lib.gv_synchronize())
+    e0 = g.lib.gv_event_record()
+    for _ in range(3):
+        g.check(g.lib.gv_memcpy_d2d(dst, src, COPY_BYTES))
+    e1 = g.lib.gv_event_record()
+    ms = g.lib.gv_event_elapsed_ms(e0, e1) / 3
+    g.lib.gv_free(src)
+    g.lib.gv_free(dst)
+    print(json.dumps({"copy_bytes": COPY_BYTES, "ms_per_copy": ms, "gbs": 2 * COPY_BYTES / ms / 1e6}))
+
+
 def main_config(args):
     import geode_amd as g
 
@@ -198,6 +222,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--tree", action="store_true", help="verify the 17-row draft tree instead of the k=4 chain")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only a 256 MiB device copy, three times: the known traffic that scales HBM byte counters")
     ap.add_argument("--config", choices=["c4", "c2", "c3", "c5"], default="c4",
                     help="c4 (default): the verify step; c2 / c3 / c5: the acceptance rules / one MoE block")
     args = ap.parse_args()
@@ -205,6 +231,9 @@ def main():
         print("bench.py measures the verify step on one GPU only: the step of one sequence does not shard "
               "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args)
+        return
     if args.config != "c4":
         main_config(args)
         return
@@ -323,7 +352,7 @@ def main():
         "step_bytes": sbytes,
         "distinct_experts_per_layer": float(np.mean(uniq)),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": PROFILED_TRAFFIC.get(dom),
                      "bytes_per_launch": dom_bytes, "avg_launch_us": dom_avg_s * 1e6,
                      "timing": "hipEvents around 10 back-to-back launches per layer (gv_model_replay), mean over "
                                "the layers"},

@@ -133,6 +133,8 @@ int gv_memcpy_d2h(void *dst, const void *src, size_t bytes) {
 
 int gv_memcpy_d2d(void *dst, const void *src, size_t bytes) {
     if (ensure_init() != 0) return -1;
+    if (bytes % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0)
+        return copy16(src, static_cast<int64_t>(bytes / 16), dst, stream());   // a vector copy kernel
     GV_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream()));
     return 0;
 }

@@ -62,6 +62,7 @@ int ensure_init();
 
 // elementwise helpers (misc.hip)
 int f16_to_f32(const uint16_t *x, int64_t n, float *y, hipStream_t st);
+int copy16(const void *src, int64_t n16, void *dst, hipStream_t st);   // n16 16-byte words, both 16-byte aligned
 int swiglu(const float *g, const float *u, int64_t n, float *m, hipStream_t st);
 int fill_normal(uint64_t seed, int64_t n, float sigma, float *out, hipStream_t st);
 

@@ -1,5 +1,6 @@
 // misc.hip - small elementwise kernels: fp16 widening, the seeded normal generator used for device-side synthetic
 // weights, and the run-time error state.
+#include <algorithm>
 #include <string>
 
 #include "common.hpp"
@@ -20,6 +21,20 @@ __global__ void f16_to_f32_kernel(const uint16_t *__restrict__ x, int64_t n, flo
 
 int f16_to_f32(const uint16_t *x, int64_t n, float *y, hipStream_t st) {
     hipLaunchKernelGGL(f16_to_f32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+    GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+// a plain 16-byte vector copy (device to device); its known traffic also scales the HBM byte counters
+__global__ void copy16_kernel(const uint4 *__restrict__ src, int64_t n, uint4 *__restrict__ dst) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+int copy16(const void *src, int64_t n16, void *dst, hipStream_t st) {
+    const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 256 * 16);
+    hipLaunchKernelGGL(copy16_kernel, dim3(static_cast<unsigned>(std::max<int64_t>(blocks, 1))), dim3(256), 0, st,
+                       static_cast<const uint4 *>(src), n16, static_cast<uint4 *>(dst));
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
