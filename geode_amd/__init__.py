@@ -72,6 +72,10 @@ SIGNATURES = {
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
     "gv_model_set_graphs": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_set_step_kernel": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_step_kernel_supported": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_step_trace": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_step_trace_read": (_c.c_int64, [_P, _P, _c.c_int64]),
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
@@ -328,6 +332,25 @@ class VerifyModel:
     def set_graphs(self, on):
         """the verify step as one HIP graph per row count (default) or plain launches"""
         check(_lib().gv_model_set_graphs(self.h, 1 if on else 0), "gv_model_set_graphs")
+
+    def set_step_kernel(self, on):
+        """on: the verify step as one persistent kernel where the shapes fit it; off: the per-phase kernels"""
+        check(_lib().gv_model_set_step_kernel(self.h, 1 if on else 0), "gv_model_set_step_kernel")
+
+    def step_kernel_supported(self, n):
+        return bool(_lib().gv_model_step_kernel_supported(self.h, int(n)))
+
+    def step_trace(self, on):
+        """the step kernel's barrier clock stamps on or off"""
+        check(_lib().gv_model_step_trace(self.h, 1 if on else 0), "gv_model_step_trace")
+
+    def step_trace_read(self, n_wg, n_barriers):
+        """the last step's stamps [workgroup][barrier][arrive, leave] in 10 ns ticks"""
+        out = np.zeros(n_wg * n_barriers * 2, np.uint64)
+        k = _lib().gv_model_step_trace_read(self.h, out.ctypes.data, out.size)
+        if k < 0:
+            check(-1, "gv_model_step_trace_read")
+        return out.reshape(n_wg, n_barriers, 2)
 
     def replay(self, cls, layer=0, reps=20):
         """mean ms of kernel class cls of one layer, launched reps times back to back on the last verify's state"""

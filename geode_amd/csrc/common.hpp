@@ -60,6 +60,34 @@ inline size_t q4_scale_bytes(int64_t rows, int64_t cols) { return static_cast<si
 inline size_t act_bytes(int64_t cols) { return static_cast<size_t>(cols) * 4; }
 __host__ __device__ inline int64_t act_halves(int64_t cols) { return cols * 2; }
 
+// ---------------------------------------------------------------- device-coherent memory operations
+// Buffer instructions with the sc1 cache policy (gfx940+: device scope, the policy of an agent-scope atomic load or
+// store), coherent across the XCDs' separate L2 caches without a cache maintenance operation: how the persistent
+// step kernel's workgroups exchange data within one launch. `base` must be uniform across the wave; offsets in bytes.
+typedef uint32_t xu4 __attribute__((ext_vector_type(4)));
+typedef uint32_t xu2 __attribute__((ext_vector_type(2)));
+constexpr int kSc1 = 16;
+// a buffer descriptor of `bytes` from a base the whole wave shares (read from lane 0: the descriptor lives in scalar
+// registers, never in a per-lane loop over distinct values)
+__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32));
+    void *p = reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), static_cast<int>(bytes), 0x00020000);
+}
+__device__ inline __amdgpu_buffer_rsrc_t xrs(const void *base) { return uniform_rsrc(base, 0x7FFFFFFFu); }
+__device__ inline xu4 xld16(const void *base, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(xrs(base), off, 0, kSc1); }
+__device__ inline void xst16(const void *base, uint32_t off, xu4 v) { __builtin_amdgcn_raw_buffer_store_b128(v, xrs(base), off, 0, kSc1); }
+__device__ inline float xldf(const float *base, uint32_t i) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs(base), i * 4u, 0, kSc1));
+}
+__device__ inline void xstf(float *base, uint32_t i, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), xrs(base), i * 4u, 0, kSc1);
+}
+__device__ inline float4 xld4f(const float *base, uint32_t i) { return __builtin_bit_cast(float4, xld16(base, i * 4u)); }   // i % 4 == 0
+__device__ inline void xst4f(float *base, uint32_t i, float4 v) { xst16(base, i * 4u, __builtin_bit_cast(xu4, v)); }
+
 // ---------------------------------------------------------------- device helpers
 __device__ inline float e4m3_to_f32(uint32_t b) {
     // E4M3FN as half bits: exponent and mantissa moved into place, then 2^8 for the bias (15 - 7); exact for every
@@ -84,6 +112,14 @@ __device__ inline void split_f16(float y, _Float16 &hi, _Float16 &lo) {
     lo = static_cast<_Float16>(y - static_cast<float>(hi));
 }
 
+// y rounded to fp16 from its fp32 value: when y is a product, two roundings (fp32, then fp16), as the reference's
+// fp32 result stored to an fp16 cache. The empty asm keeps the compiler from folding the product into the
+// conversion (v_fma_mixlo_f16, one rounding), which it does in some kernels and not in others.
+__device__ inline _Float16 f16_of(float y) {
+    asm volatile("" : "+v"(y));
+    return static_cast<_Float16>(y);
+}
+
 // DPP lane moves within 16-lane rows (quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror = 0x141,
 // row_mirror = 0x140): full-rate VALU, no LDS crossbar round trip
 template <int CTRL>
@@ -100,20 +136,27 @@ __device__ inline double dpp_d(double v) {
     return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// the sum over the wave's 64 lanes, the same bits in every lane: pairs, quads, 8s and 16s of lanes in rows, then the
-// rows' sums (0 + 16) + (32 + 48)
+// The wave reductions: pairs, quads, 8s and 16s of lanes within each 16-lane row by DPP (every lane then holds its
+// row's value), then the rows combined as (row 0 + row 1) + (row 2 + row 3) through lane swaps (xor 16, xor 32), in
+// vector registers throughout; the same bits in every lane (the swapped operand order gives the same sum)
 __device__ inline double wave_sum(double v) {
     v += dpp_d<0xB1>(v);
     v += dpp_d<0x4E>(v);
     v += dpp_d<0x141>(v);
     v += dpp_d<0x140>(v);
-    auto lane_d = [&](int l) {
-        const uint64_t u = __builtin_bit_cast(uint64_t, v);
-        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), l);
-        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), l);
-        return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
-    };
-    return (lane_d(0) + lane_d(16)) + (lane_d(32) + lane_d(48));
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ inline float wave_sum_f(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
 }
 
 // the maximum over the wave's 64 lanes, in every lane (a uniform value)
@@ -122,8 +165,9 @@ __device__ inline float wave_max(float v) {
     v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v));
     v = fmaxf(v, dpp_f<0x140>(v));
-    auto lane_f = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
-    return fmaxf(fmaxf(lane_f(0), lane_f(16)), fmaxf(lane_f(32), lane_f(48)));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
 }
 
 }  // namespace gv

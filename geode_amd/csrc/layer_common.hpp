@@ -1,0 +1,181 @@
+// layer_common.hpp - device code shared by the per-phase kernels (model.hip) and the persistent step kernel
+// (step.hip): the KV cache layout, the route of the step's rows.
+#pragma once
+
+#include "model.hpp"
+
+namespace gv {
+
+// The device KV cache of one layer: K [nkv][slots][hd] and V [nkv][slots / 64][hd][64] in fp16 (V transposed in
+// blocks of kAttnBlock positions, so that the MFMA operands of both products are contiguous loads).
+__device__ __host__ inline int64_t k_index(int64_t slots, int hd, int kh, int64_t slot, int d) {
+    return (static_cast<int64_t>(kh) * slots + slot) * hd + d;
+}
+__device__ __host__ inline int64_t v_index(int64_t slots, int hd, int nkv, int kh, int64_t slot, int d) {
+    return static_cast<int64_t>(nkv) * slots * hd +
+           ((static_cast<int64_t>(kh) * (slots / kAttnBlock) + slot / kAttnBlock) * hd + d) * kAttnBlock + slot % kAttnBlock;
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__host__ __device__ inline int attn_k_ld(int hd) { return hd + 8; }   // halves a staged key row (bank spread)
+constexpr int kAttnVld = kAttnBlock + 8;                              // halves a staged value row
+inline size_t attn_lds(int hd) { return (static_cast<size_t>(kAttnBlock) * attn_k_ld(hd) + hd * kAttnVld) * 2; }
+
+// route_topk (model.cpp:4021-4065) of NR rows by one wave, the rows' dependency chains interleaved: softmax over the
+// E <= 256 experts (max, expf, the sum, divide), the top K by probability with ties to the lower index (a wave max,
+// then ballots), the weights p / (their sum in rank order) to w[r][0..K), the ids to ids[r][0..K) (lane 0), the
+// shared expert's gate sigmoid(lg[E]) to gate[r]. The softmax denominator is a fixed tree (each lane's four values,
+// then the lanes: wave_sum_f), not the reference's index-order loop: the probabilities differ from it by an ulp or
+// so, their order (the picks) not at all. live[r] false: row r is skipped (its outputs untouched).
+template <int NR>
+__device__ inline void route_rows(const float *const (&lg)[NR], const bool (&live)[NR], int E, int K,
+                                  int *const (&ids)[NR], float *const (&w)[NR], float *const (&gate)[NR]) {
+    const int lane = threadIdx.x & 63;
+    float pv[NR][4], sum[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        float v[4];
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            v[i] = live[r] && e < E ? lg[r][e] : -__builtin_inff();
+            mx = fmaxf(mx, v[i]);
+        }
+        mx = wave_max(mx);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            pv[r][i] = live[r] && e < E ? expf(__fsub_rn(v[i], mx)) : 0.0f;
+        }
+        sum[r] = wave_sum_f(__fadd_rn(__fadd_rn(pv[r][0], pv[r][1]), __fadd_rn(pv[r][2], pv[r][3])));
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            pv[r][i] = live[r] && e < E ? __fdiv_rn(pv[r][i], sum[r]) : -1.0f;
+        }
+    float top[NR], mine[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) top[r] = mine[r] = 0.0f;
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const float bv = wave_max(fmaxf(fmaxf(pv[r][0], pv[r][1]), fmaxf(pv[r][2], pv[r][3])));
+            int bi = E;
+#pragma unroll
+            for (int i = 3; i >= 0; --i) {
+                const uint64_t hit = __ballot(pv[r][i] == bv);
+                if (hit) bi = 64 * i + __builtin_ctzll(hit);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (lane + 64 * i == bi) pv[r][i] = -1.0f;   // taken
+            if (lane == k) mine[r] = bv;
+            if (lane == 0 && live[r]) ids[r][k] = bi;
+            top[r] = __fadd_rn(top[r], bv);   // rank order
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (!live[r]) continue;
+        if (lane < K) w[r][lane] = __fdiv_rn(mine[r], top[r]);
+        if (lane == 0) *gate[r] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[r][E])));
+    }
+}
+
+// one row (route_rows of a single row)
+__device__ inline void route_row(const float *__restrict__ lg, int E, int K, int *ids, float *w, float *gate) {
+    const float *const l1[1] = {lg};
+    const bool live[1] = {true};
+    int *const i1[1] = {ids};
+    float *const w1[1] = {w};
+    float *const g1[1] = {gate};
+    route_rows<1>(l1, live, E, K, i1, w1, g1);
+}
+
+// The route of the step's rows (route_rows, two rows a wave); then the slots (distinct experts ascending, the shared
+// one last, index E) and their picks ordered by (expert, token, rank), each pick placed by counting (the rows before
+// it that picked the same expert: a bit mask per expert), so the order never depends on timing. The whole workgroup
+// (blockDim a multiple of 64, at least 256) calls this; LDS: ids [M][16], cnt / start / slot_of / rows [E + 1],
+// wtot [2][16].
+struct RouteLds {
+    int *ids, *cnt, *start, *slot_of;
+    unsigned *rows;
+    int (*wtot)[16];
+};
+
+__device__ inline void route_all(const float *__restrict__ logits, int E, int K, int M, RouteState *__restrict__ rs,
+                                 int32_t *__restrict__ ids_out, const RouteLds &r) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    const int E1 = E + 1;
+    for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
+    for (int t0 = wave; t0 < M; t0 += 2 * waves) {   // rows t0 and t0 + waves
+        const int t1 = t0 + waves;
+        const bool l1 = t1 < M;
+        const int t1c = l1 ? t1 : t0;
+        const float *const lg[2] = {logits + static_cast<int64_t>(t0) * E1, logits + static_cast<int64_t>(t1c) * E1};
+        const bool live[2] = {true, l1};
+        int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
+        float *const w[2] = {rs->weight + t0 * K, rs->weight + t1c * K};
+        float *const gate[2] = {rs->gate + t0, rs->gate + t1c};
+        route_rows<2>(lg, live, E, K, ids, w, gate);
+    }
+    __syncthreads();
+    for (int i = tid; i < M * K; i += blockDim.x) {
+        const int t = i / K, e = r.ids[t * 16 + i % K];
+        ids_out[i] = e;
+        atomicAdd(&r.cnt[e], 1);
+        atomicOr(&r.rows[e], 1u << t);
+    }
+    if (tid == 0) r.cnt[E] = M;
+    __syncthreads();
+    {   // exclusive scans over the E + 1 counters (starts, slot numbers): two a thread, waves, the waves' totals
+        const int e0 = 2 * tid, e1 = e0 + 1;
+        const int c0 = e0 <= E ? r.cnt[e0] : 0, c1 = e1 <= E ? r.cnt[e1] : 0;
+        const int u0 = c0 > 0, u1 = c1 > 0;
+        int ic = c0 + c1, iu = u0 + u1;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
+            if (lane >= o) ic += pc, iu += pu;
+        }
+        if (lane == 63) r.wtot[0][wave] = ic, r.wtot[1][wave] = iu;
+        __syncthreads();
+        int bc = 0, bu = 0;
+        for (int w2 = 0; w2 < wave; ++w2) bc += r.wtot[0][w2], bu += r.wtot[1][w2];
+        const int xc = bc + ic - (c0 + c1), xu = bu + iu - (u0 + u1);   // exclusive, before e0
+        if (e0 <= E) {
+            r.start[e0] = xc;
+            r.slot_of[e0] = u0 ? xu : -1;
+            if (e0 == E) rs->n_slots = xu + u0, rs->n_picks = xc + c0;
+        }
+        if (e1 <= E) {
+            r.start[e1] = xc + c0;
+            r.slot_of[e1] = u1 ? xu + u0 : -1;
+            if (e1 == E) rs->n_slots = xu + u0 + u1, rs->n_picks = xc + c0 + c1;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += blockDim.x)
+        if (r.slot_of[e] >= 0) {
+            rs->slot_expert[r.slot_of[e]] = e;
+            rs->slot_start[r.slot_of[e]] = r.start[e];
+            rs->slot_count[r.slot_of[e]] = r.cnt[e];
+        }
+    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
+    for (int i = tid; i < M * (K + 1); i += blockDim.x) {
+        const int t = i / (K + 1), k = i % (K + 1);
+        const int e = k < K ? r.ids[t * 16 + k] : E;
+        const int before = k < K ? __popc(r.rows[e] & ((1u << t) - 1u)) : t;
+        const int pk = r.start[e] + before;
+        rs->pick_token[pk] = t;
+        rs->pick_of[t * (K + 1) + k] = pk;
+    }
+}
+
+}  // namespace gv

@@ -65,21 +65,40 @@ __device__ inline float amax8(const float (&v)[8]) {
     return a;
 }
 
-__device__ inline void act16_group(const float (&v)[8], int g, bool live, _Float16 *ar) {
-    const float amax = fmaxf(amax8(v), __shfl_xor(amax8(v), 1, 64));
+// Where a row's operands go: device memory (a pointer), or a row of a device-coherent exchange buffer (XDst: the
+// buffer's uniform base and the row's byte offset in it)
+struct XDst {
+    const void *base;
+    uint32_t bytes;   // the buffer's size: the descriptor's range
+    uint32_t off;
+};
+__device__ inline void act16_store(_Float16 *ar, int g, bool live, const h8 &hi, const h8 &lo) {
     if (!live) return;
-    h8 hi, lo;
-    act16_operands(v, amax, hi, lo);
     h8 *p = reinterpret_cast<h8 *>(ar + static_cast<int64_t>(g) * 16);
     p[0] = hi;
     p[1] = lo;
+}
+__device__ inline void act16_store(XDst d, int g, bool live, const h8 &hi, const h8 &lo) {
+    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(d.base, d.bytes);
+    const uint32_t off = live ? d.off + static_cast<uint32_t>(g) * 32u : 0xFFFFF000u;   // past the buffer (under 2 GB): dropped
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(xu4, hi), r, off, 0, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(xu4, lo), r, off + 16u, 0, kSc1);
+}
+
+template <typename Dst>
+__device__ inline void act16_group(const float (&v)[8], int g, bool live, Dst ar) {
+    const float amax = fmaxf(amax8(v), __shfl_xor(amax8(v), 1, 64));
+    h8 hi, lo;
+    act16_operands(v, amax, hi, lo);
+    act16_store(ar, g, live, hi, lo);
 }
 
 // A row of cols (a multiple of 16, at most 32 blockDim) values, held in registers, into its operands: thread i has
 // the 8-value groups i, i + blockDim, ... (up to 4; zeros past the row), optionally RMSNorm(1 + w) first (rmsnorm's
 // arithmetic, engine/src/kernels.cpp:1520-1529: the double sum of squares, inv = 1 / sqrt(float(ss / n) + eps), x inv
 // (1 + w)) and the normalized fp32 row to h (if not null). The whole workgroup calls this; red: LDS of 16 doubles.
-__device__ inline void norm_quant_regs(float (&v)[4][8], int cols, const float *norm_w, float eps, _Float16 *ar,
+template <typename Dst>
+__device__ inline void norm_quant_regs(float (&v)[4][8], int cols, const float *norm_w, float eps, Dst ar,
                                        float *h, double *red) {
     const int ng = cols / 8, nthr = blockDim.x;
     if (norm_w) {

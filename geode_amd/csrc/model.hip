@@ -15,8 +15,10 @@
 #include <string>
 #include <vector>
 
+#include "layer_common.hpp"
 #include "mfma_gemv.hpp"
 #include "model.hpp"
+#include "step.hpp"
 
 namespace gv {
 
@@ -50,16 +52,6 @@ __global__ __launch_bounds__(256) void embed_kernel(Q4 w, const StepParams *__re
         *reinterpret_cast<float4 *>(o + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
     }
     norm_quant_regs(v, ng * 8, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
-}
-
-// The device KV cache of one layer: K [nkv][slots][hd] and V [nkv][slots / 64][hd][64] in fp16 (V transposed in
-// blocks of kAttnBlock positions, so that the MFMA operands of both products are contiguous loads).
-__device__ __host__ inline int64_t k_index(int64_t slots, int hd, int kh, int64_t slot, int d) {
-    return (static_cast<int64_t>(kh) * slots + slot) * hd + d;
-}
-__device__ __host__ inline int64_t v_index(int64_t slots, int hd, int nkv, int kh, int64_t slot, int d) {
-    return static_cast<int64_t>(nkv) * slots * hd +
-           ((static_cast<int64_t>(kh) * (slots / kAttnBlock) + slot / kAttnBlock) * hd + d) * kAttnBlock + slot % kAttnBlock;
 }
 
 // Per (row, head): the query heads' and key heads' RMSNorm(1 + w) then partial RoPE on the first rope_dim dims
@@ -125,13 +117,10 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
         q_out[qo] = hi;
         q_out[qo + static_cast<int64_t>(sp->M) * nh * hd] = lo;
     } else {
-        kv[k_index(slots, hd, kh, slot, i)] = static_cast<_Float16>(out);
+        kv[k_index(slots, hd, kh, slot, i)] = f16_of(out);
     }
 }
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef float float4v __attribute__((ext_vector_type(4)));
 
 // Split-KV attention on the matrix cores: a workgroup (4 waves) per (block of 64 positions, KV head), the block's
 // keys [64][hd] and values [hd][64] staged in LDS by all its threads (positions past the context as zeros), then a
@@ -140,9 +129,6 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 // the block's maximum, the weights exp(s - max) and their sum; O^T = V^T P^T with the weights as hi + lo halves.
 // Writes the block's partial (weighted values, max, sum) as attend_heads does per block (model.cpp:3894-4018);
 // attn_merge joins them.
-__host__ __device__ inline int attn_k_ld(int hd) { return hd + 8; }   // halves a staged key row (bank spread)
-constexpr int kAttnVld = kAttnBlock + 8;                              // halves a staged value row
-inline size_t attn_lds(int hd) { return (static_cast<size_t>(kAttnBlock) * attn_k_ld(hd) + hd * kAttnVld) * 2; }
 
 __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restrict__ q16,
                                                          const _Float16 *__restrict__ kv, int64_t slots, int nh,
@@ -397,151 +383,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     }
 }
 
-// route_topk (model.cpp:4021-4065) of one row by one wave: softmax over the E experts (max, expf, the sum in index
-// order, divide), the top K by probability with ties to the lower index (a wave max, then ballots), the weights
-// p / (their sum in rank order) to w[0..K), the ids to ids[0..K) (lane 0), the shared expert's gate sigmoid(lg[E])
-// to *gate. p: this wave's E floats of LDS.
-__device__ inline void route_row(const float *__restrict__ lg, int E, int K, float *p, int *ids, float *w,
-                                 float *gate) {
-    const int lane = threadIdx.x & 63;
-    float v[4];
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        v[i] = e < E ? lg[e] : -__builtin_inff();
-        mx = fmaxf(mx, v[i]);
-    }
-    mx = wave_max(mx);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E) p[e] = expf(__fsub_rn(v[i], mx));
-    }
-    __builtin_amdgcn_wave_barrier();
-    float sum = 0.0f;
-    if (lane == 0) {   // index order, as the reference; 64 values read ahead of their sums
-        int e = 0;
-        for (; e + 64 <= E; e += 64) {
-            float4 v4[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v4[u] = *reinterpret_cast<const float4 *>(&p[e + 4 * u]);
-#pragma unroll
-            for (int u = 0; u < 16; ++u)
-                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v4[u].x), v4[u].y), v4[u].z), v4[u].w);
-        }
-        for (; e < E; ++e) sum = __fadd_rn(sum, p[e]);
-    }
-    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
-    float pv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        pv[i] = e < E ? __fdiv_rn(p[e], sum) : -1.0f;
-    }
-    float top = 0.0f, mine = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const float bv = wave_max(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])));
-        int bi = E;
-#pragma unroll
-        for (int i = 3; i >= 0; --i) {
-            const uint64_t hit = __ballot(pv[i] == bv);
-            if (hit) bi = 64 * i + __builtin_ctzll(hit);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (lane + 64 * i == bi) pv[i] = -1.0f;   // taken
-        if (lane == k) mine = bv;
-        if (lane == 0) ids[k] = bi;
-        top = __fadd_rn(top, bv);   // rank order
-    }
-    if (lane < K) w[lane] = __fdiv_rn(mine, top);
-    if (lane == 0 && gate) *gate = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[E])));
-}
-
-// The route of the step's rows (route_row each); then the slots (distinct experts ascending, the shared one last)
-// and their picks ordered by (expert, token, rank), each pick placed by counting, so the order never depends on
-// timing. The whole workgroup (blockDim a multiple of 64, at least 256) calls this; LDS: p [M][256], ids [M][16],
-// cnt / start / slot_of [E + 1], wtot [2][16].
-struct RouteLds {
-    float (*p)[256];
-    int *ids, *cnt, *start, *slot_of;
-    int (*wtot)[16];
-};
-
-__device__ inline void route_all(const float *__restrict__ logits, int E, int K, int M, RouteState *__restrict__ rs,
-                                 int32_t *__restrict__ ids_out, const RouteLds &r) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
-    const int E1 = E + 1;
-    for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0;
-    for (int t = wave; t < M; t += waves) {
-        route_row(logits + static_cast<int64_t>(t) * E1, E, K, r.p[t], &r.ids[t * 16], rs->weight + t * K,
-                  rs->gate + t);
-        if (lane < K) ids_out[t * K + lane] = r.ids[t * 16 + lane];
-    }
-    __syncthreads();
-    // counts per expert (the shared expert, E, once per row)
-    for (int i = tid; i < M * K; i += blockDim.x) atomicAdd(&r.cnt[r.ids[(i / K) * 16 + i % K]], 1);
-    if (tid == 0) r.cnt[E] = M;
-    __syncthreads();
-    {   // exclusive scans over the E + 1 counters (starts, slot numbers): two a thread, waves, the waves' totals
-        const int e0 = 2 * tid, e1 = e0 + 1;
-        const int c0 = e0 <= E ? r.cnt[e0] : 0, c1 = e1 <= E ? r.cnt[e1] : 0;
-        const int u0 = c0 > 0, u1 = c1 > 0;
-        int ic = c0 + c1, iu = u0 + u1;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
-            if (lane >= o) ic += pc, iu += pu;
-        }
-        if (lane == 63) r.wtot[0][wave] = ic, r.wtot[1][wave] = iu;
-        __syncthreads();
-        int bc = 0, bu = 0;
-        for (int w2 = 0; w2 < wave; ++w2) bc += r.wtot[0][w2], bu += r.wtot[1][w2];
-        const int xc = bc + ic - (c0 + c1), xu = bu + iu - (u0 + u1);   // exclusive, before e0
-        if (e0 <= E) {
-            r.start[e0] = xc;
-            r.slot_of[e0] = u0 ? xu : -1;
-            if (e0 == E) rs->n_slots = xu + u0, rs->n_picks = xc + c0;
-        }
-        if (e1 <= E) {
-            r.start[e1] = xc + c0;
-            r.slot_of[e1] = u1 ? xu + u0 : -1;
-            if (e1 == E) rs->n_slots = xu + u0 + u1, rs->n_picks = xc + c0 + c1;
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e <= E; e += blockDim.x)
-        if (r.slot_of[e] >= 0) {
-            rs->slot_expert[r.slot_of[e]] = e;
-            rs->slot_start[r.slot_of[e]] = r.start[e];
-            rs->slot_count[r.slot_of[e]] = r.cnt[e];
-        }
-    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
-    for (int i = tid; i < M * (K + 1); i += blockDim.x) {
-        const int t = i / (K + 1), k = i % (K + 1);
-        const int e = k < K ? r.ids[t * 16 + k] : E;
-        int before = 0;
-        if (k < K) {
-            for (int t2 = 0; t2 < t; ++t2)
-                for (int k2 = 0; k2 < K; ++k2) before += r.ids[t2 * 16 + k2] == e;
-        } else {
-            before = t;
-        }
-        const int pk = r.start[e] + before;
-        rs->pick_token[pk] = t;
-        rs->pick_of[t * (K + 1) + k] = pk;
-    }
-}
-
 // the route alone (rows' logits given after the router: the MoE block entry point)
 __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ logits, int E, int K,
                                                     const StepParams *__restrict__ sp, RouteState *__restrict__ rs,
                                                     int32_t *__restrict__ ids_out) {
-    __shared__ float p[kMaxRows][256];
     __shared__ int ids[kMaxRows * 16];
     __shared__ int cnt[257], start[257], slot_of[257];
+    __shared__ unsigned rows[257];
     __shared__ int wtot[2][16];
-    route_all(logits, E, K, sp->M, rs, ids_out, RouteLds{p, ids, cnt, start, slot_of, wtot});
+    route_all(logits, E, K, sp->M, rs, ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
 }
 
 // The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A
@@ -554,7 +404,7 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
 constexpr int kRouterRows = 4;
 __host__ __device__ inline int router_tokens(int H) { return H <= 2048 ? 8 : 4; }
 // the route's LDS in the router's tail: p [kMaxRows][256], ids [kMaxRows][16], cnt / start / slot_of [257]
-constexpr size_t kRouteLds = (static_cast<size_t>(kMaxRows) * 256 + kMaxRows * 16 + 3 * 260) * 4;
+constexpr size_t kRouteLds = (static_cast<size_t>(kMaxRows) * 16 + 4 * 260) * 4;
 inline size_t router_lds(int H) {
     return std::max(static_cast<size_t>(router_tokens(H)) * (H + 8) * 4 + static_cast<size_t>(kRouterRows) * H * 4,
                     kRouteLds);
@@ -698,10 +548,10 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     if (!s_last) return;
     __threadfence();
     if (threadIdx.x == 0) *counter = 0;   // ready for the next launch
-    float(*p)[256] = reinterpret_cast<float(*)[256]>(lds_f);
-    int *ids = reinterpret_cast<int *>(lds_f + kMaxRows * 256);
+    int *ids = reinterpret_cast<int *>(lds_f);
     int *cnt = ids + kMaxRows * 16, *start = cnt + 260, *slot_of = start + 260;
-    route_all(logits, E, K, M, rs, ids_out, RouteLds{p, ids, cnt, start, slot_of, wtot});
+    unsigned *rows = reinterpret_cast<unsigned *>(slot_of + 260);
+    route_all(logits, E, K, M, rs, ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
 }
 
 // The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
@@ -968,10 +818,9 @@ __global__ __launch_bounds__(256) void gate_rows_kernel(const uint16_t *__restri
 __global__ __launch_bounds__(256) void route_rows_kernel(const float *__restrict__ logits, int E, int K, int M,
                                                          int *__restrict__ ids, float *__restrict__ w,
                                                          float *__restrict__ gate) {
-    __shared__ float p[4][256];
     const int wave = threadIdx.x >> 6, t = blockIdx.x * 4 + wave;
     if (t >= M) return;
-    route_row(logits + static_cast<int64_t>(t) * (E + 1), E, K, p[wave], ids + static_cast<int64_t>(t) * K,
+    route_row(logits + static_cast<int64_t>(t) * (E + 1), E, K, ids + static_cast<int64_t>(t) * K,
               w + static_cast<int64_t>(t) * K, gate + t);
 }
 
@@ -1182,6 +1031,7 @@ int run_layers(Model &m, int M, hipStream_t st) {
 // the verify step's launches: replayed from the row count's graph when there is one (captured on the second step of
 // that row count, so the first runs the launches directly and sets every kernel's attributes)
 int run_step(Model &m, int M, hipStream_t st) {
+    if (m.use_step_kernel && m.timed_class < 0 && step_supported(m, M, nullptr)) return step_run(m, M, st);
     if (!m.use_graphs || m.timed_class >= 0 || !m.seen[M]) {
         m.seen[M] = true;
         return run_layers(m, M, st);
@@ -1414,17 +1264,39 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * c.n_layers)));
     ok = ok && (m.counter = static_cast<int *>(dalloc(m, 64)));
     ok = ok && hipMemset(m.counter, 0, 64) == hipSuccess;
-    ok = ok && (m.x = static_cast<float *>(dalloc(m, Mx * H * 4)));
-    ok = ok && (m.qkv_out = static_cast<float *>(dalloc(m, Mx * qkv_rows(c) * 4)));
+    {   // the buffers one step's phases exchange, in one arena (the persistent kernel addresses them by offset)
+        const size_t sizes[] = {static_cast<size_t>(Mx) * H * 4,
+                                static_cast<size_t>(Mx) * qkv_rows(c) * 4,
+                                static_cast<size_t>(Mx) * m.E1 * 4,
+                                static_cast<size_t>(Mx) * nh * m.kv_blocks * (hd + 2) * 4,
+                                static_cast<size_t>(m.max_picks) * H * 4,
+                                static_cast<size_t>(Mx) * V * 4,
+                                static_cast<size_t>(Mx) * act_bytes(H),
+                                static_cast<size_t>(Mx) * act_bytes(nh * hd),
+                                static_cast<size_t>(m.max_picks) * act_bytes(F)};
+        size_t offs[9], tot = 0;
+        for (int i = 0; i < 9; ++i) {
+            offs[i] = tot;
+            tot += (sizes[i] + 255) / 256 * 256;
+        }
+        auto *ar = static_cast<uint8_t *>(dalloc(m, tot));
+        ok = ok && ar && tot < 0x7FFFFF00u;
+        if (ok) {
+            m.arena = ar;
+            m.arena_bytes = tot;
+            m.x = reinterpret_cast<float *>(ar + offs[0]);
+            m.qkv_out = reinterpret_cast<float *>(ar + offs[1]);
+            m.rlogits = reinterpret_cast<float *>(ar + offs[2]);
+            m.parts = reinterpret_cast<float *>(ar + offs[3]);
+            m.y = reinterpret_cast<float *>(ar + offs[4]);
+            m.logits = reinterpret_cast<float *>(ar + offs[5]);
+            m.act_h = reinterpret_cast<_Float16 *>(ar + offs[6]);
+            m.act_core = reinterpret_cast<_Float16 *>(ar + offs[7]);
+            m.act_m = reinterpret_cast<_Float16 *>(ar + offs[8]);
+        }
+    }
     ok = ok && (m.q16 = static_cast<_Float16 *>(dalloc(m, 2 * Mx * nh * hd * 2)));
-    ok = ok && (m.rlogits = static_cast<float *>(dalloc(m, Mx * m.E1 * 4)));
-    ok = ok && (m.parts = static_cast<float *>(dalloc(m, static_cast<size_t>(Mx) * nh * m.kv_blocks * (hd + 2) * 4)));
     ok = ok && (m.gu_out = static_cast<float *>(dalloc(m, static_cast<size_t>(m.max_picks) * 2 * F * 4)));
-    ok = ok && (m.y = static_cast<float *>(dalloc(m, static_cast<size_t>(m.max_picks) * H * 4)));
-    ok = ok && (m.logits = static_cast<float *>(dalloc(m, static_cast<size_t>(Mx) * V * 4)));
-    ok = ok && (m.act_h = static_cast<_Float16 *>(dalloc(m, Mx * act_bytes(H))));
-    ok = ok && (m.act_core = static_cast<_Float16 *>(dalloc(m, Mx * act_bytes(nh * hd))));
-    ok = ok && (m.act_m = static_cast<_Float16 *>(dalloc(m, m.max_picks * act_bytes(F))));
     ok = ok && (m.route_ids = static_cast<int32_t *>(dalloc(m, static_cast<size_t>(c.n_layers) * Mx * K * 4)));
     const int half = c.rope_dim / 2;
     const int npos = c.max_ctx + kMaxRows;
@@ -1468,6 +1340,7 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
                    const float *globals) {
     GV_REQUIRE(g && data, "gv_model_adopt: null pointer");
     Model &m = g->m;
+    if (step_invalidate(m) != 0) return -1;   // the step kernel's copies of the globals are rebuilt on next use
     const auto &c = m.c;
     const int64_t H = c.hidden, F = c.moe_ff, V = c.vocab, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     const bool per_layer = kind != GV_EMBED && kind != GV_LM_HEAD && kind != GV_FINAL_NORM;
@@ -1546,6 +1419,7 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
 int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sigma, int ctx) {
     GV_REQUIRE(g, "gv_model_randomize: null model");
     Model &m = g->m;
+    if (step_invalidate(m) != 0) return -1;
     const auto &c = m.c;
     GV_REQUIRE(ctx >= 0 && ctx + c.max_rows <= c.max_ctx, "gv_model_randomize: ctx too large");
     const int64_t H = c.hidden, F = c.moe_ff, V = c.vocab, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
@@ -1700,6 +1574,7 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     if (logits) {
         GV_CHECK_HIP(hipMemcpyAsync(logits, m.logits, static_cast<size_t>(n) * c.vocab * 4, hipMemcpyDeviceToHost, st));
         GV_CHECK_HIP(hipStreamSynchronize(st));
+        if (step_check(m) != 0) return -1;
     }
     m.last_pos = m.pos;
     m.last_n = n;
@@ -1858,6 +1733,26 @@ int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
     if (rc != 0) return -1;
     *ms_per_block = ms / reps;
     return 0;
+}
+
+int gv_model_set_step_kernel(gv_model *g, int on) {
+    GV_REQUIRE(g, "gv_model_set_step_kernel: null model");
+    g->m.use_step_kernel = on != 0;
+    return 0;
+}
+
+int gv_model_step_kernel_supported(const gv_model *g, int n) { return g && step_supported(g->m, n, nullptr) ? 1 : 0; }
+
+int gv_model_step_trace(gv_model *g, int on) {
+    GV_REQUIRE(g, "gv_model_step_trace: null model");
+    return step_trace(g->m, on != 0);
+}
+
+int64_t gv_model_step_trace_read(gv_model *g, uint64_t *out, int64_t n) {
+    GV_REQUIRE(g && out && n >= 0, "gv_model_step_trace_read: bad arguments");
+    const int64_t k = step_trace_read(g->m, out, n);
+    GV_REQUIRE(k >= 0, "gv_model_step_trace_read: copy failed");
+    return k;
 }
 
 int gv_model_set_graphs(gv_model *g, int on) {

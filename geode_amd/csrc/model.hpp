@@ -93,6 +93,8 @@ struct Model {
     _Float16 *q16 = nullptr;   // [max_rows][nh][hd]: the rotated queries
     float *parts = nullptr, *gu_out = nullptr, *y = nullptr, *logits = nullptr;
     _Float16 *act_h = nullptr, *act_core = nullptr, *act_m = nullptr;   // the products' operands (act16)
+    uint8_t *arena = nullptr;   // x, qkv_out, rlogits, parts, y, logits, act_h, act_core, act_m: one allocation
+    size_t arena_bytes = 0;
     int32_t *route_ids = nullptr;   // [n_layers][max_rows][K]
     _Float16 *kv_all = nullptr;
     int64_t slots = 0;   // KV positions a layer holds: max_ctx rounded up to whole attention blocks
@@ -112,6 +114,15 @@ struct Model {
     size_t events_used = 0;
     StepParams host_sp{};
     int max_slots = 0, max_picks = 0;
+    // the verify step as one persistent kernel (step.hip): on by gv_model_set_step_kernel; set up on first use
+    bool use_step_kernel = false;
+    void *layers_dev = nullptr;                       // LayerDev [n_layers]
+    void *step_dev = nullptr;                         // StepDev [2]: for 1..16 and 17..32 rows
+    unsigned *bar = nullptr;                          // the grid barrier's words; bar_gen: generations used so far
+    unsigned *step_err = nullptr;
+    unsigned bar_gen = 0;
+    int step_grid = 0;                                // workgroups of the launch: one a compute unit
+    uint64_t *stamps = nullptr;                       // the step kernel's barrier clock stamps (when traced)
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
