@@ -72,10 +72,8 @@ SIGNATURES = {
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
     "gv_model_set_graphs": (_c.c_int, [_P, _c.c_int]),
-    "gv_model_set_step_kernel": (_c.c_int, [_P, _c.c_int]),
-    "gv_model_step_kernel_supported": (_c.c_int, [_P, _c.c_int]),
-    "gv_model_step_trace": (_c.c_int, [_P, _c.c_int]),
-    "gv_model_step_trace_read": (_c.c_int64, [_P, _P, _c.c_int64]),
+    "gv_model_trace": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_trace_read": (_c.c_int64, [_P, _P, _c.c_int64]),
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
@@ -333,24 +331,18 @@ class VerifyModel:
         """the verify step as one HIP graph per row count (default) or plain launches"""
         check(_lib().gv_model_set_graphs(self.h, 1 if on else 0), "gv_model_set_graphs")
 
-    def set_step_kernel(self, on):
-        """on: the verify step as one persistent kernel where the shapes fit it; off: the per-phase kernels"""
-        check(_lib().gv_model_set_step_kernel(self.h, 1 if on else 0), "gv_model_set_step_kernel")
+    def trace(self, on):
+        """workgroup clock stamps of the traced kernels on or off (a measurement aid)"""
+        check(_lib().gv_model_trace(self.h, 1 if on else 0), "gv_model_trace")
 
-    def step_kernel_supported(self, n):
-        return bool(_lib().gv_model_step_kernel_supported(self.h, int(n)))
-
-    def step_trace(self, on):
-        """the step kernel's barrier clock stamps on or off"""
-        check(_lib().gv_model_step_trace(self.h, 1 if on else 0), "gv_model_step_trace")
-
-    def step_trace_read(self, n_wg, n_barriers):
-        """the last step's stamps [workgroup][barrier][arrive, leave] in 10 ns ticks"""
-        out = np.zeros(n_wg * n_barriers * 2, np.uint64)
-        k = _lib().gv_model_step_trace_read(self.h, out.ctypes.data, out.size)
+    def trace_read(self):
+        """the stamps [kernel class][workgroup][slot] in 10 ns ticks (0: not stamped)"""
+        n = len(KERNEL_CLASSES) * 8192 * 8
+        out = np.zeros(n, np.uint64)
+        k = _lib().gv_model_trace_read(self.h, out.ctypes.data, n)
         if k < 0:
-            check(-1, "gv_model_step_trace_read")
-        return out.reshape(n_wg, n_barriers, 2)
+            check(-1, "gv_model_trace_read")
+        return out.reshape(len(KERNEL_CLASSES), 8192, 8)
 
     def replay(self, cls, layer=0, reps=20):
         """mean ms of kernel class cls of one layer, launched reps times back to back on the last verify's state"""

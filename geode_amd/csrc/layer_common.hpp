@@ -99,9 +99,10 @@ __device__ inline void route_row(const float *__restrict__ lg, int E, int K, int
     route_rows<1>(l1, live, E, K, i1, w1, g1);
 }
 
-// The route of the step's rows (route_rows, two rows a wave); then the slots (distinct experts ascending, the shared
-// one last, index E) and their picks ordered by (expert, token, rank), each pick placed by counting (the rows before
-// it that picked the same expert: a bit mask per expert), so the order never depends on timing. The whole workgroup
+// The route of the step's rows (route_rows, two rows a wave); then the slots and their picks ordered by (expert,
+// token, rank), each pick placed by counting (the rows before it that picked the same expert: a bit mask per expert),
+// so the order never depends on timing. A slot is a run of at most kSlotRows picks of one expert: the distinct
+// experts ascending, the shared one last (index E), an expert with more picks taking consecutive slots. The whole workgroup
 // (blockDim a multiple of 64, at least 256) calls this; LDS: ids [M][16], cnt / start / slot_of / rows [E + 1],
 // wtot [2][16].
 struct RouteLds {
@@ -138,7 +139,7 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
     {   // exclusive scans over the E + 1 counters (starts, slot numbers): two a thread, waves, the waves' totals
         const int e0 = 2 * tid, e1 = e0 + 1;
         const int c0 = e0 <= E ? r.cnt[e0] : 0, c1 = e1 <= E ? r.cnt[e1] : 0;
-        const int u0 = c0 > 0, u1 = c1 > 0;
+        const int u0 = (c0 + kSlotRows - 1) / kSlotRows, u1 = (c1 + kSlotRows - 1) / kSlotRows;   // slots
         int ic = c0 + c1, iu = u0 + u1;
         for (int o = 1; o < 64; o <<= 1) {
             const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
@@ -151,7 +152,7 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         const int xc = bc + ic - (c0 + c1), xu = bu + iu - (u0 + u1);   // exclusive, before e0
         if (e0 <= E) {
             r.start[e0] = xc;
-            r.slot_of[e0] = u0 ? xu : -1;
+            r.slot_of[e0] = u0 ? xu : -1;   // the expert's first slot
             if (e0 == E) rs->n_slots = xu + u0, rs->n_picks = xc + c0;
         }
         if (e1 <= E) {
@@ -162,11 +163,13 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
     }
     __syncthreads();
     for (int e = tid; e <= E; e += blockDim.x)
-        if (r.slot_of[e] >= 0) {
-            rs->slot_expert[r.slot_of[e]] = e;
-            rs->slot_start[r.slot_of[e]] = r.start[e];
-            rs->slot_count[r.slot_of[e]] = r.cnt[e];
-        }
+        if (r.slot_of[e] >= 0)
+            for (int k = 0; k * kSlotRows < r.cnt[e]; ++k) {
+                const int u = r.slot_of[e] + k;
+                rs->slot_expert[u] = e;
+                rs->slot_start[u] = r.start[e] + k * kSlotRows;
+                rs->slot_count[u] = min(kSlotRows, r.cnt[e] - k * kSlotRows);
+            }
     // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
     for (int i = tid; i < M * (K + 1); i += blockDim.x) {
         const int t = i / (K + 1), k = i % (K + 1);

@@ -230,110 +230,182 @@ __device__ inline void load_act16(const _Float16 *ar, int64_t g, h8 &hi, h8 &lo)
     lo = *reinterpret_cast<const h8 *>(p + 8);
 }
 
-// One workgroup's share of a product: its waves split the K range [sc0, sc0 + waves KW / 4) super-chunks (wave w:
-// chunks [w KW, (w + 1) KW) of it) of row tiles [t0, t1), a tile at a time with the next two tiles' loads in flight;
-// nsc = super-chunks a row. bload(j, g, hi, lo) gives local row j's operands of k-group g (any j < M; every lane
-// calls it, j and g uniform in the lane's 16-lane group), put(row, j, v) takes the fp32 sum (before global). part: LDS of (t1 - t0) * waves * NTT KB for the waves' partial sums,
-// added once at the end (waves > 1); tab: LDS for fill_e4m3_table, filled here (every thread of the workgroup calls
-// this) while the first loads are in flight.
-template <int KW, int NTT, typename BFn, typename PutFn>
+// The tiles a call takes: local tile i is tile t0 + i of the matrix (a run), or any map i -> tile
+struct TileRun {
+    int64_t t0;
+    __device__ int64_t operator()(int i) const { return t0 + i; }
+};
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+// How a call's waves share the work: kSplitK - the workgroup's waves split the K range of every tile, their partial
+// sums added in wave order at the end (then put); kKeepParts - the same, the partial sums left in LDS for the caller;
+// kWaveTiles - each wave alone over the whole K range and its own tiles, put directly.
+enum TilesMode { kSplitK = 0, kKeepParts = 1, kWaveTiles = 2 };
+
+// One share of a product: W waves split the K range [sc0, sc0 + W KW / 4) super-chunks (wave w: chunks
+// [w KW, (w + 1) KW) of it) of nt row tiles (local tile i is tile tmap(i)), a tile at a time with the next DEPTH - 1
+// tiles' loads in flight; nsc = super-chunks a row (W = 1 in kWaveTiles). NT > 0: nt <= NT, and the tile loop is
+// unrolled NT times (straight-line code: the compiler then waits for exactly the loads a tile needs; tiles past nt
+// are computed on the last tile's data and dropped); NT = 0: a runtime loop. rowp(j) is local row j's act16 operands
+// (any j < M). PACK (M <= 8, NTT = 1): the MFMA's 16 columns hold the rows' hi halves (columns 0..7) and their lo
+// halves (8..15), so one MFMA chain makes both products (each column's sum is the one the unpacked form makes) and a
+// lane swap adds them; else the hi and lo halves are two chains. put(row, j, v) takes the fp32 sum (before global).
+// part: LDS of max(nt, NT) * W * NTT KB for the waves' partial sums (kSplitK, kKeepParts: part[((i W + w) NTT + tt)
+// 64 + lane], left there after a workgroup barrier in kKeepParts); tab: LDS for fill_e4m3_table, filled here. hook()
+// runs after the first tiles' loads are issued and before the activations are loaded (a wait for them); ready() once
+// the activations and the first tiles are in registers. Every thread of the workgroup calls this.
+template <int KW, int NTT, int MODE, int NT = 0, int DEPTH = 3, bool PACK = false, typename RowFn, typename PutFn,
+          typename MapFn = TileRun, typename HookFn = NoHook, typename ReadyFn = NoHook>
 __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, int64_t rows,
-                                  int nsc, int sc0, int64_t t0, int64_t t1, int M, BFn bload, PutFn put, f4 *part,
-                                  uint2 *tab) {
-    const int W = blockDim.x / 64;
-    const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
+                                  int nsc, int sc0, int nt, int M, RowFn rowp, PutFn put, f4 *part, uint2 *tab,
+                                  MapFn tmap, HookFn hook = HookFn{}, ReadyFn ready = ReadyFn{}) {
+    static_assert(DEPTH >= 2 && (NT > 0 || DEPTH == 3), "the runtime loop is a ring of three");
+    static_assert(!PACK || NTT == 1, "packed hi | lo columns take one 16-row tile of at most 8 rows");
+    constexpr int NB = PACK ? 1 : 2;   // operand arrays: hi | lo packed, or hi and lo
+    const int W = MODE == kWaveTiles ? 1 : static_cast<int>(blockDim.x / 64);
+    const int w = MODE == kWaveTiles ? 0 : static_cast<int>(threadIdx.x / 64);
+    const int l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
     constexpr int NS = KW / 4;   // super-chunks a wave takes
     const uint32_t magic = 0x64006400u;
-    const int nt = static_cast<int>(t1 - t0);
-    const uint8_t *cbase = codes + (t0 * nsc + sc0 + w * NS) * 1024 + l * 16;
-    const uint8_t *sbase = scales + (t0 * nsc + sc0 + w * NS) * 128 + (lq * 2 + lg / 2) * 4;
-    const int64_t tstride = static_cast<int64_t>(nsc);
+    const uint8_t *cbase = codes + static_cast<int64_t>(sc0 + w * NS) * 1024 + l * 16;
+    const uint8_t *sbase = scales + static_cast<int64_t>(sc0 + w * NS) * 128 + (lq * 2 + lg / 2) * 4;
+    // Every load is issued unconditionally (a tile past nt reads the last tile again, from the cache): a branch
+    // around a load makes the compiler wait for nearly all loads in flight before the next use. Offsets in 32 bits
+    // (a matrix < 4 GB).
+    const uint32_t nsc_u = static_cast<uint32_t>(nsc);
     auto load = [&](int i, uint4 (&cw)[NS], uint32_t (&sw)[NS]) {
+        const uint32_t T = nt > 0 ? static_cast<uint32_t>(tmap(i < nt ? i : nt - 1)) : 0u;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const u4v v = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(cbase + (i * tstride + s) * 1024));
+            const uint32_t blk = T * nsc_u + static_cast<uint32_t>(s);
+            const u4v v = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(cbase + blk * 1024u));
             cw[s] = make_uint4(v.x, v.y, v.z, v.w);
-            sw[s] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(sbase + (i * tstride + s) * 128));
+            sw[s] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(sbase + blk * 128u));
         }
     };
-    // the first two tiles' weights (HBM, the longest wait) first
-    uint4 ca[NS], cb[NS], cc[NS];
-    uint32_t sa[NS], sb[NS], sc[NS];
-    load(0, ca, sa);
-    if (nt > 1) load(1, cb, sb);
+    // the first tiles' weights (HBM, the longest wait) first
+    uint4 cw[DEPTH][NS];
+    uint32_t sw[DEPTH][NS];
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d) load(d, cw[d], sw[d]);
+    hook();
     // the activations of this wave's K range, resident for all the tiles (rows past M: row M - 1's, then zeros)
-    h8 bh[KW][NTT], bl[KW][NTT];
+    h8 b[NB][KW][NTT];
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
-        const int j = tt * 16 + lq;
+        const int j = PACK ? lq % 8 : tt * 16 + lq;
+        const _Float16 *row = rowp(j < M ? j : M - 1);
 #pragma unroll
-        for (int c = 0; c < KW; ++c)
-            bload(j < M ? j : M - 1, (static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg, bh[c][tt], bl[c][tt]);
+        for (int c = 0; c < KW; ++c) {
+            const int64_t g = (static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg;
+            if (PACK) {
+                b[0][c][tt] = *reinterpret_cast<const h8 *>(row + g * 16 + (lq >= 8 ? 8 : 0));
+            } else {
+                b[0][c][tt] = *reinterpret_cast<const h8 *>(row + g * 16);
+                b[NB - 1][c][tt] = *reinterpret_cast<const h8 *>(row + g * 16 + 8);
+            }
+        }
     }
     fill_e4m3_table(tab);
     __syncthreads();
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt)
-        if (tt * 16 + lq >= M)
+        if ((PACK ? lq % 8 : tt * 16 + lq) >= M)
 #pragma unroll
-            for (int c = 0; c < KW; ++c) bh[c][tt] = bl[c][tt] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-    auto tile = [&](int i, const uint4 (&cw)[NS], const uint32_t (&sw)[NS]) {
-        f4 acc[NTT], acl[NTT];   // the hi and lo products apart: two independent MFMA chains
+            for (int c = 0; c < KW; ++c)
 #pragma unroll
-        for (int tt = 0; tt < NTT; ++tt) acc[tt] = acl[tt] = f4{0, 0, 0, 0};
+                for (int h = 0; h < NB; ++h) b[h][c][tt] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    auto tile = [&](int i, const uint4 (&cq)[NS], const uint32_t (&sq)[NS]) {
+        f4 acc[NB][NTT];   // the hi and lo products apart: two independent MFMA chains (packed: two column halves)
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+            for (int h = 0; h < NB; ++h) acc[h][tt] = f4{0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const uint32_t words[4] = {cw[s].x, cw[s].y, cw[s].z, cw[s].w};
+            const uint32_t words[4] = {cq[s].x, cq[s].y, cq[s].z, cq[s].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const h8 a = decode8(words[j], tab[(sw[s] >> (8 * j)) & 0xFFu], magic);
+                const h8 a = decode8(words[j], tab[(sq[s] >> (8 * j)) & 0xFFu], magic);
                 const int c = s * 4 + j;
 #pragma unroll
-                for (int tt = 0; tt < NTT; ++tt) {
-                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh[c][tt], acc[tt], 0, 0, 0);
-                    acl[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl[c][tt], acl[tt], 0, 0, 0);
-                }
+                for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+                    for (int h = 0; h < NB; ++h)
+                        acc[h][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[h][c][tt], acc[h][tt], 0, 0, 0);
             }
         }
 #pragma unroll
-        for (int tt = 0; tt < NTT; ++tt) acc[tt] += acl[tt];
-        if (W > 1) {
+        for (int tt = 0; tt < NTT; ++tt) {
+            if (PACK) {   // column j < 8: hi sum + the lo sum from column j + 8 (lane l ^ 8)
+                f4 lo;
 #pragma unroll
-            for (int tt = 0; tt < NTT; ++tt) part[((i * W + w) * NTT + tt) * 64 + l] = acc[tt];
-        } else {
+                for (int r = 0; r < 4; ++r) lo[r] = __shfl_xor(acc[0][tt][r], 8, 64);
+                acc[0][tt] += lo;
+            } else {
+                acc[0][tt] += acc[NB - 1][tt];
+            }
+        }
+        f4 (&res)[NTT] = acc[0];
+        if (MODE != kWaveTiles) {
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) part[((i * W + w) * NTT + tt) * 64 + l] = res[tt];
+        } else if (i < nt) {
+            const int64_t T = tmap(i);
 #pragma unroll
             for (int tt = 0; tt < NTT; ++tt) {
                 const int j = tt * 16 + lq;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t row = (t0 + i) * kTileR + 4 * lg + r;
-                    if (j < M && row < rows) put(row, j, acc[tt][r]);
+                    const int64_t row = T * kTileR + 4 * lg + r;
+                    if (j < M && row < rows) put(row, j, res[tt][r]);
                 }
             }
         }
     };
-    // a ring of three tiles' loads: two in flight while one is computed
-    for (int i = 0; i < nt; i += 3) {
-        if (i + 2 < nt) load(i + 2, cc, sc);
-        tile(i, ca, sa);
-        if (i + 1 >= nt) break;
-        if (i + 3 < nt) load(i + 3, ca, sa);
-        tile(i + 1, cb, sb);
-        if (i + 2 >= nt) break;
-        if (i + 4 < nt) load(i + 4, cb, sb);
-        tile(i + 2, cc, sc);
+    if constexpr (NT > 0) {
+        ready();
+        // straight-line: tile i + DEPTH - 1's loads go to the slot tile i - 1 used, then tile i is computed
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            if (i + DEPTH - 1 < NT) load(i + DEPTH - 1, cw[(i + DEPTH - 1) % DEPTH], sw[(i + DEPTH - 1) % DEPTH]);
+            tile(i, cw[i % DEPTH], sw[i % DEPTH]);
+        }
+    } else {
+        // a ring of three tiles' loads: two in flight while one is computed. Everything loaded so far (the
+        // activations, the first two tiles) is waited for here, once: the loop then starts from the state its back
+        // edge has (two tiles in flight).
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0) (expcnt, lgkmcnt: no wait)
+        ready();
+        for (int i = 0; i < nt; i += 3) {
+            load(i + 2, cw[2], sw[2]);
+            tile(i, cw[0], sw[0]);
+            if (i + 1 >= nt) break;
+            load(i + 3, cw[0], sw[0]);
+            tile(i + 1, cw[1], sw[1]);
+            if (i + 2 >= nt) break;
+            load(i + 4, cw[1], sw[1]);
+            tile(i + 2, cw[2], sw[2]);
+        }
+    }
+    if (MODE == kKeepParts) {
+        __syncthreads();
+        return;
     }
     // the waves' partial sums added in wave order, each output by one thread
-    if (W > 1) {
+    if (MODE == kSplitK) {
         __syncthreads();
         for (int o = threadIdx.x; o < nt * NTT * 64; o += blockDim.x) {
             const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
             f4 sum = part[((i * W + 0) * NTT + tt) * 64 + ll];
             for (int w2 = 1; w2 < W; ++w2) sum += part[((i * W + w2) * NTT + tt) * 64 + ll];
             const int j = tt * 16 + ll % 16;
+            const int64_t T = tmap(i);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t row = (t0 + i) * kTileR + 4 * (ll / 16) + r;
+                const int64_t row = T * kTileR + 4 * (ll / 16) + r;
                 if (j < M && row < rows) put(row, j, sum[r]);
             }
         }

@@ -18,10 +18,20 @@
 #include "layer_common.hpp"
 #include "mfma_gemv.hpp"
 #include "model.hpp"
-#include "step.hpp"
 
 namespace gv {
 
+// ---------------------------------------------------------------- a measurement aid: workgroup clock stamps
+// When g_trace is set (gv_model_trace), thread 0 of each workgroup of the traced kernels writes the 100 MHz clock
+// (s_memrealtime) at a few points to g_trace[(cls * kTraceWgs + workgroup) * 8 + slot]; each launch overwrites its
+// class's stamps, so after a step they are the last layer's. Null (the default): one scalar load and branch a stamp.
+constexpr int kTraceWgs = 8192;
+__device__ uint64_t *g_trace;
+__device__ inline void trace(int cls, int slot) {
+    uint64_t *t = g_trace;
+    if (t && threadIdx.x == 0 && blockIdx.x < kTraceWgs)
+        t[(static_cast<size_t>(cls) * kTraceWgs + blockIdx.x) * 8 + slot] = __builtin_amdgcn_s_memrealtime();
+}
 
 // ---------------------------------------------------------------- kernels
 // the rows' embeddings: dequant_row of the embedding matrix (pack.cpp:356-366), bit for bit, to x; then the first
@@ -576,20 +586,148 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
     if (t0 >= ntiles) return;
     const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
-    mfma_tiles<KW, NTT>(
+    mfma_tiles<KW, NTT, kSplitK>(
         codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
-        K / kSuperK, 0, t0, t1,
+        K / kSuperK, 0, static_cast<int>(t1 - t0),
         cnt,
-        [&](int j, int64_t g, h8 &hi, h8 &lo) {
-            // UP: the row's act16 operands; DOWN: the pick's SwiGLU operands
+        [&](int j) {   // UP: the row's act16 operands; DOWN: the pick's SwiGLU operands
             const int64_t src = UP ? sl.pick_token[start + j] : start + j;
-            load_act16(act + src * act_stride, g, hi, lo);
+            return act + src * act_stride;
         },
         [&](int64_t row, int j, float v) {
             const float gl = UP ? (row < half_rows ? g0 : g1) : g2;
             out[static_cast<int64_t>(start + j) * rows + row] = v * gl;
         },
-        part_lds, tab);
+        part_lds, tab, TileRun{t0});
+}
+
+// ---------------------------------------------------------------- the decode MoE
+// The experts' products of the verify step's slots (runs of at most kSlotRows picks of one expert), in two launches.
+// Up: a workgroup per (slot, kMoePairs matched gate/up row tile pairs); its waves split K = H, and it computes gate
+// tile p and up tile p together, so the 16 values m = silu(gate) x up of a tile pair and their 16-value quantization
+// block are its own: it writes the picks' down operands (act16) directly (no gate|up buffer, no SwiGLU launch). Down:
+// a workgroup per (slot, group of row tiles), each wave kMoeDnTiles tiles over the whole K = F. Every tile loop is
+// unrolled (mfma_tiles with a fixed tile count).
+constexpr int kMoePairs = 3;       // tile pairs an up workgroup takes
+constexpr int kMoeDnTiles = 3;     // down tiles a wave takes
+
+struct MoeArgsDec {
+    const uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
+    size_t gu_cstride, gu_sstride, dn_cstride, dn_sstride;
+    int H, F;
+    const float *globals;                 // [E + 1][3]
+    const _Float16 *act;                  // the rows' operands (act16, act_stride halves apart)
+    int64_t act_stride;
+    _Float16 *act_m;                      // the picks' down operands (act16, F values a pick)
+    float *y;                             // [pick][H]
+    Slots sl;
+    int groups, E1, max_picks;
+};
+
+// the slot of this workgroup (blockIdx / groups) and its expert, first pick and pick count: all four loaded at once
+// (the slot's entries are read before knowing it is live; every index is inside the route state); false: no slot
+__device__ inline bool moe_slot(const MoeArgsDec &a, int u, int &e, int &start, int &cnt) {
+    const int ns = *a.sl.n_slots;
+    e = a.sl.expert[u], start = a.sl.start[u], cnt = a.sl.count[u];
+    return u < ns && e >= 0 && e < a.E1 && cnt >= 1 && cnt <= kSlotRows && start >= 0 && start + cnt <= a.max_picks;
+}
+
+template <int KWU>
+__global__ __launch_bounds__(256) void moe_up_kernel(const MoeArgsDec a) {
+    extern __shared__ f4 part_lds[];
+    __shared__ uint2 tab[256];
+    trace(GV_K_MOE_UP, 0);
+    const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
+    int e, start, cnt;
+    if (!moe_slot(a, u, e, start, cnt)) return;
+    trace(GV_K_MOE_UP, 4);
+    const int F = a.F, W = blockDim.x / 64, lane = threadIdx.x % 64;
+    const int64_t act_m_stride = act_halves(F);
+    const int npair = F / kTileR, p0 = grp * kMoePairs, np = min(kMoePairs, npair - p0);
+    if (np <= 0) return;
+    mfma_tiles<KWU, 1, kKeepParts, 2 * kMoePairs, 3, true>(
+        a.gu_codes + static_cast<size_t>(e) * a.gu_cstride, a.gu_scales + static_cast<size_t>(e) * a.gu_sstride,
+        2 * F, a.H / kSuperK, 0, 2 * np, cnt,
+        [&](int j) { return a.act + static_cast<int64_t>(a.sl.pick_token[start + j]) * a.act_stride; },
+        [](int64_t, int, float) {}, part_lds, tab,
+        [&](int i) -> int64_t { return (i & 1) ? npair + p0 + (i >> 1) : p0 + (i >> 1); }, NoHook{},
+        [] { trace(GV_K_MOE_UP, 5); });
+    trace(GV_K_MOE_UP, 1);
+    const float g0 = a.globals[e * 3], g1 = a.globals[e * 3 + 1];
+    // per pair (a wave each): the waves' sums in wave order, x global (the products' put), then m = silu(gate) x up
+    // (swiglu_quant_kernel's arithmetic) and the 16-value block's operands
+    for (int o = threadIdx.x; o < np * 64; o += blockDim.x) {
+        const int q = o / 64, j = lane % 16, lg = lane / 16;
+        f4 gs = part_lds[(2 * q * W) * 64 + lane], us = part_lds[((2 * q + 1) * W) * 64 + lane];
+        for (int w2 = 1; w2 < W; ++w2) {
+            gs += part_lds[(2 * q * W + w2) * 64 + lane];
+            us += part_lds[((2 * q + 1) * W + w2) * 64 + lane];
+        }
+        float mv[4], amax = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float x = gs[r] * g0, uv = us[r] * g1;
+            mv[r] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), uv);
+            amax = fmaxf(amax, fabsf(mv[r]));
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const float sc = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        uint32_t hw[2], lw[2];   // this lane's 4 values (rows 4 lg .. 4 lg + 3 of the pair): hi, lo halves
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+            _Float16 h0, l0, h1, l1;
+            const int q0 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r], qi))), -127), 127);
+            const int q1 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r + 1], qi))), -127), 127);
+            split_f16(__fmul_rn(static_cast<float>(q0), sc), h0, l0);
+            split_f16(__fmul_rn(static_cast<float>(q1), sc), h1, l1);
+            hw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+            lw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+        }
+        // k-group 2 (p0 + q) + lg / 2 holds values 0..3 (lane lg even) and 4..7 (lane lg + 1) in the slot order
+        // (0 4 1 5 2 6 3 7): the even lane takes its partner's four and writes the group
+        uint32_t ph[2], pl[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            ph[k] = __shfl_xor(hw[k], 16, 64);
+            pl[k] = __shfl_xor(lw[k], 16, 64);
+        }
+        if ((lg & 1) == 0 && j < cnt) {
+            auto inter = [](uint32_t mine, uint32_t other) {   // (m0, o0), (m1, o1) as two words
+                return make_uint2((mine & 0xFFFFu) | (other << 16), (mine >> 16) | (other & 0xFFFF0000u));
+            };
+            const uint2 h01 = inter(hw[0], ph[0]), h23 = inter(hw[1], ph[1]);
+            const uint2 l01 = inter(lw[0], pl[0]), l23 = inter(lw[1], pl[1]);
+            const int gi = 2 * (p0 + q) + lg / 2;
+            uint4 *dst = reinterpret_cast<uint4 *>(a.act_m + (start + j) * act_m_stride + static_cast<int64_t>(gi) * 16);
+            dst[0] = make_uint4(h01.x, h01.y, h23.x, h23.y);
+            dst[1] = make_uint4(l01.x, l01.y, l23.x, l23.y);
+        }
+    }
+    trace(GV_K_MOE_UP, 3);
+}
+
+template <int KWD>
+__global__ __launch_bounds__(256) void moe_down_kernel(const MoeArgsDec a) {
+    __shared__ uint2 tab[256];
+    trace(GV_K_MOE_DOWN, 0);
+    const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
+    int e, start, cnt;
+    if (!moe_slot(a, u, e, start, cnt)) return;
+    trace(GV_K_MOE_DOWN, 4);
+    const int H = a.H, F = a.F, W = blockDim.x / 64, w = threadIdx.x / 64;
+    const int64_t act_m_stride = act_halves(F);
+    const int wt0 = (grp * W + w) * kMoeDnTiles, nt = max(0, min(kMoeDnTiles, H / kTileR - wt0));
+    const float g2 = a.globals[e * 3 + 2];
+    mfma_tiles<KWD, 1, kWaveTiles, kMoeDnTiles, kMoeDnTiles, true>(
+        a.dn_codes + static_cast<size_t>(e) * a.dn_cstride, a.dn_scales + static_cast<size_t>(e) * a.dn_sstride, H,
+        F / kSuperK, 0, nt, cnt,
+        [&](int j) { return a.act_m + (start + j) * act_m_stride; },
+        [&](int64_t row, int j, float v) { a.y[static_cast<int64_t>(start + j) * H + row] = v * g2; }, nullptr, tab,
+        TileRun{wt0}, NoHook{}, [] { trace(GV_K_MOE_DOWN, 5); });
+    trace(GV_K_MOE_DOWN, 3);
 }
 
 // per pick: silu(gate) * up (kernels.hpp:141), quantized for down
@@ -713,7 +851,8 @@ __global__ void f32_to_f16_kernel(const float *__restrict__ x, int64_t n, uint16
 namespace {
 
 // the slots a step of M rows can have: its distinct experts (at most M K) and the shared one
-inline int moe_slots(const Model &m, int M) { return std::min(m.max_slots, std::min(m.c.n_experts, M * m.c.top_k) + 1); }
+inline int moe_slots_bound(int E, int K, int M) { return std::min(E, M * K) + 1 + M * (K + 1) / kSlotRows; }
+inline int moe_slots(const Model &m, int M) { return std::min(m.max_slots, moe_slots_bound(m.c.n_experts, m.c.top_k, M)); }
 
 // One launch of the experts' products over a slot list
 struct MoeArgs {
@@ -736,7 +875,7 @@ int launch_moe_raw(const MoeArgs &a, int waves, hipStream_t st) {
     // the slots' tiles over about as many workgroups as the chip holds at once
     const int per = static_cast<int>(tiles_per_wg(ntiles * a.slots, waves, NTT));
     const int tiles = static_cast<int>((ntiles + per - 1) / per);
-    const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
+    const size_t lds = static_cast<size_t>(per) * waves * NTT * 1024;   // the waves' partial sums
     static int granted = 0;
     if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 76 * 1024, granted) != 0)
         return -1;
@@ -784,8 +923,50 @@ int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float
 }
 
 int moe_products(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
-    return moe_run(m, L, up, M, up ? m.act_h : m.act_m, m.gu_out, route_slots(m.route + (&L - &m.layers[0])),
-                   up ? m.gu_out : m.y, moe_slots(m, M), m.max_picks, st);
+    return moe_run(m, L, up, std::min(M, kSlotRows), up ? m.act_h : m.act_m, m.gu_out,
+                   route_slots(m.route + (&L - &m.layers[0])), up ? m.gu_out : m.y, moe_slots(m, M), m.max_picks, st);
+}
+
+// The decode MoE kernels' shape: the up workgroup's waves split K = H (mfma_split's choice for 16-row tiles, at most
+// 4 waves) and each down wave takes K = F whole; false when the shapes fall outside the compiled variants (the
+// general products and the SwiGLU launch, moe_products, then run instead).
+bool moe_dec_shape(const gv_model_config &c, int &kwu, int &kwd, int &waves) {
+    const int64_t H = c.hidden, F = c.moe_ff;
+    if (H % kSuperK || F % kSuperK || H % kTileR) return false;
+    if (!mfma_split(H, 1, waves, kwu) || waves > 4) return false;
+    kwd = static_cast<int>(F / 32);
+    return (kwu == 16 && kwd == 16) || (kwu == 4 && kwd == 4);
+}
+
+int moe_dec(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
+    int kwu, kwd, waves;
+    GV_REQUIRE(moe_dec_shape(m.c, kwu, kwd, waves), "moe: no decode variant for this shape");
+    MoeArgsDec a{};
+    a.gu_codes = L.gu_codes, a.gu_scales = L.gu_scales, a.dn_codes = L.dn_codes, a.dn_scales = L.dn_scales;
+    a.gu_cstride = m.gu_code_stride, a.gu_sstride = m.gu_scale_stride;
+    a.dn_cstride = m.dn_code_stride, a.dn_sstride = m.dn_scale_stride;
+    a.H = m.c.hidden, a.F = m.c.moe_ff;
+    a.globals = L.expert_globals;
+    a.act = m.act_h, a.act_stride = act_halves(m.c.hidden);
+    a.act_m = m.act_m;
+    a.y = m.y;
+    a.sl = route_slots(m.route + (&L - &m.layers[0]));
+    a.E1 = m.E1, a.max_picks = m.max_picks;
+    const int slots = moe_slots(m, M);
+    if (up) {
+        a.groups = (a.F / kTileR + kMoePairs - 1) / kMoePairs;
+        const size_t lds = static_cast<size_t>(2 * kMoePairs) * waves * 1024;
+        const dim3 grid(static_cast<unsigned>(slots * a.groups));
+        if (kwu == 16) hipLaunchKernelGGL(moe_up_kernel<16>, grid, dim3(64 * waves), lds, st, a);
+        else hipLaunchKernelGGL(moe_up_kernel<4>, grid, dim3(64 * waves), lds, st, a);
+    } else {
+        a.groups = (a.H / kTileR + waves * kMoeDnTiles - 1) / (waves * kMoeDnTiles);
+        const dim3 grid(static_cast<unsigned>(slots * a.groups));
+        if (kwd == 16) hipLaunchKernelGGL(moe_down_kernel<16>, grid, dim3(64 * waves), 0, st, a);
+        else hipLaunchKernelGGL(moe_down_kernel<4>, grid, dim3(64 * waves), 0, st, a);
+    }
+    GV_CHECK_HIP(hipGetLastError());
+    return 0;
 }
 
 // ---------------------------------------------------------------- prefill MoE (C5): many rows
@@ -992,14 +1173,15 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         hipLaunchKernelGGL(route_kernel, dim3(1), dim3(1024), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
                            m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
         return 0;
-    case GV_K_MOE_UP:
-        return moe_products(m, L, M, true, st);
+    case GV_K_MOE_UP:   // with the SwiGLU and its quantization (moe_up_kernel) where the decode variant fits
+        return m.moe_dec ? moe_dec(m, L, M, true, st) : moe_products(m, L, M, true, st);
     case GV_K_SWIGLU:
+        if (m.moe_dec) return 0;
         hipLaunchKernelGGL(swiglu_quant_kernel, dim3(M * (c.top_k + 1)), dim3(256), static_cast<size_t>(c.moe_ff) * 4,
                            st, m.gu_out, c.moe_ff, &m.route[l].n_picks, m.act_m);
         return 0;
     case GV_K_MOE_DOWN:
-        return moe_products(m, L, M, false, st);
+        return m.moe_dec ? moe_dec(m, L, M, false, st) : moe_products(m, L, M, false, st);
     case GV_K_COMBINE: {   // the residual add, then the next layer's input RMSNorm (after the last: the final norm)
         const float *next_norm = m.moe_only                ? nullptr
                                  : l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm
@@ -1031,7 +1213,6 @@ int run_layers(Model &m, int M, hipStream_t st) {
 // the verify step's launches: replayed from the row count's graph when there is one (captured on the second step of
 // that row count, so the first runs the launches directly and sets every kernel's attributes)
 int run_step(Model &m, int M, hipStream_t st) {
-    if (m.use_step_kernel && m.timed_class < 0 && step_supported(m, M, nullptr)) return step_run(m, M, st);
     if (!m.use_graphs || m.timed_class >= 0 || !m.seen[M]) {
         m.seen[M] = true;
         return run_layers(m, M, st);
@@ -1257,13 +1438,18 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         L.kv = m.kv_all + static_cast<size_t>(l) * kv_layer;
     }
     const int Mx = c.max_rows, K = c.top_k;
-    m.max_slots = std::min(c.n_experts, Mx * K) + 1;
+    m.max_slots = moe_slots_bound(c.n_experts, K, Mx);
+    if (m.max_slots > kRouteSlots) return fail("gv_model_create: too many expert slots for the route state");
     m.max_picks = Mx * (K + 1);
     m.kv_blocks = (c.max_ctx + kAttnBlock - 1) / kAttnBlock;
     ok = ok && (m.sp = static_cast<StepParams *>(dalloc(m, sizeof(StepParams))));
     ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * c.n_layers)));
     ok = ok && (m.counter = static_cast<int *>(dalloc(m, 64)));
     ok = ok && hipMemset(m.counter, 0, 64) == hipSuccess;
+    {
+        int kwu, kwd, waves;
+        m.moe_dec = moe_dec_shape(c, kwu, kwd, waves);
+    }
     {   // the buffers one step's phases exchange, in one arena (the persistent kernel addresses them by offset)
         const size_t sizes[] = {static_cast<size_t>(Mx) * H * 4,
                                 static_cast<size_t>(Mx) * qkv_rows(c) * 4,
@@ -1333,6 +1519,11 @@ void gv_model_free(gv_model *g) {
         if (ge) (void)hipGraphExecDestroy(ge);
     for (void *p : g->m.allocs) (void)hipFree(p);
     for (void *p : g->m.pf.allocs) (void)hipFree(p);
+    if (g->m.trace) {   // the kernels stop stamping before the buffer goes
+        uint64_t *none = nullptr;
+        (void)hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &none, sizeof none);
+        (void)hipFree(g->m.trace);
+    }
     delete g;
 }
 
@@ -1340,7 +1531,6 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
                    const float *globals) {
     GV_REQUIRE(g && data, "gv_model_adopt: null pointer");
     Model &m = g->m;
-    if (step_invalidate(m) != 0) return -1;   // the step kernel's copies of the globals are rebuilt on next use
     const auto &c = m.c;
     const int64_t H = c.hidden, F = c.moe_ff, V = c.vocab, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     const bool per_layer = kind != GV_EMBED && kind != GV_LM_HEAD && kind != GV_FINAL_NORM;
@@ -1419,7 +1609,6 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
 int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sigma, int ctx) {
     GV_REQUIRE(g, "gv_model_randomize: null model");
     Model &m = g->m;
-    if (step_invalidate(m) != 0) return -1;
     const auto &c = m.c;
     GV_REQUIRE(ctx >= 0 && ctx + c.max_rows <= c.max_ctx, "gv_model_randomize: ctx too large");
     const int64_t H = c.hidden, F = c.moe_ff, V = c.vocab, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
@@ -1574,7 +1763,6 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     if (logits) {
         GV_CHECK_HIP(hipMemcpyAsync(logits, m.logits, static_cast<size_t>(n) * c.vocab * 4, hipMemcpyDeviceToHost, st));
         GV_CHECK_HIP(hipStreamSynchronize(st));
-        if (step_check(m) != 0) return -1;
     }
     m.last_pos = m.pos;
     m.last_n = n;
@@ -1735,23 +1923,25 @@ int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
     return 0;
 }
 
-int gv_model_set_step_kernel(gv_model *g, int on) {
-    GV_REQUIRE(g, "gv_model_set_step_kernel: null model");
-    g->m.use_step_kernel = on != 0;
+int gv_model_trace(gv_model *g, int on) {
+    GV_REQUIRE(g, "gv_model_trace: null model");
+    Model &m = g->m;
+    const size_t bytes = static_cast<size_t>(GV_K_COUNT) * kTraceWgs * 8 * 8;
+    if (on && !m.trace) {
+        GV_CHECK_HIP(hipMalloc(&m.trace, bytes));
+        GV_CHECK_HIP(hipMemset(m.trace, 0, bytes));
+    }
+    uint64_t *p = on ? m.trace : nullptr;
+    GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));
     return 0;
 }
 
-int gv_model_step_kernel_supported(const gv_model *g, int n) { return g && step_supported(g->m, n, nullptr) ? 1 : 0; }
-
-int gv_model_step_trace(gv_model *g, int on) {
-    GV_REQUIRE(g, "gv_model_step_trace: null model");
-    return step_trace(g->m, on != 0);
-}
-
-int64_t gv_model_step_trace_read(gv_model *g, uint64_t *out, int64_t n) {
-    GV_REQUIRE(g && out && n >= 0, "gv_model_step_trace_read: bad arguments");
-    const int64_t k = step_trace_read(g->m, out, n);
-    GV_REQUIRE(k >= 0, "gv_model_step_trace_read: copy failed");
+int64_t gv_model_trace_read(gv_model *g, uint64_t *out, int64_t n) {
+    GV_REQUIRE(g && out && n >= 0 && g->m.trace, "gv_model_trace_read: no trace");
+    const int64_t have = static_cast<int64_t>(GV_K_COUNT) * kTraceWgs * 8;
+    const int64_t k = std::min(n, have);
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    GV_CHECK_HIP(hipMemcpy(out, g->m.trace, static_cast<size_t>(k) * 8, hipMemcpyDeviceToHost));
     return k;
 }
 

@@ -23,14 +23,17 @@ struct StepParams {
     uint32_t vis[kMaxRows];
 };
 
-// Routing of one layer, written by the route kernel: slots are the distinct experts picked (ascending, the shared
-// expert last, index E), each with its picks (token, rank), picks ordered by (expert, token, rank).
+// Routing of one layer, written by the route kernel: slots are runs of at most kSlotRows picks (token, rank) of one
+// expert, the distinct experts picked ascending (the shared expert last, index E), an expert with more picks taking
+// consecutive slots; picks ordered by (expert, token, rank).
+constexpr int kSlotRows = 8;
+constexpr int kRouteSlots = kMaxRows * 16 + 1;   // >= E + 1 + picks / kSlotRows for every shape the model takes
 struct RouteState {
     int n_slots;
     int n_picks;
-    int slot_expert[kMaxRows * 16 + 1];
-    int slot_start[kMaxRows * 16 + 1];
-    int slot_count[kMaxRows * 16 + 1];
+    int slot_expert[kRouteSlots];
+    int slot_start[kRouteSlots];
+    int slot_count[kRouteSlots];
     int pick_token[kMaxRows * 17];
     int pick_of[kMaxRows * 17];   // [t][k] for k < K the routed pick, [t][K] the shared expert's
     float weight[kMaxRows * 16];  // [t][k]
@@ -104,6 +107,8 @@ struct Model {
     bool moe_only = false;   // gv_model_moe: the router takes the rows as they are, the combine no next norm
     bool route_in_router = false;  // the router's last workgroup routes (off: route_kernel; on measured slower)
     int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
+    bool moe_dec = false;          // the decode MoE kernels (moe_up_kernel, moe_down_kernel), where the shapes fit
+    uint64_t *trace = nullptr;     // gv_model_trace's stamps [GV_K_COUNT][8192 workgroups][8] (allocated when on)
     Prefill pf;
     std::vector<hipEvent_t> events;   // pairs around the timed class's launches
     // the verify step as a HIP graph per row count (captured on its second use; the step's parameters are read
@@ -114,15 +119,6 @@ struct Model {
     size_t events_used = 0;
     StepParams host_sp{};
     int max_slots = 0, max_picks = 0;
-    // the verify step as one persistent kernel (step.hip): on by gv_model_set_step_kernel; set up on first use
-    bool use_step_kernel = false;
-    void *layers_dev = nullptr;                       // LayerDev [n_layers]
-    void *step_dev = nullptr;                         // StepDev [2]: for 1..16 and 17..32 rows
-    unsigned *bar = nullptr;                          // the grid barrier's words; bar_gen: generations used so far
-    unsigned *step_err = nullptr;
-    unsigned bar_gen = 0;
-    int step_grid = 0;                                // workgroups of the launch: one a compute unit
-    uint64_t *stamps = nullptr;                       // the step kernel's barrier clock stamps (when traced)
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes

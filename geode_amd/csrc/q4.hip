@@ -217,7 +217,8 @@ int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm
 
 // ---------------------------------------------------------------- the skinny GEMM (mfma_gemv.hpp)
 // WMAX: the most waves a launch of the instance takes (8: a budget of 256 VGPRs a lane)
-template <int KW, int NTT, int WMAX>
+// PACK: at most 8 rows, their hi and lo halves in the MFMA's two column halves (mfma_tiles)
+template <int KW, int NTT, int WMAX, bool PACK>
 __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16 *__restrict__ act,
                                                             int64_t act_stride, int M, int sc0, int tiles_per_wg,
                                                             GemvOut out) {
@@ -227,11 +228,10 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
     if (t0 >= ntiles) return;
-    mfma_tiles<KW, NTT>(
-        w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, t0, t1, M,
-        [&](int j, int64_t g, h8 &hi, h8 &lo) { load_act16(act + j * act_stride, g, hi, lo); },
-        [&](int64_t row, int j, float v) { out.put(row, j, v); },
-        part_lds, tab);
+    mfma_tiles<KW, NTT, kSplitK, 0, 3, PACK>(
+        w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, static_cast<int>(t1 - t0), M,
+        [&](int j) { return act + j * act_stride; }, [&](int64_t row, int j, float v) { out.put(row, j, v); },
+        part_lds, tab, TileRun{t0});
 }
 
 int mfma_split(int64_t K, int ntt, int &waves, int &kw) {
@@ -250,17 +250,18 @@ int64_t tiles_per_wg(int64_t ntiles, int waves, int ntt) {
     return std::min<int64_t>(cap, std::max<int64_t>(1, (ntiles + resident - 1) / resident));
 }
 
-template <int KW, int NTT, int WMAX>
+template <int KW, int NTT, int WMAX, bool PACK>
 static int launch_gemv(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, int sc0, int waves,
                        const GemvOut &out, hipStream_t st) {
     const int64_t ntiles = tiles_rows(w.rows);
     const int64_t per = tiles_per_wg(ntiles, waves, NTT);
     const int64_t wg = (ntiles + per - 1) / per;
-    const size_t lds = waves > 1 ? static_cast<size_t>(per) * waves * NTT * 1024 : 0;
+    const size_t lds = static_cast<size_t>(per) * waves * NTT * 1024;   // the waves' partial sums
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX>), 76 * 1024, granted) != 0) return -1;
-    hipLaunchKernelGGL((gemv_q4_kernel<KW, NTT, WMAX>), dim3(static_cast<unsigned>(wg)), dim3(64 * waves), lds, st, w,
-                       act, act_stride, M, sc0, static_cast<int>(per), out);
+    if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX, PACK>), 76 * 1024, granted) != 0)
+        return -1;
+    hipLaunchKernelGGL((gemv_q4_kernel<KW, NTT, WMAX, PACK>), dim3(static_cast<unsigned>(wg)), dim3(64 * waves), lds,
+                       st, w, act, act_stride, M, sc0, static_cast<int>(per), out);
     return 0;
 }
 
@@ -272,13 +273,18 @@ static int gemv_range(const Q4 &w, const _Float16 *act, int64_t act_stride, int 
         set_error("gemv_q4: no split of this K range");
         return -1;
     }
-    if (ntt == 1) {
-        if (kw == 16) return launch_gemv<16, 1, 8>(w, act, act_stride, M, sc0, waves, out, st);
-        if (kw == 8) return launch_gemv<8, 1, 8>(w, act, act_stride, M, sc0, waves, out, st);
-        return launch_gemv<4, 1, 8>(w, act, act_stride, M, sc0, waves, out, st);
+    if (ntt == 1 && M <= 8) {
+        if (kw == 16) return launch_gemv<16, 1, 8, true>(w, act, act_stride, M, sc0, waves, out, st);
+        if (kw == 8) return launch_gemv<8, 1, 8, true>(w, act, act_stride, M, sc0, waves, out, st);
+        return launch_gemv<4, 1, 8, true>(w, act, act_stride, M, sc0, waves, out, st);
     }
-    if (kw == 8) return launch_gemv<8, 2, 8>(w, act, act_stride, M, sc0, waves, out, st);
-    return launch_gemv<4, 2, 8>(w, act, act_stride, M, sc0, waves, out, st);
+    if (ntt == 1) {
+        if (kw == 16) return launch_gemv<16, 1, 8, false>(w, act, act_stride, M, sc0, waves, out, st);
+        if (kw == 8) return launch_gemv<8, 1, 8, false>(w, act, act_stride, M, sc0, waves, out, st);
+        return launch_gemv<4, 1, 8, false>(w, act, act_stride, M, sc0, waves, out, st);
+    }
+    if (kw == 8) return launch_gemv<8, 2, 8, false>(w, act, act_stride, M, sc0, waves, out, st);
+    return launch_gemv<4, 2, 8, false>(w, act, act_stride, M, sc0, waves, out, st);
 }
 
 int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st) {

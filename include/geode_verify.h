@@ -159,18 +159,12 @@ enum {
 /* The verify step runs as one HIP graph per row count (captured on the second step of that count and replayed
  * after; every step parameter lives in device memory). on = 0: plain launches (no reference counterpart). */
 int gv_model_set_graphs(gv_model *m, int on);
-/* on = 1: the verify step runs as ONE persistent kernel (a workgroup per compute unit, a cooperative launch, grid
- * barriers between the phases; the same arithmetic and bits as the per-phase kernels), where the model's shapes fit
- * it (gv_model_step_kernel_supported), else the per-phase kernels; on = 0: the per-phase kernels (no reference
- * counterpart: the reference's GPU path is one OpenCL launch per kernel, engine/src/gpu8.cpp:798-1081). */
-int gv_model_set_step_kernel(gv_model *m, int on);
-/* 1 when the persistent step kernel takes n rows of this model, 0 when not */
-int gv_model_step_kernel_supported(const gv_model *m, int n);
-/* A measurement aid with no reference counterpart: with on = 1 every step-kernel workgroup stamps its clock
- * (s_memrealtime, 100 MHz) at each barrier, when it arrives and when its wait ends; gv_model_step_trace_read copies
- * the last step's stamps, [workgroup][barrier][arrive, leave], and returns the count copied (negative on error). */
-int gv_model_step_trace(gv_model *m, int on);
-int64_t gv_model_step_trace_read(gv_model *m, uint64_t *out, int64_t n);
+/* A measurement aid with no reference counterpart: with on = 1, thread 0 of every workgroup of the traced kernels
+ * stamps its clock (s_memrealtime, 100 MHz) at a few points of its work; each launch overwrites its kernel class's
+ * stamps. gv_model_trace_read copies them, [GV_K_COUNT][8192 workgroups][8 slots] (0: none), and returns the count
+ * copied (negative on error). */
+int gv_model_trace(gv_model *m, int on);
+int64_t gv_model_trace_read(gv_model *m, uint64_t *out, int64_t n);
 int gv_model_time_kernel(gv_model *m, int cls);
 int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
 /* Launch kernel class cls of layer `layer` (ignored for GV_K_EMBED / GV_K_LM_HEAD) reps times back to back on the
