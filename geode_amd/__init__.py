@@ -345,7 +345,8 @@ class VerifyModel:
         return out.reshape(len(KERNEL_CLASSES), 8192, 8)
 
     def replay(self, cls, layer=0, reps=20):
-        """mean ms of kernel class cls of one layer, launched reps times back to back on the last verify's state"""
+        """mean ms a launch of kernel class cls, launched reps times back to back on the last verify's state, launch i
+        on layer (layer + i) mod n_layers"""
         ms = _c.c_float(0)
         check(_lib().gv_model_replay(self.h, cls, layer, reps, _c.byref(ms)), "gv_model_replay")
         return ms.value

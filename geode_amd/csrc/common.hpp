@@ -88,6 +88,19 @@ __device__ inline void xstf(float *base, uint32_t i, float v) {
 __device__ inline float4 xld4f(const float *base, uint32_t i) { return __builtin_bit_cast(float4, xld16(base, i * 4u)); }   // i % 4 == 0
 __device__ inline void xst4f(float *base, uint32_t i, float4 v) { xst16(base, i * 4u, __builtin_bit_cast(xu4, v)); }
 
+// ---------------------------------------------------------------- a measurement aid: workgroup clock stamps
+// When a translation unit's g_trace is set (gv_model_trace; each source file's kernels have their own copy), thread 0
+// of each workgroup of the traced kernels writes the 100 MHz clock (s_memrealtime) at a few points to
+// g_trace[(cls * kTraceWgs + workgroup) * 8 + slot]; each launch overwrites its class's stamps, so after a step they
+// are the last layer's. Null (the default): a scalar load (constant memory, cached) and a branch a stamp.
+constexpr int kTraceWgs = 8192;
+static __constant__ uint64_t *g_trace;
+__device__ inline void trace(int cls, int slot) {
+    uint64_t *t = g_trace;
+    if (t && threadIdx.x == 0 && blockIdx.x < kTraceWgs)
+        t[(static_cast<size_t>(cls) * kTraceWgs + blockIdx.x) * 8 + slot] = __builtin_amdgcn_s_memrealtime();
+}
+
 // ---------------------------------------------------------------- device helpers
 __device__ inline float e4m3_to_f32(uint32_t b) {
     // E4M3FN as half bits: exponent and mantissa moved into place, then 2^8 for the bias (15 - 7); exact for every
@@ -136,17 +149,40 @@ __device__ inline double dpp_d(double v) {
     return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// The wave reductions: pairs, quads, 8s and 16s of lanes within each 16-lane row by DPP (every lane then holds its
-// row's value), then the rows combined as (row 0 + row 1) + (row 2 + row 3) through lane swaps (xor 16, xor 32), in
-// vector registers throughout; the same bits in every lane (the swapped operand order gives the same sum)
+// the value of lane l ^ 8 (the other half of the lane's 16-lane row): DPP row_ror:8, no LDS crossbar round trip
+__device__ inline float xor8(float v) { return dpp_f<0x128>(v); }
+
+// The wave reductions, in vector registers throughout (no LDS crossbar round trip): pairs, quads, 8s and 16s of lanes
+// within each 16-lane row by DPP (every lane then holds its row's value), then the rows by DPP row broadcasts (gfx9:
+// row 1 += row 0's lane 15 and row 3 += row 2's, then row 3 += row 1's lane 31), and lane 63's value read out as a
+// uniform one: the sum (row 0 + row 1) + (row 2 + row 3), the same bits whatever the lanes' order within a row pair
+template <int CTRL, int ROWS = 0xF>
+__device__ inline uint32_t dpp_u(uint32_t old, uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v), CTRL, ROWS, 0xF, false));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ inline double dpp_dd(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp_u<CTRL, ROWS>(0u, static_cast<uint32_t>(u));
+    const uint32_t hi = dpp_u<CTRL, ROWS>(0u, static_cast<uint32_t>(u >> 32));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ inline float lane63(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ inline double wave_sum(double v) {
     v += dpp_d<0xB1>(v);
     v += dpp_d<0x4E>(v);
     v += dpp_d<0x141>(v);
     v += dpp_d<0x140>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    v += dpp_dd<0x142, 0xA>(v);   // rows 1, 3: + lane 15 of rows 0, 2 (rows 0, 2: + 0)
+    v += dpp_dd<0x143, 0xC>(v);   // rows 2, 3: + lane 31
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), 63));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 __device__ inline float wave_sum_f(float v) {
@@ -154,20 +190,34 @@ __device__ inline float wave_sum_f(float v) {
     v += dpp_f<0x4E>(v);
     v += dpp_f<0x141>(v);
     v += dpp_f<0x140>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    v += __builtin_bit_cast(float, dpp_u<0x142, 0xA>(0u, __builtin_bit_cast(uint32_t, v)));
+    v += __builtin_bit_cast(float, dpp_u<0x143, 0xC>(0u, __builtin_bit_cast(uint32_t, v)));
+    return lane63(v);
+}
+
+// the inclusive prefix sum over the wave's lanes (integers, exact): shifts 1, 2, 4, 8 within each 16-lane row, then
+// the rows' totals carried by row broadcasts
+__device__ inline int wave_incl_scan(int v) {
+    v += static_cast<int>(dpp_u<0x111>(0u, static_cast<uint32_t>(v)));   // row_shr:1 (lane 0 of a row: + 0)
+    v += static_cast<int>(dpp_u<0x112>(0u, static_cast<uint32_t>(v)));   // row_shr:2
+    v += static_cast<int>(dpp_u<0x114>(0u, static_cast<uint32_t>(v)));   // row_shr:4
+    v += static_cast<int>(dpp_u<0x118>(0u, static_cast<uint32_t>(v)));   // row_shr:8
+    v += static_cast<int>(dpp_u<0x142, 0xA>(0u, static_cast<uint32_t>(v)));   // rows 1, 3: + lane 15 of rows 0, 2
+    v += static_cast<int>(dpp_u<0x143, 0xC>(0u, static_cast<uint32_t>(v)));   // rows 2, 3: + lane 31
     return v;
 }
 
-// the maximum over the wave's 64 lanes, in every lane (a uniform value)
+// the maximum over the wave's 64 lanes, a uniform value
 __device__ inline float wave_max(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v));
     v = fmaxf(v, dpp_f<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_u<0x142, 0xA>(u, u)));   // rows 0, 2 keep their own value
+    const uint32_t u2 = __builtin_bit_cast(uint32_t, v);
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_u<0x143, 0xC>(u2, u2)));
+    return lane63(v);
 }
 
 }  // namespace gv

@@ -45,6 +45,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
             v[i] = live[r] && e < E ? lg[r][e] : -__builtin_inff();
             mx = fmaxf(mx, v[i]);
         }
+        if (r == 0) trace(GV_K_ROUTE, 5);
         mx = wave_max(mx);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -60,6 +61,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
             const int e = lane + 64 * i;
             pv[r][i] = live[r] && e < E ? __fdiv_rn(pv[r][i], sum[r]) : -1.0f;
         }
+    trace(GV_K_ROUTE, 6);
     float top[NR], mine[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) top[r] = mine[r] = 0.0f;
@@ -81,6 +83,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
             top[r] = __fadd_rn(top[r], bv);   // rank order
         }
     }
+    trace(GV_K_ROUTE, 7);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         if (!live[r]) continue;
@@ -115,19 +118,34 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
                                  int32_t *__restrict__ ids_out, const RouteLds &r) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
     const int E1 = E + 1;
+    trace(GV_K_ROUTE, 0);
     for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
-    for (int t0 = wave; t0 < M; t0 += 2 * waves) {   // rows t0 and t0 + waves
-        const int t1 = t0 + waves;
-        const bool l1 = t1 < M;
-        const int t1c = l1 ? t1 : t0;
-        const float *const lg[2] = {logits + static_cast<int64_t>(t0) * E1, logits + static_cast<int64_t>(t1c) * E1};
-        const bool live[2] = {true, l1};
-        int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
-        float *const w[2] = {rs->weight + t0 * K, rs->weight + t1c * K};
-        float *const gate[2] = {rs->gate + t0, rs->gate + t1c};
-        route_rows<2>(lg, live, E, K, ids, w, gate);
+    if (M <= waves) {   // a row a wave
+        if (wave < M) {
+            const int t0 = wave;
+            const float *const lg[1] = {logits + static_cast<int64_t>(t0) * E1};
+            const bool live[1] = {true};
+            int *const ids[1] = {&r.ids[t0 * 16]};
+            float *const w[1] = {rs->weight + t0 * K};
+            float *const gate[1] = {rs->gate + t0};
+            route_rows<1>(lg, live, E, K, ids, w, gate);
+        }
+    } else {
+        for (int t0 = wave; t0 < M; t0 += 2 * waves) {   // rows t0 and t0 + waves
+            const int t1 = t0 + waves;
+            const bool l1 = t1 < M;
+            const int t1c = l1 ? t1 : t0;
+            const float *const lg[2] = {logits + static_cast<int64_t>(t0) * E1,
+                                        logits + static_cast<int64_t>(t1c) * E1};
+            const bool live[2] = {true, l1};
+            int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
+            float *const w[2] = {rs->weight + t0 * K, rs->weight + t1c * K};
+            float *const gate[2] = {rs->gate + t0, rs->gate + t1c};
+            route_rows<2>(lg, live, E, K, ids, w, gate);
+        }
     }
     __syncthreads();
+    trace(GV_K_ROUTE, 1);
     for (int i = tid; i < M * K; i += blockDim.x) {
         const int t = i / K, e = r.ids[t * 16 + i % K];
         ids_out[i] = e;
@@ -136,15 +154,12 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
     }
     if (tid == 0) r.cnt[E] = M;
     __syncthreads();
+    trace(GV_K_ROUTE, 2);
     {   // exclusive scans over the E + 1 counters (starts, slot numbers): two a thread, waves, the waves' totals
         const int e0 = 2 * tid, e1 = e0 + 1;
         const int c0 = e0 <= E ? r.cnt[e0] : 0, c1 = e1 <= E ? r.cnt[e1] : 0;
         const int u0 = (c0 + kSlotRows - 1) / kSlotRows, u1 = (c1 + kSlotRows - 1) / kSlotRows;   // slots
-        int ic = c0 + c1, iu = u0 + u1;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int pc = __shfl_up(ic, o, 64), pu = __shfl_up(iu, o, 64);
-            if (lane >= o) ic += pc, iu += pu;
-        }
+        const int ic = wave_incl_scan(c0 + c1), iu = wave_incl_scan(u0 + u1);
         if (lane == 63) r.wtot[0][wave] = ic, r.wtot[1][wave] = iu;
         __syncthreads();
         int bc = 0, bu = 0;
@@ -162,6 +177,7 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         }
     }
     __syncthreads();
+    trace(GV_K_ROUTE, 3);
     for (int e = tid; e <= E; e += blockDim.x)
         if (r.slot_of[e] >= 0)
             for (int k = 0; k * kSlotRows < r.cnt[e]; ++k) {
@@ -179,6 +195,7 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         rs->pick_token[pk] = t;
         rs->pick_of[t * (K + 1) + k] = pk;
     }
+    trace(GV_K_ROUTE, 4);
 }
 
 }  // namespace gv

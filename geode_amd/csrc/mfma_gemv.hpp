@@ -342,7 +342,7 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             if (PACK) {   // column j < 8: hi sum + the lo sum from column j + 8 (lane l ^ 8)
                 f4 lo;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) lo[r] = __shfl_xor(acc[0][tt][r], 8, 64);
+                for (int r = 0; r < 4; ++r) lo[r] = xor8(acc[0][tt][r]);
                 acc[0][tt] += lo;
             } else {
                 acc[0][tt] += acc[NB - 1][tt];

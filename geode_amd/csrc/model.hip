@@ -21,18 +21,6 @@
 
 namespace gv {
 
-// ---------------------------------------------------------------- a measurement aid: workgroup clock stamps
-// When g_trace is set (gv_model_trace), thread 0 of each workgroup of the traced kernels writes the 100 MHz clock
-// (s_memrealtime) at a few points to g_trace[(cls * kTraceWgs + workgroup) * 8 + slot]; each launch overwrites its
-// class's stamps, so after a step they are the last layer's. Null (the default): one scalar load and branch a stamp.
-constexpr int kTraceWgs = 8192;
-__device__ uint64_t *g_trace;
-__device__ inline void trace(int cls, int slot) {
-    uint64_t *t = g_trace;
-    if (t && threadIdx.x == 0 && blockIdx.x < kTraceWgs)
-        t[(static_cast<size_t>(cls) * kTraceWgs + blockIdx.x) * 8 + slot] = __builtin_amdgcn_s_memrealtime();
-}
-
 // ---------------------------------------------------------------- kernels
 // the rows' embeddings: dequant_row of the embedding matrix (pack.cpp:356-366), bit for bit, to x; then the first
 // layer's input RMSNorm and its operands (norm_quant_regs). A workgroup (256 threads) per row.
@@ -145,12 +133,32 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
                                                          int nkv, int hd, const StepParams *__restrict__ sp,
                                                          float *__restrict__ parts, int nb_max) {
     extern __shared__ _Float16 lds_h[];
+    trace(GV_K_ATTN, 0);
     const int b = blockIdx.x, kh = blockIdx.y;
     const int pos = sp->pos, M = sp->M, total = pos + M;
     const int s0 = b * kAttnBlock;
     if (s0 >= total) return;
     const int kld = attn_k_ld(hd);
     _Float16 *ks = lds_h, *vs = lds_h + kAttnBlock * kld;
+    const int group = nh / nkv, NQ = group * M, nqt = (NQ + 15) / 16;
+    const int wave = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
+    const int nch = hd / 32;
+    const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
+    // the queries of tile qt as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query qt * 16 + lq
+    auto load_q = [&](int qt, half8 (&qb)[8], half8 (&ql)[8]) {
+        const int qi = qt * 16 + lq;
+        const bool ok = qi < NQ;
+        const int tq = ok ? qi / group : 0, hq = kh * group + (ok ? qi % group : 0);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) {
+            const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            const int64_t qo = (static_cast<int64_t>(tq) * nh + hq) * hd + ch * 32 + 8 * lg;
+            qb[ch] = (ok && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qo) : z;
+            ql[ch] = (ok && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
+        }
+    };
+    half8 qb[8], ql[8];
+    load_q(wave, qb, ql);   // the wave's first tile of queries, in flight with the staging loads
     {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load, every load of
         // the thread issued before the first store (hd / 32 <= 8 of each)
         const _Float16 *kg = kv + k_index(slots, hd, kh, s0, 0);
@@ -188,24 +196,13 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
         }
     }
     __syncthreads();
-    const int group = nh / nkv, NQ = group * M, nqt = (NQ + 15) / 16;
-    const int wave = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
-    const int nch = hd / 32;
+    trace(GV_K_ATTN, 1);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(hd)));
-    const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
     for (int qt = wave; qt < nqt; qt += 4) {
+        if (qt != wave) load_q(qt, qb, ql);
         const int qi = qt * 16 + lq;
         const bool qvalid = qi < NQ;
         const int tq = qvalid ? qi / group : 0, hq = kh * group + (qvalid ? qi % group : 0);
-        // the queries as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query lq
-        half8 qb[8], ql[8];
-#pragma unroll
-        for (int ch = 0; ch < 8; ++ch) {
-            const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            const int64_t qo = (static_cast<int64_t>(tq) * nh + hq) * hd + ch * 32 + 8 * lg;
-            qb[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qo) : z;
-            ql[ch] = (qvalid && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
-        }
         const uint32_t vis = qvalid ? sp->vis[tq] : 0u;
         // the four 16-position tiles' scores, hi and lo products apart: eight independent MFMA chains
         float4v ch_[4], cl_[4];
@@ -232,6 +229,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
                 sc[pt][r] = ok ? (ch_[pt][r] + cl_[pt][r]) * scale : -__builtin_inff();
                 mx = fmaxf(mx, sc[pt][r]);
             }
+        if (qt == wave) trace(GV_K_ATTN, 2);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         float lsum = 0.0f;
@@ -289,6 +287,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             dst[hd] = mx;
             dst[hd + 1] = lsum;
         }
+        if (qt == wave) trace(GV_K_ATTN, 3);
     }
 }
 
@@ -303,72 +302,94 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     __shared__ float fw[1024];
     __shared__ float red[2][4];
     __shared__ float4 osum[4][64];
+    trace(GV_K_MERGE, 0);
     const int t = blockIdx.x, h = blockIdx.y;
     if (t >= sp->M) return;
     const int nbw = (sp->pos + sp->M + kAttnBlock - 1) / kAttnBlock;
     const int ld = hd + 2;
     const float *base = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max) * ld;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float mx = -__builtin_inff();
-    for (int b = threadIdx.x; b < nbw; b += 256) mx = fmaxf(mx, base[b * ld + hd]);
+    // Every load of the first pass issued at once: the blocks' maxima and sums (four blocks a thread), the first
+    // kMergeBatch blocks' values of the wave (blocks wave, wave + 4, ...; four dims a lane) and the gate values of
+    // wave 0's output dims; the values do not wait for the maximum (their weights are applied after).
+    constexpr int kMergeBatch = 20;   // blocks a wave (80 blocks a workgroup)
+    float bm[4], bs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int bb = threadIdx.x + 256 * k;
+        bm[k] = bb < nbw ? base[bb * ld + hd] : -__builtin_inff();
+        bs[k] = bb < nbw ? base[bb * ld + hd + 1] : 0.0f;
+    }
+    const bool dl = lane * 4 < hd;
+    float4 pv[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+        const int bb = wave + 4 * u;
+        pv[u] = dl && bb < nbw ? *reinterpret_cast<const float4 *>(base + bb * ld + lane * 4) : make_float4(0, 0, 0, 0);
+    }
+    const int ng = hd / 8;
+    float gate[8];
+    {
+        const bool live = wave == 0 && lane < ng;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            gate[i] = live ? qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + 8 * lane + i] : 0.0f;
+    }
+    float mx = fmaxf(fmaxf(bm[0], bm[1]), fmaxf(bm[2], bm[3]));
     mx = wave_max(mx);
     if (lane == 0) red[0][wave] = mx;
     __syncthreads();
+    trace(GV_K_MERGE, 1);
     mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     float l = 0.0f;
-    for (int b = threadIdx.x; b < nbw; b += 256) {
-        const float mb = base[b * ld + hd];
-        const float f = mb == -__builtin_inff() ? 0.0f : expf(__fsub_rn(mb, mx));
-        fw[b] = f;
-        l = __builtin_fmaf(base[b * ld + hd + 1], f, l);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int bb = threadIdx.x + 256 * k;
+        if (bb >= nbw) break;
+        const float f = bm[k] == -__builtin_inff() ? 0.0f : expf(__fsub_rn(bm[k], mx));
+        fw[bb] = f;
+        l = __builtin_fmaf(bs[k], f, l);
     }
     l = static_cast<float>(wave_sum(static_cast<double>(l)));
     if (lane == 0) red[1][wave] = l;
     __syncthreads();
     const float inv = __fdiv_rn(1.0f, ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3]);
-    // wave w: blocks w, w + 4, ...; lane: dims 4 lane .. 4 lane + 3 (hd / 4 lanes)
+    // wave w: blocks w, w + 4, ... in order; lane: dims 4 lane .. 4 lane + 3 (hd / 4 lanes)
     float4 o = make_float4(0, 0, 0, 0);
-    if (lane * 4 < hd) {
-        int b = wave;
-        for (; b + 60 < nbw; b += 64) {   // sixteen blocks' loads ahead of their sums
-            float4 v[16];
+    if (dl) {
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const int bb = wave + 4 * u;
+            const float f = bb < nbw ? fw[bb] : 0.0f;
+            o.x = __builtin_fmaf(pv[u].x, f, o.x);
+            o.y = __builtin_fmaf(pv[u].y, f, o.y);
+            o.z = __builtin_fmaf(pv[u].z, f, o.z);
+            o.w = __builtin_fmaf(pv[u].w, f, o.w);
+        }
+        for (int b = wave + 4 * kMergeBatch; b < nbw; b += 64) {   // longer contexts: sixteen blocks at a time
+            float4 w4[16];
             float f[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-                v[u] = *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4);
-                f[u] = fw[b + 4 * u];
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                o.x = __builtin_fmaf(v[u].x, f[u], o.x);
-                o.y = __builtin_fmaf(v[u].y, f[u], o.y);
-                o.z = __builtin_fmaf(v[u].z, f[u], o.z);
-                o.w = __builtin_fmaf(v[u].w, f[u], o.w);
-            }
-        }
-        for (; b < nbw; b += 16) {   // the rest, four at a time
-            float4 v[4];
-            float f[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
                 const bool in = b + 4 * u < nbw;
-                v[u] = in ? *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4) : make_float4(0, 0, 0, 0);
+                w4[u] = in ? *reinterpret_cast<const float4 *>(base + (b + 4 * u) * ld + lane * 4) : make_float4(0, 0, 0, 0);
                 f[u] = in ? fw[b + 4 * u] : 0.0f;
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                o.x = __builtin_fmaf(v[u].x, f[u], o.x);
-                o.y = __builtin_fmaf(v[u].y, f[u], o.y);
-                o.z = __builtin_fmaf(v[u].z, f[u], o.z);
-                o.w = __builtin_fmaf(v[u].w, f[u], o.w);
+            for (int u = 0; u < 16; ++u) {
+                o.x = __builtin_fmaf(w4[u].x, f[u], o.x);
+                o.y = __builtin_fmaf(w4[u].y, f[u], o.y);
+                o.z = __builtin_fmaf(w4[u].z, f[u], o.z);
+                o.w = __builtin_fmaf(w4[u].w, f[u], o.w);
             }
         }
     }
     osum[wave][lane] = o;
     __syncthreads();
+    trace(GV_K_MERGE, 2);
     // the gated output, 8 dims (one k-group of the projection's operands) a lane of wave 0
     if (wave == 0) {
-        const int g = lane, ng = hd / 8;
+        const int g = lane;
         const bool live = g < ng;
         float v[8];
 #pragma unroll
@@ -383,14 +404,13 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int d = 8 * g + 4 * half + i;
-                const float gate = live ? qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + d] : 0.0f;
-                const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate)));
+                const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate[4 * half + i])));
                 v[4 * half + i] = __fmul_rn(__fmul_rn(sv[i], inv), sig);
             }
         }
         act16_group(v, h * ng + g, live, act + static_cast<int64_t>(t) * act_stride);
     }
+    trace(GV_K_MERGE, 3);
 }
 
 // the route alone (rows' logits given after the router: the MoE block entry point)
@@ -435,6 +455,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     float *hs = lds_f;                 // [TG][ldh] the normalized rows
     float *ws = hs + TG * ldh;         // [4][H] the router rows as fp32
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    trace(GV_K_ROUTER, 0);
     const int M = sp->M, r0 = blockIdx.x * kRouterRows;
     // the workgroup's router rows: 4 x H bf16, 8 a load (H / 256 loads a thread)
     uint4 wr[GPT * 4];
@@ -476,8 +497,10 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
             }
         // 1 / RMS per row: the thread's squares, the wave sums, the waves' in order
         __syncthreads();   // the previous group's sums are done with hs and red
+        trace(GV_K_ROUTER, 1);
 #pragma unroll
         for (int tt = 0; tt < TG; ++tt) {
+            if (tt >= nt) break;   // uniform
             double ss = 0.0;
 #pragma unroll
             for (int q = 0; q < GPT; ++q)
@@ -525,6 +548,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
             }
         }
         __syncthreads();
+        trace(GV_K_ROUTER, 2);
         const int tt = lane / 8, j = lane % 8;
         const int ra = r0 + wave;
         if (ra >= E1) continue;
@@ -547,6 +571,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
         const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
         if (j == 0 && tt < nt) logits[static_cast<int64_t>(t0 + tt) * E1 + ra] = s3;
     }
+    trace(GV_K_ROUTER, 3);
     if (!route) return;
     // the last workgroup to finish routes the rows (the others' logits made visible by their fences)
     __shared__ int s_last;
@@ -1522,6 +1547,7 @@ void gv_model_free(gv_model *g) {
     if (g->m.trace) {   // the kernels stop stamping before the buffer goes
         uint64_t *none = nullptr;
         (void)hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &none, sizeof none);
+        (void)trace_set_q4(nullptr);
         (void)hipFree(g->m.trace);
     }
     delete g;
@@ -1818,8 +1844,8 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
     GV_CHECK_HIP(hipEventCreate(&e0));
     GV_CHECK_HIP(hipEventCreate(&e1));
     GV_CHECK_HIP(hipEventRecord(e0, st));
-    int rc = 0;
-    for (int i = 0; i < reps && rc == 0; ++i) rc = launch_class(m, cls, layer, m.last_n, st);
+    int rc = 0;   // launch i on layer (layer + i) mod n_layers: each launch reads other weights than the last
+    for (int i = 0; i < reps && rc == 0; ++i) rc = launch_class(m, cls, (layer + i) % m.c.n_layers, m.last_n, st);
     GV_CHECK_HIP(hipEventRecord(e1, st));
     GV_CHECK_HIP(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -1933,7 +1959,7 @@ int gv_model_trace(gv_model *g, int on) {
     }
     uint64_t *p = on ? m.trace : nullptr;
     GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));
-    return 0;
+    return trace_set_q4(p);
 }
 
 int64_t gv_model_trace_read(gv_model *g, uint64_t *out, int64_t n) {

@@ -234,6 +234,11 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
         part_lds, tab, TileRun{t0});
 }
 
+int trace_set_q4(uint64_t *p) {
+    GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));
+    return 0;
+}
+
 int mfma_split(int64_t K, int ntt, int &waves, int &kw) {
     const int chunks = static_cast<int>(K / 32);
     kw = ntt == 1 ? 16 : 8;
