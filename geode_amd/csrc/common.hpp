@@ -55,7 +55,10 @@ struct Q4 {
 
 inline int64_t q4_tile_rows(int64_t rows) { return (rows + 15) / 16 * 16; }
 inline size_t q4_code_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(q4_tile_rows(rows)) * static_cast<size_t>(cols / 2); }
-inline size_t q4_scale_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(q4_tile_rows(rows)) * static_cast<size_t>(cols / 16); }
+// the scales: per 16-row tile, per quad of four 128-value super-chunks, 512 bytes (a lane's four words adjacent)
+inline size_t q4_scale_bytes(int64_t rows, int64_t cols) {
+    return static_cast<size_t>(q4_tile_rows(rows) / 16) * static_cast<size_t>((cols / 128 + 3) / 4) * 512;
+}
 // one row's activations for the products: cols fp16 hi + lo halves (mfma_gemv.hpp)
 inline size_t act_bytes(int64_t cols) { return static_cast<size_t>(cols) * 4; }
 __host__ __device__ inline int64_t act_halves(int64_t cols) { return cols * 2; }
@@ -97,8 +100,12 @@ constexpr int kTraceWgs = 8192;
 static __constant__ uint64_t *g_trace;
 __device__ inline void trace(int cls, int slot) {
     uint64_t *t = g_trace;
-    if (t && threadIdx.x == 0 && blockIdx.x < kTraceWgs)
-        t[(static_cast<size_t>(cls) * kTraceWgs + blockIdx.x) * 8 + slot] = __builtin_amdgcn_s_memrealtime();
+    if (t && threadIdx.x == 0 && blockIdx.x < kTraceWgs) {
+        uint64_t *w = t + (static_cast<size_t>(cls) * kTraceWgs + blockIdx.x) * 8;
+        w[slot] = __builtin_amdgcn_s_memrealtime();
+        if (slot == 0)   // where the workgroup runs: XCC id (high word) and HW_ID (CU, SH, SE: low word)
+            w[7] = (static_cast<uint64_t>(__builtin_amdgcn_s_getreg(0xF814)) << 32) | __builtin_amdgcn_s_getreg(0xF804);
+    }
 }
 
 // ---------------------------------------------------------------- device helpers

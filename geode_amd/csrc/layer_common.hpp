@@ -186,7 +186,9 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
                 rs->slot_start[u] = r.start[e] + k * kSlotRows;
                 rs->slot_count[u] = min(kSlotRows, r.cnt[e] - k * kSlotRows);
             }
-    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once)
+    // pick (t, k) of expert e goes after the earlier rows' picks of e (a row picks an expert at most once); its
+    // row also goes to its slot's token list (a slot's unused entries: the slot's first row, by the pick before = 0
+    // of each slot writing them)
     for (int i = tid; i < M * (K + 1); i += blockDim.x) {
         const int t = i / (K + 1), k = i % (K + 1);
         const int e = k < K ? r.ids[t * 16 + k] : E;
@@ -194,6 +196,14 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         const int pk = r.start[e] + before;
         rs->pick_token[pk] = t;
         rs->pick_of[t * (K + 1) + k] = pk;
+        const int u = r.slot_of[e] + before / kSlotRows, j = before % kSlotRows;
+        const int n = min(kSlotRows, r.cnt[e] - (before / kSlotRows) * kSlotRows);
+        if (j > 0) {
+            rs->slot_token[u * kSlotRows + j] = t;
+        } else {
+            for (int jj = n; jj < kSlotRows; ++jj) rs->slot_token[u * kSlotRows + jj] = t;
+            rs->slot_token[u * kSlotRows] = t;
+        }
     }
     trace(GV_K_ROUTE, 4);
 }

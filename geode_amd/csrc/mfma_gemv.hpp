@@ -11,9 +11,10 @@
 // The q4 layout of these kernels ("tiles"): rows in tiles of 16, K in super-chunks of 128 values. A tile's
 // super-chunk is 1 KB of codes: lane l (row l % 16, k-group g = l / 16) has 16 bytes = the pack's code words
 // 16 sc + 4 j + g (j = 0..3: the 32-value chunks of the super-chunk, 8 values of the k-group each), nibbles remapped
-// to the affine order (level = 2c' - 15) and placed for decode8 (tile_word); then 128 bytes of E4M3 scales, byte
-// (r * 2 + g / 2) * 4 + j = the block of chunk j that k-group g falls in. One load instruction of a wave reads the
-// 1 KB whole.
+// to the affine order (level = 2c' - 15) and placed for decode8 (tile_word). One load instruction of a wave reads the
+// 1 KB whole. The E4M3 scales apart, per tile and per quad of four super-chunks (sc = 4 q + s), 512 bytes: byte
+// ((r * 2 + g / 2) * 4 + s) * 4 + j = the block of chunk j of super-chunk sc that k-group g falls in, so a lane's
+// words of the quad's four super-chunks are one 16-byte load (tq4_scale_off).
 #pragma once
 
 #include "common.hpp"
@@ -31,7 +32,11 @@ constexpr int kSuperK = 128;  // values a super-chunk
 
 __host__ __device__ inline int64_t tiles_rows(int64_t rows) { return (rows + kTileR - 1) / kTileR; }
 inline size_t tq4_code_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * kTileR * (cols / 2); }
-inline size_t tq4_scale_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * kTileR * (cols / 16); }
+inline size_t tq4_scale_bytes(int64_t rows, int64_t cols) { return static_cast<size_t>(tiles_rows(rows)) * ((cols / kSuperK + 3) / 4) * 512; }
+// the byte of the scale of (tile T, super-chunk sc, row r of the tile, k-group g, chunk j); nsq = quads a tile row
+__host__ __device__ inline int64_t tq4_scale_off(int64_t T, int64_t nsq, int64_t sc, int64_t r, int64_t g, int64_t j) {
+    return (T * nsq + sc / 4) * 512 + ((r * 2 + g / 2) * 4 + sc % 4) * 4 + j;
+}
 
 // The activations' layout for these kernels: per row, per k-group g (values 8 g .. 8 g + 7; chunk g / 4, k-group g % 4
 // of it), 8 hi halves then 8 lo halves (32 bytes) of values 8 g + (0 4 1 5 2 6 3 7), the order the nibble pairs come
@@ -187,7 +192,7 @@ __device__ inline void tq4_word(const Q4 &w, int64_t r, int64_t wi, uint32_t &wo
     const int64_t sc = wi / 16, j = (wi % 16) / 4, g = wi % 4;
     const int64_t blk = T * nsc + sc;
     word = untile_word(*reinterpret_cast<const uint32_t *>(w.codes + blk * 1024 + (rr + 16 * g) * 16 + j * 4));
-    scale = w.scales[blk * 128 + (rr * 2 + g / 2) * 4 + j];
+    scale = w.scales[tq4_scale_off(T, (nsc + 3) / 4, sc, rr, g, j)];
 }
 
 // The scale table: per E4M3 byte, the fp16 pairs (e4 / 32, -47 e4). With a nibble c' at bits 6..9 of the fp16
@@ -230,6 +235,11 @@ __device__ inline void load_act16(const _Float16 *ar, int64_t g, h8 &hi, h8 &lo)
     lo = *reinterpret_cast<const h8 *>(p + 8);
 }
 
+// An act16 row of zeros for the operand rows past M (64 KB: rows of up to 16,384 values): loading zeros instead of
+// zeroing the registers after a load keeps the compiler from waiting for every load in flight before the first tile
+static __device__ uint4 g_zero_act16[4096];
+constexpr int64_t kMaxActCols = 16384;
+
 // The tiles a call takes: local tile i is tile t0 + i of the matrix (a run), or any map i -> tile
 struct TileRun {
     int64_t t0;
@@ -270,7 +280,10 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
     constexpr int NS = KW / 4;   // super-chunks a wave takes
     const uint32_t magic = 0x64006400u;
     const uint8_t *cbase = codes + static_cast<int64_t>(sc0 + w * NS) * 1024 + l * 16;
-    const uint8_t *sbase = scales + static_cast<int64_t>(sc0 + w * NS) * 128 + (lq * 2 + lg / 2) * 4;
+    // the lane's scale words of its NS super-chunks: adjacent in one quad (sc0 a multiple of 4, NS = 1, 2 or 4)
+    const uint32_t nsq_u = static_cast<uint32_t>((nsc + 3) / 4);
+    const uint8_t *sbase =
+        scales + static_cast<int64_t>((sc0 + w * NS) / 4) * 512 + ((lq * 2 + lg / 2) * 4 + (sc0 + w * NS) % 4) * 4;
     // Every load is issued unconditionally (a tile past nt reads the last tile again, from the cache): a branch
     // around a load makes the compiler wait for nearly all loads in flight before the next use. Offsets in 32 bits
     // (a matrix < 4 GB).
@@ -282,21 +295,33 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             const uint32_t blk = T * nsc_u + static_cast<uint32_t>(s);
             const u4v v = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(cbase + blk * 1024u));
             cw[s] = make_uint4(v.x, v.y, v.z, v.w);
-            sw[s] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(sbase + blk * 128u));
+        }
+        const uint8_t *sp = sbase + T * nsq_u * 512u;
+        if constexpr (NS == 4) {
+            const u4v v = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(sp));
+            sw[0] = v.x, sw[1] = v.y, sw[2] = v.z, sw[3] = v.w;
+        } else if constexpr (NS == 2) {
+            typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+            const u2v v = __builtin_nontemporal_load(reinterpret_cast<const u2v *>(sp));
+            sw[0] = v.x, sw[1] = v.y;
+        } else {
+            sw[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(sp));
         }
     };
-    // the first tiles' weights (HBM, the longest wait) first
+    // the first two tiles' weights (HBM, the longest wait) first, then the activations, then the rest of the
+    // prologue's tiles: loads complete in issue order, so the first tile waits for two tiles and the activations only
+    constexpr int PRE = DEPTH - 1 < 2 ? DEPTH - 1 : 2;
     uint4 cw[DEPTH][NS];
     uint32_t sw[DEPTH][NS];
 #pragma unroll
-    for (int d = 0; d < DEPTH - 1; ++d) load(d, cw[d], sw[d]);
+    for (int d = 0; d < PRE; ++d) load(d, cw[d], sw[d]);
     hook();
-    // the activations of this wave's K range, resident for all the tiles (rows past M: row M - 1's, then zeros)
+    // the activations of this wave's K range, resident for all the tiles (rows past M: zeros)
     h8 b[NB][KW][NTT];
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
         const int j = PACK ? lq % 8 : tt * 16 + lq;
-        const _Float16 *row = rowp(j < M ? j : M - 1);
+        const _Float16 *row = j < M ? rowp(j) : reinterpret_cast<const _Float16 *>(g_zero_act16);
 #pragma unroll
         for (int c = 0; c < KW; ++c) {
             const int64_t g = (static_cast<int64_t>(sc0) * 4 + w * KW + c) * 4 + lg;
@@ -308,15 +333,10 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             }
         }
     }
+#pragma unroll
+    for (int d = PRE; d < DEPTH - 1; ++d) load(d, cw[d], sw[d]);
     fill_e4m3_table(tab);
     __syncthreads();
-#pragma unroll
-    for (int tt = 0; tt < NTT; ++tt)
-        if ((PACK ? lq % 8 : tt * 16 + lq) >= M)
-#pragma unroll
-            for (int c = 0; c < KW; ++c)
-#pragma unroll
-                for (int h = 0; h < NB; ++h) b[h][c][tt] = h8{0, 0, 0, 0, 0, 0, 0, 0};
     auto tile = [&](int i, const uint4 (&cq)[NS], const uint32_t (&sq)[NS]) {
         f4 acc[NB][NTT];   // the hi and lo products apart: two independent MFMA chains (packed: two column halves)
 #pragma unroll

@@ -128,10 +128,14 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
 // Writes the block's partial (weighted values, max, sum) as attend_heads does per block (model.cpp:3894-4018);
 // attn_merge joins them.
 
+// NCH = head_dim / 32: every loop over the head's dims, and every load, fixed at compile time (no branch around a
+// load, so the compiler waits for exactly the loads each step needs)
+template <int NCH>
 __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restrict__ q16,
                                                          const _Float16 *__restrict__ kv, int64_t slots, int nh,
-                                                         int nkv, int hd, const StepParams *__restrict__ sp,
+                                                         int nkv, const StepParams *__restrict__ sp,
                                                          float *__restrict__ parts, int nb_max) {
+    constexpr int hd = NCH * 32;
     extern __shared__ _Float16 lds_h[];
     trace(GV_K_ATTN, 0);
     const int b = blockIdx.x, kh = blockIdx.y;
@@ -142,25 +146,26 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
     _Float16 *ks = lds_h, *vs = lds_h + kAttnBlock * kld;
     const int group = nh / nkv, NQ = group * M, nqt = (NQ + 15) / 16;
     const int wave = threadIdx.x / 64, l = threadIdx.x % 64, lq = l % 16, lg = l / 16;
-    const int nch = hd / 32;
     const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
     // the queries of tile qt as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query qt * 16 + lq
-    auto load_q = [&](int qt, half8 (&qb)[8], half8 (&ql)[8]) {
+    auto load_q = [&](int qt, half8 (&qb)[NCH], half8 (&ql)[NCH]) {
         const int qi = qt * 16 + lq;
-        const bool ok = qi < NQ;
+        const bool ok = qi < NQ;   // (a query past the tile's end reads query 0 and is zeroed)
         const int tq = ok ? qi / group : 0, hq = kh * group + (ok ? qi % group : 0);
+        const _Float16 *qp = q16 + (static_cast<int64_t>(tq) * nh + hq) * hd + 8 * lg;
 #pragma unroll
-        for (int ch = 0; ch < 8; ++ch) {
+        for (int ch = 0; ch < NCH; ++ch) {
             const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            const int64_t qo = (static_cast<int64_t>(tq) * nh + hq) * hd + ch * 32 + 8 * lg;
-            qb[ch] = (ok && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qo) : z;
-            ql[ch] = (ok && ch < nch) ? *reinterpret_cast<const half8 *>(q16 + qlo + qo) : z;
+            const half8 a = *reinterpret_cast<const half8 *>(qp + ch * 32);
+            const half8 c = *reinterpret_cast<const half8 *>(qp + qlo + ch * 32);
+            qb[ch] = ok ? a : z;
+            ql[ch] = ok ? c : z;
         }
     };
-    half8 qb[8], ql[8];
+    half8 qb[NCH], ql[NCH];
     load_q(wave, qb, ql);   // the wave's first tile of queries, in flight with the staging loads
     {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load, every load of
-        // the thread issued before the first store (hd / 32 <= 8 of each)
+        // the thread issued before the first store (NCH of each)
         const _Float16 *kg = kv + k_index(slots, hd, kh, s0, 0);
         const _Float16 *vg = kv + v_index(slots, hd, nkv, kh, s0, 0);
         const int kpr = hd / 8;   // loads a key row
@@ -171,8 +176,8 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             if (u >= nl) break;
             const int i = threadIdx.x + u * 256;
             const int r = i / kpr, c = i % kpr;
-            kr[u] = s0 + r < total ? *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8)
-                                   : make_uint4(0, 0, 0, 0);
+            const uint4 kk = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8);
+            kr[u] = s0 + r < total ? kk : make_uint4(0, 0, 0, 0);   // (rows past the context: inside the cache)
             vr[u] = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(i) * 8);
         }
 #pragma unroll
@@ -209,8 +214,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) ch_[pt] = cl_[pt] = float4v{0, 0, 0, 0};
 #pragma unroll
-        for (int ch = 0; ch < 8; ++ch) {
-            if (ch >= nch) break;
+        for (int ch = 0; ch < NCH; ++ch) {
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
                 const half8 a = *reinterpret_cast<const half8 *>(ks + (pt * 16 + lq) * kld + 8 * lg + ch * 32);
@@ -649,12 +653,15 @@ struct MoeArgsDec {
     int groups, E1, max_picks;
 };
 
-// the slot of this workgroup (blockIdx / groups) and its expert, first pick and pick count: all four loaded at once
-// (the slot's entries are read before knowing it is live; every index is inside the route state); false: no slot
-__device__ inline bool moe_slot(const MoeArgsDec &a, int u, int &e, int &start, int &cnt) {
+// the slot of this workgroup (blockIdx / groups) and its expert, first pick and pick count, and the lane's pick's
+// row (pick lane % 8 of the slot; a lane past the count: the slot's first): all loaded at once (the slot's entries
+// are read before knowing it is live; every index is inside the route state); false: no slot
+__device__ inline bool moe_slot(const MoeArgsDec &a, int u, int &e, int &start, int &cnt, int &tok) {
     const int ns = *a.sl.n_slots;
     e = a.sl.expert[u], start = a.sl.start[u], cnt = a.sl.count[u];
-    return u < ns && e >= 0 && e < a.E1 && cnt >= 1 && cnt <= kSlotRows && start >= 0 && start + cnt <= a.max_picks;
+    tok = a.sl.token[u * kSlotRows + (threadIdx.x % 64) % 8];
+    return u < ns && e >= 0 && e < a.E1 && cnt >= 1 && cnt <= kSlotRows && start >= 0 && start + cnt <= a.max_picks &&
+           tok >= 0 && tok < kMaxRows;
 }
 
 template <int KWU>
@@ -663,8 +670,8 @@ __global__ __launch_bounds__(256) void moe_up_kernel(const MoeArgsDec a) {
     __shared__ uint2 tab[256];
     trace(GV_K_MOE_UP, 0);
     const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
-    int e, start, cnt;
-    if (!moe_slot(a, u, e, start, cnt)) return;
+    int e, start, cnt, tok;
+    if (!__builtin_amdgcn_readfirstlane(moe_slot(a, u, e, start, cnt, tok))) return;
     trace(GV_K_MOE_UP, 4);
     const int F = a.F, W = blockDim.x / 64, lane = threadIdx.x % 64;
     const int64_t act_m_stride = act_halves(F);
@@ -673,7 +680,7 @@ __global__ __launch_bounds__(256) void moe_up_kernel(const MoeArgsDec a) {
     mfma_tiles<KWU, 1, kKeepParts, 2 * kMoePairs, 3, true>(
         a.gu_codes + static_cast<size_t>(e) * a.gu_cstride, a.gu_scales + static_cast<size_t>(e) * a.gu_sstride,
         2 * F, a.H / kSuperK, 0, 2 * np, cnt,
-        [&](int j) { return a.act + static_cast<int64_t>(a.sl.pick_token[start + j]) * a.act_stride; },
+        [&](int) { return a.act + static_cast<int64_t>(tok) * a.act_stride; },   // (packed: j = lane % 8)
         [](int64_t, int, float) {}, part_lds, tab,
         [&](int i) -> int64_t { return (i & 1) ? npair + p0 + (i >> 1) : p0 + (i >> 1); }, NoHook{},
         [] { trace(GV_K_MOE_UP, 5); });
@@ -739,8 +746,8 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeArgsDec a) {
     __shared__ uint2 tab[256];
     trace(GV_K_MOE_DOWN, 0);
     const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
-    int e, start, cnt;
-    if (!moe_slot(a, u, e, start, cnt)) return;
+    int e, start, cnt, tok;
+    if (!__builtin_amdgcn_readfirstlane(moe_slot(a, u, e, start, cnt, tok))) return;
     trace(GV_K_MOE_DOWN, 4);
     const int H = a.H, F = a.F, W = blockDim.x / 64, w = threadIdx.x / 64;
     const int64_t act_m_stride = act_halves(F);
@@ -1143,6 +1150,30 @@ struct Tick {
     }
 };
 
+template <int NCH>
+int launch_attn_n(Model &m, LayerW &L, hipStream_t st) {
+    const auto &c = m.c;
+    static int granted = 0;
+    const size_t lds = attn_lds(NCH * 32);
+    if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel<NCH>), lds, granted) != 0) return -1;
+    hipLaunchKernelGGL(attn_block_kernel<NCH>, dim3(m.kv_blocks, c.n_kv_heads), dim3(256), lds, st, m.q16, L.kv,
+                       m.slots, c.n_heads, c.n_kv_heads, m.sp, m.parts, m.kv_blocks);
+    return 0;
+}
+
+int launch_attn(Model &m, LayerW &L, hipStream_t st) {
+    switch (m.c.head_dim / 32) {
+    case 1: return launch_attn_n<1>(m, L, st);
+    case 2: return launch_attn_n<2>(m, L, st);
+    case 3: return launch_attn_n<3>(m, L, st);
+    case 4: return launch_attn_n<4>(m, L, st);
+    case 5: return launch_attn_n<5>(m, L, st);
+    case 6: return launch_attn_n<6>(m, L, st);
+    case 7: return launch_attn_n<7>(m, L, st);
+    default: return launch_attn_n<8>(m, L, st);
+    }
+}
+
 // One kernel class of layer l (the embedding and lm_head: l ignored) for M rows; the verify step is these in order.
 int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     const auto &c = m.c;
@@ -1163,11 +1194,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
                            m.slots);
         return 0;
     case GV_K_ATTN: {
-        static int granted = 0;
-        if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel), attn_lds(hd), granted) != 0) return -1;
-        hipLaunchKernelGGL(attn_block_kernel, dim3(m.kv_blocks, nkv), dim3(256), attn_lds(hd), st, m.q16, L.kv,
-                           m.slots, nh, nkv, hd, m.sp, m.parts, m.kv_blocks);
-        return 0;
+        return launch_attn(m, L, st);
     }
     case GV_K_MERGE:
         hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
@@ -1324,7 +1351,7 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     hipLaunchKernelGGL(fill_picks_kernel, dim3(m.E1), dim3(256), 0, st, pf.ids, M, K, E, pf.start, pf.pick_token,
                        pf.pick_of);
     GV_CHECK_HIP(hipGetLastError());
-    const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks};
+    const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks, nullptr};
     const int picks = M * (K + 1);
     if (moe_run(m, L, true, 32, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st) != 0) return -1;
     hipLaunchKernelGGL(swiglu_quant_kernel, dim3(picks), dim3(256), static_cast<size_t>(F) * 4, st, pf.gu, F,
@@ -1411,7 +1438,9 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         set_error(msg);
         return nullptr;
     };
-    if (c.hidden <= 0 || c.hidden % 128 != 0) return fail("hidden must be a positive multiple of 128");
+    if (c.hidden <= 0 || c.hidden % 128 != 0 || c.hidden > kMaxActCols)
+        return fail("hidden must be a positive multiple of 128, at most 16384");
+    if (c.moe_ff > kMaxActCols) return fail("moe_ff at most 16384");
     if (c.moe_ff <= 0 || c.moe_ff % 128 != 0 || c.shared_ff != c.moe_ff)
         return fail("moe_ff must be a positive multiple of 128 and shared_ff equal to it");
     if (c.head_dim <= 0 || c.head_dim > 256 || c.head_dim % 32 != 0 || c.rope_dim > c.head_dim || c.rope_dim % 2)

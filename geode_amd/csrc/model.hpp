@@ -34,6 +34,7 @@ struct RouteState {
     int slot_expert[kRouteSlots];
     int slot_start[kRouteSlots];
     int slot_count[kRouteSlots];
+    int slot_token[kRouteSlots * kSlotRows];   // [slot][j]: the row of the slot's pick j (past the count: the first's)
     int pick_token[kMaxRows * 17];
     int pick_of[kMaxRows * 17];   // [t][k] for k < K the routed pick, [t][K] the shared expert's
     float weight[kMaxRows * 16];  // [t][k]
@@ -44,9 +45,11 @@ struct RouteState {
 // pick_token[p]. The decode step's come from its RouteState, the prefill's from its own buffers.
 struct Slots {
     const int *n_slots, *expert, *start, *count, *pick_token, *n_picks;
+    const int *token;   // [slot][kSlotRows] the rows of a slot's picks (the decode step's; null for the prefill's)
 };
 inline Slots route_slots(const RouteState *rs) {   // member addresses of a device struct (no host access)
-    return Slots{&rs->n_slots, rs->slot_expert, rs->slot_start, rs->slot_count, rs->pick_token, &rs->n_picks};
+    return Slots{&rs->n_slots, rs->slot_expert, rs->slot_start, rs->slot_count, rs->pick_token, &rs->n_picks,
+                 rs->slot_token};
 }
 // What the combine reads: the shared gate [M], the routed weights [M][K], the picks of each row [M][K + 1]
 struct MixView {

@@ -39,17 +39,20 @@ __global__ void q4_from_pack_kernel(const uint8_t *__restrict__ pack, int64_t ro
     const int64_t blk = T * nsc + sc;
     *reinterpret_cast<uint32_t *>(codes + blk * 1024 + (rr + 16 * g) * 16 + j * 4) = tile_word(affine_nibbles(w));
     if (g % 2 == 0)   // the block of (chunk j, k-groups g, g + 1): pack scale 8 sc + 2 j + g / 2
-        scales[blk * 128 + (rr * 2 + g / 2) * 4 + j] = row[cols / 2 + 8 * sc + 2 * j + g / 2];
+        scales[tq4_scale_off(T, (nsc + 3) / 4, sc, rr, g, j)] = row[cols / 2 + 8 * sc + 2 * j + g / 2];
 }
 
 int q4_from_pack(const uint8_t *pack_dev, int64_t rows, int64_t cols, float global, uint8_t *codes, uint8_t *scales,
                  Q4 &out, hipStream_t st) {
     GV_REQUIRE(rows > 0 && cols > 0 && cols % kSuperK == 0, "q4: cols must be a positive multiple of 128");
+    const int64_t nsc = cols / kSuperK, nsq = (nsc + 3) / 4;
     if (rows % kTileR != 0) {   // the last tile's missing rows: zero codes and scales (their sums are discarded)
-        const int64_t T = rows / kTileR, nsc = cols / kSuperK;
+        const int64_t T = rows / kTileR;
         GV_CHECK_HIP(hipMemsetAsync(codes + T * nsc * 1024, 0, nsc * 1024, st));
-        GV_CHECK_HIP(hipMemsetAsync(scales + T * nsc * 128, 0, nsc * 128, st));
+        GV_CHECK_HIP(hipMemsetAsync(scales + T * nsq * 512, 0, nsq * 512, st));
     }
+    if (nsc % 4 != 0)   // the last quad's unused super-chunks: zero scales (never read, kept defined)
+        GV_CHECK_HIP(hipMemsetAsync(scales, 0, static_cast<size_t>(tiles_rows(rows)) * nsq * 512, st));
     const int64_t n = rows * (cols / 8);
     hipLaunchKernelGGL(q4_from_pack_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, pack_dev,
                        rows, cols, codes, scales);
@@ -294,7 +297,7 @@ static int gemv_range(const Q4 &w, const _Float16 *act, int64_t act_stride, int 
 
 int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st) {
     GV_REQUIRE(M >= 1 && M <= kMaxRows, "gemv_q4: 1 <= M <= 32 rows");
-    GV_REQUIRE(w.cols % kSuperK == 0, "gemv_q4: cols must be a multiple of 128");
+    GV_REQUIRE(w.cols % kSuperK == 0 && w.cols <= kMaxActCols, "gemv_q4: cols must be a multiple of 128, at most 16384");
     const int ntt = M <= 16 ? 1 : 2;
     const int nsc = static_cast<int>(w.cols / kSuperK);
     // K ranges whose activations fit the waves' registers: one launch up to 4096 (2048 for 17..32 rows) values,
@@ -303,6 +306,7 @@ int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const G
         int n = std::min(nsc - sc0, ntt == 1 ? 32 : 16);
         int waves, kw;
         while (n > 1 && !mfma_split(static_cast<int64_t>(n) * kSuperK, ntt, waves, kw)) --n;
+        GV_REQUIRE(sc0 % 4 == 0, "gemv_q4: a K range must start on a quad of super-chunks");
         GemvOut o = out;
         if (part > 0) o.accumulate = 1;
         if (gemv_range(w, act, act_stride, M, ntt, sc0, n, o, st) != 0) return -1;
