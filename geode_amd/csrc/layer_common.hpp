@@ -198,6 +198,7 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         rs->pick_of[t * (K + 1) + k] = pk;
         const int u = r.slot_of[e] + before / kSlotRows, j = before % kSlotRows;
         const int n = min(kSlotRows, r.cnt[e] - (before / kSlotRows) * kSlotRows);
+        rs->slot_dst[u * kSlotRows + j] = t * (K + 1) + k;
         if (j > 0) {
             rs->slot_token[u * kSlotRows + j] = t;
         } else {

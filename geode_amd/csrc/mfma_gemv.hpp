@@ -102,24 +102,41 @@ __device__ inline void act16_group(const float (&v)[8], int g, bool live, Dst ar
 // the 8-value groups i, i + blockDim, ... (up to 4; zeros past the row), optionally RMSNorm(1 + w) first (rmsnorm's
 // arithmetic, engine/src/kernels.cpp:1520-1529: the double sum of squares, inv = 1 / sqrt(float(ss / n) + eps), x inv
 // (1 + w)) and the normalized fp32 row to h (if not null). The whole workgroup calls this; red: LDS of 16 doubles.
+// the thread's norm weights 1 + w of its groups (as norm_quant_regs takes them), loaded ahead of their use
+__device__ inline void norm_weights(const float *norm_w, int cols, float (&w1)[4][8]) {
+    const int ng = cols / 8, nthr = blockDim.x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * nthr;
+        float4 a = make_float4(0, 0, 0, 0), b = a;
+        if (norm_w && g < ng) {
+            a = *reinterpret_cast<const float4 *>(norm_w + g * 8);
+            b = *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4);
+        }
+        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[q][i] = __fadd_rn(1.0f, t[i]);
+    }
+}
+
+// norm_quant_regs with the norm weights already in registers (has_norm false: no norm)
+template <typename Dst>
+__device__ inline void norm_quant_regs_w(float (&v)[4][8], int cols, bool has_norm, const float (&w1)[4][8],
+                                         float eps, Dst ar, float *h, double *red);
+
 template <typename Dst>
 __device__ inline void norm_quant_regs(float (&v)[4][8], int cols, const float *norm_w, float eps, Dst ar,
                                        float *h, double *red) {
+    float w1[4][8];
+    if (norm_w) norm_weights(norm_w, cols, w1);
+    norm_quant_regs_w(v, cols, norm_w != nullptr, w1, eps, ar, h, red);
+}
+
+template <typename Dst>
+__device__ inline void norm_quant_regs_w(float (&v)[4][8], int cols, bool has_norm, const float (&w1)[4][8],
+                                         float eps, Dst ar, float *h, double *red) {
     const int ng = cols / 8, nthr = blockDim.x;
-    if (norm_w) {
-        float w1[4][8];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int g = threadIdx.x + q * nthr;
-            float4 a = make_float4(0, 0, 0, 0), b = a;
-            if (g < ng) {
-                a = *reinterpret_cast<const float4 *>(norm_w + g * 8);
-                b = *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4);
-            }
-            const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) w1[q][i] = __fadd_rn(1.0f, t[i]);
-        }
+    if (has_norm) {
         double ss = 0.0;
 #pragma unroll
         for (int q = 0; q < 4; ++q)

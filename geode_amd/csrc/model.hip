@@ -747,6 +747,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeArgsDec a) {
     trace(GV_K_MOE_DOWN, 0);
     const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
     int e, start, cnt, tok;
+    const int dst = a.sl.dst[u * kSlotRows + (threadIdx.x % 64) % 8];   // the lane's pick's output row
     if (!__builtin_amdgcn_readfirstlane(moe_slot(a, u, e, start, cnt, tok))) return;
     trace(GV_K_MOE_DOWN, 4);
     const int H = a.H, F = a.F, W = blockDim.x / 64, w = threadIdx.x / 64;
@@ -757,7 +758,8 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeArgsDec a) {
         a.dn_codes + static_cast<size_t>(e) * a.dn_cstride, a.dn_scales + static_cast<size_t>(e) * a.dn_sstride, H,
         F / kSuperK, 0, nt, cnt,
         [&](int j) { return a.act_m + (start + j) * act_m_stride; },
-        [&](int64_t row, int j, float v) { a.y[static_cast<int64_t>(start + j) * H + row] = v * g2; }, nullptr, tab,
+        [&](int64_t row, int, float v) { a.y[static_cast<int64_t>(dst) * H + row] = v * g2; },   // (j = lane % 16)
+        nullptr, tab,
         TileRun{wt0}, NoHook{}, [] { trace(GV_K_MOE_DOWN, 5); });
     trace(GV_K_MOE_DOWN, 3);
 }
@@ -781,6 +783,8 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
 
 // x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365); a workgroup per
 // (row, 256 columns)
+// x += sigmoid(gate) x shared + sum_k w_k y_k in rank order (model.cpp:4554-4585, :5363-5365), then the next RMSNorm
+// and its operands; a workgroup per row
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K, const MixView mix,
                                                       int M, float *__restrict__ x, const float *__restrict__ norm_w,
                                                       float eps, _Float16 *__restrict__ act, int64_t act_stride) {
@@ -789,7 +793,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     if (t >= M) return;
     const int ng = H / 8;
     const float gs = mix.gate[t];
-    const float *ysh = y + static_cast<int64_t>(mix.pick_of[t * (K + 1) + K]) * H;
+    auto row_of = [&](int k) { return mix.pick_of ? mix.pick_of[t * (K + 1) + k] : t * (K + 1) + k; };
+    const float *ysh = y + static_cast<int64_t>(row_of(K)) * H;
     float v[4][8];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -812,7 +817,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
                 const int k = k0 + u;
                 wk[u] = k < K ? mix.weight[t * K + k] : 0.0f;
                 if (k < K) {
-                    const float *yk = y + static_cast<int64_t>(mix.pick_of[t * (K + 1) + k]) * H + g * 8;
+                    const float *yk = y + static_cast<int64_t>(row_of(k)) * H + g * 8;
                     ya[u] = *reinterpret_cast<const float4 *>(yk);
                     yb[u] = *reinterpret_cast<const float4 *>(yk + 4);
                 }
@@ -834,6 +839,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
         *reinterpret_cast<float4 *>(xr + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
     }
     if (act) norm_quant_regs(v, H, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
+}
+
+inline int combine_launch(const float *y, int H, int K, const MixView &mix, int M, float *x, const float *norm_w,
+                          float eps, _Float16 *act, int64_t act_stride, hipStream_t st) {
+    hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, y, H, K, mix, M, x, norm_w, eps, act, act_stride);
+    return 0;
 }
 
 // verify_keep of a tree: the kept path's keys and values moved to the kept slots in every layer; a thread per
@@ -1209,19 +1220,20 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
-                               m.route_in_router ? 1 : 0, c.n_experts, c.top_k, m.route + l,
+                               m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
                                m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
-                               m.route_in_router ? 1 : 0, c.n_experts, c.top_k, m.route + l,
+                               m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
                                m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter);
         }
         return 0;
     }
     case GV_K_ROUTE:
+        if (m.route_in_router && !m.moe_only) return 0;   // done by the router's last workgroup
         hipLaunchKernelGGL(route_kernel, dim3(1), dim3(1024), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
                            m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
         return 0;
@@ -1238,8 +1250,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         const float *next_norm = m.moe_only                ? nullptr
                                  : l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm
                                                       : m.final_norm;
-        hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, m.y, H, c.top_k, route_mix(m.route + l), M, m.x,
-                           next_norm, c.eps, m.act_h, abH);
+        combine_launch(m.y, H, c.top_k, route_mix(m.route + l, m.moe_dec), M, m.x, next_norm, c.eps, m.act_h, abH, st);
         return 0;
     }
     case GV_K_LM_HEAD:
@@ -1351,15 +1362,15 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     hipLaunchKernelGGL(fill_picks_kernel, dim3(m.E1), dim3(256), 0, st, pf.ids, M, K, E, pf.start, pf.pick_token,
                        pf.pick_of);
     GV_CHECK_HIP(hipGetLastError());
-    const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks, nullptr};
+    const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks, nullptr,
+                   nullptr};
     const int picks = M * (K + 1);
     if (moe_run(m, L, true, 32, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st) != 0) return -1;
     hipLaunchKernelGGL(swiglu_quant_kernel, dim3(picks), dim3(256), static_cast<size_t>(F) * 4, st, pf.gu, F,
                        pf.n_picks, pf.act_m);
     if (moe_run(m, L, false, 32, pf.act_m, pf.gu, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
     GV_CHECK_HIP(hipMemsetAsync(pf.out, 0, static_cast<size_t>(M) * H * 4, st));
-    hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M,
-                       pf.out, nullptr, 0.0f, nullptr, 0);
+    combine_launch(pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M, pf.out, nullptr, 0.0f, nullptr, 0, st);
     GV_CHECK_HIP(hipGetLastError());
     pf.M = M;
     return 0;

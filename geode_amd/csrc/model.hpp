@@ -35,6 +35,7 @@ struct RouteState {
     int slot_start[kRouteSlots];
     int slot_count[kRouteSlots];
     int slot_token[kRouteSlots * kSlotRows];   // [slot][j]: the row of the slot's pick j (past the count: the first's)
+    int slot_dst[kRouteSlots * kSlotRows];     // [slot][j]: t (K + 1) + k of the slot's pick j (its output row)
     int pick_token[kMaxRows * 17];
     int pick_of[kMaxRows * 17];   // [t][k] for k < K the routed pick, [t][K] the shared expert's
     float weight[kMaxRows * 16];  // [t][k]
@@ -46,17 +47,21 @@ struct RouteState {
 struct Slots {
     const int *n_slots, *expert, *start, *count, *pick_token, *n_picks;
     const int *token;   // [slot][kSlotRows] the rows of a slot's picks (the decode step's; null for the prefill's)
+    const int *dst;     // [slot][kSlotRows] their output rows t (K + 1) + k (the decode step's; null for the prefill's)
 };
 inline Slots route_slots(const RouteState *rs) {   // member addresses of a device struct (no host access)
     return Slots{&rs->n_slots, rs->slot_expert, rs->slot_start, rs->slot_count, rs->pick_token, &rs->n_picks,
-                 rs->slot_token};
+                 rs->slot_token, rs->slot_dst};
 }
-// What the combine reads: the shared gate [M], the routed weights [M][K], the picks of each row [M][K + 1]
+// What the combine reads: the shared gate [M], the routed weights [M][K], the output row of each pick of each row
+// [M][K + 1] (null: row t (K + 1) + k, the decode MoE kernels' layout)
 struct MixView {
     const float *gate, *weight;
     const int *pick_of;
 };
-inline MixView route_mix(const RouteState *rs) { return MixView{rs->gate, rs->weight, rs->pick_of}; }
+inline MixView route_mix(const RouteState *rs, bool direct) {
+    return MixView{rs->gate, rs->weight, direct ? nullptr : rs->pick_of};
+}
 
 struct LayerW {
     Q4 qkv;   // [nh*2*hd (q | gate per head) + nkv*hd (k) + nkv*hd (v)] x H, three globals
@@ -108,7 +113,8 @@ struct Model {
     int pos = 0, last_pos = 0, last_n = 0;
     int timed_class = -1;
     bool moe_only = false;   // gv_model_moe: the router takes the rows as they are, the combine no next norm
-    bool route_in_router = false;  // the router's last workgroup routes (off: route_kernel; on measured slower)
+    bool route_in_router = false;  // the router's last workgroup routes (off: route_kernel; on measured slower:
+                                   // 23.5 us vs 10.6 + 6.2, the device-scope fences and one workgroup's route)
     int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
     bool moe_dec = false;          // the decode MoE kernels (moe_up_kernel, moe_down_kernel), where the shapes fit
     uint64_t *trace = nullptr;     // gv_model_trace's stamps [GV_K_COUNT][8192 workgroups][8] (allocated when on)
