@@ -30,7 +30,7 @@ COPY_BYTES = 256 << 20
 # HBM bytes a launch of the dominant kernel moves, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes (KiB a dispatch)
 # scaled by what the same counters read for a copy of known size (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000); the
 # commands and figures are in profiles/moe_up_c4_m5_traffic.md
-PROFILED_TRAFFIC = {"moe_up": (22444.5 * 2.000 + 180.0 * 1.000) * 1024}
+PROFILED_TRAFFIC = {("moe_up", 5): (22876.0 * 2.000 + 90.0 * 1.000) * 1024}
 Q4_ROW = lambda cols: cols // 16 * 9   # noqa: E731  bytes of a q4 row (engine/src/kernels.cpp:900-902)
 
 
@@ -351,11 +351,11 @@ def main():
         "step_bytes": sbytes,
         "distinct_experts_per_layer": float(np.mean(uniq)),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": PROFILED_TRAFFIC.get(dom),
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": PROFILED_TRAFFIC.get((dom, M)),
                      "bytes_per_launch": dom_bytes, "avg_launch_us": dom_avg_s * 1e6,
                      "timing": "hipEvents around 80 back-to-back launches cycling through the 40 layers "
                                "(gv_model_replay)"},
-        "kernel_ms_per_step": {k: round(v[0], 4) for k, v in per_class.items()},
+        "kernel_ms_per_step": {k: round(v[0], 4) for k, v in per_class.items() if v[1]},
         "init_s": t_init,
     }
     if not args.no_cpu:

@@ -63,34 +63,6 @@ inline size_t q4_scale_bytes(int64_t rows, int64_t cols) {
 inline size_t act_bytes(int64_t cols) { return static_cast<size_t>(cols) * 4; }
 __host__ __device__ inline int64_t act_halves(int64_t cols) { return cols * 2; }
 
-// ---------------------------------------------------------------- device-coherent memory operations
-// Buffer instructions with the sc1 cache policy (gfx940+: device scope, the policy of an agent-scope atomic load or
-// store), coherent across the XCDs' separate L2 caches without a cache maintenance operation: how the persistent
-// step kernel's workgroups exchange data within one launch. `base` must be uniform across the wave; offsets in bytes.
-typedef uint32_t xu4 __attribute__((ext_vector_type(4)));
-typedef uint32_t xu2 __attribute__((ext_vector_type(2)));
-constexpr int kSc1 = 16;
-// a buffer descriptor of `bytes` from a base the whole wave shares (read from lane 0: the descriptor lives in scalar
-// registers, never in a per-lane loop over distinct values)
-__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base, uint32_t bytes) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32));
-    void *p = reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), static_cast<int>(bytes), 0x00020000);
-}
-__device__ inline __amdgpu_buffer_rsrc_t xrs(const void *base) { return uniform_rsrc(base, 0x7FFFFFFFu); }
-__device__ inline xu4 xld16(const void *base, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(xrs(base), off, 0, kSc1); }
-__device__ inline void xst16(const void *base, uint32_t off, xu4 v) { __builtin_amdgcn_raw_buffer_store_b128(v, xrs(base), off, 0, kSc1); }
-__device__ inline float xldf(const float *base, uint32_t i) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs(base), i * 4u, 0, kSc1));
-}
-__device__ inline void xstf(float *base, uint32_t i, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), xrs(base), i * 4u, 0, kSc1);
-}
-__device__ inline float4 xld4f(const float *base, uint32_t i) { return __builtin_bit_cast(float4, xld16(base, i * 4u)); }   // i % 4 == 0
-__device__ inline void xst4f(float *base, uint32_t i, float4 v) { xst16(base, i * 4u, __builtin_bit_cast(xu4, v)); }
-
 // ---------------------------------------------------------------- a measurement aid: workgroup clock stamps
 // When a translation unit's g_trace is set (gv_model_trace; each source file's kernels have their own copy), thread 0
 // of each workgroup of the traced kernels writes the 100 MHz clock (s_memrealtime) at a few points to

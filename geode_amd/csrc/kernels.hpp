@@ -19,6 +19,7 @@ struct GemvOut {
     int nseg = 1;
     int64_t seg_end[4] = {0, 0, 0, 0};
     float seg_global[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    int trace_cls = -1;   // the kernel class whose clock stamps the launch writes (a measurement aid; -1: none)
     __device__ inline void put(int64_t row, int t, float v) const {
         float g = seg_global[0];
         for (int s = 1; s < nseg; ++s)

@@ -1,5 +1,5 @@
-// layer_common.hpp - device code shared by the per-phase kernels (model.hip) and the persistent step kernel
-// (step.hip): the KV cache layout, the route of the step's rows.
+// layer_common.hpp - device code of the verify step's layers (model.hip): the KV cache layout, the route of the
+// step's rows.
 #pragma once
 
 #include "model.hpp"

@@ -70,26 +70,12 @@ __device__ inline float amax8(const float (&v)[8]) {
     return a;
 }
 
-// Where a row's operands go: device memory (a pointer), or a row of a device-coherent exchange buffer (XDst: the
-// buffer's uniform base and the row's byte offset in it)
-struct XDst {
-    const void *base;
-    uint32_t bytes;   // the buffer's size: the descriptor's range
-    uint32_t off;
-};
 __device__ inline void act16_store(_Float16 *ar, int g, bool live, const h8 &hi, const h8 &lo) {
     if (!live) return;
     h8 *p = reinterpret_cast<h8 *>(ar + static_cast<int64_t>(g) * 16);
     p[0] = hi;
     p[1] = lo;
 }
-__device__ inline void act16_store(XDst d, int g, bool live, const h8 &hi, const h8 &lo) {
-    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(d.base, d.bytes);
-    const uint32_t off = live ? d.off + static_cast<uint32_t>(g) * 32u : 0xFFFFF000u;   // past the buffer (under 2 GB): dropped
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(xu4, hi), r, off, 0, kSc1);
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(xu4, lo), r, off + 16u, 0, kSc1);
-}
-
 template <typename Dst>
 __device__ inline void act16_group(const float (&v)[8], int g, bool live, Dst ar) {
     const float amax = fmaxf(amax8(v), __shfl_xor(amax8(v), 1, 64));

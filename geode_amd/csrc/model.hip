@@ -1191,14 +1191,19 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     const int H = c.hidden, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     const int64_t abH = act_halves(H), abC = act_halves(static_cast<int64_t>(nh) * hd);
     LayerW &L = m.layers[static_cast<size_t>(l)];
-    Tick tk(m, cls, st);
+    // classes fused into a neighbour launch nothing and take no events
+    const bool fused = (cls == GV_K_SWIGLU && m.moe_dec) || (cls == GV_K_ROUTE && m.route_in_router && !m.moe_only);
+    Tick tk(m, fused ? -2 : cls, st);
     switch (cls) {
     case GV_K_EMBED:
         hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x, m.layers[0].in_norm, c.eps,
                            m.act_h, abH);
         return 0;
-    case GV_K_QKV:
-        return gemv_q4(L.qkv, m.act_h, abH, M, qkv_out(m, L), st);
+    case GV_K_QKV: {
+        GemvOut o = qkv_out(m, L);
+        o.trace_cls = GV_K_QKV;
+        return gemv_q4(L.qkv, m.act_h, abH, M, o, st);
+    }
     case GV_K_ROPE:
         hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
                            c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
@@ -1211,8 +1216,11 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
                            m.kv_blocks, m.sp, m.act_core, abC);
         return 0;
-    case GV_K_O:   // the residual add is the product's accumulate
-        return gemv_q4(L.o, m.act_core, abC, M, gemv_out(m.x, H, L.o.global, 1), st);
+    case GV_K_O: {   // the residual add is the product's accumulate
+        GemvOut o = gemv_out(m.x, H, L.o.global, 1);
+        o.trace_cls = GV_K_O;
+        return gemv_q4(L.o, m.act_core, abC, M, o, st);
+    }
     case GV_K_ROUTER: {
         const int wgs = std::max((m.E1 + kRouterRows - 1) / kRouterRows, M);
         if (H <= 2048) {
@@ -1515,7 +1523,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         int kwu, kwd, waves;
         m.moe_dec = moe_dec_shape(c, kwu, kwd, waves);
     }
-    {   // the buffers one step's phases exchange, in one arena (the persistent kernel addresses them by offset)
+    {   // the buffers one step's phases exchange, in one arena (one allocation, 256-byte aligned pieces)
         const size_t sizes[] = {static_cast<size_t>(Mx) * H * 4,
                                 static_cast<size_t>(Mx) * qkv_rows(c) * 4,
                                 static_cast<size_t>(Mx) * m.E1 * 4,

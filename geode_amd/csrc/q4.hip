@@ -227,6 +227,8 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
                                                             GemvOut out) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
+    const int tc = out.trace_cls;
+    if (tc >= 0) trace(tc, 0);
     const int64_t ntiles = tiles_rows(w.rows);
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
@@ -234,7 +236,8 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     mfma_tiles<KW, NTT, kSplitK, 0, 3, PACK>(
         w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, static_cast<int>(t1 - t0), M,
         [&](int j) { return act + j * act_stride; }, [&](int64_t row, int j, float v) { out.put(row, j, v); },
-        part_lds, tab, TileRun{t0});
+        part_lds, tab, TileRun{t0}, NoHook{}, [&] { if (tc >= 0) trace(tc, 5); });
+    if (tc >= 0) trace(tc, 3);
 }
 
 int trace_set_q4(uint64_t *p) {
