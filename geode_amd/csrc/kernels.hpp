@@ -20,11 +20,14 @@ struct GemvOut {
     int64_t seg_end[4] = {0, 0, 0, 0};
     float seg_global[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     int trace_cls = -1;   // the kernel class whose clock stamps the launch writes (a measurement aid; -1: none)
-    __device__ inline void put(int64_t row, int t, float v) const {
+    __device__ inline float scaled(int64_t row, float v) const {   // v x the row's global
         float g = seg_global[0];
         for (int s = 1; s < nseg; ++s)
             if (row >= seg_end[s - 1]) g = seg_global[s];
-        const float r = v * g;
+        return v * g;
+    }
+    __device__ inline void put(int64_t row, int t, float v) const {
+        const float r = scaled(row, v);
         float *p = y + t * ldy + row;
         if (accumulate) *p += r;
         else *p = r;

@@ -34,7 +34,15 @@ template <int NR>
 __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&live)[NR], int E, int K,
                                   int *const (&ids)[NR], float *const (&w)[NR], float *const (&gate)[NR]) {
     const int lane = threadIdx.x & 63;
-    float pv[NR][4], sum[NR];
+    float pv[NR][4], sum[NR], raw[NR][4], lge[NR];
+    // every logit up front (indices clamped, no branch around a load), the shared expert's gate logit too
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) raw[r][i] = lg[r][min(lane + 64 * i, E - 1)];
+        lge[r] = lg[r][E];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         float v[4];
@@ -42,7 +50,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = lane + 64 * i;
-            v[i] = live[r] && e < E ? lg[r][e] : -__builtin_inff();
+            v[i] = live[r] && e < E ? raw[r][i] : -__builtin_inff();
             mx = fmaxf(mx, v[i]);
         }
         if (r == 0) trace(GV_K_ROUTE, 5);
@@ -88,7 +96,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
     for (int r = 0; r < NR; ++r) {
         if (!live[r]) continue;
         if (lane < K) w[r][lane] = __fdiv_rn(mine[r], top[r]);
-        if (lane == 0) *gate[r] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg[r][E])));
+        if (lane == 0) *gate[r] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lge[r])));
     }
 }
 

@@ -85,7 +85,17 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
         kh = head - nh - nkv;
         src = qkv + t * ldq + static_cast<int64_t>(nh) * 2 * hd + kv_row + static_cast<int64_t>(kh) * hd;
     }
-    const float xv = i < hd ? src[i] : 0.0f;
+    // every load up front, indices clamped (no branch around a load): the value, its norm weight, its rotation
+    const float *zero = reinterpret_cast<const float *>(g_zero_act16);
+    const int ic = min(i, hd - 1);
+    const float xr = src[ic];
+    const float nwr = *(nw ? nw + ic : zero);
+    const int p = sp->pos + sp->depth[t];
+    const int jc = min(i < half ? i : i - half, half - 1);
+    const float cr = *(half > 0 ? cos_t + static_cast<int64_t>(p) * half + jc : zero);
+    const float sr = *(half > 0 ? sin_t + static_cast<int64_t>(p) * half + jc : zero);
+    __builtin_amdgcn_sched_barrier(0);
+    const float xv = i < hd ? xr : 0.0f;
     if (kind == 2) {
         if (i < hd) kv[v_index(slots, hd, nkv, kh, slot, i)] = static_cast<_Float16>(xv);
         return;
@@ -95,19 +105,12 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
     __syncthreads();
     ss = ((red[0] + red[1]) + red[2]) + red[3];
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(ss / static_cast<double>(hd)), eps)));
-    if (i < hd) v[i] = __fmul_rn(__fmul_rn(xv, inv), __fadd_rn(1.0f, nw[i]));
+    if (i < hd) v[i] = __fmul_rn(__fmul_rn(xv, inv), __fadd_rn(1.0f, nwr));
     __syncthreads();
     if (i >= hd) return;
-    const int p = sp->pos + sp->depth[t];
     float out = v[i];
-    if (i < half) {
-        const float c = cos_t[static_cast<int64_t>(p) * half + i], s = sin_t[static_cast<int64_t>(p) * half + i];
-        out = __fsub_rn(__fmul_rn(v[i], c), __fmul_rn(v[i + half], s));
-    } else if (i < 2 * half) {
-        const int j = i - half;
-        const float c = cos_t[static_cast<int64_t>(p) * half + j], s = sin_t[static_cast<int64_t>(p) * half + j];
-        out = __fadd_rn(__fmul_rn(v[i], c), __fmul_rn(v[j], s));
-    }
+    if (i < half) out = __fsub_rn(__fmul_rn(v[i], cr), __fmul_rn(v[i + half], sr));
+    else if (i < 2 * half) out = __fadd_rn(__fmul_rn(v[i], cr), __fmul_rn(v[i - half], sr));
     if (kind == 0) {   // the query as two halves, hi + lo, for near-fp32 scores from fp16 products
         const int64_t qo = (static_cast<int64_t>(t) * nh + head) * hd + i;
         _Float16 hi, lo;
@@ -149,21 +152,23 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
     const int64_t qlo = static_cast<int64_t>(M) * nh * hd;
     // the queries of tile qt as B operands (hi and lo halves): dims ch * 32 + 8 lg .. + 8 of query qt * 16 + lq
     auto load_q = [&](int qt, half8 (&qb)[NCH], half8 (&ql)[NCH]) {
+        // (a query past the tile's end reads query 0: its scores are masked and its output is not written, so
+        // nothing waits on a select of the loaded values)
         const int qi = qt * 16 + lq;
-        const bool ok = qi < NQ;   // (a query past the tile's end reads query 0 and is zeroed)
+        const bool ok = qi < NQ;
         const int tq = ok ? qi / group : 0, hq = kh * group + (ok ? qi % group : 0);
         const _Float16 *qp = q16 + (static_cast<int64_t>(tq) * nh + hq) * hd + 8 * lg;
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
-            const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            const half8 a = *reinterpret_cast<const half8 *>(qp + ch * 32);
-            const half8 c = *reinterpret_cast<const half8 *>(qp + qlo + ch * 32);
-            qb[ch] = ok ? a : z;
-            ql[ch] = ok ? c : z;
+            qb[ch] = *reinterpret_cast<const half8 *>(qp + ch * 32);
+            ql[ch] = *reinterpret_cast<const half8 *>(qp + qlo + ch * 32);
         }
     };
     half8 qb[NCH], ql[NCH];
     load_q(wave, qb, ql);   // the wave's first tile of queries, in flight with the staging loads
+    // the visibility masks of the lane's query rows (sp->vis: bit j = the row sees new row j), loaded with them
+    auto vis_of = [&](int qt) { return sp->vis[min((qt * 16 + lq) / group, M - 1)]; };
+    uint32_t vis_first = vis_of(wave);
     {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load, every load of
         // the thread issued before the first store (NCH of each)
         const _Float16 *kg = kv + k_index(slots, hd, kh, s0, 0);
@@ -176,10 +181,12 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             if (u >= nl) break;
             const int i = threadIdx.x + u * 256;
             const int r = i / kpr, c = i % kpr;
-            const uint4 kk = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8);
-            kr[u] = s0 + r < total ? kk : make_uint4(0, 0, 0, 0);   // (rows past the context: inside the cache)
+            // (rows past the context: inside the cache, their scores masked; values past it are zeroed below, as
+            // a weight 0 times a stale non-finite value would not be 0)
+            kr[u] = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8);
             vr[u] = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(i) * 8);
         }
+        __builtin_amdgcn_sched_barrier(0);   // every load issued before the first store waits for one
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             if (u >= nl) break;
@@ -187,16 +194,11 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             const int r = i / kpr, c = i % kpr;
             *reinterpret_cast<uint4 *>(ks + r * kld + c * 8) = kr[u];
             const int d = i / (kAttnBlock / 8), cv = i % (kAttnBlock / 8);
-            uint4 v = vr[u];
             const int lim = total - s0 - cv * 8;   // positions of this load inside the context
-            if (lim < 8) {
-                uint32_t w[4] = {v.x, v.y, v.z, v.w};
-                for (int k = 0; k < 4; ++k) {
-                    if (2 * k >= lim) w[k] = 0;
-                    else if (2 * k + 1 >= lim) w[k] &= 0xFFFFu;
-                }
-                v = make_uint4(w[0], w[1], w[2], w[3]);
-            }
+            auto keep = [&](int k) {   // the word's halves (positions 2k, 2k + 1) inside the context: kept (no branch)
+                return lim >= 2 * k + 2 ? 0xFFFFFFFFu : lim == 2 * k + 1 ? 0xFFFFu : 0u;
+            };
+            const uint4 v = make_uint4(vr[u].x & keep(0), vr[u].y & keep(1), vr[u].z & keep(2), vr[u].w & keep(3));
             *reinterpret_cast<uint4 *>(vs + d * kAttnVld + cv * 8) = v;
         }
     }
@@ -208,7 +210,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
         const int qi = qt * 16 + lq;
         const bool qvalid = qi < NQ;
         const int tq = qvalid ? qi / group : 0, hq = kh * group + (qvalid ? qi % group : 0);
-        const uint32_t vis = qvalid ? sp->vis[tq] : 0u;
+        const uint32_t vis = qvalid ? (qt == wave ? vis_first : vis_of(qt)) : 0u;
         // the four 16-position tiles' scores, hi and lo products apart: eight independent MFMA chains
         float4v ch_[4], cl_[4];
 #pragma unroll
@@ -317,28 +319,32 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     // kMergeBatch blocks' values of the wave (blocks wave, wave + 4, ...; four dims a lane) and the gate values of
     // wave 0's output dims; the values do not wait for the maximum (their weights are applied after).
     constexpr int kMergeBatch = 20;   // blocks a wave (80 blocks a workgroup)
+    // Unconditional loads, indices clamped: a block past nbw reads block nbw - 1 again (its maximum changes no
+    // maximum; its sum and values are never added, their weights being 0), a lane past the head's dims reads the
+    // last four (unused).
     float bm[4], bs[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int bb = threadIdx.x + 256 * k;
-        bm[k] = bb < nbw ? base[bb * ld + hd] : -__builtin_inff();
-        bs[k] = bb < nbw ? base[bb * ld + hd + 1] : 0.0f;
+        const int bb = min(static_cast<int>(threadIdx.x) + 256 * k, nbw - 1);
+        bm[k] = base[bb * ld + hd];
+        bs[k] = base[bb * ld + hd + 1];
     }
     const bool dl = lane * 4 < hd;
+    const int dc = min(lane * 4, hd - 4);
     float4 pv[kMergeBatch];
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-        const int bb = wave + 4 * u;
-        pv[u] = dl && bb < nbw ? *reinterpret_cast<const float4 *>(base + bb * ld + lane * 4) : make_float4(0, 0, 0, 0);
-    }
+    for (int u = 0; u < kMergeBatch; ++u)
+        pv[u] = *reinterpret_cast<const float4 *>(base + min(wave + 4 * u, nbw - 1) * ld + dc);
     const int ng = hd / 8;
     float gate[8];
     {
-        const bool live = wave == 0 && lane < ng;
+        const float *gp = qkv + t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + 8 * min(lane, ng - 1);
+        const float4 a = *reinterpret_cast<const float4 *>(gp), b = *reinterpret_cast<const float4 *>(gp + 4);
+        const float g8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            gate[i] = live ? qkv[t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + 8 * lane + i] : 0.0f;
+        for (int i = 0; i < 8; ++i) gate[i] = g8[i];
     }
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the first use waits for one
     float mx = fmaxf(fmaxf(bm[0], bm[1]), fmaxf(bm[2], bm[3]));
     mx = wave_max(mx);
     if (lane == 0) red[0][wave] = mx;
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) {
             const int bb = wave + 4 * u;
-            const float f = bb < nbw ? fw[bb] : 0.0f;
+            const float f = bb < nbw ? fw[bb] : 0.0f;   // (a clamped block: weight 0)
             o.x = __builtin_fmaf(pv[u].x, f, o.x);
             o.y = __builtin_fmaf(pv[u].y, f, o.y);
             o.z = __builtin_fmaf(pv[u].z, f, o.z);
@@ -461,46 +467,47 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     trace(GV_K_ROUTER, 0);
     const int M = sp->M, r0 = blockIdx.x * kRouterRows;
-    // the workgroup's router rows: 4 x H bf16, 8 a load (H / 256 loads a thread)
-    uint4 wr[GPT * 4];
-#pragma unroll
-    for (int k = 0; k < GPT * 4; ++k) {
-        const int i = threadIdx.x + k * 256, rr = i / (H / 8), c8 = i % (H / 8);
-        wr[k] = i < 4 * (H / 8) && r0 + rr < E1
-                    ? *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(r0 + rr) * H + c8 * 8)
-                    : make_uint4(0, 0, 0, 0);
-    }
-    float nw[GPT][8];
-#pragma unroll
-    for (int q = 0; q < GPT; ++q) {
-        const int g = threadIdx.x + q * 256;
-        const bool ld = norm_w && g < H / 8;
-        const float4 a = ld ? *reinterpret_cast<const float4 *>(norm_w + g * 8) : make_float4(0, 0, 0, 0);
-        const float4 b = ld ? *reinterpret_cast<const float4 *>(norm_w + g * 8 + 4) : make_float4(0, 0, 0, 0);
-        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);   // no norm: 1, and inv = 1 below
-    }
-    bool wrote_w = false;
-    for (int t0 = 0; t0 < M; t0 += TG) {
+    // Every load is unconditional (indices clamped into the arrays), so that none waits for the ones before it:
+    // the first group's rows (needed first), the norm weights, then the workgroup's router rows (4 x H bf16, 8 a
+    // load, H / 256 loads a thread; rows past E1 read row E1 - 1 and are never used).
+    float xv[TG][GPT][8];
+    const float *zero = reinterpret_cast<const float *>(g_zero_act16);   // 64 KB of zeros
+    auto load_x = [&](int t0) {   // (rows past the group's count: a copy of its last, unused; columns past H: 0)
         const int nt = min(TG, M - t0);
-        float xv[TG][GPT][8];
 #pragma unroll
         for (int tt = 0; tt < TG; ++tt)
 #pragma unroll
             for (int q = 0; q < GPT; ++q) {
-                float4 a = make_float4(0, 0, 0, 0), b = a;
-                if (tt < nt && threadIdx.x + q * 256 < H / 8) {
-                    const float *src = x + static_cast<int64_t>(t0 + tt) * H + (threadIdx.x + q * 256) * 8;
-                    a = *reinterpret_cast<const float4 *>(src);
-                    b = *reinterpret_cast<const float4 *>(src + 4);
-                }
+                const int g = threadIdx.x + q * 256;
+                const float *src = g < H / 8 ? x + static_cast<int64_t>(t0 + min(tt, nt - 1)) * H + g * 8 : zero;
+                const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
                 const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
                 for (int i = 0; i < 8; ++i) xv[tt][q][i] = t[i];
             }
-        // 1 / RMS per row: the thread's squares, the wave sums, the waves' in order
-        __syncthreads();   // the previous group's sums are done with hs and red
+    };
+    load_x(0);
+    float nw[GPT][8];   // 1 + w (no norm: w read from the zeros)
+#pragma unroll
+    for (int q = 0; q < GPT; ++q) {
+        const int g = threadIdx.x + q * 256;
+        const float *src = norm_w && g < H / 8 ? norm_w + g * 8 : zero;
+        const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
+        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);
+    }
+    uint4 wr[GPT * 4];
+#pragma unroll
+    for (int k = 0; k < GPT * 4; ++k) {
+        const int i = min(static_cast<int>(threadIdx.x) + k * 256, 4 * (H / 8) - 1), rr = i / (H / 8), c8 = i % (H / 8);
+        wr[k] = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(min(r0 + rr, E1 - 1)) * H + c8 * 8);
+    }
+    // one group of up to TG rows: 1 / RMS per row (the thread's squares, the wave sums, the waves' in order), the
+    // normalized rows to LDS (and row blockIdx.x's operands), then the dots
+    auto group = [&](int t0, bool first) {
+        const int nt = min(TG, M - t0);
+        if (!first) __syncthreads();   // the previous group's dots are done with hs and red
         trace(GV_K_ROUTER, 1);
 #pragma unroll
         for (int tt = 0; tt < TG; ++tt) {
@@ -513,7 +520,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
             ss = wave_sum(ss);
             if (lane == 0) red[wave][tt] = ss;
         }
-        if (!wrote_w) {   // the router rows to LDS as fp32
+        if (first) {   // the router rows to LDS as fp32
 #pragma unroll
             for (int k = 0; k < GPT * 4; ++k) {
                 const int i = threadIdx.x + k * 256;
@@ -526,7 +533,6 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
                     d[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
                 }
             }
-            wrote_w = true;
         }
         __syncthreads();
         const int tq = static_cast<int>(blockIdx.x) - t0;
@@ -555,7 +561,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
         trace(GV_K_ROUTER, 2);
         const int tt = lane / 8, j = lane % 8;
         const int ra = r0 + wave;
-        if (ra >= E1) continue;
+        if (ra >= E1) return;
         const float *hr = hs + (tt < nt ? tt : 0) * ldh;
         const float *wrow = ws + wave * H;
         float a0 = 0.0f;
@@ -574,6 +580,11 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
         const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
         const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
         if (j == 0 && tt < nt) logits[static_cast<int64_t>(t0 + tt) * E1 + ra] = s3;
+    };
+    group(0, true);
+    for (int t0 = TG; t0 < M; t0 += TG) {
+        load_x(t0);
+        group(t0, false);
     }
     trace(GV_K_ROUTER, 3);
     if (!route) return;
@@ -792,53 +803,76 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     const int t = blockIdx.x;
     if (t >= M) return;
     const int ng = H / 8;
+    const float *zero = reinterpret_cast<const float *>(g_zero_act16);
     const float gs = mix.gate[t];
     auto row_of = [&](int k) { return mix.pick_of ? mix.pick_of[t * (K + 1) + k] : t * (K + 1) + k; };
     const float *ysh = y + static_cast<int64_t>(row_of(K)) * H;
-    float v[4][8];
+    // Every load of a group of eight values issued before the first use (indices clamped, no branch around a
+    // load): the next norm's weights, the shared expert's row, the first eight picks' rows (picks past K read pick
+    // K - 1 and are not added), the residual row.
+    float w1[4][8];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int g = threadIdx.x + q * blockDim.x;
+        const float *src = norm_w && g < ng ? norm_w + g * 8 : zero;
+        const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
+        const float tw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[q][i] = __fadd_rn(1.0f, tw[i]);
+    }
+    float v[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[q][i] = 0.0f;
-        if (g >= ng) continue;
+        if (q * static_cast<int>(blockDim.x) >= ng) continue;   // uniform
+        const int g = threadIdx.x + q * blockDim.x, gc = min(g, ng - 1);
+        const bool live = g < ng;
+        float4 ya[9], yb[9];
+        ya[8] = *reinterpret_cast<const float4 *>(ysh + gc * 8);
+        yb[8] = *reinterpret_cast<const float4 *>(ysh + gc * 8 + 4);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float *yk = y + static_cast<int64_t>(row_of(min(u, K - 1))) * H + gc * 8;
+            ya[u] = *reinterpret_cast<const float4 *>(yk);
+            yb[u] = *reinterpret_cast<const float4 *>(yk + 4);
+        }
+        float *xr = x + static_cast<int64_t>(t) * H + gc * 8;
+        const float4 xa = *reinterpret_cast<const float4 *>(xr), xb = *reinterpret_cast<const float4 *>(xr + 4);
+        __builtin_amdgcn_sched_barrier(0);
         float o[8];
         {
-            const float4 a = *reinterpret_cast<const float4 *>(ysh + g * 8), b = *reinterpret_cast<const float4 *>(ysh + g * 8 + 4);
-            const float yv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const float yv[8] = {ya[8].x, ya[8].y, ya[8].z, ya[8].w, yb[8].x, yb[8].y, yb[8].z, yb[8].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = __fmul_rn(gs, yv[i]);
         }
-        for (int k0 = 0; k0 < K; k0 += 8) {   // rank order; eight picks' loads ahead of their sums
-            float4 ya[8], yb[8];
-            float wk[8];
+        // rank order, skipping zero weights
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int k = k0 + u;
-                wk[u] = k < K ? mix.weight[t * K + k] : 0.0f;
-                if (k < K) {
-                    const float *yk = y + static_cast<int64_t>(row_of(k)) * H + g * 8;
-                    ya[u] = *reinterpret_cast<const float4 *>(yk);
-                    yb[u] = *reinterpret_cast<const float4 *>(yk + 4);
-                }
-            }
+        for (int u = 0; u < 8; ++u) {
+            const float wk = u < K ? mix.weight[t * K + u] : 0.0f;
+            if (wk == 0.0f) continue;   // uniform
+            const float yv[8] = {ya[u].x, ya[u].y, ya[u].z, ya[u].w, yb[u].x, yb[u].y, yb[u].z, yb[u].w};
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (k0 + u >= K || wk[u] == 0.0f) continue;
-                const float yv[8] = {ya[u].x, ya[u].y, ya[u].z, ya[u].w, yb[u].x, yb[u].y, yb[u].z, yb[u].w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(o[i], __fmul_rn(wk[u], yv[i]));
-            }
+            for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(o[i], __fmul_rn(wk, yv[i]));
         }
-        float *xr = x + static_cast<int64_t>(t) * H + g * 8;
-        const float4 a = *reinterpret_cast<const float4 *>(xr), b = *reinterpret_cast<const float4 *>(xr + 4);
-        const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        for (int k = 8; k < K; ++k) {   // more than eight picks a row: one at a time
+            const float wk = mix.weight[t * K + k];
+            if (wk == 0.0f) continue;
+            const float *yk = y + static_cast<int64_t>(row_of(k)) * H + gc * 8;
+            const float4 a = *reinterpret_cast<const float4 *>(yk), b = *reinterpret_cast<const float4 *>(yk + 4);
+            const float yv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[q][i] = __fadd_rn(xv[i], o[i]);
-        *reinterpret_cast<float4 *>(xr) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
-        *reinterpret_cast<float4 *>(xr + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+            for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(o[i], __fmul_rn(wk, yv[i]));
+        }
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[q][i] = live ? __fadd_rn(xv[i], o[i]) : 0.0f;
+        if (live) {
+            *reinterpret_cast<float4 *>(xr) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+            *reinterpret_cast<float4 *>(xr + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+        }
     }
-    if (act) norm_quant_regs(v, H, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
+    if (act) norm_quant_regs_w(v, H, norm_w != nullptr, w1, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
 }
 
 inline int combine_launch(const float *y, int H, int K, const MixView &mix, int M, float *x, const float *norm_w,

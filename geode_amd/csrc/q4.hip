@@ -233,10 +233,48 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
     if (t0 >= ntiles) return;
-    mfma_tiles<KW, NTT, kSplitK, 0, 3, PACK>(
-        w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, static_cast<int>(t1 - t0), M,
-        [&](int j) { return act + j * act_stride; }, [&](int64_t row, int j, float v) { out.put(row, j, v); },
-        part_lds, tab, TileRun{t0}, NoHook{}, [&] { if (tc >= 0) trace(tc, 5); });
+    const int nt = static_cast<int>(t1 - t0);
+    // The outputs are written as mfma_tiles' split-K epilogue writes them (output o = (tile, column, 4 rows) by
+    // thread o mod blockDim), here so that an accumulating product's earlier values for the thread's first output
+    // are loaded with the weights (in the hook) rather than one round trip a row at the end.
+    const int o0 = threadIdx.x;
+    auto item = [&](int o, int64_t &row0, int &j) {
+        const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+        row0 = (t0 + i) * kTileR + 4 * (ll / 16);
+        j = tt * 16 + ll % 16;
+    };
+    float old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto prefetch = [&] {
+        if (!out.accumulate) return;   // uniform
+        int64_t row0;
+        int j;
+        item(min(o0, nt * NTT * 64 - 1), row0, j);
+        const float *p = out.y + min(j, M - 1) * out.ldy;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) old[r] = p[min(row0 + r, w.rows - 1)];   // (clamped: always a valid address)
+    };
+    mfma_tiles<KW, NTT, kKeepParts, 0, 3, PACK>(
+        w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, nt, M,
+        [&](int j) { return act + j * act_stride; }, [](int64_t, int, float) {}, part_lds, tab, TileRun{t0}, prefetch,
+        [&] { if (tc >= 0) trace(tc, 5); });
+    if (tc >= 0) trace(tc, 6);
+    const int W = blockDim.x / 64;
+    for (int o = o0; o < nt * NTT * 64; o += blockDim.x) {   // the waves' partial sums added in wave order
+        const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+        f4 sum = part_lds[((i * W + 0) * NTT + tt) * 64 + ll];
+        for (int w2 = 1; w2 < W; ++w2) sum += part_lds[((i * W + w2) * NTT + tt) * 64 + ll];
+        int64_t row0;
+        int j;
+        item(o, row0, j);
+        if (j >= M) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = row0 + r;
+            if (row >= w.rows) break;
+            if (o == o0 && out.accumulate) out.y[j * out.ldy + row] = old[r] + out.scaled(row, sum[r]);
+            else out.put(row, j, sum[r]);
+        }
+    }
     if (tc >= 0) trace(tc, 3);
 }
 
