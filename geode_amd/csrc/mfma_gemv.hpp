@@ -346,12 +346,18 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
         for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
             for (int h = 0; h < NB; ++h) acc[h][tt] = f4{0, 0, 0, 0};
+        uint2 tv[NS][4];   // the tile's scale table entries, all read from the LDS before the first is used
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tv[s][j] = tab[(sq[s] >> (8 * j)) & 0xFFu];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const uint32_t words[4] = {cq[s].x, cq[s].y, cq[s].z, cq[s].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const h8 a = decode8(words[j], tab[(sq[s] >> (8 * j)) & 0xFFu], magic);
+                const h8 a = decode8(words[j], tv[s][j], magic);
                 const int c = s * 4 + j;
 #pragma unroll
                 for (int tt = 0; tt < NTT; ++tt)

@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     // Every load of the first pass issued at once: the blocks' maxima and sums (four blocks a thread), the first
     // kMergeBatch blocks' values of the wave (blocks wave, wave + 4, ...; four dims a lane) and the gate values of
     // wave 0's output dims; the values do not wait for the maximum (their weights are applied after).
-    constexpr int kMergeBatch = 20;   // blocks a wave (80 blocks a workgroup)
+    constexpr int kMergeBatch = 36;   // blocks a wave (144 blocks a workgroup: 9216 positions)
     // Unconditional loads, indices clamped: a block past nbw reads block nbw - 1 again (its maximum changes no
     // maximum; its sum and values are never added, their weights being 0), a lane past the head's dims reads the
     // last four (unused).
