@@ -676,7 +676,7 @@ __device__ inline bool moe_slot(const MoeArgsDec &a, int u, int &e, int &start, 
 }
 
 template <int KWU>
-__global__ __launch_bounds__(256) void moe_up_kernel(const MoeArgsDec a) {
+__global__ __launch_bounds__(512) void moe_up_kernel(const MoeArgsDec a) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
     trace(GV_K_MOE_UP, 0);
@@ -1032,10 +1032,15 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
     const int slots = moe_slots(m, M);
     if (up) {
         a.groups = (a.F / kTileR + kMoePairs - 1) / kMoePairs;
-        const size_t lds = static_cast<size_t>(2 * kMoePairs) * waves * 1024;
         const dim3 grid(static_cast<unsigned>(slots * a.groups));
-        if (kwu == 16) hipLaunchKernelGGL(moe_up_kernel<16>, grid, dim3(64 * waves), lds, st, a);
-        else hipLaunchKernelGGL(moe_up_kernel<4>, grid, dim3(64 * waves), lds, st, a);
+        if (kwu == 16 && waves <= 4) {   // eight waves, each half the K range
+            const size_t lds = static_cast<size_t>(2 * kMoePairs) * (2 * waves) * 1024;
+            hipLaunchKernelGGL(moe_up_kernel<8>, grid, dim3(128 * waves), lds, st, a);
+        } else {
+            const size_t lds = static_cast<size_t>(2 * kMoePairs) * waves * 1024;
+            if (kwu == 16) hipLaunchKernelGGL(moe_up_kernel<16>, grid, dim3(64 * waves), lds, st, a);
+            else hipLaunchKernelGGL(moe_up_kernel<4>, grid, dim3(64 * waves), lds, st, a);
+        }
     } else {
         a.groups = (a.H / kTileR + waves * kMoeDnTiles - 1) / (waves * kMoeDnTiles);
         const dim3 grid(static_cast<unsigned>(slots * a.groups));
