@@ -649,7 +649,7 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
 // a workgroup per (slot, group of row tiles), each wave kMoeDnTiles tiles over the whole K = F. Every tile loop is
 // unrolled (mfma_tiles with a fixed tile count).
 constexpr int kMoePairs = 3;       // tile pairs an up workgroup takes
-constexpr int kMoeDnTiles = 3;     // down tiles a wave takes
+constexpr int kMoeDnTiles = 2;     // down tiles a wave takes
 
 struct MoeArgsDec {
     const uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
