@@ -7,7 +7,7 @@ packer), an fp16 KV cache of 8,192 context positions N(0, 1). A step verifies k 
 token (M = 5 rows): every layer, the final norm and lm_head, logits left on the device. The drafts are the target
 model's own greedy continuation, so a greedy sample-and-match accepts all of them (5 tokens emitted a step).
 
-    python bench.py [--steps K] [--warmup W] [--tree] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--tree] [--kv-int8] [--no-cpu]
     python bench.py --config c2|c3|c5      (the acceptance rules; one MoE block at M = 5 or 512)
 """
 import argparse
@@ -64,8 +64,8 @@ def algorithmic_bytes(cls, c, M, uniq_per_layer, ctx):
         return H * Q4_ROW(nh * hd)
     if cls == "lm_head":
         return V * Q4_ROW(H)
-    if cls == "attention":
-        return 2 * nkv * (ctx + M) * hd * 2
+    if cls == "attention":   # K and V of every position: fp16, or int8 and a float scale a row
+        return 2 * nkv * (ctx + M) * (hd + 4 if c.get("kv_int8") else hd * 2)
     if cls == "router":
         return (c["n_experts"] + 1) * H * 2
     return None
@@ -83,7 +83,7 @@ def step_bytes(c, M, uniq_per_layer, ctx):
     return tot
 
 
-def cpu_baseline(M, threads):
+def cpu_baseline(M, threads, kv_int8=False):
     """The oracle (the reference's CPU arithmetic restated, int8 path) on the host cores: a bounded sample of the
     same workload, 1 of the 40 layers plus the final norm and lm_head at full shapes (timing-only random q4
     bytes); the step time is extrapolated as t_head + 40 x t_layer."""
@@ -91,7 +91,7 @@ def cpu_baseline(M, threads):
     import pyoracle as po
 
     po.lib.orc_set_threads(threads)
-    cfg = dict(C4)
+    cfg = dict(C4, kv_int8=int(kv_int8))
     cfg["n_layers"] = 1
     om = po.Model(cfg, seed=SEED, ctx=CTX, fast=True)
     toks = (np.arange(M) * 1000 + 7).astype(np.int32)
@@ -107,6 +107,7 @@ def cpu_baseline(M, threads):
         reps += 1
     return {"value": M / best, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"1 of 40 layers + final norm + lm_head at full shapes, M={M}, ctx {CTX}, int8 path, "
+                      f"{'int8' if kv_int8 else 'fp16'} KV, "
                       f"best of {reps}; step = t_head + 40 x t_layer = {best * 1e3:.1f} ms"}
 
 
@@ -221,6 +222,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--tree", action="store_true", help="verify the 17-row draft tree instead of the k=4 chain")
+    ap.add_argument("--kv-int8", action="store_true",
+                    help="the int8 KV cache (the reference's default cache) instead of the configs' fp16")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a 256 MiB device copy, three times: the known traffic that scales HBM byte counters")
@@ -241,9 +244,10 @@ def main():
     import geode_amd as g
 
     g.init(0)
+    C = dict(C4, kv_int8=1) if args.kv_int8 else C4
     M = 17 if args.tree else 5
     parents = tree_parents() if args.tree else None
-    m = g.VerifyModel(C4)
+    m = g.VerifyModel(C)
     t0 = time.time()
     m.randomize(SEED, 0.02, 0.0221, CTX)
     g.check(g.lib.gv_synchronize())
@@ -257,7 +261,7 @@ def main():
         toks.append(int(np.argmax(lg[0])))
     toks = np.array(toks, np.int32)
     if args.tree:   # a tree's first child of each node follows the chain, the rest other tokens
-        toks = np.array([(7 + 1000 * i) % C4["vocab"] for i in range(M)], np.int32)
+        toks = np.array([(7 + 1000 * i) % C["vocab"] for i in range(M)], np.int32)
 
     def step():
         m.position = CTX
@@ -284,7 +288,7 @@ def main():
     m.position = CTX
     logits = m.verify(toks, parents)
     route = m.route_ids(M)
-    uniq = [len(np.unique(route[l])) for l in range(C4["n_layers"])]
+    uniq = [len(np.unique(route[l])) for l in range(C["n_layers"])]
     if not args.tree:
         emitted = 1
         for i in range(M - 1):
@@ -312,19 +316,19 @@ def main():
         per_class[name] = (tms / 3, n // 3)
     m.time_kernel(-1)
     # the dominant kernel: the class moving the most algorithmic bytes a step (the experts' gate|up products)
-    dom = max((k for k in per_class if algorithmic_bytes(k, C4, M, uniq, CTX)),
-              key=lambda k: algorithmic_bytes(k, C4, M, uniq, CTX) * max(per_class[k][1], 1))
+    dom = max((k for k in per_class if algorithmic_bytes(k, C, M, uniq, CTX)),
+              key=lambda k: algorithmic_bytes(k, C, M, uniq, CTX) * max(per_class[k][1], 1))
     # the dominant kernel's launch time: its launches of every layer replayed back to back between two events on
     # the step's own state, each launch on the next layer's weights (none of them cached by the previous launch)
     m.position = CTX
     m.verify(toks, parents, want_logits=False)
     cls = g.KERNEL_CLASSES.index(dom)
-    dom_avg_s = m.replay(cls, 0, reps=2 * C4["n_layers"]) / 1e3
-    dom_bytes = algorithmic_bytes(dom, C4, M, uniq, CTX)
+    dom_avg_s = m.replay(cls, 0, reps=2 * C["n_layers"]) / 1e3
+    dom_bytes = algorithmic_bytes(dom, C, M, uniq, CTX)
     achieved = dom_bytes / dom_avg_s
 
     steps_s = 1e3 / ms
-    sbytes = step_bytes(C4, M, uniq, CTX)
+    sbytes = step_bytes(C, M, uniq, CTX)
     out = {
         "metric": "verify-step tok/s, 35B-A3B-shape MoE k=4; HBM GB/s vs peak",
         "value": steps_s * emitted,
@@ -340,7 +344,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": ("C4 full 40-layer 35B-A3B-shape verify step, " +
                                 ("draft tree 16 nodes (4,3) + root, M=17" if args.tree else "chain k=4, M=5") +
-                                f", ctx {CTX}, vocab 151936, q4 weights, fp16 KV, int8-path products"),
+                                f", ctx {CTX}, vocab 151936, q4 weights, {'int8' if args.kv_int8 else 'fp16'} KV, int8-path products"),
                    "rows": M, "tokens_emitted_per_step": emitted, "acceptance": "greedy sample-and-match on the "
                    "step's logits; drafts = the target's own greedy chain" if not args.tree else "greedy tree walk"},
         "verify_steps_per_s": steps_s,
@@ -360,7 +364,7 @@ def main():
     }
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
-        out["cpu_baseline"] = cpu_baseline(M, threads)
+        out["cpu_baseline"] = cpu_baseline(M, threads, args.kv_int8)
     print(json.dumps(out))
 
 

@@ -23,12 +23,13 @@ class GvQ4(_c.Structure):
 class GvModelConfig(_c.Structure):
     _fields_ = [(n, _c.c_int32) for n in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff",
                                           "n_heads", "n_kv_heads", "head_dim", "rope_dim")] + \
-               [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int32), ("max_rows", _c.c_int32)]
+               [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int32), ("max_rows", _c.c_int32),
+                ("kv_int8", _c.c_int32)]
 
 
 # tensor kinds of gv_model_adopt
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, QKV, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, \
-    SHARED_EXPERT, KV = 0, 1, 2, 3, 4, 5, 8, 9, 10, 11, 12, 13, 14, 17
+    SHARED_EXPERT, KV, KV_I8 = 0, 1, 2, 3, 4, 5, 8, 9, 10, 11, 12, 13, 14, 17, 18
 
 # every symbol include/geode_verify.h declares, with its signature
 SIGNATURES = {
@@ -270,7 +271,7 @@ class VerifyModel:
 
     def __init__(self, cfg: dict):
         self.cfg = dict(cfg)
-        c = GvModelConfig(**{k: cfg[k] for k, _ in GvModelConfig._fields_})
+        c = GvModelConfig(**{k: cfg.get(k, 0) if k == "kv_int8" else cfg[k] for k, _ in GvModelConfig._fields_})
         err = _c.create_string_buffer(512)
         self.h = _lib().gv_model_create(_c.byref(c), err, 512)
         if not self.h:

@@ -7,7 +7,11 @@
 namespace gv {
 
 // The device KV cache of one layer: K [nkv][slots][hd] and V [nkv][slots / 64][hd][64] in fp16 (V transposed in
-// blocks of kAttnBlock positions, so that the MFMA operands of both products are contiguous loads).
+// blocks of kAttnBlock positions, so that the MFMA operands of both products are contiguous loads), or the same in
+// int8 followed by the scales K [nkv][slots], V [nkv][slots] (kv_scale_index).
+__device__ __host__ inline int64_t kv_scale_index(int64_t slots, int nkv, int which, int kh, int64_t slot) {
+    return (static_cast<int64_t>(which) * nkv + kh) * slots + slot;
+}
 __device__ __host__ inline int64_t k_index(int64_t slots, int hd, int kh, int64_t slot, int d) {
     return (static_cast<int64_t>(kh) * slots + slot) * hd + d;
 }

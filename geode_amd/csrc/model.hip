@@ -52,6 +52,19 @@ __global__ __launch_bounds__(256) void embed_kernel(Q4 w, const StepParams *__re
     norm_quant_regs(v, ng * 8, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
 }
 
+// quant_kv_row (model.cpp:3766-3774) of a row held one value a thread (256 threads; threads past the row: live
+// false): amax over the row, q = clamp(nearbyint(x * (127 / amax)), -127, 127) to *q (live threads), returns the
+// scale amax / 127. Every thread of the workgroup calls it (one barrier).
+__device__ inline float kv_quant_row(float x, float *red4, int8_t *q, bool live) {
+    const float a = wave_max(live ? fabsf(x) : 0.0f);
+    if (threadIdx.x % 64 == 0) red4[threadIdx.x / 64] = a;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+    const float inv = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    if (live) *q = static_cast<int8_t>(fminf(fmaxf(rintf(__fmul_rn(x, inv)), -127.0f), 127.0f));
+    return __fdiv_rn(amax, 127.0f);
+}
+
 // Per (row, head): the query heads' and key heads' RMSNorm(1 + w) then partial RoPE on the first rope_dim dims
 // (pairs i, i + half; model.cpp:3714-3733, rotary position pos + depth), the keys and values appended to the fp16
 // cache at slot pos + row (static_cast<_Float16>: round to nearest even). Query heads go to q_out as two fp16
@@ -61,11 +74,13 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
                                                       const float *__restrict__ k_norm, float eps,
                                                       const float *__restrict__ cos_t, const float *__restrict__ sin_t,
                                                       const StepParams *__restrict__ sp, _Float16 *__restrict__ q_out,
-                                                      _Float16 *__restrict__ kv, int64_t slots) {
+                                                      _Float16 *__restrict__ kv, int8_t *__restrict__ kv8,
+                                                      float *__restrict__ kvs, int64_t slots) {
     const int t = blockIdx.x, head = blockIdx.y, i = threadIdx.x;
     if (t >= sp->M) return;
     __shared__ double red[4];
     __shared__ float v[256];
+    __shared__ float ared[4];
     const int64_t kv_row = static_cast<int64_t>(nkv) * hd;
     const int slot = sp->pos + t;
     const float *src;
@@ -97,7 +112,12 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
     __builtin_amdgcn_sched_barrier(0);
     const float xv = i < hd ? xr : 0.0f;
     if (kind == 2) {
-        if (i < hd) kv[v_index(slots, hd, nkv, kh, slot, i)] = static_cast<_Float16>(xv);
+        if (kv8) {   // quant_kv_row of the value row (model.cpp:3766-3774)
+            const float sc = kv_quant_row(xv, ared, kv8 + v_index(slots, hd, nkv, kh, slot, i), i < hd);
+            if (i == 0) kvs[kv_scale_index(slots, nkv, 1, kh, slot)] = sc;
+        } else if (i < hd) {
+            kv[v_index(slots, hd, nkv, kh, slot, i)] = static_cast<_Float16>(xv);
+        }
         return;
     }
     double ss = wave_sum(static_cast<double>(xv) * static_cast<double>(xv));
@@ -107,8 +127,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(ss / static_cast<double>(hd)), eps)));
     if (i < hd) v[i] = __fmul_rn(__fmul_rn(xv, inv), __fadd_rn(1.0f, nwr));
     __syncthreads();
-    if (i >= hd) return;
-    float out = v[i];
+    if (i >= hd && !(kind == 1 && kv8)) return;   // (the int8 key row's amax takes every thread)
+    float out = i < hd ? v[i] : 0.0f;
     if (i < half) out = __fsub_rn(__fmul_rn(v[i], cr), __fmul_rn(v[i + half], sr));
     else if (i < 2 * half) out = __fadd_rn(__fmul_rn(v[i], cr), __fmul_rn(v[i - half], sr));
     if (kind == 0) {   // the query as two halves, hi + lo, for near-fp32 scores from fp16 products
@@ -117,6 +137,9 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
         split_f16(out, hi, lo);
         q_out[qo] = hi;
         q_out[qo + static_cast<int64_t>(sp->M) * nh * hd] = lo;
+    } else if (kv8) {
+        const float sc = kv_quant_row(out, ared, kv8 + k_index(slots, hd, kh, slot, i), i < hd);
+        if (i == 0) kvs[kv_scale_index(slots, nkv, 0, kh, slot)] = sc;
     } else {
         kv[k_index(slots, hd, kh, slot, i)] = f16_of(out);
     }
@@ -133,13 +156,18 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const float *__restrict__ 
 
 // NCH = head_dim / 32: every loop over the head's dims, and every load, fixed at compile time (no branch around a
 // load, so the compiler waits for exactly the loads each step needs)
-template <int NCH>
+// I8: the int8 cache (attend<int8_t>): keys and values staged as fp16 (the int8 values, exact), the block's K and V
+// scales in LDS; a score is the dot times (1 / sqrt(hd)) x the position's K scale (model.cpp:3948), the weights'
+// sum is the softmax's own and each weight then takes the position's V scale before the values (:3965-3972).
+template <int NCH, bool I8>
 __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restrict__ q16,
-                                                         const _Float16 *__restrict__ kv, int64_t slots, int nh,
+                                                         const void *__restrict__ kvp,
+                                                         const float *__restrict__ kvs, int64_t slots, int nh,
                                                          int nkv, const StepParams *__restrict__ sp,
                                                          float *__restrict__ parts, int nb_max) {
     constexpr int hd = NCH * 32;
     extern __shared__ _Float16 lds_h[];
+    __shared__ float sc_l[I8 ? 256 : 1];   // int8: the block's K scales [0, 64), V scales [64, 128)
     trace(GV_K_ATTN, 0);
     const int b = blockIdx.x, kh = blockIdx.y;
     const int pos = sp->pos, M = sp->M, total = pos + M;
@@ -169,8 +197,46 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
     // the visibility masks of the lane's query rows (sp->vis: bit j = the row sees new row j), loaded with them
     auto vis_of = [&](int qt) { return sp->vis[min((qt * 16 + lq) / group, M - 1)]; };
     uint32_t vis_first = vis_of(wave);
-    {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load, every load of
-        // the thread issued before the first store (NCH of each)
+    if constexpr (I8) {   // int8: a block's K (or V) is 64 x hd bytes, 16 a load; fp16 in the LDS
+        const int8_t *kv8 = static_cast<const int8_t *>(kvp);
+        const int8_t *kg = kv8 + k_index(slots, hd, kh, s0, 0);
+        const int8_t *vg = kv8 + v_index(slots, hd, nkv, kh, s0, 0);
+        constexpr int nld = kAttnBlock * hd / 16, nl = (nld + 255) / 256;   // 16-byte loads of each, a thread's
+        uint4 kr[nl], vr[nl];
+#pragma unroll
+        for (int u = 0; u < nl; ++u) {
+            const int i = min(static_cast<int>(threadIdx.x) + u * 256, nld - 1);
+            kr[u] = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(i / (hd / 16)) * hd + (i % (hd / 16)) * 16);
+            vr[u] = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(i) * 16);
+        }
+        // the block's scales: thread j < 64 the K scale of position j, 64 <= j < 128 the V scale (0 past the
+        // context, so that a weight 0 stays 0)
+        const int j = threadIdx.x % kAttnBlock, which = (threadIdx.x / kAttnBlock) & 1;
+        const float scv = kvs[kv_scale_index(slots, nkv, which, kh, s0 + j)];
+        __builtin_amdgcn_sched_barrier(0);
+        auto to_h8 = [](uint32_t lo, uint32_t hi) {   // 8 int8 values (little-endian) as fp16 (exact)
+            half8 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[e] = static_cast<_Float16>(static_cast<int8_t>((lo >> (8 * e)) & 0xFF));
+                h[4 + e] = static_cast<_Float16>(static_cast<int8_t>((hi >> (8 * e)) & 0xFF));
+            }
+            return h;
+        };
+#pragma unroll
+        for (int u = 0; u < nl; ++u) {   // (a thread past nld stores item nld - 1 again: no branch to sink loads into)
+            const int i = min(static_cast<int>(threadIdx.x) + u * 256, nld - 1);
+            const int r = i / (hd / 16), c = i % (hd / 16);
+            *reinterpret_cast<half8 *>(ks + r * kld + c * 16) = to_h8(kr[u].x, kr[u].y);
+            *reinterpret_cast<half8 *>(ks + r * kld + c * 16 + 8) = to_h8(kr[u].z, kr[u].w);
+            const int d = i / (kAttnBlock / 16), cv = i % (kAttnBlock / 16);
+            *reinterpret_cast<half8 *>(vs + d * kAttnVld + cv * 16) = to_h8(vr[u].x, vr[u].y);
+            *reinterpret_cast<half8 *>(vs + d * kAttnVld + cv * 16 + 8) = to_h8(vr[u].z, vr[u].w);
+        }
+        sc_l[threadIdx.x] = which == 1 && s0 + j >= total ? 0.0f : scv;   // (threads >= 128: copies, unused)
+    } else {   // stage: keys row by row, values (already [hd][64] in the cache) row by row; 8 halves a load, every
+               // load of the thread issued before the first store (NCH of each)
+        const _Float16 *kv = static_cast<const _Float16 *>(kvp);
         const _Float16 *kg = kv + k_index(slots, hd, kh, s0, 0);
         const _Float16 *vg = kv + v_index(slots, hd, nkv, kh, s0, 0);
         const int kpr = hd / 8;   // loads a key row
@@ -232,7 +298,8 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             for (int r = 0; r < 4; ++r) {   // S^T[position pt*16 + 4 lg + r][query lq]
                 const int slot = s0 + pt * 16 + 4 * lg + r;
                 const bool ok = qvalid && slot < total && (slot < pos || ((vis >> (slot - pos)) & 1u));
-                sc[pt][r] = ok ? (ch_[pt][r] + cl_[pt][r]) * scale : -__builtin_inff();
+                const float f = I8 ? scale * sc_l[pt * 16 + 4 * lg + r] : scale;
+                sc[pt][r] = ok ? (ch_[pt][r] + cl_[pt][r]) * f : -__builtin_inff();
                 mx = fmaxf(mx, sc[pt][r]);
             }
         if (qt == wave) trace(GV_K_ATTN, 2);
@@ -246,7 +313,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             for (int r = 0; r < 4; ++r) {
                 const float e = sc[pt][r] == -__builtin_inff() ? 0.0f : expf(sc[pt][r] - mx);
                 _Float16 eh, el;
-                split_f16(e, eh, el);
+                split_f16(I8 ? e * sc_l[kAttnBlock + pt * 16 + 4 * lg + r] : e, eh, el);
                 pe[pt][r] = eh;
                 pl[pt][r] = el;
                 lsum += e;
@@ -883,17 +950,23 @@ inline int combine_launch(const float *y, int H, int K, const MixView &mix, int 
 
 // verify_keep of a tree: the kept path's keys and values moved to the kept slots in every layer; a thread per
 // (layer, KV head, dim)
-__global__ void kv_compact_kernel(_Float16 *kv_all, int n_layers, int nkv, int hd, int64_t slots, int pos, int kept,
-                                  const int *__restrict__ path) {
+// (T: _Float16, or int8_t for the int8 cache, whose scales follow each layer's values: dim 0's thread moves them)
+template <typename T>
+__global__ void kv_compact_kernel(uint8_t *kv_all, size_t layer_bytes, int n_layers, int nkv, int hd, int64_t slots,
+                                  int pos, int kept, const int *__restrict__ path) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<int64_t>(n_layers) * nkv * hd) return;
     const int l = static_cast<int>(i / (static_cast<int64_t>(nkv) * hd)), kh = static_cast<int>((i / hd) % nkv);
     const int d = static_cast<int>(i % hd);
-    _Float16 *kv = kv_all + static_cast<int64_t>(l) * 2 * nkv * slots * hd;
+    T *kv = reinterpret_cast<T *>(kv_all + static_cast<size_t>(l) * layer_bytes);
+    float *sc = reinterpret_cast<float *>(kv + 2 * static_cast<int64_t>(nkv) * slots * hd);
     for (int j = 1; j < kept; ++j) {   // ascending: path[j] >= j, so no source is overwritten before it is read
         if (path[j] == j) continue;
         kv[k_index(slots, hd, kh, pos + j, d)] = kv[k_index(slots, hd, kh, pos + path[j], d)];
         kv[v_index(slots, hd, nkv, kh, pos + j, d)] = kv[v_index(slots, hd, nkv, kh, pos + path[j], d)];
+        if (sizeof(T) == 1 && d == 0)
+            for (int w = 0; w < 2; ++w)
+                sc[kv_scale_index(slots, nkv, w, kh, pos + j)] = sc[kv_scale_index(slots, nkv, w, kh, pos + path[j])];
     }
 }
 
@@ -909,6 +982,33 @@ __global__ void kv_from_rows_kernel(const float *__restrict__ src, int n, int nk
     const _Float16 v = static_cast<_Float16>(src[i]);
     if (which == 0) kv[k_index(slots, hd, kh, p, d)] = v;
     else kv[v_index(slots, hd, nkv, kh, p, d)] = v;
+}
+
+// the int8 cache from fp32 rows ([K, V][position][nkv * hd], positions [0, n)): quant_kv_row of each (K or V,
+// position, KV head) row, a workgroup (256 threads, hd <= 256) a row
+__global__ __launch_bounds__(256) void kv8_from_rows_kernel(const float *__restrict__ src, int n, int nkv, int hd,
+                                                            int64_t slots, int8_t *__restrict__ kv8,
+                                                            float *__restrict__ kvs) {
+    __shared__ float red4[4];
+    const int row = blockIdx.x, which = row / (n * nkv), p = (row / nkv) % n, kh = row % nkv, d = threadIdx.x;
+    const bool live = d < hd;
+    const float x = live ? src[(static_cast<int64_t>(which) * n + p) * nkv * hd + static_cast<int64_t>(kh) * hd + d] : 0.0f;
+    int8_t *q = kv8 + (which == 0 ? k_index(slots, hd, kh, p, d) : v_index(slots, hd, nkv, kh, p, d));
+    const float sc = kv_quant_row(x, red4, q, live);
+    if (d == 0) kvs[kv_scale_index(slots, nkv, which, kh, p)] = sc;
+}
+
+// the int8 cache from the reference's int8 rows: int8 [K, V][position][nkv * hd] and float [K, V][position][nkv]
+__global__ void kv8_copy_kernel(const int8_t *__restrict__ src, const float *__restrict__ ssrc, int n, int nkv, int hd,
+                                int64_t slots, int8_t *__restrict__ kv8, float *__restrict__ kvs) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t kv_row = static_cast<int64_t>(nkv) * hd;
+    if (i >= 2 * n * kv_row) return;
+    const int which = static_cast<int>(i / (n * kv_row));
+    const int p = static_cast<int>((i / kv_row) % n);
+    const int kh = static_cast<int>((i % kv_row) / hd), d = static_cast<int>(i % hd);
+    kv8[which == 0 ? k_index(slots, hd, kh, p, d) : v_index(slots, hd, nkv, kh, p, d)] = src[i];
+    if (d == 0) kvs[kv_scale_index(slots, nkv, which, kh, p)] = ssrc[(static_cast<int64_t>(which) * n + p) * nkv + kh];
 }
 
 __global__ void f32_to_bf16_kernel(const float *__restrict__ x, int64_t n, uint16_t *__restrict__ y) {
@@ -1200,15 +1300,20 @@ struct Tick {
     }
 };
 
-template <int NCH>
-int launch_attn_n(Model &m, LayerW &L, hipStream_t st) {
+template <int NCH, bool I8>
+int launch_attn_t(Model &m, LayerW &L, hipStream_t st) {
     const auto &c = m.c;
     static int granted = 0;
     const size_t lds = attn_lds(NCH * 32);
-    if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel<NCH>), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL(attn_block_kernel<NCH>, dim3(m.kv_blocks, c.n_kv_heads), dim3(256), lds, st, m.q16, L.kv,
-                       m.slots, c.n_heads, c.n_kv_heads, m.sp, m.parts, m.kv_blocks);
+    if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel<NCH, I8>), lds, granted) != 0) return -1;
+    hipLaunchKernelGGL((attn_block_kernel<NCH, I8>), dim3(m.kv_blocks, c.n_kv_heads), dim3(256), lds, st, m.q16,
+                       I8 ? static_cast<const void *>(L.kv8) : static_cast<const void *>(L.kv), L.kvs, m.slots,
+                       c.n_heads, c.n_kv_heads, m.sp, m.parts, m.kv_blocks);
     return 0;
+}
+template <int NCH>
+int launch_attn_n(Model &m, LayerW &L, hipStream_t st) {
+    return m.kv_i8 ? launch_attn_t<NCH, true>(m, L, st) : launch_attn_t<NCH, false>(m, L, st);
 }
 
 int launch_attn(Model &m, LayerW &L, hipStream_t st) {
@@ -1246,7 +1351,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     case GV_K_ROPE:
         hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
                            c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
-                           m.slots);
+                           L.kv8, L.kvs, m.slots);
         return 0;
     case GV_K_ATTN: {
         return launch_attn(m, L, st);
@@ -1528,8 +1633,11 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     bool ok = alloc_q4(m, m.embed, V, H) && alloc_q4(m, m.lm_head, V, H);
     ok = ok && (m.final_norm = static_cast<float *>(dalloc(m, H * 4)));
     m.slots = (static_cast<int64_t>(c.max_ctx) + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
-    const size_t kv_layer = 2 * static_cast<size_t>(nkv) * m.slots * hd;   // halves
-    m.kv_all = static_cast<_Float16 *>(dalloc(m, static_cast<size_t>(c.n_layers) * kv_layer * 2));
+    const size_t kv_layer = 2 * static_cast<size_t>(nkv) * m.slots * hd;   // values a layer
+    m.kv_i8 = c.kv_int8 != 0;
+    m.kv_layer_bytes = m.kv_i8 ? kv_layer + 2 * static_cast<size_t>(nkv) * m.slots * 4 : kv_layer * 2;
+    m.kv_layer_bytes = (m.kv_layer_bytes + 255) / 256 * 256;
+    m.kv_all = static_cast<_Float16 *>(dalloc(m, static_cast<size_t>(c.n_layers) * m.kv_layer_bytes));
     ok = ok && m.kv_all;
     m.layers.resize(static_cast<size_t>(c.n_layers));
     for (int l = 0; ok && l < c.n_layers; ++l) {
@@ -1547,7 +1655,13 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         if (!ok) break;
         L.gu_codes = gu, L.gu_scales = gu + m.gu_code_stride * m.E1;
         L.dn_codes = dn, L.dn_scales = dn + m.dn_code_stride * m.E1;
-        L.kv = m.kv_all + static_cast<size_t>(l) * kv_layer;
+        uint8_t *kb = reinterpret_cast<uint8_t *>(m.kv_all) + static_cast<size_t>(l) * m.kv_layer_bytes;
+        if (m.kv_i8) {
+            L.kv8 = reinterpret_cast<int8_t *>(kb);
+            L.kvs = reinterpret_cast<float *>(kb + kv_layer);
+        } else {
+            L.kv = reinterpret_cast<_Float16 *>(kb);
+        }
     }
     const int Mx = c.max_rows, K = c.top_k;
     m.max_slots = moe_slots_bound(c.n_experts, K, Mx);
@@ -1619,7 +1733,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         (hipMemcpy(m.rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
          hipMemcpy(m.rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess))
         return fail("gv_model_create: rope table copy failed");
-    if (hipMemset(m.kv_all, 0, static_cast<size_t>(c.n_layers) * kv_layer * 2) != hipSuccess)
+    if (hipMemset(m.kv_all, 0, static_cast<size_t>(c.n_layers) * m.kv_layer_bytes) != hipSuccess)
         return fail("gv_model_create: memset failed");
     return g.release();
 }
@@ -1708,8 +1822,32 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
         float *dsrc = nullptr;
         GV_CHECK_HIP(hipMalloc(&dsrc, f.size() * 4 + 4));
         GV_CHECK_HIP(hipMemcpy(dsrc, f.data(), f.size() * 4, hipMemcpyHostToDevice));
-        hipLaunchKernelGGL(kv_from_rows_kernel, dim3(static_cast<unsigned>((f.size() + 255) / 256)), dim3(256), 0,
-                           stream(), dsrc, static_cast<int>(n), static_cast<int>(nkv), static_cast<int>(hd), m.slots, L->kv);
+        if (m.kv_i8)   // an int8 cache quantizes the rows (quant_kv_row)
+            hipLaunchKernelGGL(kv8_from_rows_kernel, dim3(static_cast<unsigned>(2 * n * nkv)), dim3(256), 0, stream(),
+                               dsrc, static_cast<int>(n), static_cast<int>(nkv), static_cast<int>(hd), m.slots, L->kv8,
+                               L->kvs);
+        else
+            hipLaunchKernelGGL(kv_from_rows_kernel, dim3(static_cast<unsigned>((f.size() + 255) / 256)), dim3(256), 0,
+                               stream(), dsrc, static_cast<int>(n), static_cast<int>(nkv), static_cast<int>(hd), m.slots,
+                               L->kv);
+        GV_CHECK_HIP(hipGetLastError());
+        GV_CHECK_HIP(hipStreamSynchronize(stream()));
+        GV_CHECK_HIP(hipFree(dsrc));
+        return 0;
+    }
+    case GV_KV_I8: {   // the reference's int8 rows and scales, as they are
+        GV_REQUIRE(m.kv_i8, "gv_model_adopt: GV_KV_I8 needs a model made with kv_int8");
+        const int64_t kv_row = nkv * hd, per = 2 * (kv_row + nkv * 4);   // bytes a position
+        GV_REQUIRE(bytes % per == 0 && bytes / per <= c.max_ctx, "gv_model_adopt: int8 kv size");
+        const int64_t n = bytes / per;
+        void *dsrc = nullptr;
+        GV_CHECK_HIP(hipMalloc(&dsrc, static_cast<size_t>(bytes)));
+        GV_CHECK_HIP(hipMemcpy(dsrc, data, static_cast<size_t>(bytes), hipMemcpyHostToDevice));
+        const auto *q = static_cast<const int8_t *>(dsrc);
+        const auto *sc = reinterpret_cast<const float *>(q + 2 * n * kv_row);
+        hipLaunchKernelGGL(kv8_copy_kernel, dim3(static_cast<unsigned>((2 * n * kv_row + 255) / 256)), dim3(256), 0,
+                           stream(), q, sc, static_cast<int>(n), static_cast<int>(nkv), static_cast<int>(hd), m.slots,
+                           L->kv8, L->kvs);
         GV_CHECK_HIP(hipGetLastError());
         GV_CHECK_HIP(hipStreamSynchronize(stream()));
         GV_CHECK_HIP(hipFree(dsrc));
@@ -1823,8 +1961,12 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
             for (int kvi = 0; kvi < 2; ++kvi)
                 rc |= fill_normal(tseed(GV_KV, l, kvi), static_cast<int64_t>(ctx) * kv_row, 1.0f,
                                   wf + static_cast<int64_t>(kvi) * ctx * kv_row, st);
-            hipLaunchKernelGGL(kv_from_rows_kernel, dim3(static_cast<unsigned>((2 * ctx * kv_row + 255) / 256)), dim3(256),
-                               0, st, wf, ctx, static_cast<int>(nkv), static_cast<int>(hd), m.slots, L.kv);
+            if (m.kv_i8)
+                hipLaunchKernelGGL(kv8_from_rows_kernel, dim3(static_cast<unsigned>(2 * ctx * nkv)), dim3(256), 0, st,
+                                   wf, ctx, static_cast<int>(nkv), static_cast<int>(hd), m.slots, L.kv8, L.kvs);
+            else
+                hipLaunchKernelGGL(kv_from_rows_kernel, dim3(static_cast<unsigned>((2 * ctx * kv_row + 255) / 256)),
+                                   dim3(256), 0, st, wf, ctx, static_cast<int>(nkv), static_cast<int>(hd), m.slots, L.kv);
         }
     }
     (void)hipStreamSynchronize(st);
@@ -1894,8 +2036,15 @@ int gv_verify_keep(gv_model *g, int kept, const int32_t *path) {
         int *dpath = reinterpret_cast<int *>(m.rlogits);   // scratch: free between verifies
         GV_CHECK_HIP(hipMemcpyAsync(dpath, path, static_cast<size_t>(kept) * 4, hipMemcpyHostToDevice, stream()));
         const int64_t n = static_cast<int64_t>(m.c.n_layers) * m.c.n_kv_heads * m.c.head_dim;
-        hipLaunchKernelGGL(kv_compact_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream(),
-                           m.kv_all, m.c.n_layers, m.c.n_kv_heads, m.c.head_dim, m.slots, m.last_pos, kept, dpath);
+        auto *base = reinterpret_cast<uint8_t *>(m.kv_all);
+        if (m.kv_i8)
+            hipLaunchKernelGGL(kv_compact_kernel<int8_t>, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                               stream(), base, m.kv_layer_bytes, m.c.n_layers, m.c.n_kv_heads, m.c.head_dim, m.slots,
+                               m.last_pos, kept, dpath);
+        else
+            hipLaunchKernelGGL(kv_compact_kernel<_Float16>, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                               stream(), base, m.kv_layer_bytes, m.c.n_layers, m.c.n_kv_heads, m.c.head_dim, m.slots,
+                               m.last_pos, kept, dpath);
         GV_CHECK_HIP(hipGetLastError());
         GV_CHECK_HIP(hipStreamSynchronize(stream()));
     }

@@ -73,6 +73,8 @@ struct LayerW {
     uint8_t *dn_codes = nullptr, *dn_scales = nullptr;   // [E + 1] experts' down
     float *expert_globals = nullptr;                     // [E + 1][3]: gate half, up half, down
     _Float16 *kv = nullptr;   // K [nkv][slots][hd], then V [nkv][slots / 64][hd][64] (model.hip: k_index, v_index)
+    int8_t *kv8 = nullptr;    // the int8 cache: the same layout in int8,
+    float *kvs = nullptr;     // then the scales: K [nkv][slots], V [nkv][slots]
 };
 
 // The prefill MoE's buffers (C5: many rows), allocated for `cap` rows on first use
@@ -108,6 +110,8 @@ struct Model {
     size_t arena_bytes = 0;
     int32_t *route_ids = nullptr;   // [n_layers][max_rows][K]
     _Float16 *kv_all = nullptr;
+    bool kv_i8 = false;              // the KV cache in int8 (config kv_int8)
+    size_t kv_layer_bytes = 0;       // a layer's cache (values, then the int8 cache's scales)
     int64_t slots = 0;   // KV positions a layer holds: max_ctx rounded up to whole attention blocks
     // host side
     int pos = 0, last_pos = 0, last_n = 0;

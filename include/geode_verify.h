@@ -103,6 +103,8 @@ typedef struct gv_model_config {
     float rope_theta, eps;
     int32_t max_ctx;  /* KV positions the cache holds */
     int32_t max_rows; /* rows a verify takes at most (<= 32) */
+    int32_t kv_int8;  /* 1: the KV cache in int8 with a float scale a (position, KV head), ModelOptions::kv_int8
+                         (engine/src/model.cpp:360-363, :3756-3792); 0: fp16 (attend<_Float16>) */
 } gv_model_config;
 
 /* tensor kinds for gv_model_adopt (numbered as the CPU oracle's) */
@@ -121,7 +123,10 @@ enum {
     GV_EXPERT = 13,       /* the pack's expert block: q4 gate_up [2ff x hidden] then down [hidden x ff];
                              globals[0] gate_up, globals[1] down (engine/src/pack.cpp:329-333) */
     GV_SHARED_EXPERT = 14,/* q4 gate [ff x hidden], up [ff x hidden], down [hidden x ff]; globals[3] */
-    GV_KV = 17            /* fp16 [2][n_positions][n_kv_heads*hd]: K then V of positions 0.. */
+    GV_KV = 17,           /* fp16 [2][n_positions][n_kv_heads*hd]: K then V of positions 0.. (an int8 cache
+                             quantizes each (position, KV head) row as quant_kv_row does, model.cpp:3766-3774) */
+    GV_KV_I8 = 18         /* int8 cache only: int8 [2][n_positions][n_kv_heads*hd] then float [2][n_positions]
+                             [n_kv_heads] scales, the reference's int8 chunk layout (model.cpp:3756-3763) */
 };
 
 typedef struct gv_model gv_model;

@@ -84,16 +84,22 @@ typedef struct {
     float rope_theta, eps;
     int max_ctx;
     int attn_block;   // positions per attention block (model.hpp:458, kAttnBlock = 1024)
+    int kv_int8;      // 1: the KV cache in int8, a scale a (position, KV head) (ModelOptions::kv_int8); 0: fp16
 } orc_config;
 
 // tensor kinds (shared numbering with include/geode_verify.h)
 enum {
     ORC_EMBED = 0, ORC_LM_HEAD = 1, ORC_FINAL_NORM = 2, ORC_IN_NORM = 3, ORC_POST_NORM = 4, ORC_Q = 5, ORC_K = 6,
     ORC_V = 7, ORC_O = 8, ORC_Q_NORM = 9, ORC_K_NORM = 10, ORC_ROUTER = 11, ORC_SHARED_GATE = 12, ORC_EXPERT = 13,
-    ORC_SH_GATE = 14, ORC_SH_UP = 15, ORC_SH_DOWN = 16, ORC_KV = 17
+    ORC_SH_GATE = 14, ORC_SH_UP = 15, ORC_SH_DOWN = 16, ORC_KV = 17,
+    ORC_KV8 = 18,   // int8 KV: [K, V][max_ctx][nkv * hd] bytes
+    ORC_KVS = 19    // int8 KV: [K, V][max_ctx][nkv] float scales
 };
 
 typedef struct orc_model orc_model;
+// quant_kv_row (model.cpp:3766-3774): a KV head's row to int8, scale = amax / 127, q = clamp(nearbyint(x * (127 /
+// amax)), -127, 127) (0 when amax = 0)
+void orc_quant_kv_row(const float *x, int n, int8_t *q, float *scale);
 orc_model *orc_model_create(const orc_config *cfg);
 void orc_model_free(orc_model *m);
 // A tensor's bytes (pack layout / f32 / bf16 / fp16 KV [2][max_ctx][nkv*hd]), their size and global scale(s)

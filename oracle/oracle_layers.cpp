@@ -118,6 +118,8 @@ struct Layer {
     float gq = 1, gk = 1, gv = 1, go = 1, gsg = 1, gsu = 1, gsd = 1;
     std::vector<float> expert_globals;   // [E][2]
     std::vector<uint16_t> router, shared_gate, kv;   // kv: [2][max_ctx][nkv * hd] fp16
+    std::vector<int8_t> kv8;                         // int8 KV: [2][max_ctx][nkv * hd]
+    std::vector<float> kvs;                          // int8 KV: [2][max_ctx][nkv] scales
 };
 
 }  // namespace orc
@@ -160,8 +162,19 @@ std::vector<char> ancestry(const int32_t *parents, int n) {
     return a;
 }
 
+// quant_kv_row (model.cpp:3766-3774)
+void quant_kv_row(const float *x, int n, int8_t *q, float &scale) {
+    float amax = 0.0f;
+    for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(x[i]));
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    for (int i = 0; i < n; ++i) q[i] = static_cast<int8_t>(std::clamp(std::nearbyint(x[i] * inv), -127.0f, 127.0f));
+    scale = amax / 127.0f;
+}
+
 // Model::attention + attend + attend_heads (model.cpp:3690-4019) for the n rows at slots pos.., rotary positions
-// pos + depth. KV in fp16 (attend<_Float16>). h: the in-norm's output; mix: o_proj's.
+// pos + depth. KV in fp16 (attend<_Float16>) or int8 (attend<int8_t>: a scale a position and KV head, the K scale
+// in the score's factor, model.cpp:3929-3948, the V scale in the weights after their sum, :3965-3972). h: the
+// in-norm's output; mix: o_proj's.
 void attention(const orc_model &m, Layer &L, int n, const float *h, int pos, const int32_t *parents, int mode,
                float *mix) {
     const auto &c = m.c;
@@ -205,12 +218,32 @@ void attention(const orc_model &m, Layer &L, int n, const float *h, int pos, con
             rope(k);
         }
     }
-    uint16_t *K = L.kv.data(), *V = L.kv.data() + static_cast<size_t>(c.max_ctx) * kv_row;
-    for (int t = 0; t < n; ++t)
+    const bool i8 = c.kv_int8 != 0;
+    uint16_t *K = i8 ? nullptr : L.kv.data(), *V = i8 ? nullptr : L.kv.data() + static_cast<size_t>(c.max_ctx) * kv_row;
+    int8_t *K8 = i8 ? L.kv8.data() : nullptr, *V8 = i8 ? L.kv8.data() + static_cast<size_t>(c.max_ctx) * kv_row : nullptr;
+    float *KS = i8 ? L.kvs.data() : nullptr, *VS = i8 ? L.kvs.data() + static_cast<size_t>(c.max_ctx) * nkv : nullptr;
+    for (int t = 0; t < n; ++t) {
+        if (i8) {   // attend<int8_t> (model.cpp:3787-3792)
+            for (int kh = 0; kh < nkv; ++kh) {
+                const size_t o = static_cast<size_t>(kh) * hd, r = static_cast<size_t>(pos + t);
+                quant_kv_row(ks.data() + static_cast<size_t>(t) * kv_row + o, hd, K8 + r * kv_row + o, KS[r * nkv + kh]);
+                quant_kv_row(vs.data() + static_cast<size_t>(t) * kv_row + o, hd, V8 + r * kv_row + o, VS[r * nkv + kh]);
+            }
+            continue;
+        }
         for (size_t i = 0; i < kv_row; ++i) {
             K[static_cast<size_t>(pos + t) * kv_row + i] = f32_to_f16(ks[static_cast<size_t>(t) * kv_row + i]);
             V[static_cast<size_t>(pos + t) * kv_row + i] = f32_to_f16(vs[static_cast<size_t>(t) * kv_row + i]);
         }
+    }
+    auto kval = [&](int s, int kh, int i) {   // K as the attention reads it: fp16, or the int8 value itself
+        const size_t o = static_cast<size_t>(s) * kv_row + static_cast<size_t>(kh) * hd + i;
+        return i8 ? static_cast<float>(K8[o]) : f16_to_f32(K[o]);
+    };
+    auto vval = [&](int s, int kh, int i) {
+        const size_t o = static_cast<size_t>(s) * kv_row + static_cast<size_t>(kh) * hd + i;
+        return i8 ? static_cast<float>(V8[o]) : f16_to_f32(V[o]);
+    };
     const std::vector<char> vis = ancestry(parents, n);
     const int group = nh / nkv, blk = c.attn_block;
     const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
@@ -232,12 +265,12 @@ void attention(const orc_model &m, Layer &L, int n, const float *h, int pos, con
                 float mx = -std::numeric_limits<float>::infinity();
                 sc.resize(slots.size());
                 for (size_t p = 0; p < slots.size(); ++p) {
-                    const uint16_t *k = K + static_cast<size_t>(slots[p]) * kv_row + static_cast<size_t>(kh) * hd;
                     float acc[8] = {};
                     for (int i = 0; i < hd; i += 8)
-                        for (int j = 0; j < 8; ++j) acc[j] += q[i + j] * f16_to_f32(k[i + j]);
+                        for (int j = 0; j < 8; ++j) acc[j] += q[i + j] * kval(slots[p], kh, i + j);
                     const float dot = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
-                    const float sv = dot * scale;
+                    const float f = i8 ? scale * KS[static_cast<size_t>(slots[p]) * nkv + kh] : scale;
+                    const float sv = dot * f;
                     sc[p] = sv;
                     mx = std::max(mx, sv);
                 }
@@ -246,15 +279,15 @@ void attention(const orc_model &m, Layer &L, int n, const float *h, int pos, con
                     sc[p] = std::exp(sc[p] - mx);
                     sum += sc[p];
                 }
+                if (i8)   // each position's V scale into its weights (the sum above is the softmax's own)
+                    for (size_t p = 0; p < slots.size(); ++p) sc[p] *= VS[static_cast<size_t>(slots[p]) * nkv + kh];
                 float *dst = part.data() + static_cast<size_t>(b) * (hd + 2);
                 dst[hd] = mx;
                 dst[hd + 1] = sum;
                 for (int i = 0; i < hd; i += 8) {
                     float acc[8] = {};
-                    for (size_t p = 0; p < slots.size(); ++p) {
-                        const uint16_t *v = V + static_cast<size_t>(slots[p]) * kv_row + static_cast<size_t>(kh) * hd + i;
-                        for (int j = 0; j < 8; ++j) acc[j] += sc[p] * f16_to_f32(v[j]);
-                    }
+                    for (size_t p = 0; p < slots.size(); ++p)
+                        for (int j = 0; j < 8; ++j) acc[j] += sc[p] * vval(slots[p], kh, i + j);
                     std::memcpy(dst + i, acc, sizeof acc);
                 }
             }
@@ -369,6 +402,8 @@ orc_model *orc_model_create(const orc_config *cfg) {
 
 void orc_model_free(orc_model *m) { delete m; }
 
+void orc_quant_kv_row(const float *x, int n, int8_t *q, float *scale) { orc::quant_kv_row(x, n, q, *scale); }
+
 void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma, int ctx, int fast) {
     const auto &c = m->c;
     const int H = c.hidden, E = c.n_experts, F = c.moe_ff, SF = c.shared_ff, nh = c.n_heads, nkv = c.n_kv_heads,
@@ -404,11 +439,27 @@ void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma
         L.gsg = fill_q4(L.sh_gate, SF, H, tensor_seed(seed, ORC_SH_GATE, l, 0), sigma, fast);
         L.gsu = fill_q4(L.sh_up, SF, H, tensor_seed(seed, ORC_SH_UP, l, 0), sigma, fast);
         L.gsd = fill_q4(L.sh_down, H, SF, tensor_seed(seed, ORC_SH_DOWN, l, 0), sigma, fast);
-        L.kv.assign(2 * static_cast<size_t>(c.max_ctx) * kv_row, 0);
-        if (ctx > 0) {
+        if (c.kv_int8) {
+            L.kv.clear();
+            L.kv8.assign(2 * static_cast<size_t>(c.max_ctx) * kv_row, 0);
+            L.kvs.assign(2 * static_cast<size_t>(c.max_ctx) * nkv, 0.0f);
+        } else {
+            L.kv.assign(2 * static_cast<size_t>(c.max_ctx) * kv_row, 0);
+        }
+        if (ctx > 0) {   // the context's keys and values N(0, 1), stored as the cache stores them
             std::vector<float> f(static_cast<size_t>(ctx) * kv_row);
             for (int kvi = 0; kvi < 2; ++kvi) {
                 orc_fill_normal(tensor_seed(seed, ORC_KV, l, kvi), static_cast<int64_t>(f.size()), 0.0f, 1.0f, f.data());
+                if (c.kv_int8) {
+                    int8_t *dst = L.kv8.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
+                    float *sd = L.kvs.data() + static_cast<size_t>(kvi) * c.max_ctx * nkv;
+                    for (int p = 0; p < ctx; ++p)
+                        for (int kh = 0; kh < nkv; ++kh) {
+                            const size_t o = static_cast<size_t>(p) * kv_row + static_cast<size_t>(kh) * hd;
+                            quant_kv_row(f.data() + o, hd, dst + o, sd[static_cast<size_t>(p) * nkv + kh]);
+                        }
+                    continue;
+                }
                 uint16_t *dst = L.kv.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
                 for (size_t i = 0; i < f.size(); ++i) dst[i] = f32_to_f16(f[i]);
             }
@@ -443,6 +494,8 @@ uint8_t *orc_model_tensor(orc_model *m, int kind, int layer, int expert, int64_t
     case ORC_SH_UP: return ret(L.sh_up, L.gsu, 0);
     case ORC_SH_DOWN: return ret(L.sh_down, L.gsd, 0);
     case ORC_KV: return ret(L.kv, 0, 0);
+    case ORC_KV8: return ret(L.kv8, 0, 0);
+    case ORC_KVS: return ret(L.kvs, 0, 0);
     case ORC_EXPERT: {
         if (expert < 0 || expert >= m->c.n_experts) return nullptr;
         const size_t eb = expert_block_bytes(m->c);
@@ -518,14 +571,22 @@ int orc_model_keep(orc_model *m, int kept, const int32_t *path) {
     if (path) {
         for (int j = 0; j < kept; ++j)
             if (path[j] < 0 || path[j] >= m->last_n || (j > 0 && path[j] <= path[j - 1])) return -1;
+        const size_t nkv = static_cast<size_t>(c.n_kv_heads);
         for (auto &L : m->layers)
-            for (int kvi = 0; kvi < 2; ++kvi) {
-                uint16_t *base = L.kv.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
-                for (int j = 0; j < kept; ++j)
-                    if (path[j] != j)
-                        std::memmove(base + static_cast<size_t>(m->last_pos + j) * kv_row,
-                                     base + static_cast<size_t>(m->last_pos + path[j]) * kv_row, kv_row * 2);
-            }
+            for (int kvi = 0; kvi < 2; ++kvi)
+                for (int j = 0; j < kept; ++j) {
+                    if (path[j] == j) continue;
+                    const size_t to = static_cast<size_t>(m->last_pos + j), from = static_cast<size_t>(m->last_pos + path[j]);
+                    if (c.kv_int8) {
+                        int8_t *base = L.kv8.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
+                        float *sb = L.kvs.data() + static_cast<size_t>(kvi) * c.max_ctx * nkv;
+                        std::memmove(base + to * kv_row, base + from * kv_row, kv_row);
+                        std::memmove(sb + to * nkv, sb + from * nkv, nkv * sizeof(float));
+                    } else {
+                        uint16_t *base = L.kv.data() + static_cast<size_t>(kvi) * c.max_ctx * kv_row;
+                        std::memmove(base + to * kv_row, base + from * kv_row, kv_row * 2);
+                    }
+                }
     }
     m->pos = m->last_pos + kept;
     return 0;

@@ -27,7 +27,8 @@ def q4_row_bytes(cols):
 class Config(_c.Structure):
     _fields_ = [(n, _c.c_int) for n in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff",
                                         "n_heads", "n_kv_heads", "head_dim", "rope_dim")] + \
-               [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int), ("attn_block", _c.c_int)]
+               [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int), ("attn_block", _c.c_int),
+                ("kv_int8", _c.c_int)]
 
 
 class MoeWeights(_c.Structure):
@@ -38,7 +39,7 @@ class MoeWeights(_c.Structure):
 
 # tensor kinds, numbered as in oracle.h and include/geode_verify.h
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, Q, K, V, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, SH_GATE, \
-    SH_UP, SH_DOWN, KV = range(18)
+    SH_UP, SH_DOWN, KV, KV8, KVS = range(20)
 
 
 def _load():
@@ -69,6 +70,7 @@ def _load():
         "orc_ffn_swiglu": (None, [_P, _P, _P, _c.c_float, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _c.c_int, _P,
                                   _c.c_int, _P]),
         "orc_moe_layer": (None, [_c.POINTER(MoeWeights), _c.c_int, _P, _P, _c.c_int, _P, _P, _P, _P]),
+        "orc_quant_kv_row": (None, [_P, _c.c_int, _P, _P]),
         "orc_model_create": (_P, [_c.POINTER(Config)]),
         "orc_model_free": (None, [_P]),
         "orc_model_tensor": (_P, [_P, _c.c_int, _c.c_int, _c.c_int, _c.POINTER(_c.c_int64), _P]),
@@ -201,6 +203,15 @@ def rmsnorm(x, w, eps=1e-6, zero_centered=True):
     lib.orc_rmsnorm(_ptr(x), _ptr(np.ascontiguousarray(w, np.float32)) if w is not None else None, _ptr(out), x.size,
                     eps, int(zero_centered))
     return out
+
+
+def quant_kv_row(x):
+    """(int8 row, scale) as quant_kv_row makes them (model.cpp:3766-3774)"""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(x.size, np.int8)
+    s = np.zeros(1, np.float32)
+    lib.orc_quant_kv_row(_ptr(x), x.size, _ptr(q), _ptr(s))
+    return q, float(s[0])
 
 
 def route_topk(logits, K):

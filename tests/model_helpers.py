@@ -52,9 +52,17 @@ def adopt_oracle_model(gm, om, ctx):
         su, gsu = om.tensor(po.SH_UP, l)
         sd, gsd = om.tensor(po.SH_DOWN, l)
         gm.adopt(g.SHARED_EXPERT, np.concatenate([sg, su, sd]), layer=l, globals_=[gsg[0], gsu[0], gsd[0]])
-        kv, _ = om.tensor(po.KV, l)
-        kv = kv.view(np.uint16).reshape(2, c["max_ctx"], nkv * hd)
-        gm.adopt(g.KV, np.ascontiguousarray(kv[:, :ctx]), layer=l)
+        if c.get("kv_int8"):   # the int8 rows and their scales, the reference's int8 chunk layout
+            q, _ = om.tensor(po.KV8, l)
+            sc, _ = om.tensor(po.KVS, l)
+            q = q.reshape(2, c["max_ctx"], nkv * hd)[:, :ctx]
+            sc = sc.view(np.float32).reshape(2, c["max_ctx"], nkv)[:, :ctx]
+            gm.adopt(g.KV_I8, np.concatenate([q.reshape(-1), np.ascontiguousarray(sc).view(np.uint8).reshape(-1)]),
+                     layer=l)
+        else:
+            kv, _ = om.tensor(po.KV, l)
+            kv = kv.view(np.uint16).reshape(2, c["max_ctx"], nkv * hd)
+            gm.adopt(g.KV, np.ascontiguousarray(kv[:, :ctx]), layer=l)
     gm.position = ctx
 
 
