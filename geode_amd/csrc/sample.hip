@@ -30,6 +30,7 @@ namespace {
 
 constexpr int kSelThreads = 1024;
 constexpr int kMaxCand = 16384;   // candidates a row can keep (the full-vocabulary nucleus must fit)
+constexpr int kRowBatch = 8;      // a row's values a thread loads at once in the full-row passes
 
 // float -> a key whose unsigned order is the float order (-0 taken as +0: equal floats, equal keys)
 __device__ inline uint32_t fkey(float f) {
@@ -106,10 +107,17 @@ __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float *__restri
         __syncthreads();
         const uint32_t prefix = s_prefix, mask = s_mask, need = s_need;
         uint32_t mk = 0;
-        for (int i = tid; i < V; i += nthr) {
-            const uint32_t k = fkey(row[i]);
-            if (p == 0) mk = max(mk, k);
-            if ((k & mask) == prefix) atomicAdd(&hist[(k >> sh) & (nb - 1)], 1u);
+        for (int i0 = tid; i0 < V; i0 += kRowBatch * nthr) {   // kRowBatch loads in flight a thread
+            float v[kRowBatch];
+#pragma unroll
+            for (int u = 0; u < kRowBatch; ++u) v[u] = row[min(i0 + u * nthr, V - 1)];
+#pragma unroll
+            for (int u = 0; u < kRowBatch; ++u) {   // (no branch before the uses: no load sinks into one)
+                const bool in = i0 + u * nthr < V;
+                const uint32_t k = fkey(v[u]);
+                if (p == 0) mk = max(mk, in ? k : 0u);
+                if (in && (k & mask) == prefix) atomicAdd(&hist[(k >> sh) & (nb - 1)], 1u);
+            }
         }
         if (p == 0) atomicMax(&s_maxkey, mk);
         __syncthreads();
@@ -143,14 +151,22 @@ __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float *__restri
     const bool all_eq = cnt_eq == need_eq;
     const float mx = key_val(s_maxkey);
     double esum = 0.0;
-    for (int i = tid; i < V; i += nthr) {
-        const float f = row[i];
-        const uint32_t k = fkey(f);
-        if (full_sum) esum += static_cast<double>(expf(__fdiv_rn(__fsub_rn(f, mx), T)));
-        if (k > tau || (all_eq && k == tau)) {
-            const uint32_t slot = atomicAdd(&s_cnt, 1u);
-            if (slot < static_cast<uint32_t>(K))
-                comp[slot] = (static_cast<uint64_t>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+    for (int i0 = tid; i0 < V; i0 += kRowBatch * nthr) {
+        float v[kRowBatch];
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) v[u] = row[min(i0 + u * nthr, V - 1)];
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+            const int i = i0 + u * nthr;
+            const bool in = i < V;
+            const float f = v[u];
+            const uint32_t k = fkey(f);
+            if (full_sum) esum += in ? static_cast<double>(expf(__fdiv_rn(__fsub_rn(f, mx), T))) : 0.0;
+            if (in && (k > tau || (all_eq && k == tau))) {
+                const uint32_t slot = atomicAdd(&s_cnt, 1u);
+                if (slot < static_cast<uint32_t>(K))
+                    comp[slot] = (static_cast<uint64_t>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+            }
         }
     }
     if (!all_eq) {   // ties at the threshold beyond what is needed: the lowest indices, in index order
