@@ -188,7 +188,9 @@ __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float *__restri
         if (tid == 0) osum[blockIdx.x] = s;
     }
     __syncthreads();
-    // bitonic sort, descending
+    // bitonic sort, descending. Pair i of a stage of stride s <= 64 has both elements in [128 (i / 64), + 128): a
+    // wave's 64 consecutive pairs keep the same 128 elements from one such stage to the next, so between two of them
+    // the wave only waits for its own LDS writes; a workgroup barrier follows every other stage.
     for (int size = 2; size <= KP; size <<= 1)
         for (int stride = size / 2; stride > 0; stride >>= 1) {
             for (int i = tid; i < KP / 2; i += nthr) {
@@ -200,7 +202,14 @@ __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float *__restri
                     comp[hi] = a;
                 }
             }
-            __syncthreads();
+            const int next = stride > 1 ? stride / 2 : size;   // the next stage's stride (size * 2 / 2)
+            if (stride <= 64 && next <= 64 && !(stride == 1 && size == KP)) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            } else {
+                __syncthreads();
+            }
         }
     uint32_t *ok = okey + static_cast<int64_t>(blockIdx.x) * ostride;
     int32_t *oi = oidx + static_cast<int64_t>(blockIdx.x) * ostride;
