@@ -77,6 +77,7 @@ SIGNATURES = {
     "gv_model_trace_read": (_c.c_int64, [_P, _P, _c.c_int64]),
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
+    "gv_model_layer": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
                                   _P, _P]),
     "gv_accept_match": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
@@ -365,6 +366,20 @@ class VerifyModel:
                                   else None, out.ctypes.data_as(_P), ids.ctypes.data_as(_P), wts.ctypes.data_as(_P)),
               "gv_model_moe")
         return out, ids, wts
+
+    def layer(self, layer, x_in, parents=None):
+        """one layer on the residual stream x_in [n][hidden] at the current position: (x after the attention, x after
+        the MoE, routed ids [n][top_k]); the position does not move"""
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        n, H, K = x_in.shape[0], self.cfg["hidden"], self.cfg["top_k"]
+        par = np.ascontiguousarray(parents, np.int32) if parents is not None else None
+        mid = np.empty((n, H), np.float32)
+        out = np.empty((n, H), np.float32)
+        ids = np.empty((n, K), np.int32)
+        check(_lib().gv_model_layer(self.h, layer, x_in.ctypes.data_as(_P), n,
+                                    par.ctypes.data_as(_P) if par is not None else None, mid.ctypes.data_as(_P),
+                                    out.ctypes.data_as(_P), ids.ctypes.data_as(_P)), "gv_model_layer")
+        return mid, out, ids
 
     def moe_replay(self, reps=20):
         """mean ms of the last moe() block re-run on its device-staged inputs (device work only)"""

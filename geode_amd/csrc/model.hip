@@ -333,7 +333,9 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
                 pbl[kc][4 + j] = pl[2 * kc + 1][j];
             }
         float *dst = parts + ((static_cast<int64_t>(tq) * nh + hq) * nb_max + b) * (hd + 2);
-        for (int dt0 = 0; dt0 < hd / 16; dt0 += 4) {   // four 16-dim tiles at a time, hi and lo apart
+        constexpr int NDT = hd / 16;   // 16-dim tiles of the head (2 NCH: not always a multiple of four)
+#pragma unroll
+        for (int dt0 = 0; dt0 < NDT; dt0 += 4) {   // four 16-dim tiles at a time, hi and lo apart
             float4v oh[4], ol[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) oh[k] = ol[k] = float4v{0, 0, 0, 0};
@@ -341,6 +343,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
+                    if (dt0 + k >= NDT) break;   // (compile time: the loops are unrolled)
                     const _Float16 *vrow = vs + ((dt0 + k) * 16 + lq) * kAttnVld;
                     const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
                     const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
@@ -352,6 +355,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             if (qvalid)
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
+                    if (dt0 + k >= NDT) break;
                     const float4v c = oh[k] + ol[k];
                     *reinterpret_cast<float4 *>(dst + (dt0 + k) * 16 + 4 * lg) = make_float4(c[0], c[1], c[2], c[3]);
                 }
@@ -1596,7 +1600,12 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         return nullptr;
     }
     const gv_model_config c = *cfg;
+    Model *made = nullptr;   // once set, a failure frees what it allocated
     auto fail = [&](const std::string &msg) -> gv_model * {
+        if (made) {
+            for (void *p : made->allocs) (void)hipFree(p);
+            made->allocs.clear();
+        }
         put_err(err, err_len, msg);
         set_error(msg);
         return nullptr;
@@ -1623,6 +1632,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     }
     auto g = std::make_unique<gv_model>();
     Model &m = g->m;
+    made = &m;
     m.c = c;
     m.E1 = c.n_experts + 1;
     const int64_t H = c.hidden, F = c.moe_ff, V = c.vocab, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
@@ -1714,11 +1724,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     const int npos = c.max_ctx + kMaxRows;
     ok = ok && (m.rope_cos = static_cast<float *>(dalloc(m, static_cast<size_t>(npos) * std::max(1, half) * 4)));
     ok = ok && (m.rope_sin = static_cast<float *>(dalloc(m, static_cast<size_t>(npos) * std::max(1, half) * 4)));
-    if (!ok) {
-        for (void *p : m.allocs) (void)hipFree(p);
-        m.allocs.clear();
-        return fail("gv_model_create: out of device memory");
-    }
+    if (!ok) return fail("gv_model_create: out of device memory");
     // the rotary table on the host with the reference's float functions (model.cpp:739-740, :3719-3723)
     std::vector<float> inv(static_cast<size_t>(half)), cs(static_cast<size_t>(npos) * half), sn(cs.size());
     for (int i = 0; i < half; ++i)
@@ -2032,7 +2038,14 @@ int gv_verify_keep(gv_model *g, int kept, const int32_t *path) {
     GV_REQUIRE(kept >= 1 && kept <= m.last_n, "gv_verify_keep: 1 <= kept <= n");
     if (path) {
         GV_REQUIRE(path[0] == 0, "gv_verify_keep: the path starts at the root (row 0)");
-        for (int j = 1; j < kept; ++j) GV_REQUIRE(path[j] > path[j - 1] && path[j] < m.last_n, "gv_verify_keep: path");
+        // an ancestor chain of the last verify's tree: path[j] at depth j, its parent path[j - 1] (each kept key was
+        // rotated at pos + depth, so any other path would leave keys at the wrong rotary positions)
+        const StepParams &sp = m.host_sp;
+        for (int j = 1; j < kept; ++j) {
+            GV_REQUIRE(path[j] > path[j - 1] && path[j] < m.last_n, "gv_verify_keep: path must ascend within the rows");
+            GV_REQUIRE(sp.depth[path[j]] == j && ((sp.vis[path[j]] >> path[j - 1]) & 1u) != 0,
+                       "gv_verify_keep: path[j] must be a depth-j child of path[j - 1] in the last verify's tree");
+        }
         int *dpath = reinterpret_cast<int *>(m.rlogits);   // scratch: free between verifies
         GV_CHECK_HIP(hipMemcpyAsync(dpath, path, static_cast<size_t>(kept) * 4, hipMemcpyHostToDevice, stream()));
         const int64_t n = static_cast<int64_t>(m.c.n_layers) * m.c.n_kv_heads * m.c.head_dim;
@@ -2159,6 +2172,48 @@ int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *rou
                                     hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
     m.last_n = 0;   // the step's state is this block's, not a verify's
+    return 0;
+}
+
+int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32_t *parents, float *x_mid,
+                   float *x_out, int32_t *ids) {
+    GV_REQUIRE(g && x_in, "gv_model_layer: null pointer");
+    Model &m = g->m;
+    const auto &c = m.c;
+    GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_layer: no such layer");
+    GV_REQUIRE(n >= 1 && n <= c.max_rows && m.pos + n <= c.max_ctx, "gv_model_layer: 1 <= n <= max_rows, in context");
+    StepParams &sp = m.host_sp;
+    std::memset(&sp, 0, sizeof sp);
+    sp.pos = m.pos;
+    sp.M = n;
+    for (int i = 0; i < n; ++i) {
+        if (parents) {
+            GV_REQUIRE(i == 0 ? parents[0] == -1 : (parents[i] >= 0 && parents[i] < i), "gv_model_layer: parents");
+            sp.depth[i] = i == 0 ? 0 : sp.depth[parents[i]] + 1;
+            sp.vis[i] = (i == 0 ? 0u : sp.vis[parents[i]]) | (1u << i);
+        } else {
+            sp.depth[i] = i;
+            sp.vis[i] = (i == 31) ? 0xFFFFFFFFu : ((1u << (i + 1)) - 1u);
+        }
+    }
+    const hipStream_t st = stream();
+    const int H = c.hidden;
+    GV_CHECK_HIP(hipMemcpyAsync(m.sp, &sp, sizeof sp, hipMemcpyHostToDevice, st));
+    GV_CHECK_HIP(hipMemcpyAsync(m.x, x_in, static_cast<size_t>(n) * H * 4, hipMemcpyHostToDevice, st));
+    // the layer's input norm and operands (in a step: the previous layer's combine, or the embedding)
+    LayerW &L = m.layers[static_cast<size_t>(layer)];
+    if (quantize_act(m.x, H, n, H, L.in_norm, c.eps, m.act_h, act_halves(H), nullptr, 0, st) != 0) return -1;
+    for (int cls : {GV_K_QKV, GV_K_ROPE, GV_K_ATTN, GV_K_MERGE, GV_K_O})
+        if (launch_class(m, cls, layer, n, st) != 0) return -1;
+    if (x_mid) GV_CHECK_HIP(hipMemcpyAsync(x_mid, m.x, static_cast<size_t>(n) * H * 4, hipMemcpyDeviceToHost, st));
+    for (int cls : {GV_K_ROUTER, GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN, GV_K_COMBINE})
+        if (launch_class(m, cls, layer, n, st) != 0) return -1;
+    if (x_out) GV_CHECK_HIP(hipMemcpyAsync(x_out, m.x, static_cast<size_t>(n) * H * 4, hipMemcpyDeviceToHost, st));
+    if (ids)
+        GV_CHECK_HIP(hipMemcpyAsync(ids, m.route_ids + static_cast<int64_t>(layer) * c.max_rows * c.top_k,
+                                    static_cast<size_t>(n) * c.top_k * 4, hipMemcpyDeviceToHost, st));
+    GV_CHECK_HIP(hipStreamSynchronize(st));
+    m.last_n = 0;   // nothing to keep: the position is unchanged
     return 0;
 }
 

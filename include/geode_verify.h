@@ -187,6 +187,13 @@ int gv_model_replay(gv_model *m, int cls, int layer, int reps, float *ms_per_lau
  * output without the residual; ids / weights [M][top_k] (may be NULL). The int8 path. Leaves no verify to keep. */
 int gv_model_moe(gv_model *m, int layer, const float *h, int M, const float *router_logits, float *out,
                  int32_t *ids, float *weights);
+/* One layer of the verify step (the loop body of forward_batch, engine/src/model.cpp:5324-5366) on a given residual
+ * stream: x_in [n][hidden] (host) at the model's position (a chain, or the tree of parents as gv_verify takes it);
+ * x_mid = after the attention's residual add, x_out = after the MoE's, ids [n][top_k] the routed experts (each may be
+ * NULL). The rows' keys and values go to the cache at slots pos.. ; the position does not move and there is nothing
+ * to keep. A checking aid: the layers of a step compared one at a time, each fed the same input. */
+int gv_model_layer(gv_model *m, int layer, const float *x_in, int n, const int32_t *parents, float *x_mid,
+                   float *x_out, int32_t *ids);
 /* Re-run the last gv_model_moe call's block on its device-staged rows and logits reps times back to back and return
  * the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */
 int gv_model_moe_replay(gv_model *m, int reps, float *ms_per_block);

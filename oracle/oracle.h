@@ -116,6 +116,10 @@ int orc_model_position(const orc_model *m);
 // logits [n][vocab]. The position advances by n. trace (may be NULL): per layer the routed ids [L][n][K].
 int orc_model_verify(orc_model *m, const int32_t *tokens, int n, const int32_t *parents, int mode, float *logits,
                      int32_t *route_ids);
+// orc_model_verify plus, per layer l, trace[l][4][n][hidden]: the residual stream into the layer, after the attention's
+// residual add, the post-attention RMSNorm's output (the MoE block's input), and the MoE block's output (may be NULL)
+int orc_model_verify_trace(orc_model *m, const int32_t *tokens, int n, const int32_t *parents, int mode,
+                           float *logits, int32_t *route_ids, float *trace);
 // verify_keep: kept rows stay (chain: rows 0..kept-1; tree: path[0..kept) of row indices, their KV moved to the
 // kept slots); the position becomes the one before the verify plus kept.
 int orc_model_keep(orc_model *m, int kept, const int32_t *path);

@@ -3,12 +3,17 @@
 //
 // TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the HIP path, never part of it.
 //
-// Pinning (tests/test_oracle_layers.py): the reference's Model does not build without a real pack, so these
-// compositions are pinned by reduction to the pinned primitives (oracle_core.cpp) plus invariants the reference
-// states: verify logits equal one-token-at-a-time logits bit for bit (model.hpp:189-193); attention bits do not
-// depend on the block size up to the merge (model.cpp:3799-3804) and equal a float64 softmax within fp32 rounding;
-// a tree row equals the chain over its ancestors; verify + keep equals a verify of the kept prefix. The MoE block is
-// checked against a brute-force restatement (every expert computed densely, the unpicked ones weighted 0).
+// Pinning: the reference's Model does not build without a real pack, so these compositions are pinned
+// (tests/test_oracle_layers.py) against an independent float64 restatement of the whole forward pass written from
+// the reference's formulas (tests/f64_model.py: RMSNorm(1 + w), gated q, q/k norm, RoPE pairs (i, i + half), fp16
+// KV, 1/sqrt(hd) softmax, sigmoid gate, bf16 router, renormalised top-K, SwiGLU experts, sigmoid-gated shared
+// expert), in both arithmetic modes, chain and tree: logits within 4e-6 (exact path) and 4e-5 (int8 path), routing
+// identical; eleven planted slips in the restatement (a dropped scale or gate, a RoPE sign or pairing, the norm's
+// (1 + w), the renormalisation, silu, the mask, the fp16 KV rounding) each land far outside that. The MoE block
+// alone against a dense float64 brute force (every expert computed, the unpicked ones weighted 0); attention bits
+// independent of the block size up to the merge (model.cpp:3799-3855). tests/test_oracle_kv8.py adds the
+// reference's stated invariants: verify logits equal one-token-at-a-time logits bit for bit (model.hpp:189-193), a
+// tree row equals the chain over its ancestors, verify + keep equals a verify of the kept prefix.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -514,6 +519,11 @@ int orc_model_position(const orc_model *m) { return m->pos; }
 
 int orc_model_verify(orc_model *m, const int32_t *tokens, int n, const int32_t *parents, int mode, float *logits,
                      int32_t *route_ids) {
+    return orc_model_verify_trace(m, tokens, n, parents, mode, logits, route_ids, nullptr);
+}
+
+int orc_model_verify_trace(orc_model *m, const int32_t *tokens, int n, const int32_t *parents, int mode,
+                           float *logits, int32_t *route_ids, float *trace) {
     const auto &c = m->c;
     const int H = c.hidden;
     if (n <= 0 || m->pos + n > c.max_ctx) return -1;
@@ -532,6 +542,8 @@ int orc_model_verify(orc_model *m, const int32_t *tokens, int n, const int32_t *
     std::vector<int> ids(static_cast<size_t>(n) * c.top_k);
     for (int l = 0; l < c.n_layers; ++l) {
         Layer &L = m->layers[static_cast<size_t>(l)];
+        float *tr = trace ? trace + static_cast<size_t>(l) * 4 * n * H : nullptr;   // [x in, x mid, h2, moe out]
+        if (tr) std::copy(x.begin(), x.end(), tr);
         for (int t = 0; t < n; ++t)
             rmsnorm(x.data() + static_cast<size_t>(t) * H, L.in_norm.data(), h.data() + static_cast<size_t>(t) * H, H,
                     c.eps, true);
@@ -542,8 +554,13 @@ int orc_model_verify(orc_model *m, const int32_t *tokens, int n, const int32_t *
             for (int i = 0; i < H; ++i) xr[i] += mr[i];
             rmsnorm(xr, L.post_norm.data(), h.data() + static_cast<size_t>(t) * H, H, c.eps, true);
         }
+        if (tr) {
+            std::copy(x.begin(), x.end(), tr + static_cast<size_t>(n) * H);
+            std::copy(h.begin(), h.end(), tr + 2 * static_cast<size_t>(n) * H);
+        }
         const orc_moe_weights w = moe_view(*m, L);
         moe_layer(w, n, h.data(), nullptr, mode, mix.data(), ids.data(), nullptr, nullptr);
+        if (tr) std::copy(mix.begin(), mix.end(), tr + 3 * static_cast<size_t>(n) * H);
         if (route_ids)
             std::copy(ids.begin(), ids.end(), route_ids + static_cast<size_t>(l) * n * c.top_k);
         for (size_t i = 0; i < x.size(); ++i) x[i] += mix[i];

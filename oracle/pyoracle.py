@@ -78,6 +78,7 @@ def _load():
         "orc_model_set_position": (None, [_P, _c.c_int]),
         "orc_model_position": (_c.c_int, [_P]),
         "orc_model_verify": (_c.c_int, [_P, _P, _c.c_int, _P, _c.c_int, _P, _P]),
+        "orc_model_verify_trace": (_c.c_int, [_P, _P, _c.c_int, _P, _c.c_int, _P, _P, _P]),
         "orc_model_keep": (_c.c_int, [_P, _c.c_int, _P]),
         "orc_model_last_times": (None, [_P, _P, _P]),
         "orc_sample": (_c.c_int, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _c.c_double]),
@@ -338,6 +339,20 @@ class Model:
         if rc != 0:
             raise ValueError("orc_model_verify failed")
         return (logits, ids) if route else logits
+
+    def verify_trace(self, tokens, parents=None, mode=0):
+        """(logits, route ids [L][n][K], trace [L][4][n][hidden]: per layer the residual stream in, after the
+        attention's residual add, the MoE block's input (post-norm) and the MoE block's output)"""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        n = tokens.size
+        c = self.cfg
+        logits = np.empty((n, c["vocab"]), np.float32)
+        par = np.ascontiguousarray(parents, np.int32) if parents is not None else None
+        ids = np.empty((c["n_layers"], n, c["top_k"]), np.int32)
+        tr = np.empty((c["n_layers"], 4, n, c["hidden"]), np.float32)
+        if lib.orc_model_verify_trace(self.h, _ptr(tokens), n, _ptr(par), mode, _ptr(logits), _ptr(ids), _ptr(tr)):
+            raise ValueError("orc_model_verify_trace failed")
+        return logits, ids, tr
 
     def keep(self, kept, path=None):
         p = np.ascontiguousarray(path, np.int32) if path is not None else None

@@ -1,0 +1,99 @@
+"""GPU parity at BASELINE.json configs[3]'s own sizes: hidden 2048, 16 query / 2 KV heads of 256 (RoPE on 64 dims),
+256 experts + 1 shared of ff 512, top-8, a context of 8,192 positions and the full 151,936-token vocabulary; the chain
+(k = 4, M = 5) and the 16-node draft tree (M = 17). One layer keeps the oracle within seconds; depth is covered by
+the per-layer comparisons of tests/test_gpu_layers.py. The weights are the oracle's seeded random q4 bytes (valid codes
+and finite E4M3 scales, fast=True: the arithmetic is what is compared), the cache N(0, 1) in fp16.
+
+The bar (north_star): logits within 1e-2 of the oracle's int8 path (max error over max |logit|), routed experts
+identical, greedy tokens identical except at near-ties (rows whose top-2 logit gap is below twice the largest logit
+error). A context of 10,000 positions (157 attention blocks) also runs the merge's loop past its first 144 blocks."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+from model_helpers import adopt_oracle_model, near_tie_rows, rel_err, tree_parents
+
+pytestmark = pytest.mark.gpu
+
+FULL = dict(hidden=2048, vocab=151936, n_layers=1, n_experts=256, top_k=8, moe_ff=512, shared_ff=512, n_heads=16,
+            n_kv_heads=2, head_dim=256, rope_dim=64, rope_theta=1e7, eps=1e-6, max_ctx=8192 + 32, max_rows=17)
+CTX = 8192
+
+
+def _pair(cfg, ctx, seed):
+    import geode_amd
+
+    geode_amd.init(0)
+    om = po.Model(cfg, seed=seed, router_sigma=1.0 / np.sqrt(cfg["hidden"]), ctx=ctx, fast=True)
+    gm = geode_amd.VerifyModel(cfg)
+    adopt_oracle_model(gm, om, ctx)
+    return om, gm
+
+
+@pytest.fixture(scope="module")
+def full():
+    om, gm = _pair(FULL, CTX, 21)
+    yield om, gm
+    gm.close()
+
+
+def _compare(ol, gl, oids, gids, what):
+    err = rel_err(gl, ol)
+    ties = near_tie_rows(ol, 2 * float(np.abs(gl - ol).max()))
+    same = [bool(np.argmax(gl[r]) == np.argmax(ol[r])) for r in range(ol.shape[0])]
+    print(f"{what}: logits max error {err:.3e}, routing agreement {np.mean(oids == gids):.4f}, greedy same "
+          f"{sum(same)}/{len(same)}, near-tie rows {sorted(ties)}", flush=True)
+    assert err <= 1e-2, f"{what}: logits max error {err:.3e}"
+    assert np.array_equal(oids, gids), f"{what}: routing agrees on {np.mean(oids == gids):.4f} of picks"
+    for r in range(ol.shape[0]):
+        assert same[r] or r in ties, f"{what}: greedy token differs at row {r} (no near-tie)"
+
+
+@pytest.mark.parametrize("tree", [False, True])
+def test_full_size_verify_step(full, tree):
+    om, gm = full
+    parents = tree_parents((4, 3)) if tree else None
+    n = 17 if tree else 5
+    toks = (np.arange(n) * 7919 + 101) % FULL["vocab"]
+    om.position = CTX
+    gm.position = CTX
+    ol, oids = om.verify(toks, parents, route=True)
+    gl = gm.verify(toks, parents=parents)
+    _compare(ol, gl, oids, gm.route_ids(n), f"ctx {CTX}, V {FULL['vocab']}, M {n}")
+
+
+def test_full_size_keep_then_verify(full):
+    """verify_keep of a tree path at full size, then the next chain step over the compacted cache"""
+    om, gm = full
+    parents = tree_parents((4, 3))
+    toks = (np.arange(17) * 31 + 5) % FULL["vocab"]
+    kids = [i for i in range(17) if parents[i] == 2]
+    path = [0, 2, kids[1]]   # the root, its second child, that child's second child
+    assert parents[path[1]] == 0 and parents[path[2]] == path[1]
+    om.position = CTX
+    gm.position = CTX
+    om.verify(toks, parents)
+    gm.verify(toks, parents=parents, want_logits=False)
+    om.keep(3, np.array(path, np.int32))
+    gm.keep(3, path)
+    assert gm.position == om.position == CTX + 3
+    toks2 = np.array([17, 4242, 99999, 151935, 0], np.int32)
+    ol, oids = om.verify(toks2, route=True)
+    gl = gm.verify(toks2)
+    _compare(ol, gl, oids, gm.route_ids(5), "after keep")
+
+
+def test_context_past_the_merge_first_pass():
+    """10,000 positions: 157 attention blocks, past the merge's first pass of 144"""
+    cfg = dict(FULL, vocab=1024, max_ctx=10000 + 32)
+    om, gm = _pair(cfg, 10000, 23)
+    try:
+        for parents, n in ((None, 5), (tree_parents((4, 3)), 17)):
+            toks = (np.arange(n) * 131 + 17) % cfg["vocab"]
+            om.position = 10000
+            gm.position = 10000
+            ol, oids = om.verify(toks, parents, route=True)
+            gl = gm.verify(toks, parents=parents)
+            _compare(ol, gl, oids, gm.route_ids(n), f"ctx 10000, M {n}")
+    finally:
+        gm.close()

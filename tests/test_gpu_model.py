@@ -177,3 +177,45 @@ def test_graph_replays_match_direct_launches(models):
         other, _ = step(2, rep % 2 == 0)   # another row count, graphs on and off, between the replays
         assert np.array_equal(other.view(np.uint32), step(2, False)[0].view(np.uint32))
     gm.set_graphs(True)
+
+
+@pytest.mark.parametrize("hd,rope", [(96, 32), (32, 16), (160, 64)])
+def test_head_dims_off_the_64_grid(gv, hd, rope):
+    """head sizes whose 16-dim value tiles are not a multiple of four (the attention's output loop takes them in
+    fours): chain and tree against the oracle"""
+    cfg = dict(SMALL, head_dim=hd, rope_dim=rope, n_heads=4 if hd % 32 == 0 and (4 * hd) % 128 == 0 else 8)
+    om = po.Model(cfg, seed=13, router_sigma=SMALL_ROUTER_SIGMA, ctx=CTX)
+    gm = gv.VerifyModel(cfg)
+    try:
+        adopt_oracle_model(gm, om, CTX)
+        for parents, n in ((None, 5), (tree_parents((4, 3)), 17)):
+            toks = (np.arange(n) * 29 + 3) % cfg["vocab"]
+            om.position = CTX
+            gm.position = CTX
+            ol, oids = om.verify(toks, parents, route=True)
+            gl = gm.verify(toks, parents=parents)
+            _check(ol, gl, oids, gm.route_ids(n))
+    finally:
+        gm.close()
+
+
+def test_route_ties_go_to_the_lower_index(models):
+    """the GPU route (route_kernel through the MoE block entry point) on router logits with exact ties: the lower
+    expert index ranks first, as the oracle's route_topk and the reference's GPU route (gpu8_kernels.inc:974-978)"""
+    om, gm = models
+    E, K, H = SMALL["n_experts"], SMALL["top_k"], SMALL["hidden"]
+    M = 6
+    lg = np.zeros((M, E), np.float32)
+    lg[0, [2, 9, 11, 14, 15]] = 1.5            # five equal maxima for four picks
+    lg[1, :] = 0.25                            # every logit equal
+    lg[2, [0, 15]] = 3.0; lg[2, [4, 5, 6]] = 2.0
+    lg[3] = np.repeat(np.arange(E // 2, dtype=np.float32), 2)[::-1]   # pairs of equal values
+    lg[4, [7, 8]] = -1.0
+    lg[5] = po.normal(77, E, 1.0)
+    lg[5, 3] = lg[5, 12] = lg[5].max()
+    h = po.normal(78, M * H, 1.0).reshape(M, H)
+    _, gids, gw = gm.moe(0, h, lg)
+    for t in range(M):
+        ids, w = po.route_topk(lg[t], K)
+        assert list(gids[t]) == list(ids), (t, list(gids[t]), list(ids))
+        assert np.abs(gw[t] - w).max() <= 1e-6

@@ -10,8 +10,17 @@ import pytest
 import pyoracle as po
 
 GOLDEN = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
-REF = po.load_ref()
 P = po._ptr
+
+
+@pytest.fixture(scope="module")
+def ref():
+    """the reference built here from its own sources (oracle/_ref), loaded only by the CPU tests that use it: it is
+    never shipped to or loaded on the GPU box"""
+    r = po.load_ref()
+    if r is None:
+        pytest.skip("oracle/_ref not built here")
+    return r
 
 
 def u32(a):
@@ -109,19 +118,17 @@ def test_q4_global_formula():
     assert u32(np.float32(GOLDEN["mat_global"])) == u32(np.float32(po.lib.orc_q4_global(P(w), w.size)))
 
 
-def test_q4_pack_matches_reference_blocks():
+def test_q4_pack_matches_reference_blocks(ref):
     # the packed matrix of the fixture: every block equals the reference's q4_block on it (nibble order 2k | 2k+1)
     w, wq, g = GOLDEN["mat_w"], GOLDEN["mat_q4"], float(GOLDEN["mat_global"])
     mine, g2 = po.q4_pack(w)
     assert np.array_equal(mine, wq) and g2 == g
-    if REF is None:
-        pytest.skip("oracle/_ref not built here")
     cols = w.shape[1]
     for r in range(w.shape[0]):
         for b in range(cols // 16):
             s = np.zeros(1, np.uint8)
             c = np.zeros(16, np.uint8)
-            REF.ref_q4_block(P(np.ascontiguousarray(w[r, b * 16:(b + 1) * 16])), g, P(s), P(c))
+            ref.ref_q4_block(P(np.ascontiguousarray(w[r, b * 16:(b + 1) * 16])), g, P(s), P(c))
             assert wq[r, cols // 2 + b] == s[0]
             assert np.array_equal(wq[r, b * 8:(b + 1) * 8], (c[0::2] | (c[1::2] << 4)).astype(np.uint8))
 
@@ -217,15 +224,14 @@ def test_rmsnorm_matches_reference_fixture_and_closed_form():
     assert np.abs(po.rmsnorm(x, w) - want).max() <= 1e-5 * np.abs(want).max()
 
 
-@pytest.mark.skipif(REF is None, reason="oracle/_ref not built here")
 @pytest.mark.parametrize("seed", [11, 12, 13])
-def test_products_against_reference_build(seed):
+def test_products_against_reference_build(ref, seed):
     rows, cols = 48, 512
     wq, g = po.q4_random(seed, rows, cols, 0.05)
     x = po.normal(seed + 100, cols, 2.0)
     for mine, refname in ((po.matvec(wq, cols, g, x), "ref_matvec_rows"), (po.matvec_q(wq, cols, g, x), "ref_matvec_rows_q")):
         y = np.empty(rows, np.float32)
-        getattr(REF, refname)(P(wq), rows, cols, g, P(x), P(y))
+        getattr(ref, refname)(P(wq), rows, cols, g, P(x), P(y))
         assert np.array_equal(u32(mine), u32(y))
 
 
