@@ -1822,6 +1822,7 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
         const int64_t kv_row = nkv * hd;
         GV_REQUIRE(bytes % (2 * kv_row * 2) == 0 && bytes / (2 * kv_row * 2) <= c.max_ctx, "gv_model_adopt: kv size");
         const int64_t n = bytes / (2 * kv_row * 2);
+        if (n == 0) return 0;   // an empty context: nothing to convert
         std::vector<float> f(static_cast<size_t>(2 * n * kv_row));
         const auto *hsrc = static_cast<const uint16_t *>(data);
         for (size_t i = 0; i < f.size(); ++i) f[i] = static_cast<float>(__builtin_bit_cast(_Float16, hsrc[i]));
@@ -1846,6 +1847,7 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
         const int64_t kv_row = nkv * hd, per = 2 * (kv_row + nkv * 4);   // bytes a position
         GV_REQUIRE(bytes % per == 0 && bytes / per <= c.max_ctx, "gv_model_adopt: int8 kv size");
         const int64_t n = bytes / per;
+        if (n == 0) return 0;
         void *dsrc = nullptr;
         GV_CHECK_HIP(hipMalloc(&dsrc, static_cast<size_t>(bytes)));
         GV_CHECK_HIP(hipMemcpy(dsrc, data, static_cast<size_t>(bytes), hipMemcpyHostToDevice));

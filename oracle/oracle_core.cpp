@@ -110,9 +110,12 @@ public:
         quit_ = false;
         for (int i = 1; i < n; ++i) workers_.emplace_back([this] { loop(); });
     }
+    // One caller at a time uses the workers; a caller that finds them busy (another host thread's call, or a call
+    // from inside a task) runs its whole range itself, so concurrent callers never share the pool's state.
     void run(int64_t items, int64_t chunk, const std::function<void(int64_t, int64_t)> &fn) {
         if (items <= 0) return;
-        if (workers_.empty() || items <= chunk) {
+        std::unique_lock<std::mutex> own(busy_, std::try_to_lock);
+        if (!own.owns_lock() || workers_.empty() || items <= chunk) {
             fn(0, items);
             return;
         }
@@ -164,6 +167,7 @@ private:
         workers_.clear();
     }
     std::vector<std::thread> workers_;
+    std::mutex busy_;   // held by the caller whose range the workers are on
     std::mutex mu_;
     std::condition_variable cv_, done_cv_;
     const std::function<void(int64_t, int64_t)> *fn_ = nullptr;

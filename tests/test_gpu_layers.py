@@ -6,9 +6,17 @@ thus compared without the errors of the layers before it, which a 40-layer end-t
 cannot do: there, two correct paths that differ only in fp32 summation order flip a routing near-tie within a few
 layers and then diverge (a different expert's output is a different number, not a rounding).
 
-What is asserted a layer (the int8 path's tolerance): the stream after the attention and after the MoE within 1e-3 of
-the oracle's (max error over max |value|), the MoE block's output within 1e-2 of its own scale, and the routed
-experts identical unless the oracle's router has a near-tie at the 8th pick (then reported, not failed)."""
+Measured (MI355X): fed the same input, the attention's stream agrees to ~1e-6 and the MoE block to ~1e-6, yet
+the composed layer's output can differ by ~3e-3: a 1e-6 difference in the MoE's input moves some of its int8
+activation codes (quantize_activation rounds x * 127 / amax) by one step, each step ~1/127 of its block's amax. That
+is the int8 path's own sensitivity, not a GPU error: the oracle moved by the same input difference moves as much.
+So the composition is checked on the GPU's own stream: the oracle's MoE block fed the GPU's post-attention stream
+(its RMSNorm is bit-exact on both sides) must give the GPU's layer output.
+
+Asserted a layer: the attention's stream within 1e-3 of the oracle's (max error over max |value|); the oracle's MoE
+on the GPU's stream within 1e-4 of the GPU's layer output; the MoE block alone within 1e-2; the routed experts
+identical unless the oracle's router has a near-tie at the 8th pick (reported, not failed). The oracle's own
+sensitivity (its MoE fed the GPU's stream against fed its own) is printed beside the GPU's difference."""
 import numpy as np
 import pytest
 
@@ -57,20 +65,26 @@ def test_layers_one_at_a_time(pair, tree):
     for l in range(CFG["n_layers"]):
         x_in, x_mid, h2, moe = tr[l]
         g_mid, g_out, g_ids = gm.layer(l, x_in, parents)
-        want_out = x_mid + moe
-        e_mid, e_out = rel_err(g_mid, x_mid), rel_err(g_out, want_out)
+        e_mid, e_out = rel_err(g_mid, x_mid), rel_err(g_out, x_mid + moe)
+        # the oracle's MoE on the GPU's own stream (the same RMSNorm: bit-exact on both sides)
+        post = om.tensor(po.POST_NORM, l)[0].view(np.float32)
+        h2_g = np.stack([po.rmsnorm(g_mid[r], post, CFG["eps"]) for r in range(n)])
+        moe_g, ids_g, _ = po.moe_layer(om, l, h2_g)
+        e_comp = rel_err(g_out, g_mid + moe_g)
+        e_sens = rel_err(g_mid + moe_g, x_mid + moe)   # the oracle's own move for the GPU's input difference
         m_out, m_ids, _ = gm.moe(l, h2)
         e_moe = rel_err(m_out, moe)
         margin = _router_margin(om, l, h2)
-        agree = float(np.mean(g_ids == oids[l]))
-        print(f"layer {l} M {n}: attention stream {e_mid:.2e}, layer out {e_out:.2e}, MoE block {e_moe:.2e}, "
-              f"routing {agree:.4f} (MoE-alone {np.mean(m_ids == oids[l]):.4f}), smallest 8th/9th gap "
-              f"{margin.min():.2e}", flush=True)
+        print(f"layer {l} M {n}: attention stream {e_mid:.2e}; layer out vs oracle {e_out:.2e}, vs the oracle on "
+              f"the GPU's stream {e_comp:.2e} (the oracle's own sensitivity {e_sens:.2e}); MoE block alone "
+              f"{e_moe:.2e}; routing {np.mean(g_ids == oids[l]):.4f}; smallest 8th/9th gap {margin.min():.2e}",
+              flush=True)
         assert e_mid <= 1e-3, f"layer {l}: the attention's stream differs by {e_mid:.3e}"
         near = margin < 1e-4
         for r in range(n):
             if not near[r]:
                 assert np.array_equal(np.sort(m_ids[r]), np.sort(oids[l][r])), f"layer {l} row {r}: routing differs"
+                assert np.array_equal(np.sort(g_ids[r]), np.sort(ids_g[r])), f"layer {l} row {r}: routing differs"
+        assert e_comp <= 1e-4, f"layer {l}: the GPU layer differs from the oracle on its own stream by {e_comp:.3e}"
         if not near.any():
             assert e_moe <= 1e-2, f"layer {l}: the MoE block differs by {e_moe:.3e}"
-            assert e_out <= 1e-3, f"layer {l}: the layer's output differs by {e_out:.3e}"
