@@ -54,6 +54,7 @@ SIGNATURES = {
     "gv_gemv_q4": (_c.c_int, [_c.POINTER(GvQ4), _P, _c.c_int, _P, _c.c_int64, _c.c_int]),
     "gv_ffn_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int]),
     "gv_ffn_swiglu": (_c.c_int, [_c.POINTER(GvQ4), _c.POINTER(GvQ4), _c.POINTER(GvQ4), _c.c_int, _P, _P, _P]),
+    "gv_ffn_swiglu_noalloc": (_c.c_int, [_c.POINTER(GvQ4), _c.POINTER(GvQ4), _c.POINTER(GvQ4), _c.c_int, _P, _P]),
     "gv_open": (_P, [_c.c_int, _c.c_char_p, _c.c_int]),
     "gv_close": (None, [_P]),
     "gv_adopt_q4": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int64, _c.c_size_t, _c.c_float]),

@@ -13,10 +13,18 @@
 
 namespace gv {
 
+// The workspace of gv_ffn_swiglu_noalloc: a file-scope device array, one copy on each GPU the library runs on, held
+// until the process ends. Host code never passes `scratch` itself (on the host it is only a stand-in for the symbol):
+// gv_init looks up the array's device address once per device (hipGetSymbolAddress) and every use goes through that.
+constexpr size_t kNoAllocScratchBytes = size_t{4} << 20;   // 4 MiB: C1's shape (2048 -> 6144 -> 2048) up to 32 rows
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 struct Runtime {
     int device = -1;
     hipStream_t stream = nullptr;
     std::vector<hipEvent_t> events;
+    void *scratch_dev[kMaxDevices] = {};   // scratch's device address on each device (set by gv_init)
 };
 
 Runtime &rt() {
@@ -73,6 +81,9 @@ struct Scratch {
     }
 };
 
+int ffn_swiglu_ws(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16, float *y,
+                  void *ws);
+
 }  // namespace gv
 
 using namespace gv;
@@ -86,8 +97,14 @@ int gv_init(int device) {
     if (r.stream && r.device == device) return 0;
     int n = 0;
     GV_CHECK_HIP(hipGetDeviceCount(&n));
-    GV_REQUIRE(device >= 0 && device < n, "gv_init: no such device");
+    GV_REQUIRE(device >= 0 && device < n && device < kMaxDevices, "gv_init: no such device");
     GV_CHECK_HIP(hipSetDevice(device));
+    if (!r.scratch_dev[device]) {   // this device's copy of the no-alloc entry point's scratch
+        void *p = nullptr;
+        GV_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        GV_REQUIRE(p, "gv_init: no device address for the scratch array");
+        r.scratch_dev[device] = p;
+    }
     if (r.stream) GV_CHECK_HIP(hipStreamDestroy(r.stream));
     GV_CHECK_HIP(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking));
     r.device = device;
@@ -226,6 +243,30 @@ size_t gv_ffn_workspace_bytes(int64_t hidden, int64_t ff, int M) {
 int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16, float *y,
                   void *ws) {
     if (ensure_init() != 0) return -1;
+    return ffn_swiglu_ws(gate, up, down, M, x_f16, y, ws);
+}
+
+int gv_ffn_swiglu_noalloc(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16,
+                          float *y) {
+    if (ensure_init() != 0) return -1;
+    GV_REQUIRE(gate && up && down, "gv_ffn_swiglu_noalloc: null pointer");
+    GV_REQUIRE(M >= 1 && M <= kMaxRows, "gv_ffn_swiglu_noalloc: 1 <= M <= 32");
+    const size_t need = gv_ffn_workspace_bytes(gate->cols, gate->rows, M);
+    GV_REQUIRE(need <= kNoAllocScratchBytes,
+               "gv_ffn_swiglu_noalloc: this shape needs " + std::to_string(need) +
+                   " bytes of workspace, more than the 4 MiB scratch holds (use gv_ffn_swiglu)");
+    void *ws = rt().scratch_dev[rt().device];
+    GV_REQUIRE(ws, "gv_ffn_swiglu_noalloc: no scratch address for this device");
+    return ffn_swiglu_ws(gate, up, down, M, x_f16, y, ws);
+}
+
+}  // extern "C"
+
+namespace gv {
+// The C1 products on a caller's workspace ws (gv_ffn_workspace_bytes of it): every piece of it is written before it
+// is read (x, the gate and up products, m, the operands), so nothing is cleared between calls.
+int ffn_swiglu_ws(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16, float *y,
+                  void *ws) {
     GV_REQUIRE(gate && up && down && x_f16 && y && ws, "gv_ffn_swiglu: null pointer");
     const int64_t H = gate->cols, F = gate->rows;
     GV_REQUIRE(up->rows == F && up->cols == H && down->rows == H && down->cols == F, "gv_ffn_swiglu: shapes");
@@ -245,8 +286,7 @@ int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, 
     if (quantize_act(m, F, M, static_cast<int>(F), nullptr, 0.0f, act, ab_f, nullptr, 0, st) != 0) return -1;
     return gemv_q4(to_q4(*down), act, ab_f, M, gemv_out(y, H, down->global), st);
 }
-
-}  // extern "C"
+}  // namespace gv
 
 // ---------------------------------------------------------------- the NPU plugin's calls (npu/host/npu_api.h)
 struct gv_ctx {

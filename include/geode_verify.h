@@ -78,6 +78,14 @@ int gv_gemv_q4(const gv_q4 *w, const uint8_t *act, int M, float *y, int64_t ldy,
 size_t gv_ffn_workspace_bytes(int64_t hidden, int64_t ff, int M);
 int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16, float *y,
                   void *ws);
+/* gv_ffn_swiglu without a workspace argument and without allocating: no reference counterpart. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is the library's own 4 MiB device array, one per GPU (its address looked up by gv_init), so
+ * gv_ffn_workspace_bytes(hidden, ff, M) must be at most 4 MiB (C1's 2048 -> 6144 -> 2048 takes up to 32 rows) or the
+ * call fails with a message. Calls on one GPU share that array: calls that overlap on one GPU (other threads,
+ * other streams) race. Same results as gv_ffn_swiglu, bit for bit. */
+int gv_ffn_swiglu_noalloc(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16,
+                          float *y);
 
 /* ------------------------------------------------------------------ the NPU plugin's calls, on this GPU
  * The same names' meaning as npu/host/npu_api.h (gnpu_open / gnpu_adopt_q4 / gnpu_gemm / gnpu_mlp): a handle,
