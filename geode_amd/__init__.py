@@ -74,6 +74,7 @@ SIGNATURES = {
     "gv_model_kernel_time": (_c.c_int, [_P, _P, _P]),
     "gv_model_replay": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _P]),
     "gv_model_set_graphs": (_c.c_int, [_P, _c.c_int]),
+    "gv_model_set_fused": (_c.c_int, [_P, _c.c_int]),
     "gv_model_trace": (_c.c_int, [_P, _c.c_int]),
     "gv_model_trace_read": (_c.c_int64, [_P, _P, _c.c_int64]),
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
@@ -333,6 +334,10 @@ class VerifyModel:
     def set_graphs(self, on):
         """the verify step as one HIP graph per row count (default) or plain launches"""
         check(_lib().gv_model_set_graphs(self.h, 1 if on else 0), "gv_model_set_graphs")
+
+    def set_fused(self, on):
+        """dependent phases chained within one launch where the shapes fit (default) or one launch a phase"""
+        check(_lib().gv_model_set_fused(self.h, 1 if on else 0), "gv_model_set_fused")
 
     def trace(self, on):
         """workgroup clock stamps of the traced kernels on or off (a measurement aid)"""

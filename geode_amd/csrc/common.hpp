@@ -63,6 +63,71 @@ inline size_t q4_scale_bytes(int64_t rows, int64_t cols) {
 inline size_t act_bytes(int64_t cols) { return static_cast<size_t>(cols) * 4; }
 __host__ __device__ inline int64_t act_halves(int64_t cols) { return cols * 2; }
 
+// ---------------------------------------------------------------- data exchanged within one launch
+// Workgroups of one launch on different XCDs do not share an L2: a plain store may sit in the writer's L2 and a plain
+// load may hit a stale line in the reader's. Buffer loads and stores with the sc1 cache policy (gfx940+: device
+// scope) are coherent across the XCDs without a cache maintenance operation (no L2 write-back or invalidate, which on
+// gfx950 costs about as much as a kernel boundary). Every buffer one workgroup writes and another reads later in the
+// same launch goes through these; a producer then waits for its stores and bumps a counter (relaxed, device scope),
+// and its consumers poll the counter before loading. `base` must be uniform across the wave; offsets in bytes.
+typedef uint32_t xu4 __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;   // the sc1 bit of the buffer instructions' cache policy operand
+__device__ inline __amdgpu_buffer_rsrc_t xrs(const void *base) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32));
+    void *p = reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo);
+    // (num_records: the whole 31-bit range; word 3: the 32-bit data format gfx9 buffer accesses require)
+    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), 0x7FFFFFFF, 0x00020000);
+}
+__device__ inline xu4 xld16(const void *base, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(xrs(base), off, 0, kSc1);
+}
+__device__ inline void xst16(void *base, uint32_t off, xu4 v) { __builtin_amdgcn_raw_buffer_store_b128(v, xrs(base), off, 0, kSc1); }
+__device__ inline float xldf(const float *base, uint32_t i) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs(base), i * 4u, 0, kSc1));
+}
+__device__ inline void xstf(float *base, uint32_t i, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), xrs(base), i * 4u, 0, kSc1);
+}
+__device__ inline float4 xld4f(const float *base, uint32_t i) { return __builtin_bit_cast(float4, xld16(base, i * 4u)); }
+__device__ inline void xst4f(float *base, uint32_t i, float4 v) { xst16(base, i * 4u, __builtin_bit_cast(xu4, v)); }
+
+// The producer side: every thread's stores complete, then the workgroup's own flag word is set (a device-scope store;
+// one word a producer: many workgroups bumping one counter serialize at the memory side, ~40 ns each).
+__device__ inline void signal_done(int *flag) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's stores acknowledged (gfx9: vmcnt counts them)
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The consumer side: the first wave polls the n producers' flags (device-scope loads, a few per lane) until every one
+// is set, then the workgroup goes on. Producers always have lower workgroup ids than their consumers (workgroups are
+// dispatched in id order), so they are resident or done and never wait themselves: the wait ends. A bound on the
+// polls all the same (~0.1 s): past it the flag err is set (the host reports it) and the workgroup goes on, so no wave
+// can spin forever.
+constexpr int kMaxPolls = 1 << 17;
+__device__ inline void wait_flags(const int *flags, int n, int *err) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        for (int polls = 0;; ++polls) {
+            int ok = 1;
+            for (int i = lane; i < n; i += 64) ok &= __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+            if (__all(ok)) break;
+            if (polls > kMaxPolls) {
+                if (lane == 0) __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+// Every flag of [0, n) back to zero for the launch's next use (by the launch's last consumer, once every other
+// workgroup has passed its waits)
+__device__ inline void clear_flags(int *flags, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) __hip_atomic_store(flags + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------- a measurement aid: workgroup clock stamps
 // When a translation unit's g_trace is set (gv_model_trace; each source file's kernels have their own copy), thread 0
 // of each workgroup of the traced kernels writes the 100 MHz clock (s_memrealtime) at a few points to

@@ -675,6 +675,227 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     route_all(logits, E, K, M, rs, ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
 }
 
+// ---------------------------------------------------------------- output projection, router and route in one launch
+// Three roles of one launch, each consuming the previous one's results as soon as they exist (no kernel boundary, no
+// cache maintenance: common.hpp's sc1 exchange and counters):
+//   workgroups [0, n_o)            the output projection x += O core (gemv_q4_kernel's products), x stored sc1;
+//   workgroups [n_o, n_o + n_r)    the router: each loads its 4 router rows and the post-norm weights first, then
+//                                  waits for the projection, loads the rows of x, makes the post-attention RMSNorm
+//                                  and the router logits (router_kernel's arithmetic), logits stored sc1;
+//   workgroup n_o + n_r            the route (route_kernel's): waits for the router, then routes the rows.
+// Workgroups are dispatched in id order, so each waits only for workgroups that are resident or done. The route's
+// workgroup clears the launch's flags once everything has passed them (for the next step).
+constexpr int kRT = 260;   // floats a transposed router chain (256 steps + 4: the lanes' 16-byte reads spread over banks)
+constexpr int kMaxRowsMixOut = 8;   // rows the fused launch takes (the verify step's chains; more rows: the kernels apart)
+
+struct MixOutArgs {
+    Q4 o;                       // the output projection [H x nh hd]
+    const _Float16 *act_core;   // its operands (act16 rows)
+    int64_t core_stride;
+    float *x;                   // the residual rows [M][H]
+    int o_per;                  // row tiles a projection workgroup takes
+    const uint16_t *router;     // [E + 1][H] bf16, the shared expert's gate row last
+    const float *post_norm;
+    float eps;
+    float *logits;              // [M][E + 1]
+    _Float16 *act_h;            // the experts' operands (act16 rows of the normalized x)
+    int64_t act_stride;
+    int H, E, E1, K;
+    RouteState *rs;
+    int32_t *ids_out;
+    const StepParams *sp;
+    int *ctr;                   // flags: [0, n_o) a projection workgroup done, [n_o, n_o + n_r) a router workgroup
+    int *err;
+    int n_o, n_r;
+};
+
+template <int KW>
+__device__ inline void mixout_o(const MixOutArgs &a, int wg, f4 *part, uint2 *tab) {
+    trace(GV_K_O, 0);
+    const int M = a.sp->M, H = a.H;
+    const int64_t ntiles = tiles_rows(H);
+    const int64_t t0 = static_cast<int64_t>(wg) * a.o_per;
+    const int nt = static_cast<int>(std::min<int64_t>(a.o_per, ntiles - t0));
+    const int o0 = threadIdx.x;
+    const float g = a.o.global;
+    // the thread's first output item (gemv_q4_kernel's order): its four rows of x loaded with the weights
+    auto item = [&](int o, int64_t &row0, int &j) {
+        const int i = o / 64, ll = o % 64;
+        row0 = (t0 + i) * kTileR + 4 * (ll / 16);
+        j = ll % 16;
+    };
+    float old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto prefetch = [&] {
+        int64_t row0;
+        int j;
+        item(min(o0, nt * 64 - 1), row0, j);
+        const float *p = a.x + static_cast<int64_t>(min(j, M - 1)) * H;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) old[r] = p[min(row0 + r, static_cast<int64_t>(H) - 1)];
+    };
+    if (nt > 0)
+        mfma_tiles<KW, 1, kKeepParts, 0, 3, true>(
+            a.o.codes, a.o.scales, H, static_cast<int>(a.o.cols / kSuperK), 0, nt, M,
+            [&](int j) { return a.act_core + j * a.core_stride; }, [](int64_t, int, float) {}, part, tab, TileRun{t0},
+            prefetch);
+    const int W = blockDim.x / 64;
+    for (int o = o0; o < nt * 64; o += blockDim.x) {   // the waves' partial sums in wave order, then x += sum x global
+        const int i = o / 64, ll = o % 64;
+        f4 sum = part[(i * W + 0) * 64 + ll];
+        for (int w2 = 1; w2 < W; ++w2) sum += part[(i * W + w2) * 64 + ll];
+        int64_t row0;
+        int j;
+        item(o, row0, j);
+        if (j >= M || row0 >= H) continue;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float prev = o == o0 ? old[r] : a.x[j * static_cast<int64_t>(H) + row0 + r];
+            v[r] = prev + sum[r] * g;
+        }
+        xst4f(a.x, static_cast<uint32_t>(j * H + row0), make_float4(v[0], v[1], v[2], v[3]));
+    }
+    trace(GV_K_O, 3);
+    signal_done(a.ctr + wg);
+}
+
+// the router's part (router_kernel's arithmetic on 512 threads, rows of x read once the projection is done)
+__device__ inline void mixout_router(const MixOutArgs &a, int wg, float *lds, double (*red)[4]) {
+    trace(GV_K_ROUTER, 0);
+    const int M = a.sp->M, H = a.H, ng = H / 8, steps = H / 8;
+    const int tid = threadIdx.x, half = tid / 256, g = tid % 256, wave = tid / 64, lane = tid % 64;
+    const int r0 = wg * 4;
+    float *hT = lds;                          // [M][8][kRT]: row t, partial j: values j, j + 8, ... (step u = group)
+    float *wT = hT + static_cast<size_t>(M) * 8 * kRT;   // [4][8][kRT]: the workgroup's router rows, the same order
+    // before the wait: the router rows (4 x H bf16: two 16-byte loads a thread) and the norm weights
+    const float *zero = reinterpret_cast<const float *>(g_zero_act16);
+    uint4 wr[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = min(tid + k * 512, 4 * ng - 1), rr = i / ng, c8 = i % ng;
+        wr[k] = *reinterpret_cast<const uint4 *>(a.router + static_cast<int64_t>(min(r0 + rr, a.E1 - 1)) * H + c8 * 8);
+    }
+    float nw[8];
+    {
+        const float *src = g < ng ? a.post_norm + g * 8 : zero;
+        const float4 p = *reinterpret_cast<const float4 *>(src), q = *reinterpret_cast<const float4 *>(src + 4);
+        const float t8[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nw[i] = __fadd_rn(1.0f, t8[i]);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {   // the router rows into LDS as fp32, transposed: value c of row rr at chain c % 8, step c / 8
+        const int i = tid + k * 512;
+        if (i >= 4 * ng) break;
+        const int rr = i / ng, c8 = i % ng;
+        const uint32_t u[4] = {wr[k].x, wr[k].y, wr[k].z, wr[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            wT[(rr * 8 + 2 * e) * kRT + c8] = __uint_as_float(u[e] << 16);
+            wT[(rr * 8 + 2 * e + 1) * kRT + c8] = __uint_as_float(u[e] & 0xFFFF0000u);
+        }
+    }
+    trace(GV_K_ROUTER, 1);
+    wait_flags(a.ctr, a.n_o, a.err);
+    trace(GV_K_ROUTER, 2);
+    // the rows of x (sc1: written by the projection in this launch): threads [0, 256) rows 0, 2, ..., [256, 512) rows
+    // 1, 3, ...; group g of each (8 values)
+    constexpr int kRowsPerHalf = kMaxRowsMixOut / 2;
+    float xv[kRowsPerHalf][8];
+#pragma unroll
+    for (int q = 0; q < kRowsPerHalf; ++q) {
+        const int t = min(half + 2 * q, M - 1);
+        const float4 p = g < ng ? xld4f(a.x, static_cast<uint32_t>(t * H + g * 8)) : make_float4(0, 0, 0, 0);
+        const float4 s = g < ng ? xld4f(a.x, static_cast<uint32_t>(t * H + g * 8 + 4)) : make_float4(0, 0, 0, 0);
+        const float t8[8] = {p.x, p.y, p.z, p.w, s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[q][i] = t8[i];
+    }
+    // per row: the double sum of squares (the thread's eight in order, the wave's, then the four waves' in order:
+    // router_kernel's), 1 / RMS, x inv (1 + w) to LDS (transposed) and, for row wg, the experts' operands
+#pragma unroll
+    for (int q = 0; q < kRowsPerHalf; ++q) {
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += static_cast<double>(xv[q][i]) * static_cast<double>(xv[q][i]);
+        ss = wave_sum(ss);
+        if (lane == 0) red[half + 2 * q][wave % 4] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kRowsPerHalf; ++q) {
+        const int t = half + 2 * q;
+        if (t >= M) break;   // uniform over the half
+        const double tot = ((red[t][0] + red[t][1]) + red[t][2]) + red[t][3];
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(H)), a.eps)));
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(xv[q][i], inv), nw[i]);
+        const bool live = g < ng;
+        if (live)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hT[(t * 8 + e) * kRT + g] = v[e];
+        if (t == wg) act16_group(v, g, live, a.act_h + static_cast<int64_t>(wg) * a.act_stride);
+    }
+    __syncthreads();
+    // the dots: wave w < 4 takes router row r0 + w, lane (t = lane / 8, j = lane % 8) partial j of row t in order
+    const int ra = r0 + wave;
+    if (wave < 4 && ra < a.E1) {
+        const int t = lane / 8, j = lane % 8;
+        const float4 *hp = reinterpret_cast<const float4 *>(hT + (min(t, M - 1) * 8 + j) * kRT);
+        const float4 *wp = reinterpret_cast<const float4 *>(wT + (wave * 8 + j) * kRT);
+        float acc = 0.0f;
+        for (int u4 = 0; u4 < steps / 4; u4 += 4) {   // 16 steps' operands read ahead of their sums
+            float4 hh[4], ww[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                hh[k] = hp[u4 + k];
+                ww[k] = wp[u4 + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc = __fadd_rn(acc, __fmul_rn(ww[k].x, hh[k].x));
+                acc = __fadd_rn(acc, __fmul_rn(ww[k].y, hh[k].y));
+                acc = __fadd_rn(acc, __fmul_rn(ww[k].z, hh[k].z));
+                acc = __fadd_rn(acc, __fmul_rn(ww[k].w, hh[k].w));
+            }
+        }
+        // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)) (bf16_row_dots)
+        const float s1 = __fadd_rn(acc, __shfl_down(acc, 4, 64));
+        const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
+        const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
+        if (j == 0 && t < M) xstf(a.logits, static_cast<uint32_t>(t * a.E1 + ra), s3);
+    }
+    trace(GV_K_ROUTER, 3);
+    signal_done(a.ctr + a.n_o + wg);
+}
+
+// the route's part: the router's logits (sc1) into LDS, then route_kernel's route
+__device__ inline void mixout_route(const MixOutArgs &a, float *lds) {
+    const int M = a.sp->M, E1 = a.E1;
+    wait_flags(a.ctr + a.n_o, a.n_r, a.err);
+    float *lg = lds;   // [M][E1]
+    for (int i = threadIdx.x; i < M * E1; i += blockDim.x) lg[i] = xldf(a.logits, static_cast<uint32_t>(i));
+    int *ids = reinterpret_cast<int *>(lg + M * E1);
+    int *cnt = ids + kMaxRows * 16, *start = cnt + 260, *slot_of = start + 260;
+    unsigned *rows = reinterpret_cast<unsigned *>(slot_of + 260);
+    __shared__ int wtot[2][16];
+    clear_flags(a.ctr, a.n_o + a.n_r);   // every other workgroup has passed its waits: ready for the next step
+    __syncthreads();
+    route_all(lg, a.E, a.K, M, a.rs, a.ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
+}
+
+template <int KW>
+__global__ __launch_bounds__(512) void mixout_kernel(const MixOutArgs a) {
+    extern __shared__ uint4 mix_lds[];
+    __shared__ uint2 tab[256];
+    __shared__ double red[kMaxRowsMixOut][4];
+    const int b = blockIdx.x;
+    if (b < a.n_o) mixout_o<KW>(a, b, reinterpret_cast<f4 *>(mix_lds), tab);
+    else if (b < a.n_o + a.n_r) mixout_router(a, b - a.n_o, reinterpret_cast<float *>(mix_lds), red);
+    else mixout_route(a, reinterpret_cast<float *>(mix_lds));
+}
+
 // The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
 // the post-norm rows of the slot's tokens, DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each
 // pick's rows go to out [pick][rows].
@@ -950,6 +1171,23 @@ inline int combine_launch(const float *y, int H, int K, const MixView &mix, int 
                           float eps, _Float16 *act, int64_t act_stride, hipStream_t st) {
     hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, y, H, K, mix, M, x, norm_w, eps, act, act_stride);
     return 0;
+}
+
+// the fused projection + router + route (mixout_kernel) where the shapes fit it: at most 8 rows, hidden <= 2048, the
+// projection's K split over exactly the launch's 8 waves
+inline bool mixout_fits(const Model &m, int M, int &kw) {
+    const auto &c = m.c;
+    if (!m.fused || m.moe_only || M > kMaxRowsMixOut || c.hidden > 2048 || c.hidden % kSuperK || m.E1 > 257) return false;
+    int waves = 0;
+    if (!mfma_split(static_cast<int64_t>(c.n_heads) * c.head_dim, 1, waves, kw) || waves != 8) return false;
+    return kw == 16 || kw == 8 || kw == 4;
+}
+
+inline size_t mixout_lds(int M, int E1, int o_per) {
+    const size_t router = static_cast<size_t>(M + 4) * 8 * kRT * 4;
+    const size_t route = (static_cast<size_t>(M) * E1 + kMaxRows * 16 + 4 * 260) * 4;
+    const size_t o = static_cast<size_t>(o_per) * 8 * 1024;
+    return std::max({router, route, o});
 }
 
 // verify_keep of a tree: the kept path's keys and values moved to the kept slots in every layer; a thread per
@@ -1333,6 +1571,45 @@ int launch_attn(Model &m, LayerW &L, hipStream_t st) {
     }
 }
 
+template <int KW>
+int launch_mixout_t(Model &m, LayerW &L, int l, int M, hipStream_t st) {
+    const auto &c = m.c;
+    const int H = c.hidden;
+    MixOutArgs a{};
+    a.o = L.o;
+    a.act_core = m.act_core;
+    a.core_stride = act_halves(static_cast<int64_t>(c.n_heads) * c.head_dim);
+    a.x = m.x;
+    const int64_t ntiles = tiles_rows(H);
+    a.o_per = static_cast<int>(tiles_per_wg(ntiles, 8, 1));
+    a.router = L.router;
+    a.post_norm = L.post_norm;
+    a.eps = c.eps;
+    a.logits = m.rlogits;
+    a.act_h = m.act_h;
+    a.act_stride = act_halves(H);
+    a.H = H, a.E = c.n_experts, a.E1 = m.E1, a.K = c.top_k;
+    a.rs = m.route + l;
+    a.ids_out = m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k;
+    a.sp = m.sp;
+    a.ctr = m.ctr + static_cast<int64_t>(l) * kFlagsPerLayer;
+    a.err = m.err;
+    a.n_o = static_cast<int>((ntiles + a.o_per - 1) / a.o_per);
+    a.n_r = (m.E1 + 3) / 4;
+    const size_t lds = mixout_lds(M, m.E1, a.o_per);
+    static int granted = 0;
+    if (lds_grant(reinterpret_cast<const void *>(&mixout_kernel<KW>), lds, granted) != 0) return -1;
+    hipLaunchKernelGGL(mixout_kernel<KW>, dim3(static_cast<unsigned>(a.n_o + a.n_r + 1)), dim3(512), lds, st, a);
+    GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+int launch_mixout(Model &m, LayerW &L, int l, int M, int kw, hipStream_t st) {
+    if (kw == 16) return launch_mixout_t<16>(m, L, l, M, st);
+    if (kw == 8) return launch_mixout_t<8>(m, L, l, M, st);
+    return launch_mixout_t<4>(m, L, l, M, st);
+}
+
 // One kernel class of layer l (the embedding and lm_head: l ignored) for M rows; the verify step is these in order.
 int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     const auto &c = m.c;
@@ -1340,7 +1617,11 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     const int64_t abH = act_halves(H), abC = act_halves(static_cast<int64_t>(nh) * hd);
     LayerW &L = m.layers[static_cast<size_t>(l)];
     // classes fused into a neighbour launch nothing and take no events
-    const bool fused = (cls == GV_K_SWIGLU && m.moe_dec) || (cls == GV_K_ROUTE && m.route_in_router && !m.moe_only);
+    int mix_kw = 0;
+    const bool mixout = mixout_fits(m, M, mix_kw);
+    const bool fused = (cls == GV_K_SWIGLU && m.moe_dec) || (cls == GV_K_ROUTE && m.route_in_router && !m.moe_only) ||
+                       ((cls == GV_K_ROUTER || cls == GV_K_ROUTE) && mixout);
+    if (fused) return 0;
     Tick tk(m, fused ? -2 : cls, st);
     switch (cls) {
     case GV_K_EMBED:
@@ -1365,6 +1646,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
                            m.kv_blocks, m.sp, m.act_core, abC);
         return 0;
     case GV_K_O: {   // the residual add is the product's accumulate
+        if (mixout) return launch_mixout(m, L, l, M, mix_kw, st);   // with the router and the route
         GemvOut o = gemv_out(m.x, H, L.o.global, 1);
         o.trace_cls = GV_K_O;
         return gemv_q4(L.o, m.act_core, abC, M, o, st);
@@ -1426,6 +1708,16 @@ int run_layers(Model &m, int M, hipStream_t st) {
             if (launch_class(m, cls, l, M, st) != 0) return -1;
     if (launch_class(m, GV_K_LM_HEAD, 0, M, st) != 0) return -1;
     GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+// A fused launch's bounded wait that ran out (a producer never signalled: a bug, reported rather than hung on): the
+// flag read back after the stream's work; the step's results are then not to be trusted.
+int check_wait_flag(Model &m, hipStream_t st) {
+    int flag = 0;
+    GV_CHECK_HIP(hipMemcpyAsync(&flag, m.err, 4, hipMemcpyDeviceToHost, st));
+    GV_CHECK_HIP(hipStreamSynchronize(st));
+    GV_REQUIRE(flag == 0, "verify: a fused launch's wait for its producers ran out (the step's results are invalid)");
     return 0;
 }
 
@@ -1682,6 +1974,10 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * c.n_layers)));
     ok = ok && (m.counter = static_cast<int *>(dalloc(m, 64)));
     ok = ok && hipMemset(m.counter, 0, 64) == hipSuccess;
+    const size_t ctr_bytes = static_cast<size_t>(c.n_layers) * kFlagsPerLayer * 4 + 256;   // the fused launches' flags, err
+    ok = ok && (m.ctr = static_cast<int *>(dalloc(m, ctr_bytes)));
+    ok = ok && hipMemset(m.ctr, 0, ctr_bytes) == hipSuccess;
+    if (ok) m.err = m.ctr + static_cast<size_t>(c.n_layers) * kFlagsPerLayer;
     {
         int kwu, kwd, waves;
         m.moe_dec = moe_dec_shape(c, kwu, kwd, waves);
@@ -2025,7 +2321,7 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     if (run_step(m, n, st) != 0) return -1;
     if (logits) {
         GV_CHECK_HIP(hipMemcpyAsync(logits, m.logits, static_cast<size_t>(n) * c.vocab * 4, hipMemcpyDeviceToHost, st));
-        GV_CHECK_HIP(hipStreamSynchronize(st));
+        if (check_wait_flag(m, st) != 0) return -1;
     }
     m.last_pos = m.pos;
     m.last_n = n;
@@ -2214,7 +2510,7 @@ int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32
     if (ids)
         GV_CHECK_HIP(hipMemcpyAsync(ids, m.route_ids + static_cast<int64_t>(layer) * c.max_rows * c.top_k,
                                     static_cast<size_t>(n) * c.top_k * 4, hipMemcpyDeviceToHost, st));
-    GV_CHECK_HIP(hipStreamSynchronize(st));
+    if (check_wait_flag(m, st) != 0) return -1;
     m.last_n = 0;   // nothing to keep: the position is unchanged
     return 0;
 }
@@ -2267,6 +2563,20 @@ int64_t gv_model_trace_read(gv_model *g, uint64_t *out, int64_t n) {
 int gv_model_set_graphs(gv_model *g, int on) {
     GV_REQUIRE(g, "gv_model_set_graphs: null model");
     g->m.use_graphs = on != 0;
+    return 0;
+}
+
+int gv_model_set_fused(gv_model *g, int on) {
+    GV_REQUIRE(g, "gv_model_set_fused: null model");
+    Model &m = g->m;
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    m.fused = on != 0;
+    for (auto &ge : m.graphs)   // the graphs hold the other launches: captured again on the next steps
+        if (ge) {
+            (void)hipGraphExecDestroy(ge);
+            ge = nullptr;
+        }
+    for (bool &s : m.seen) s = false;
     return 0;
 }
 

@@ -121,6 +121,9 @@ struct Model {
                                    // 23.5 us vs 10.6 + 6.2, the device-scope fences and one workgroup's route)
     int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
     bool moe_dec = false;          // the decode MoE kernels (moe_up_kernel, moe_down_kernel), where the shapes fit
+    bool fused = true;             // dependent phases chained within one launch where the shapes fit (gv_model_set_fused)
+    int *ctr = nullptr;            // [n_layers][kFlagsPerLayer] the fused launches' flags (each launch clears its own)
+    int *err = nullptr;            // set by a fused launch whose wait ran out (read back by gv_verify)
     uint64_t *trace = nullptr;     // gv_model_trace's stamps [GV_K_COUNT][8192 workgroups][8] (allocated when on)
     Prefill pf;
     std::vector<hipEvent_t> events;   // pairs around the timed class's launches
@@ -135,5 +138,6 @@ struct Model {
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
+constexpr int kFlagsPerLayer = 1024;   // flag words a layer's fused launches have (one a producer workgroup)
 
 }  // namespace gv

@@ -172,6 +172,11 @@ enum {
 /* The verify step runs as one HIP graph per row count (captured on the second step of that count and replayed
  * after; every step parameter lives in device memory). on = 0: plain launches (no reference counterpart). */
 int gv_model_set_graphs(gv_model *m, int on);
+/* on (the default): dependent phases of a layer chained within one launch where the shapes fit (the output
+ * projection, the post-attention RMSNorm + router and the route: workgroups of each phase wait for the previous
+ * phase's counter instead of a kernel boundary); off: one launch a phase. The same results bit for bit (no reference
+ * counterpart). */
+int gv_model_set_fused(gv_model *m, int on);
 /* A measurement aid with no reference counterpart: with on = 1, thread 0 of every workgroup of the traced kernels
  * stamps its clock (s_memrealtime, 100 MHz) at a few points of its work; each launch overwrites its kernel class's
  * stamps. gv_model_trace_read copies them, [GV_K_COUNT][8192 workgroups][8 slots] (0: none), and returns the count

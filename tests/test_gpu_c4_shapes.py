@@ -77,3 +77,23 @@ def test_repeated_steps_identical(models):
         gm.position = CTX
         again = gm.verify(toks)
         assert np.array_equal(again.view(np.uint32), first.view(np.uint32))
+
+
+@pytest.mark.parametrize("tree", [False, True])
+def test_fused_launches_match_separate_kernels(models, tree):
+    """the dependent phases chained within one launch (the default where the shapes fit) against one launch a phase:
+    the same arithmetic in the same order, so the same bits; several steps in a row (graph replays after the second)"""
+    om, gm = models
+    parents = tree_parents((4, 3)) if tree else None
+    n = 17 if tree else 5
+    toks = (np.arange(n) * 211 + 9) % C4_1L["vocab"]
+    gm.set_fused(False)
+    gm.position = CTX
+    want = gm.verify(toks, parents=parents)
+    want_ids = gm.route_ids(n)
+    gm.set_fused(True)
+    for _ in range(5):
+        gm.position = CTX
+        got = gm.verify(toks, parents=parents)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(gm.route_ids(n), want_ids)
