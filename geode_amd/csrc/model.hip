@@ -169,10 +169,15 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
     extern __shared__ _Float16 lds_h[];
     __shared__ float sc_l[I8 ? 256 : 1];   // int8: the block's K scales [0, 64), V scales [64, 128)
     trace(GV_K_ATTN, 0);
-    const int b = blockIdx.x, kh = blockIdx.y;
     const int pos = sp->pos, M = sp->M, total = pos + M;
+    // workgroup i -> (block, KV head): the context's last block (usually a few new rows) of every KV head takes the
+    // highest ids, so that the workgroups past one a CU, dispatched last, are those short ones
+    const int nb_live = (total + kAttnBlock - 1) / kAttnBlock, wi = blockIdx.x;
+    if (wi >= nb_live * nkv) return;
+    const int b = wi < (nb_live - 1) * nkv ? wi / nkv : nb_live - 1;
+    const int kh = wi < (nb_live - 1) * nkv ? wi % nkv : wi - (nb_live - 1) * nkv;
     const int s0 = b * kAttnBlock;
-    if (s0 >= total) return;
+    const int live = total - s0;   // positions of the block inside the context (1 .. 64)
     const int kld = attn_k_ld(hd);
     _Float16 *ks = lds_h, *vs = lds_h + kAttnBlock * kld;
     const int group = nh / nkv, NQ = group * M, nqt = (NQ + 15) / 16;
@@ -206,8 +211,12 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
 #pragma unroll
         for (int u = 0; u < nl; ++u) {
             const int i = min(static_cast<int>(threadIdx.x) + u * 256, nld - 1);
-            kr[u] = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(i / (hd / 16)) * hd + (i % (hd / 16)) * 16);
-            vr[u] = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(i) * 16);
+            // (rows past the context read the last live row again, from the cache: their scores are masked and
+            // their weights zero)
+            const int kr_row = min(i / (hd / 16), live - 1);
+            kr[u] = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(kr_row) * hd + (i % (hd / 16)) * 16);
+            const int vd = i / (kAttnBlock / 16), vc = min(i % (kAttnBlock / 16), (live - 1) / 16);
+            vr[u] = *reinterpret_cast<const uint4 *>(vg + (static_cast<int64_t>(vd) * (kAttnBlock / 16) + vc) * 16);
         }
         // the block's scales: thread j < 64 the K scale of position j, 64 <= j < 128 the V scale (0 past the
         // context, so that a weight 0 stays 0)
@@ -247,10 +256,12 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             if (u >= nl) break;
             const int i = threadIdx.x + u * 256;
             const int r = i / kpr, c = i % kpr;
-            // (rows past the context: inside the cache, their scores masked; values past it are zeroed below, as
-            // a weight 0 times a stale non-finite value would not be 0)
-            kr[u] = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(r) * hd + c * 8);
-            vr[u] = *reinterpret_cast<const uint4 *>(vg + static_cast<int64_t>(i) * 8);
+            // (rows past the context read the last live row again, from the cache: their scores are masked; values
+            // past it are zeroed below, as a weight 0 times a stale non-finite value would not be 0, and their
+            // 8-position pieces past the last live one read that one again)
+            kr[u] = *reinterpret_cast<const uint4 *>(kg + static_cast<int64_t>(min(r, live - 1)) * hd + c * 8);
+            const int vd = i / (kAttnBlock / 8), vc = min(i % (kAttnBlock / 8), (live - 1) / 8);
+            vr[u] = *reinterpret_cast<const uint4 *>(vg + (static_cast<int64_t>(vd) * (kAttnBlock / 8) + vc) * 8);
         }
         __builtin_amdgcn_sched_barrier(0);   // every load issued before the first store waits for one
 #pragma unroll
@@ -1548,7 +1559,7 @@ int launch_attn_t(Model &m, LayerW &L, hipStream_t st) {
     static int granted = 0;
     const size_t lds = attn_lds(NCH * 32);
     if (lds_grant(reinterpret_cast<const void *>(&attn_block_kernel<NCH, I8>), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL((attn_block_kernel<NCH, I8>), dim3(m.kv_blocks, c.n_kv_heads), dim3(256), lds, st, m.q16,
+    hipLaunchKernelGGL((attn_block_kernel<NCH, I8>), dim3(m.kv_blocks * c.n_kv_heads), dim3(256), lds, st, m.q16,
                        I8 ? static_cast<const void *>(L.kv8) : static_cast<const void *>(L.kv), L.kvs, m.slots,
                        c.n_heads, c.n_kv_heads, m.sp, m.parts, m.kv_blocks);
     return 0;
