@@ -84,6 +84,8 @@ SIGNATURES = {
                                   _P, _P]),
     "gv_accept_match": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
                                    _c.c_int, _P, _P, _P]),
+    "gv_accept_match_ex": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
+                                      _c.c_int, _P, _P, _c.c_int, _c.c_float, _P, _c.c_int, _P, _P]),
     "gv_accept_textbook": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
                                       _P, _P, _c.c_float, _P]),
 }
@@ -252,6 +254,25 @@ def accept_match(logits, batch, temperature, top_p=1.0, top_k=0, cap=1024, u=Non
                                 uu.ctypes.data_as(_P), out.ctypes.data_as(_P), _c.byref(kept))
     check(-1 if rc < 0 else 0, "gv_accept_match")
     return out[:rc].copy(), kept.value
+
+
+def accept_match_ex(logits, batch, temperature, top_p=1.0, top_k=0, cap=1024, u=None, seen=(), presence_penalty=0.0,
+                    stop=()):
+    """sample-and-match with the generate loop's presence penalty and stop tokens (engine/src/geode.cpp:236-255,
+    :331-350): (emitted tokens, kept rows, the rows' logits after the penalty)"""
+    buf, ptr, V = _dev_rows(logits)
+    n = logits.shape[0]
+    b = np.ascontiguousarray(batch, np.int32)
+    uu = np.ascontiguousarray(u if u is not None else np.zeros(n), np.float64)
+    sn = np.ascontiguousarray(np.asarray(seen, np.int32).reshape(-1))
+    st = np.ascontiguousarray(np.asarray(stop, np.int32).reshape(-1))
+    out = np.empty(n, np.int32)
+    kept = _c.c_int(0)
+    rc = _lib().gv_accept_match_ex(ptr, V, V, b.ctypes.data_as(_P), n, temperature, top_p, top_k, cap,
+                                   uu.ctypes.data_as(_P), sn.ctypes.data_as(_P), sn.size, presence_penalty,
+                                   st.ctypes.data_as(_P), st.size, out.ctypes.data_as(_P), _c.byref(kept))
+    check(-1 if rc < 0 else 0, "gv_accept_match_ex")
+    return out[:rc].copy(), kept.value, buf.download(np.float32, (n, V))
 
 
 def accept_textbook(target, draft, temperature, top_p, greedy, u_draft=None, u_acc=None, u_res=0.0):

@@ -22,6 +22,7 @@
 #include <climits>
 #include <vector>
 
+#include "../../include/geode_verify.h"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -295,14 +296,17 @@ __global__ __launch_bounds__(kSelThreads) void nucleus_kernel(const uint32_t *__
 }
 
 // sample-and-match over the sampled rows (geode.cpp:331-350): out = the stood drafts then the first sampled token
-// that is no draft; res = {emitted, kept}
+// that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}
 __global__ void match_kernel(const int32_t *__restrict__ pick, const int32_t *__restrict__ batch, int n,
-                             int32_t *__restrict__ out, int *__restrict__ res) {
+                             const int32_t *__restrict__ stop, int n_stop, int32_t *__restrict__ out,
+                             int *__restrict__ res) {
     if (threadIdx.x != 0) return;
     int emitted = 0, kept = 1;
     for (int i = 0; i < n; ++i) {
         out[emitted++] = pick[i];
-        if (i + 1 < n && pick[i] == batch[i + 1]) {
+        bool is_stop = false;
+        for (int j = 0; j < n_stop; ++j) is_stop |= stop[j] == pick[i];
+        if (i + 1 < n && pick[i] == batch[i + 1] && !is_stop) {
             ++kept;
             continue;
         }
@@ -310,6 +314,18 @@ __global__ void match_kernel(const int32_t *__restrict__ pick, const int32_t *__
     }
     res[0] = emitted;
     res[1] = kept;
+}
+
+// The presence penalty of the generate loop (geode.cpp:236-255) on the verified rows, in place: row i (a workgroup)
+// loses `penalty` at each of the answer's seen tokens (distinct) and at each draft batch[j], 1 <= j <= i, that is
+// new (fresh[j]: in neither `seen` nor an earlier draft), the tokens rows 0..i-1 sampled if their drafts stood (a
+// row after a fallen draft is never used). One subtraction a token, as the reference's once-each list.
+__global__ void penalty_kernel(float *__restrict__ logits, int64_t ld, const int32_t *__restrict__ seen, int n_seen,
+                               const int32_t *__restrict__ batch, const int32_t *__restrict__ fresh, float penalty) {
+    float *lg = logits + static_cast<int64_t>(blockIdx.x) * ld;
+    for (int j = threadIdx.x; j < n_seen; j += blockDim.x) lg[seen[j]] -= penalty;
+    for (int j = 1 + static_cast<int>(threadIdx.x); j <= static_cast<int>(blockIdx.x); j += blockDim.x)
+        if (fresh[j]) lg[batch[j]] -= penalty;
 }
 
 __global__ void first_kernel(const int32_t *__restrict__ idx, int64_t cs, int rows, int32_t *__restrict__ pick) {
@@ -574,20 +590,57 @@ int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float tempe
 
 int gv_accept_match(const float *logits, int64_t ld, int V, const int32_t *batch, int n, float temperature,
                     float top_p, int top_k, int cap, const double *u, int32_t *out, int *kept) {
+    // (no penalty: the rows are only read)
+    return gv_accept_match_ex(const_cast<float *>(logits), ld, V, batch, n, temperature, top_p, top_k, cap, u, nullptr,
+                              0, 0.0f, nullptr, 0, out, kept);
+}
+
+int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, int n, float temperature, float top_p,
+                       int top_k, int cap, const double *u, const int32_t *seen, int n_seen, float presence_penalty,
+                       const int32_t *stop, int n_stop, int32_t *out, int *kept) {
     if (ensure_init() != 0) return -1;
     GV_REQUIRE(logits && batch && out && n >= 1 && n <= 32 && V >= 1 && ld >= V, "gv_accept_match: bad arguments");
     GV_REQUIRE(temperature <= 0.0f || u, "gv_accept_match: uniforms needed when temperature > 0");
+    GV_REQUIRE(n_seen >= 0 && (n_seen == 0 || seen) && n_seen <= V, "gv_accept_match: seen tokens");
+    GV_REQUIRE(n_stop >= 0 && n_stop <= 1024 && (n_stop == 0 || stop), "gv_accept_match: at most 1024 stop tokens");
+    const bool penalize = presence_penalty != 0.0f;
+    // which drafts are new to the answer (one subtraction a token); seen must hold distinct tokens of the vocabulary
+    std::vector<int32_t> fresh(33, 0);
+    if (penalize) {
+        std::vector<uint8_t> in(static_cast<size_t>(V), 0);
+        for (int j = 0; j < n_seen; ++j) {
+            GV_REQUIRE(seen[j] >= 0 && seen[j] < V && !in[static_cast<size_t>(seen[j])],
+                       "gv_accept_match: seen tokens must be distinct tokens of the vocabulary");
+            in[static_cast<size_t>(seen[j])] = 1;
+        }
+        for (int j = 1; j < n; ++j) {
+            GV_REQUIRE(batch[j] >= 0 && batch[j] < V, "gv_accept_match: draft out of range");
+            if (!in[static_cast<size_t>(batch[j])]) fresh[static_cast<size_t>(j)] = 1, in[static_cast<size_t>(batch[j])] = 1;
+        }
+    }
     const size_t nb = nuclei_bytes(n, kMaxCand);
-    char *base = static_cast<char *>(ws().get(nb + 512));
+    const size_t extra = (64 + 33 + static_cast<size_t>(n_stop) + (penalize ? static_cast<size_t>(n_seen) : 0)) * 4 + 256;
+    char *base = static_cast<char *>(ws().get(nb + extra));
     GV_REQUIRE(base, "gv_accept_match: out of device memory");
     const Nuclei nu = carve(base, n, kMaxCand);
     int32_t *dbatch = reinterpret_cast<int32_t *>(base + nb);
     int32_t *dout = dbatch + 32;
     int *dres = reinterpret_cast<int *>(dout + 32);
+    int32_t *dfresh = reinterpret_cast<int32_t *>(dres + 4);
+    int32_t *dstop = dfresh + 33;
+    int32_t *dseen = dstop + n_stop;
     const hipStream_t st = stream();
-    if (nuclei(logits, ld, n, V, temperature, top_p, top_k, cap, u, nu, st) != 0) return -1;
     GV_CHECK_HIP(hipMemcpyAsync(dbatch, batch, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, st));
-    hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, nu.pick, dbatch, n, dout, dres);
+    if (n_stop) GV_CHECK_HIP(hipMemcpyAsync(dstop, stop, static_cast<size_t>(n_stop) * 4, hipMemcpyHostToDevice, st));
+    if (penalize) {
+        GV_CHECK_HIP(hipMemcpyAsync(dfresh, fresh.data(), 33 * 4, hipMemcpyHostToDevice, st));
+        if (n_seen) GV_CHECK_HIP(hipMemcpyAsync(dseen, seen, static_cast<size_t>(n_seen) * 4, hipMemcpyHostToDevice, st));
+        hipLaunchKernelGGL(penalty_kernel, dim3(n), dim3(256), 0, st, logits, ld, dseen, n_seen, dbatch, dfresh,
+                           presence_penalty);
+        GV_CHECK_HIP(hipGetLastError());
+    }
+    if (nuclei(logits, ld, n, V, temperature, top_p, top_k, cap, u, nu, st) != 0) return -1;
+    hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, nu.pick, dbatch, n, dstop, n_stop, dout, dres);
     GV_CHECK_HIP(hipGetLastError());
     int res[2] = {0, 0};
     GV_CHECK_HIP(hipMemcpyAsync(res, dres, 8, hipMemcpyDeviceToHost, st));

@@ -226,6 +226,14 @@ int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float tempe
  * is no draft; returns their count (or -1), *kept = the rows that stay (verify_keep's argument). n <= 32. */
 int gv_accept_match(const float *logits, int64_t ld, int V, const int32_t *batch, int n, float temperature,
                     float top_p, int top_k, int cap, const double *u, int32_t *out, int *kept);
+/* gv_accept_match with the generate loop's presence penalty and stop tokens (engine/src/geode.cpp:236-255, :331-350):
+ * seen[0..n_seen) are the answer's tokens so far (distinct); before row i is sampled, presence_penalty is subtracted
+ * (in place, as the reference's loop does) from its logits at every seen token and at each draft batch[1..i] new to
+ * the answer (the tokens rows 0..i-1 sampled when their drafts stood); a draft stands only if the row before samples
+ * exactly it and it is none of stop[0..n_stop). The caller adds the emitted tokens to its seen list. */
+int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, int n, float temperature, float top_p,
+                       int top_k, int cap, const double *u, const int32_t *seen, int n_seen, float presence_penalty,
+                       const int32_t *stop, int n_stop, int32_t *out, int *kept);
 /* The textbook rule (Leviathan et al. 2023, Alg. 1; no reference counterpart: the reference accepts by
  * sample-and-match). p_i, q_i = the full-vocabulary top-p nucleus of target row i / draft row i at temperature T.
  * Draft i: greedy: argmax q_i, accepted iff argmax p_i equals it; else d_i ~ q_i by u_draft[i], accepted iff

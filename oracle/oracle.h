@@ -137,6 +137,12 @@ void orc_sample_seeded(const float *logits, int n, float temperature, float top_
 // Sample-and-match over a verified chain (geode.cpp:318-374): batch = [tok, d1..d_{n-1}]; each row sampled with
 // its uniform u[i]; a draft stands while row i samples exactly it. out: the tokens emitted (stood drafts, then the
 // first sampled token that is no draft). Returns how many; *kept = the rows that stay (verify_keep's argument).
+// The same with the generate loop's presence penalty and stop tokens (geode.cpp:236-255, :331-350): seen (the answer's
+// tokens so far) lose presence_penalty in each row's logits (modified in place) before it is sampled, every sampled
+// token joining seen; a draft stands only if it is no stop token either.
+int orc_accept_match_ex(float *logits, int V, const int32_t *batch, int n, float temperature, float top_p, int top_k,
+                        int cap, const double *u, const int32_t *seen, int n_seen, float presence_penalty,
+                        const int32_t *stop, int n_stop, int32_t *out, int *kept);
 int orc_accept_match(const float *logits, int V, const int32_t *batch, int n, float temperature, float top_p,
                      int top_k, int cap, const double *u, int32_t *out, int *kept);
 // The textbook rule (Leviathan et al. 2023, Alg. 1). Not in the reference (which is sample-and-match above).

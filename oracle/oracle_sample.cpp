@@ -114,6 +114,47 @@ void orc_sample_seeded(const float *logits, int n, float temperature, float top_
     }
 }
 
+// geode.cpp:236-255 and :331-350 as written: `seen` holds the answer's distinct tokens so far (in order), each row's
+// logits lose presence_penalty at every seen token before it is sampled, a sampled token joins `seen` once, and a draft
+// stands while the row before samples exactly it and it is no stop token. logits are modified in place (as there).
+int orc_accept_match_ex(float *logits, int V, const int32_t *batch, int n, float temperature, float top_p, int top_k,
+                        int cap, const double *u, const int32_t *seen_in, int n_seen, float presence_penalty,
+                        const int32_t *stop, int n_stop, int32_t *out, int *kept) {
+    std::vector<int32_t> seen;
+    std::vector<uint8_t> is_seen(presence_penalty != 0.0f ? static_cast<size_t>(V) : 0, 0);
+    if (!is_seen.empty())
+        for (int j = 0; j < n_seen; ++j) {
+            const int32_t t = seen_in[j];
+            if (t >= 0 && t < V && !is_seen[static_cast<size_t>(t)]) {
+                is_seen[static_cast<size_t>(t)] = 1;
+                seen.push_back(t);
+            }
+        }
+    auto is_stop = [&](int32_t t) {
+        for (int j = 0; j < n_stop; ++j)
+            if (stop[j] == t) return true;
+        return false;
+    };
+    int emitted = 0, k = 1;
+    for (int i = 0; i < n; ++i) {
+        float *lg = logits + static_cast<size_t>(i) * V;
+        for (int32_t t : seen) lg[static_cast<size_t>(t)] -= presence_penalty;
+        const int y = sample(lg, V, temperature, top_p, top_k, cap, u[i]);
+        if (!is_seen.empty() && y >= 0 && y < V && !is_seen[static_cast<size_t>(y)]) {
+            is_seen[static_cast<size_t>(y)] = 1;
+            seen.push_back(y);
+        }
+        out[emitted++] = y;
+        if (i + 1 < n && y == batch[i + 1] && !is_stop(y)) {   // the draft stands (geode.cpp:333)
+            ++k;
+            continue;
+        }
+        break;
+    }
+    if (kept) *kept = k;
+    return emitted;
+}
+
 int orc_accept_match(const float *logits, int V, const int32_t *batch, int n, float temperature, float top_p,
                      int top_k, int cap, const double *u, int32_t *out, int *kept) {
     int emitted = 0, k = 1;

@@ -85,6 +85,8 @@ def _load():
         "orc_sample_seeded": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_uint64, _c.c_int, _P]),
         "orc_accept_match": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _P,
                                         _P, _P]),
+        "orc_accept_match_ex": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
+                                           _P, _P, _c.c_int, _c.c_float, _P, _c.c_int, _P, _P]),
         "orc_accept_textbook": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _P, _P,
                                            _c.c_float, _P]),
         "orc_nucleus_probs": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _P]),
@@ -292,6 +294,22 @@ def accept_match(logits, batch, temperature, top_p, top_k=0, cap=1024, u=None):
     cnt = lib.orc_accept_match(_ptr(logits), V, _ptr(np.ascontiguousarray(batch, np.int32)), n, temperature, top_p,
                                top_k, cap, _ptr(u), _ptr(out), _c.byref(kept))
     return out[:cnt], kept.value
+
+
+def accept_match_ex(logits, batch, temperature, top_p, top_k=0, cap=1024, u=None, seen=(), presence_penalty=0.0,
+                    stop=()):
+    """sample-and-match with the presence penalty and stop tokens: (emitted tokens, kept rows, the penalized logits)"""
+    lg = np.array(logits, np.float32, copy=True, order="C")
+    n, V = lg.shape
+    u = np.ascontiguousarray(u if u is not None else np.full(n, 0.5), np.float64)
+    sn = np.ascontiguousarray(np.asarray(seen, np.int32).reshape(-1))
+    st = np.ascontiguousarray(np.asarray(stop, np.int32).reshape(-1))
+    out = np.empty(n, np.int32)
+    kept = _c.c_int(0)
+    cnt = lib.orc_accept_match_ex(_ptr(lg), V, _ptr(np.ascontiguousarray(batch, np.int32)), n, temperature, top_p,
+                                  top_k, cap, _ptr(u), _ptr(sn), sn.size, presence_penalty, _ptr(st), st.size,
+                                  _ptr(out), _c.byref(kept))
+    return out[:cnt], kept.value, lg
 
 
 class Model:

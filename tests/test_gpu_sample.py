@@ -127,3 +127,30 @@ def test_textbook_rule_greedy(gv):
     want = po.accept_textbook(target, draft, 0.7, 0.95, True, ud, ua, ur)
     assert list(got) == list(want)
     assert len(got) >= 3
+
+
+@pytest.mark.parametrize("temp", [0.0, 0.7])
+def test_sample_and_match_presence_penalty_and_stops(gv, temp):
+    """the generate loop's presence penalty (geode.cpp:236-255) and stop tokens (:333) against the oracle: the same
+    emitted tokens, kept rows and penalized logits; drafts built so that penalties change the samples"""
+    x = _rows(91, 5, 1.0)
+    u = _uniforms(91, 5)
+    rng = np.random.default_rng(92)
+    for trial in range(12):
+        seen = rng.choice(V, size=int(rng.integers(0, 400)), replace=False).astype(np.int32)
+        pen = float(rng.choice([0.5, 1.5, 4.0]))
+        # drafts: what the oracle's penalized rows sample (so that they stand), one of them replaced on odd trials
+        _, _, lg0 = po.accept_match_ex(x, [1, 2, 3, 4, 5], temp, 0.95, 0, 1024, u, seen, pen)
+        batch = [11]
+        for i in range(4):   # the row i sample with row i's penalty set (seen + the drafts before)
+            out_i, _, _ = po.accept_match_ex(x[i:i + 1], [0], temp, 0.95, 0, 1024, u[i:i + 1],
+                                             np.unique(np.concatenate([seen, batch[1:]])).astype(np.int32), pen)
+            batch.append(int(out_i[0]))
+        if trial % 2:
+            batch[1 + trial % 4] = (batch[1 + trial % 4] + 1) % V
+        stop = [batch[3]] if trial % 3 == 0 else []
+        want, wk, wlg = po.accept_match_ex(x, batch, temp, 0.95, 0, 1024, u, seen, pen, stop)
+        got, gk, glg = gv.accept_match_ex(x, batch, temp, 0.95, 0, 1024, u, seen, pen, stop)
+        assert list(got) == list(want) and gk == wk, (trial, list(got), list(want))
+        for r in range(wk):   # the rows that were sampled carry the same penalized logits
+            assert np.array_equal(glg[r].view(np.uint32), wlg[r].view(np.uint32))

@@ -135,3 +135,57 @@ def test_textbook_rule_chi_square_and_greedy():
     draft_g[1] = np.roll(target[1], 1)
     out = po.accept_textbook(target, draft_g, 0.7, 0.95, True, [0] * k, [0] * k, 0)
     assert list(out) == [int(np.argmax(target[0])), int(np.argmax(target[1]))]
+
+
+# ---------------------------------------------------------------- the presence penalty and stop tokens
+def test_accept_match_ex_without_penalty_or_stops_is_accept_match():
+    rng = np.random.default_rng(71)
+    x = (rng.standard_normal((5, 500)) * 2).astype(np.float32)
+    u = rng.random(5)
+    for t in (0.0, 0.8):
+        for trial in range(6):
+            batch = np.concatenate([[3], rng.integers(0, 500, 4)]).astype(np.int32)
+            if trial % 2:   # drafts the rows sample: some stand
+                batch[1:] = [po.sample(x[i], t, 0.95, 0, 1024, u[i]) for i in range(4)]
+            a, ka = po.accept_match(x, batch, t, 0.95, 0, 1024, u)
+            b, kb, lg = po.accept_match_ex(x, batch, t, 0.95, 0, 1024, u)
+            assert list(a) == list(b) and ka == kb
+            assert np.array_equal(lg, x)   # no penalty: the rows untouched
+
+
+def test_presence_penalty_closed_form_greedy():
+    """geode.cpp:247-255: every seen token loses the penalty once before the row is sampled; a draft that stood joins
+    the seen tokens of the rows after it"""
+    V = 16
+    x = np.zeros((3, V), np.float32)
+    x[:, 5] = 3.0   # the favourite of every row
+    x[:, 9] = 2.5
+    x[:, 2] = 2.0
+    # nothing seen: rows 0.. sample 5; with 5 seen (penalty 1: 5 -> 2.0 < 2.5), row 0 samples 9
+    out, kept, lg = po.accept_match_ex(x, [1, 9, 2], 0.0, 1.0, seen=[5], presence_penalty=1.0)
+    # row 0: argmax of (5: 2.0, 9: 2.5, 2: 2.0) = 9 = draft 1, stands; row 1: 5 and 9 seen: (2.0, 1.5, 2.0): the first
+    # argmax is token 2 = draft 2, stands; row 2: the last row, sampled: 5, 9, 2 all seen -> (2.0, 1.5, 1.0) -> 5
+    assert list(out) == [9, 2, 5] and kept == 3
+    assert lg[0, 5] == 2.0 and lg[0, 9] == 2.5                     # row 0: only the seen token
+    assert lg[1, 5] == 2.0 and lg[1, 9] == 1.5 and lg[1, 2] == 2.0   # row 1: + the stood draft 9
+    assert lg[2, 2] == 1.0                                          # row 2: + the stood draft 2
+    # a token that is both seen and a stood draft again loses the penalty once: row 0 samples 5 (5: 3.0 > 9: 2.25),
+    # the draft 5 stands; rows 1 and 2 lose 0.25 at 9 and at 5, once each
+    out, kept, lg = po.accept_match_ex(x, [1, 5, 5], 0.0, 1.0, seen=[9], presence_penalty=0.25)
+    assert list(out) == [5, 5, 5] and kept == 3
+    assert lg[1, 5] == np.float32(2.75) and lg[1, 9] == np.float32(2.25)
+    assert lg[2, 5] == np.float32(2.75) and lg[2, 9] == np.float32(2.25)
+
+
+def test_stop_token_draft_does_not_stand():
+    """geode.cpp:333: a draft equal to the sampled token stands only if it is no stop token; the stop token is then
+    the token emitted (and the answer ends there)"""
+    V = 8
+    x = np.zeros((3, V), np.float32)
+    x[0, 4] = x[1, 6] = x[2, 1] = 5.0
+    out, kept, _ = po.accept_match_ex(x, [0, 4, 6], 0.0, 1.0)
+    assert list(out) == [4, 6, 1] and kept == 3
+    out, kept, _ = po.accept_match_ex(x, [0, 4, 6], 0.0, 1.0, stop=[6])
+    assert list(out) == [4, 6] and kept == 2
+    out, kept, _ = po.accept_match_ex(x, [0, 4, 6], 0.0, 1.0, stop=[4, 7])
+    assert list(out) == [4] and kept == 1
