@@ -27,6 +27,12 @@ class GvModelConfig(_c.Structure):
                 ("kv_int8", _c.c_int32)]
 
 
+class GvStateInfo(_c.Structure):
+    _fields_ = [("pack_print", _c.c_uint64), ("conv_id", _c.c_uint64), ("extra", _c.c_int32),
+                ("rope_delta", _c.c_int32), ("has_mtp", _c.c_int32), ("has_vision", _c.c_int32), ("hidden", _P),
+                ("has_hidden", _c.c_int32)]
+
+
 # tensor kinds of gv_model_adopt
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, QKV, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, \
     SHARED_EXPERT, KV, KV_I8 = 0, 1, 2, 3, 4, 5, 8, 9, 10, 11, 12, 13, 14, 17, 18
@@ -80,6 +86,8 @@ SIGNATURES = {
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_model_layer": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
+    "gv_model_save_state": (_c.c_int, [_P, _c.c_char_p, _c.c_int, _c.POINTER(GvStateInfo)]),
+    "gv_model_load_state": (_c.c_int, [_P, _c.c_char_p, _c.POINTER(GvStateInfo)]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
                                   _P, _P]),
     "gv_accept_match": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
@@ -97,6 +105,19 @@ KERNEL_CLASSES = ["embed", "quantize", "qkv", "rope_kv", "attention", "attn_merg
 
 class GeodeError(RuntimeError):
     pass
+
+
+# the error classes of gv_model_save_state / gv_model_load_state (GEODE_E_IO, _FORMAT, _ARG, _MEMORY of the
+# reference's geode_state_save / geode_state_load)
+STATE_ERRORS = {-1: "io", -2: "format", -3: "arg", -4: "memory"}
+
+
+class StateError(GeodeError):
+    """a refused save or load; .kind is one of STATE_ERRORS' values"""
+
+    def __init__(self, kind, msg):
+        super().__init__(msg)
+        self.kind = kind
 
 
 def _load():
@@ -407,6 +428,29 @@ class VerifyModel:
                                     par.ctypes.data_as(_P) if par is not None else None, mid.ctypes.data_as(_P),
                                     out.ctypes.data_as(_P), ids.ctypes.data_as(_P)), "gv_model_layer")
         return mid, out, ids
+
+    def save_state(self, path, append=False, *, pack_print=0, conv_id=0, extra=0, rope_delta=0, has_mtp=False,
+                   has_vision=False, hidden=None):
+        """Model::save_state (engine/src/state.cpp:251-371): the conversation to path in the reference's state format;
+        append: in place when path holds an earlier state of the same conversation. hidden: [hidden] float32 or None
+        (the last hidden state an MTP layer drafts from, kept when has_mtp)."""
+        hid = np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
+        info = GvStateInfo(pack_print, conv_id, extra, rope_delta, int(has_mtp), int(has_vision),
+                           hid.ctypes.data_as(_P) if hid is not None else None, 0)
+        rc = _lib().gv_model_save_state(self.h, os.fsencode(path), 1 if append else 0, _c.byref(info))
+        if rc != 0:
+            raise StateError(STATE_ERRORS.get(rc, "io"), _lib().gv_last_error().decode())
+
+    def load_state(self, path, *, pack_print=0, has_mtp=False, has_vision=False):
+        """Model::load_state (engine/src/state.cpp:373-463): the saved conversation replaces this one; returns
+        {conv_id, extra, rope_delta, hidden (or None)}. On failure StateError and the position is 0."""
+        hid = np.zeros(self.cfg["hidden"], np.float32)
+        info = GvStateInfo(pack_print, 0, 0, 0, int(has_mtp), int(has_vision), hid.ctypes.data_as(_P), 0)
+        rc = _lib().gv_model_load_state(self.h, os.fsencode(path), _c.byref(info))
+        if rc != 0:
+            raise StateError(STATE_ERRORS.get(rc, "io"), _lib().gv_last_error().decode())
+        return {"conv_id": info.conv_id, "extra": info.extra, "rope_delta": info.rope_delta,
+                "hidden": hid if info.has_hidden else None}
 
     def moe_replay(self, reps=20):
         """mean ms of the last moe() block re-run on its device-staged inputs (device work only)"""

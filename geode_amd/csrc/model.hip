@@ -1867,6 +1867,8 @@ struct gv_model {
     std::vector<uint8_t *> staging;   // device staging, freed at the end of the call that made it
 };
 
+Model &gv::model_of(gv_model *g) { return g->m; }
+
 namespace {
 void put_err(char *err, int err_len, const std::string &msg) {
     if (err && err_len > 0) {

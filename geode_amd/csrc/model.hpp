@@ -140,4 +140,7 @@ struct Model {
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
 constexpr int kFlagsPerLayer = 1024;   // flag words a layer's fused launches have (one a producer workgroup)
 
+// the model behind a C-ABI handle (model.hip), for the entry points of other files
+Model &model_of(gv_model *g);
+
 }  // namespace gv

@@ -211,6 +211,36 @@ int gv_model_layer(gv_model *m, int layer, const float *x_in, int n, const int32
  * the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */
 int gv_model_moe_replay(gv_model *m, int reps, float *ms_per_block);
 
+/* ------------------------------------------------------------------ a conversation's state in a file (F4)
+ * The reference's state file (engine/src/state.cpp:1-20): a 4096-byte header with an FNV-1a checksum, the fixed part
+ * (gen at both ends), the KV cache in blocks of 256 positions [K, V][layer][256][n_kv_heads * hd] (fp16 or int8, then
+ * the int8 cache's float scales [K, V][layer][256][n_kv_heads]). A state saved by the reference's CPU or GPU path
+ * loads here and the other way round, for a model of the same pack and KV format; this model is attention-only
+ * (no Gated DeltaNet states) and takes no images. */
+typedef struct gv_state_info {
+    uint64_t pack_print; /* FNV-1a 64 of the pack's geode.json bytes (Model::fingerprint, engine/src/state.cpp:227-245;
+                            0: none, taken as 1); a load refuses a file of another pack */
+    uint64_t conv_id;    /* the conversation (save: written, an append goes only to a file of the same one; load: read) */
+    int32_t extra;       /* the caller's value kept with the state (geode.cpp: the token passed on, not computed yet) */
+    int32_t rope_delta;
+    int32_t has_mtp;     /* the fingerprint's flags (state.cpp:240-242): the model that exchanges the state has an MTP */
+    int32_t has_vision;  /* layer / a vision encoder */
+    float *hidden;       /* host [hidden] or NULL: the last hidden state an MTP layer drafts from (save: written when
+                            has_mtp and the position > 0; load: filled when the file holds one) */
+    int32_t has_hidden;  /* load: 1 when the file held a hidden state and `hidden` received it */
+} gv_state_info;
+/* error classes of the two calls (geode_state_save / geode_state_load's GEODE_E_*, engine/src/geode.cpp:490-518) */
+enum { GV_STATE_E_IO = -1, GV_STATE_E_FORMAT = -2, GV_STATE_E_ARG = -3, GV_STATE_E_MEMORY = -4 };
+/* Model::save_state (engine/src/state.cpp:251-371): the conversation (the model's position and its KV rows) to path.
+ * append: path holds an earlier state of the same conversation (fingerprint and conv_id): the fixed part and the
+ * blocks from the one holding its last position are written in place, the header last; anything else is written
+ * whole to path.tmp and renamed over path. Between verify steps only. */
+int gv_model_save_state(gv_model *m, const char *path, int append, const gv_state_info *info);
+/* Model::load_state (engine/src/state.cpp:373-463): the saved conversation replaces the model's (the position becomes
+ * the saved one, nothing to keep); conv_id, extra, rope_delta and has_hidden come back in *info, which also names
+ * the pack and flags to check the fingerprint against. On failure the position is 0. */
+int gv_model_load_state(gv_model *m, const char *path, gv_state_info *info);
+
 /* ------------------------------------------------------------------ sampling and acceptance (C2)
  * Rows of logits in device memory (ld floats apart, e.g. gv_model_logits'), uniforms and results on the host.
  * The double sums of the sampler run as parallel scans and expf is the device's: a sampled index can differ from

@@ -123,8 +123,24 @@ int orc_model_verify_trace(orc_model *m, const int32_t *tokens, int n, const int
 // verify_keep: kept rows stay (chain: rows 0..kept-1; tree: path[0..kept) of row indices, their KV moved to the
 // kept slots); the position becomes the one before the verify plus kept.
 int orc_model_keep(orc_model *m, int kept, const int32_t *path);
+const orc_config *orc_model_config(const orc_model *m);
 // seconds of the last verify spent in the layers and in the final norm + lm_head
 void orc_model_last_times(const orc_model *m, double *t_layers, double *t_head);
+
+// ---- a conversation's state in the reference's file format (state.cpp, Model::save_state / load_state) ----
+typedef struct {
+    uint64_t pack_print;       // the pack's print folded into the fingerprint (0: taken as 1)
+    uint64_t conv_id;
+    int32_t extra, rope_delta;
+    int32_t has_mtp, has_vision;   // the fingerprint's flags
+    float *hidden;             // [hidden] or NULL: the last hidden state (written when has_mtp and the position > 0)
+    int32_t has_hidden;        // load: the file held one and `hidden` received it
+} orc_state_info;
+uint64_t orc_fnv1a(const void *data, size_t n, uint64_t seed);   // state.cpp:71-75 (seed 1469598103934665603)
+// Model::save_state (state.cpp:251-371) of the oracle model's position and KV cache; 0 or -1 with err
+int orc_state_save(orc_model *m, const char *path, int append, const orc_state_info *info, char *err, int err_len);
+// Model::load_state (state.cpp:373-463): the position becomes the saved one (0 on failure)
+int orc_state_load(orc_model *m, const char *path, orc_state_info *info, char *err, int err_len);
 
 // ---- sampling and acceptance ----
 // Sampler::sample (sampler.cpp:16-50) with the uniform injected: u in [0, 1) stands for

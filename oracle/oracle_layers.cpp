@@ -517,6 +517,8 @@ uint8_t *orc_model_tensor(orc_model *m, int kind, int layer, int expert, int64_t
 void orc_model_set_position(orc_model *m, int pos) { m->pos = pos; }
 int orc_model_position(const orc_model *m) { return m->pos; }
 
+const orc_config *orc_model_config(const orc_model *m) { return &m->c; }
+
 int orc_model_verify(orc_model *m, const int32_t *tokens, int n, const int32_t *parents, int mode, float *logits,
                      int32_t *route_ids) {
     return orc_model_verify_trace(m, tokens, n, parents, mode, logits, route_ids, nullptr);

@@ -42,6 +42,12 @@ EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, Q, K, V, O, Q_NORM, K_NORM, ROUT
     SH_UP, SH_DOWN, KV, KV8, KVS = range(20)
 
 
+class StateInfo(_c.Structure):
+    _fields_ = [("pack_print", _c.c_uint64), ("conv_id", _c.c_uint64), ("extra", _c.c_int32),
+                ("rope_delta", _c.c_int32), ("has_mtp", _c.c_int32), ("has_vision", _c.c_int32), ("hidden", _P),
+                ("has_hidden", _c.c_int32)]
+
+
 def _load():
     if not os.path.exists(LIB_PATH):
         raise RuntimeError("oracle/liboracle.so is not built (run __graft_entry__.build())")
@@ -90,6 +96,10 @@ def _load():
         "orc_accept_textbook": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _P, _P,
                                            _c.c_float, _P]),
         "orc_nucleus_probs": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _P]),
+        "orc_fnv1a": (_c.c_uint64, [_P, _c.c_size_t, _c.c_uint64]),
+        "orc_model_config": (_P, [_P]),
+        "orc_state_save": (_c.c_int, [_P, _c.c_char_p, _c.c_int, _c.POINTER(StateInfo), _c.c_char_p, _c.c_int]),
+        "orc_state_load": (_c.c_int, [_P, _c.c_char_p, _c.POINTER(StateInfo), _c.c_char_p, _c.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -376,6 +386,25 @@ class Model:
         p = np.ascontiguousarray(path, np.int32) if path is not None else None
         if lib.orc_model_keep(self.h, kept, _ptr(p)) != 0:
             raise ValueError("orc_model_keep failed")
+
+    def save_state(self, path, append=False, *, pack_print=0, conv_id=0, extra=0, rope_delta=0, has_mtp=False,
+                   has_vision=False, hidden=None):
+        """orc_state_save: Model::save_state (state.cpp:251-371) of this model's position and KV cache"""
+        hid = np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
+        info = StateInfo(pack_print, conv_id, extra, rope_delta, int(has_mtp), int(has_vision), _ptr(hid), 0)
+        err = _c.create_string_buffer(512)
+        if lib.orc_state_save(self.h, os.fsencode(path), int(append), _c.byref(info), err, 512) != 0:
+            raise OSError(err.value.decode())
+
+    def load_state(self, path, *, pack_print=0, has_mtp=False, has_vision=False):
+        """orc_state_load: Model::load_state (state.cpp:373-463); ValueError with the reference's message on refusal"""
+        hid = np.zeros(self.cfg["hidden"], np.float32)
+        info = StateInfo(pack_print, 0, 0, 0, int(has_mtp), int(has_vision), _ptr(hid), 0)
+        err = _c.create_string_buffer(512)
+        if lib.orc_state_load(self.h, os.fsencode(path), _c.byref(info), err, 512) != 0:
+            raise ValueError(err.value.decode())
+        return {"conv_id": info.conv_id, "extra": info.extra, "rope_delta": info.rope_delta,
+                "hidden": hid if info.has_hidden else None}
 
     def last_times(self):
         a, b = _c.c_double(0), _c.c_double(0)

@@ -1,0 +1,165 @@
+"""The GPU model's conversation state (gv_model_save_state / gv_model_load_state) against the oracle's and the
+format's restatement in tests/state_format.py: a save of the same cache is the same file byte for byte (fp16 and
+int8), a state saved by either side loads into the other and the next verify continues bit for bit (GPU -> GPU) or
+within the verify tolerance (GPU -> oracle), an append equals a whole save but for its generation, another block size
+loads, and damaged files are refused with the reference's error classes and an empty conversation."""
+import struct
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+import state_format as sf
+from model_helpers import SMALL, SMALL_ROUTER_SIGMA, adopt_oracle_model, rel_err
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(SMALL, max_ctx=640)
+CTX = 600
+META = dict(pack_print=0xFEED_5EED, conv_id=123, extra=-1, rope_delta=0, has_mtp=True)
+
+
+@pytest.fixture(scope="module")
+def gv():
+    import geode_amd
+
+    geode_amd.init(0)
+    return geode_amd
+
+
+@pytest.fixture(scope="module", params=[0, 1], ids=["fp16", "int8"])
+def pair(gv, request):
+    """(oracle model, GPU model holding the oracle's first CTX positions, the config)"""
+    cfg = dict(CFG, kv_int8=request.param)
+    om = po.Model(cfg, seed=11, router_sigma=SMALL_ROUTER_SIGMA, ctx=CTX)
+    gm = gv.VerifyModel(cfg)
+    adopt_oracle_model(gm, om, CTX)
+    return om, gm, cfg
+
+
+def _fresh(gv, om, cfg):
+    """a GPU model with the oracle's weights and an empty cache"""
+    gm = gv.VerifyModel(cfg)
+    adopt_oracle_model(gm, om, 0)
+    return gm
+
+
+@pytest.mark.parametrize("pos", [1, 255, 256, 257, 600])
+def test_save_equals_the_oracles(pair, tmp_path, pos):
+    om, gm, _ = pair
+    hidden = po.normal(3, CFG["hidden"])
+    om.position = pos
+    gm.position = pos
+    om.save_state(str(tmp_path / "o.geode"), hidden=hidden, **META)
+    gm.save_state(str(tmp_path / "g.geode"), hidden=hidden, **META)
+    want = open(tmp_path / "o.geode", "rb").read()
+    got = open(tmp_path / "g.geode", "rb").read()
+    assert len(got) == len(want)
+    assert got == want
+
+
+def test_oracle_state_loads_and_continues(gv, pair, tmp_path):
+    om, gm, cfg = pair
+    om.position = 555
+    om.save_state(str(tmp_path / "o.geode"), **META)
+    g2 = _fresh(gv, om, cfg)
+    info = g2.load_state(str(tmp_path / "o.geode"), pack_print=META["pack_print"], has_mtp=True)
+    assert (info["conv_id"], info["extra"], g2.position) == (123, -1, 555)
+    gm.position = 555
+    toks = np.array([5, 9, 300, 2, 77], np.int32)
+    np.testing.assert_array_equal(g2.verify(toks), gm.verify(toks))
+
+
+def test_state_after_gpu_steps_round_trips(gv, pair, tmp_path):
+    """KV rows the GPU's own steps appended (across the 256-position block edge) survive a save and a load: the next
+    verify is bit-identical on the GPU and within the verify tolerance on the oracle"""
+    om, _, cfg = pair
+    gm = gv.VerifyModel(cfg)   # its own model: the steps overwrite cache rows the other tests compare
+    adopt_oracle_model(gm, om, 250)
+    rng = np.random.default_rng(4)
+    for _ in range(3):
+        gm.verify(rng.integers(0, cfg["vocab"], 5).astype(np.int32))
+        gm.keep(4)
+    assert gm.position == 262
+    path = str(tmp_path / "g.geode")
+    gm.save_state(path, **META)
+    g2 = _fresh(gv, om, cfg)
+    g2.load_state(path, pack_print=META["pack_print"], has_mtp=True)
+    toks = np.array([1, 2, 3], np.int32)
+    want = gm.verify(toks)
+    np.testing.assert_array_equal(g2.verify(toks), want)
+    o2 = po.Model(cfg, seed=11, router_sigma=SMALL_ROUTER_SIGMA, ctx=0)
+    o2.load_state(path, pack_print=META["pack_print"], has_mtp=True)
+    assert o2.position == 262
+    err = rel_err(want, o2.verify(toks))
+    assert err <= 1e-2, f"logits max error {err:.3e}"
+
+
+def _with_gen(buf, gen):
+    """a whole save's bytes as an append of generation gen writes them"""
+    b = bytearray(buf)
+    h = sf.read_header(b)
+    lo = sf.layout(h)
+    h["gen"] = gen
+    b[:sf.HEADER.size] = sf.pack_header(h)[0]
+    struct.pack_into("<Q", b, h["fixed_offset"], gen)
+    struct.pack_into("<Q", b, lo["trail"], gen)
+    return bytes(b)
+
+
+def test_append_equals_a_whole_save(pair, tmp_path):
+    om, gm, _ = pair
+    path = str(tmp_path / "a.geode")
+    gm.position = 300
+    gm.save_state(path, **META)
+    gm.position = 590
+    gm.save_state(path, append=True, **META)
+    gm.save_state(str(tmp_path / "w.geode"), **META)
+    assert open(path, "rb").read() == _with_gen(open(tmp_path / "w.geode", "rb").read(), 2)
+
+
+def test_another_block_size_loads(gv, pair, tmp_path):
+    om, gm, cfg = pair
+    kv_row = cfg["n_kv_heads"] * cfg["head_dim"]
+    rows, scales = [], None
+    for l in range(cfg["n_layers"]):
+        if cfg["kv_int8"]:
+            rows.append(om.tensor(po.KV8, l)[0].view(np.int8).reshape(2, cfg["max_ctx"], kv_row))
+        else:
+            rows.append(om.tensor(po.KV, l)[0].view(np.uint16).reshape(2, cfg["max_ctx"], kv_row))
+    if cfg["kv_int8"]:
+        scales = [om.tensor(po.KVS, l)[0].view(np.float32).reshape(2, cfg["max_ctx"], cfg["n_kv_heads"])
+                  for l in range(cfg["n_layers"])]
+    path = str(tmp_path / "b.geode")
+    open(path, "wb").write(sf.state_bytes(cfg, rows, scales, 333, block=128, conv_id=8))
+    g2 = _fresh(gv, om, cfg)
+    assert g2.load_state(path)["conv_id"] == 8 and g2.position == 333
+    gm.position = 333
+    toks = np.array([40, 41], np.int32)
+    np.testing.assert_array_equal(g2.verify(toks), gm.verify(toks))
+
+
+@pytest.mark.parametrize("what,kind", [("checksum", "format"), ("interrupted", "io"), ("cut", "io"),
+                                       ("pack", "format"), ("longer", "arg")])
+def test_damaged_files_are_refused(gv, pair, tmp_path, what, kind):
+    om, gm, cfg = pair
+    path = str(tmp_path / "d.geode")
+    gm.position = 300
+    gm.save_state(path, **META)
+    buf = bytearray(open(path, "rb").read())
+    h = sf.read_header(buf)
+    if what == "checksum":
+        buf[40] ^= 1
+    elif what == "interrupted":
+        struct.pack_into("<Q", buf, h["fixed_offset"], h["gen"] + 1)
+    elif what == "cut":
+        buf = buf[:-1]
+    open(path, "wb").write(bytes(buf))
+    g2 = gv.VerifyModel(dict(cfg, max_ctx=300)) if what == "longer" else _fresh(gv, om, cfg)
+    if what == "longer":
+        adopt_oracle_model(g2, om, 0)
+    g2.position = 5
+    with pytest.raises(gv.StateError) as e:
+        g2.load_state(path, pack_print=META["pack_print"] + (what == "pack"), has_mtp=True)
+    assert e.value.kind == kind
+    assert g2.position == 0
