@@ -4,8 +4,11 @@ Workload (the metric's config): the full 40-layer 35B-
 attention (16 query heads, 2 KV heads, head_dim 256, RoPE theta 1e7) plus the MoE (256 experts, top-8 softmax
 routing, 1 shared expert, ff 512), vocab 151,936, q4 weights seeded on the device (N(0, 0.02) through the RTN
 packer), an fp16 KV cache of 8,192 context positions N(0, 1). A step verifies k = 4 chained drafts plus the last
-token (M = 5 rows): every layer, the final norm and lm_head, logits left on the device. The drafts are the target
-model's own greedy continuation, so a greedy sample-and-match accepts all of them (5 tokens emitted a step).
+token (M = 5 rows): every layer, the final norm and lm_head, logits left on the device, then the GPU's greedy
+sample-and-match of the drafts on those logits (gv_accept_match, its result copied to the host) — a timed step is
+both. The drafts are the target model's own greedy continuation, so all of them stand (5 tokens emitted a step):
+`value` (tok/s) is the ceiling of acceptance; `verify_steps_per_s` (the verify alone) is the headline figure
+independent of it. The draft tree (M = 17) is timed in the same run (`tree_m17`).
 
     python bench.py [--steps K] [--warmup W] [--tree] [--kv-int8] [--no-cpu]
     python bench.py --config c2|c3|c5      (the acceptance rules; one MoE block at M = 5 or 512)
@@ -84,9 +87,10 @@ def step_bytes(c, M, uniq_per_layer, ctx):
 
 
 def cpu_baseline(M, threads, kv_int8=False):
-    """The oracle (the reference's CPU arithmetic restated, int8 path) on the host cores: a bounded sample of the
-    same workload, 1 of the 40 layers plus the final norm and lm_head at full shapes (timing-only random q4
-    bytes); the step time is extrapolated as t_head + 40 x t_layer."""
+    """The oracle (the reference's CPU arithmetic restated, int8 path; g++ -O3 -march=x86-64-v3, rows split over
+    `threads` in chunks of 16 as ThreadPool::parallel_for) on the host cores: a bounded sample of the same workload,
+    1 of the 40 layers plus the final norm and lm_head at full shapes (timing-only random q4 bytes); the step time
+    is extrapolated as t_head + 40 x t_layer."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as po
 
@@ -98,7 +102,7 @@ def cpu_baseline(M, threads, kv_int8=False):
     best = None
     t_start = time.time()
     reps = 0
-    while reps < 2 or (time.time() - t_start < 10 and reps < 5):
+    while reps < 2 or (time.time() - t_start < 8 and reps < 4):
         om.position = CTX
         om.verify(toks)
         tl, th = om.last_times()
@@ -114,9 +118,10 @@ def cpu_baseline(M, threads, kv_int8=False):
 def bench_moe_block(g, M, reps):
     """C3 (M = 5) / C5 (M = 512): one MoE block at the configs' shapes (256 experts + the shared one, hidden 2048,
     ff 512), rows fp16-valued N(0, 1), routed logits N(0, 1) given; device time of the block re-run on its staged
-    inputs (gv_model_moe_replay)"""
+    inputs (gv_model_moe_replay), each run on the next of 3 layers of distinct weights: 3 x 257 expert blocks =
+    1.36 GB, more than the 256 MB Infinity Cache holds, so that every run reads its experts from HBM"""
     cfg = dict(C4)
-    cfg["n_layers"] = 1
+    cfg["n_layers"] = 3
     m = g.VerifyModel(cfg)
     m.randomize(SEED, 0.02, 0.0221, 0)
     rng = np.random.default_rng(SEED + M)
@@ -267,14 +272,36 @@ def main():
         m.position = CTX
         m.verify(toks, parents, want_logits=False)
 
-    for _ in range(args.warmup):
+    import ctypes as ct
+    acc_out, kept, u0 = np.empty(M, np.int32), ct.c_int(0), np.zeros(M)
+
+    def step_accept():
+        """the verify, then the GPU's greedy sample-and-match of the chain on its device logits (geode.cpp:318-374)"""
         step()
+        n = g.lib.gv_accept_match(g.lib.gv_model_logits(m.h), C["vocab"], C["vocab"], toks.ctypes.data_as(ct.c_void_p),
+                                  M, 0.0, 1.0, 0, 1024, u0.ctypes.data_as(ct.c_void_p),
+                                  acc_out.ctypes.data_as(ct.c_void_p), ct.byref(kept))
+        g.check(-1 if n < 0 else 0, "gv_accept_match")
+        return n
+
+    timed = step if args.tree else step_accept   # the tree's acceptance is a walk on the host, not timed
+    for _ in range(args.warmup):
+        timed()
     g.check(g.lib.gv_synchronize())
+    t0 = time.perf_counter()
+    e0 = g.lib.gv_event_record()
+    for _ in range(args.steps):
+        timed()
+    e1 = g.lib.gv_event_record()
+    g.check(g.lib.gv_synchronize())
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_events = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+    # the verify alone (graph replays back to back, no host wait between them)
     e0 = g.lib.gv_event_record()
     for _ in range(args.steps):
         step()
     e1 = g.lib.gv_event_record()
-    ms = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+    ms_verify = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
     # the same steps as plain launches (no graph), for comparison
     m.set_graphs(False)
     e0 = g.lib.gv_event_record()
@@ -284,17 +311,20 @@ def main():
     ms_direct = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
     m.set_graphs(True)
 
-    # acceptance of the last step's logits: greedy sample-and-match (engine/src/geode.cpp:331-350)
+    # acceptance of the last step's logits: the GPU's own count for the chain (checked against the host's greedy
+    # walk), a greedy walk on the host for the tree
     m.position = CTX
     logits = m.verify(toks, parents)
     route = m.route_ids(M)
     uniq = [len(np.unique(route[l])) for l in range(C["n_layers"])]
     if not args.tree:
-        emitted = 1
+        emitted = step_accept()
+        host = 1
         for i in range(M - 1):
             if int(np.argmax(logits[i])) != int(toks[i + 1]):
                 break
-            emitted += 1
+            host += 1
+        assert host == emitted, f"GPU acceptance emitted {emitted} tokens, the host's greedy walk {host}"
     else:
         emitted = 1
         node = 0
@@ -328,7 +358,32 @@ def main():
     achieved = dom_bytes / dom_avg_s
 
     steps_s = 1e3 / ms
+    verify_steps_s = 1e3 / ms_verify
     sbytes = step_bytes(C, M, uniq, CTX)
+    tree = None
+    if not args.tree:   # the draft tree of configs[3] on the same model: 16 nodes (4, 3) + the root, M = 17
+        tp = tree_parents()
+        ttoks = np.array([(7 + 1000 * i) % C["vocab"] for i in range(17)], np.int32)
+
+        def tstep():
+            m.position = CTX
+            m.verify(ttoks, tp, want_logits=False)
+
+        for _ in range(3):
+            tstep()
+        e0 = g.lib.gv_event_record()
+        for _ in range(args.steps):
+            tstep()
+        e1 = g.lib.gv_event_record()
+        tms = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+        m.position = CTX
+        m.verify(ttoks, tp, want_logits=False)
+        troute = m.route_ids(17)
+        tuniq = [len(np.unique(troute[l])) for l in range(C["n_layers"])]
+        tbytes = step_bytes(C, 17, tuniq, CTX)
+        tree = {"rows": 17, "ms_per_step": tms, "verify_steps_per_s": 1e3 / tms, "verified_rows_per_s": 17e3 / tms,
+                "step_bytes": tbytes, "step_roofline_frac": tbytes / (tms / 1e3) / PEAK_HBM,
+                "distinct_experts_per_layer": float(np.mean(tuniq))}
     out = {
         "metric": "verify-step tok/s, 35B-A3B-shape MoE k=4; HBM GB/s vs peak",
         "value": steps_s * emitted,
@@ -347,11 +402,13 @@ def main():
                                 f", ctx {CTX}, vocab 151936, q4 weights, {'int8' if args.kv_int8 else 'fp16'} KV, int8-path products"),
                    "rows": M, "tokens_emitted_per_step": emitted, "acceptance": "greedy sample-and-match on the "
                    "step's logits; drafts = the target's own greedy chain" if not args.tree else "greedy tree walk"},
-        "verify_steps_per_s": steps_s,
-        "ms_per_step_without_graphs": ms_direct,
-        "verified_rows_per_s": steps_s * M,
-        "step_hbm_gbs": sbytes / (ms / 1e3) / 1e9,
-        "step_roofline_frac": sbytes / (ms / 1e3) / PEAK_HBM,
+        "verify_steps_per_s": verify_steps_s,
+        "ms_per_verify": ms_verify,
+        "ms_per_step_device_events": ms_events,
+        "ms_per_verify_without_graphs": ms_direct,
+        "verified_rows_per_s": verify_steps_s * M,
+        "step_hbm_gbs": sbytes / (ms_verify / 1e3) / 1e9,
+        "step_roofline_frac": sbytes / (ms_verify / 1e3) / PEAK_HBM,
         "step_bytes": sbytes,
         "distinct_experts_per_layer": float(np.mean(uniq)),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
@@ -362,9 +419,14 @@ def main():
         "kernel_ms_per_step": {k: round(v[0], 4) for k, v in per_class.items() if v[1]},
         "init_s": t_init,
     }
+    if tree:
+        out["tree_m17"] = tree
     if not args.no_cpu:
+        # the box's CPU share for one GPU is 16 threads (whatever os.cpu_count() shows there), and one core
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(M, threads, args.kv_int8)
+        one = cpu_baseline(M, 1, args.kv_int8)
+        out["cpu_baseline"]["one_core"] = {"value": one["value"], "unit": one["unit"], "sample": one["sample"]}
     print(json.dumps(out))
 
 

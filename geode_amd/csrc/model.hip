@@ -2539,7 +2539,8 @@ int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
     GV_CHECK_HIP(hipEventCreate(&e1));
     GV_CHECK_HIP(hipEventRecord(e0, st));
     int rc = 0;
-    for (int i = 0; i < reps && rc == 0; ++i) rc = moe_block(m, m.pf.layer, m.pf.M, m.pf.given, st);
+    for (int i = 0; i < reps && rc == 0; ++i)   // launch i on layer (layer + i) mod n_layers: other weights each time
+        rc = moe_block(m, (m.pf.layer + i) % m.c.n_layers, m.pf.M, m.pf.given, st);
     GV_CHECK_HIP(hipEventRecord(e1, st));
     GV_CHECK_HIP(hipEventSynchronize(e1));
     float ms = 0.0f;

@@ -207,8 +207,9 @@ int gv_model_moe(gv_model *m, int layer, const float *h, int M, const float *rou
  * to keep. A checking aid: the layers of a step compared one at a time, each fed the same input. */
 int gv_model_layer(gv_model *m, int layer, const float *x_in, int n, const int32_t *parents, float *x_mid,
                    float *x_out, int32_t *ids);
-/* Re-run the last gv_model_moe call's block on its device-staged rows and logits reps times back to back and return
- * the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */
+/* Re-run the last gv_model_moe call's block on its device-staged rows and logits reps times back to back, run i on
+ * layer (layer + i) mod n_layers (so that a model of several layers rotates through distinct expert weights), and
+ * return the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */
 int gv_model_moe_replay(gv_model *m, int reps, float *ms_per_block);
 
 /* ------------------------------------------------------------------ a conversation's state in a file (F4)
