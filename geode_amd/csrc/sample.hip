@@ -1,4 +1,4 @@
-// sample.hip - the sampler and the two acceptance rules on the GPU.
+// sample.hip - the sampler and the two acceptance rules on the GPU (C2).
 //
 //   Sampler::sample       sampler.cpp:16-50        T <= 0: the first argmax. Else the candidates (top_k, else the
 //                                                   top `cap` = 1024, ties to the lower index) by logit descending,
@@ -12,14 +12,24 @@
 //                                                   max(0, p - q) by inverse CDF in index order; a bonus from p_k
 //                                                   when every draft stands.
 //
-// Per row, topk_kernel selects the K candidates with a three-pass radix select on order-preserving 32-bit keys
-// (11 + 11 + 10 bits, LDS histograms), collects them (ties at the threshold to the lower index) and sorts them with
-// a bitonic sort in LDS; nucleus_kernel computes e, the top-p prefix, the kept mass and the draw; the acceptance
-// kernels walk the rows. The double sums run as parallel scans: they differ from the reference's sequential sums in
-// the last bits (~1e-16 relative), which moves a decision only when a uniform or top_p falls that close to a
-// boundary; expf is the device's (within 1 ulp of glibc's).
+// The sorted order of a row (logit descending, index ascending) is walked without sorting the row: a walk finds the
+// element where the running weight of that order first reaches a target, by three histogram levels of an
+// order-preserving 32-bit key (bits 31..21, 20..10, 9..0), each level a pass of S workgroups a row over the
+// elements under the bits fixed so far. The last level leaves a key tau, the ties of it taken (in index order) and
+// the weight of the elements before them; the pass that builds the last level's histogram also lists the few
+// elements under its 22-bit prefix, from which the element itself and tie ranks are read. The weight is 1 a
+// candidate for the top-K candidates, and e = exp((l - max) / T) for the full-vocabulary nucleus (its top-p prefix,
+// then the draw within it): no candidate limit there. Each pass decides the previous level itself from that
+// level's histogram (its loads in flight with the row's), so a level costs one launch.
+//
+// The top-K candidates (at most 16,384) are collected by the count walk's last pass and sorted in LDS by one
+// workgroup a row, which then runs the reference's nucleus arithmetic on them as written. The histogram weights are
+// summed by double atomics and the other double sums as parallel reductions: they differ from the reference's
+// sequential sums in the last bits (~1e-15 relative), which moves a decision only when a uniform or top_p falls that
+// close to a boundary; expf is the device's (within 1 ulp of glibc's).
 #include <algorithm>
 #include <climits>
+#include <cmath>
 #include <vector>
 
 #include "../../include/geode_verify.h"
@@ -29,9 +39,18 @@
 namespace gv {
 namespace {
 
-constexpr int kSelThreads = 1024;
-constexpr int kMaxCand = 16384;   // candidates a row can keep (the full-vocabulary nucleus must fit)
-constexpr int kRowBatch = 8;      // a row's values a thread loads at once in the full-row passes
+constexpr int kPass = 256;        // threads of a row-pass workgroup
+constexpr int kLoads = 16;        // values a thread holds in a pass
+constexpr int kChunk = kPass * kLoads;   // values a row-pass workgroup takes at most
+constexpr int kMaxChunks = 64;    // workgroups a row at most (a vocabulary up to 262,144)
+constexpr int kBins = 2048;       // bins of a histogram level (the last level uses 1024)
+constexpr int kSortThreads = 1024;
+constexpr int kMaxCand = 16384;   // top-K candidates a row can keep (the full-vocabulary nucleus has no limit)
+constexpr int kList = 1024;       // elements a walk lists under its last level's prefix
+constexpr int kSampleRows = 64;   // rows gv_sample_rows takes at most
+
+__host__ __device__ constexpr int level_shift(int l) { return l == 0 ? 21 : l == 1 ? 10 : 0; }
+__host__ __device__ constexpr int level_bins(int l) { return l == 2 ? 1024 : 2048; }
 
 // float -> a key whose unsigned order is the float order (-0 taken as +0: equal floats, equal keys)
 __device__ inline uint32_t fkey(float f) {
@@ -40,6 +59,9 @@ __device__ inline uint32_t fkey(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 __device__ inline float key_val(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k); }
+
+// e = exp((l - max) / T) as the reference computes it (float), sampler.cpp:31
+__device__ inline float e_of(float l, float mx, float T) { return expf(__fdiv_rn(__fsub_rn(l, mx), T)); }
 
 template <typename T>
 __device__ inline T wave_incl_scan(T v) {
@@ -75,118 +97,555 @@ __device__ inline T block_sum(T v, T *tmp) {
     return tot;
 }
 
-// The K largest of a row (K <= KP, KP a power of two), by value descending, ties to the lower index: keys to okey,
-// indices to oidx. full_sum: also the sum over the whole row of exp((l - max) / T) in double (the full-vocabulary
-// nucleus's denominator) to osum.
-template <int KP>
-__global__ __launch_bounds__(kSelThreads) void topk_kernel(const float *__restrict__ x, int64_t ldx, int V, int K,
-                                                            float T, int full_sum, uint32_t *__restrict__ okey,
-                                                            int32_t *__restrict__ oidx, int64_t ostride,
-                                                            double *__restrict__ osum) {
-    extern __shared__ uint64_t comp[];   // [KP] (key << 32) | (~index): descending = value desc, index asc
-    __shared__ uint32_t hist[2048];
-    __shared__ uint32_t tmp_u[16];
-    __shared__ double tmp_d[16];
-    __shared__ uint32_t s_prefix, s_mask, s_above, s_need, s_maxkey, s_cnt, s_bin, s_add, s_bincnt;
-    const float *row = x + static_cast<int64_t>(blockIdx.x) * ldx;
-    const int tid = threadIdx.x, nthr = blockDim.x;
+// ---------------------------------------------------------------- the state of a row
+struct LevelHist {   // a row's histogram of one level: element counts and weights per bin
+    uint32_t cnt[kBins];
+    double w[kBins];
+};
+enum { H_L1 = 0, H_L2P = 1, H_L3P = 2, H_L2D = 3, H_L3D = 4, kHists = 5 };
+
+// A walk down the sorted order to the element where the running weight first reaches a target.
+struct Walk {
+    uint32_t prefix, mask;   // the key bits fixed so far
+    double t;                // the weight still to reach among the elements under prefix (inf: to the last one)
+    double above;            // the weight of the elements before them
+    uint32_t above_cnt;      // their count
+    uint32_t tau, n, c;      // at the end: the key reached, its ties taken (in index order), its ties there are
+    double w_tau;            // a tie's weight
+};
+
+struct RowInfo {
+    float mx;          // the row's largest logit
+    int32_t pick;      // the sampled (or first largest) index
+    double sum;        // the nucleus's denominator: the whole row's e (full vocabulary) or the candidates'
+    double kept;       // e of the kept prefix
+    uint32_t keep;     // its length
+    uint32_t unused;
+    // the walks' states, a slot a pass (a pass reads the previous pass's slot while its own workgroup 0 writes the
+    // next): the top-p (top-K) walk after levels 0 and 1 and at its end, the draw's after levels 0 and 1 (its last
+    // level is decided where the pick is read)
+    Walk wk[5];
+    __device__ const Walk &p() const { return wk[2]; }
+};
+enum { W_P0 = 0, W_P1 = 1, W_P = 2, W_D0 = 3, W_D1 = 4 };
+enum { L_P = 0, L_D = 1 };          // the two walks' lists
+enum { N_CAND = 0, N_LIST = 1 };    // a row's counters: candidates collected, elements listed (P, then D)
+
+struct Rows {   // rows [0, R1) of x1, then rows of x2, ld floats apart; a row in S chunks of C values
+    const float *x1, *x2;
+    int64_t ld;
+    int R1, V, S, C;
+    __device__ const float *row(int r) const {
+        return r < R1 ? x1 + static_cast<int64_t>(r) * ld : x2 + static_cast<int64_t>(r - R1) * ld;
+    }
+};
+
+struct Ws {   // device arrays of R rows
+    RowInfo *info;        // [R]
+    uint32_t *pmax;       // [R][kMaxChunks] a chunk's largest key
+    int32_t *pidx;        //                 the lowest index holding it
+    double *psum;         //                 a chunk's e sum
+    LevelHist *h;         // [R][kHists]
+    uint32_t *cnt;        // [R][4] counters (N_*), zeroed by the first pass
+    uint64_t *cand;       // [R][kMaxCand] (key << 32) | ~index
+    uint64_t *lst;        // [R][2][kList] (key << 32) | index
+    int32_t *picks;       // [R] the rows' picks
+    double *u;            // [R] the uniforms
+};
+
+// ---------------------------------------------------------------- loads
+__device__ inline void preload(const float *row, int c0, int c1, float (&v)[kLoads]) {
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) v[u] = row[min(c0 + u * kPass + static_cast<int>(threadIdx.x), c1 - 1)];
+}
+
+// ---------------------------------------------------------------- a walk's steps (every thread of a workgroup)
+struct WalkLds {
+    double tmp_d[16];
+    uint32_t tmp_u[16];
+    uint32_t first, lastp1;
+};
+
+// Level `level` of the walk `in` from its histogram: the first nonempty bin (from the top) where the running weight
+// reaches in.t, else (rounding left the target past the end) the last nonempty bin, whose elements are then all
+// taken. The next state goes to `out` (LDS). Workgroups of 256 or 1024 threads.
+__device__ void walk_level(const LevelHist &h, int level, const Walk in, Walk &out, WalkLds &L) {
+    const int nb = level_bins(level), sh = level_shift(level), per = nb / static_cast<int>(blockDim.x);
+    const int tid = threadIdx.x;
+    double w[8];
+    uint32_t c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int b = nb - 1 - (tid * per + j);
+        c[j] = j < per ? h.cnt[b] : 0u;
+        w[j] = j < per ? h.w[b] : 0.0;
+    }
+    double lw = 0.0;
+    uint32_t lc = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        lw += w[j];
+        lc += c[j];
+    }
     if (tid == 0) {
-        s_prefix = 0;
-        s_mask = 0;
-        s_above = 0;
-        s_need = static_cast<uint32_t>(K);
-        s_maxkey = 0;
-        s_cnt = 0;
+        L.first = UINT_MAX;
+        L.lastp1 = 0;
+    }
+    double wtot;
+    const double wex = block_excl_scan(lw, L.tmp_d, wtot);   // (its barriers publish the resets above)
+    uint32_t ctot;
+    const uint32_t cex = block_excl_scan(lc, L.tmp_u, ctot);
+    double acc = wex;
+    uint32_t first = UINT_MAX, lastp1 = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (j < per && c[j]) {
+            if (first == UINT_MAX && acc + w[j] >= in.t) first = static_cast<uint32_t>(tid * per + j);
+            lastp1 = static_cast<uint32_t>(tid * per + j + 1);
+        }
+        acc += w[j];
+    }
+    if (first != UINT_MAX) atomicMin(&L.first, first);
+    if (lastp1) atomicMax(&L.lastp1, lastp1);
+    __syncthreads();
+    const bool reached = L.first != UINT_MAX;
+    const uint32_t rank = reached ? L.first : L.lastp1 - 1;   // (a walk's elements are never none)
+    if (tid == static_cast<int>(rank / per)) {
+        const int j0 = static_cast<int>(rank % per);
+        double above = wex;
+        uint32_t cabove = cex, cj = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j < j0) {
+                above += w[j];
+                cabove += c[j];
+            }
+            if (j == j0) cj = c[j];
+        }
+        const uint32_t bin = static_cast<uint32_t>(nb - 1) - rank;
+        Walk s = in;
+        s.above += above;
+        s.above_cnt += cabove;
+        s.t = reached ? in.t - above : INFINITY;
+        s.prefix |= bin << sh;
+        s.mask |= static_cast<uint32_t>(nb - 1) << sh;
+        if (level == 2) {
+            s.tau = s.prefix;
+            s.c = cj;
+        }
+        out = s;
     }
     __syncthreads();
-    constexpr int kShift[3] = {21, 10, 0}, kWidth[3] = {11, 11, 10};
-    uint32_t cnt_eq = 0;
+}
+
+// after the last level (one thread): a tie's weight and the ties taken through the target
+__device__ void walk_finish(Walk &s, bool mass, float mx, float T) {
+    s.w_tau = mass ? static_cast<double>(e_of(key_val(s.tau), mx, T)) : 1.0;
+    uint32_t n = s.c;
+    if (!isinf(s.t)) {
+        const double q = ceil(s.t / s.w_tau);
+        n = q < 1.0 ? 1u : (q >= static_cast<double>(s.c) ? s.c : static_cast<uint32_t>(q));
+        while (n < s.c && static_cast<double>(n) * s.w_tau < s.t) ++n;   // (the division's rounding)
+    }
+    s.n = n;
+}
+
+// ---------------------------------------------------------------- row passes: grid (S, R), kPass threads
+// (a chunk is at most kChunk values: thread t holds the values c0 + t + 256 u, u < kLoads)
+struct PassOut {
+    LevelHist *g;
+    double *chunk_e;     // every element's e summed (the mass walk's first level), or null
+    uint64_t *list;      // the last level: the elements under the prefix listed, or null
+    uint32_t *nlist;
+    uint64_t *cand;      // the count walk's last level: the elements above the prefix collected, or null
+    uint32_t *ncand;
+};
+
+struct PassLds {
+    uint32_t lc[kBins];
+    double lw[kBins];
+    uint32_t tmp_u[16];
+    double tmp_d[16];
+    uint32_t base_l, base_c;
+};
+
+// A chunk's elements under the walk's prefix into level `level`'s histogram (LDS, then the row's by atomics);
+// mass: weights e, else 1. The listed and collected elements get their slots in one reservation a workgroup.
+template <bool MASS>
+__device__ void hist_chunk(int c0, int c1, const float (&v)[kLoads], uint32_t prefix, uint32_t mask, int level,
+                           float mx, float T, PassLds &S, const PassOut &o) {
+    const int tid = threadIdx.x, nb = level_bins(level), sh = level_shift(level);
+    for (int b = tid; b < nb; b += kPass) {
+        S.lc[b] = 0;
+        S.lw[b] = 0.0;
+    }
+    __syncthreads();
+    double acc = 0.0;
+    uint32_t nl = 0, nc = 0;
 #pragma unroll
-    for (int p = 0; p < 3; ++p) {
-        const int sh = kShift[p], nb = 1 << kWidth[p];
-        for (int i = tid; i < nb; i += nthr) hist[i] = 0;
-        __syncthreads();
-        const uint32_t prefix = s_prefix, mask = s_mask, need = s_need;
-        uint32_t mk = 0;
-        for (int i0 = tid; i0 < V; i0 += kRowBatch * nthr) {   // kRowBatch loads in flight a thread
-            float v[kRowBatch];
-#pragma unroll
-            for (int u = 0; u < kRowBatch; ++u) v[u] = row[min(i0 + u * nthr, V - 1)];
-#pragma unroll
-            for (int u = 0; u < kRowBatch; ++u) {   // (no branch before the uses: no load sinks into one)
-                const bool in = i0 + u * nthr < V;
-                const uint32_t k = fkey(v[u]);
-                if (p == 0) mk = max(mk, in ? k : 0u);
-                if (in && (k & mask) == prefix) atomicAdd(&hist[(k >> sh) & (nb - 1)], 1u);
-            }
+    for (int u = 0; u < kLoads; ++u) {
+        if (c0 + u * kPass + tid >= c1) continue;
+        const uint32_t k = fkey(v[u]);
+        const bool under = (k & mask) == prefix;
+        if (MASS && (o.chunk_e || under)) {
+            const float e = e_of(v[u], mx, T);
+            acc += static_cast<double>(e);
+            if (under) atomicAdd(&S.lw[(k >> sh) & (nb - 1)], static_cast<double>(e));
         }
-        if (p == 0) atomicMax(&s_maxkey, mk);
-        __syncthreads();
-        // from the top bin down: the bin where the count reaches need (thread t: bins nb-1-2t, nb-2-2t)
-        const int r0 = 2 * tid, r1 = 2 * tid + 1;
-        const uint32_t c0 = r1 < nb ? hist[nb - 1 - r0] : 0u, c1 = r1 < nb ? hist[nb - 1 - r1] : 0u;
-        uint32_t tot;
-        const uint32_t ex = block_excl_scan(c0 + c1, tmp_u, tot);
-        if (r1 < nb) {
-            if (ex < need && ex + c0 >= need) {
-                s_bin = static_cast<uint32_t>(nb - 1 - r0);
-                s_add = ex;
-                s_bincnt = c0;
-            } else if (ex + c0 < need && ex + c0 + c1 >= need) {
-                s_bin = static_cast<uint32_t>(nb - 1 - r1);
-                s_add = ex + c0;
-                s_bincnt = c1;
-            }
-        }
-        __syncthreads();
+        if (under) atomicAdd(&S.lc[(k >> sh) & (nb - 1)], 1u);
+        nl += under;
+        nc += (k & mask) > prefix;
+    }
+    if (o.chunk_e) *o.chunk_e = acc;
+    if (o.list || o.cand) {
+        uint32_t tl, tc;
+        uint32_t al = block_excl_scan(o.list ? nl : 0u, S.tmp_u, tl);
+        uint32_t ac = block_excl_scan(o.cand ? nc : 0u, S.tmp_u, tc);
         if (tid == 0) {
-            s_prefix = prefix | (s_bin << sh);
-            s_mask = mask | (static_cast<uint32_t>(nb - 1) << sh);
-            s_above += s_add;
-            s_need = need - s_add;
+            S.base_l = tl ? atomicAdd(o.nlist, tl) : 0u;
+            S.base_c = tc ? atomicAdd(o.ncand, tc) : 0u;
         }
-        cnt_eq = s_bincnt;
         __syncthreads();
-    }
-    const uint32_t tau = s_prefix, above = s_above, need_eq = s_need;
-    const bool all_eq = cnt_eq == need_eq;
-    const float mx = key_val(s_maxkey);
-    double esum = 0.0;
-    for (int i0 = tid; i0 < V; i0 += kRowBatch * nthr) {
-        float v[kRowBatch];
+        al += S.base_l;
+        ac += S.base_c;
 #pragma unroll
-        for (int u = 0; u < kRowBatch; ++u) v[u] = row[min(i0 + u * nthr, V - 1)];
-#pragma unroll
-        for (int u = 0; u < kRowBatch; ++u) {
-            const int i = i0 + u * nthr;
-            const bool in = i < V;
-            const float f = v[u];
-            const uint32_t k = fkey(f);
-            if (full_sum) esum += in ? static_cast<double>(expf(__fdiv_rn(__fsub_rn(f, mx), T))) : 0.0;
-            if (in && (k > tau || (all_eq && k == tau))) {
-                const uint32_t slot = atomicAdd(&s_cnt, 1u);
-                if (slot < static_cast<uint32_t>(K))
-                    comp[slot] = (static_cast<uint64_t>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+        for (int u = 0; u < kLoads; ++u) {
+            const int i = c0 + u * kPass + tid;
+            if (i >= c1) continue;
+            const uint32_t k = fkey(v[u]);
+            if (o.list && (k & mask) == prefix) {
+                if (al < static_cast<uint32_t>(kList)) o.list[al] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(i);
+                ++al;
+            }
+            if (o.cand && (k & mask) > prefix) {
+                if (ac < static_cast<uint32_t>(kMaxCand))
+                    o.cand[ac] = (static_cast<uint64_t>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+                ++ac;
             }
         }
     }
-    if (!all_eq) {   // ties at the threshold beyond what is needed: the lowest indices, in index order
+    __syncthreads();
+    for (int b = tid; b < nb; b += kPass)
+        if (S.lc[b]) {
+            atomicAdd(&o.g->cnt[b], S.lc[b]);
+            atomicAdd(&o.g->w[b], MASS ? S.lw[b] : static_cast<double>(S.lc[b]));
+        }
+}
+
+// pass 0: a chunk's largest key and the lowest index holding it; the row's histograms and counters zeroed for the
+// passes after it (a share each workgroup)
+__global__ __launch_bounds__(kPass) void max_pass(Rows rs, Ws ws) {
+    __shared__ uint64_t red[kPass / 64];
+    const int w = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const float *row = rs.row(r);
+    const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
+    float v[kLoads];
+    preload(row, c0, c1, v);
+    {
+        uint32_t *h = reinterpret_cast<uint32_t *>(ws.h + r * kHists);
+        constexpr int words = static_cast<int>(sizeof(LevelHist) * kHists / 4);
+        for (int i = w * kPass + tid; i < words; i += rs.S * kPass) h[i] = 0u;
+        if (w == 0 && tid < 4) ws.cnt[r * 4 + tid] = 0u;
+    }
+    uint64_t best = 0;   // (key << 32) | ~index: the largest is the largest key at the lowest index
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+        const int i = c0 + u * kPass + tid;
+        if (i < c1) best = max(best, (static_cast<uint64_t>(fkey(v[u])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i)));
+    }
+    for (int o = 32; o > 0; o >>= 1) best = max(best, static_cast<uint64_t>(__shfl_xor(best, o, 64)));
+    if ((tid & 63) == 0) red[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < kPass / 64; ++i) best = max(best, red[i]);
+        ws.pmax[r * kMaxChunks + w] = static_cast<uint32_t>(best >> 32);
+        ws.pidx[r * kMaxChunks + w] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+    }
+}
+
+// the first argmax of each row from its chunks' (a wave a row, a lane a chunk)
+__global__ __launch_bounds__(64) void argmax_reduce(Ws ws, int S) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    uint64_t best = 0;
+    if (lane < S)
+        best = (static_cast<uint64_t>(ws.pmax[r * kMaxChunks + lane]) << 32) |
+               (0xFFFFFFFFu - static_cast<uint32_t>(ws.pidx[r * kMaxChunks + lane]));
+    for (int o = 32; o > 0; o >>= 1) best = max(best, static_cast<uint64_t>(__shfl_xor(best, o, 64)));
+    if (lane == 0) {
+        const int32_t pick = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+        ws.info[r].pick = pick;
+        ws.info[r].mx = key_val(static_cast<uint32_t>(best >> 32));
+        ws.picks[r] = pick;
+    }
+}
+
+// pass 1: the first level's histogram; mass: with the row's max and each chunk's e sum
+template <bool MASS>
+__global__ __launch_bounds__(kPass) void level1_pass(Rows rs, Ws ws, float T) {
+    __shared__ PassLds S;
+    const int w = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const float *row = rs.row(r);
+    const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
+    float v[kLoads];
+    preload(row, c0, c1, v);
+    float mx = 0.0f;
+    if (MASS) {   // the row's largest logit from its chunks'
+        uint32_t mk = ws.pmax[r * kMaxChunks];
+        for (int i = 1; i < rs.S; ++i) mk = max(mk, ws.pmax[r * kMaxChunks + i]);
+        mx = key_val(mk);
+        if (w == 0 && tid == 0) ws.info[r].mx = mx;
+    }
+    double part = 0.0;
+    const PassOut o{ws.h + r * kHists + H_L1, MASS ? &part : nullptr, nullptr, nullptr, nullptr, nullptr};
+    hist_chunk<MASS>(c0, c1, v, 0u, 0u, 0, mx, T, S, o);
+    if (MASS) {
+        const double s = block_sum(part, S.tmp_d);
+        if (tid == 0) ws.psum[r * kMaxChunks + w] = s;
+    }
+}
+
+enum Stage {
+    ST_P1 = 0,   // start the top-p (top-K) walk: level 0 from the first histogram; level 1's histogram
+    ST_P2 = 1,   // level 1; level 2's histogram, the elements under the prefix listed (and the top-K's above it)
+    ST_D1 = 2,   // finish the top-p walk (the kept prefix), start the draw: level 0; level 1's histogram
+    ST_D2 = 3    // level 1 of the draw; level 2's histogram, the elements under the prefix listed
+};
+
+// passes 2..5 of the walks (mass: the nucleus and the draw; count: the top-K walk, stages P1 and P2 only)
+template <bool MASS, int STAGE>
+__global__ __launch_bounds__(kPass) void walk_pass(Rows rs, Ws ws, float T, float top_p, int K) {
+    __shared__ PassLds S;
+    __shared__ Walk s, s2;
+    __shared__ WalkLds L;
+    const int w = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    RowInfo &info = ws.info[r];
+    LevelHist *h = ws.h + r * kHists;
+    const float *row = rs.row(r);
+    const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
+    float v[kLoads];
+    preload(row, c0, c1, v);   // (in flight while the previous level is decided)
+    const float mx = MASS ? info.mx : 0.0f;
+    int level = 1, out = H_L2P;
+    if (STAGE == ST_P1) {
+        double target = static_cast<double>(K);
+        if (MASS) {
+            double tot = 0.0;   // the row's e sum, chunks in order
+            for (int i = 0; i < rs.S; ++i) tot += ws.psum[r * kMaxChunks + i];
+            target = top_p < 1.0f ? static_cast<double>(top_p) * tot : INFINITY;
+            if (w == 0 && tid == 0) info.sum = tot;
+        }
+        walk_level(h[H_L1], 0, Walk{0u, 0u, target, 0.0, 0u, 0u, 0u, 0u, 0.0}, s, L);
+    } else if (STAGE == ST_P2) {
+        walk_level(h[H_L2P], 1, info.wk[W_P0], s, L);
+        level = 2;
+        out = H_L3P;
+    } else if (STAGE == ST_D1) {
+        walk_level(h[H_L3P], 2, info.wk[W_P1], s2, L);
+        if (tid == 0) {
+            walk_finish(s2, true, mx, T);
+            const double kept = s2.above + static_cast<double>(s2.n) * s2.w_tau;
+            if (w == 0) {
+                info.wk[W_P] = s2;
+                info.keep = s2.above_cnt + s2.n;
+                info.kept = kept;
+            }
+            s2 = Walk{0u, 0u, kept * ws.u[r], 0.0, 0u, 0u, 0u, 0u, 0.0};
+        }
         __syncthreads();
-        const int ch = (V + nthr - 1) / nthr, b0 = tid * ch, b1 = min(V, b0 + ch);
-        uint32_t c = 0;
-        for (int i = b0; i < b1; ++i) c += fkey(row[i]) == tau;
+        walk_level(h[H_L1], 0, s2, s, L);
+        out = H_L2D;
+    } else {
+        walk_level(h[H_L2D], 1, info.wk[W_D0], s, L);
+        level = 2;
+        out = H_L3D;
+    }
+    if (w == 0 && tid == 0) info.wk[STAGE == ST_P1 ? W_P0 : STAGE == ST_P2 ? W_P1 : STAGE == ST_D1 ? W_D0 : W_D1] = s;
+    const int wl = STAGE == ST_D2 ? L_D : L_P;
+    const bool last = level == 2;
+    const PassOut o{h + out, nullptr, last ? ws.lst + (static_cast<int64_t>(r) * 2 + wl) * kList : nullptr,
+                    ws.cnt + r * 4 + N_LIST + wl,
+                    (!MASS && last) ? ws.cand + static_cast<int64_t>(r) * kMaxCand : nullptr, ws.cnt + r * 4 + N_CAND};
+    hist_chunk<MASS>(c0, c1, v, s.prefix, s.mask, level, mx, T, S, o);
+}
+
+// ---------------------------------------------------------------- the element of a key, the rank of an index
+struct FindLds {
+    uint32_t tmp_u[16];
+    int found;
+};
+
+// The n-th (1-based) smallest index among the row's elements of key `key`, from the walk's list when it holds every
+// element under the walk's last prefix, else by a scan of the row in index order (every thread of the workgroup)
+__device__ int nth_of_key(const Rows &rs, const Ws &ws, int r, int wl, uint32_t key, uint32_t n, FindLds &F) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t m = ws.cnt[r * 4 + N_LIST + wl];
+    if (tid == 0) F.found = -1;
+    __syncthreads();
+    if (m <= static_cast<uint32_t>(kList)) {
+        const uint64_t *lst = ws.lst + (static_cast<int64_t>(r) * 2 + wl) * kList;
+        for (uint32_t j = tid; j < m; j += nthr) {
+            const uint64_t e = lst[j];
+            if (static_cast<uint32_t>(e >> 32) != key) continue;
+            const uint32_t x = static_cast<uint32_t>(e);
+            uint32_t below = 0;
+            for (uint32_t q = 0; q < m; ++q) {
+                const uint64_t f = lst[q];
+                below += static_cast<uint32_t>(f >> 32) == key && static_cast<uint32_t>(f) < x;
+            }
+            if (below + 1 == n) F.found = static_cast<int>(x);
+        }
+        __syncthreads();
+        return F.found;
+    }
+    // (more elements under the prefix than a list holds: a scan, each thread a run of consecutive indices)
+    const float *row = rs.row(r);
+    uint32_t carry = 0;
+    for (int b0 = 0; b0 < rs.V; b0 += nthr * kLoads) {
+        const int x0 = b0 + tid * kLoads, x1 = min(rs.V, x0 + kLoads);
+        uint32_t mine = 0;
+        for (int x = x0; x < x1; ++x) mine += fkey(row[x]) == key;
         uint32_t tot;
-        uint32_t r = block_excl_scan(c, tmp_u, tot);
-        for (int i = b0; i < b1 && r < need_eq && above + r < static_cast<uint32_t>(K); ++i)
-            if (fkey(row[i]) == tau) {
-                comp[above + r] = (static_cast<uint64_t>(tau) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
-                ++r;
-            }
+        uint32_t at = carry + block_excl_scan(mine, F.tmp_u, tot);
+        if (at < n && at + mine >= n)
+            for (int x = x0; x < x1; ++x)
+                if (fkey(row[x]) == key && ++at == n) F.found = x;
+        carry += tot;
+        if (carry >= n) break;
     }
-    for (int i = K + tid; i < KP; i += nthr) comp[i] = 0;
-    if (full_sum) {
-        const double s = block_sum(esum, tmp_d);
-        if (tid == 0) osum[blockIdx.x] = s;
+    __syncthreads();
+    return F.found;
+}
+
+// how many of the row's elements of key `key` have an index below x (the same two ways)
+__device__ uint32_t rank_of_key(const Rows &rs, const Ws &ws, int r, int wl, uint32_t key, int x, FindLds &F) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t m = ws.cnt[r * 4 + N_LIST + wl];
+    uint32_t below = 0;
+    if (m <= static_cast<uint32_t>(kList)) {
+        const uint64_t *lst = ws.lst + (static_cast<int64_t>(r) * 2 + wl) * kList;
+        for (uint32_t j = tid; j < m; j += nthr) {
+            const uint64_t e = lst[j];
+            below += static_cast<uint32_t>(e >> 32) == key && static_cast<uint32_t>(e) < static_cast<uint32_t>(x);
+        }
+    } else {
+        const float *row = rs.row(r);
+        for (int i = tid; i < x; i += nthr) below += fkey(row[i]) == key;
+    }
+    return block_sum(below, F.tmp_u);
+}
+
+// whether index x (key kx) of row r is in its kept prefix: above the top-p walk's key, or one of its first n ties
+__device__ bool in_kept(const Rows &rs, const Ws &ws, int r, int x, uint32_t kx, FindLds &F) {
+    const Walk &p = ws.info[r].p();
+    if (kx != p.tau) return kx > p.tau;
+    if (p.n == p.c) return true;
+    return rank_of_key(rs, ws, r, L_P, p.tau, x, F) < p.n;
+}
+
+// the draws of the full-vocabulary nuclei (a workgroup a row): the draw's last level, at most to the kept prefix's
+// last element, the element from the lists
+__global__ __launch_bounds__(kPass) void draw_pick(Rows rs, Ws ws, float T) {
+    __shared__ Walk s;
+    __shared__ WalkLds L;
+    __shared__ FindLds F;
+    const int r = blockIdx.x, tid = threadIdx.x;
+    RowInfo &info = ws.info[r];
+    walk_level(ws.h[r * kHists + H_L3D], 2, info.wk[W_D1], s, L);
+    if (tid == 0) walk_finish(s, true, info.mx, T);
+    __syncthreads();
+    const Walk &p = info.p();
+    const bool past = s.tau < p.tau || (s.tau == p.tau && s.n > p.n);   // rounding past the kept prefix: its last
+    const int at = past ? nth_of_key(rs, ws, r, L_P, p.tau, p.n, F) : nth_of_key(rs, ws, r, L_D, s.tau, s.n, F);
+    if (tid == 0) {
+        const int pick = min(max(at, 0), rs.V - 1);   // (always found: the counts and the elements agree)
+        info.pick = pick;
+        ws.picks[r] = pick;
+    }
+}
+
+// ---------------------------------------------------------------- the top-K candidates (count walk)
+// A workgroup a row: the count walk's last level (tau, the ties taken); the candidates: those collected above the
+// walk's last prefix, those under it above tau and the first ties of tau in index order; sorted by value descending,
+// index ascending, in LDS; then the reference's nucleus on them as written (sampler.cpp:31-49): e_i = exp((l_i -
+// max) / T), their sum, keep = the top-p prefix, kept = e_0 + .. + e_{keep-1}, and the draw of u[row]: the first
+// i < keep where kept u <= e_0 + .. + e_i (else keep - 1).
+template <int KP>
+__global__ __launch_bounds__(kSortThreads) void cand_nucleus(Rows rs, Ws ws, float T, float top_p) {
+    extern __shared__ uint64_t comp[];   // [KP]
+    __shared__ Walk s;
+    __shared__ WalkLds L;
+    __shared__ uint32_t tmp_u[16];
+    __shared__ double tmp_d[16];
+    __shared__ int s_first;
+    const int r = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
+    RowInfo &info = ws.info[r];
+    walk_level(ws.h[r * kHists + H_L3P], 2, info.wk[W_P1], s, L);
+    if (tid == 0) {
+        walk_finish(s, false, 0.0f, 1.0f);
+        info.wk[W_P] = s;
+    }
+    __syncthreads();
+    const int K = min(static_cast<int>(s.above_cnt + s.n), KP);
+    const int above = static_cast<int>(min(ws.cnt[r * 4 + N_CAND], static_cast<uint32_t>(K)));
+    const uint64_t *cand = ws.cand + static_cast<int64_t>(r) * kMaxCand;
+    for (int i = tid; i < KP; i += nthr) comp[i] = i < above ? cand[i] : 0ull;
+    __syncthreads();
+    // the prefix's elements above tau, then the first n ties of tau (in index order), after the collected ones
+    const uint32_t m = ws.cnt[r * 4 + N_LIST + L_P];
+    const uint32_t tau = s.tau, n = s.n;
+    if (m <= static_cast<uint32_t>(kList)) {
+        const uint64_t *lst = ws.lst + static_cast<int64_t>(r) * 2 * kList;
+        uint32_t carry = 0;
+        for (uint32_t j0 = 0; j0 < m; j0 += nthr) {   // those above tau: any order
+            const uint32_t j = j0 + tid;
+            const uint64_t e = j < m ? lst[j] : 0ull;
+            const uint32_t f = j < m && static_cast<uint32_t>(e >> 32) > tau;
+            uint32_t tot;
+            const uint32_t at = carry + block_excl_scan(f, tmp_u, tot);
+            if (f && above + static_cast<int>(at) < K)
+                comp[above + at] = (e & 0xFFFFFFFF00000000ull) | (0xFFFFFFFFu - static_cast<uint32_t>(e));
+            carry += tot;
+        }
+        const int base = above + static_cast<int>(carry);
+        for (uint32_t j = tid; j < m; j += nthr) {   // the ties: by their rank in index order
+            const uint64_t e = lst[j];
+            if (static_cast<uint32_t>(e >> 32) != tau) continue;
+            uint32_t below = 0;
+            for (uint32_t q = 0; q < m; ++q)
+                below += static_cast<uint32_t>(lst[q] >> 32) == tau && static_cast<uint32_t>(lst[q]) < static_cast<uint32_t>(e);
+            if (below < n && base + static_cast<int>(below) < K)
+                comp[base + below] = (e & 0xFFFFFFFF00000000ull) | (0xFFFFFFFFu - static_cast<uint32_t>(e));
+        }
+    } else {   // (more elements under the prefix than the list holds: a scan of the row in index order)
+        const float *row = rs.row(r);
+        const uint32_t pmask = s.mask & ~1023u, pre22 = s.prefix & ~1023u;
+        uint32_t ca = 0, ct = 0;
+        for (int b0 = 0; b0 < rs.V; b0 += nthr * kLoads) {
+            const int x0 = b0 + tid * kLoads, x1 = min(rs.V, x0 + kLoads);
+            uint32_t na = 0, nt = 0;
+            for (int x = x0; x < x1; ++x) {
+                const uint32_t k = fkey(row[x]);
+                na += (k & pmask) == pre22 && k > tau;
+                nt += k == tau;
+            }
+            uint32_t ta, tt;
+            uint32_t aa = ca + block_excl_scan(na, tmp_u, ta);
+            uint32_t at = ct + block_excl_scan(nt, tmp_u, tt);
+            for (int x = x0; x < x1; ++x) {
+                const uint32_t k = fkey(row[x]);
+                const uint64_t e = (static_cast<uint64_t>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(x));
+                if ((k & pmask) == pre22 && k > tau) {
+                    if (above + static_cast<int>(aa) < K) comp[above + aa] = e;
+                    ++aa;
+                }
+                if (k == tau) {
+                    if (at < n && K - static_cast<int>(n) + static_cast<int>(at) >= 0) comp[K - static_cast<int>(n) + at] = e;
+                    ++at;
+                }
+            }
+            ca += ta;
+            ct += tt;
+        }
     }
     __syncthreads();
     // bitonic sort, descending. Pair i of a stage of stride s <= 64 has both elements in [128 (i / 64), + 128): a
@@ -212,47 +671,18 @@ __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float *__restri
                 __syncthreads();
             }
         }
-    uint32_t *ok = okey + static_cast<int64_t>(blockIdx.x) * ostride;
-    int32_t *oi = oidx + static_cast<int64_t>(blockIdx.x) * ostride;
-    for (int i = tid; i < K; i += nthr) {
-        ok[i] = static_cast<uint32_t>(comp[i] >> 32);
-        oi[i] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(comp[i]));
-    }
-}
-
-// Per row: e_i = exp((l_i - max) / T) of its K sorted candidates (to oe), the sum (osum[row] when given: the whole
-// row's; else the candidates'), keep = the top-p prefix (K when top_p >= 1; *short_out set when the candidates
-// run out first), kept = e_0 + .. + e_{keep-1}, and the draw of u[row]: the first i < keep where kept u <= e_0 + .. +
-// e_i (else keep - 1), its position to opos and index to opick.
-__global__ __launch_bounds__(kSelThreads) void nucleus_kernel(const uint32_t *__restrict__ okey,
-                                                               const int32_t *__restrict__ oidx, int64_t cs, int K,
-                                                               const double *__restrict__ osum, float T, float top_p,
-                                                               const double *__restrict__ u, float *__restrict__ oe,
-                                                               int *__restrict__ okeep, double *__restrict__ okept,
-                                                               int *__restrict__ opos, int32_t *__restrict__ opick,
-                                                               int *__restrict__ short_out) {
-    __shared__ double tmp_d[16];
-    __shared__ int s_first;
-    const int row = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
-    const uint32_t *key = okey + static_cast<int64_t>(row) * cs;
-    float *e = oe + static_cast<int64_t>(row) * cs;
-    const float mx = key_val(key[0]);
+    const float mx = key_val(static_cast<uint32_t>(comp[0] >> 32));
+    auto e_at = [&](int i) { return e_of(key_val(static_cast<uint32_t>(comp[i] >> 32)), mx, T); };
     double part = 0.0;
-    for (int i = tid; i < K; i += nthr) {
-        const float v = expf(__fdiv_rn(__fsub_rn(key_val(key[i]), mx), T));
-        e[i] = v;
-        part += static_cast<double>(v);
-    }
-    const double cand_sum = block_sum(part, tmp_d);   // (its syncs also publish e)
-    const double sum = osum ? osum[row] : cand_sum;
-    // keep: the first i where (e_0 + .. + e_i) / sum ... as the reference: acc += e_i / sum, acc >= top_p
+    for (int i = tid; i < K; i += nthr) part += static_cast<double>(e_at(i));
+    const double sum = block_sum(part, tmp_d);
     int keep = K;
-    if (top_p < 1.0f) {
+    if (top_p < 1.0f) {   // the first i where acc += e_i / sum reaches top_p
         if (tid == 0) s_first = K;
         double carry = 0.0;
         for (int c0 = 0; c0 < K; c0 += nthr) {
             const int i = c0 + tid;
-            const double t = i < K ? static_cast<double>(e[i]) / sum : 0.0;
+            const double t = i < K ? static_cast<double>(e_at(i)) / sum : 0.0;
             double tot;
             const double acc = carry + block_excl_scan(t, tmp_d, tot) + t;
             if (i < K && acc >= static_cast<double>(top_p)) atomicMin(&s_first, i);
@@ -261,26 +691,22 @@ __global__ __launch_bounds__(kSelThreads) void nucleus_kernel(const uint32_t *__
             if (s_first < K) break;
         }
         keep = s_first < K ? s_first + 1 : K;
-        if (tid == 0 && short_out && s_first >= K) atomicOr(short_out, 1);
     }
-    // kept and the draw
     __syncthreads();   // every thread has read s_first
     if (tid == 0) s_first = INT32_MAX;
-    double carry = 0.0;
-    for (int c0 = 0; c0 < keep; c0 += nthr) {   // kept: the sum of the first keep
-        const int i = c0 + tid;
-        const double t = i < keep ? static_cast<double>(e[i]) : 0.0;
-        carry += block_sum(t, tmp_d);
-    }
-    const double kept = carry;
-    const double r = kept * u[row];
-    carry = 0.0;
+    double kept = 0.0;
     for (int c0 = 0; c0 < keep; c0 += nthr) {
         const int i = c0 + tid;
-        const double t = i < keep ? static_cast<double>(e[i]) : 0.0;
+        kept += block_sum(i < keep ? static_cast<double>(e_at(i)) : 0.0, tmp_d);
+    }
+    const double rr = kept * ws.u[r];
+    double carry = 0.0;
+    for (int c0 = 0; c0 < keep; c0 += nthr) {
+        const int i = c0 + tid;
+        const double t = i < keep ? static_cast<double>(e_at(i)) : 0.0;
         double tot;
         const double acc = carry + block_excl_scan(t, tmp_d, tot) + t;
-        if (i < keep && r - acc <= 0.0) atomicMin(&s_first, i);
+        if (i < keep && rr - acc <= 0.0) atomicMin(&s_first, i);
         carry += tot;
         __syncthreads();
         if (s_first != INT32_MAX) break;
@@ -288,25 +714,40 @@ __global__ __launch_bounds__(kSelThreads) void nucleus_kernel(const uint32_t *__
     __syncthreads();
     if (tid == 0) {
         const int at = s_first != INT32_MAX ? s_first : keep - 1;   // rounding past the end: the last kept
-        okeep[row] = keep;
-        okept[row] = kept;
-        opos[row] = at;
-        opick[row] = oidx[static_cast<int64_t>(row) * cs + at];
+        const int32_t pick = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(comp[at]));
+        info.mx = mx;
+        info.sum = sum;
+        info.keep = static_cast<uint32_t>(keep);
+        info.kept = kept;
+        info.pick = pick;
+        ws.picks[r] = pick;
     }
 }
 
+// ---------------------------------------------------------------- acceptance
 // sample-and-match over the sampled rows (geode.cpp:331-350): out = the stood drafts then the first sampled token
 // that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}
-__global__ void match_kernel(const int32_t *__restrict__ pick, const int32_t *__restrict__ batch, int n,
-                             const int32_t *__restrict__ stop, int n_stop, int32_t *__restrict__ out,
-                             int *__restrict__ res) {
-    if (threadIdx.x != 0) return;
+__global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ picks, const int32_t *__restrict__ batch,
+                                                   int n, const int32_t *__restrict__ stop, int n_stop,
+                                                   int32_t *__restrict__ out, int *__restrict__ res) {
+    __shared__ int32_t pick[32], next[32];
+    __shared__ int stopped[32];
+    const int t = threadIdx.x;
+    if (t < n) {
+        pick[t] = picks[t];
+        next[t] = t + 1 < n ? batch[t + 1] : -1;
+        stopped[t] = 0;
+    }
+    __syncthreads();
+    for (int j = t; j < n_stop; j += blockDim.x)   // which rows sampled a stop token
+        for (int i = 0; i < n; ++i)
+            if (stop[j] == pick[i]) stopped[i] = 1;
+    __syncthreads();
+    if (t != 0) return;
     int emitted = 0, kept = 1;
     for (int i = 0; i < n; ++i) {
         out[emitted++] = pick[i];
-        bool is_stop = false;
-        for (int j = 0; j < n_stop; ++j) is_stop |= stop[j] == pick[i];
-        if (i + 1 < n && pick[i] == batch[i + 1] && !is_stop) {
+        if (i + 1 < n && pick[i] == next[i] && !stopped[i]) {
             ++kept;
             continue;
         }
@@ -328,129 +769,196 @@ __global__ void penalty_kernel(float *__restrict__ logits, int64_t ld, const int
         if (fresh[j]) lg[batch[j]] -= penalty;
 }
 
-__global__ void first_kernel(const int32_t *__restrict__ idx, int64_t cs, int rows, int32_t *__restrict__ pick) {
-    for (int r = threadIdx.x; r < rows; r += blockDim.x) pick[r] = idx[static_cast<int64_t>(r) * cs];
-}
-
-struct RowSet {   // the nucleus outputs of a set of rows
-    const uint32_t *key;
-    const int32_t *idx;
-    const float *e;
-    const int *keep;
-    const double *kept;
-    const int *pos;
-    const int32_t *pick;
-    int64_t cs;
+// max(0, p_x - q_x) of a row pair (target row rp, draft row rq): p_x = e_x / kept over the target's kept prefix (0
+// outside it), q_x likewise
+struct Residual {
+    const float *tp, *tq;
+    float mxp, mxq, T;
+    double keptp, keptq;
+    Walk P, Q;
+    int rp, rq;
+    // (every thread) the residual of the elements x0 + j, j < kLoads, below c1, into v; the partly taken ties of the
+    // walks' keys ranked through the lists
+    __device__ void run(const Rows &rs, const Ws &ws, int x0, int c1, double (&v)[kLoads], FindLds &F,
+                        int *s_flag) const {
+        float lp[kLoads], lq[kLoads];
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {   // (the loads first, all in flight)
+            const int x = min(x0 + j, c1 - 1);
+            lp[j] = tp[x];
+            lq[j] = tq[x];
+        }
+        bool tied = false;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            v[j] = 0.0;
+            if (x0 + j >= c1) continue;
+            const uint32_t kp = fkey(lp[j]), kq = fkey(lq[j]);
+            const bool inp = kp > P.tau || (kp == P.tau && P.n == P.c);
+            const bool inq = kq > Q.tau || (kq == Q.tau && Q.n == Q.c);
+            tied |= (kp == P.tau && P.n < P.c) || (kq == Q.tau && Q.n < Q.c);
+            const double p = inp ? static_cast<double>(e_of(lp[j], mxp, T)) / keptp : 0.0;
+            const double q = inq ? static_cast<double>(e_of(lq[j], mxq, T)) / keptq : 0.0;
+            v[j] = fmax(0.0, p - q);
+        }
+        // partly taken ties (rare): ranked one element at a time, the whole workgroup together
+        if (threadIdx.x == 0) *s_flag = 0;
+        __syncthreads();
+        if (tied) *s_flag = 1;
+        __syncthreads();
+        if (!*s_flag) return;
+        for (int t = 0; t < static_cast<int>(blockDim.x); ++t) {
+            __syncthreads();
+            if (static_cast<int>(threadIdx.x) == t) *s_flag = tied ? x0 : -1;
+            __syncthreads();
+            const int y0 = *s_flag;
+            if (y0 < 0) continue;
+            for (int j = 0; j < kLoads && y0 + j < c1; ++j) {
+                const float a = tp[y0 + j], b = tq[y0 + j];
+                const uint32_t kp = fkey(a), kq = fkey(b);
+                const bool tp_ = kp == P.tau && P.n < P.c, tq_ = kq == Q.tau && Q.n < Q.c;
+                if (!tp_ && !tq_) continue;
+                const bool inp = tp_ ? rank_of_key(rs, ws, rp, L_P, P.tau, y0 + j, F) < P.n
+                                     : (kp > P.tau || (kp == P.tau && P.n == P.c));
+                const bool inq = tq_ ? rank_of_key(rs, ws, rq, L_P, Q.tau, y0 + j, F) < Q.n
+                                     : (kq > Q.tau || (kq == Q.tau && Q.n == Q.c));
+                if (static_cast<int>(threadIdx.x) == t) {
+                    const double p = inp ? static_cast<double>(e_of(a, mxp, T)) / keptp : 0.0;
+                    const double q = inq ? static_cast<double>(e_of(b, mxq, T)) / keptq : 0.0;
+                    v[j] = fmax(0.0, p - q);
+                }
+            }
+        }
+        __syncthreads();
+    }
 };
 
-// The textbook rule over k drafts (target rows 0..k, draft rows 0..k-1), one workgroup. qq: a zeroed device array
-// of V doubles (left zeroed). res[0] = emitted.
-__global__ __launch_bounds__(kSelThreads) void textbook_kernel(RowSet P, RowSet Q, int k, int greedy,
-                                                               const float *__restrict__ u_acc, float u_res,
-                                                               double *__restrict__ qq, int32_t *__restrict__ out,
-                                                               int *__restrict__ res) {
-    extern __shared__ uint64_t srt[];   // [kMaxCand] (index << 32) | slot, for the residual in index order
+// The textbook rule (target rows 0..k, draft rows k+1..2k, their nuclei and draws done; grid S, or 1 when greedy).
+// Every workgroup takes the decisions: d_i stands with probability min(1, p_i(d_i) / q_i(d_i)); at the first
+// rejection, each workgroup sums the residual over its chunk, and the last to finish draws by inverse CDF in index
+// order (u_res x the total; no residual mass: the target row's own draw). out: the stood drafts, then that token
+// or, when all stand, the bonus (target row k's draw; its argmax when greedy). st[0] = emitted.
+__global__ __launch_bounds__(kPass) void textbook_finish(Rows rs, Ws ws, int k, int greedy, float T,
+                                                         const float *__restrict__ u_acc, float u_res,
+                                                         double *__restrict__ rsum, uint32_t *__restrict__ done,
+                                                         int32_t *__restrict__ out, int *__restrict__ st) {
+    __shared__ FindLds F;
     __shared__ double tmp_d[16];
-    __shared__ int s_pd_pos, s_first;
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    int emitted = 0;
-    bool all_stood = true;
+    __shared__ int s_last, s_w, s_first, s_lastpos, s_flag;
+    __shared__ double s_goal;
+    const int w = blockIdx.x, tid = threadIdx.x;
+    int emitted = 0, rej = -1;
+    bool fell = false;
     for (int i = 0; i < k; ++i) {
-        if (greedy) {   // argmax = the first candidate (ties to the lower index, as max_element)
-            const int y = P.idx[i * P.cs], d = Q.idx[i * Q.cs];
-            if (tid == 0) out[emitted] = y;
+        const int d = min(max(ws.picks[k + 1 + i], 0), rs.V - 1);
+        if (greedy) {   // the first argmaxes: the target's token is emitted; a different draft ends the step
             ++emitted;
-            if (y != d) {
-                all_stood = false;
+            if (ws.picks[i] != d) {
+                fell = true;
                 break;
             }
             continue;
         }
-        const int d = Q.pick[i];
-        const double qd = static_cast<double>(Q.e[i * Q.cs + Q.pos[i]]) / Q.kept[i];
-        if (tid == 0) s_pd_pos = -1;
-        __syncthreads();
-        const int kp = P.keep[i];
-        for (int j = tid; j < kp; j += nthr)
-            if (P.idx[i * P.cs + j] == d) s_pd_pos = j;
-        __syncthreads();
-        const double pd = s_pd_pos >= 0 ? static_cast<double>(P.e[i * P.cs + s_pd_pos]) / P.kept[i] : 0.0;
+        const RowInfo &P = ws.info[i], &Q = ws.info[k + 1 + i];
+        const float lq = rs.row(k + 1 + i)[d], lp = rs.row(i)[d];
+        const double qd = static_cast<double>(e_of(lq, Q.mx, T)) / Q.kept;
+        const bool in_p = in_kept(rs, ws, i, d, fkey(lp), F);
+        const double pd = in_p ? static_cast<double>(e_of(lp, P.mx, T)) / P.kept : 0.0;
         if (static_cast<double>(u_acc[i]) * qd < pd) {   // accepted with probability min(1, p/q)
-            if (tid == 0) out[emitted] = d;
             ++emitted;
             continue;
         }
-        // rejected: a token from max(0, p - q), normalized, by inverse CDF in index order
-        const int kq = Q.keep[i];
-        for (int j = tid; j < kq; j += nthr)
-            qq[Q.idx[i * Q.cs + j]] = static_cast<double>(Q.e[i * Q.cs + j]) / Q.kept[i];
-        __syncthreads();
-        int np = 1;
-        while (np < kp) np <<= 1;
-        for (int j = tid; j < np; j += nthr)
-            srt[j] = j < kp ? (static_cast<uint64_t>(static_cast<uint32_t>(P.idx[i * P.cs + j])) << 32) |
-                                  static_cast<uint32_t>(j)
-                            : ~0ull;
-        __syncthreads();
-        for (int size = 2; size <= np; size <<= 1)   // ascending by index
-            for (int stride = size / 2; stride > 0; stride >>= 1) {
-                for (int j = tid; j < np / 2; j += nthr) {
-                    const int lo = 2 * stride * (j / stride) + (j % stride), hi = lo + stride;
-                    const bool asc = (lo & size) == 0;
-                    const uint64_t a = srt[lo], b = srt[hi];
-                    if ((a > b) == asc) {
-                        srt[lo] = b;
-                        srt[hi] = a;
-                    }
-                }
-                __syncthreads();
+        rej = i;
+        break;
+    }
+    auto write_head = [&](int n_head) {   // the stood drafts (greedy: the target's argmaxes)
+        for (int i = tid; i < n_head; i += kPass) out[i] = greedy ? ws.picks[i] : ws.picks[k + 1 + i];
+    };
+    if (rej < 0) {
+        if (w == 0) {
+            write_head(emitted);
+            if (!fell) {   // every draft stood: the bonus
+                if (tid == 0) out[emitted] = ws.picks[k];
+                ++emitted;
             }
-        // residual weights in index order, their total, and the inverse CDF
-        auto resid = [&](int j) -> double {
-            if (j >= kp) return 0.0;
-            const int slot = static_cast<int>(srt[j] & 0xFFFFFFFFu), x = static_cast<int>(srt[j] >> 32);
-            const double pp = static_cast<double>(P.e[i * P.cs + slot]) / P.kept[i];
-            return fmax(0.0, pp - qq[x]);
-        };
-        double total = 0.0;
-        for (int c0 = 0; c0 < kp; c0 += nthr) total += block_sum(resid(c0 + tid), tmp_d);
-        int pick;
-        if (!(total > 0.0)) {
-            pick = P.pick[i];   // the row's own draw; the caller drew target rows with u_res
-        } else {
-            const double goal = static_cast<double>(u_res) * total;
-            if (tid == 0) s_first = kp;
-            double carry = 0.0;
-            for (int c0 = 0; c0 < kp; c0 += nthr) {
-                const int j = c0 + tid;
-                const double t = resid(j);
-                double tot;
-                const double acc = carry + block_excl_scan(t, tmp_d, tot) + t;
-                if (j < kp && t > 0.0 && acc >= goal) atomicMin(&s_first, j);
-                carry += tot;
-                __syncthreads();
-                if (s_first < kp) break;
-            }
-            __syncthreads();
-            int j = s_first;
-            if (j >= kp) {   // rounding left the goal past the end: the last positive weight
-                j = kp - 1;
-                while (j > 0 && !(resid(j) > 0.0)) --j;
-            }
-            pick = static_cast<int>(srt[j] >> 32);
+            if (tid == 0) st[0] = emitted;
         }
-        __syncthreads();   // every thread is done reading qq
-        for (int j = tid; j < kq; j += nthr) qq[Q.idx[i * Q.cs + j]] = 0.0;   // leave qq zeroed
-        if (tid == 0) out[emitted] = pick;
-        ++emitted;
-        if (tid == 0) res[0] = emitted;
         return;
     }
-    if (all_stood) {   // every draft stood: the bonus token from the last target row
-        if (tid == 0) out[emitted] = greedy ? P.idx[k * P.cs] : P.pick[k];
-        ++emitted;
+    // the residual of pair rej over this chunk, thread tid taking a run of consecutive indices
+    const RowInfo &P = ws.info[rej], &Q = ws.info[k + 1 + rej];
+    const Residual R{rs.row(rej), rs.row(k + 1 + rej), P.mx, Q.mx, T, P.kept, Q.kept, P.p(), Q.p(), rej, k + 1 + rej};
+    {
+        double v[kLoads];
+        const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
+        R.run(rs, ws, c0 + tid * kLoads, c1, v, F, &s_flag);
+        double acc = 0.0;
+        for (int j = 0; j < kLoads; ++j) acc += v[j];
+        const double s = block_sum(acc, tmp_d);
+        if (tid == 0) {
+            rsum[w] = s;
+            __threadfence();
+            s_last = atomicAdd(done, 1u) == static_cast<uint32_t>(gridDim.x - 1);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();
     }
-    if (tid == 0) res[0] = emitted;
+    // the last workgroup: the chunk where u_res x total is reached, then the element in it
+    if (tid == 0) {
+        double total = 0.0;
+        for (int c = 0; c < rs.S; ++c) total += __hip_atomic_load(rsum + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_w = -1;
+        if (total > 0.0) {
+            const double goal = static_cast<double>(u_res) * total;
+            double cum = 0.0;
+            int last = -1;
+            for (int c = 0; c < rs.S; ++c) {
+                const double rc = __hip_atomic_load(rsum + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (rc > 0.0) last = c;
+                if (rc > 0.0 && cum + rc >= goal) {
+                    s_w = c;
+                    break;
+                }
+                cum += rc;
+            }
+            // rounding left the goal past the end: the last chunk with mass, to its last positive weight
+            s_goal = s_w < 0 ? INFINITY : goal - cum;
+            if (s_w < 0) s_w = last;
+        }
+        s_first = INT32_MAX;
+        s_lastpos = -1;
+    }
+    __syncthreads();
+    int pick;
+    if (s_w < 0) {
+        pick = ws.picks[rej];   // no residual mass: the target row's own draw
+    } else {
+        double v[kLoads];
+        const int c0 = s_w * rs.C, c1 = min(rs.V, c0 + rs.C), x0 = c0 + tid * kLoads;
+        R.run(rs, ws, x0, c1, v, F, &s_flag);
+        double mine = 0.0;
+        for (int j = 0; j < kLoads; ++j) mine += v[j];
+        double tot;
+        double acc = block_excl_scan(mine, tmp_d, tot);
+        const double goal = s_goal;
+        for (int j = 0; j < kLoads; ++j) {
+            if (!(v[j] > 0.0)) continue;
+            acc += v[j];
+            atomicMax(&s_lastpos, x0 + j);
+            if (acc >= goal) {
+                atomicMin(&s_first, x0 + j);
+                break;
+            }
+        }
+        __syncthreads();
+        pick = s_first != INT32_MAX ? s_first : s_lastpos;   // rounding past the end: the last positive weight
+    }
+    write_head(emitted);
+    if (tid == 0) {
+        out[emitted] = pick;
+        st[0] = emitted + 1;
+    }
 }
 
 // ---------------------------------------------------------------- host side
@@ -468,102 +976,126 @@ struct Workspace {
     }
 };
 
-struct Nuclei {   // device arrays for R rows of up to C candidates
-    uint32_t *key;
-    int32_t *idx;
-    float *e;
-    double *sum, *kept, *u;
-    int *keep, *pos, *flag;
-    int32_t *pick;
-    int64_t cs;
-    RowSet rows(int r0) const {
-        return RowSet{key + r0 * cs, idx + r0 * cs, e + r0 * cs, keep + r0, kept + r0, pos + r0, pick + r0, cs};
+// pinned host memory for a call's inputs and results (one copy each way)
+struct Pinned {
+    void *p = nullptr;
+    size_t n = 0;
+    void *get(size_t want) {
+        if (want <= n) return p;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) return nullptr;
+        n = want;
+        return p;
     }
 };
 
-size_t nuclei_bytes(int R, int C) {
-    return static_cast<size_t>(R) * C * (4 + 4 + 4) + static_cast<size_t>(R) * (8 * 3 + 4 * 3 + 4) + 64;
+Workspace &ws_mem() {
+    static Workspace w;
+    return w;
+}
+Pinned &pinned() {
+    static Pinned p;
+    return p;
 }
 
-Nuclei carve(void *base, int R, int C) {
+constexpr size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// The arrays of R rows, carved from one allocation, then `io` bytes for the call's inputs and results: the inputs
+// (the uniforms first, then the caller's) are copied in one piece from pinned memory, the results back likewise.
+struct Carved {
+    Ws ws;
+    char *io;   // device: [R] doubles of uniforms, then the caller's arrays
+};
+
+size_t ws_bytes(int R, size_t io) {
+    size_t b = 0;
+    b += align256(sizeof(RowInfo) * R);
+    b += align256(static_cast<size_t>(R) * kMaxChunks * 16);
+    b += align256(sizeof(LevelHist) * kHists * R);
+    b += align256(16 * static_cast<size_t>(R) + 4 * static_cast<size_t>(R));
+    b += align256(static_cast<size_t>(R) * kMaxCand * 8);
+    b += align256(static_cast<size_t>(R) * 2 * kList * 8);
+    b += align256(8 * static_cast<size_t>(R) + io);
+    return b;
+}
+
+Carved carve(void *base, int R) {
     char *p = static_cast<char *>(base);
-    Nuclei n;
-    n.cs = C;
-    n.key = reinterpret_cast<uint32_t *>(p);
-    p += static_cast<size_t>(R) * C * 4;
-    n.idx = reinterpret_cast<int32_t *>(p);
-    p += static_cast<size_t>(R) * C * 4;
-    n.e = reinterpret_cast<float *>(p);
-    p += static_cast<size_t>(R) * C * 4;
-    n.sum = reinterpret_cast<double *>(p);
-    p += static_cast<size_t>(R) * 8;
-    n.kept = reinterpret_cast<double *>(p);
-    p += static_cast<size_t>(R) * 8;
-    n.u = reinterpret_cast<double *>(p);
-    p += static_cast<size_t>(R) * 8;
-    n.keep = reinterpret_cast<int *>(p);
-    p += static_cast<size_t>(R) * 4;
-    n.pos = reinterpret_cast<int *>(p);
-    p += static_cast<size_t>(R) * 4;
-    n.pick = reinterpret_cast<int32_t *>(p);
-    p += static_cast<size_t>(R) * 4;
-    n.flag = reinterpret_cast<int *>(p);
-    return n;
+    Carved c{};
+    Ws &w = c.ws;
+    w.info = reinterpret_cast<RowInfo *>(p);
+    p += align256(sizeof(RowInfo) * R);
+    const size_t ch = static_cast<size_t>(R) * kMaxChunks;
+    w.psum = reinterpret_cast<double *>(p);
+    w.pmax = reinterpret_cast<uint32_t *>(p + ch * 8);
+    w.pidx = reinterpret_cast<int32_t *>(p + ch * 12);
+    p += align256(ch * 16);
+    w.h = reinterpret_cast<LevelHist *>(p);
+    p += align256(sizeof(LevelHist) * kHists * R);
+    w.cnt = reinterpret_cast<uint32_t *>(p);
+    w.picks = reinterpret_cast<int32_t *>(p + 16 * static_cast<size_t>(R));
+    p += align256(16 * static_cast<size_t>(R) + 4 * static_cast<size_t>(R));
+    w.cand = reinterpret_cast<uint64_t *>(p);
+    p += align256(static_cast<size_t>(R) * kMaxCand * 8);
+    w.lst = reinterpret_cast<uint64_t *>(p);
+    p += align256(static_cast<size_t>(R) * 2 * kList * 8);
+    c.io = p;
+    w.u = reinterpret_cast<double *>(p);
+    return c;
+}
+
+Rows make_rows(const float *x1, int R1, const float *x2, int64_t ld, int V) {
+    Rows rs{x1, x2, ld, R1, V, 1, V};
+    rs.S = std::max(1, (V + kChunk - 1) / kChunk);
+    rs.C = (V + rs.S - 1) / rs.S;
+    rs.S = (V + rs.C - 1) / rs.C;   // (no empty chunk)
+    return rs;
 }
 
 template <int KP>
-int launch_topk(const float *x, int64_t ldx, int rows, int V, int K, float T, int full, const Nuclei &n,
-                hipStream_t st) {
+int launch_cand_nucleus(const Rows &rs, const Ws &ws, int R, float T, float top_p, hipStream_t st) {
     static int granted = 0;
     const size_t lds = static_cast<size_t>(KP) * 8;
-    if (lds_grant(reinterpret_cast<const void *>(&topk_kernel<KP>), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL(topk_kernel<KP>, dim3(rows), dim3(kSelThreads), lds, st, x, ldx, V, K, T, full, n.key, n.idx,
-                       n.cs, n.sum);
+    if (lds_grant(reinterpret_cast<const void *>(&cand_nucleus<KP>), lds, granted) != 0) return -1;
+    hipLaunchKernelGGL(cand_nucleus<KP>, dim3(R), dim3(kSortThreads), lds, st, rs, ws, T, top_p);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-int topk(const float *x, int64_t ldx, int rows, int V, int K, float T, int full, const Nuclei &n, hipStream_t st) {
-    if (K <= 1024) return launch_topk<1024>(x, ldx, rows, V, K, T, full, n, st);
-    if (K <= 4096) return launch_topk<4096>(x, ldx, rows, V, K, T, full, n, st);
-    return launch_topk<kMaxCand>(x, ldx, rows, V, K, T, full, n, st);
-}
-
-// The nuclei of `rows` rows with uniforms u (host): candidates K = top_k, else cap, else (cap = 0, the full
-// vocabulary) the smallest of 4096 / 16384 that holds the top-p prefix. T <= 0: K = 1 (the first argmax).
-int nuclei(const float *x, int64_t ldx, int rows, int V, float T, float top_p, int top_k, int cap, const double *u,
-           const Nuclei &n, hipStream_t st) {
-    GV_REQUIRE(x && rows >= 1 && V >= 1, "sampler: bad arguments");
-    if (T <= 0.0f) {   // the first argmax: the top candidate (ties to the lower index)
-        if (topk(x, ldx, rows, V, 1, 1.0f, 0, n, st) != 0) return -1;
-        hipLaunchKernelGGL(first_kernel, dim3(1), dim3(64), 0, st, n.idx, n.cs, rows, n.pick);
+// The pick of each of R rows into ws.picks (and, sampling, its nucleus into ws.info), the uniforms already in ws.u:
+// T <= 0 the first argmax; top_k or cap below V the top-K candidates' nucleus (K <= 16384); else the full
+// vocabulary's.
+int nuclei(const Rows &rs, int R, float T, float top_p, int top_k, int cap, const Ws &ws, hipStream_t st) {
+    GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
+    const dim3 grid(rs.S, R), block(kPass);
+    hipLaunchKernelGGL(max_pass, grid, block, 0, st, rs, ws);
+    if (T <= 0.0f) {
+        hipLaunchKernelGGL(argmax_reduce, dim3(R), dim3(64), 0, st, ws, rs.S);
         GV_CHECK_HIP(hipGetLastError());
         return 0;
     }
-    GV_CHECK_HIP(hipMemcpyAsync(n.u, u, static_cast<size_t>(rows) * 8, hipMemcpyHostToDevice, st));
-    const bool full = top_k <= 0 && cap <= 0;
-    GV_REQUIRE(!full || top_p < 1.0f, "sampler: the full vocabulary needs top_p < 1 (the nucleus is sorted on the GPU)");
-    for (int K0 : {4096, kMaxCand}) {
-        int K = top_k > 0 ? std::min(top_k, V) : (cap > 0 ? std::min(cap, V) : std::min(K0, V));
-        GV_REQUIRE(K <= kMaxCand, "sampler: at most 16384 candidates");
-        GV_CHECK_HIP(hipMemsetAsync(n.flag, 0, 4, st));
-        if (topk(x, ldx, rows, V, K, T, full ? 1 : 0, n, st) != 0) return -1;
-        hipLaunchKernelGGL(nucleus_kernel, dim3(rows), dim3(kSelThreads), 0, st, n.key, n.idx, n.cs, K,
-                           full ? n.sum : nullptr, T, top_p, n.u, n.e, n.keep, n.kept, n.pos, n.pick, n.flag);
+    const int K = top_k > 0 ? std::min(top_k, rs.V) : (cap > 0 ? std::min(cap, rs.V) : rs.V);
+    if (K < rs.V) {   // the top-K candidates: a count walk to the K-th, collected, sorted, the nucleus as written
+        GV_REQUIRE(K <= kMaxCand, "sampler: at most 16384 top-k candidates (top_k or cap); 0 takes the whole vocabulary");
+        hipLaunchKernelGGL(level1_pass<false>, grid, block, 0, st, rs, ws, T);
+        hipLaunchKernelGGL((walk_pass<false, ST_P1>), grid, block, 0, st, rs, ws, T, top_p, K);
+        hipLaunchKernelGGL((walk_pass<false, ST_P2>), grid, block, 0, st, rs, ws, T, top_p, K);
         GV_CHECK_HIP(hipGetLastError());
-        if (!full) return 0;
-        int flag = 0;
-        GV_CHECK_HIP(hipMemcpyAsync(&flag, n.flag, 4, hipMemcpyDeviceToHost, st));
-        GV_CHECK_HIP(hipStreamSynchronize(st));
-        if (!flag || K == V) return 0;
-        GV_REQUIRE(K0 != kMaxCand, "sampler: the top-p nucleus holds more than 16384 candidates");
+        return K <= 1024 ? launch_cand_nucleus<1024>(rs, ws, R, T, top_p, st)
+             : K <= 4096 ? launch_cand_nucleus<4096>(rs, ws, R, T, top_p, st)
+                         : launch_cand_nucleus<kMaxCand>(rs, ws, R, T, top_p, st);
     }
+    // every token a candidate: the mass walks over the whole row, no sort
+    hipLaunchKernelGGL(level1_pass<true>, grid, block, 0, st, rs, ws, T);
+    hipLaunchKernelGGL((walk_pass<true, ST_P1>), grid, block, 0, st, rs, ws, T, top_p, K);
+    hipLaunchKernelGGL((walk_pass<true, ST_P2>), grid, block, 0, st, rs, ws, T, top_p, K);
+    hipLaunchKernelGGL((walk_pass<true, ST_D1>), grid, block, 0, st, rs, ws, T, top_p, K);
+    hipLaunchKernelGGL((walk_pass<true, ST_D2>), grid, block, 0, st, rs, ws, T, top_p, K);
+    hipLaunchKernelGGL(draw_pick, dim3(R), block, 0, st, rs, ws, T);
+    GV_CHECK_HIP(hipGetLastError());
     return 0;
-}
-
-Workspace &ws() {
-    static Workspace w;
-    return w;
 }
 
 }  // namespace
@@ -576,15 +1108,22 @@ extern "C" {
 int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float temperature, float top_p, int top_k,
                    int cap, const double *u, int32_t *out) {
     if (ensure_init() != 0) return -1;
-    GV_REQUIRE(logits && out && rows >= 1 && rows <= 64 && V >= 1 && ld >= V, "gv_sample_rows: bad arguments");
+    GV_REQUIRE(logits && out && rows >= 1 && rows <= kSampleRows && V >= 1 && ld >= V, "gv_sample_rows: bad arguments");
     GV_REQUIRE(temperature <= 0.0f || u, "gv_sample_rows: uniforms needed when temperature > 0");
-    void *base = ws().get(nuclei_bytes(rows, kMaxCand));
-    GV_REQUIRE(base, "gv_sample_rows: out of device memory");
-    const Nuclei n = carve(base, rows, kMaxCand);
+    void *base = ws_mem().get(ws_bytes(rows, 0));
+    auto *pin = static_cast<char *>(pinned().get(8 * static_cast<size_t>(rows)));
+    GV_REQUIRE(base && pin, "gv_sample_rows: out of memory");
+    const Carved c = carve(base, rows);
     const hipStream_t st = stream();
-    if (nuclei(logits, ld, rows, V, temperature, top_p, top_k, cap, u, n, st) != 0) return -1;
-    GV_CHECK_HIP(hipMemcpyAsync(out, n.pick, static_cast<size_t>(rows) * 4, hipMemcpyDeviceToHost, st));
+    if (temperature > 0.0f) {
+        std::copy(u, u + rows, reinterpret_cast<double *>(pin));
+        GV_CHECK_HIP(hipMemcpyAsync(c.ws.u, pin, 8 * static_cast<size_t>(rows), hipMemcpyHostToDevice, st));
+    }
+    const Rows rs = make_rows(logits, rows, nullptr, ld, V);
+    if (nuclei(rs, rows, temperature, top_p, top_k, cap, c.ws, st) != 0) return -1;
+    GV_CHECK_HIP(hipMemcpyAsync(pin, c.ws.picks, 4 * static_cast<size_t>(rows), hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
+    std::copy(reinterpret_cast<int32_t *>(pin), reinterpret_cast<int32_t *>(pin) + rows, out);
     return 0;
 }
 
@@ -605,7 +1144,7 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
     GV_REQUIRE(n_stop >= 0 && n_stop <= 1024 && (n_stop == 0 || stop), "gv_accept_match: at most 1024 stop tokens");
     const bool penalize = presence_penalty != 0.0f;
     // which drafts are new to the answer (one subtraction a token); seen must hold distinct tokens of the vocabulary
-    std::vector<int32_t> fresh(33, 0);
+    int32_t fresh[33] = {};
     if (penalize) {
         std::vector<uint8_t> in(static_cast<size_t>(V), 0);
         for (int j = 0; j < n_seen; ++j) {
@@ -615,39 +1154,43 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
         }
         for (int j = 1; j < n; ++j) {
             GV_REQUIRE(batch[j] >= 0 && batch[j] < V, "gv_accept_match: draft out of range");
-            if (!in[static_cast<size_t>(batch[j])]) fresh[static_cast<size_t>(j)] = 1, in[static_cast<size_t>(batch[j])] = 1;
+            if (!in[static_cast<size_t>(batch[j])]) fresh[j] = 1, in[static_cast<size_t>(batch[j])] = 1;
         }
     }
-    const size_t nb = nuclei_bytes(n, kMaxCand);
-    const size_t extra = (64 + 33 + static_cast<size_t>(n_stop) + (penalize ? static_cast<size_t>(n_seen) : 0)) * 4 + 256;
-    char *base = static_cast<char *>(ws().get(nb + extra));
-    GV_REQUIRE(base, "gv_accept_match: out of device memory");
-    const Nuclei nu = carve(base, n, kMaxCand);
-    int32_t *dbatch = reinterpret_cast<int32_t *>(base + nb);
-    int32_t *dout = dbatch + 32;
-    int *dres = reinterpret_cast<int *>(dout + 32);
-    int32_t *dfresh = reinterpret_cast<int32_t *>(dres + 4);
-    int32_t *dstop = dfresh + 33;
-    int32_t *dseen = dstop + n_stop;
+    // io: [n] uniforms (doubles), then out[32], res[4], batch[32], fresh[33], stop[n_stop], seen[n_seen] (int32)
+    const int n_seen_dev = penalize ? n_seen : 0;
+    const size_t ints = 32 + 4 + 32 + 33 + static_cast<size_t>(n_stop) + static_cast<size_t>(n_seen_dev);
+    const size_t io = 8 * static_cast<size_t>(n) + 4 * ints;
+    void *base = ws_mem().get(ws_bytes(n, io));
+    auto *pin = static_cast<char *>(pinned().get(io));
+    GV_REQUIRE(base && pin, "gv_accept_match: out of memory");
+    const Carved c = carve(base, n);
+    int32_t *hint = reinterpret_cast<int32_t *>(pin + 8 * static_cast<size_t>(n));
+    int32_t *dint = reinterpret_cast<int32_t *>(c.io + 8 * static_cast<size_t>(n));
+    if (temperature > 0.0f) std::copy(u, u + n, reinterpret_cast<double *>(pin));
+    std::copy(batch, batch + n, hint + 36);
+    std::copy(fresh, fresh + 33, hint + 68);
+    if (n_stop) std::copy(stop, stop + n_stop, hint + 101);
+    if (n_seen_dev) std::copy(seen, seen + n_seen_dev, hint + 101 + n_stop);
     const hipStream_t st = stream();
-    GV_CHECK_HIP(hipMemcpyAsync(dbatch, batch, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, st));
-    if (n_stop) GV_CHECK_HIP(hipMemcpyAsync(dstop, stop, static_cast<size_t>(n_stop) * 4, hipMemcpyHostToDevice, st));
+    GV_CHECK_HIP(hipMemcpyAsync(c.io, pin, io, hipMemcpyHostToDevice, st));
+    int32_t *dout = dint, *dres = dint + 32, *dbatch = dint + 36, *dfresh = dint + 68, *dstop = dint + 101;
+    int32_t *dseen = dstop + n_stop;
     if (penalize) {
-        GV_CHECK_HIP(hipMemcpyAsync(dfresh, fresh.data(), 33 * 4, hipMemcpyHostToDevice, st));
-        if (n_seen) GV_CHECK_HIP(hipMemcpyAsync(dseen, seen, static_cast<size_t>(n_seen) * 4, hipMemcpyHostToDevice, st));
-        hipLaunchKernelGGL(penalty_kernel, dim3(n), dim3(256), 0, st, logits, ld, dseen, n_seen, dbatch, dfresh,
+        hipLaunchKernelGGL(penalty_kernel, dim3(n), dim3(256), 0, st, logits, ld, dseen, n_seen_dev, dbatch, dfresh,
                            presence_penalty);
         GV_CHECK_HIP(hipGetLastError());
     }
-    if (nuclei(logits, ld, n, V, temperature, top_p, top_k, cap, u, nu, st) != 0) return -1;
-    hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, nu.pick, dbatch, n, dstop, n_stop, dout, dres);
+    const Rows rs = make_rows(logits, n, nullptr, ld, V);
+    if (nuclei(rs, n, temperature, top_p, top_k, cap, c.ws, st) != 0) return -1;
+    hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, dbatch, n, dstop, n_stop, dout, dres);
     GV_CHECK_HIP(hipGetLastError());
-    int res[2] = {0, 0};
-    GV_CHECK_HIP(hipMemcpyAsync(res, dres, 8, hipMemcpyDeviceToHost, st));
+    GV_CHECK_HIP(hipMemcpyAsync(hint, dout, 36 * 4, hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
-    GV_CHECK_HIP(hipMemcpy(out, dout, static_cast<size_t>(res[0]) * 4, hipMemcpyDeviceToHost));
-    if (kept) *kept = res[1];
-    return res[0];
+    const int emitted = hint[32];
+    for (int i = 0; i < emitted; ++i) out[i] = hint[i];
+    if (kept) *kept = hint[33];
+    return emitted;
 }
 
 int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int V, int k, float temperature,
@@ -656,50 +1199,39 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
     GV_REQUIRE(target && draft && out && k >= 1 && k <= 31 && V >= 1 && ld >= V, "gv_accept_textbook: bad arguments");
     GV_REQUIRE(greedy || (u_draft && u_acc && temperature > 0.0f), "gv_accept_textbook: uniforms and T > 0 needed");
     const int R = 2 * k + 1;
-    const size_t nb = nuclei_bytes(R, kMaxCand);
-    const size_t qb = static_cast<size_t>(V) * 8;
-    char *base = static_cast<char *>(ws().get(nb + qb + 1024));
-    GV_REQUIRE(base, "gv_accept_textbook: out of device memory");
-    double *qq = reinterpret_cast<double *>(base + nb);
-    float *dacc = reinterpret_cast<float *>(base + nb + qb);
-    int32_t *dout = reinterpret_cast<int32_t *>(dacc + 32);
-    int *dres = reinterpret_cast<int *>(dout + 32);
+    // io: [R] uniforms, then rsum[kMaxChunks] (double), u_acc[32] (float), done, out[32], st (uint32 / int32)
+    const size_t io = 8 * static_cast<size_t>(R) + 8 * kMaxChunks + 4 * 32 + 4 + 4 * 33;
+    void *base = ws_mem().get(ws_bytes(R, io));
+    auto *pin = static_cast<char *>(pinned().get(io));
+    GV_REQUIRE(base && pin, "gv_accept_textbook: out of memory");
+    const Carved c = carve(base, R);
+    double *rsum = reinterpret_cast<double *>(c.io + 8 * static_cast<size_t>(R));
+    float *dacc = reinterpret_cast<float *>(rsum + kMaxChunks);
+    uint32_t *ddone = reinterpret_cast<uint32_t *>(dacc + 32);
+    int32_t *dout = reinterpret_cast<int32_t *>(ddone + 1);
+    int *dst = dout + 32;
+    // target rows 0..k draw with u_res (row k's is the bonus; a rejected row with no residual mass falls back to its
+    // own), draft rows with u_draft
+    double *hu = reinterpret_cast<double *>(pin);
+    for (int r = 0; r <= k; ++r) hu[r] = static_cast<double>(u_res);
+    for (int i = 0; i < k; ++i) hu[k + 1 + i] = greedy ? 0.0 : static_cast<double>(u_draft[i]);
+    float *hacc = reinterpret_cast<float *>(pin + 8 * static_cast<size_t>(R) + 8 * kMaxChunks);
+    for (int i = 0; i < k; ++i) hacc[i] = greedy ? 0.0f : u_acc[i];
+    *reinterpret_cast<uint32_t *>(hacc + 32) = 0u;   // the finishing count
     const hipStream_t st = stream();
-    GV_CHECK_HIP(hipMemsetAsync(qq, 0, qb, st));
-    // target rows 0..k (row k draws the bonus with u_res; rows < k draw nothing used), draft rows 0..k-1 (u_draft)
-    std::vector<double> ut(static_cast<size_t>(k) + 1, 0.0), ud(static_cast<size_t>(k), 0.0);
-    ut[static_cast<size_t>(k)] = u_res;
-    for (int i = 0; i < k; ++i) {
-        ut[static_cast<size_t>(i)] = u_res;   // a rejected row with no residual mass draws from p with u_res
-        ud[static_cast<size_t>(i)] = greedy ? 0.0 : u_draft[i];
-    }
+    GV_CHECK_HIP(hipMemcpyAsync(c.io, pin, io, hipMemcpyHostToDevice, st));
     const float Tn = greedy ? 0.0f : temperature;
-    const Nuclei np = carve(base, R, kMaxCand);
-    Nuclei nq = np;   // draft rows after the k + 1 target rows
-    nq.key += (k + 1) * np.cs;
-    nq.idx += (k + 1) * np.cs;
-    nq.e += (k + 1) * np.cs;
-    nq.sum += k + 1;
-    nq.kept += k + 1;
-    nq.u += k + 1;
-    nq.keep += k + 1;
-    nq.pos += k + 1;
-    nq.pick += k + 1;
-    nq.flag = np.flag;
-    if (nuclei(target, ld, k + 1, V, Tn, top_p, 0, 0, ut.data(), np, st) != 0) return -1;
-    if (nuclei(draft, ld, k, V, Tn, top_p, 0, 0, ud.data(), nq, st) != 0) return -1;
-    if (!greedy) GV_CHECK_HIP(hipMemcpyAsync(dacc, u_acc, static_cast<size_t>(k) * 4, hipMemcpyHostToDevice, st));
-    static int granted = 0;
-    const size_t lds = static_cast<size_t>(kMaxCand) * 8;
-    if (lds_grant(reinterpret_cast<const void *>(&textbook_kernel), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL(textbook_kernel, dim3(1), dim3(kSelThreads), lds, st, np.rows(0), nq.rows(0), k, greedy, dacc,
-                       u_res, qq, dout, dres);
+    const Rows rs = make_rows(target, k + 1, draft, ld, V);
+    if (nuclei(rs, R, Tn, top_p, 0, 0, c.ws, st) != 0) return -1;
+    hipLaunchKernelGGL(textbook_finish, dim3(greedy ? 1 : rs.S), dim3(kPass), 0, st, rs, c.ws, k, greedy, temperature,
+                       dacc, u_res, rsum, ddone, dout, dst);
     GV_CHECK_HIP(hipGetLastError());
-    int res = 0;
-    GV_CHECK_HIP(hipMemcpyAsync(&res, dres, 4, hipMemcpyDeviceToHost, st));
+    int32_t *hout = reinterpret_cast<int32_t *>(hacc + 33);
+    GV_CHECK_HIP(hipMemcpyAsync(hout, dout, 33 * 4, hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
-    GV_CHECK_HIP(hipMemcpy(out, dout, static_cast<size_t>(res) * 4, hipMemcpyDeviceToHost));
-    return res;
+    const int emitted = hout[32];
+    for (int i = 0; i < emitted; ++i) out[i] = hout[i];
+    return emitted;
 }
 
 }  // extern "C"

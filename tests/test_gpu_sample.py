@@ -154,3 +154,44 @@ def test_sample_and_match_presence_penalty_and_stops(gv, temp):
         assert list(got) == list(want) and gk == wk, (trial, list(got), list(want))
         for r in range(wk):   # the rows that were sampled carry the same penalized logits
             assert np.array_equal(glg[r].view(np.uint32), wlg[r].view(np.uint32))
+
+
+@pytest.mark.parametrize("top_p", [0.95, 1.0])
+def test_full_vocabulary_flat_rows(gv, top_p):
+    """T = 1 on N(0, 1) logits: the 0.95 nucleus holds most of the 151,936 tokens (no candidate limit)"""
+    x = _rows(71, 4, 1.0)
+    for rep in range(4):
+        u = _uniforms(710 + rep, 4)
+        got = gv.sample_rows(x, 1.0, top_p, 0, 0, u)
+        assert list(got) == [po.sample(x[r], 1.0, top_p, 0, 0, u[r]) for r in range(4)], rep
+
+
+def test_full_vocabulary_ties(gv):
+    """logits on a coarse grid: thousands of equal values at the top-p boundary and at the draws; ties are taken in
+    index order by both walks"""
+    x = np.round(_rows(72, 3, 1.0) * 4.0).astype(np.float32) / 4.0
+    for rep in range(6):
+        u = _uniforms(720 + rep, 3)
+        got = gv.sample_rows(x, 0.8, 0.9, 0, 0, u)
+        assert list(got) == [po.sample(x[r], 0.8, 0.9, 0, 0, u[r]) for r in range(3)], rep
+
+
+def test_textbook_rule_flat_and_tied_rows(gv):
+    """the textbook rule where the nuclei span most of the vocabulary and where logits tie, rejections forced at each
+    position in turn (the residual over the full vocabulary)"""
+    for flat, coarse in ((True, False), (False, True)):
+        sig = 1.0 if flat else 3.0
+        target = _rows(73, 5, sig)
+        draft = target[:4] + po.normal(74, 4 * V, 0.5).reshape(4, V)
+        if coarse:
+            target = np.round(target * 2.0).astype(np.float32) / 2.0
+            draft = np.round(draft * 2.0).astype(np.float32) / 2.0
+        rng = np.random.default_rng(75)
+        ud, ur = rng.random(4).astype(np.float32), np.float32(rng.random())
+        for first_reject in range(5):
+            ua = np.zeros(4, np.float32)
+            if first_reject < 4:
+                ua[first_reject] = np.float32(0.999999)
+            got = gv.accept_textbook(target, draft, 1.0, 0.95, False, ud, ua, ur)
+            want = po.accept_textbook(target, draft, 1.0, 0.95, False, ud, ua, ur)
+            assert list(got) == list(want), (flat, coarse, first_reject, list(got), list(want))
