@@ -27,6 +27,11 @@ class GvModelConfig(_c.Structure):
                 ("kv_int8", _c.c_int32)]
 
 
+class GvPackTensorInfo(_c.Structure):
+    _fields_ = [("type", _c.c_int32), ("rows", _c.c_int64), ("cols", _c.c_int64), ("file", _c.c_int32),
+                ("offset", _c.c_uint64), ("bytes", _c.c_uint64), ("global_", _c.c_float)]
+
+
 class GvStateInfo(_c.Structure):
     _fields_ = [("pack_print", _c.c_uint64), ("conv_id", _c.c_uint64), ("extra", _c.c_int32),
                 ("rope_delta", _c.c_int32), ("has_mtp", _c.c_int32), ("has_vision", _c.c_int32), ("hidden", _P),
@@ -86,6 +91,15 @@ SIGNATURES = {
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_model_layer": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
+    "gv_pack_open": (_P, [_c.c_char_p, _c.c_char_p, _c.c_int]),
+    "gv_pack_close": (None, [_P]),
+    "gv_pack_print": (_c.c_uint64, [_P]),
+    "gv_pack_model_config": (_c.c_int, [_P, _c.c_int, _c.c_int, _c.c_int, _c.POINTER(GvModelConfig)]),
+    "gv_pack_tensor": (_c.c_int, [_P, _c.c_char_p, _c.POINTER(GvPackTensorInfo)]),
+    "gv_pack_expert": (_c.c_int, [_P, _c.c_int, _c.c_int, _P, _P, _P]),
+    "gv_pack_tile8": (_c.c_int, [_P]),
+    "gv_q4_untile8": (_c.c_int, [_c.c_int64, _c.c_int64, _P, _P]),
+    "gv_model_load_pack": (_c.c_int, [_P, _P]),
     "gv_model_save_state": (_c.c_int, [_P, _c.c_char_p, _c.c_int, _c.POINTER(GvStateInfo)]),
     "gv_model_load_state": (_c.c_int, [_P, _c.c_char_p, _c.POINTER(GvStateInfo)]),
     "gv_sample_rows": (_c.c_int, [_P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int,
@@ -310,6 +324,60 @@ def accept_textbook(target, draft, temperature, top_p, greedy, u_draft=None, u_a
     return out[:rc].copy()
 
 
+class Pack:
+    """A geode-pack opened on the host (Pack::open, engine/src/pack.cpp:39-308): the manifest and its tables checked,
+    nothing read until a model loads it."""
+
+    DTYPES = {0: "f32", 1: "bf16", 2: "q2", 3: "q3", 4: "nvfp4", 5: "q8", 6: "q4", 8: "q4i"}
+
+    def __init__(self, directory):
+        err = _c.create_string_buffer(512)
+        self.h = _lib().gv_pack_open(os.fsencode(directory), err, 512)
+        if not self.h:
+            raise GeodeError(err.value.decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            _lib().gv_pack_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def print(self):
+        """FNV-1a of geode.json (the pack print a state file carries)"""
+        return _lib().gv_pack_print(self.h)
+
+    @property
+    def tile8(self):
+        return bool(_lib().gv_pack_tile8(self.h))
+
+    def model_config(self, max_ctx, max_rows=17, kv_int8=0):
+        c = GvModelConfig()
+        check(_lib().gv_pack_model_config(self.h, max_ctx, max_rows, kv_int8, _c.byref(c)), "gv_pack_model_config")
+        return {k: getattr(c, k) for k, _ in GvModelConfig._fields_}
+
+    def tensor(self, name):
+        t = GvPackTensorInfo()
+        check(_lib().gv_pack_tensor(self.h, name.encode(), _c.byref(t)), "gv_pack_tensor")
+        return {"type": self.DTYPES.get(t.type, "?"), "rows": t.rows, "cols": t.cols, "file": t.file,
+                "offset": t.offset, "bytes": t.bytes, "global": t.global_}
+
+    def expert(self, layer, e):
+        f, o, t = _c.c_int(0), _c.c_uint64(0), _c.c_int(0)
+        check(_lib().gv_pack_expert(self.h, layer, e, _c.byref(f), _c.byref(o), _c.byref(t)), "gv_pack_expert")
+        return f.value, o.value, self.DTYPES.get(t.value, "?")
+
+
+def q4_untile8(rows, cols, tiled):
+    """gv_q4_untile8: tile8 bytes (engine/src/kernels.cpp:971-991) back to the pack's rows"""
+    src = np.ascontiguousarray(tiled, np.uint8)
+    dst = np.empty_like(src)
+    check(_lib().gv_q4_untile8(rows, cols, src.ctypes.data_as(_P), dst.ctypes.data_as(_P)), "gv_q4_untile8")
+    return dst
+
+
 class VerifyModel:
     """A whole model on the device and the verify contract: verify(tokens, parents) then keep(kept, path), as
     Model::verify_n / verify_keep (engine/src/model.cpp:1483-1634)."""
@@ -451,6 +519,10 @@ class VerifyModel:
             raise StateError(STATE_ERRORS.get(rc, "io"), _lib().gv_last_error().decode())
         return {"conv_id": info.conv_id, "extra": info.extra, "rope_delta": info.rope_delta,
                 "hidden": hid if info.has_hidden else None}
+
+    def load_pack(self, pack):
+        """gv_model_load_pack: every tensor of an open Pack adopted (Model::bind, engine/src/model.cpp:95-202)"""
+        check(_lib().gv_model_load_pack(self.h, pack.h), "gv_model_load_pack")
 
     def moe_replay(self, reps=20):
         """mean ms of the last moe() block re-run on its device-staged inputs (device work only)"""

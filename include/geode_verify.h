@@ -212,6 +212,38 @@ int gv_model_layer(gv_model *m, int layer, const float *x_in, int n, const int32
  * return the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */
 int gv_model_moe_replay(gv_model *m, int reps, float *ms_per_block);
 
+/* ------------------------------------------------------------------ a geode-pack (F3)
+ * Pack::open (engine/src/pack.cpp:39-308): the manifest geode.json (format "geode-pack" v1, its files and their
+ * sizes, the config, the tensor table, the expert table) checked as the reference checks it, nothing read yet; the
+ * tensors are read from their files by gv_model_load_pack. Host calls (no device work) except that one. */
+typedef struct gv_pack gv_pack;
+gv_pack *gv_pack_open(const char *dir, char *err, int err_len);
+void gv_pack_close(gv_pack *p);
+/* FNV-1a 64 of geode.json's bytes (Model::fingerprint's pack print, engine/src/state.cpp:227-238): the pack_print a
+ * state file of this pack carries (gv_state_info) */
+uint64_t gv_pack_print(const gv_pack *p);
+/* The GPU model's config from the pack's (and the caller's context, rows and KV format). Fails for what the GPU
+ * model does not run: another architecture than qwen35moe, Gated DeltaNet layers, a shared expert of another width. */
+int gv_pack_model_config(const gv_pack *p, int max_ctx, int max_rows, int kv_int8, gv_model_config *out);
+typedef struct gv_pack_tensor_info {
+    int32_t type;      /* the reference's DType: 0 f32, 1 bf16, 2 q2, 3 q3, 4 nvfp4, 5 q8, 6 q4, 8 q4i (kernels.hpp:16) */
+    int64_t rows, cols;/* shape[0] and the product of the rest (one dimension: 1 x n) */
+    int32_t file;      /* index among the pack's files present */
+    uint64_t offset, bytes;
+    float global;
+} gv_pack_tensor_info;
+int gv_pack_tensor(const gv_pack *p, const char *name, gv_pack_tensor_info *out);
+/* Pack::expert (pack.cpp:317-328): where expert e of a layer (n_layers: the MTP layer's) is and its format */
+int gv_pack_expert(const gv_pack *p, int layer, int expert, int *file, uint64_t *offset, int *type);
+/* 1 when the pack's q4 experts are in the tile8 layout (geode.json formats.q4.layout) */
+int gv_pack_tile8(const gv_pack *p);
+/* tile8 (to_tile8, engine/src/kernels.cpp:971-991) back to the pack's rows, host memory, rows % 32, cols % 64 */
+int gv_q4_untile8(int64_t rows, int64_t cols, const uint8_t *src, uint8_t *dst);
+/* Every tensor of the pack adopted by a model created with gv_pack_model_config's config (Model::bind,
+ * engine/src/model.cpp:95-202: the norms, q | k | v, o, q / k norms, the router and shared gate, the shared expert,
+ * the routed experts with their scales, embed_tokens, norm, lm_head); the position becomes 0. */
+int gv_model_load_pack(gv_model *m, const gv_pack *p);
+
 /* ------------------------------------------------------------------ a conversation's state in a file (F4)
  * The reference's state file (engine/src/state.cpp:1-20): a 4096-byte header with an FNV-1a checksum, the fixed part
  * (gen at both ends), the KV cache in blocks of 256 positions [K, V][layer][256][n_kv_heads * hd] (fp16 or int8, then
@@ -249,7 +281,8 @@ int gv_model_load_state(gv_model *m, const char *path, gv_state_info *info);
 
 /* Sampler::sample (engine/src/sampler.cpp:16-50) of each row with its injected uniform u[r] in [0, 1) standing for
  * uniform_real_distribution<double>(0, kept): T <= 0 the first argmax; else the top_k candidates (else the top
- * `cap`, 1024 in the reference; cap 0 with top_p < 1: the whole vocabulary), ties to the lower index. rows <= 64. */
+ * `cap`, 1024 in the reference; top_k and cap at most 16384; both 0: the whole vocabulary, any top_p), ties to the lower
+ * index. rows <= 64, V <= 262,144. */
 int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float temperature, float top_p, int top_k,
                    int cap, const double *u, int32_t *out);
 /* Sample-and-match over a verified chain (engine/src/geode.cpp:318-374): batch = [tok, d1..d_{n-1}]; row i sampled

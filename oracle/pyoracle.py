@@ -127,6 +127,8 @@ def load_ref():
         "ref_matvec_bf16_multi": (None, [_P, _c.c_int64, _c.c_int64, _c.c_int, _P, _P]),
         "ref_rmsnorm": (None, [_P, _P, _P, _c.c_int, _c.c_float, _c.c_int]),
         "ref_sample_seeded": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_uint64, _c.c_int, _P]),
+        "ref_to_tile8": (None, [_c.c_int64, _c.c_int64, _P, _P]),
+        "ref_tile8_row": (None, [_P, _c.c_int64, _c.c_int64, _c.c_int64, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(r, name)

@@ -94,4 +94,18 @@ __attribute__((visibility("default"))) void ref_sample_seeded(const float *logit
     for (int d = 0; d < draws; ++d) out[d] = s.sample(logits, n, p);
 }
 
+// to_tile8 (kernels.cpp:971-991) of q4 pack rows, and row r of such a tiled matrix read back by the reference's own
+// quad_row (kernels.cpp:1143)
+__attribute__((visibility("default"))) void ref_to_tile8(int64_t rows, int64_t cols, const uint8_t *src, uint8_t *dst) {
+    to_tile8(DType::Q4, rows, cols, src, dst);
+}
+
+__attribute__((visibility("default"))) void ref_tile8_row(const uint8_t *data, int64_t rows, int64_t cols, int64_t r,
+                                                          uint8_t *out) {
+    QView v = q4_view(data, rows, cols, 1.0f);
+    v.quad = true;
+    v.tile8 = true;
+    quad_row(v, r, out);
+}
+
 }  // extern "C"

@@ -94,6 +94,16 @@ def main():
         draws.append(o)
     out["sample_settings"] = np.array(settings, np.float64)
     out["sample_draws"] = np.stack(draws)
+    # tile8 (the reference's expert layout of q4 packs): two matrices of pack rows, their tiled bytes, and row 37 of
+    # the second read back by the reference's own quad_row
+    for name, (rows, cols, seed) in (("tile8_a", (64, 128, 11)), ("tile8_b", (96, 192, 12))):
+        wq, _ = po.q4_pack(po.normal(seed, rows * cols, 0.02).reshape(rows, cols))
+        tiled = np.empty_like(wq)
+        ref.ref_to_tile8(rows, cols, P(wq), P(tiled))
+        out[name + "_rows"], out[name + "_tiled"] = wq, tiled
+    back = np.empty(192 // 16 * 9, np.uint8)
+    ref.ref_tile8_row(P(out["tile8_b_tiled"]), 96, 192, 37, P(back))
+    out["tile8_b_row37"] = back
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_vectors.npz")
     np.savez_compressed(path, **out)
     print("wrote", path, os.path.getsize(path), "bytes")

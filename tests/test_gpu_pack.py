@@ -1,0 +1,56 @@
+"""A geode-pack loaded into the GPU model (gv_model_load_pack) against the same tensors adopted directly: the next
+verify is bit-identical (chain and tree), with the experts in rows and in the tile8 layout; a state saved under the
+pack's print loads only with it."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+from model_helpers import SMALL, SMALL_ROUTER_SIGMA, adopt_oracle_model, tree_parents
+from pack_writer import write_pack
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gv():
+    import geode_amd
+
+    geode_amd.init(0)
+    return geode_amd
+
+
+@pytest.fixture(scope="module")
+def om():
+    return po.Model(SMALL, seed=21, router_sigma=SMALL_ROUTER_SIGMA, ctx=0)
+
+
+@pytest.mark.parametrize("tile8", [False, True], ids=["rows", "tile8"])
+def test_pack_loads_as_the_direct_adoption(gv, om, tmp_path, tile8):
+    write_pack(om, str(tmp_path), tile8=tile8)
+    pack = gv.Pack(str(tmp_path))
+    cfg = pack.model_config(max_ctx=SMALL["max_ctx"], max_rows=SMALL["max_rows"])
+    for k in SMALL:
+        assert cfg[k] == (np.float32(SMALL[k]) if isinstance(SMALL[k], float) else SMALL[k]), k
+    a = gv.VerifyModel(SMALL)
+    adopt_oracle_model(a, om, 0)
+    b = gv.VerifyModel(cfg)
+    b.load_pack(pack)
+    assert b.position == 0
+    toks = np.array([3, 77, 410, 9, 200], np.int32)
+    np.testing.assert_array_equal(b.verify(toks), a.verify(toks))
+    par = tree_parents((4, 3))
+    ttoks = (np.arange(par.size) * 37 % SMALL["vocab"]).astype(np.int32)
+    np.testing.assert_array_equal(b.verify(ttoks, par), a.verify(ttoks, par))
+
+
+def test_state_carries_the_pack_print(gv, om, tmp_path):
+    write_pack(om, str(tmp_path / "p"))
+    pack = gv.Pack(str(tmp_path / "p"))
+    m = gv.VerifyModel(pack.model_config(max_ctx=SMALL["max_ctx"]))
+    m.load_pack(pack)
+    m.verify(np.array([1, 2, 3], np.int32))
+    path = str(tmp_path / "s.geode")
+    m.save_state(path, pack_print=pack.print)
+    with pytest.raises(gv.StateError, match="another model"):
+        m.load_state(path, pack_print=pack.print ^ 1)
+    assert m.load_state(path, pack_print=pack.print)["conv_id"] == 0 and m.position == 3

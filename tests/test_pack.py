@@ -1,0 +1,150 @@
+"""The geode-pack reader (gv_pack_*, host calls: no GPU) against the manifests and files of tests/pack_writer.py: the
+tensor table as Python's own json reads it, the expert table, the refusals of Pack::open (engine/src/pack.cpp:39-308)
+one planted damage each, the pack print (FNV-1a of geode.json from the reference's start), and the tile8 layout
+against the reference's own to_tile8 (golden fixture) in both directions."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+import state_format as sf
+from pack_writer import to_tile8, write_pack
+
+CFG = dict(hidden=128, vocab=256, n_layers=2, n_experts=8, top_k=2, moe_ff=64, shared_ff=64, n_heads=4, n_kv_heads=2,
+           head_dim=32, rope_dim=16, rope_theta=1e4, eps=1e-6, max_ctx=96)
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_vectors.npz")
+
+
+@pytest.fixture(scope="module")
+def gv():
+    import geode_amd
+
+    return geode_amd
+
+
+@pytest.fixture(scope="module")
+def om():
+    return po.Model(CFG, seed=5, ctx=0)
+
+
+@pytest.mark.parametrize("name", ["tile8_a", "tile8_b"])
+def test_tile8_against_the_reference(gv, name):
+    g = np.load(GOLDEN)
+    rows, tiled = g[name + "_rows"], g[name + "_tiled"]
+    r, c = rows.shape[0], rows.shape[1] // 9 * 16
+    assert np.array_equal(to_tile8(r, c, rows), tiled)                    # the test's writer = the reference's
+    assert np.array_equal(gv.q4_untile8(r, c, tiled).reshape(rows.shape), rows)   # the library's inverse
+    if name == "tile8_b":
+        assert np.array_equal(g["tile8_b_row37"], rows[37])
+
+
+def test_tile8_round_trip_random_bytes(gv):
+    rng = np.random.default_rng(3)
+    rows, cols = 64, 256
+    m = rng.integers(0, 256, (rows, cols // 16 * 9), dtype=np.uint8)
+    assert np.array_equal(gv.q4_untile8(rows, cols, to_tile8(rows, cols, m)).reshape(m.shape), m)
+
+
+@pytest.mark.parametrize("tile8", [False, True])
+def test_open_reads_the_tables(gv, om, tmp_path, tile8):
+    m = write_pack(om, str(tmp_path), tile8=tile8)
+    p = gv.Pack(str(tmp_path))
+    assert p.tile8 == tile8
+    text = open(tmp_path / "geode.json", "rb").read()
+    assert p.print == sf.fnv1a(text)
+    files = [f["name"] for f in m["files"]]
+    for name, t in m["tensors"].items():
+        got = p.tensor(name)
+        shape = t["shape"]
+        rows, cols = (1, shape[0]) if len(shape) == 1 else (shape[0], int(np.prod(shape[1:])))
+        assert (got["type"], got["rows"], got["cols"], got["file"], got["offset"]) == \
+               (t["type"], rows, cols, files.index(t["file"]), t["offset"]), name
+        assert got["global"] == np.float32(t.get("global", 1.0))
+    for l, layer in enumerate(m["experts"]["layers"]):
+        for e in (0, 3, CFG["n_experts"] - 1):
+            assert p.expert(l, e) == (files.index("experts.bin"), layer["offset"] + e * layer["stride"], "q4")
+    cfg = p.model_config(max_ctx=96, max_rows=17)
+    for k in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff", "n_heads", "n_kv_heads",
+              "head_dim", "rope_dim"):
+        assert cfg[k] == CFG[k], k
+    assert cfg["rope_theta"] == np.float32(CFG["rope_theta"]) and cfg["eps"] == np.float32(CFG["eps"])
+
+
+def _damage(what):
+    def mutate(m):
+        if what == "format":
+            m["format"] = "other"
+        elif what == "version":
+            m["version"] = 2
+        elif what == "arch":
+            m["arch"] = "llama"
+        elif what == "size":
+            m["files"][0]["size"] += 1
+        elif what == "layers":
+            m["config"]["layer_types"] = m["config"]["layer_types"][:1]
+        elif what == "geometry":
+            m["config"]["hidden_size"] = 130
+        elif what == "type":
+            m["tensors"]["norm.weight"]["type"] = "f64"
+        elif what == "past_end":
+            m["tensors"]["lm_head.weight"]["offset"] = m["files"][0]["size"] - 8
+        elif what == "negative":
+            m["tensors"]["lm_head.weight"]["offset"] = -1
+        elif what == "cols":
+            m["tensors"]["lm_head.weight"]["shape"] = [256, 120]
+        elif what == "unlisted":
+            m["tensors"]["norm.weight"]["file"] = "other.bin"
+        elif what == "no_dense":
+            for t in m["tensors"].values():
+                t["file"] = "experts.bin"
+        elif what == "embed":
+            del m["tensors"]["embed_tokens.weight"]
+        elif what == "experts":
+            m["experts"]["layers"] = m["experts"]["layers"][:1]
+        elif what == "scales":
+            del m["tensors"]["layers.1.mlp.experts.scales"]
+        elif what == "expert_count":
+            e = m["experts"]["layers"][0]
+            m["experts"]["layers"][0] = {"file": e["file"], "offsets": [e["offset"]] * 3, "formats": ["q4"] * 3}
+    return mutate
+
+
+@pytest.mark.parametrize("what,message", [
+    ("format", "not a geode-pack v1"), ("version", "not a geode-pack v1"), ("arch", "unknown architecture"),
+    ("size", "bytes, expected"), ("layers", "layer_types"), ("geometry", "inconsistent model geometry"),
+    ("type", "unknown type"), ("past_end", "runs past the end"), ("negative", "out of range"),
+    ("cols", "not a multiple of 16"), ("unlisted", "does not list"), ("no_dense", "no tensors in dense.bin"),
+    ("embed", "embed_tokens"), ("experts", "does not cover every layer"), ("scales", "no expert scales"),
+    ("expert_count", "wrong number of experts")])
+def test_open_refuses(gv, om, tmp_path, what, message):
+    write_pack(om, str(tmp_path), mutate=_damage(what))
+    with pytest.raises(gv.GeodeError, match=message):
+        gv.Pack(str(tmp_path))
+
+
+def test_json_reader_against_pythons(gv, om, tmp_path):
+    """a manifest with escapes, unicode (\\u and raw UTF-8, a surrogate pair), exponents and odd spacing: the names and
+    numbers the library reads are those Python's json reads"""
+    m = write_pack(om, str(tmp_path))
+    odd = {"läyer \"x\"\\\t€\U0001F600": dict(m["tensors"]["norm.weight"]),
+           "plain": dict(m["tensors"]["norm.weight"], global_=1)}
+    odd["plain"]["global"] = 2.5e-3
+    m["tensors"].update(odd)
+    text = json.dumps(m, ensure_ascii=True, indent=None, separators=(" ,", " :  "))
+    assert '"global" :  0.0025' in text
+    text = text.replace('"global" :  0.0025', '"global":2.5E-3')
+    with open(tmp_path / "geode.json", "w") as f:
+        f.write(text)
+    p = gv.Pack(str(tmp_path))
+    got = p.tensor("läyer \"x\"\\\t€\U0001F600")
+    assert got["offset"] == m["tensors"]["norm.weight"]["offset"]
+    assert p.tensor("plain")["global"] == np.float32(2.5e-3)
+
+
+def test_gated_deltanet_layers_are_refused_by_the_gpu_config(gv, om, tmp_path):
+    write_pack(om, str(tmp_path), extra_config={"layer_types": ["linear_attention", "full_attention"]})
+    p = gv.Pack(str(tmp_path))
+    with pytest.raises(gv.GeodeError, match="Gated DeltaNet"):
+        p.model_config(96)
