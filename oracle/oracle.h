@@ -85,6 +85,10 @@ typedef struct {
     int max_ctx;
     int attn_block;   // positions per attention block (model.hpp:458, kAttnBlock = 1024)
     int kv_int8;      // 1: the KV cache in int8, a scale a (position, KV head) (ModelOptions::kv_int8); 0: fp16
+    // Gated DeltaNet layers (model.cpp:3497-3688; 0 heads: none): key / value heads and dims, the conv's width, and
+    // per layer 1 for a GDN layer (else gated attention)
+    int gdn_k_heads, gdn_v_heads, gdn_k_dim, gdn_v_dim, conv_kernel;
+    unsigned char gdn_layers[256];
 } orc_config;
 
 // tensor kinds (shared numbering with include/geode_verify.h)
@@ -93,8 +97,21 @@ enum {
     ORC_V = 7, ORC_O = 8, ORC_Q_NORM = 9, ORC_K_NORM = 10, ORC_ROUTER = 11, ORC_SHARED_GATE = 12, ORC_EXPERT = 13,
     ORC_SH_GATE = 14, ORC_SH_UP = 15, ORC_SH_DOWN = 16, ORC_KV = 17,
     ORC_KV8 = 18,   // int8 KV: [K, V][max_ctx][nkv * hd] bytes
-    ORC_KVS = 19    // int8 KV: [K, V][max_ctx][nkv] float scales
+    ORC_KVS = 19,   // int8 KV: [K, V][max_ctx][nkv] float scales
+    // a GDN layer's (model.cpp:129-138): in_proj_qkv q4 [2 kd + vd][H], in_proj_z q4 [vd][H], out_proj q4 [H][vd],
+    // in_proj_a / in_proj_b bf16 [nv][H], A_log f32 [nv], dt_bias f32 [nv], conv1d f32 [2 kd + vd][K], norm f32 [dv]
+    ORC_GDN_QKV = 20, ORC_GDN_Z = 21, ORC_GDN_OUT = 22, ORC_GDN_A = 23, ORC_GDN_B = 24, ORC_GDN_ALOG = 25,
+    ORC_GDN_DTB = 26, ORC_GDN_CONV = 27, ORC_GDN_NORM = 28,
+    ORC_GDN_CONV_ST = 29,   // the conv's state: [2 kd + vd][K - 1], the last K - 1 inputs oldest first
+    ORC_GDN_S = 30          // the recurrent state: [nv][dk][dv]
 };
+
+// fast_exp (kernels.hpp:142-163: Cephes' expf, the reduction by ln 2 in two parts and a degree-6 polynomial)
+float orc_fast_exp(float x);
+// One token of the gated delta rule on one value head (model.cpp:3499-3524): S [dk][dv] in place, S *= decay,
+// delta = beta (v - S^T k), S += k delta^T, out = S^T q
+void orc_gdn_step(float *S, int dk, int dv, const float *q, const float *k, const float *v, float decay, float beta,
+                  float *out);
 
 typedef struct orc_model orc_model;
 // quant_kv_row (model.cpp:3766-3774): a KV head's row to int8, scale = amax / 127, q = clamp(nearbyint(x * (127 /

@@ -116,6 +116,49 @@ void moe_layer(const orc_moe_weights &w, int n, const float *h, const float *rou
     if (wts_out) std::copy(wts.begin(), wts.end(), wts_out);
 }
 
+// ---------------------------------------------------------------- Gated DeltaNet (model.cpp:3497-3688)
+// fast_exp (kernels.hpp:142-163): Cephes' expf (the reduction by ln 2 in two parts, a degree-6 polynomial, 2^n by
+// the exponent's bits), within 2 ulp; below -87 it is e^-87
+float fast_exp(float x) {
+    x = std::fmin(std::fmax(x, -87.0f), 88.0f);
+    const float n = std::floor(x * 1.44269504088896341f + 0.5f);
+    float r = x - n * 0.693359375f;
+    r = r + n * 2.12194440e-4f;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = p * r * r + r + 1.0f;
+    uint32_t bits;
+    std::memcpy(&bits, &p, 4);
+    bits += static_cast<uint32_t>(static_cast<int32_t>(n)) << 23;
+    std::memcpy(&p, &bits, 4);
+    return p;
+}
+float silu_fast(float x) { return x / (1.0f + fast_exp(-x)); }   // kernels.hpp:165
+float softplus(float x) { return x > 20.0f ? x : std::log1p(std::exp(x)); }   // kernels.hpp:168
+
+// one token of the delta rule on one head's state S [dk][dv] (the generic loop of model.cpp:3602-3627): column j
+// sums over the rows in order
+void delta_step(float *S, int dk, int dv, const float *q, const float *k, const float *v, float decay, float beta,
+                float *out) {
+    std::vector<float> mem(static_cast<size_t>(dv), 0.0f), o(static_cast<size_t>(dv), 0.0f);
+    for (int i = 0; i < dk; ++i)
+        for (int j = 0; j < dv; ++j) {
+            S[i * dv + j] *= decay;
+            mem[static_cast<size_t>(j)] += S[i * dv + j] * k[i];
+        }
+    for (int j = 0; j < dv; ++j) mem[static_cast<size_t>(j)] = (v[j] - mem[static_cast<size_t>(j)]) * beta;
+    for (int i = 0; i < dk; ++i)
+        for (int j = 0; j < dv; ++j) {
+            S[i * dv + j] += k[i] * mem[static_cast<size_t>(j)];
+            o[static_cast<size_t>(j)] += S[i * dv + j] * q[i];
+        }
+    std::copy(o.begin(), o.end(), out);
+}
+
 // ---------------------------------------------------------------- the model
 struct Layer {
     std::vector<float> in_norm, post_norm, q_norm, k_norm;
@@ -125,6 +168,14 @@ struct Layer {
     std::vector<uint16_t> router, shared_gate, kv;   // kv: [2][max_ctx][nkv * hd] fp16
     std::vector<int8_t> kv8;                         // int8 KV: [2][max_ctx][nkv * hd]
     std::vector<float> kvs;                          // int8 KV: [2][max_ctx][nkv] scales
+    // a Gated DeltaNet layer (model.cpp:129-138) instead of the attention
+    bool gdn = false;
+    std::vector<uint8_t> gqkv, gz, gout;             // q4 [2 kd + vd][H], [vd][H], [H][vd]
+    float g_qkv = 1, g_z = 1, g_out = 1;
+    std::vector<uint16_t> ga, gb;                    // bf16 [nv][H]
+    std::vector<float> A_log, dt_bias, conv_w, gnorm;   // [nv], [nv], [2 kd + vd][K], [dv]
+    std::vector<float> conv_st, S;                   // [2 kd + vd][K - 1], [nv][dk][dv]
+    std::vector<float> conv_bk, S_bk;                // the last verify's rows' states (verify_keep takes them back)
 };
 
 }  // namespace orc
@@ -333,6 +384,91 @@ orc_moe_weights moe_view(const orc_model &m, const Layer &L) {
     return w;
 }
 
+// A Gated DeltaNet layer on n rows h (model.cpp:3526-3688): the projections (the int8 path in mode 0, model.cpp:
+// 3540-3547), the bf16 a / b rows, the causal conv over the last K inputs + silu (:3558-3584), q and k L2-normalised
+// per key head, q by 1/sqrt(dk) (:3586-3603), beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt_bias))
+// (:3605-3612), the delta rule per value head (:3614-3666), the gated RMSNorm o / rms(o) w silu(z) (:3670-3682), the
+// output projection into mix. A row's states start from its parent's (parents null: the row before; the first row:
+// the layer's), and every row's states are kept (conv_bk, S_bk): a chain ends with its last row's in the layer,
+// verify_keep takes back those of the last kept row.
+void gdn_layer(const orc_model &m, Layer &L, int n, const float *h, const int32_t *parents, int mode, float *mix) {
+    const auto &c = m.c;
+    const int H = c.hidden, nk = c.gdn_k_heads, nv = c.gdn_v_heads, dk = c.gdn_k_dim, dv = c.gdn_v_dim, K = c.conv_kernel;
+    const int kd = nk * dk, vd = nv * dv, conv_dim = 2 * kd + vd, rep = nv / nk;
+    const size_t cs_n = static_cast<size_t>(conv_dim) * (K - 1), s_n = static_cast<size_t>(nv) * dk * dv;
+    std::vector<float> proj(static_cast<size_t>(n) * conv_dim), z(static_cast<size_t>(n) * vd), a(static_cast<size_t>(n) * nv),
+        b(static_cast<size_t>(n) * nv), core(static_cast<size_t>(n) * vd);
+    const auto hs = crow_ptrs(h, n, static_cast<size_t>(H));
+    {
+        auto ps = row_ptrs(proj.data(), n, static_cast<size_t>(conv_dim));
+        auto zs = row_ptrs(z.data(), n, static_cast<size_t>(vd));
+        matmul(L.gqkv.data(), conv_dim, H, L.g_qkv, n, hs.data(), ps.data(), mode);
+        matmul(L.gz.data(), vd, H, L.g_z, n, hs.data(), zs.data(), mode);
+        auto as = row_ptrs(a.data(), n, static_cast<size_t>(nv));
+        auto bs = row_ptrs(b.data(), n, static_cast<size_t>(nv));
+        bf16_rows(L.ga.data(), H, n, hs.data(), as.data(), 0, nv);
+        bf16_rows(L.gb.data(), H, n, hs.data(), bs.data(), 0, nv);
+    }
+    L.conv_bk.assign(static_cast<size_t>(n) * cs_n, 0.0f);
+    L.S_bk.assign(static_cast<size_t>(n) * s_n, 0.0f);
+    const float qscale = 1.0f / std::sqrt(static_cast<float>(dk));
+    for (int t = 0; t < n; ++t) {
+        const int parent = parents ? parents[t] : t - 1;
+        // the conv: the parent's last K - 1 inputs, then this row's; the new state is the last K - 1 of them
+        const float *cin = parent < 0 ? L.conv_st.data() : L.conv_bk.data() + static_cast<size_t>(parent) * cs_n;
+        float *cout = L.conv_bk.data() + static_cast<size_t>(t) * cs_n;
+        float *row = proj.data() + static_cast<size_t>(t) * conv_dim;
+        for (int ch = 0; ch < conv_dim; ++ch) {
+            const float *w = L.conv_w.data() + static_cast<size_t>(ch) * K;
+            const float *st = cin + static_cast<size_t>(ch) * (K - 1);
+            float *so = cout + static_cast<size_t>(ch) * (K - 1);
+            const float in = row[ch];
+            float acc = 0.0f;
+            for (int k = 0; k < K - 1; ++k) acc += w[k] * st[k];
+            acc += w[K - 1] * in;
+            for (int k = 0; k + 1 < K - 1; ++k) so[k] = st[k + 1];
+            if (K > 1) so[K - 2] = in;
+            row[ch] = silu_fast(acc);
+        }
+        for (int kh = 0; kh < nk; ++kh) {   // q, k: L2-normalised, q scaled
+            float *q = row + kh * dk, *k = row + kd + kh * dk;
+            float sq = 0.0f, sk = 0.0f;
+            for (int j = 0; j < dk; ++j) {
+                sq += q[j] * q[j];
+                sk += k[j] * k[j];
+            }
+            const float iq = 1.0f / std::sqrt(sq + 1e-6f), ik = 1.0f / std::sqrt(sk + 1e-6f);
+            for (int j = 0; j < dk; ++j) {
+                q[j] = q[j] * iq * qscale;
+                k[j] = k[j] * ik;
+            }
+        }
+        const float *sin = parent < 0 ? L.S.data() : L.S_bk.data() + static_cast<size_t>(parent) * s_n;
+        float *sout = L.S_bk.data() + static_cast<size_t>(t) * s_n;
+        std::copy(sin, sin + s_n, sout);
+        for (int vh = 0; vh < nv; ++vh) {
+            const int kh = vh / rep;
+            const float beta = sigmoid(b[static_cast<size_t>(t) * nv + vh]);
+            const float decay = std::exp(-std::exp(L.A_log[static_cast<size_t>(vh)]) *
+                                         softplus(a[static_cast<size_t>(t) * nv + vh] + L.dt_bias[static_cast<size_t>(vh)]));
+            float *o = core.data() + static_cast<size_t>(t) * vd + static_cast<size_t>(vh) * dv;
+            delta_step(sout + static_cast<size_t>(vh) * dk * dv, dk, dv, row + kh * dk, row + kd + kh * dk,
+                       row + 2 * kd + vh * dv, decay, beta, o);
+            float ss = 0.0f;   // the gated RMSNorm of the head's output
+            for (int j = 0; j < dv; ++j) ss += o[j] * o[j];
+            const float inv = 1.0f / std::sqrt(ss / static_cast<float>(dv) + c.eps);
+            const float *zz = z.data() + static_cast<size_t>(t) * vd + static_cast<size_t>(vh) * dv;
+            for (int j = 0; j < dv; ++j) o[j] = o[j] * inv * L.gnorm[static_cast<size_t>(j)] * silu_fast(zz[j]);
+        }
+    }
+    // (the chain's end: the last row's states; a tree's keep takes back the right ones)
+    std::copy(L.conv_bk.end() - static_cast<ptrdiff_t>(cs_n), L.conv_bk.end(), L.conv_st.begin());
+    std::copy(L.S_bk.end() - static_cast<ptrdiff_t>(s_n), L.S_bk.end(), L.S.begin());
+    const auto cr = crow_ptrs(core.data(), n, static_cast<size_t>(vd));
+    auto ms = row_ptrs(mix, n, static_cast<size_t>(H));
+    matmul(L.gout.data(), H, vd, L.g_out, n, cr.data(), ms.data(), mode);
+}
+
 uint64_t tensor_seed(uint64_t seed, int kind, int layer, int expert) {
     return orc_hash(seed, (static_cast<uint64_t>(kind) << 48) | (static_cast<uint64_t>(layer) << 24) |
                               static_cast<uint64_t>(expert));
@@ -407,6 +543,13 @@ orc_model *orc_model_create(const orc_config *cfg) {
 
 void orc_model_free(orc_model *m) { delete m; }
 
+float orc_fast_exp(float x) { return orc::fast_exp(x); }
+
+void orc_gdn_step(float *S, int dk, int dv, const float *q, const float *k, const float *v, float decay, float beta,
+                  float *out) {
+    orc::delta_step(S, dk, dv, q, k, v, decay, beta, out);
+}
+
 void orc_quant_kv_row(const float *x, int n, int8_t *q, float *scale) { orc::quant_kv_row(x, n, q, *scale); }
 
 void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma, int ctx, int fast) {
@@ -440,6 +583,27 @@ void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma
             L.expert_globals[static_cast<size_t>(2 * e + 1)] =
                 fill_q4(tmp, H, F, tensor_seed(seed, ORC_EXPERT, l, 2 * e + 1), sigma, fast);
             std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e + gu));
+        }
+        L.gdn = c.gdn_v_heads > 0 && c.gdn_layers[l] != 0;
+        if (L.gdn) {   // the GDN layer's weights, then (a context) its states
+            const int nk = c.gdn_k_heads, nv = c.gdn_v_heads, dk = c.gdn_k_dim, dv = c.gdn_v_dim, K = c.conv_kernel;
+            const int kd = nk * dk, vd = nv * dv, conv_dim = 2 * kd + vd;
+            L.g_qkv = fill_q4(L.gqkv, conv_dim, H, tensor_seed(seed, ORC_GDN_QKV, l, 0), sigma, fast);
+            L.g_z = fill_q4(L.gz, vd, H, tensor_seed(seed, ORC_GDN_Z, l, 0), sigma, fast);
+            L.g_out = fill_q4(L.gout, H, vd, tensor_seed(seed, ORC_GDN_OUT, l, 0), sigma, fast);
+            fill_bf16(L.ga, static_cast<size_t>(nv) * H, tensor_seed(seed, ORC_GDN_A, l, 0), router_sigma);
+            fill_bf16(L.gb, static_cast<size_t>(nv) * H, tensor_seed(seed, ORC_GDN_B, l, 0), router_sigma);
+            fill_f32(L.A_log, static_cast<size_t>(nv), tensor_seed(seed, ORC_GDN_ALOG, l, 0), 0.5f);
+            fill_f32(L.dt_bias, static_cast<size_t>(nv), tensor_seed(seed, ORC_GDN_DTB, l, 0), 0.5f);
+            fill_f32(L.conv_w, static_cast<size_t>(conv_dim) * K, tensor_seed(seed, ORC_GDN_CONV, l, 0), 0.3f);
+            fill_f32(L.gnorm, static_cast<size_t>(dv), tensor_seed(seed, ORC_GDN_NORM, l, 0), 0.02f);
+            for (float &g : L.gnorm) g += 1.0f;
+            L.conv_st.assign(static_cast<size_t>(conv_dim) * (K - 1), 0.0f);
+            L.S.assign(static_cast<size_t>(nv) * dk * dv, 0.0f);
+            if (ctx > 0) {   // a conversation's states: the conv's last inputs N(0, 1), the recurrent state N(0, 0.05)
+                fill_f32(L.conv_st, L.conv_st.size(), tensor_seed(seed, ORC_GDN_CONV_ST, l, 0), 1.0f);
+                fill_f32(L.S, L.S.size(), tensor_seed(seed, ORC_GDN_S, l, 0), 0.05f);
+            }
         }
         L.gsg = fill_q4(L.sh_gate, SF, H, tensor_seed(seed, ORC_SH_GATE, l, 0), sigma, fast);
         L.gsu = fill_q4(L.sh_up, SF, H, tensor_seed(seed, ORC_SH_UP, l, 0), sigma, fast);
@@ -501,6 +665,17 @@ uint8_t *orc_model_tensor(orc_model *m, int kind, int layer, int expert, int64_t
     case ORC_KV: return ret(L.kv, 0, 0);
     case ORC_KV8: return ret(L.kv8, 0, 0);
     case ORC_KVS: return ret(L.kvs, 0, 0);
+    case ORC_GDN_QKV: return ret(L.gqkv, L.g_qkv, 0);
+    case ORC_GDN_Z: return ret(L.gz, L.g_z, 0);
+    case ORC_GDN_OUT: return ret(L.gout, L.g_out, 0);
+    case ORC_GDN_A: return ret(L.ga, 0, 0);
+    case ORC_GDN_B: return ret(L.gb, 0, 0);
+    case ORC_GDN_ALOG: return ret(L.A_log, 0, 0);
+    case ORC_GDN_DTB: return ret(L.dt_bias, 0, 0);
+    case ORC_GDN_CONV: return ret(L.conv_w, 0, 0);
+    case ORC_GDN_NORM: return ret(L.gnorm, 0, 0);
+    case ORC_GDN_CONV_ST: return ret(L.conv_st, 0, 0);
+    case ORC_GDN_S: return ret(L.S, 0, 0);
     case ORC_EXPERT: {
         if (expert < 0 || expert >= m->c.n_experts) return nullptr;
         const size_t eb = expert_block_bytes(m->c);
@@ -549,7 +724,8 @@ int orc_model_verify_trace(orc_model *m, const int32_t *tokens, int n, const int
         for (int t = 0; t < n; ++t)
             rmsnorm(x.data() + static_cast<size_t>(t) * H, L.in_norm.data(), h.data() + static_cast<size_t>(t) * H, H,
                     c.eps, true);
-        attention(*m, L, n, h.data(), m->pos, parents, mode, mix.data());
+        if (L.gdn) gdn_layer(*m, L, n, h.data(), parents, mode, mix.data());
+        else attention(*m, L, n, h.data(), m->pos, parents, mode, mix.data());
         for (int t = 0; t < n; ++t) {
             float *xr = x.data() + static_cast<size_t>(t) * H;
             const float *mr = mix.data() + static_cast<size_t>(t) * H;
@@ -606,6 +782,16 @@ int orc_model_keep(orc_model *m, int kept, const int32_t *path) {
                         std::memmove(base + to * kv_row, base + from * kv_row, kv_row * 2);
                     }
                 }
+    }
+    // the Gated DeltaNet layers' states as after the last kept row (model.cpp:1617-1633)
+    const int last = path ? path[kept - 1] : kept - 1;
+    for (auto &L : m->layers) {
+        if (!L.gdn) continue;
+        const size_t cs_n = L.conv_st.size(), s_n = L.S.size();
+        std::copy(L.conv_bk.begin() + static_cast<ptrdiff_t>(last * cs_n), L.conv_bk.begin() + static_cast<ptrdiff_t>((last + 1) * cs_n),
+                  L.conv_st.begin());
+        std::copy(L.S_bk.begin() + static_cast<ptrdiff_t>(last * s_n), L.S_bk.begin() + static_cast<ptrdiff_t>((last + 1) * s_n),
+                  L.S.begin());
     }
     m->pos = m->last_pos + kept;
     return 0;

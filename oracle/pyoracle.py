@@ -28,7 +28,9 @@ class Config(_c.Structure):
     _fields_ = [(n, _c.c_int) for n in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff",
                                         "n_heads", "n_kv_heads", "head_dim", "rope_dim")] + \
                [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int), ("attn_block", _c.c_int),
-                ("kv_int8", _c.c_int)]
+                ("kv_int8", _c.c_int)] + \
+               [(n, _c.c_int) for n in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")] + \
+               [("gdn_layers", _c.c_ubyte * 256)]
 
 
 class MoeWeights(_c.Structure):
@@ -40,6 +42,7 @@ class MoeWeights(_c.Structure):
 # tensor kinds, numbered as in oracle.h and include/geode_verify.h
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, Q, K, V, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, SH_GATE, \
     SH_UP, SH_DOWN, KV, KV8, KVS = range(20)
+GDN_QKV, GDN_Z, GDN_OUT, GDN_A, GDN_B, GDN_ALOG, GDN_DTB, GDN_CONV, GDN_NORM, GDN_CONV_ST, GDN_S = range(20, 31)
 
 
 class StateInfo(_c.Structure):
@@ -97,6 +100,8 @@ def _load():
                                            _c.c_float, _P]),
         "orc_nucleus_probs": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _P]),
         "orc_fnv1a": (_c.c_uint64, [_P, _c.c_size_t, _c.c_uint64]),
+        "orc_fast_exp": (_c.c_float, [_c.c_float]),
+        "orc_gdn_step": (None, [_P, _c.c_int, _c.c_int, _P, _P, _P, _c.c_float, _c.c_float, _P]),
         "orc_model_config": (_P, [_P]),
         "orc_state_save": (_c.c_int, [_P, _c.c_char_p, _c.c_int, _c.POINTER(StateInfo), _c.c_char_p, _c.c_int]),
         "orc_state_load": (_c.c_int, [_P, _c.c_char_p, _c.POINTER(StateInfo), _c.c_char_p, _c.c_int]),
@@ -329,7 +334,9 @@ class Model:
 
     def __init__(self, cfg: dict, seed=1, sigma=0.02, router_sigma=0.0221, ctx=0, fast=False):
         self.cfg = dict(cfg)
-        c = Config(**{k: cfg[k] for k, _ in Config._fields_ if k in cfg})
+        c = Config(**{k: cfg[k] for k, _ in Config._fields_ if k in cfg and k != "gdn_layers"})
+        for l, g in enumerate(cfg.get("gdn_layers", ())):
+            c.gdn_layers[l] = 1 if g else 0
         if "attn_block" not in cfg:
             c.attn_block = 1024
         self._c = c
@@ -412,3 +419,17 @@ class Model:
         a, b = _c.c_double(0), _c.c_double(0)
         lib.orc_model_last_times(self.h, _c.byref(a), _c.byref(b))
         return a.value, b.value
+
+
+def fast_exp(x):
+    return lib.orc_fast_exp(float(x))
+
+
+def gdn_step(S, q, k, v, decay, beta):
+    """one token of the delta rule on one head: (new S [dk][dv], out [dv]) (orc_gdn_step)"""
+    S = np.array(S, np.float32, copy=True)
+    dk, dv = S.shape
+    out = np.empty(dv, np.float32)
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+    lib.orc_gdn_step(_ptr(S), dk, dv, _ptr(q), _ptr(k), _ptr(v), decay, beta, _ptr(out))
+    return S, out

@@ -37,6 +37,17 @@ MISTAKES = (
     "no_causal",           # every row sees every new row (no causal / tree mask)
     "kv_f32",              # the new keys and values kept in fp32 instead of fp16
 )
+# slips in a Gated DeltaNet layer (model.cpp:3526-3688)
+GDN_MISTAKES = (
+    "gdn_no_decay",        # the state not decayed (decay 1)
+    "gdn_no_beta",         # the delta's step size dropped (beta 1)
+    "gdn_softplus",        # the decay's exp(-exp(A_log) (a + dt_bias)) without the softplus
+    "gdn_conv_reversed",   # the conv's taps in reverse order (newest input on the oldest tap)
+    "gdn_no_l2norm",       # q and k not L2-normalised
+    "gdn_no_qscale",       # q without 1/sqrt(dk)
+    "gdn_no_gate",         # the output's RMSNorm without the silu(z) gate
+    "gdn_state_reset",     # every row from the layer's state instead of its parent's
+)
 
 
 def _f16(x):
@@ -106,6 +117,21 @@ class F64Model:
             L["sd"] = q4(po.SH_DOWN, H, SF, l)
             kv = om.tensor(po.KV, l)[0].view(np.float16).astype(np.float64).reshape(2, c["max_ctx"], nkv * hd)
             L["kcache"], L["vcache"] = kv[0].copy(), kv[1].copy()
+            L["gdn"] = bool(c.get("gdn_layers") and c["gdn_layers"][l])
+            if L["gdn"]:
+                nk, nv, dk, dv, K = (c["gdn_k_heads"], c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"],
+                                     c["conv_kernel"])
+                cd, vd = 2 * nk * dk + nv * dv, nv * dv
+                f32 = lambda kind: om.tensor(kind, l)[0].view(np.float32).astype(np.float64)   # noqa: E731
+                L["gqkv"] = q4(po.GDN_QKV, cd, H, l)
+                L["gz"] = q4(po.GDN_Z, vd, H, l)
+                L["gout"] = q4(po.GDN_OUT, H, vd, l)
+                L["ga"] = _bf16(om.tensor(po.GDN_A, l)[0].view(np.uint16)).reshape(nv, H)
+                L["gb"] = _bf16(om.tensor(po.GDN_B, l)[0].view(np.uint16)).reshape(nv, H)
+                L["alog"], L["dtb"], L["gnorm"] = f32(po.GDN_ALOG), f32(po.GDN_DTB), f32(po.GDN_NORM)
+                L["convw"] = f32(po.GDN_CONV).reshape(cd, K)
+                L["conv"] = f32(po.GDN_CONV_ST).reshape(cd, K - 1)
+                L["S"] = f32(po.GDN_S).reshape(nv, dk, dv)
             self.layers.append(L)
 
     def _mm(self, W, x, mode):
@@ -180,6 +206,54 @@ class F64Model:
                 core[t, hh] = o if "no_attn_gate" in mistakes else o * _sigmoid(gate[t, hh])
         return self._mm(L["o"], core.reshape(n, -1), mode)
 
+    def gdn(self, L, h, parents, mode, mistakes=()):
+        """a Gated DeltaNet layer in float64 (model.cpp:3526-3688); the layer's states move on as the oracle's do (a
+        chain's last row)"""
+        c = self.c
+        nk, nv, dk, dv, K = c["gdn_k_heads"], c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"], c["conv_kernel"]
+        kd, rep = nk * dk, nv // nk
+        n = h.shape[0]
+        h32 = np.asarray(h, np.float32).astype(np.float64)
+        proj = self._mm(L["gqkv"], h, mode)
+        z = self._mm(L["gz"], h, mode)
+        a, b = h32 @ L["ga"].T, h32 @ L["gb"].T
+        silu = lambda x: x * _sigmoid(x)   # noqa: E731
+        convs, states, core = [], [], np.empty((n, nv * dv))
+        w = L["convw"][:, ::-1] if "gdn_conv_reversed" in mistakes else L["convw"]
+        for t in range(n):
+            parent = (t - 1 if parents is None else parents[t])
+            if "gdn_state_reset" in mistakes:
+                parent = -1
+            cin = L["conv"] if parent < 0 else convs[parent]
+            window = np.concatenate([cin, proj[t][:, None]], axis=1)   # [ch][K]: oldest first
+            convs.append(window[:, 1:])
+            x = silu((window * w).sum(axis=1))
+            q = x[:kd].reshape(nk, dk)
+            k = x[kd:2 * kd].reshape(nk, dk)
+            v = x[2 * kd:].reshape(nv, dv)
+            if "gdn_no_l2norm" not in mistakes:
+                q = q / np.sqrt((q * q).sum(axis=1, keepdims=True) + 1e-6)
+                k = k / np.sqrt((k * k).sum(axis=1, keepdims=True) + 1e-6)
+            if "gdn_no_qscale" not in mistakes:
+                q = q / np.sqrt(dk)
+            sp = a[t] + L["dtb"]
+            if "gdn_softplus" not in mistakes:
+                sp = np.where(sp > 20.0, sp, np.log1p(np.exp(sp)))
+            decay = np.ones(nv) if "gdn_no_decay" in mistakes else np.exp(-np.exp(L["alog"]) * sp)
+            beta = np.ones(nv) if "gdn_no_beta" in mistakes else _sigmoid(b[t])
+            S = (L["S"] if parent < 0 else states[parent]).copy()
+            for vh in range(nv):
+                kh = vh // rep
+                S[vh] *= decay[vh]
+                delta = (v[vh] - S[vh].T @ k[kh]) * beta[vh]
+                S[vh] += np.outer(k[kh], delta)
+                o = S[vh].T @ q[kh]
+                o = o / np.sqrt(np.mean(o * o) + c["eps"]) * L["gnorm"]
+                core[t, vh * dv:(vh + 1) * dv] = o if "gdn_no_gate" in mistakes else o * silu(z[t, vh * dv:(vh + 1) * dv])
+            states.append(S)
+        L["conv"], L["S"] = convs[-1], states[-1]
+        return self._mm(L["gout"], core, mode)
+
     def moe(self, L, h, mode, mistakes=(), logits=None):
         c = self.c
         E, K = c["n_experts"], c["top_k"]
@@ -216,7 +290,10 @@ class F64Model:
         all_ids, all_p = [], []
         for L in self.layers:
             h = _rms(x, L["in"], c["eps"])
-            x = x + self.attention(L, h, pos, parents, mode, mistakes)
+            if L["gdn"]:
+                x = x + self.gdn(L, h, parents, mode, mistakes)
+            else:
+                x = x + self.attention(L, h, pos, parents, mode, mistakes)
             h2 = _rms(x, L["post"], c["eps"])
             o, ids, _, p = self.moe(L, h2, mode, mistakes)
             all_ids.append(ids)
