@@ -24,7 +24,23 @@ class GvModelConfig(_c.Structure):
     _fields_ = [(n, _c.c_int32) for n in ("hidden", "vocab", "n_layers", "n_experts", "top_k", "moe_ff", "shared_ff",
                                           "n_heads", "n_kv_heads", "head_dim", "rope_dim")] + \
                [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int32), ("max_rows", _c.c_int32),
-                ("kv_int8", _c.c_int32)]
+                ("kv_int8", _c.c_int32)] + \
+               [(n, _c.c_int32) for n in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")] + \
+               [("gdn_layers", _c.c_uint8 * 256)]
+
+    @classmethod
+    def of(cls, cfg):
+        """the C struct of a config dict (kv_int8 and the Gated DeltaNet fields optional, gdn_layers a list of flags)"""
+        optional = ("kv_int8", "gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")
+        c = cls(**{k: cfg.get(k, 0) if k in optional else cfg[k] for k, _ in cls._fields_ if k != "gdn_layers"})
+        for l, g in enumerate(cfg.get("gdn_layers", ())):
+            c.gdn_layers[l] = 1 if g else 0
+        return c
+
+    def to_dict(self):
+        d = {k: getattr(self, k) for k, _ in self._fields_ if k != "gdn_layers"}
+        d["gdn_layers"] = [int(self.gdn_layers[l]) for l in range(min(self.n_layers, 256))]
+        return d
 
 
 class GvPackTensorInfo(_c.Structure):
@@ -41,6 +57,7 @@ class GvStateInfo(_c.Structure):
 # tensor kinds of gv_model_adopt
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, QKV, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, \
     SHARED_EXPERT, KV, KV_I8 = 0, 1, 2, 3, 4, 5, 8, 9, 10, 11, 12, 13, 14, 17, 18
+GDN_QKV, GDN_Z, GDN_OUT, GDN_A, GDN_B, GDN_ALOG, GDN_DTB, GDN_CONV, GDN_NORM, GDN_CONV_ST, GDN_S = range(20, 31)
 
 # every symbol include/geode_verify.h declares, with its signature
 SIGNATURES = {
@@ -91,6 +108,7 @@ SIGNATURES = {
     "gv_model_moe": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_model_layer": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
+    "gv_model_gdn_state": (_c.c_int, [_P, _c.c_int, _P, _P]),
     "gv_pack_open": (_P, [_c.c_char_p, _c.c_char_p, _c.c_int]),
     "gv_pack_close": (None, [_P]),
     "gv_pack_print": (_c.c_uint64, [_P]),
@@ -114,7 +132,7 @@ SIGNATURES = {
 
 # kernel classes of a verify step (gv_model_time_kernel)
 KERNEL_CLASSES = ["embed", "quantize", "qkv", "rope_kv", "attention", "attn_merge", "o_proj", "router", "route",
-                  "moe_up", "swiglu", "moe_down", "combine", "lm_head"]
+                  "moe_up", "swiglu", "moe_down", "combine", "lm_head", "gdn_ab", "gdn_conv", "gdn_core", "gdn_norm"]
 
 
 class GeodeError(RuntimeError):
@@ -356,7 +374,7 @@ class Pack:
     def model_config(self, max_ctx, max_rows=17, kv_int8=0):
         c = GvModelConfig()
         check(_lib().gv_pack_model_config(self.h, max_ctx, max_rows, kv_int8, _c.byref(c)), "gv_pack_model_config")
-        return {k: getattr(c, k) for k, _ in GvModelConfig._fields_}
+        return c.to_dict()
 
     def tensor(self, name):
         t = GvPackTensorInfo()
@@ -384,7 +402,7 @@ class VerifyModel:
 
     def __init__(self, cfg: dict):
         self.cfg = dict(cfg)
-        c = GvModelConfig(**{k: cfg.get(k, 0) if k == "kv_int8" else cfg[k] for k, _ in GvModelConfig._fields_})
+        c = GvModelConfig.of(cfg)
         err = _c.create_string_buffer(512)
         self.h = _lib().gv_model_create(_c.byref(c), err, 512)
         if not self.h:
@@ -430,6 +448,17 @@ class VerifyModel:
     def keep(self, kept, path=None):
         p = np.ascontiguousarray(path, np.int32) if path is not None else None
         check(_lib().gv_verify_keep(self.h, kept, p.ctypes.data_as(_P) if p is not None else None), "gv_verify_keep")
+
+    def gdn_state(self, layer):
+        """a Gated DeltaNet layer's states as the last verify / keep left them: (conv [2 kd + vd][K - 1],
+        S [nv][dk][dv])"""
+        c = self.cfg
+        conv = np.empty((2 * c["gdn_k_heads"] * c["gdn_k_dim"] + c["gdn_v_heads"] * c["gdn_v_dim"],
+                         c["conv_kernel"] - 1), np.float32)
+        S = np.empty((c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"]), np.float32)
+        check(_lib().gv_model_gdn_state(self.h, layer, conv.ctypes.data_as(_P), S.ctypes.data_as(_P)),
+              "gv_model_gdn_state")
+        return conv, S
 
     def time_kernel(self, cls):
         """events around every launch of kernel class cls (an index into KERNEL_CLASSES; -1 off) from now on"""

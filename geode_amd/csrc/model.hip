@@ -636,7 +636,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
                     *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8) = make_float4(v[0], v[1], v[2], v[3]);
                     *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8 + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 }
-                if (tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(blockIdx.x) * act_stride);
+                if (act && tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(blockIdx.x) * act_stride);
             }
         }
         __syncthreads();
@@ -1627,9 +1627,14 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     const int H = c.hidden, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     const int64_t abH = act_halves(H), abC = act_halves(static_cast<int64_t>(nh) * hd);
     LayerW &L = m.layers[static_cast<size_t>(l)];
+    // the token mixer's classes of the other kind of layer (attention / Gated DeltaNet) launch nothing
+    const bool per_layer = cls != GV_K_EMBED && cls != GV_K_LM_HEAD && cls != GV_K_QUANT;
+    const bool gdn_cls = cls >= GV_K_GDN_AB && cls <= GV_K_GDN_NORM;
+    const bool attn_cls = cls == GV_K_ROPE || cls == GV_K_ATTN || cls == GV_K_MERGE;
+    if (per_layer && (L.gdn ? attn_cls : gdn_cls)) return 0;
     // classes fused into a neighbour launch nothing and take no events
     int mix_kw = 0;
-    const bool mixout = mixout_fits(m, M, mix_kw);
+    const bool mixout = !L.gdn && mixout_fits(m, M, mix_kw);
     const bool fused = (cls == GV_K_SWIGLU && m.moe_dec) || (cls == GV_K_ROUTE && m.route_in_router && !m.moe_only) ||
                        ((cls == GV_K_ROUTER || cls == GV_K_ROUTE) && mixout);
     if (fused) return 0;
@@ -1639,11 +1644,38 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, st, m.embed, m.sp, m.x, m.layers[0].in_norm, c.eps,
                            m.act_h, abH);
         return 0;
-    case GV_K_QKV: {
+    case GV_K_QKV: {   // (a Gated DeltaNet layer: in_proj_qkv | in_proj_z, two globals)
         GemvOut o = qkv_out(m, L);
+        if (L.gdn) {
+            o.nseg = 2;
+            o.seg_end[0] = gdn_conv_dim(c);
+            o.seg_end[1] = INT64_MAX;
+        }
         o.trace_cls = GV_K_QKV;
         return gemv_q4(L.qkv, m.act_h, abH, M, o, st);
     }
+    case GV_K_GDN_AB: {   // the bf16 a / b rows . RMSNorm(x) (the router kernel's arithmetic, bf16_rows' sum order)
+        const int E1 = 2 * c.gdn_v_heads, wgs = (E1 + kRouterRows - 1) / kRouterRows;
+        if (H <= 2048) {
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
+            hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.gdn_ab, E1, H, m.x,
+                               L.in_norm, c.eps, m.sp, m.rlogits, nullptr, 0, 0, c.n_experts, c.top_k, m.route + l,
+                               nullptr, m.counter);
+        } else {
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
+            hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.gdn_ab, E1, H, m.x,
+                               L.in_norm, c.eps, m.sp, m.rlogits, nullptr, 0, 0, c.n_experts, c.top_k, m.route + l,
+                               nullptr, m.counter);
+        }
+        GV_CHECK_HIP(hipGetLastError());
+        return 0;
+    }
+    case GV_K_GDN_CONV:
+    case GV_K_GDN_CORE:
+    case GV_K_GDN_NORM:
+        return gdn_launch(m, L, cls, st);
     case GV_K_ROPE:
         hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
                            c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
@@ -1660,7 +1692,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         if (mixout) return launch_mixout(m, L, l, M, mix_kw, st);   // with the router and the route
         GemvOut o = gemv_out(m.x, H, L.o.global, 1);
         o.trace_cls = GV_K_O;
-        return gemv_q4(L.o, m.act_core, abC, M, o, st);
+        return gemv_q4(L.o, m.act_core, L.gdn ? act_halves(L.o.cols) : abC, M, o, st);
     }
     case GV_K_ROUTER: {
         const int wgs = std::max((m.E1 + kRouterRows - 1) / kRouterRows, M);
@@ -1709,8 +1741,10 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     }
 }
 
-constexpr int kLayerClasses[] = {GV_K_QKV,    GV_K_ROPE,  GV_K_ATTN,   GV_K_MERGE,  GV_K_O,       GV_K_ROUTER,
-                                 GV_K_ROUTE,  GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN, GV_K_COMBINE};
+// (an attention layer skips the GV_K_GDN_* classes, a Gated DeltaNet layer GV_K_ROPE, GV_K_ATTN and GV_K_MERGE)
+constexpr int kLayerClasses[] = {GV_K_QKV,      GV_K_GDN_AB, GV_K_GDN_CONV, GV_K_GDN_CORE, GV_K_GDN_NORM,
+                                 GV_K_ROPE,     GV_K_ATTN,   GV_K_MERGE,    GV_K_O,        GV_K_ROUTER,
+                                 GV_K_ROUTE,    GV_K_MOE_UP, GV_K_SWIGLU,   GV_K_MOE_DOWN, GV_K_COMBINE};
 
 int run_layers(Model &m, int M, hipStream_t st) {
     if (launch_class(m, GV_K_EMBED, 0, M, st) != 0) return -1;
@@ -1852,6 +1886,12 @@ bool alloc_q4(Model &m, Q4 &q, int64_t rows, int64_t cols) {
     return true;
 }
 
+// the Gated DeltaNet layers' slots of a step: the rows start from the base, their states go to the other set
+void set_gdn_slots(const Model &m, StepParams &sp) {
+    sp.gdn_base = m.gdn_base;
+    sp.gdn_wset = m.gdn_base < m.c.max_rows ? m.c.max_rows : 0;
+}
+
 int64_t qkv_rows(const gv_model_config &c) {
     return static_cast<int64_t>(c.n_heads) * 2 * c.head_dim + 2 * static_cast<int64_t>(c.n_kv_heads) * c.head_dim;
 }
@@ -1930,6 +1970,13 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     if (c.max_rows <= 0 || c.max_rows > kMaxRows) return fail("max_rows must be 1..32");
     if (c.vocab <= 0 || c.n_layers <= 0 || c.max_ctx <= c.max_rows) return fail("vocab, n_layers, max_ctx");
     {
+        std::string why;
+        if (!gdn_shape_ok(c, why)) return fail(why);
+        for (int l = c.n_layers; l < 256; ++l)
+            if (c.gdn_layers[l] != 0) return fail("gdn_layers marks a layer past n_layers");
+        if (c.n_layers > 256 && c.gdn_v_heads > 0) return fail("Gated DeltaNet models take at most 256 layers");
+    }
+    {
         int waves, kw;
         const int ntt = c.max_rows <= 16 ? 1 : 2;
         if (!mfma_split(c.hidden, ntt, waves, kw) || !mfma_split(c.moe_ff, ntt, waves, kw))
@@ -1955,10 +2002,25 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     m.kv_all = static_cast<_Float16 *>(dalloc(m, static_cast<size_t>(c.n_layers) * m.kv_layer_bytes));
     ok = ok && m.kv_all;
     m.layers.resize(static_cast<size_t>(c.n_layers));
+    const int64_t gconv = gdn_conv_dim(c), gvd = static_cast<int64_t>(c.gdn_v_heads) * c.gdn_v_dim;
     for (int l = 0; ok && l < c.n_layers; ++l) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
-        ok = alloc_q4(m, L.qkv, qkv_rows(c), H) && alloc_q4(m, L.o, H, nh * hd);
-        auto *f = static_cast<float *>(dalloc(m, (2 * H + 2 * hd) * 4));
+        L.gdn = c.gdn_v_heads > 0 && l < 256 && c.gdn_layers[l] != 0;
+        if (L.gdn) {   // in_proj_qkv | in_proj_z, out_proj, the bf16 a / b rows, the small tensors, the state slots
+            const int64_t nv = c.gdn_v_heads, K = c.conv_kernel, Mx2 = 2 * static_cast<int64_t>(c.max_rows);
+            ok = alloc_q4(m, L.qkv, gconv + gvd, H) && alloc_q4(m, L.o, H, gvd);
+            ok = ok && (L.gdn_ab = static_cast<uint16_t *>(dalloc(m, static_cast<size_t>(2 * nv * H) * 2)));
+            auto *gf = ok ? static_cast<float *>(dalloc(m, static_cast<size_t>(2 * nv + gconv * K + c.gdn_v_dim) * 4))
+                          : nullptr;
+            ok = ok && gf;
+            if (ok) L.A_log = gf, L.dt_bias = gf + nv, L.conv_w = gf + 2 * nv, L.gnorm = gf + 2 * nv + gconv * K;
+            const size_t sb = static_cast<size_t>(Mx2 * gdn_s_floats(c)) * 4, cb = static_cast<size_t>(Mx2 * gdn_c_floats(c)) * 4;
+            ok = ok && (L.s_slots = static_cast<float *>(dalloc(m, sb))) && hipMemset(L.s_slots, 0, sb) == hipSuccess;
+            ok = ok && (L.c_slots = static_cast<float *>(dalloc(m, cb))) && hipMemset(L.c_slots, 0, cb) == hipSuccess;
+        } else {
+            ok = alloc_q4(m, L.qkv, qkv_rows(c), H) && alloc_q4(m, L.o, H, nh * hd);
+        }
+        auto *f = ok ? static_cast<float *>(dalloc(m, (2 * H + 2 * hd) * 4)) : nullptr;
         ok = ok && f;
         if (!ok) break;
         L.in_norm = f, L.post_norm = f + H, L.q_norm = f + 2 * H, L.k_norm = f + 2 * H + hd;
@@ -1997,16 +2059,17 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     }
     {   // the buffers one step's phases exchange, in one arena (one allocation, 256-byte aligned pieces)
         const size_t sizes[] = {static_cast<size_t>(Mx) * H * 4,
-                                static_cast<size_t>(Mx) * qkv_rows(c) * 4,
-                                static_cast<size_t>(Mx) * m.E1 * 4,
+                                static_cast<size_t>(Mx) * std::max(qkv_rows(c), gconv + gvd) * 4,
+                                static_cast<size_t>(Mx) * std::max(m.E1, 2 * c.gdn_v_heads) * 4,
                                 static_cast<size_t>(Mx) * nh * m.kv_blocks * (hd + 2) * 4,
                                 static_cast<size_t>(m.max_picks) * H * 4,
                                 static_cast<size_t>(Mx) * V * 4,
                                 static_cast<size_t>(Mx) * act_bytes(H),
-                                static_cast<size_t>(Mx) * act_bytes(nh * hd),
-                                static_cast<size_t>(m.max_picks) * act_bytes(F)};
-        size_t offs[9], tot = 0;
-        for (int i = 0; i < 9; ++i) {
+                                static_cast<size_t>(Mx) * act_bytes(std::max(nh * hd, gvd)),
+                                static_cast<size_t>(m.max_picks) * act_bytes(F),
+                                static_cast<size_t>(Mx) * gvd * 4};
+        size_t offs[10], tot = 0;
+        for (int i = 0; i < 10; ++i) {
             offs[i] = tot;
             tot += (sizes[i] + 255) / 256 * 256;
         }
@@ -2024,6 +2087,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
             m.act_h = reinterpret_cast<_Float16 *>(ar + offs[6]);
             m.act_core = reinterpret_cast<_Float16 *>(ar + offs[7]);
             m.act_m = reinterpret_cast<_Float16 *>(ar + offs[8]);
+            m.gdn_core = gvd > 0 ? reinterpret_cast<float *>(ar + offs[9]) : nullptr;
         }
     }
     ok = ok && (m.q16 = static_cast<_Float16 *>(dalloc(m, 2 * Mx * nh * hd * 2)));
@@ -2084,7 +2148,42 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
         GV_CHECK_HIP(hipMemcpy(dst, data, static_cast<size_t>(bytes), hipMemcpyHostToDevice));
         return 0;
     };
+    const bool gdn_kind = kind >= GV_GDN_QKV && kind <= GV_GDN_S;
+    const bool attn_kind = kind == GV_QKV || kind == GV_O || kind == GV_Q_NORM || kind == GV_K_NORM || kind == GV_KV ||
+                           kind == GV_KV_I8;
+    GV_REQUIRE(!gdn_kind || L->gdn, "gv_model_adopt: a Gated DeltaNet tensor for an attention layer");
+    GV_REQUIRE(!attn_kind || !L->gdn, "gv_model_adopt: an attention tensor for a Gated DeltaNet layer");
+    const int64_t nv = c.gdn_v_heads, gconv = gdn_conv_dim(c), gvd = nv * c.gdn_v_dim;
     switch (kind) {
+    case GV_GDN_QKV:
+    case GV_GDN_Z: {   // the two parts of the layer's qkv matrix (whole 16-row tiles each: conv_dim is a multiple of 64)
+        const bool z = kind == GV_GDN_Z;
+        const int64_t rows = z ? gvd : gconv;
+        GV_REQUIRE(globals && bytes == q4_size(rows, H), "gv_model_adopt: in_proj_qkv / in_proj_z size");
+        Q4 tmp;
+        const size_t co = z ? q4_code_bytes(gconv, H) : 0, so = z ? q4_scale_bytes(gconv, H) : 0;
+        if (upload_q4(data, false, rows, H, const_cast<uint8_t *>(L->qkv.codes) + co,
+                      const_cast<uint8_t *>(L->qkv.scales) + so, 1.0f, tmp) != 0)
+            return -1;
+        (z ? L->g_k : L->g_q) = globals[0];
+        return 0;
+    }
+    case GV_GDN_OUT:
+        GV_REQUIRE(globals && bytes == q4_size(H, gvd), "gv_model_adopt: out_proj size");
+        return upload_q4(data, false, H, gvd, const_cast<uint8_t *>(L->o.codes), const_cast<uint8_t *>(L->o.scales),
+                         globals[0], L->o);
+    case GV_GDN_A: return copy(L->gdn_ab, nv * H * 2);
+    case GV_GDN_B: return copy(L->gdn_ab + nv * H, nv * H * 2);
+    case GV_GDN_ALOG: return copy(L->A_log, nv * 4);
+    case GV_GDN_DTB: return copy(L->dt_bias, nv * 4);
+    case GV_GDN_CONV: return copy(L->conv_w, gconv * c.conv_kernel * 4);
+    case GV_GDN_NORM: return copy(L->gnorm, static_cast<int64_t>(c.gdn_v_dim) * 4);
+    case GV_GDN_CONV_ST:   // the states go to the base slot: the next verify's rows start from them
+        GV_REQUIRE(bytes == gdn_c_floats(c) * 4, "gv_model_adopt: conv state size");
+        return gdn_put_state(m, *L, m.gdn_base, static_cast<const float *>(data), nullptr);
+    case GV_GDN_S:
+        GV_REQUIRE(bytes == gdn_s_floats(c) * 4, "gv_model_adopt: recurrent state size");
+        return gdn_put_state(m, *L, m.gdn_base, nullptr, static_cast<const float *>(data));
     case GV_EMBED:
     case GV_LM_HEAD: {
         GV_REQUIRE(globals && bytes == q4_size(V, H), "gv_model_adopt: embed / lm_head size");
@@ -2183,7 +2282,9 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
     const int64_t kv_row = nkv * hd;
     hipStream_t st = stream();
     const int64_t biggest = std::max<int64_t>({V * H, qkv_rows(c) * H, 2 * F * H, 2 * static_cast<int64_t>(ctx) * kv_row,
-                                               static_cast<int64_t>(m.E1) * H});
+                                               static_cast<int64_t>(m.E1) * H, (gdn_conv_dim(c) + 2 * c.gdn_v_heads *
+                                               static_cast<int64_t>(c.gdn_v_dim)) * H, gdn_s_floats(c),
+                                               gdn_c_floats(c) * c.conv_kernel});
     float *wf = nullptr;
     uint8_t *pack = nullptr;
     unsigned int *u32 = nullptr;
@@ -2224,6 +2325,52 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
         LayerW &L = m.layers[static_cast<size_t>(l)];
         rc |= make_f32(tseed(GV_IN_NORM, l, 0), H, 0.02f, L.in_norm);
         rc |= make_f32(tseed(GV_POST_NORM, l, 0), H, 0.02f, L.post_norm);
+        if (L.gdn) {   // the oracle's seeds and spreads (oracle_layers.cpp orc_model_fill)
+            const int64_t nv = c.gdn_v_heads, gconv = gdn_conv_dim(c), gvd = nv * c.gdn_v_dim, K = c.conv_kernel;
+            const int64_t parts[2] = {gconv, gvd};
+            float *gh[2] = {&L.g_q, &L.g_k};
+            int64_t off = 0;
+            for (int i = 0; i < 2 && rc == 0; ++i) {   // in_proj_qkv | in_proj_z, then one permutation of the whole
+                rc |= fill_normal(tseed(GV_GDN_QKV + i, l, 0), parts[i] * H, sigma, wf, st);
+                rc |= q4_pack(wf, parts[i], H, u32, pack + off * (H / 16) * 9, gdev, st);
+                GV_CHECK_HIP(hipMemcpyAsync(gh[i], gdev, 4, hipMemcpyDeviceToHost, st));
+                GV_CHECK_HIP(hipStreamSynchronize(st));
+                off += parts[i];
+            }
+            const float gq = L.g_q, gz = L.g_k;
+            rc |= q4_from_pack(pack, gconv + gvd, H, 1.0f, const_cast<uint8_t *>(L.qkv.codes),
+                               const_cast<uint8_t *>(L.qkv.scales), L.qkv, st);
+            L.g_q = gq, L.g_k = gz;
+            rc |= make_q4(tseed(GV_GDN_OUT, l, 0), H, gvd, const_cast<uint8_t *>(L.o.codes),
+                          const_cast<uint8_t *>(L.o.scales), &L.o.global, nullptr);
+            rc |= fill_normal(tseed(GV_GDN_A, l, 0), nv * H, router_sigma, wf, st);
+            rc |= fill_normal(tseed(GV_GDN_B, l, 0), nv * H, router_sigma, wf + nv * H, st);
+            hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(static_cast<unsigned>((2 * nv * H + 255) / 256)), dim3(256), 0,
+                               st, wf, 2 * nv * H, L.gdn_ab);
+            rc |= make_f32(tseed(GV_GDN_ALOG, l, 0), nv, 0.5f, L.A_log);
+            rc |= make_f32(tseed(GV_GDN_DTB, l, 0), nv, 0.5f, L.dt_bias);
+            rc |= make_f32(tseed(GV_GDN_CONV, l, 0), gconv * K, 0.3f, L.conv_w);
+            {   // the gated norm's weight: 1 + N(0, 0.02)
+                std::vector<float> gn(static_cast<size_t>(c.gdn_v_dim));
+                rc |= make_f32(tseed(GV_GDN_NORM, l, 0), c.gdn_v_dim, 0.02f, wf);
+                GV_CHECK_HIP(hipMemcpyAsync(gn.data(), wf, gn.size() * 4, hipMemcpyDeviceToHost, st));
+                GV_CHECK_HIP(hipStreamSynchronize(st));
+                for (float &v : gn) v += 1.0f;
+                GV_CHECK_HIP(hipMemcpy(L.gnorm, gn.data(), gn.size() * 4, hipMemcpyHostToDevice));
+            }
+            // the states: a conversation's (N(0, 1) conv inputs, an N(0, 0.05) recurrent state), or zero at ctx 0
+            std::vector<float> cs(static_cast<size_t>(gdn_c_floats(c)), 0.0f), ss(static_cast<size_t>(gdn_s_floats(c)), 0.0f);
+            if (ctx > 0) {
+                rc |= fill_normal(tseed(GV_GDN_CONV_ST, l, 0), static_cast<int64_t>(cs.size()), 1.0f, wf, st);
+                GV_CHECK_HIP(hipMemcpyAsync(cs.data(), wf, cs.size() * 4, hipMemcpyDeviceToHost, st));
+                GV_CHECK_HIP(hipStreamSynchronize(st));
+                rc |= fill_normal(tseed(GV_GDN_S, l, 0), static_cast<int64_t>(ss.size()), 0.05f, wf, st);
+                GV_CHECK_HIP(hipMemcpyAsync(ss.data(), wf, ss.size() * 4, hipMemcpyDeviceToHost, st));
+                GV_CHECK_HIP(hipStreamSynchronize(st));
+            }
+            if (rc == 0) rc |= gdn_put_state(m, L, m.gdn_base, cs.data(), ss.data());
+        }
+        if (!L.gdn) {
         rc |= make_f32(tseed(GV_Q_NORM, l, 0), hd, 0.02f, L.q_norm);
         rc |= make_f32(tseed(GV_K_NORM, l, 0), hd, 0.02f, L.k_norm);
         // q | k | v packed one part at a time (each its own global), then one permutation of the whole
@@ -2247,6 +2394,7 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
         }
         rc |= make_q4(tseed(GV_O, l, 0), H, nh * hd, const_cast<uint8_t *>(L.o.codes), const_cast<uint8_t *>(L.o.scales),
                       &L.o.global, nullptr);
+        }
         // router rows and the shared gate row in bf16
         rc |= fill_normal(tseed(GV_ROUTER, l, 0), static_cast<int64_t>(c.n_experts) * H, router_sigma, wf, st);
         rc |= fill_normal(tseed(GV_SHARED_GATE, l, 0), H, sigma, wf + static_cast<int64_t>(c.n_experts) * H, st);
@@ -2274,7 +2422,7 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
             }
             (void)gd;
         }
-        if (ctx > 0) {   // K then V of positions [0, ctx) in the reference's row layout, then the device's
+        if (ctx > 0 && !L.gdn) {   // K then V of positions [0, ctx) in the reference's row layout, then the device's
             for (int kvi = 0; kvi < 2; ++kvi)
                 rc |= fill_normal(tseed(GV_KV, l, kvi), static_cast<int64_t>(ctx) * kv_row, 1.0f,
                                   wf + static_cast<int64_t>(kvi) * ctx * kv_row, st);
@@ -2316,6 +2464,7 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;
     sp.M = n;
+    set_gdn_slots(m, sp);
     for (int i = 0; i < n; ++i) {
         GV_REQUIRE(tokens[i] >= 0 && tokens[i] < c.vocab, "gv_verify: token out of range");
         sp.tokens[i] = tokens[i];
@@ -2339,6 +2488,7 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     m.last_pos = m.pos;
     m.last_n = n;
     m.pos += n;
+    m.gdn_base = sp.gdn_wset + n - 1;   // (a chain's states as after its last row)
     return 0;
 }
 
@@ -2373,6 +2523,7 @@ int gv_verify_keep(gv_model *g, int kept, const int32_t *path) {
         GV_CHECK_HIP(hipStreamSynchronize(stream()));
     }
     m.pos = m.last_pos + kept;
+    m.gdn_base = m.host_sp.gdn_wset + (path ? path[kept - 1] : kept - 1);   // the states as after the last kept row
     m.last_n = 0;
     return 0;
 }
@@ -2497,6 +2648,7 @@ int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;
     sp.M = n;
+    set_gdn_slots(m, sp);   // (the rows' states go to the other set: the base stays)
     for (int i = 0; i < n; ++i) {
         if (parents) {
             GV_REQUIRE(i == 0 ? parents[0] == -1 : (parents[i] >= 0 && parents[i] < i), "gv_model_layer: parents");
@@ -2514,7 +2666,8 @@ int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32
     // the layer's input norm and operands (in a step: the previous layer's combine, or the embedding)
     LayerW &L = m.layers[static_cast<size_t>(layer)];
     if (quantize_act(m.x, H, n, H, L.in_norm, c.eps, m.act_h, act_halves(H), nullptr, 0, st) != 0) return -1;
-    for (int cls : {GV_K_QKV, GV_K_ROPE, GV_K_ATTN, GV_K_MERGE, GV_K_O})
+    for (int cls : {GV_K_QKV, GV_K_GDN_AB, GV_K_GDN_CONV, GV_K_GDN_CORE, GV_K_GDN_NORM, GV_K_ROPE, GV_K_ATTN, GV_K_MERGE,
+                    GV_K_O})
         if (launch_class(m, cls, layer, n, st) != 0) return -1;
     if (x_mid) GV_CHECK_HIP(hipMemcpyAsync(x_mid, m.x, static_cast<size_t>(n) * H * 4, hipMemcpyDeviceToHost, st));
     for (int cls : {GV_K_ROUTER, GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN, GV_K_COMBINE})
@@ -2526,6 +2679,14 @@ int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32
     if (check_wait_flag(m, st) != 0) return -1;
     m.last_n = 0;   // nothing to keep: the position is unchanged
     return 0;
+}
+
+int gv_model_gdn_state(const gv_model *g, int layer, float *conv, float *S) {
+    GV_REQUIRE(g && layer >= 0 && layer < g->m.c.n_layers, "gv_model_gdn_state: no such layer");
+    const Model &m = g->m;
+    const LayerW &L = m.layers[static_cast<size_t>(layer)];
+    GV_REQUIRE(L.gdn, "gv_model_gdn_state: not a Gated DeltaNet layer");
+    return gdn_get_state(m, L, m.gdn_base, conv, S);
 }
 
 int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
 #include <vector>
 
 #include "../../include/geode_verify.h"
@@ -21,6 +22,8 @@ struct StepParams {
     int tokens[kMaxRows];
     int depth[kMaxRows];
     uint32_t vis[kMaxRows];
+    int gdn_base;   // the Gated DeltaNet layers' slot holding the states the rows start from
+    int gdn_wset;   // the first slot of the set the rows' states go to (the set without gdn_base)
 };
 
 // Routing of one layer, written by the route kernel: slots are runs of at most kSlotRows picks (token, rank) of one
@@ -75,6 +78,12 @@ struct LayerW {
     _Float16 *kv = nullptr;   // K [nkv][slots][hd], then V [nkv][slots / 64][hd][64] (model.hip: k_index, v_index)
     int8_t *kv8 = nullptr;    // the int8 cache: the same layout in int8,
     float *kvs = nullptr;     // then the scales: K [nkv][slots], V [nkv][slots]
+    // a Gated DeltaNet layer (gdn.hip): qkv holds in_proj_qkv then in_proj_z (globals g_q, g_k), o out_proj [H x vd]
+    bool gdn = false;
+    uint16_t *gdn_ab = nullptr;   // bf16 [2 nv][H]: in_proj_a then in_proj_b
+    float *A_log = nullptr, *dt_bias = nullptr, *conv_w = nullptr, *gnorm = nullptr;   // [nv], [nv], [conv_dim][K], [dv]
+    float *s_slots = nullptr;     // [2 max_rows] recurrent states in the core kernel's layout (gdn.hip: s_index)
+    float *c_slots = nullptr;     // [2 max_rows][K - 1][conv_dim] conv states
 };
 
 // The prefill MoE's buffers (C5: many rows), allocated for `cap` rows on first use
@@ -135,6 +144,8 @@ struct Model {
     size_t events_used = 0;
     StepParams host_sp{};
     int max_slots = 0, max_picks = 0;
+    float *gdn_core = nullptr;   // [max_rows][nv dv] the delta rule's outputs
+    int gdn_base = 0;            // the Gated DeltaNet layers' base slot (StepParams::gdn_base)
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
@@ -142,5 +153,14 @@ constexpr int kFlagsPerLayer = 1024;   // flag words a layer's fused launches ha
 
 // the model behind a C-ABI handle (model.hip), for the entry points of other files
 Model &model_of(gv_model *g);
+
+// the Gated DeltaNet layer (gdn.hip)
+bool gdn_shape_ok(const gv_model_config &c, std::string &why);
+int64_t gdn_conv_dim(const gv_model_config &c);
+int64_t gdn_s_floats(const gv_model_config &c);   // a slot's recurrent state
+int64_t gdn_c_floats(const gv_model_config &c);   // a slot's conv state
+int gdn_launch(Model &m, LayerW &L, int cls, hipStream_t st);   // GV_K_GDN_CONV, _CORE, _NORM
+int gdn_put_state(Model &m, LayerW &L, int slot, const float *conv, const float *S);
+int gdn_get_state(const Model &m, const LayerW &L, int slot, float *conv, float *S);
 
 }  // namespace gv

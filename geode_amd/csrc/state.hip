@@ -244,6 +244,7 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
     Model &m = model_of(g);
     const auto &c = m.c;
     GV_REQUIRE(c.head_dim % 16 == 0, "gv_model_save_state: head_dim must be a multiple of 16");
+    GV_REQUIRE(c.gdn_v_heads == 0, "gv_model_save_state: the Gated DeltaNet layers' states are not in the file yet");
     const Shapes s = shapes_of(m);
     StateHeader h{};
     std::memcpy(h.magic, kMagic, sizeof kMagic);
@@ -348,6 +349,7 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
     Model &m = model_of(g);
     const auto &c = m.c;
     GV_REQUIRE(c.head_dim % 16 == 0, "gv_model_load_state: head_dim must be a multiple of 16");
+    GV_REQUIRE(c.gdn_v_heads == 0, "gv_model_load_state: the Gated DeltaNet layers' states are not in the file yet");
     // whatever the failure, the conversation is empty after it (state.cpp:383-388)
     m.pos = 0;
     m.last_n = 0;

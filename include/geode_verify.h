@@ -113,6 +113,12 @@ typedef struct gv_model_config {
     int32_t max_rows; /* rows a verify takes at most (<= 32) */
     int32_t kv_int8;  /* 1: the KV cache in int8 with a float scale a (position, KV head), ModelOptions::kv_int8
                          (engine/src/model.cpp:360-363, :3756-3792); 0: fp16 (attend<_Float16>) */
+    /* Gated DeltaNet layers (ModelConfig::gdn_*, engine/src/pack.hpp:36-38; gdn_v_heads = 0: none): layer l is one
+     * iff gdn_layers[l] != 0 (ModelConfig::attention[l] false, pack.hpp:43: layer_types "linear_attention"). Key heads nk of dk, value heads nv of dv
+     * (nv a multiple of nk; dk in {32, 64, 128, 256}; dv a multiple of 16 with dv / 8 a power of two, at most 256;
+     * nv x dv a multiple of 128), causal conv of conv_kernel taps (2 .. 8). */
+    int32_t gdn_k_heads, gdn_v_heads, gdn_k_dim, gdn_v_dim, conv_kernel;
+    uint8_t gdn_layers[256];
 } gv_model_config;
 
 /* tensor kinds for gv_model_adopt (numbered as the CPU oracle's) */
@@ -133,8 +139,20 @@ enum {
     GV_SHARED_EXPERT = 14,/* q4 gate [ff x hidden], up [ff x hidden], down [hidden x ff]; globals[3] */
     GV_KV = 17,           /* fp16 [2][n_positions][n_kv_heads*hd]: K then V of positions 0.. (an int8 cache
                              quantizes each (position, KV head) row as quant_kv_row does, model.cpp:3766-3774) */
-    GV_KV_I8 = 18         /* int8 cache only: int8 [2][n_positions][n_kv_heads*hd] then float [2][n_positions]
+    GV_KV_I8 = 18,        /* int8 cache only: int8 [2][n_positions][n_kv_heads*hd] then float [2][n_positions]
                              [n_kv_heads] scales, the reference's int8 chunk layout (model.cpp:3756-3763) */
+    /* a Gated DeltaNet layer's tensors (Model::bind_layer, engine/src/model.cpp:129-138; kd = nk dk, vd = nv dv) */
+    GV_GDN_QKV = 20,      /* q4 in_proj_qkv [2 kd + vd x hidden], globals[0] */
+    GV_GDN_Z = 21,        /* q4 in_proj_z [vd x hidden], globals[0] */
+    GV_GDN_OUT = 22,      /* q4 out_proj [hidden x vd], globals[0] */
+    GV_GDN_A = 23,        /* bf16 in_proj_a [nv x hidden] */
+    GV_GDN_B = 24,        /* bf16 in_proj_b [nv x hidden] */
+    GV_GDN_ALOG = 25,     /* f32 A_log [nv] */
+    GV_GDN_DTB = 26,      /* f32 dt_bias [nv] */
+    GV_GDN_CONV = 27,     /* f32 conv1d [2 kd + vd][conv_kernel] */
+    GV_GDN_NORM = 28,     /* f32 norm [dv] (the gated RMSNorm's weight as it is: no 1 + w) */
+    GV_GDN_CONV_ST = 29,  /* f32 the conv's state [2 kd + vd][conv_kernel - 1], the last inputs oldest first */
+    GV_GDN_S = 30         /* f32 the recurrent state [nv][dk][dv] */
 };
 
 typedef struct gv_model gv_model;
@@ -164,7 +182,10 @@ int gv_model_route_ids(const gv_model *m, int32_t *out);
 enum {
     GV_K_EMBED = 0, GV_K_QUANT = 1, GV_K_QKV = 2, GV_K_ROPE = 3, GV_K_ATTN = 4, GV_K_MERGE = 5, GV_K_O = 6,
     GV_K_ROUTER = 7, GV_K_ROUTE = 8, GV_K_MOE_UP = 9, GV_K_SWIGLU = 10, GV_K_MOE_DOWN = 11, GV_K_COMBINE = 12,
-    GV_K_LM_HEAD = 13, GV_K_COUNT = 14
+    GV_K_LM_HEAD = 13,
+    /* a Gated DeltaNet layer's own (its projections are GV_K_QKV's and GV_K_O's launches): the bf16 a / b rows, the
+     * causal conv, the delta rule, the gated RMSNorm with the output projection's operands */
+    GV_K_GDN_AB = 14, GV_K_GDN_CONV = 15, GV_K_GDN_CORE = 16, GV_K_GDN_NORM = 17, GV_K_COUNT = 18
 };
 /* From now on, every launch of kernel class cls is bracketed by events on the library's stream (cls < 0: off);
  * gv_model_kernel_time waits and returns their summed milliseconds and launches since (no reference counterpart:
@@ -207,6 +228,10 @@ int gv_model_moe(gv_model *m, int layer, const float *h, int M, const float *rou
  * to keep. A checking aid: the layers of a step compared one at a time, each fed the same input. */
 int gv_model_layer(gv_model *m, int layer, const float *x_in, int n, const int32_t *parents, float *x_mid,
                    float *x_out, int32_t *ids);
+/* A Gated DeltaNet layer's states as the last verify or keep left them (a chain: after its last row; after a keep:
+ * after the last kept row, model.cpp:1617-1633): conv [2 kd + vd][conv_kernel - 1] and S [nv][dk][dv], host (either
+ * may be NULL). gv_model_layer reads the states and leaves them as they were. */
+int gv_model_gdn_state(const gv_model *m, int layer, float *conv, float *S);
 /* Re-run the last gv_model_moe call's block on its device-staged rows and logits reps times back to back, run i on
  * layer (layer + i) mod n_layers (so that a model of several layers rotates through distinct expert weights), and
  * return the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */

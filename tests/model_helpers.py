@@ -35,16 +35,28 @@ def adopt_oracle_model(gm, om, ctx):
     t, gl = om.tensor(po.LM_HEAD)
     gm.adopt(g.LM_HEAD, t, globals_=gl[:1])
     gm.adopt(g.FINAL_NORM, om.tensor(po.FINAL_NORM)[0])
+    gdn = c.get("gdn_layers", ())
     for l in range(c["n_layers"]):
-        for k_o, k_g in ((po.IN_NORM, g.IN_NORM), (po.POST_NORM, g.POST_NORM), (po.Q_NORM, g.Q_NORM),
-                         (po.K_NORM, g.K_NORM), (po.ROUTER, g.ROUTER), (po.SHARED_GATE, g.SHARED_GATE)):
+        for k_o, k_g in ((po.IN_NORM, g.IN_NORM), (po.POST_NORM, g.POST_NORM), (po.ROUTER, g.ROUTER),
+                         (po.SHARED_GATE, g.SHARED_GATE)):
             gm.adopt(k_g, om.tensor(k_o, l)[0], layer=l)
-        q, gq = om.tensor(po.Q, l)
-        k, gk = om.tensor(po.K, l)
-        v, gv = om.tensor(po.V, l)
-        gm.adopt(g.QKV, np.concatenate([q, k, v]), layer=l, globals_=[gq[0], gk[0], gv[0]])
-        o, go = om.tensor(po.O, l)
-        gm.adopt(g.O, o, layer=l, globals_=go[:1])
+        if l < len(gdn) and gdn[l]:   # a Gated DeltaNet layer: its tensors, its states
+            for k_o, k_g in ((po.GDN_QKV, g.GDN_QKV), (po.GDN_Z, g.GDN_Z), (po.GDN_OUT, g.GDN_OUT)):
+                t, gl = om.tensor(k_o, l)
+                gm.adopt(k_g, t, layer=l, globals_=gl[:1])
+            for k_o, k_g in ((po.GDN_A, g.GDN_A), (po.GDN_B, g.GDN_B), (po.GDN_ALOG, g.GDN_ALOG),
+                             (po.GDN_DTB, g.GDN_DTB), (po.GDN_CONV, g.GDN_CONV), (po.GDN_NORM, g.GDN_NORM),
+                             (po.GDN_CONV_ST, g.GDN_CONV_ST), (po.GDN_S, g.GDN_S)):
+                gm.adopt(k_g, om.tensor(k_o, l)[0], layer=l)
+        else:
+            for k_o, k_g in ((po.Q_NORM, g.Q_NORM), (po.K_NORM, g.K_NORM)):
+                gm.adopt(k_g, om.tensor(k_o, l)[0], layer=l)
+            q, gq = om.tensor(po.Q, l)
+            k, gk = om.tensor(po.K, l)
+            v, gv = om.tensor(po.V, l)
+            gm.adopt(g.QKV, np.concatenate([q, k, v]), layer=l, globals_=[gq[0], gk[0], gv[0]])
+            o, go = om.tensor(po.O, l)
+            gm.adopt(g.O, o, layer=l, globals_=go[:1])
         for e in range(c["n_experts"]):
             blk, ge = om.tensor(po.EXPERT, l, e)
             gm.adopt(g.EXPERT, blk, layer=l, expert=e, globals_=ge)
@@ -52,6 +64,8 @@ def adopt_oracle_model(gm, om, ctx):
         su, gsu = om.tensor(po.SH_UP, l)
         sd, gsd = om.tensor(po.SH_DOWN, l)
         gm.adopt(g.SHARED_EXPERT, np.concatenate([sg, su, sd]), layer=l, globals_=[gsg[0], gsu[0], gsd[0]])
+        if l < len(gdn) and gdn[l]:
+            continue
         if c.get("kv_int8"):   # the int8 rows and their scales, the reference's int8 chunk layout
             q, _ = om.tensor(po.KV8, l)
             sc, _ = om.tensor(po.KVS, l)
@@ -75,3 +89,17 @@ def near_tie_rows(logits, tol):
     """rows whose top-2 logit gap is below tol (greedy tokens there may legitimately differ)"""
     s = np.sort(logits, axis=1)
     return set(np.nonzero(s[:, -1] - s[:, -2] < tol)[0].tolist())
+
+
+def route_margins(om, trace):
+    """[n_layers][n]: the gap between the K-th and (K+1)-th router logit of each row at each layer, from the oracle's
+    MoE inputs (trace[l][2]) and the layer's bf16 router; a small gap is a routing near-tie, where a perturbation of
+    the row's input far below the logits' tolerance may swap an expert"""
+    c = om.cfg
+    K, E, H = c["top_k"], c["n_experts"], c["hidden"]
+    out = []
+    for l in range(c["n_layers"]):
+        R = (om.tensor(po.ROUTER, l)[0].view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(E, H)
+        lg = -np.sort(-(trace[l, 2].astype(np.float64) @ R.T.astype(np.float64)), axis=1)
+        out.append(lg[:, K - 1] - lg[:, K])
+    return np.array(out)
