@@ -12,6 +12,7 @@ independent of it. The draft tree (M = 17) is timed in the same run (`tree_m17`)
 
     python bench.py [--steps K] [--warmup W] [--tree] [--kv-int8] [--no-cpu]
     python bench.py --config c2|c3|c5      (the acceptance rules; one MoE block at M = 5 or 512)
+    python bench.py --config real          (the real model's shape: 30 Gated DeltaNet + 10 attention layers)
 """
 import argparse
 import json
@@ -26,6 +27,10 @@ sys.path.insert(0, ROOT)
 
 C4 = dict(hidden=2048, vocab=151936, n_layers=40, n_experts=256, top_k=8, moe_ff=512, shared_ff=512, n_heads=16,
           n_kv_heads=2, head_dim=256, rope_dim=64, rope_theta=1e7, eps=1e-6, max_ctx=8192 + 64, max_rows=17)
+# the real model (Qwen3.6-35B-A3B, engine/src/gpu_check.cpp:277-281): 30 Gated DeltaNet layers (16 key heads, 32 value
+# heads, 128-wide, conv of 4) and 10 gated-attention layers (every fourth), vocab 248,320, the int8 KV cache
+REAL = dict(C4, vocab=248320, kv_int8=1, gdn_k_heads=16, gdn_v_heads=32, gdn_k_dim=128, gdn_v_dim=128, conv_kernel=4,
+            gdn_layers=[0 if l % 4 == 3 else 1 for l in range(40)])
 CTX = 8192
 SEED = 20261201
 PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s
@@ -71,6 +76,15 @@ def algorithmic_bytes(cls, c, M, uniq_per_layer, ctx):
         return 2 * nkv * (ctx + M) * (hd + 4 if c.get("kv_int8") else hd * 2)
     if cls == "router":
         return (c["n_experts"] + 1) * H * 2
+    nk, nv, dk, dv = c.get("gdn_k_heads", 0), c.get("gdn_v_heads", 0), c.get("gdn_k_dim", 0), c.get("gdn_v_dim", 0)
+    if cls == "gdn_core":   # the recurrent state read once, each row's state written to its slot
+        return nv * dk * dv * 4 * (1 + M)
+    if cls == "gdn_qkvz":
+        return (2 * nk * dk + 2 * nv * dv) * Q4_ROW(H)
+    if cls == "gdn_out":
+        return H * Q4_ROW(nv * dv)
+    if cls == "gdn_ab":
+        return 2 * nv * H * 2
     return None
 
 
@@ -195,10 +209,64 @@ def calibrate_copy(args):
     print(json.dumps({"copy_bytes": COPY_BYTES, "ms_per_copy": ms, "gbs": 2 * COPY_BYTES / ms / 1e6}))
 
 
+def bench_real(g, args):
+    """The real model's shape: 30 Gated DeltaNet + 10 gated-attention layers, vocab 248,320, int8 KV, ctx 8,192;
+    the chain (M = 5) and the 16-node tree (M = 17): device time of the verify step (graph replays back to back),
+    the kernel classes' times, and the delta rule's launch against its state traffic."""
+    C = REAL
+    m = g.VerifyModel(C)
+    m.randomize(SEED, 0.02, 0.0221, CTX)
+    g.check(g.lib.gv_synchronize())
+    out = {}
+    gdn = [l for l in range(C["n_layers"]) if C["gdn_layers"][l]]
+    for M, parents in ((5, None), (17, tree_parents())):
+        toks = np.array([(7 + 1000 * i) % C["vocab"] for i in range(M)], np.int32)
+
+        def step():
+            m.position = CTX
+            m.verify(toks, parents, want_logits=False)
+
+        for _ in range(3):
+            step()
+        e0 = g.lib.gv_event_record()
+        for _ in range(args.steps):
+            step()
+        e1 = g.lib.gv_event_record()
+        ms = g.lib.gv_event_elapsed_ms(e0, e1) / args.steps
+        per_class = {}
+        for cls, name in enumerate(g.KERNEL_CLASSES):
+            m.time_kernel(cls)
+            for _ in range(3):
+                step()
+            tms, n = m.kernel_time()
+            if n:
+                per_class[name] = round(tms / 3, 4)
+        m.time_kernel(-1)
+        step()
+        core_s = m.replay(g.KERNEL_CLASSES.index("gdn_core"), gdn[0], reps=60) / 1e3
+        core_b = algorithmic_bytes("gdn_core", C, M, [], CTX)
+        out[f"m{M}"] = {"rows": M, "ms_per_verify": ms, "verify_steps_per_s": 1e3 / ms,
+                        "kernel_ms_per_step": per_class,
+                        "gdn_core": {"avg_launch_us": core_s * 1e6, "bytes_per_launch": core_b,
+                                     "achieved_gbs": core_b / core_s / 1e9, "frac": core_b / core_s / PEAK_HBM}}
+    m.close()
+    return out
+
+
 def main_config(args):
     import geode_amd as g
 
     g.init(0)
+    if args.config == "real":
+        r = bench_real(g, args)
+        print(json.dumps({"metric": "real-shape verify steps/s (30 GDN + 10 attention layers)",
+                          "value": r["m5"]["verify_steps_per_s"], "unit": "verify-steps/s", "n_gpus": 1,
+                          "steps": args.steps, "higher_is_better": True, "dtype": "int8", "data": "synthetic",
+                          "config": {"workload": "Qwen3.6-35B-A3B shape: 30 Gated DeltaNet (16/32 heads of 128, "
+                                                 "conv 4) + 10 gated-attention layers, 256 experts top-8 + shared, "
+                                                 "vocab 248320, int8 KV, ctx 8192; chain M=5 and tree M=17"},
+                          "detail": r}))
+        return
     if args.config in ("c3", "c5"):
         M = 5 if args.config == "c3" else 512
         ms, touched, byts, flops = bench_moe_block(g, M, 20 if M > 5 else 100)
@@ -232,8 +300,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a 256 MiB device copy, three times: the known traffic that scales HBM byte counters")
-    ap.add_argument("--config", choices=["c4", "c2", "c3", "c5"], default="c4",
-                    help="c4 (default): the verify step; c2 / c3 / c5: the acceptance rules / one MoE block")
+    ap.add_argument("--config", choices=["c4", "c2", "c3", "c5", "real"], default="c4",
+                    help="c4 (default): the verify step; c2 / c3 / c5: the acceptance rules / one MoE block; real: "
+                         "the real model's shape with its Gated DeltaNet layers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the verify step on one GPU only: the step of one sequence does not shard "

@@ -55,6 +55,7 @@ int q4_pack(const float *w, int64_t rows, int64_t cols, unsigned int *scratch_u3
 int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, _Float16 *act,
                  int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st);
 int trace_set_q4(uint64_t *p);   // the gemv kernels' g_trace (q4.hip)
+int trace_set_gdn(uint64_t *p);  // the Gated DeltaNet kernel's g_trace (gdn.hip)
 int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st);
 // the waves a product's K (a multiple of 128) splits over and the 32-value chunks each takes, for ntt 16-row tiles
 // of activations; 0 when one launch cannot take K (more than 8 waves)

@@ -2,6 +2,7 @@
 // step's rows.
 #pragma once
 
+#include "mfma_gemv.hpp"
 #include "model.hpp"
 
 namespace gv {
@@ -219,6 +220,166 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         }
     }
     trace(GV_K_ROUTE, 4);
+}
+
+// The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A
+// workgroup takes 4 rows of the router ([E + 1][H] bf16, the
+// shared expert's gate row last; one a wave) and the tokens in groups of router_tokens(H). Every load is issued
+// first (the rows, the residual rows, the norm weights); the sums of squares, 1 / RMS and x inv (1 + w) (rmsnorm's
+// arithmetic) then come from registers, workgroup b also writing token b's operands for the experts' products, and
+// the normalized rows and the router rows (as fp32) go to LDS for the sums. Each logit is eight partial sums in the
+// reference's fixed order (bf16_row_dots, kernels.cpp:1446-1483), a lane per (token, partial).
+constexpr int kRouterRows = 4;
+__host__ __device__ inline int router_tokens(int H) { return H <= 2048 ? 8 : 4; }
+// the route's LDS in the router's tail: p [kMaxRows][256], ids [kMaxRows][16], cnt / start / slot_of [257]
+constexpr size_t kRouteLds = (static_cast<size_t>(kMaxRows) * 16 + 4 * 260) * 4;
+inline size_t router_lds(int H) {
+    return std::max(static_cast<size_t>(router_tokens(H)) * (H + 8) * 4 + static_cast<size_t>(kRouterRows) * H * 4,
+                    kRouteLds);
+}
+
+
+// The router's rows for workgroup wg (router_kernel's body; also the a / b dots of a Gated DeltaNet layer, gdn.hip):
+// logits [M][E1] of the rows (RMSNorm(x) with norm_w, or x as it is when null) against bf16 rows [wg 4, wg 4 + 4) of w;
+// out_sc1: the logits stored with the sc1 policy (read later in the same launch); act (not null): workgroup wg also
+// writes row wg's operands for the experts' products.
+template <int GPT>   // 8-value groups a thread takes per row: 1 for H <= 2048, 2 up to 4096
+__device__ inline void router_rows(int wg, const uint16_t *__restrict__ w, int E1, int H, const float *__restrict__ x,
+                                   const float *__restrict__ norm_w, float eps, const StepParams *__restrict__ sp,
+                                   float *__restrict__ logits, bool out_sc1, _Float16 *__restrict__ act,
+                                   int64_t act_stride, float *lds_f) {
+    constexpr int TG = GPT == 1 ? 8 : 4;
+    __shared__ double red[4][TG];
+    const int ldh = H + 8;
+    float *hs = lds_f;                 // [TG][ldh] the normalized rows
+    float *ws = hs + TG * ldh;         // [4][H] the router rows as fp32
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    trace(GV_K_ROUTER, 0);
+    const int M = sp->M, r0 = wg * kRouterRows;
+    // Every load is unconditional (indices clamped into the arrays), so that none waits for the ones before it:
+    // the first group's rows (needed first), the norm weights, then the workgroup's router rows (4 x H bf16, 8 a
+    // load, H / 256 loads a thread; rows past E1 read row E1 - 1 and are never used).
+    float xv[TG][GPT][8];
+    const float *zero = reinterpret_cast<const float *>(g_zero_act16);   // 64 KB of zeros
+    auto load_x = [&](int t0) {   // (rows past the group's count: a copy of its last, unused; columns past H: 0)
+        const int nt = min(TG, M - t0);
+#pragma unroll
+        for (int tt = 0; tt < TG; ++tt)
+#pragma unroll
+            for (int q = 0; q < GPT; ++q) {
+                const int g = threadIdx.x + q * 256;
+                const float *src = g < H / 8 ? x + static_cast<int64_t>(t0 + min(tt, nt - 1)) * H + g * 8 : zero;
+                const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
+                const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv[tt][q][i] = t[i];
+            }
+    };
+    load_x(0);
+    float nw[GPT][8];   // 1 + w (no norm: w read from the zeros)
+#pragma unroll
+    for (int q = 0; q < GPT; ++q) {
+        const int g = threadIdx.x + q * 256;
+        const float *src = norm_w && g < H / 8 ? norm_w + g * 8 : zero;
+        const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
+        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);
+    }
+    uint4 wr[GPT * 4];
+#pragma unroll
+    for (int k = 0; k < GPT * 4; ++k) {
+        const int i = min(static_cast<int>(threadIdx.x) + k * 256, 4 * (H / 8) - 1), rr = i / (H / 8), c8 = i % (H / 8);
+        wr[k] = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(min(r0 + rr, E1 - 1)) * H + c8 * 8);
+    }
+    // one group of up to TG rows: 1 / RMS per row (the thread's squares, the wave sums, the waves' in order), the
+    // normalized rows to LDS (and row wg's operands), then the dots
+    auto group = [&](int t0, bool first) {
+        const int nt = min(TG, M - t0);
+        if (!first) __syncthreads();   // the previous group's dots are done with hs and red
+        trace(GV_K_ROUTER, 1);
+#pragma unroll
+        for (int tt = 0; tt < TG; ++tt) {
+            if (tt >= nt) break;   // uniform
+            double ss = 0.0;
+#pragma unroll
+            for (int q = 0; q < GPT; ++q)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += static_cast<double>(xv[tt][q][i]) * static_cast<double>(xv[tt][q][i]);
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave][tt] = ss;
+        }
+        if (first) {   // the router rows to LDS as fp32
+#pragma unroll
+            for (int k = 0; k < GPT * 4; ++k) {
+                const int i = threadIdx.x + k * 256;
+                if (i >= 4 * (H / 8)) break;
+                const uint32_t u[4] = {wr[k].x, wr[k].y, wr[k].z, wr[k].w};
+                float *d = ws + (i / (H / 8)) * H + (i % (H / 8)) * 8;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    d[2 * h] = __uint_as_float(u[h] << 16);
+                    d[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
+                }
+            }
+        }
+        __syncthreads();
+        const int tq = wg - t0;
+#pragma unroll
+        for (int tt = 0; tt < TG; ++tt) {
+            if (tt >= nt) break;
+            const double tot = ((red[0][tt] + red[1][tt]) + red[2][tt]) + red[3][tt];
+            const float inv =
+                norm_w ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(H)), eps)))
+                       : 1.0f;
+#pragma unroll
+            for (int q = 0; q < GPT; ++q) {
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(xv[tt][q][i], inv), nw[q][i]);
+                const int g = threadIdx.x + q * 256;
+                const bool live = g < H / 8;
+                if (live) {
+                    *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                }
+                if (act && tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(wg) * act_stride);
+            }
+        }
+        __syncthreads();
+        trace(GV_K_ROUTER, 2);
+        const int tt = lane / 8, j = lane % 8;
+        const int ra = r0 + wave;
+        if (ra >= E1) return;
+        const float *hr = hs + (tt < nt ? tt : 0) * ldh;
+        const float *wrow = ws + wave * H;
+        float a0 = 0.0f;
+        for (int c0 = j; c0 < H; c0 += 8 * 16) {   // 16 steps' operands read ahead of their sums
+            float hv[16], wv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                hv[u] = hr[c0 + 8 * u];
+                wv[u] = wrow[c0 + 8 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) a0 = __fadd_rn(a0, __fmul_rn(wv[u], hv[u]));
+        }
+        // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7))
+        const float s1 = __fadd_rn(a0, __shfl_down(a0, 4, 64));
+        const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
+        const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
+        if (j == 0 && tt < nt) {
+            const int64_t li = static_cast<int64_t>(t0 + tt) * E1 + ra;
+            if (out_sc1) xstf(logits, static_cast<uint32_t>(li), s3);
+            else logits[li] = s3;
+        }
+    };
+    group(0, true);
+    for (int t0 = TG; t0 < M; t0 += TG) {
+        load_x(t0);
+        group(t0, false);
+    }
+    trace(GV_K_ROUTER, 3);
 }
 
 }  // namespace gv

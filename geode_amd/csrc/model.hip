@@ -516,22 +516,6 @@ __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ l
     route_all(logits, E, K, sp->M, rs, ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
 }
 
-// The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A
-// workgroup takes 4 rows of the router ([E + 1][H] bf16, the
-// shared expert's gate row last; one a wave) and the tokens in groups of router_tokens(H). Every load is issued
-// first (the rows, the residual rows, the norm weights); the sums of squares, 1 / RMS and x inv (1 + w) (rmsnorm's
-// arithmetic) then come from registers, workgroup b also writing token b's operands for the experts' products, and
-// the normalized rows and the router rows (as fp32) go to LDS for the sums. Each logit is eight partial sums in the
-// reference's fixed order (bf16_row_dots, kernels.cpp:1446-1483), a lane per (token, partial).
-constexpr int kRouterRows = 4;
-__host__ __device__ inline int router_tokens(int H) { return H <= 2048 ? 8 : 4; }
-// the route's LDS in the router's tail: p [kMaxRows][256], ids [kMaxRows][16], cnt / start / slot_of [257]
-constexpr size_t kRouteLds = (static_cast<size_t>(kMaxRows) * 16 + 4 * 260) * 4;
-inline size_t router_lds(int H) {
-    return std::max(static_cast<size_t>(router_tokens(H)) * (H + 8) * 4 + static_cast<size_t>(kRouterRows) * H * 4,
-                    kRouteLds);
-}
-
 template <int GPT>   // 8-value groups a thread takes per row: 1 for H <= 2048, 2 up to 4096
 __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict__ w, int E1, int H,
                                                      const float *__restrict__ x, const float *__restrict__ norm_w,
@@ -540,135 +524,8 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
                                                      int64_t act_stride, int route, int E, int K,
                                                      RouteState *__restrict__ rs, int32_t *__restrict__ ids_out,
                                                      int *__restrict__ counter) {
-    constexpr int TG = GPT == 1 ? 8 : 4;
     extern __shared__ float lds_f[];
-    __shared__ double red[4][TG];
-    const int ldh = H + 8;
-    float *hs = lds_f;                 // [TG][ldh] the normalized rows
-    float *ws = hs + TG * ldh;         // [4][H] the router rows as fp32
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    trace(GV_K_ROUTER, 0);
-    const int M = sp->M, r0 = blockIdx.x * kRouterRows;
-    // Every load is unconditional (indices clamped into the arrays), so that none waits for the ones before it:
-    // the first group's rows (needed first), the norm weights, then the workgroup's router rows (4 x H bf16, 8 a
-    // load, H / 256 loads a thread; rows past E1 read row E1 - 1 and are never used).
-    float xv[TG][GPT][8];
-    const float *zero = reinterpret_cast<const float *>(g_zero_act16);   // 64 KB of zeros
-    auto load_x = [&](int t0) {   // (rows past the group's count: a copy of its last, unused; columns past H: 0)
-        const int nt = min(TG, M - t0);
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt)
-#pragma unroll
-            for (int q = 0; q < GPT; ++q) {
-                const int g = threadIdx.x + q * 256;
-                const float *src = g < H / 8 ? x + static_cast<int64_t>(t0 + min(tt, nt - 1)) * H + g * 8 : zero;
-                const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
-                const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) xv[tt][q][i] = t[i];
-            }
-    };
-    load_x(0);
-    float nw[GPT][8];   // 1 + w (no norm: w read from the zeros)
-#pragma unroll
-    for (int q = 0; q < GPT; ++q) {
-        const int g = threadIdx.x + q * 256;
-        const float *src = norm_w && g < H / 8 ? norm_w + g * 8 : zero;
-        const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
-        const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) nw[q][i] = __fadd_rn(1.0f, t[i]);
-    }
-    uint4 wr[GPT * 4];
-#pragma unroll
-    for (int k = 0; k < GPT * 4; ++k) {
-        const int i = min(static_cast<int>(threadIdx.x) + k * 256, 4 * (H / 8) - 1), rr = i / (H / 8), c8 = i % (H / 8);
-        wr[k] = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(min(r0 + rr, E1 - 1)) * H + c8 * 8);
-    }
-    // one group of up to TG rows: 1 / RMS per row (the thread's squares, the wave sums, the waves' in order), the
-    // normalized rows to LDS (and row blockIdx.x's operands), then the dots
-    auto group = [&](int t0, bool first) {
-        const int nt = min(TG, M - t0);
-        if (!first) __syncthreads();   // the previous group's dots are done with hs and red
-        trace(GV_K_ROUTER, 1);
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt) {
-            if (tt >= nt) break;   // uniform
-            double ss = 0.0;
-#pragma unroll
-            for (int q = 0; q < GPT; ++q)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) ss += static_cast<double>(xv[tt][q][i]) * static_cast<double>(xv[tt][q][i]);
-            ss = wave_sum(ss);
-            if (lane == 0) red[wave][tt] = ss;
-        }
-        if (first) {   // the router rows to LDS as fp32
-#pragma unroll
-            for (int k = 0; k < GPT * 4; ++k) {
-                const int i = threadIdx.x + k * 256;
-                if (i >= 4 * (H / 8)) break;
-                const uint32_t u[4] = {wr[k].x, wr[k].y, wr[k].z, wr[k].w};
-                float *d = ws + (i / (H / 8)) * H + (i % (H / 8)) * 8;
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    d[2 * h] = __uint_as_float(u[h] << 16);
-                    d[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
-                }
-            }
-        }
-        __syncthreads();
-        const int tq = static_cast<int>(blockIdx.x) - t0;
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt) {
-            if (tt >= nt) break;
-            const double tot = ((red[0][tt] + red[1][tt]) + red[2][tt]) + red[3][tt];
-            const float inv =
-                norm_w ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / static_cast<double>(H)), eps)))
-                       : 1.0f;
-#pragma unroll
-            for (int q = 0; q < GPT; ++q) {
-                float v[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(xv[tt][q][i], inv), nw[q][i]);
-                const int g = threadIdx.x + q * 256;
-                const bool live = g < H / 8;
-                if (live) {
-                    *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8) = make_float4(v[0], v[1], v[2], v[3]);
-                    *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8 + 4) = make_float4(v[4], v[5], v[6], v[7]);
-                }
-                if (act && tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(blockIdx.x) * act_stride);
-            }
-        }
-        __syncthreads();
-        trace(GV_K_ROUTER, 2);
-        const int tt = lane / 8, j = lane % 8;
-        const int ra = r0 + wave;
-        if (ra >= E1) return;
-        const float *hr = hs + (tt < nt ? tt : 0) * ldh;
-        const float *wrow = ws + wave * H;
-        float a0 = 0.0f;
-        for (int c0 = j; c0 < H; c0 += 8 * 16) {   // 16 steps' operands read ahead of their sums
-            float hv[16], wv[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                hv[u] = hr[c0 + 8 * u];
-                wv[u] = wrow[c0 + 8 * u];
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) a0 = __fadd_rn(a0, __fmul_rn(wv[u], hv[u]));
-        }
-        // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7))
-        const float s1 = __fadd_rn(a0, __shfl_down(a0, 4, 64));
-        const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
-        const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
-        if (j == 0 && tt < nt) logits[static_cast<int64_t>(t0 + tt) * E1 + ra] = s3;
-    };
-    group(0, true);
-    for (int t0 = TG; t0 < M; t0 += TG) {
-        load_x(t0);
-        group(t0, false);
-    }
-    trace(GV_K_ROUTER, 3);
+    router_rows<GPT>(blockIdx.x, w, E1, H, x, norm_w, eps, sp, logits, false, act, act_stride, lds_f);
     if (!route) return;
     // the last workgroup to finish routes the rows (the others' logits made visible by their fences)
     __shared__ int s_last;
@@ -683,7 +540,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     int *ids = reinterpret_cast<int *>(lds_f);
     int *cnt = ids + kMaxRows * 16, *start = cnt + 260, *slot_of = start + 260;
     unsigned *rows = reinterpret_cast<unsigned *>(slot_of + 260);
-    route_all(logits, E, K, M, rs, ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
+    route_all(logits, E, K, sp->M, rs, ids_out, RouteLds{ids, cnt, start, slot_of, rows, wtot});
 }
 
 // ---------------------------------------------------------------- output projection, router and route in one launch
@@ -1186,11 +1043,12 @@ inline int combine_launch(const float *y, int H, int K, const MixView &mix, int 
 
 // the fused projection + router + route (mixout_kernel) where the shapes fit it: at most 8 rows, hidden <= 2048, the
 // projection's K split over exactly the launch's 8 waves
-inline bool mixout_fits(const Model &m, int M, int &kw) {
+// (o_cols: the output projection's input width, n_heads x head_dim or a Gated DeltaNet layer's nv x dv)
+inline bool mixout_fits(const Model &m, int M, int64_t o_cols, int &kw) {
     const auto &c = m.c;
     if (!m.fused || m.moe_only || M > kMaxRowsMixOut || c.hidden > 2048 || c.hidden % kSuperK || m.E1 > 257) return false;
     int waves = 0;
-    if (!mfma_split(static_cast<int64_t>(c.n_heads) * c.head_dim, 1, waves, kw) || waves != 8) return false;
+    if (!mfma_split(o_cols, 1, waves, kw) || waves != 8) return false;
     return kw == 16 || kw == 8 || kw == 4;
 }
 
@@ -1589,7 +1447,7 @@ int launch_mixout_t(Model &m, LayerW &L, int l, int M, hipStream_t st) {
     MixOutArgs a{};
     a.o = L.o;
     a.act_core = m.act_core;
-    a.core_stride = act_halves(static_cast<int64_t>(c.n_heads) * c.head_dim);
+    a.core_stride = act_halves(L.o.cols);
     a.x = m.x;
     const int64_t ntiles = tiles_rows(H);
     a.o_per = static_cast<int>(tiles_per_wg(ntiles, 8, 1));
@@ -1607,6 +1465,7 @@ int launch_mixout_t(Model &m, LayerW &L, int l, int M, hipStream_t st) {
     a.err = m.err;
     a.n_o = static_cast<int>((ntiles + a.o_per - 1) / a.o_per);
     a.n_r = (m.E1 + 3) / 4;
+    GV_REQUIRE(a.n_o + a.n_r <= kGdnFlagBase, "mixout: more flags than the launch's share of the layer's");
     const size_t lds = mixout_lds(M, m.E1, a.o_per);
     static int granted = 0;
     if (lds_grant(reinterpret_cast<const void *>(&mixout_kernel<KW>), lds, granted) != 0) return -1;
@@ -1634,9 +1493,10 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     if (per_layer && (L.gdn ? attn_cls : gdn_cls)) return 0;
     // classes fused into a neighbour launch nothing and take no events
     int mix_kw = 0;
-    const bool mixout = !L.gdn && mixout_fits(m, M, mix_kw);
+    const bool mixout = mixout_fits(m, M, L.o.cols, mix_kw);
     const bool fused = (cls == GV_K_SWIGLU && m.moe_dec) || (cls == GV_K_ROUTE && m.route_in_router && !m.moe_only) ||
-                       ((cls == GV_K_ROUTER || cls == GV_K_ROUTE) && mixout);
+                       ((cls == GV_K_ROUTER || cls == GV_K_ROUTE) && mixout) || (cls == GV_K_GDN_AB && m.fused) ||
+                       cls == GV_K_GDN_CONV || cls == GV_K_GDN_NORM;   // (the Gated DeltaNet's: in GV_K_GDN_CORE's)
     if (fused) return 0;
     Tick tk(m, fused ? -2 : cls, st);
     switch (cls) {
@@ -1672,10 +1532,8 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         GV_CHECK_HIP(hipGetLastError());
         return 0;
     }
-    case GV_K_GDN_CONV:
-    case GV_K_GDN_CORE:
-    case GV_K_GDN_NORM:
-        return gdn_launch(m, L, cls, st);
+    case GV_K_GDN_CORE:   // the conv, the delta rule, the gated norm (and the a / b dots when fused) in one launch
+        return gdn_launch(m, L, l, M, !m.fused, st);
     case GV_K_ROPE:
         hipLaunchKernelGGL(qk_rope_kernel, dim3(M, nh + 2 * nkv), dim3(256), 0, st, m.qkv_out, L.qkv.rows, nh, nkv, hd,
                            c.rope_dim / 2, L.q_norm, L.k_norm, c.eps, m.rope_cos, m.rope_sin, m.sp, m.q16, L.kv,
@@ -2128,6 +1986,7 @@ void gv_model_free(gv_model *g) {
         uint64_t *none = nullptr;
         (void)hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &none, sizeof none);
         (void)trace_set_q4(nullptr);
+        (void)trace_set_gdn(nullptr);
         (void)hipFree(g->m.trace);
     }
     delete g;
@@ -2550,13 +2409,24 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
     // the step's row count and position as the last verify left them
     m.host_sp.pos = m.last_pos;
     GV_CHECK_HIP(hipMemcpyAsync(m.sp, &m.host_sp, sizeof(StepParams), hipMemcpyHostToDevice, st));
-    if (launch_class(m, cls, layer, m.last_n, st) != 0) return -1;   // warm
+    // the layers the class launches on (a Gated DeltaNet class: those layers; an attention class: the others),
+    // from `layer` on, cycled
+    std::vector<int> on;
+    const bool gdn_cls = cls >= GV_K_GDN_AB && cls <= GV_K_GDN_NORM;
+    const bool attn_cls = cls == GV_K_ROPE || cls == GV_K_ATTN || cls == GV_K_MERGE;
+    for (int i = 0; i < m.c.n_layers; ++i) {
+        const int l = (layer + i) % m.c.n_layers;
+        const bool gdn = m.layers[static_cast<size_t>(l)].gdn;
+        if (!(gdn_cls && !gdn) && !(attn_cls && gdn)) on.push_back(l);
+    }
+    GV_REQUIRE(!on.empty(), "gv_model_replay: no layer has this kernel class");
+    if (launch_class(m, cls, on[0], m.last_n, st) != 0) return -1;   // warm
     hipEvent_t e0, e1;
     GV_CHECK_HIP(hipEventCreate(&e0));
     GV_CHECK_HIP(hipEventCreate(&e1));
     GV_CHECK_HIP(hipEventRecord(e0, st));
-    int rc = 0;   // launch i on layer (layer + i) mod n_layers: each launch reads other weights than the last
-    for (int i = 0; i < reps && rc == 0; ++i) rc = launch_class(m, cls, (layer + i) % m.c.n_layers, m.last_n, st);
+    int rc = 0;   // launch i on the i-th such layer (cycled): each launch reads other weights than the last
+    for (int i = 0; i < reps && rc == 0; ++i) rc = launch_class(m, cls, on[static_cast<size_t>(i) % on.size()], m.last_n, st);
     GV_CHECK_HIP(hipEventRecord(e1, st));
     GV_CHECK_HIP(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -2722,8 +2592,14 @@ int gv_model_trace(gv_model *g, int on) {
         GV_CHECK_HIP(hipMemset(m.trace, 0, bytes));
     }
     uint64_t *p = on ? m.trace : nullptr;
+    // no kernel of the library's stream may run while the pointer changes: the stream is non-blocking, so the
+    // symbol copies below would not wait for it, and a kernel reading the pointer mid-copy may see half of each
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    GV_CHECK_HIP(hipDeviceSynchronize());
     GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));
-    return trace_set_q4(p);
+    const int rc = trace_set_q4(p) != 0 ? -1 : trace_set_gdn(p);
+    GV_CHECK_HIP(hipDeviceSynchronize());
+    return rc;
 }
 
 int64_t gv_model_trace_read(gv_model *g, uint64_t *out, int64_t n) {

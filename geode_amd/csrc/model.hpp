@@ -150,6 +150,7 @@ struct Model {
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
 constexpr int kFlagsPerLayer = 1024;   // flag words a layer's fused launches have (one a producer workgroup)
+constexpr int kGdnFlagBase = 512;      // the Gated DeltaNet launch's: words [512, 1024); the output projection's below
 
 // the model behind a C-ABI handle (model.hip), for the entry points of other files
 Model &model_of(gv_model *g);
@@ -159,7 +160,8 @@ bool gdn_shape_ok(const gv_model_config &c, std::string &why);
 int64_t gdn_conv_dim(const gv_model_config &c);
 int64_t gdn_s_floats(const gv_model_config &c);   // a slot's recurrent state
 int64_t gdn_c_floats(const gv_model_config &c);   // a slot's conv state
-int gdn_launch(Model &m, LayerW &L, int cls, hipStream_t st);   // GV_K_GDN_CONV, _CORE, _NORM
+// the layer after its projections in one launch (ab_given: the a / b dots already in rlogits, launched apart)
+int gdn_launch(Model &m, LayerW &L, int l, int M, bool ab_given, hipStream_t st);
 int gdn_put_state(Model &m, LayerW &L, int slot, const float *conv, const float *S);
 int gdn_get_state(const Model &m, const LayerW &L, int slot, float *conv, float *S);
 

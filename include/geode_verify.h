@@ -206,8 +206,9 @@ int gv_model_trace(gv_model *m, int on);
 int64_t gv_model_trace_read(gv_model *m, uint64_t *out, int64_t n);
 int gv_model_time_kernel(gv_model *m, int cls);
 int gv_model_kernel_time(gv_model *m, float *total_ms, int *launches);
-/* Launch kernel class cls reps times back to back on the last verify's rows, launch i on layer (layer + i) mod
- * n_layers (ignored for GV_K_EMBED / GV_K_LM_HEAD), so that consecutive launches read different weights, and return
+/* Launch kernel class cls reps times back to back on the last verify's rows, launch i on the i-th layer from `layer`
+ * on (cycled) that has the class (ignored for GV_K_EMBED / GV_K_LM_HEAD; a GV_K_GDN_* class: the Gated DeltaNet
+ * layers; GV_K_ROPE / _ATTN / _MERGE: the attention layers), so that consecutive launches read different weights, and return
  * the mean milliseconds a launch; a measurement aid with no reference counterpart.
  * The kernels run on the state the last verify left; classes that accumulate (GV_K_O, GV_K_COMBINE) change it, so
  * verify again before trusting the model's state. */

@@ -6,12 +6,17 @@ tokens identical away from near-ties, and the layers' states after the step (con
 1617-1633) followed by the next verify; a tree row equal to the chain of its ancestors; gv_model_layer leaving the
 states as they were.
 
-Routing near-ties: the GPU sums the delta rule's products in another order than the oracle (each lane a quarter of
-the rows, then the quarters), a 1e-7 relative difference that can move an int8 activation code by a step further on
-and so a router logit by ~1e-3. An expert swap is accepted only where the oracle's K-th and (K+1)-th router logits
-are within 0.01 (the oracle's own trace); the swapped row and every row after it are then left out of the logits
-check, and a layer's states out of the state check when a swap came before it. Layer by layer from the same inputs
-the mixer agrees to ~3e-7 (tests/test_gpu_layers.py's method: gv_model_layer on the oracle's trace)."""
+The int8 path's steps: the GPU sums the delta rule's products in another order than the oracle (each lane a quarter
+of the rows, then the quarters) and its exp / log1p are not glibc's, a 1e-7 relative difference that can move an int8
+activation code by a step further on (the output projection's operands: ~5e-4 of that row's mixer output, seen), so a
+row's logits or a router logit by up to ~1e-2. Hence:
+  - logits: within 1e-2 of the int8 CPU path, or, where that misses, the reference's own GPU criterion
+    (engine/src/gpu_check.cpp:80-94): against the exact path (fp32 activations, the oracle's mode 1, from the same
+    states) the GPU's largest error at most 1.5 x the int8 CPU path's + 1e-6 of the exact logits' scale;
+  - routing: an expert swap is accepted only where the oracle's K-th and (K+1)-th router logits are within 0.01 (its
+    own trace); the swapped row and every row after it are then left out of the logits check, and a layer's states
+    out of the state check when a swap came before it.
+Layer by layer from the same inputs the mixer agrees to ~3e-7 away from such a step (test_layer_by_layer)."""
 import numpy as np
 import pytest
 
@@ -58,15 +63,26 @@ class Pair:
         self.om.position = CTX
         self.gm.position = CTX
 
-    def check_states(self, swapped_before=99):
+    def check_states(self, step=(99, None)):
+        """the GDN layers' states against the oracle's: within STATE_TOL, or (given the exact path's states of the
+        step) no further from those than the oracle's int8 path is (gpu_check.cpp:93); layers after an expert swap
+        are skipped"""
+        swapped_before, exact = step
         for l in GDN_LAYERS:
             if l > swapped_before:
                 continue
             conv, S = self.gm.gdn_state(l)
             oc = self.om.tensor(po.GDN_CONV_ST, l)[0].view(np.float32).reshape(conv.shape)
             os_ = self.om.tensor(po.GDN_S, l)[0].view(np.float32).reshape(S.shape)
-            assert rel_err(conv, oc) <= STATE_TOL, f"layer {l} conv state: {rel_err(conv, oc):.3e}"
-            assert rel_err(S, os_) <= STATE_TOL, f"layer {l} recurrent state: {rel_err(S, os_):.3e}"
+            for what, g, c, e in (("conv", conv, oc, exact and exact[l][0]), ("recurrent", S, os_, exact and exact[l][1])):
+                err = rel_err(g, c)
+                if err <= STATE_TOL:
+                    continue
+                assert e is not None, f"layer {l} {what} state: {err:.3e}"
+                e = e.view(np.float32).reshape(g.shape)
+                e_gpu, e_cpu = np.abs(g - e).max(), np.abs(c - e).max()
+                assert e_gpu <= 1.5 * e_cpu + 1e-6 * np.abs(e).max(), \
+                    f"layer {l} {what} state: {err:.3e}; against the exact path GPU {e_gpu:.3e}, int8 CPU {e_cpu:.3e}"
 
 
 @pytest.fixture(scope="module", params=sorted(SHAPES))
@@ -78,7 +94,16 @@ def pair(gv, request):
 
 def _verify(pair, toks, parents=None):
     """both models' verify; checks the step and returns the first layer with an expert swap (99: none)"""
-    ol, oids, tr = pair.om.verify_trace(toks, parents)
+    om = pair.om
+    pos, snap = om.position, {l: (om.tensor(po.GDN_CONV_ST, l)[0].copy(), om.tensor(po.GDN_S, l)[0].copy())
+                              for l in GDN_LAYERS}
+    exact = om.verify(toks, parents, mode=1)   # the exact path from the same states, then back to them
+    exact_states = {l: (om.tensor(po.GDN_CONV_ST, l)[0].copy(), om.tensor(po.GDN_S, l)[0].copy()) for l in GDN_LAYERS}
+    for l, (cs, st) in snap.items():
+        om.tensor(po.GDN_CONV_ST, l)[0][:] = cs
+        om.tensor(po.GDN_S, l)[0][:] = st
+    om.position = pos
+    ol, oids, tr = om.verify_trace(toks, parents)   # (its KV rows overwrite the exact path's)
     gl = pair.gm.verify(toks, parents=parents)
     gids = pair.gm.route_ids(len(toks))
     margins = route_margins(pair.om, tr)
@@ -86,16 +111,19 @@ def _verify(pair, toks, parents=None):
     for l, r in swaps:
         assert margins[l, r] < TIE, f"experts differ at layer {l} row {r} (router gap {margins[l, r]:.3e})"
     first_row = int(swaps[:, 1].min()) if len(swaps) else len(toks)
-    assert first_row > 0 or len(toks) == 1, "the root row swapped: pick other tokens"
     keep = slice(0, first_row)   # (rows in BFS order: a swapped row's descendants come after it)
     if first_row > 0:
         err = rel_err(gl[keep], ol[keep])
-        assert err <= 1e-2, f"logits max error {err:.3e}"
+        if err > 1e-2:   # gpu_check.cpp:93
+            e_gpu, e_cpu = np.abs(gl[keep] - exact[keep]).max(), np.abs(ol[keep] - exact[keep]).max()
+            ref = np.abs(exact[keep]).max()
+            assert e_gpu <= 1.5 * e_cpu + 1e-6 * ref, \
+                f"logits max error {err:.3e}; against the exact path GPU {e_gpu / ref:.3e}, int8 CPU {e_cpu / ref:.3e}"
         ties = near_tie_rows(ol[keep], 2 * np.abs(gl[keep] - ol[keep]).max())
         for r in range(first_row):
             if r not in ties:
                 assert np.argmax(gl[r]) == np.argmax(ol[r]), f"greedy token differs at row {r}"
-    return int(swaps[:, 0].min()) if len(swaps) else 99
+    return (int(swaps[:, 0].min()) if len(swaps) else 99), exact_states
 
 
 def _tokens(n, a=37, b=11):
@@ -117,24 +145,26 @@ def test_tree_verify(pair):
 
 def test_chain_keep_then_verify(pair):
     pair.reset()
-    first = _verify(pair, _tokens(5))
+    first, _ = _verify(pair, _tokens(5))
     pair.om.keep(3)
     pair.gm.keep(3)
-    pair.check_states(first)
-    pair.check_states(min(first, _verify(pair, _tokens(4, 29, 3))))
+    pair.check_states((first, None))
+    second, exact = _verify(pair, _tokens(4, 29, 3))
+    pair.check_states((min(first, second), exact))
 
 
 def test_tree_keep_then_verify(pair):
     pair.reset()
     parents = tree_parents((4, 3))
     toks = _tokens(parents.size, 53, 5)
-    first = _verify(pair, toks, parents)
+    first, _ = _verify(pair, toks, parents)
     path = [0, 2, 9]
     assert parents[2] == 0 and parents[9] == 2
     pair.om.keep(3, path)
     pair.gm.keep(3, path)
-    pair.check_states(first)
-    pair.check_states(min(first, _verify(pair, _tokens(5, 31, 7))))
+    pair.check_states((first, None))
+    second, exact = _verify(pair, _tokens(5, 31, 7))
+    pair.check_states((min(first, second), exact))
 
 
 @pytest.mark.parametrize("tree", [False, True])
@@ -177,6 +207,27 @@ def test_one_token_at_a_time_equals_the_chain(pair):
     pair.reset()
     ones = np.concatenate([pair.gm.verify(toks[i:i + 1]) for i in range(5)])
     assert rel_err(ones, whole) <= 1e-5
+
+
+@pytest.mark.parametrize("tree", [False, True])
+def test_fused_launch_equals_the_phases_apart(pair, tree):
+    """the Gated DeltaNet layer's one launch (the a / b dots as its first workgroups) against the a / b dots in a
+    launch of their own (gv_model_set_fused(0)): the same logits and states, bit for bit"""
+    parents = tree_parents((4, 3)) if tree else None
+    toks = _tokens(17 if tree else 5, 43, 2)
+    pair.reset()
+    fused = pair.gm.verify(toks, parents=parents)
+    fs = [pair.gm.gdn_state(l) for l in GDN_LAYERS]
+    pair.gm.set_fused(False)
+    try:
+        pair.reset()
+        apart = pair.gm.verify(toks, parents=parents)
+        ps = [pair.gm.gdn_state(l) for l in GDN_LAYERS]
+    finally:
+        pair.gm.set_fused(True)
+    assert np.array_equal(fused, apart)
+    for (c0, s0), (c1, s1) in zip(fs, ps):
+        assert np.array_equal(c0, c1) and np.array_equal(s0, s1)
 
 
 def test_layer_call_leaves_the_states(pair):
