@@ -48,22 +48,18 @@ __device__ inline float fast_exp(float x) {
 }
 __device__ inline float silu_fast(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, fast_exp(-x))); }   // kernels.hpp:165
 
-// row t's parent: the highest row below t that it sees (-1 for the first row)
-__device__ inline int parent_of(const StepParams *sp, int t) {
-    const uint32_t below = t == 0 ? 0u : (sp->vis[t] & ((1u << t) - 1u));
-    return below ? 31 - __clz(static_cast<int>(below)) : -1;
-}
-
 constexpr int kMaxConvK = 8;
 constexpr int kGdnThreads = 256;
 
-// The recurrent state's device layout: value head vh's [dk][dv] in blocks of 16 columns, a block
-// [dk / 16 (i4)][4 (part)][16 (column)][4 (e)] for rows i = part (dk / 4) + 4 i4 + e: a lane (part, column) of a
-// core wave holds rows part (dk / 4) .. + dk / 4 - 1 of its column, read and written 16 bytes at a time, the wave's
-// 64 lanes 1 KB contiguous.
+// The recurrent state's device layout: value head vh's [dk][dv] in blocks of 16 columns; in a block, column
+// j0 + 4 w + c is held by lanes c 16 .. c 16 + 15 of wave w of a core workgroup, lane part taking rows
+// part rpt .. part rpt + rpt - 1 (rpt = dk / 16), those rows vec (= min(rpt, 4)) floats at a time, a wave's 64 lanes
+// contiguous per load.
 __host__ __device__ inline int64_t s_index(int vh, int i, int j, int dk, int dv) {
-    const int rpt = dk / 4, part = i / rpt, ii = i % rpt, i4 = ii / 4, e = ii % 4, cg = j / 16, col = j % 16;
-    return (static_cast<int64_t>(vh) * (dv / 16) + cg) * dk * 16 + ((i4 * 4 + part) * 16 + col) * 4 + e;
+    const int rpt = dk / 16, vec = rpt < 4 ? rpt : 4;
+    const int cg = j / 16, w = (j % 16) / 4, c = j % 4, part = i / rpt, r = i % rpt, lane = c * 16 + part;
+    return (static_cast<int64_t>(vh) * (dv / 16) + cg) * dk * 16 + static_cast<int64_t>(w) * 64 * rpt +
+           ((r / vec) * 64 + lane) * vec + r % vec;
 }
 
 struct GdnArgs {
@@ -85,144 +81,200 @@ struct GdnArgs {
     int *flags;            // [0, n_ab) the a / b workgroups, [n_ab, n_ab + n_core) the core workgroups
     int *passed;           // the norm workgroups past their waits (the last one clears the flags)
     int *err;
-    int n_ab, n_core, cpw; // a / b workgroups (0: the dots given), core workgroups, value columns a core
-                           // workgroup takes (min(dv, 64))
+    int n_ab, n_core;      // a / b workgroups (0: the dots given), core workgroups
 };
 
-// An a / b workgroup: the bf16 rows [4 wg, 4 wg + 4) of in_proj_a | in_proj_b against RMSNorm(x) of every row
+// An a / b workgroup: bf16 rows [4 dg, 4 dg + 4) of in_proj_a | in_proj_b against RMSNorm(x) of a group of rows
 // (model.cpp:3548-3551, bf16_rows): the router kernel's rows (layer_common.hpp router_rows), the same bits, stored sc1
 __device__ void gdn_ab_role(const GdnArgs &a, int wg, float *lds) {
     trace(GV_K_GDN_CORE, 0);
-    if (a.H <= 2048) router_rows<1>(wg, a.ab_w, 2 * a.nv, a.H, a.x, a.in_norm, a.eps, a.sp, a.ab, true, nullptr, 0, lds);
-    else router_rows<2>(wg, a.ab_w, 2 * a.nv, a.H, a.x, a.in_norm, a.eps, a.sp, a.ab, true, nullptr, 0, lds);
+    // (router_rows<2>: groups of four rows whatever H, its LDS (65 KB at hidden 2048) leaving room for a second
+    // workgroup on the CU; for H <= 2048 the same bits as router_rows<1>: the second 8-value group is zeros)
+    const int n_dg = (2 * a.nv + kRouterRows - 1) / kRouterRows, dg = wg % n_dg, tg = wg / n_dg;   // (rows, tokens)
+    router_rows<2>(dg, tg, 0x7FFF, a.ab_w, 2 * a.nv, a.H, a.x, a.in_norm, a.eps, a.sp, a.ab, true, nullptr, -1, 0, lds);
     trace(GV_K_GDN_CORE, 5);
     signal_done(a.flags + wg);
     trace(GV_K_GDN_CORE, 6);
 }
 
-// the four parts' partial sums of a lane's column (lanes c, c + 16, c + 32, c + 48) on every lane:
-// (p0 + p2) + (p1 + p3), the same bits on each (the additions commute)
-__device__ inline float parts_sum(float v) {
-    const float s = __fadd_rn(v, __shfl_xor(v, 32, 64));
-    return __fadd_rn(s, __shfl_xor(s, 16, 64));
+// the sum of a 16-lane row's values on each of its lanes, the same bits on each (pairs, quads, halves, then the row
+// by DPP: full-rate VALU, no LDS crossbar round trip)
+__device__ inline float row16_sum(float v) {
+    v = __fadd_rn(v, dpp_f<0xB1>(v));    // quad_perm [1, 0, 3, 2]
+    v = __fadd_rn(v, dpp_f<0x4E>(v));    // quad_perm [2, 3, 0, 1]
+    v = __fadd_rn(v, dpp_f<0x141>(v));   // row_half_mirror
+    return __fadd_rn(v, dpp_f<0x140>(v));   // row_mirror
 }
 
-// A core workgroup: value head vh, value columns j0 .. j0 + cpw - 1 (a wave each 16 of them); the channels it reads:
-// q and k of the head's key head and its own v columns.
-//  1. the raw conv inputs of every row and the base slot's conv state for those channels into LDS;
-//  2. the causal conv (model.cpp:3558-3584), a thread a channel, the rows from the last to the first (in place: a
-//     row's window is its ancestors' raw inputs, newest first, then the base state's): w . window in order, silu;
-//     each row's new conv state (its window after it) to its slot, by one workgroup a channel;
+// the core workgroup's LDS, in floats (M rows, nch channels, K taps)
+__host__ __device__ inline size_t gdn_core_lds_floats(int M, int nch, int K) {
+    return static_cast<size_t>(2 * M + 2 * K) * nch + (4 + (kMaxConvK - 1)) * kMaxRows;
+}
+
+// A core workgroup: value head vh, value columns j0 .. j0 + 15 (wave w: columns j0 + 4 w .. j0 + 4 w + 3, a 16-lane
+// row of the wave each); the channels it reads: q and k of the head's key head and its own 16 v columns (three runs of
+// the projections' row).
+//  1. every load first: the recurrent state of the base slot (registers), the raw conv inputs of every row, the base
+//     slot's conv state and the conv weights of those channels (LDS, 16 bytes a load, batched);
+//  2. the causal conv (model.cpp:3558-3584), a thread a (row, channel), four at a time: the row's window is its
+//     ancestors' raw inputs, newest first, then the base state's; w . window in order, silu; each row's new conv state
+//     (its window after it) to its slot, by one workgroup a channel;
 //  3. q and k L2-normalised per row (q also by 1 / sqrt(dk)), a wave a (row, q | k);
 //  4. the gates from the a / b dots: beta = sigmoid(b), decay = exp(-exp(A_log) softplus(a + dt_bias));
-//  5. the delta rule (model.cpp:3614-3666), a wave a 16 columns x 4 parts of dk / 4 rows, the state in registers:
-//     per row S *= decay, mem = S^T k, delta = (v - mem) beta, S += k delta^T, o = S^T q (each lane's rows in order,
-//     then the parts (p0 + p2) + (p1 + p3)); the row's state to its slot, o to core.
+//  5. the delta rule (model.cpp:3614-3666): lane p of a column's 16 holds rows p RPT .. p RPT + RPT - 1 of the state
+//     (RPT = dk / 16); per row S *= decay, mem = S^T k, delta = (v - mem) beta, S += k delta^T, o = S^T q (each lane's
+//     rows as two interleaved fused multiply-add chains, then the 16 lanes: row16_sum); the row's state to its slot,
+//     o to core.
 template <int RPT>
 __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
+    constexpr int VEC = RPT < 4 ? RPT : 4;
     const StepParams *sp = a.sp;
     const int M = sp->M, base = sp->gdn_base, wset = sp->gdn_wset;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int dk = a.dk, dv = a.dv, kd = a.nk * dk, ncw = dv / a.cpw;
-    const int vh = w / ncw, j0 = (w % ncw) * a.cpw, kh = vh / (a.nv / a.nk), K1 = a.K - 1;
-    const int nch = 2 * dk + a.cpw;
-    float *cv = lds;                    // [M][nch] raw inputs, then the conv outputs (q, k normalised)
-    float *bs = cv + M * nch;           // [K - 1][nch] the base conv state
-    float *gd = bs + K1 * nch;          // [M] decay
+    const int dk = a.dk, dv = a.dv, kd = a.nk * dk, ncw = dv / 16, K = a.K;
+    const int vh = w / ncw, j0 = (w % ncw) * 16, kh = vh / (a.nv / a.nk), K1 = K - 1;
+    const int nch = 2 * dk + 16, n4 = nch / 4;
+    float *cv = lds;                    // [M][nch] the raw conv inputs
+    float *co = cv + M * nch;           // [M][nch] the conv outputs (q, k then normalised)
+    float *bs = co + M * nch;           // [K - 1][nch] the base conv state
+    float *cw = bs + K1 * nch;          // [K][nch] the conv weights, tap-major
+    float *gd = cw + K * nch;           // [M] decay
     float *gb = gd + kMaxRows;          // [M] beta
     int *par = reinterpret_cast<int *>(gb + kMaxRows);   // [M] each row's parent (-1: the base)
     int *anc = par + kMaxRows;          // [M][K - 1] the n-th newest conv input before the row: a row, or -1 - b for
                                         // the base state's entry b
+    uint32_t *vis = reinterpret_cast<uint32_t *>(anc + kMaxRows * (kMaxConvK - 1));   // [M] the rows' visibility masks
+    // the channel of local index lc: q of the key head, k of the key head, then the workgroup's v columns
     auto gch = [&](int lc) { return lc < dk ? kh * dk + lc : lc < 2 * dk ? kd + kh * dk + (lc - dk) : 2 * kd + vh * dv + j0 + (lc - 2 * dk); };
-    // the delta rule's lanes: wave `wave` takes columns j0 + 16 wave ..; its state prefetched first
-    const bool dwave = wave * 16 < a.cpw;
-    const int col = lane & 15, part = lane >> 4, jl = wave * 16 + col, j = j0 + jl;
-    const int64_t blk = (static_cast<int64_t>(vh) * (dv / 16) + j / 16) * dk * 16 + (part * 16 + col) * 4;
+    // the delta rule's lanes: column jl = 4 wave + lane / 16 of the workgroup's, rows part RPT .. of it
+    const int part = lane & 15, jl = wave * 4 + (lane >> 4), j = j0 + jl;
+    const int64_t blk = (static_cast<int64_t>(vh) * ncw + j0 / 16) * dk * 16 + static_cast<int64_t>(wave) * 64 * RPT +
+                        lane * VEC;
     float s[RPT];
     auto load = [&](int slot) {
         const float *src = a.s_slots + slot * a.s_slot_floats + blk;
 #pragma unroll
-        for (int i4 = 0; i4 < RPT / 4; ++i4) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + i4 * 256);
-            s[4 * i4] = v.x, s[4 * i4 + 1] = v.y, s[4 * i4 + 2] = v.z, s[4 * i4 + 3] = v.w;
+        for (int v4 = 0; v4 < RPT / VEC; ++v4) {
+            if constexpr (VEC == 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + v4 * 256);
+                s[4 * v4] = v.x, s[4 * v4 + 1] = v.y, s[4 * v4 + 2] = v.z, s[4 * v4 + 3] = v.w;
+            } else {
+                const float2 v = *reinterpret_cast<const float2 *>(src + v4 * 128);
+                s[2 * v4] = v.x, s[2 * v4 + 1] = v.y;
+            }
+        }
+    };
+    auto store = [&](int slot) {
+        float *dst = a.s_slots + slot * a.s_slot_floats + blk;
+#pragma unroll
+        for (int v4 = 0; v4 < RPT / VEC; ++v4) {
+            if constexpr (VEC == 4)
+                *reinterpret_cast<float4 *>(dst + v4 * 256) = make_float4(s[4 * v4], s[4 * v4 + 1], s[4 * v4 + 2], s[4 * v4 + 3]);
+            else
+                *reinterpret_cast<float2 *>(dst + v4 * 128) = make_float2(s[2 * v4], s[2 * v4 + 1]);
         }
     };
     trace(GV_K_GDN_CORE, 0);
-    if (dwave) load(base);
-    if (tid < M) {   // the rows' parents and conv windows (the ancestors' inputs, then the base state's newest first)
-        par[tid] = parent_of(sp, tid);
+    load(base);
+    // 1. the raw inputs (rows 0 .. M - 1) and the base conv state (K - 1 rows of conv_dim) in 16-byte pieces: a thread
+    // piece c4 of rows r, r + rstep, .. (pieces a row padded to a power of two, so no division), eight loads issued
+    // before their LDS stores; then the conv weights, a thread a channel
+    {
+        const int n4p = 1 << (32 - __clz(n4 - 1)), c4 = tid & (n4p - 1), rstep = kGdnThreads / n4p;
+        const int nrows = M + K1;
+        if (c4 < n4) {
+            const int lc = 4 * c4, gc = gch(lc);
+            for (int r0 = tid / n4p; r0 < nrows; r0 += 8 * rstep) {
+                float4 r[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {   // (past the end: the last row again, not stored)
+                    const int row = min(r0 + u * rstep, nrows - 1);
+                    const float *src = row < M ? a.proj + row * a.ld + gc
+                                               : a.c_slots + base * a.c_slot_floats + static_cast<int64_t>(row - M) * a.conv_dim + gc;
+                    r[u] = *reinterpret_cast<const float4 *>(src);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int row = r0 + u * rstep;
+                    if (row < nrows) *reinterpret_cast<float4 *>((row < M ? cv + row * nch : bs + (row - M) * nch) + lc) = r[u];
+                }
+            }
+        }
+        if (tid < M) vis[tid] = sp->vis[tid];
+        for (int lc = tid; lc < nch; lc += kGdnThreads) {   // conv_w [ch][K] to cw [k][lc]
+            const float *src = a.conv_w + static_cast<int64_t>(gch(lc)) * K;
+            float r[kMaxConvK];
+#pragma unroll
+            for (int k = 0; k < kMaxConvK; ++k) r[k] = src[min(k, K - 1)];
+#pragma unroll
+            for (int k = 0; k < kMaxConvK; ++k)
+                if (k < K) cw[k * nch + lc] = r[k];
+        }
+    }
+    __syncthreads();
+    // the rows' parents (the highest row below each that it sees) and conv windows (the ancestors' inputs, then the
+    // base state's newest first), from the masks in LDS
+    auto parent = [&](int r) {
+        const uint32_t below = r == 0 ? 0u : (vis[r] & ((1u << r) - 1u));
+        return below ? 31 - __clz(static_cast<int>(below)) : -1;
+    };
+    if (tid < M) {
+        par[tid] = parent(tid);
         int r = tid, got = 0;
         for (int n = 1; n <= K1; ++n) {
-            const int p = r >= 0 ? parent_of(sp, r) : -1;
+            const int p = r >= 0 ? parent(r) : -1;
             if (p >= 0) ++got;
             anc[tid * (kMaxConvK - 1) + n - 1] = p >= 0 ? p : -1 - (K1 - (n - got));
             r = p;
         }
     }
-    // 1. raw inputs and the base conv state
-    for (int i = tid; i < M * nch; i += kGdnThreads) {
-        const int t = i / nch, lc = i % nch;
-        cv[i] = a.proj[t * a.ld + gch(lc)];
-    }
-    for (int i = tid; i < K1 * nch; i += kGdnThreads) {
-        const int k = i / nch, lc = i % nch;
-        bs[i] = a.c_slots[base * a.c_slot_floats + static_cast<int64_t>(k) * a.conv_dim + gch(lc)];
-    }
     __syncthreads();
     trace(GV_K_GDN_CORE, 1);
-    // 2. the conv, a thread a channel; the conv state's slots written by one workgroup a channel (q and k: the key
-    // head's first value head's first workgroup)
+    // 2. the conv: the q and k channels a thread each (rows split over the threads left: shifts, no division), the 16
+    // v channels as (row, column) pairs over every thread; each (row, channel) w . window in order, silu; the conv
+    // state's slots written by one workgroup a channel (q and k: the key head's first value head's first workgroup)
     const bool qk_writer = vh % (a.nv / a.nk) == 0 && j0 == 0;
-    for (int lc = tid; lc < nch; lc += kGdnThreads) {
-        const int ch = gch(lc);
-        float wc[kMaxConvK];
+    auto conv_one = [&](int t, int lc, bool writer) {
+        float *dst = a.c_slots + (wset + t) * a.c_slot_floats + gch(lc);
+        float acc = 0.0f;   // w . window (oldest first: the (K - 1 - k)-th newest before row t), then the input
+        for (int k = 0; k < K1; ++k) {
+            const int code = anc[t * (kMaxConvK - 1) + (K1 - 1 - k)];
+            const float v = code >= 0 ? cv[code * nch + lc] : bs[(-1 - code) * nch + lc];
+            acc = __fadd_rn(acc, __fmul_rn(cw[k * nch + lc], v));
+            if (writer && k > 0) dst[static_cast<int64_t>(k - 1) * a.conv_dim] = v;   // the state after the row
+        }
+        const float in = cv[t * nch + lc];
+        acc = __fadd_rn(acc, __fmul_rn(cw[K1 * nch + lc], in));
+        if (writer) dst[static_cast<int64_t>(K1 - 1) * a.conv_dim] = in;
+        co[t * nch + lc] = silu_fast(acc);
+    };
+    {
+        const int qk = 2 * dk, lg = 31 - __clz(qk);   // (a power of two: 64 .. 512)
+        const int per = qk > kGdnThreads ? qk / kGdnThreads : 1;   // channels a thread
+        const int t_first = qk >= kGdnThreads ? 0 : tid >> lg, t_step = qk >= kGdnThreads ? 1 : kGdnThreads >> lg;
+        for (int c = 0; c < per; ++c) {
+            const int lc = qk >= kGdnThreads ? tid + c * kGdnThreads : tid & (qk - 1);
+            for (int t0 = t_first; t0 < M; t0 += 4 * t_step) {
 #pragma unroll
-        for (int k = 0; k < kMaxConvK; ++k) wc[k] = k < a.K ? a.conv_w[static_cast<int64_t>(ch) * a.K + k] : 0.0f;
-        const bool writer = lc >= 2 * dk || qk_writer;
-        for (int t = M - 1; t >= 0; --t) {
-            // the window before row t, newest first (its ancestors' raw inputs, still in place: rows below t; then
-            // the base state's); win(k) the window oldest first (selects, no indexing)
-            float nw[kMaxConvK - 1];
-#pragma unroll
-            for (int n = 1; n < kMaxConvK; ++n) {
-                float v = 0.0f;
-                if (n <= K1) {
-                    const int code = anc[t * (kMaxConvK - 1) + n - 1];
-                    v = code >= 0 ? cv[code * nch + lc] : bs[(-1 - code) * nch + lc];
+                for (int u = 0; u < 4; ++u) {
+                    const int t = t0 + u * t_step;
+                    if (t < M) conv_one(t, lc, qk_writer);
                 }
-                nw[n - 1] = v;
             }
-            auto win = [&](int k) {
-                float v = 0.0f;
+        }
+        for (int p0 = tid; p0 < 16 * M; p0 += 4 * kGdnThreads) {
 #pragma unroll
-                for (int m = 0; m < kMaxConvK - 1; ++m)
-                    if (m == K1 - 1 - k) v = nw[m];
-                return v;
-            };
-            const float in = cv[t * nch + lc];
-            float acc = 0.0f;   // w . window in order, then the row's own input
-#pragma unroll
-            for (int k = 0; k < kMaxConvK - 1; ++k)
-                if (k < K1) acc = __fadd_rn(acc, __fmul_rn(wc[k], win(k)));
-            float wl = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kMaxConvK; ++k)
-                if (k == K1) wl = wc[k];
-            acc = __fadd_rn(acc, __fmul_rn(wl, in));
-            if (writer) {   // the state after the row: the window's last K - 2, then its input
-                float *dst = a.c_slots + (wset + t) * a.c_slot_floats + ch;
-#pragma unroll
-                for (int k = 0; k < kMaxConvK - 1; ++k)
-                    if (k < K1) dst[static_cast<int64_t>(k) * a.conv_dim] = k + 1 < K1 ? win(k + 1) : in;
+            for (int u = 0; u < 4; ++u) {
+                const int p = p0 + u * kGdnThreads;
+                if (p < 16 * M) conv_one(p >> 4, qk + (p & 15), true);
             }
-            cv[t * nch + lc] = silu_fast(acc);
         }
     }
     __syncthreads();
     trace(GV_K_GDN_CORE, 2);
     // 3. the L2 norms: pair p = 2 t + (k ? 1 : 0), a wave a pair
     for (int pr = wave; pr < 2 * M; pr += kGdnThreads / 64) {
-        float *v = cv + (pr >> 1) * nch + (pr & 1) * dk;
+        float *v = co + (pr >> 1) * nch + (pr & 1) * dk;
         float sq = 0.0f;
         for (int e = lane; e < dk; e += 64) sq = __fadd_rn(sq, __fmul_rn(v[e], v[e]));
         const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(wave_sum_f(sq), 1e-6f)));
@@ -243,42 +295,48 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
     }
     __syncthreads();
     // 5. the delta rule
-    if (dwave) {
-        int held = -1;
-        for (int t = 0; t < M; ++t) {
-            const int p = par[t];
-            if (p != held) load(wset + p);
-            const float *row = cv + t * nch;
-            float q[RPT], k[RPT];
+    int held = -1;
+    for (int t = 0; t < M; ++t) {
+        const int p = par[t];
+        if (p != held) load(wset + p);
+        const float *row = co + t * nch;
+        float q[RPT], k[RPT];
 #pragma unroll
-            for (int i4 = 0; i4 < RPT / 4; ++i4) {
-                const float4 qv = *reinterpret_cast<const float4 *>(row + part * RPT + 4 * i4);
-                const float4 kv = *reinterpret_cast<const float4 *>(row + dk + part * RPT + 4 * i4);
-                q[4 * i4] = qv.x, q[4 * i4 + 1] = qv.y, q[4 * i4 + 2] = qv.z, q[4 * i4 + 3] = qv.w;
-                k[4 * i4] = kv.x, k[4 * i4 + 1] = kv.y, k[4 * i4 + 2] = kv.z, k[4 * i4 + 3] = kv.w;
+        for (int v4 = 0; v4 < RPT / VEC; ++v4) {
+            if constexpr (VEC == 4) {
+                const float4 qv = *reinterpret_cast<const float4 *>(row + part * RPT + 4 * v4);
+                const float4 kv = *reinterpret_cast<const float4 *>(row + dk + part * RPT + 4 * v4);
+                q[4 * v4] = qv.x, q[4 * v4 + 1] = qv.y, q[4 * v4 + 2] = qv.z, q[4 * v4 + 3] = qv.w;
+                k[4 * v4] = kv.x, k[4 * v4 + 1] = kv.y, k[4 * v4 + 2] = kv.z, k[4 * v4 + 3] = kv.w;
+            } else {
+                const float2 qv = *reinterpret_cast<const float2 *>(row + part * RPT + 2 * v4);
+                const float2 kv = *reinterpret_cast<const float2 *>(row + dk + part * RPT + 2 * v4);
+                q[2 * v4] = qv.x, q[2 * v4 + 1] = qv.y;
+                k[2 * v4] = kv.x, k[2 * v4 + 1] = kv.y;
             }
-            const float v = row[2 * dk + jl], decay = gd[t], beta = gb[t];
-            float mem = 0.0f;
-#pragma unroll
-            for (int i = 0; i < RPT; ++i) {
-                s[i] = __fmul_rn(s[i], decay);
-                mem = __fadd_rn(mem, __fmul_rn(s[i], k[i]));
-            }
-            const float delta = __fmul_rn(__fsub_rn(v, parts_sum(mem)), beta);
-            float o = 0.0f;
-#pragma unroll
-            for (int i = 0; i < RPT; ++i) {
-                s[i] = __fadd_rn(s[i], __fmul_rn(k[i], delta));
-                o = __fadd_rn(o, __fmul_rn(s[i], q[i]));
-            }
-            o = parts_sum(o);
-            if (part == 0) xstf(a.core, static_cast<uint32_t>(t * a.nv * dv + vh * dv + j), o);
-            float *dst = a.s_slots + (wset + t) * a.s_slot_floats + blk;
-#pragma unroll
-            for (int i4 = 0; i4 < RPT / 4; ++i4)
-                *reinterpret_cast<float4 *>(dst + i4 * 256) = make_float4(s[4 * i4], s[4 * i4 + 1], s[4 * i4 + 2], s[4 * i4 + 3]);
-            held = t;
         }
+        const float v = row[2 * dk + jl], decay = gd[t], beta = gb[t];
+        float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RPT; i += 2) {
+            s[i] = __fmul_rn(s[i], decay);
+            s[i + 1] = __fmul_rn(s[i + 1], decay);
+            m0 = fmaf(s[i], k[i], m0);
+            m1 = fmaf(s[i + 1], k[i + 1], m1);
+        }
+        const float delta = __fmul_rn(__fsub_rn(v, row16_sum(__fadd_rn(m0, m1))), beta);
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RPT; i += 2) {
+            s[i] = fmaf(k[i], delta, s[i]);
+            s[i + 1] = fmaf(k[i + 1], delta, s[i + 1]);
+            o0 = fmaf(s[i], q[i], o0);
+            o1 = fmaf(s[i + 1], q[i + 1], o1);
+        }
+        const float o = row16_sum(__fadd_rn(o0, o1));
+        if (part == 0) xstf(a.core, static_cast<uint32_t>(t * a.nv * dv + vh * dv + j), o);
+        store(wset + t);
+        held = t;
     }
     trace(GV_K_GDN_CORE, 5);
     signal_done(a.flags + a.n_ab + w);
@@ -374,12 +432,16 @@ bool gdn_shape_ok(const gv_model_config &c, std::string &why) {
         why = "the Gated DeltaNet's projections are too wide";
         return false;
     }
-    if (nv * std::max(1, dv / 64) + (2 * nv + 3) / 4 > kFlagsPerLayer - kGdnFlagBase - 1) {
+    if (nv * (dv / 16) + (2 * nv + 3) / 4 * ((c.max_rows + 3) / 4) > kFlagsPerLayer - kGdnFlagBase - 1) {
         why = "too many Gated DeltaNet value heads";
         return false;
     }
     if (c.hidden > 4096) {
         why = "Gated DeltaNet models take hidden up to 4096";
+        return false;
+    }
+    if (gdn_core_lds_floats(c.max_rows, 2 * dk + 16, K) * 4 > 160 * 1024) {
+        why = "max_rows x gdn_k_dim too large for the Gated DeltaNet kernel's LDS";
         return false;
     }
     return true;
@@ -418,19 +480,17 @@ int gdn_launch(Model &m, LayerW &L, int l, int M, bool ab_given, hipStream_t st)
     a.flags = area + kGdnFlagBase;
     a.passed = area + kFlagsPerLayer - 1;
     a.err = m.err;
-    a.cpw = std::min(c.gdn_v_dim, 64);
-    a.n_core = c.gdn_v_heads * (c.gdn_v_dim / a.cpw);
-    a.n_ab = ab_given ? 0 : (2 * c.gdn_v_heads + kRouterRows - 1) / kRouterRows;
-    const int nch = 2 * c.gdn_k_dim + a.cpw;
-    const size_t core_lds = (static_cast<size_t>(M + c.conv_kernel - 1) * nch + 3 * kMaxRows + kMaxRows * (kMaxConvK - 1)) * 4;
-    const size_t ab_lds = ab_given ? 0 : static_cast<size_t>(router_tokens(c.hidden)) * (c.hidden + 8) * 4 +
-                                             static_cast<size_t>(kRouterRows) * c.hidden * 4;
+    a.n_core = c.gdn_v_heads * (c.gdn_v_dim / 16);
+    a.n_ab = ab_given ? 0 : (2 * c.gdn_v_heads + kRouterRows - 1) / kRouterRows * ((M + 3) / 4);   // (router_rows<2>)
+    const int nch = 2 * c.gdn_k_dim + 16;
+    const size_t core_lds = gdn_core_lds_floats(M, nch, c.conv_kernel) * 4;
+    const size_t ab_lds = ab_given ? 0 : static_cast<size_t>(4) * (c.hidden + 8) * 4 + static_cast<size_t>(kRouterRows) * c.hidden * 4;
     const size_t lds = std::max(core_lds, ab_lds);
-    switch (c.gdn_k_dim) {
-    case 32: return launch_gdn_t<8>(a, M, lds, st);
-    case 64: return launch_gdn_t<16>(a, M, lds, st);
-    case 128: return launch_gdn_t<32>(a, M, lds, st);
-    default: return launch_gdn_t<64>(a, M, lds, st);
+    switch (c.gdn_k_dim) {   // (rows a lane holds of its column: dk / 16)
+    case 32: return launch_gdn_t<2>(a, M, lds, st);
+    case 64: return launch_gdn_t<4>(a, M, lds, st);
+    case 128: return launch_gdn_t<8>(a, M, lds, st);
+    default: return launch_gdn_t<16>(a, M, lds, st);
     }
 }
 

@@ -239,15 +239,16 @@ inline size_t router_lds(int H) {
 }
 
 
-// The router's rows for workgroup wg (router_kernel's body; also the a / b dots of a Gated DeltaNet layer, gdn.hip):
-// logits [M][E1] of the rows (RMSNorm(x) with norm_w, or x as it is when null) against bf16 rows [wg 4, wg 4 + 4) of w;
-// out_sc1: the logits stored with the sc1 policy (read later in the same launch); act (not null): workgroup wg also
-// writes row wg's operands for the experts' products.
+// The router's rows for workgroup (wg, token groups tg0, tg0 + tg_step, ..) (router_kernel's body; also the a / b dots
+// of a Gated DeltaNet layer, gdn.hip): logits [M][E1] of the rows (RMSNorm(x) with norm_w, or x as it is when null) of
+// those groups of router_tokens(H) rows against bf16 rows [wg 4, wg 4 + 4) of w; out_sc1: the logits stored with the
+// sc1 policy (read later in the same launch); act (not null) and act_row >= 0: the workgroup also writes row act_row's
+// operands for the experts' products (a row of its groups).
 template <int GPT>   // 8-value groups a thread takes per row: 1 for H <= 2048, 2 up to 4096
-__device__ inline void router_rows(int wg, const uint16_t *__restrict__ w, int E1, int H, const float *__restrict__ x,
-                                   const float *__restrict__ norm_w, float eps, const StepParams *__restrict__ sp,
-                                   float *__restrict__ logits, bool out_sc1, _Float16 *__restrict__ act,
-                                   int64_t act_stride, float *lds_f) {
+__device__ inline void router_rows(int wg, int tg0, int tg_step, const uint16_t *__restrict__ w, int E1, int H,
+                                   const float *__restrict__ x, const float *__restrict__ norm_w, float eps,
+                                   const StepParams *__restrict__ sp, float *__restrict__ logits, bool out_sc1,
+                                   _Float16 *__restrict__ act, int act_row, int64_t act_stride, float *lds_f) {
     constexpr int TG = GPT == 1 ? 8 : 4;
     __shared__ double red[4][TG];
     const int ldh = H + 8;
@@ -275,7 +276,9 @@ __device__ inline void router_rows(int wg, const uint16_t *__restrict__ w, int E
                 for (int i = 0; i < 8; ++i) xv[tt][q][i] = t[i];
             }
     };
-    load_x(0);
+    const int first = tg0 * TG;
+    if (first >= M) return;   // (uniform: no rows for this workgroup)
+    load_x(first);
     float nw[GPT][8];   // 1 + w (no norm: w read from the zeros)
 #pragma unroll
     for (int q = 0; q < GPT; ++q) {
@@ -324,7 +327,7 @@ __device__ inline void router_rows(int wg, const uint16_t *__restrict__ w, int E
             }
         }
         __syncthreads();
-        const int tq = wg - t0;
+        const int tq = act_row - t0;
 #pragma unroll
         for (int tt = 0; tt < TG; ++tt) {
             if (tt >= nt) break;
@@ -343,7 +346,7 @@ __device__ inline void router_rows(int wg, const uint16_t *__restrict__ w, int E
                     *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8) = make_float4(v[0], v[1], v[2], v[3]);
                     *reinterpret_cast<float4 *>(hs + tt * ldh + g * 8 + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 }
-                if (act && tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(wg) * act_stride);
+                if (act && tt == tq) act16_group(v, g, live, act + static_cast<int64_t>(act_row) * act_stride);
             }
         }
         __syncthreads();
@@ -374,8 +377,8 @@ __device__ inline void router_rows(int wg, const uint16_t *__restrict__ w, int E
             else logits[li] = s3;
         }
     };
-    group(0, true);
-    for (int t0 = TG; t0 < M; t0 += TG) {
+    group(first, true);
+    for (int t0 = first + tg_step * TG; t0 < M; t0 += tg_step * TG) {
         load_x(t0);
         group(t0, false);
     }

@@ -523,9 +523,14 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
                                                      float *__restrict__ logits, _Float16 *__restrict__ act,
                                                      int64_t act_stride, int route, int E, int K,
                                                      RouteState *__restrict__ rs, int32_t *__restrict__ ids_out,
-                                                     int *__restrict__ counter) {
+                                                     int *__restrict__ counter, int n_dg) {
+    // workgroup b: router rows 4 (b % n_dg) .., token group b / n_dg; it writes the experts' operands of row
+    // (b / n_dg) TG + b % n_dg (when b % n_dg < TG: every row's by one workgroup, n_dg >= min(M, TG))
     extern __shared__ float lds_f[];
-    router_rows<GPT>(blockIdx.x, w, E1, H, x, norm_w, eps, sp, logits, false, act, act_stride, lds_f);
+    constexpr int TG = GPT == 1 ? 8 : 4;
+    const int dg = static_cast<int>(blockIdx.x) % n_dg, tg = static_cast<int>(blockIdx.x) / n_dg;
+    router_rows<GPT>(dg, tg, 0x7FFF, w, E1, H, x, norm_w, eps, sp, logits, false, act, dg < TG ? tg * TG + dg : -1,
+                     act_stride, lds_f);
     if (!route) return;
     // the last workgroup to finish routes the rows (the others' logits made visible by their fences)
     __shared__ int s_last;
@@ -1515,19 +1520,20 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         return gemv_q4(L.qkv, m.act_h, abH, M, o, st);
     }
     case GV_K_GDN_AB: {   // the bf16 a / b rows . RMSNorm(x) (the router kernel's arithmetic, bf16_rows' sum order)
-        const int E1 = 2 * c.gdn_v_heads, wgs = (E1 + kRouterRows - 1) / kRouterRows;
+        const int E1 = 2 * c.gdn_v_heads, n_dg = (E1 + kRouterRows - 1) / kRouterRows;
+        const int wgs = n_dg * ((M + router_tokens(H) - 1) / router_tokens(H));
         if (H <= 2048) {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.gdn_ab, E1, H, m.x,
                                L.in_norm, c.eps, m.sp, m.rlogits, nullptr, 0, 0, c.n_experts, c.top_k, m.route + l,
-                               nullptr, m.counter);
+                               nullptr, m.counter, n_dg);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.gdn_ab, E1, H, m.x,
                                L.in_norm, c.eps, m.sp, m.rlogits, nullptr, 0, 0, c.n_experts, c.top_k, m.route + l,
-                               nullptr, m.counter);
+                               nullptr, m.counter, n_dg);
         }
         GV_CHECK_HIP(hipGetLastError());
         return 0;
@@ -1552,22 +1558,24 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         o.trace_cls = GV_K_O;
         return gemv_q4(L.o, m.act_core, L.gdn ? act_halves(L.o.cols) : abC, M, o, st);
     }
-    case GV_K_ROUTER: {
-        const int wgs = std::max((m.E1 + kRouterRows - 1) / kRouterRows, M);
+    case GV_K_ROUTER: {   // workgroups: (router row group, token group), each row's operands by one of them
+        const int TG = router_tokens(H);
+        const int n_dg = std::max((m.E1 + kRouterRows - 1) / kRouterRows, std::min(M, TG));
+        const int wgs = n_dg * ((M + TG - 1) / TG);
         if (H <= 2048) {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
                                m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
-                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter);
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
                                m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
-                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter);
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg);
         }
         return 0;
     }
