@@ -1906,6 +1906,10 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
             L.kv = reinterpret_cast<_Float16 *>(kb);
         }
     }
+    for (int l = 0; l < c.n_layers; ++l) (m.layers[static_cast<size_t>(l)].gdn ? m.gdn_layers : m.attn_layers).push_back(l);
+    ok = ok && (m.attn_index = static_cast<int *>(dalloc(m, std::max<size_t>(1, m.attn_layers.size()) * 4)));
+    ok = ok && (m.attn_layers.empty() || hipMemcpy(m.attn_index, m.attn_layers.data(), m.attn_layers.size() * 4,
+                                                   hipMemcpyHostToDevice) == hipSuccess);
     const int Mx = c.max_rows, K = c.top_k;
     m.max_slots = moe_slots_bound(c.n_experts, K, Mx);
     if (m.max_slots > kRouteSlots) return fail("gv_model_create: too many expert slots for the route state");

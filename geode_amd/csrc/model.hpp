@@ -146,6 +146,8 @@ struct Model {
     int max_slots = 0, max_picks = 0;
     float *gdn_core = nullptr;   // [max_rows][nv dv] the delta rule's outputs
     int gdn_base = 0;            // the Gated DeltaNet layers' base slot (StepParams::gdn_base)
+    std::vector<int> attn_layers, gdn_layers;   // the attention / Gated DeltaNet layers' indices, in order
+    int *attn_index = nullptr;   // device copy of attn_layers
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes

@@ -6,12 +6,13 @@
 // part (gen, the images' (kv0, s, gh, gw) x image_cap, the last hidden state, the GDN layers' conv then recurrent
 // states, gen again); at kv_offset (4 KB aligned) the KV cache in blocks of 256 positions, [K, V][attention layer]
 // [256][kv_row] elements, then for an int8 cache the scales [K, V][attention layer][256][kv_heads] floats; positions
-// past the conversation's end are zeros. The model here is attention-only and takes no images: its conv / recurrent
-// parts are empty and its image table zeros.
+// past the conversation's end are zeros. The Gated DeltaNet layers' states are those of the model's base slot: each
+// layer's conv state [conv_dim][K - 1], then each layer's recurrent state with each head in the reference's strips of
+// 16 columns ([dv / 16][dk][16], model.cpp:3649-3656). The model takes no images: the image table is zeros.
 //
 // Device side: one kernel converts a run of whole blocks between the cache's device layout (K [nkv][slots][hd],
-// V [nkv][slots / 64][hd][64], the int8 scales [K, V][nkv][slots]) and the file's, every layer at once; the host
-// moves batches of up to 16 MB of blocks between a device buffer and the file.
+// V [nkv][slots / 64][hd][64], the int8 scales [K, V][nkv][slots]) and the file's, every attention layer at once; the
+// host moves batches of up to 16 MB of blocks between a device buffer and the file.
 #include <algorithm>
 #include <cstddef>
 #include <cstdio>
@@ -86,21 +87,22 @@ Shapes shapes_of(const Model &m) {
     s.elem = m.kv_i8 ? 1 : 2;
     s.kv_row = static_cast<uint32_t>(m.c.n_kv_heads * m.c.head_dim);
     s.scale_bytes = m.kv_i8 ? static_cast<uint32_t>(m.c.n_kv_heads) * 4 : 0;
-    s.block_bytes = 2 * static_cast<uint64_t>(m.c.n_layers) * kStateBlock * (uint64_t{s.kv_row} * s.elem + s.scale_bytes);
+    s.block_bytes = 2 * static_cast<uint64_t>(m.attn_layers.size()) * kStateBlock * (uint64_t{s.kv_row} * s.elem + s.scale_bytes);
     return s;
 }
+uint64_t conv_n_of(const Model &m) { return m.gdn_layers.size() * static_cast<uint64_t>(gdn_c_floats(m.c)); }
+uint64_t gdn_n_of(const Model &m) { return m.gdn_layers.size() * static_cast<uint64_t>(gdn_s_floats(m.c)); }
 
-// Model::fingerprint (state.cpp:227-245): the pack's print folded with the shapes a state holds (the conv and
-// recurrent state sizes are 0 here)
+// Model::fingerprint (state.cpp:227-245): the pack's print folded with the shapes a state holds
 uint64_t fingerprint_of(const Model &m, const gv_state_info &info) {
     const auto &c = m.c;
     const uint64_t shapes[] = {kVersion,
                                m.kv_i8 ? 1u : 2u,
-                               static_cast<uint64_t>(c.n_layers),
+                               static_cast<uint64_t>(m.attn_layers.size()),
                                static_cast<uint64_t>(c.n_kv_heads),
                                static_cast<uint64_t>(c.n_kv_heads) * static_cast<uint64_t>(c.head_dim),
-                               0u,
-                               0u,
+                               conv_n_of(m),
+                               gdn_n_of(m),
                                static_cast<uint64_t>(c.hidden),
                                static_cast<uint64_t>(c.n_layers),
                                info.has_mtp ? 1u : 0u,
@@ -108,12 +110,53 @@ uint64_t fingerprint_of(const Model &m, const gv_state_info &info) {
     return fnv(shapes, sizeof shapes, info.pack_print ? info.pack_print : 1);
 }
 
-// Whole blocks [b0, b0 + nb) of B positions between the device cache and the file's layout at `file`, every layer;
+// the Gated DeltaNet layers' states of the base slot in the file's order and layout (conv of every layer, then the
+// recurrent state of every layer in strips), or back into the base slot
+int gdn_states_io(Model &m, std::vector<float> &conv, std::vector<float> &rec, bool to_file) {
+    const auto &c = m.c;
+    const int nv = c.gdn_v_heads, dk = c.gdn_k_dim, dv = c.gdn_v_dim;
+    const size_t cp = static_cast<size_t>(gdn_c_floats(c)), sp = static_cast<size_t>(gdn_s_floats(c));
+    conv.resize(m.gdn_layers.size() * cp);
+    rec.resize(m.gdn_layers.size() * sp);
+    std::vector<float> S(sp);
+    for (size_t g = 0; g < m.gdn_layers.size(); ++g) {
+        LayerW &L = m.layers[static_cast<size_t>(m.gdn_layers[g])];
+        float *fc = conv.data() + g * cp, *fs = rec.data() + g * sp;
+        if (to_file && gdn_get_state(m, L, m.gdn_base, fc, S.data()) != 0) return -1;
+        for (int h = 0; h < nv; ++h)
+            for (int i = 0; i < dk; ++i)
+                for (int j = 0; j < dv; ++j) {   // (dv is a power of two of at least 16: the strips always apply)
+                    const size_t o = static_cast<size_t>(h) * dk * dv, rows = o + static_cast<size_t>(i) * dv + j;
+                    const size_t strip = o + (static_cast<size_t>(j / 16) * dk + i) * 16 + j % 16;
+                    if (to_file) fs[strip] = S[rows];
+                    else S[rows] = fs[strip];
+                }
+        if (!to_file && gdn_put_state(m, L, m.gdn_base, fc, S.data()) != 0) return -1;
+    }
+    return 0;
+}
+
+// Model::reset's states (model.cpp:1918-1925): every Gated DeltaNet slot zero
+int gdn_zero(Model &m) {
+    const size_t cb = 2 * static_cast<size_t>(m.c.max_rows) * gdn_c_floats(m.c) * 4,
+                 sb = 2 * static_cast<size_t>(m.c.max_rows) * gdn_s_floats(m.c) * 4;
+    for (int l : m.gdn_layers) {
+        LayerW &L = m.layers[static_cast<size_t>(l)];
+        GV_CHECK_HIP(hipMemsetAsync(L.c_slots, 0, cb, stream()));
+        GV_CHECK_HIP(hipMemsetAsync(L.s_slots, 0, sb, stream()));
+    }
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    return 0;
+}
+
+// Whole blocks [b0, b0 + nb) of B positions between the device cache and the file's layout at `file`, every
+// attention layer (n_layers of them, model layer attn_index[l]);
 // positions from `position` on are zeros in the file and left alone on the device. A thread per (block, K/V, layer,
 // position, 16-byte word of the row), then for an int8 cache a thread per (block, K/V, layer, position) for its
 // scales.
 template <typename T, bool TO_FILE>
-__global__ __launch_bounds__(256) void state_blocks_kernel(uint8_t *kv_all, size_t layer_bytes, int n_layers, int nkv,
+__global__ __launch_bounds__(256) void state_blocks_kernel(uint8_t *kv_all, size_t layer_bytes,
+                                                           const int *__restrict__ attn_index, int n_layers, int nkv,
                                                            int hd, int64_t slots, int B, int b0, int nb, int position,
                                                            uint8_t *file) {
     constexpr int E = 16 / sizeof(T);   // elements a word
@@ -135,7 +178,7 @@ __global__ __launch_bounds__(256) void state_blocks_kernel(uint8_t *kv_all, size
     const int l = static_cast<int>((row / B) % n_layers), q = static_cast<int>(row % B);
     const int64_t p = static_cast<int64_t>(b0 + bi) * B + q;
     const bool live = p < position;
-    T *kv = reinterpret_cast<T *>(kv_all + static_cast<size_t>(l) * layer_bytes);
+    T *kv = reinterpret_cast<T *>(kv_all + static_cast<size_t>(attn_index[l]) * layer_bytes);
     if (scale_item) {
         float *fs = reinterpret_cast<float *>(blk + rows * row_bytes) + row * nkv;
         float *sc = reinterpret_cast<float *>(kv + 2 * static_cast<int64_t>(nkv) * slots * hd);
@@ -163,17 +206,18 @@ template <bool TO_FILE>
 void launch_blocks(Model &m, int B, int b0, int nb, int position, uint8_t *dev_file, hipStream_t st) {
     const auto &c = m.c;
     const int E = m.kv_i8 ? 16 : 8;
-    const int64_t per_block = 2 * static_cast<int64_t>(c.n_layers) * B *
-                              (c.n_kv_heads * c.head_dim / E + (m.kv_i8 ? 1 : 0));
+    const int n_attn = static_cast<int>(m.attn_layers.size());
+    const int64_t per_block = 2 * static_cast<int64_t>(n_attn) * B * (c.n_kv_heads * c.head_dim / E + (m.kv_i8 ? 1 : 0));
+    if (per_block == 0) return;   // (no attention layer)
     const int64_t n = per_block * nb;
     const dim3 grid(static_cast<unsigned>((n + 255) / 256)), block(256);
     auto *base = reinterpret_cast<uint8_t *>(m.kv_all);
     if (m.kv_i8)
         hipLaunchKernelGGL((state_blocks_kernel<int8_t, TO_FILE>), grid, block, 0, st, base, m.kv_layer_bytes,
-                           c.n_layers, c.n_kv_heads, c.head_dim, m.slots, B, b0, nb, position, dev_file);
+                           m.attn_index, n_attn, c.n_kv_heads, c.head_dim, m.slots, B, b0, nb, position, dev_file);
     else
         hipLaunchKernelGGL((state_blocks_kernel<_Float16, TO_FILE>), grid, block, 0, st, base, m.kv_layer_bytes,
-                           c.n_layers, c.n_kv_heads, c.head_dim, m.slots, B, b0, nb, position, dev_file);
+                           m.attn_index, n_attn, c.n_kv_heads, c.head_dim, m.slots, B, b0, nb, position, dev_file);
 }
 
 // a file read and written at offsets, in pieces of at most 1 GB
@@ -244,7 +288,6 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
     Model &m = model_of(g);
     const auto &c = m.c;
     GV_REQUIRE(c.head_dim % 16 == 0, "gv_model_save_state: head_dim must be a multiple of 16");
-    GV_REQUIRE(c.gdn_v_heads == 0, "gv_model_save_state: the Gated DeltaNet layers' states are not in the file yet");
     const Shapes s = shapes_of(m);
     StateHeader h{};
     std::memcpy(h.magic, kMagic, sizeof kMagic);
@@ -259,14 +302,14 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
     h.n_images = 0;
     h.image_cap = 16;
     h.kv_elem = s.elem;
-    h.n_attn = static_cast<uint32_t>(c.n_layers);
+    h.n_attn = static_cast<uint32_t>(m.attn_layers.size());
     h.kv_heads = static_cast<uint32_t>(c.n_kv_heads);
     h.kv_row = s.kv_row;
     h.hidden = static_cast<uint32_t>(c.hidden);
     h.has_hidden = info->hidden && info->has_mtp && m.pos > 0 ? 1 : 0;
     h.block = kStateBlock;
-    h.conv_n = 0;
-    h.gdn_n = 0;
+    h.conv_n = conv_n_of(m);
+    h.gdn_n = gdn_n_of(m);
     h.fixed_offset = kHeaderBytes;
     h.block_bytes = s.block_bytes;
     // an append: the file holds an earlier state of this conversation in this shape (state.cpp:283-299); the blocks
@@ -304,10 +347,13 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
         return code;
     };
     {   // the fixed part: gen first; gen last once the rest is on the disk
-        std::vector<uint8_t> head(static_cast<size_t>(L.trail - h.fixed_offset), 0);
+        std::vector<uint8_t> head(static_cast<size_t>(L.conv - h.fixed_offset), 0);
         std::memcpy(head.data(), &h.gen, sizeof h.gen);
         if (h.has_hidden) std::memcpy(head.data() + (L.hidden - h.fixed_offset), info->hidden, size_t{h.hidden} * 4);
-        if (!f.write(h.fixed_offset, head.data(), head.size()) || !f.sync() || !f.write(L.trail, &h.gen, sizeof h.gen))
+        std::vector<float> conv, rec;
+        if (gdn_states_io(m, conv, rec, true) != 0) return fail(GV_STATE_E_IO, "cannot read the layers' states");
+        if (!f.write(h.fixed_offset, head.data(), head.size()) || !f.write(L.conv, conv.data(), conv.size() * 4) ||
+            !f.write(L.gdn, rec.data(), rec.size() * 4) || !f.sync() || !f.write(L.trail, &h.gen, sizeof h.gen))
             return fail(GV_STATE_E_IO, "cannot write the conversation's states");
     }
     const int blocks = (m.pos + kStateBlock - 1) / kStateBlock;
@@ -349,15 +395,17 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
     Model &m = model_of(g);
     const auto &c = m.c;
     GV_REQUIRE(c.head_dim % 16 == 0, "gv_model_load_state: head_dim must be a multiple of 16");
-    GV_REQUIRE(c.gdn_v_heads == 0, "gv_model_load_state: the Gated DeltaNet layers' states are not in the file yet");
-    // whatever the failure, the conversation is empty after it (state.cpp:383-388)
-    m.pos = 0;
-    m.last_n = 0;
-    info->has_hidden = 0;
-    auto refuse = [&](int code, const std::string &e) {
+    // whatever the failure, the conversation is empty after it (state.cpp:376-380: Model::reset, the Gated DeltaNet
+    // states zero)
+    auto reset = [&] {
         m.pos = 0;
         m.last_n = 0;
         info->has_hidden = 0;
+        return gdn_zero(m);
+    };
+    if (reset() != 0) return GV_STATE_E_IO;
+    auto refuse = [&](int code, const std::string &e) {
+        (void)reset();
         set_error("gv_model_load_state: " + e);
         return code;
     };
@@ -367,10 +415,10 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
     std::string e;
     if (!read_header(f, h, e)) return refuse(GV_STATE_E_FORMAT, e);
     const Shapes s = shapes_of(m);
-    if (h.fingerprint != fingerprint_of(m, *info) || h.kv_elem != s.elem || h.n_attn != static_cast<uint32_t>(c.n_layers) ||
-        h.kv_heads != static_cast<uint32_t>(c.n_kv_heads) || h.kv_row != s.kv_row ||
-        h.hidden != static_cast<uint32_t>(c.hidden) || h.conv_n != 0 || h.gdn_n != 0 || h.block == 0 ||
-        h.block > (1u << 24))
+    if (h.fingerprint != fingerprint_of(m, *info) || h.kv_elem != s.elem ||
+        h.n_attn != static_cast<uint32_t>(m.attn_layers.size()) || h.kv_heads != static_cast<uint32_t>(c.n_kv_heads) ||
+        h.kv_row != s.kv_row || h.hidden != static_cast<uint32_t>(c.hidden) || h.conv_n != conv_n_of(m) ||
+        h.gdn_n != gdn_n_of(m) || h.block == 0 || h.block > (1u << 24))
         return refuse(GV_STATE_E_FORMAT, "the conversation was saved by another model or another KV cache format");
     if (h.position < 0 || h.position >= c.max_ctx)
         return refuse(GV_STATE_E_ARG, "the saved conversation (" + std::to_string(h.position) +
@@ -379,7 +427,7 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
     const uint64_t B = h.block;
     const int blocks = static_cast<int>((static_cast<uint64_t>(h.position) + B - 1) / B);
     if (L.fixed_bytes != h.fixed_bytes || L.kv_offset != h.kv_offset || h.n_images > h.image_cap ||
-        h.block_bytes != 2 * static_cast<uint64_t>(c.n_layers) * B * (uint64_t{s.kv_row} * s.elem + s.scale_bytes) ||
+        h.block_bytes != 2 * static_cast<uint64_t>(m.attn_layers.size()) * B * (uint64_t{s.kv_row} * s.elem + s.scale_bytes) ||
         f.size() < h.kv_offset + static_cast<uint64_t>(blocks) * h.block_bytes)
         return refuse(GV_STATE_E_IO, "the saved conversation is cut short");
     uint64_t lead = 0, trail = 0;
@@ -390,6 +438,12 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
         return refuse(GV_STATE_E_FORMAT, "the saved conversation holds images (this model has no vision encoder)");
     if (h.has_hidden && info->hidden && !f.read(L.hidden, info->hidden, size_t{h.hidden} * 4))
         return refuse(GV_STATE_E_IO, "cannot read the last hidden state");
+    {
+        std::vector<float> conv(static_cast<size_t>(h.conv_n)), rec(static_cast<size_t>(h.gdn_n));
+        if (!f.read(L.conv, conv.data(), conv.size() * 4) || !f.read(L.gdn, rec.data(), rec.size() * 4))
+            return refuse(GV_STATE_E_IO, "cannot read the layers' states");
+        if (gdn_states_io(m, conv, rec, false) != 0) return refuse(GV_STATE_E_IO, "cannot copy the layers' states");
+    }
     if (blocks > 0) {
         const size_t bb = static_cast<size_t>(h.block_bytes);
         const int per = static_cast<int>(std::max<size_t>(1, kIoBatch / bb));

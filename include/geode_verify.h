@@ -290,14 +290,16 @@ typedef struct gv_state_info {
 } gv_state_info;
 /* error classes of the two calls (geode_state_save / geode_state_load's GEODE_E_*, engine/src/geode.cpp:490-518) */
 enum { GV_STATE_E_IO = -1, GV_STATE_E_FORMAT = -2, GV_STATE_E_ARG = -3, GV_STATE_E_MEMORY = -4 };
-/* Model::save_state (engine/src/state.cpp:251-371): the conversation (the model's position and its KV rows) to path.
+/* Model::save_state (engine/src/state.cpp:251-371): the conversation (the model's position, its attention layers' KV
+ * rows and its Gated DeltaNet layers' states as the last verify or keep left them) to path.
  * append: path holds an earlier state of the same conversation (fingerprint and conv_id): the fixed part and the
  * blocks from the one holding its last position are written in place, the header last; anything else is written
  * whole to path.tmp and renamed over path. Between verify steps only. */
 int gv_model_save_state(gv_model *m, const char *path, int append, const gv_state_info *info);
 /* Model::load_state (engine/src/state.cpp:373-463): the saved conversation replaces the model's (the position becomes
  * the saved one, nothing to keep); conv_id, extra, rope_delta and has_hidden come back in *info, which also names
- * the pack and flags to check the fingerprint against. On failure the position is 0. */
+ * the pack and flags to check the fingerprint against. On failure the position is 0 and the Gated DeltaNet states
+ * zero (Model::reset). */
 int gv_model_load_state(gv_model *m, const char *path, gv_state_info *info);
 
 /* ------------------------------------------------------------------ sampling and acceptance (C2)

@@ -163,3 +163,74 @@ def test_damaged_files_are_refused(gv, pair, tmp_path, what, kind):
         g2.load_state(path, pack_print=META["pack_print"] + (what == "pack"), has_mtp=True)
     assert e.value.kind == kind
     assert g2.position == 0
+
+
+# a model of Gated DeltaNet layers around an attention layer (its states in the file's fixed part)
+GDN_CFG = dict(CFG, n_layers=3, gdn_k_heads=2, gdn_v_heads=4, gdn_k_dim=32, gdn_v_dim=32, conv_kernel=4,
+               gdn_layers=[1, 0, 1])
+
+
+@pytest.fixture(scope="module", params=[0, 1], ids=["fp16", "int8"])
+def gdn_pair(gv, request):
+    cfg = dict(GDN_CFG, kv_int8=request.param)
+    om = po.Model(cfg, seed=12, router_sigma=SMALL_ROUTER_SIGMA, ctx=300)
+    gm = gv.VerifyModel(cfg)
+    adopt_oracle_model(gm, om, 300)
+    yield om, gm, cfg
+    gm.close()
+
+
+@pytest.mark.parametrize("pos", [0, 300])
+def test_gdn_save_equals_the_oracles(gdn_pair, tmp_path, pos):
+    """the same states and cache (adopted, no step since): the same file byte for byte"""
+    om, gm, _ = gdn_pair
+    om.position = pos
+    gm.position = pos
+    om.save_state(str(tmp_path / "o.geode"), **META)
+    gm.save_state(str(tmp_path / "g.geode"), **META)
+    assert open(tmp_path / "g.geode", "rb").read() == open(tmp_path / "o.geode", "rb").read()
+
+
+def test_gdn_state_round_trips_and_continues(gv, gdn_pair, tmp_path):
+    """a GPU save after a verify and keep (the states of the kept row) loads into a fresh GPU model: its states the
+    same, and the next verify the same bit for bit"""
+    om, gm, cfg = gdn_pair
+    gm.position = 300
+    gm.verify(np.array([4, 8, 15, 16, 23], np.int32))
+    gm.keep(3)
+    path = str(tmp_path / "g.geode")
+    gm.save_state(path, **META)
+    g2 = gv.VerifyModel(cfg)
+    adopt_oracle_model(g2, om, 0)
+    assert g2.load_state(path, pack_print=META["pack_print"], has_mtp=True)["conv_id"] == 123
+    assert g2.position == 303
+    for l in (0, 2):
+        for a, b in zip(gm.gdn_state(l), g2.gdn_state(l)):
+            np.testing.assert_array_equal(a, b)
+    toks = np.array([42, 7, 99], np.int32)
+    np.testing.assert_array_equal(g2.verify(toks), gm.verify(toks))
+    # the file's states read by the format's restatement are the model's
+    buf = open(path, "rb").read()
+    for (conv, S), l in zip(sf.gdn_states(cfg, buf), (0, 2)):
+        g2.position = 303
+        g2.load_state(path, pack_print=META["pack_print"], has_mtp=True)
+        gc, gs = g2.gdn_state(l)
+        np.testing.assert_array_equal(conv, gc)
+        np.testing.assert_array_equal(S, gs)
+    g2.close()
+
+
+def test_gdn_refused_load_leaves_zero_states(gv, gdn_pair, tmp_path):
+    om, gm, cfg = gdn_pair
+    gm.position = 300
+    path = str(tmp_path / "g.geode")
+    gm.save_state(path, **META)
+    g2 = gv.VerifyModel(cfg)
+    adopt_oracle_model(g2, om, 300)
+    with pytest.raises(gv.StateError):
+        g2.load_state(path, pack_print=META["pack_print"] + 1, has_mtp=True)
+    assert g2.position == 0
+    for l in (0, 2):
+        conv, S = g2.gdn_state(l)
+        assert not conv.any() and not S.any()
+    g2.close()

@@ -185,3 +185,92 @@ def test_hidden_only_with_mtp_and_a_position(tmp_path):
     om.save_state(path, has_mtp=True, hidden=np.ones(CFG["hidden"], np.float32))
     assert sf.read_header(open(path, "rb").read())["has_hidden"] == 1
     assert om.load_state(path, has_mtp=True)["hidden"].tolist() == [1.0] * CFG["hidden"]
+
+
+# a model of two Gated DeltaNet layers and an attention layer: its states go in the fixed part (each GDN layer's conv
+# state, then each one's recurrent state in the reference's strips), its KV only for the attention layer
+GDN = dict(CFG, n_layers=3, gdn_k_heads=2, gdn_v_heads=4, gdn_k_dim=32, gdn_v_dim=32, conv_kernel=4,
+           gdn_layers=[1, 0, 1])
+
+
+def _gdn_model(ctx, seed=3, kv_int8=0):
+    return po.Model(dict(GDN, kv_int8=kv_int8), seed=seed, ctx=ctx)
+
+
+def _gdn_parts(om):
+    """(attention layers' rows, scales, GDN layers' (conv, S)) of the oracle model"""
+    c = om.cfg
+    kv_row = c["n_kv_heads"] * c["head_dim"]
+    conv_dim = 2 * c["gdn_k_heads"] * c["gdn_k_dim"] + c["gdn_v_heads"] * c["gdn_v_dim"]
+    rows, scales, gdn = [], [], []
+    for l in range(c["n_layers"]):
+        if c["gdn_layers"][l]:
+            gdn.append((om.tensor(po.GDN_CONV_ST, l)[0].view(np.float32).reshape(conv_dim, c["conv_kernel"] - 1),
+                        om.tensor(po.GDN_S, l)[0].view(np.float32).reshape(c["gdn_v_heads"], c["gdn_k_dim"],
+                                                                           c["gdn_v_dim"])))
+        elif c.get("kv_int8"):
+            rows.append(om.tensor(po.KV8, l)[0].view(np.int8).reshape(2, c["max_ctx"], kv_row))
+            scales.append(om.tensor(po.KVS, l)[0].view(np.float32).reshape(2, c["max_ctx"], c["n_kv_heads"]))
+        else:
+            rows.append(om.tensor(po.KV, l)[0].view(np.uint16).reshape(2, c["max_ctx"], kv_row))
+    return rows, (scales if c.get("kv_int8") else None), gdn
+
+
+def test_strips_are_the_references_layout():
+    """[dv / 16][dk][16] a head: element (i, j) of head h at h dk dv + (j / 16) dk 16 + i 16 + j % 16"""
+    S = np.arange(2 * 8 * 32, dtype=np.float32).reshape(2, 8, 32)
+    flat = sf.strips(S).reshape(-1)
+    for h, i, j in ((0, 0, 0), (0, 3, 17), (1, 7, 31), (1, 5, 2)):
+        assert flat[h * 8 * 32 + (j // 16) * 8 * 16 + i * 16 + j % 16] == S[h, i, j]
+    np.testing.assert_array_equal(sf.unstrips(flat, 2, 8, 32), S)
+
+
+@pytest.mark.parametrize("kv_int8", [0, 1])
+@pytest.mark.parametrize("pos", [0, 300])
+def test_gdn_save_writes_the_format(tmp_path, kv_int8, pos):
+    om = _gdn_model(300, kv_int8=kv_int8)
+    om.position = pos
+    path = str(tmp_path / "s.geode")
+    om.save_state(path, pack_print=99, conv_id=3)
+    rows, scales, gdn = _gdn_parts(om)
+    assert np.abs(gdn[0][1]).max() > 0 and np.abs(gdn[1][0]).max() > 0   # (a conversation's states, not zeros)
+    got = open(path, "rb").read()
+    want = sf.state_bytes(om.cfg, rows, scales, pos, pack_print=99, conv_id=3, gdn=gdn)
+    assert got == want
+    h = sf.read_header(got)
+    assert h["n_attn"] == 1 and h["conv_n"] == 2 * 256 * 3 and h["gdn_n"] == 2 * 4 * 32 * 32
+
+
+@pytest.mark.parametrize("kv_int8", [0, 1])
+def test_gdn_round_trip_continues_identically(tmp_path, kv_int8):
+    a = _gdn_model(300, kv_int8=kv_int8)
+    a.position = 300
+    path = str(tmp_path / "s.geode")
+    a.save_state(path, conv_id=8)
+    b = _gdn_model(0, kv_int8=kv_int8)   # the same weights, zero states and an empty cache
+    assert b.load_state(path)["conv_id"] == 8 and b.position == 300
+    ra, sa, ga = _gdn_parts(a)
+    rb, sb, gb = _gdn_parts(b)
+    np.testing.assert_array_equal(ra[0][:, :300], rb[0][:, :300])
+    for (ca, Sa), (cb, Sb) in zip(ga, gb):
+        np.testing.assert_array_equal(ca, cb)
+        np.testing.assert_array_equal(Sa, Sb)
+    toks = np.array([3, 17, 200, 5], np.int32)
+    np.testing.assert_array_equal(a.verify(toks), b.verify(toks))
+
+
+def test_gdn_refused_load_leaves_zero_states(tmp_path):
+    """Model::reset on a refused load (state.cpp:376-380, model.cpp:1918-1925): the GDN states zero, no position"""
+    a = _gdn_model(300)
+    a.position = 300
+    path = str(tmp_path / "s.geode")
+    a.save_state(path, pack_print=1)
+    b = _gdn_model(300)
+    with pytest.raises(ValueError, match="another model"):
+        b.load_state(path, pack_print=2)
+    assert b.position == 0
+    for conv, S in _gdn_parts(b)[2]:
+        assert not conv.any() and not S.any()
+    # an attention-only model does not take a GDN model's file, nor the other way round
+    with pytest.raises(ValueError, match="another model"):
+        _model(0, ctx=0).load_state(path, pack_print=1)
