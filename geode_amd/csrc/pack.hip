@@ -603,10 +603,9 @@ int gv_pack_model_config(const gv_pack *p, int max_ctx, int max_rows, int kv_int
     GV_REQUIRE(p && out, "gv_pack_model_config: null pointer");
     GV_REQUIRE(p->arch == "qwen35moe", "gv_pack_model_config: the GPU model takes qwen35moe packs (this one is '" +
                                            p->arch + "')");
-    for (int l = 0; l < p->n_layers; ++l)
-        GV_REQUIRE(p->attention[static_cast<size_t>(l)], "gv_pack_model_config: layer " + std::to_string(l) +
-                                                             " is a Gated DeltaNet layer (the GPU model has attention "
-                                                             "layers only)");
+    bool any_gdn = false;
+    for (int l = 0; l < p->n_layers; ++l) any_gdn = any_gdn || !p->attention[static_cast<size_t>(l)];
+    GV_REQUIRE(!any_gdn || p->n_layers <= 256, "gv_pack_model_config: a Gated DeltaNet model of more than 256 layers");
     GV_REQUIRE(p->shared_ff == p->moe_ff, "gv_pack_model_config: the shared expert's width differs from the experts'");
     gv_model_config c{};
     c.hidden = p->hidden;
@@ -625,6 +624,14 @@ int gv_pack_model_config(const gv_pack *p, int max_ctx, int max_rows, int kv_int
     c.max_ctx = max_ctx;
     c.max_rows = max_rows;
     c.kv_int8 = kv_int8;
+    if (any_gdn) {   // ModelConfig's Gated DeltaNet shape (pack.cpp:96-100), the layers not "full_attention"
+        c.gdn_k_heads = p->gdn_k_heads;
+        c.gdn_v_heads = p->gdn_v_heads;
+        c.gdn_k_dim = p->gdn_k_dim;
+        c.gdn_v_dim = p->gdn_v_dim;
+        c.conv_kernel = p->conv_kernel;
+        for (int l = 0; l < p->n_layers; ++l) c.gdn_layers[l] = p->attention[static_cast<size_t>(l)] ? 0 : 1;
+    }
     *out = c;
     return 0;
 }
@@ -686,6 +693,15 @@ int gv_model_load_pack(gv_model *g, const gv_pack *p) {
         GV_REQUIRE(rd.tensor(*t, buf), "gv_model_load_pack: cannot read " + name);
         return 0;
     };
+    // an f32 tensor of count values, whatever its shape (Model::bind_layer's f32, model.cpp:96-104)
+    auto get_f32 = [&](const std::string &name, int64_t count, const Tensor *&t) -> int {
+        t = p->find(name);
+        GV_REQUIRE(t, "gv_model_load_pack: the pack has no " + name);
+        GV_REQUIRE(t->type == T_F32 && t->rows * t->cols == count,
+                   "gv_model_load_pack: " + name + ": expected f32 x " + std::to_string(count));
+        GV_REQUIRE(rd.tensor(*t, buf), "gv_model_load_pack: cannot read " + name);
+        return 0;
+    };
     auto adopt = [&](int kind, int layer, int expert, const void *data, size_t bytes, const float *globals) -> int {
         return gv_model_adopt(g, kind, layer, expert, data, static_cast<int64_t>(bytes), globals);
     };
@@ -695,8 +711,10 @@ int gv_model_load_pack(gv_model *g, const gv_pack *p) {
                                      std::make_pair(std::string("lm_head.weight"), GV_LM_HEAD)}) {
         if (get(name, T_Q4, V, H, t) != 0 || adopt(kind, 0, 0, buf.data(), buf.size(), &t->global) != 0) return -1;
     }
-    if (get("norm.weight", T_F32, 1, H, t) != 0 || adopt(GV_FINAL_NORM, 0, 0, buf.data(), buf.size(), nullptr) != 0)
+    if (get_f32("norm.weight", H, t) != 0 || adopt(GV_FINAL_NORM, 0, 0, buf.data(), buf.size(), nullptr) != 0)
         return -1;
+    const int64_t nk = p->gdn_k_heads, nv = p->gdn_v_heads, dk = p->gdn_k_dim, dv = p->gdn_v_dim, K = p->conv_kernel;
+    const int64_t conv_dim = 2 * nk * dk + nv * dv, vd = nv * dv;
     for (int l = 0; l < p->n_layers; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
         struct F32 {
@@ -704,24 +722,49 @@ int gv_model_load_pack(gv_model *g, const gv_pack *p) {
             int kind;
             int64_t n;
         };
-        for (const F32 &f : {F32{"input_layernorm.weight", GV_IN_NORM, H}, F32{"post_attention_layernorm.weight", GV_POST_NORM, H},
-                             F32{"self_attn.q_norm.weight", GV_Q_NORM, hd}, F32{"self_attn.k_norm.weight", GV_K_NORM, hd}})
-            if (get(pre + f.name, T_F32, 1, f.n, t) != 0 || adopt(f.kind, l, 0, buf.data(), buf.size(), nullptr) != 0)
+        for (const F32 &f : {F32{"input_layernorm.weight", GV_IN_NORM, H}, F32{"post_attention_layernorm.weight", GV_POST_NORM, H}})
+            if (get_f32(pre + f.name, f.n, t) != 0 || adopt(f.kind, l, 0, buf.data(), buf.size(), nullptr) != 0)
                 return -1;
-        // q | k | v rows in one matrix, a global each
         float gl[3];
-        cat.clear();
-        const int64_t qkv_rows[3] = {nh * hd * 2, nkv * hd, nkv * hd};
-        const char *qkv_names[3] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight"};
-        for (int i = 0; i < 3; ++i) {
-            if (get(pre + qkv_names[i], T_Q4, qkv_rows[i], H, t) != 0) return -1;
-            gl[i] = t->global;
-            cat.insert(cat.end(), buf.begin(), buf.end());
+        if (!p->attention[static_cast<size_t>(l)]) {   // a Gated DeltaNet layer (model.cpp:136-146)
+            struct Q {
+                const char *name;
+                int kind;
+                int64_t rows, cols;
+            };
+            for (const Q &q : {Q{"linear_attn.in_proj_qkv.weight", GV_GDN_QKV, conv_dim, H},
+                               Q{"linear_attn.in_proj_z.weight", GV_GDN_Z, vd, H},
+                               Q{"linear_attn.out_proj.weight", GV_GDN_OUT, H, vd}})
+                if (get(pre + q.name, T_Q4, q.rows, q.cols, t) != 0 ||
+                    adopt(q.kind, l, 0, buf.data(), buf.size(), &t->global) != 0)
+                    return -1;
+            for (const auto &[name, kind] : {std::make_pair("linear_attn.in_proj_a.weight", GV_GDN_A),
+                                             std::make_pair("linear_attn.in_proj_b.weight", GV_GDN_B)})
+                if (get(pre + name, T_BF16, nv, H, t) != 0 || adopt(kind, l, 0, buf.data(), buf.size(), nullptr) != 0)
+                    return -1;
+            for (const F32 &f : {F32{"linear_attn.A_log", GV_GDN_ALOG, nv}, F32{"linear_attn.dt_bias", GV_GDN_DTB, nv},
+                                 F32{"linear_attn.conv1d.weight", GV_GDN_CONV, conv_dim * K},
+                                 F32{"linear_attn.norm.weight", GV_GDN_NORM, dv}})
+                if (get_f32(pre + f.name, f.n, t) != 0 || adopt(f.kind, l, 0, buf.data(), buf.size(), nullptr) != 0)
+                    return -1;
+        } else {
+            for (const F32 &f : {F32{"self_attn.q_norm.weight", GV_Q_NORM, hd}, F32{"self_attn.k_norm.weight", GV_K_NORM, hd}})
+                if (get_f32(pre + f.name, f.n, t) != 0 || adopt(f.kind, l, 0, buf.data(), buf.size(), nullptr) != 0)
+                    return -1;
+            // q | k | v rows in one matrix, a global each
+            cat.clear();
+            const int64_t qkv_rows[3] = {nh * hd * 2, nkv * hd, nkv * hd};
+            const char *qkv_names[3] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight"};
+            for (int i = 0; i < 3; ++i) {
+                if (get(pre + qkv_names[i], T_Q4, qkv_rows[i], H, t) != 0) return -1;
+                gl[i] = t->global;
+                cat.insert(cat.end(), buf.begin(), buf.end());
+            }
+            if (adopt(GV_QKV, l, 0, cat.data(), cat.size(), gl) != 0) return -1;
+            if (get(pre + "self_attn.o_proj.weight", T_Q4, H, nh * hd, t) != 0 ||
+                adopt(GV_O, l, 0, buf.data(), buf.size(), &t->global) != 0)
+                return -1;
         }
-        if (adopt(GV_QKV, l, 0, cat.data(), cat.size(), gl) != 0) return -1;
-        if (get(pre + "self_attn.o_proj.weight", T_Q4, H, nh * hd, t) != 0 ||
-            adopt(GV_O, l, 0, buf.data(), buf.size(), &t->global) != 0)
-            return -1;
         if (get(pre + "mlp.gate.weight", T_BF16, p->n_experts, H, t) != 0 ||
             adopt(GV_ROUTER, l, 0, buf.data(), buf.size(), nullptr) != 0)
             return -1;

@@ -248,8 +248,10 @@ void gv_pack_close(gv_pack *p);
 /* FNV-1a 64 of geode.json's bytes (Model::fingerprint's pack print, engine/src/state.cpp:227-238): the pack_print a
  * state file of this pack carries (gv_state_info) */
 uint64_t gv_pack_print(const gv_pack *p);
-/* The GPU model's config from the pack's (and the caller's context, rows and KV format). Fails for what the GPU
- * model does not run: another architecture than qwen35moe, Gated DeltaNet layers, a shared expert of another width. */
+/* The GPU model's config from the pack's (and the caller's context, rows and KV format): the layers that are not
+ * "full_attention" Gated DeltaNet layers with the pack's linear_* shape. Fails for what the GPU model does not run:
+ * another architecture than qwen35moe, a shared expert of another width (gv_model_create refuses the shapes it does
+ * not take). */
 int gv_pack_model_config(const gv_pack *p, int max_ctx, int max_rows, int kv_int8, gv_model_config *out);
 typedef struct gv_pack_tensor_info {
     int32_t type;      /* the reference's DType: 0 f32, 1 bf16, 2 q2, 3 q3, 4 nvfp4, 5 q8, 6 q4, 8 q4i (kernels.hpp:16) */

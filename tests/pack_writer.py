@@ -1,6 +1,7 @@
 """Writes a geode-pack (the format engine/src/pack.cpp:39-308 reads) from the oracle model's tensors, for the pack
-loader's tests: geode.json, dense.bin (every tensor but the experts) and experts.bin (per layer the routed experts'
-blocks, gate_up rows then down rows, pack.cpp:329-333), the experts optionally in the tile8 layout
+loader's tests: geode.json, dense.bin (every tensor but the experts; a Gated DeltaNet layer's linear_attn.* tensors in
+place of its self_attn.* ones) and experts.bin (per layer the routed experts' blocks, gate_up rows then down rows,
+pack.cpp:329-333), the experts optionally in the tile8 layout
 (engine/src/kernels.cpp:971-991, restated in `to_tile8` below and pinned against the reference's own to_tile8 by the
 golden fixture). Tensor names and shapes as Model::bind_layer binds them (engine/src/model.cpp:95-202)."""
 import json
@@ -86,17 +87,33 @@ def write_pack(om, directory, tile8=False, extra_config=None, mutate=None):
     put("lm_head.weight", "q4", (V, H), t, g[0])
     put("norm.weight", "f32", (H,), om.tensor(po.FINAL_NORM)[0])
     layers = []
+    gdn = c.get("gdn_layers", ())
     for l in range(L):
         p = f"layers.{l}."
         put(p + "input_layernorm.weight", "f32", (H,), om.tensor(po.IN_NORM, l)[0])
         put(p + "post_attention_layernorm.weight", "f32", (H,), om.tensor(po.POST_NORM, l)[0])
-        for kind, name, rows in ((po.Q, "q_proj", nh * hd * 2), (po.K, "k_proj", nkv * hd), (po.V, "v_proj", nkv * hd)):
-            t, g = om.tensor(kind, l)
-            put(p + f"self_attn.{name}.weight", "q4", (rows, H), t, g[0])
-        t, g = om.tensor(po.O, l)
-        put(p + "self_attn.o_proj.weight", "q4", (H, nh * hd), t, g[0])
-        put(p + "self_attn.q_norm.weight", "f32", (hd,), om.tensor(po.Q_NORM, l)[0])
-        put(p + "self_attn.k_norm.weight", "f32", (hd,), om.tensor(po.K_NORM, l)[0])
+        if l < len(gdn) and gdn[l]:   # a Gated DeltaNet layer (Model::bind_layer, model.cpp:136-146)
+            nk, nv, dk, dv, K = c["gdn_k_heads"], c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"], c["conv_kernel"]
+            conv_dim, vd = 2 * nk * dk + nv * dv, nv * dv
+            for kind, name, shape in ((po.GDN_QKV, "in_proj_qkv", (conv_dim, H)), (po.GDN_Z, "in_proj_z", (vd, H)),
+                                      (po.GDN_OUT, "out_proj", (H, vd))):
+                t, g = om.tensor(kind, l)
+                put(p + f"linear_attn.{name}.weight", "q4", shape, t, g[0])
+            put(p + "linear_attn.in_proj_a.weight", "bf16", (nv, H), om.tensor(po.GDN_A, l)[0])
+            put(p + "linear_attn.in_proj_b.weight", "bf16", (nv, H), om.tensor(po.GDN_B, l)[0])
+            put(p + "linear_attn.A_log", "f32", (nv,), om.tensor(po.GDN_ALOG, l)[0])
+            put(p + "linear_attn.dt_bias", "f32", (nv,), om.tensor(po.GDN_DTB, l)[0])
+            put(p + "linear_attn.conv1d.weight", "f32", (conv_dim, 1, K), om.tensor(po.GDN_CONV, l)[0])
+            put(p + "linear_attn.norm.weight", "f32", (dv,), om.tensor(po.GDN_NORM, l)[0])
+        else:
+            for kind, name, rows in ((po.Q, "q_proj", nh * hd * 2), (po.K, "k_proj", nkv * hd),
+                                     (po.V, "v_proj", nkv * hd)):
+                t, g = om.tensor(kind, l)
+                put(p + f"self_attn.{name}.weight", "q4", (rows, H), t, g[0])
+            t, g = om.tensor(po.O, l)
+            put(p + "self_attn.o_proj.weight", "q4", (H, nh * hd), t, g[0])
+            put(p + "self_attn.q_norm.weight", "f32", (hd,), om.tensor(po.Q_NORM, l)[0])
+            put(p + "self_attn.k_norm.weight", "f32", (hd,), om.tensor(po.K_NORM, l)[0])
         put(p + "mlp.gate.weight", "bf16", (E, H), om.tensor(po.ROUTER, l)[0])
         put(p + "mlp.shared_expert_gate.weight", "bf16", (1, H), om.tensor(po.SHARED_GATE, l)[0])
         for kind, name, shape in ((po.SH_GATE, "gate_proj", (F, H)), (po.SH_UP, "up_proj", (F, H)),
@@ -121,7 +138,12 @@ def write_pack(om, directory, tile8=False, extra_config=None, mutate=None):
               "num_attention_heads": nh, "num_key_value_heads": nkv, "head_dim": hd,
               "rope_parameters": {"rope_theta": c["rope_theta"], "partial_rotary_factor": c["rope_dim"] / hd},
               "num_experts": E, "num_experts_per_tok": c["top_k"], "moe_intermediate_size": F,
-              "shared_expert_intermediate_size": c["shared_ff"], "layer_types": ["full_attention"] * L}
+              "shared_expert_intermediate_size": c["shared_ff"],
+              "layer_types": ["linear_attention" if l < len(gdn) and gdn[l] else "full_attention" for l in range(L)]}
+    if any(gdn):
+        config.update({"linear_num_key_heads": c["gdn_k_heads"], "linear_num_value_heads": c["gdn_v_heads"],
+                       "linear_key_head_dim": c["gdn_k_dim"], "linear_value_head_dim": c["gdn_v_dim"],
+                       "linear_conv_kernel_dim": c["conv_kernel"]})
     config.update(extra_config or {})
     dense.write(os.path.join(directory, "dense.bin"))
     experts.write(os.path.join(directory, "experts.bin"))

@@ -54,3 +54,33 @@ def test_state_carries_the_pack_print(gv, om, tmp_path):
     with pytest.raises(gv.StateError, match="another model"):
         m.load_state(path, pack_print=pack.print ^ 1)
     assert m.load_state(path, pack_print=pack.print)["conv_id"] == 0 and m.position == 3
+
+
+GDN = dict(SMALL, n_layers=3, gdn_k_heads=2, gdn_v_heads=4, gdn_k_dim=32, gdn_v_dim=32, conv_kernel=4,
+           gdn_layers=[1, 0, 1])
+
+
+@pytest.mark.parametrize("tile8", [False, True], ids=["rows", "tile8"])
+def test_gdn_pack_loads_as_the_direct_adoption(gv, tmp_path, tile8):
+    """a pack with Gated DeltaNet layers (linear_attn.* tensors, layer_types linear_attention): the config's shape
+    and the next verifies (chain, then a tree from the states the chain left) bit-identical to the direct adoption"""
+    om = po.Model(GDN, seed=22, router_sigma=SMALL_ROUTER_SIGMA, ctx=0)
+    write_pack(om, str(tmp_path), tile8=tile8)
+    pack = gv.Pack(str(tmp_path))
+    cfg = pack.model_config(max_ctx=GDN["max_ctx"], max_rows=GDN["max_rows"])
+    for k in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel", "gdn_layers", "n_layers"):
+        assert cfg[k] == GDN[k], k
+    a = gv.VerifyModel(GDN)
+    adopt_oracle_model(a, om, 0)
+    b = gv.VerifyModel(cfg)
+    b.load_pack(pack)
+    toks = np.array([3, 77, 410, 9, 200], np.int32)
+    np.testing.assert_array_equal(b.verify(toks), a.verify(toks))
+    par = tree_parents((4, 3))
+    ttoks = (np.arange(par.size) * 37 % GDN["vocab"]).astype(np.int32)
+    np.testing.assert_array_equal(b.verify(ttoks, par), a.verify(ttoks, par))
+    for l in (0, 2):
+        for x, y in zip(a.gdn_state(l), b.gdn_state(l)):
+            np.testing.assert_array_equal(x, y)
+    a.close()
+    b.close()

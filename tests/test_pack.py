@@ -143,8 +143,24 @@ def test_json_reader_against_pythons(gv, om, tmp_path):
     assert p.tensor("plain")["global"] == np.float32(2.5e-3)
 
 
-def test_gated_deltanet_layers_are_refused_by_the_gpu_config(gv, om, tmp_path):
-    write_pack(om, str(tmp_path), extra_config={"layer_types": ["linear_attention", "full_attention"]})
+GDN_CFG = dict(CFG, n_layers=3, gdn_k_heads=2, gdn_v_heads=4, gdn_k_dim=32, gdn_v_dim=32, conv_kernel=4,
+               gdn_layers=[1, 0, 1])
+
+
+def test_gated_deltanet_pack(gv, tmp_path):
+    """a pack of Gated DeltaNet layers (layer_types "linear_attention", the linear_* shape, pack.cpp:96-100): the
+    GPU config takes its shape and layers, its linear_attn tensors are where the manifest says"""
+    om = po.Model(GDN_CFG, seed=6, ctx=0)
+    m = write_pack(om, str(tmp_path))
     p = gv.Pack(str(tmp_path))
-    with pytest.raises(gv.GeodeError, match="Gated DeltaNet"):
-        p.model_config(96)
+    cfg = p.model_config(96)
+    for k in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel", "gdn_layers"):
+        assert cfg[k] == GDN_CFG[k], k
+    conv = p.tensor("layers.0.linear_attn.conv1d.weight")
+    assert (conv["type"], conv["rows"], conv["cols"]) == ("f32", 256, 4)   # [conv_dim, 1, K]: rows, the rest
+    t = m["tensors"]["layers.2.linear_attn.in_proj_qkv.weight"]
+    got = p.tensor("layers.2.linear_attn.in_proj_qkv.weight")
+    assert (got["rows"], got["cols"], got["offset"]) == (256, 128, t["offset"])
+    assert got["global"] == np.float32(om.tensor(po.GDN_QKV, 2)[1][0])
+    with pytest.raises(gv.GeodeError, match="no layers.0.self_attn"):
+        p.tensor("layers.0.self_attn.q_proj.weight")
