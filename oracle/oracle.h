@@ -89,6 +89,9 @@ typedef struct {
     // per layer 1 for a GDN layer (else gated attention)
     int gdn_k_heads, gdn_v_heads, gdn_k_dim, gdn_v_dim, conv_kernel;
     unsigned char gdn_layers[256];
+    // 1: an MTP layer (model.cpp:175-191): a full-attention layer at index n_layers (its KV after the main layers',
+    // its experts at expert layer n_layers) behind fc, with its own final norm
+    int mtp;
 } orc_config;
 
 // tensor kinds (shared numbering with include/geode_verify.h)
@@ -103,7 +106,10 @@ enum {
     ORC_GDN_QKV = 20, ORC_GDN_Z = 21, ORC_GDN_OUT = 22, ORC_GDN_A = 23, ORC_GDN_B = 24, ORC_GDN_ALOG = 25,
     ORC_GDN_DTB = 26, ORC_GDN_CONV = 27, ORC_GDN_NORM = 28,
     ORC_GDN_CONV_ST = 29,   // the conv's state: [2 kd + vd][K - 1], the last K - 1 inputs oldest first
-    ORC_GDN_S = 30          // the recurrent state: [nv][dk][dv]
+    ORC_GDN_S = 30,         // the recurrent state: [nv][dk][dv]
+    // the MTP layer's own tensors (model.cpp:178-190; its decoder layer's: the kinds above at layer n_layers):
+    // mtp.fc.weight q4 [H][2 H], mtp.norm / pre_fc_norm_embedding / pre_fc_norm_hidden f32 [H]
+    ORC_MTP_FC = 31, ORC_MTP_NORM = 32, ORC_MTP_PRE_E = 33, ORC_MTP_PRE_H = 34
 };
 
 // fast_exp (kernels.hpp:142-163: Cephes' expf, the reduction by ln 2 in two parts and a degree-6 polynomial)
@@ -141,6 +147,23 @@ int orc_model_verify_trace(orc_model *m, const int32_t *tokens, int n, const int
 // kept slots); the position becomes the one before the verify plus kept.
 int orc_model_keep(orc_model *m, int kept, const int32_t *path);
 const orc_config *orc_model_config(const orc_model *m);
+// The last verify's hidden rows after the final norm ([n][hidden], the MTP layer's input; n = the rows written)
+int orc_model_hidden(const orc_model *m, float *out, int max_rows);
+// Model::forward_mtp (model.cpp:4965-5039): n rows at MTP positions pos.., row t the pair (hidden row t, the token
+// after it: toks[t]); hidden NULL = the last verify's final-normed rows (after a keep with a path: the path's rows).
+// The layer's KV goes to slots pos..pos+n-1. logits (may be NULL: a prompt's pass, the KV only): the last row's,
+// over the draft vocabulary when one is set, else the whole vocabulary.
+int orc_model_mtp(orc_model *m, const int32_t *toks, int n, int pos, const float *hidden, int mode, float *logits);
+// Model::draft (model.cpp:1295-1432): forward_mtp, draft = argmax of the last row's logits (the first maximum,
+// mapped through the draft vocabulary), prob = its softmax probability summed in double (softmax_at, :1286-1292).
+// logits may be NULL.
+int orc_model_draft(orc_model *m, const int32_t *toks, int n, int pos, const float *hidden, int mode, float *logits,
+                    int32_t *draft, float *prob);
+// Model::draft_next (model.cpp:1434-1479): one more MTP row at position pos from the last MTP pass's normed output
+// (its last row) and the token tok (the draft it made)
+int orc_model_draft_next(orc_model *m, int32_t tok, int pos, int mode, float *logits, int32_t *draft, float *prob);
+// The draft head (model.cpp:803-827): lm_head's rows of ids[0..n) (draft_vocab.bin); n = 0: the whole vocabulary
+int orc_model_set_draft_vocab(orc_model *m, const int32_t *ids, int n);
 // seconds of the last verify spent in the layers and in the final norm + lm_head
 void orc_model_last_times(const orc_model *m, double *t_layers, double *t_head);
 

@@ -185,8 +185,17 @@ struct orc_model {
     std::vector<uint8_t> embed, lm_head;
     float g_embed = 1, g_lm = 1;
     std::vector<float> final_norm, inv_freq;
-    std::vector<orc::Layer> layers;
+    std::vector<orc::Layer> layers;   // [n_layers] (+ the MTP layer's, index n_layers)
     int pos = 0, last_n = 0, last_pos = 0;
+    // the MTP layer's own tensors (model.cpp:178-190)
+    std::vector<uint8_t> mtp_fc;   // q4 [H][2 H]
+    float g_fc = 1;
+    std::vector<float> mtp_norm, mtp_pre_e, mtp_pre_h;
+    std::vector<float> hid;        // the last verify's final-normed rows [last_n][H] (the MTP layer's input)
+    std::vector<int> hid_rows;     // after a keep with a path: the kept rows (row t of a draft: hid row hid_rows[t])
+    std::vector<float> mtp_out;    // the last MTP pass's last row after mtp.norm (draft_next's hidden state)
+    std::vector<int32_t> draft_ids;     // the draft vocabulary (empty: the whole vocabulary)
+    std::vector<uint8_t> draft_head;    // lm_head's rows of draft_ids
     double t_layers = 0, t_head = 0;
 };
 
@@ -537,7 +546,7 @@ orc_model *orc_model_create(const orc_config *cfg) {
     for (int i = 0; i < half; ++i)   // model.cpp:739-740
         m->inv_freq[static_cast<size_t>(i)] =
             1.0f / std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(c.rope_dim));
-    m->layers.resize(static_cast<size_t>(c.n_layers));
+    m->layers.resize(static_cast<size_t>(c.n_layers + (c.mtp ? 1 : 0)));
     return m.release();
 }
 
@@ -560,7 +569,13 @@ void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma
     m->g_lm = fill_q4(m->lm_head, c.vocab, H, tensor_seed(seed, ORC_LM_HEAD, 0, 0), sigma, fast);
     fill_f32(m->final_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_FINAL_NORM, 0, 0), 0.02f);
     const size_t kv_row = static_cast<size_t>(nkv) * hd;
-    for (int l = 0; l < c.n_layers; ++l) {
+    if (c.mtp) {   // the MTP layer's fc and norms; its decoder layer is filled as layer n_layers below
+        m->g_fc = fill_q4(m->mtp_fc, H, 2 * static_cast<int64_t>(H), tensor_seed(seed, ORC_MTP_FC, 0, 0), sigma, fast);
+        fill_f32(m->mtp_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_MTP_NORM, 0, 0), 0.02f);
+        fill_f32(m->mtp_pre_e, static_cast<size_t>(H), tensor_seed(seed, ORC_MTP_PRE_E, 0, 0), 0.02f);
+        fill_f32(m->mtp_pre_h, static_cast<size_t>(H), tensor_seed(seed, ORC_MTP_PRE_H, 0, 0), 0.02f);
+    }
+    for (int l = 0; l < static_cast<int>(m->layers.size()); ++l) {
         Layer &L = m->layers[static_cast<size_t>(l)];
         fill_f32(L.in_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_IN_NORM, l, 0), 0.02f);
         fill_f32(L.post_norm, static_cast<size_t>(H), tensor_seed(seed, ORC_POST_NORM, l, 0), 0.02f);
@@ -584,7 +599,7 @@ void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma
                 fill_q4(tmp, H, F, tensor_seed(seed, ORC_EXPERT, l, 2 * e + 1), sigma, fast);
             std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e + gu));
         }
-        L.gdn = c.gdn_v_heads > 0 && c.gdn_layers[l] != 0;
+        L.gdn = c.gdn_v_heads > 0 && l < c.n_layers && c.gdn_layers[l] != 0;
         if (L.gdn) {   // the GDN layer's weights, then (a context) its states
             const int nk = c.gdn_k_heads, nv = c.gdn_v_heads, dk = c.gdn_k_dim, dv = c.gdn_v_dim, K = c.conv_kernel;
             const int kd = nk * dk, vd = nv * dv, conv_dim = 2 * kd + vd;
@@ -646,7 +661,13 @@ uint8_t *orc_model_tensor(orc_model *m, int kind, int layer, int expert, int64_t
     if (kind == ORC_EMBED) return ret(m->embed, m->g_embed, 0);
     if (kind == ORC_LM_HEAD) return ret(m->lm_head, m->g_lm, 0);
     if (kind == ORC_FINAL_NORM) return ret(m->final_norm, 0, 0);
-    if (layer < 0 || layer >= m->c.n_layers) return nullptr;
+    if (m->c.mtp) {
+        if (kind == ORC_MTP_FC) return ret(m->mtp_fc, m->g_fc, 0);
+        if (kind == ORC_MTP_NORM) return ret(m->mtp_norm, 0, 0);
+        if (kind == ORC_MTP_PRE_E) return ret(m->mtp_pre_e, 0, 0);
+        if (kind == ORC_MTP_PRE_H) return ret(m->mtp_pre_h, 0, 0);
+    }
+    if (layer < 0 || layer >= static_cast<int>(m->layers.size())) return nullptr;
     Layer &L = m->layers[static_cast<size_t>(layer)];
     switch (kind) {
     case ORC_IN_NORM: return ret(L.in_norm, 0, 0);
@@ -750,6 +771,8 @@ int orc_model_verify_trace(orc_model *m, const int32_t *tokens, int n, const int
     const auto hs = crow_ptrs(h.data(), n, static_cast<size_t>(H));
     auto ls = row_ptrs(logits, n, static_cast<size_t>(c.vocab));
     matmul(m->lm_head.data(), c.vocab, H, m->g_lm, n, hs.data(), ls.data(), mode);
+    m->hid = h;   // the final-normed rows: the MTP layer drafts from them (model.cpp:1580-1585)
+    m->hid_rows.clear();
     const auto t2 = std::chrono::steady_clock::now();
     m->t_layers = std::chrono::duration<double>(t1 - t0).count();
     m->t_head = std::chrono::duration<double>(t2 - t1).count();
@@ -767,7 +790,8 @@ int orc_model_keep(orc_model *m, int kept, const int32_t *path) {
         for (int j = 0; j < kept; ++j)
             if (path[j] < 0 || path[j] >= m->last_n || (j > 0 && path[j] <= path[j - 1])) return -1;
         const size_t nkv = static_cast<size_t>(c.n_kv_heads);
-        for (auto &L : m->layers)
+        for (int l = 0; l < c.n_layers; ++l) {   // (the MTP layer's KV is its own passes', not the verify's)
+            Layer &L = m->layers[static_cast<size_t>(l)];
             for (int kvi = 0; kvi < 2; ++kvi)
                 for (int j = 0; j < kept; ++j) {
                     if (path[j] == j) continue;
@@ -782,9 +806,12 @@ int orc_model_keep(orc_model *m, int kept, const int32_t *path) {
                         std::memmove(base + to * kv_row, base + from * kv_row, kv_row * 2);
                     }
                 }
+        }
     }
     // the Gated DeltaNet layers' states as after the last kept row (model.cpp:1617-1633)
     const int last = path ? path[kept - 1] : kept - 1;
+    m->hid_rows.clear();
+    if (path) m->hid_rows.assign(path, path + kept);
     for (auto &L : m->layers) {
         if (!L.gdn) continue;
         const size_t cs_n = L.conv_st.size(), s_n = L.S.size();
@@ -795,6 +822,112 @@ int orc_model_keep(orc_model *m, int kept, const int32_t *path) {
     }
     m->pos = m->last_pos + kept;
     return 0;
+}
+
+int orc_model_hidden(const orc_model *m, float *out, int max_rows) {
+    const int H = m->c.hidden, n = static_cast<int>(m->hid.size() / static_cast<size_t>(H));
+    const int k = std::min(n, max_rows);
+    std::copy(m->hid.begin(), m->hid.begin() + static_cast<ptrdiff_t>(k) * H, out);
+    return k;
+}
+
+int orc_model_set_draft_vocab(orc_model *m, const int32_t *ids, int n) {
+    const auto &c = m->c;
+    if (n < 0 || (n > 0 && !ids)) return -1;
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= c.vocab) return -1;
+    const size_t rb = q4_row_bytes(c.hidden);
+    m->draft_ids.assign(ids, ids + n);
+    m->draft_head.resize(static_cast<size_t>(n) * rb);
+    for (int i = 0; i < n; ++i)   // model.cpp:812-818: the rows copied in the draft vocabulary's order
+        std::memcpy(m->draft_head.data() + static_cast<size_t>(i) * rb, m->lm_head.data() + static_cast<size_t>(ids[i]) * rb, rb);
+    return 0;
+}
+
+int orc_model_mtp(orc_model *m, const int32_t *toks, int n, int pos, const float *hidden, int mode, float *logits) {
+    const auto &c = m->c;
+    const int H = c.hidden;
+    if (!c.mtp || n <= 0 || pos < 0 || pos + n > c.max_ctx) return -1;
+    for (int t = 0; t < n; ++t)
+        if (toks[t] < 0 || toks[t] >= c.vocab) return -1;
+    std::vector<const float *> hs(static_cast<size_t>(n));
+    for (int t = 0; t < n; ++t) {
+        if (hidden) {
+            hs[static_cast<size_t>(t)] = hidden + static_cast<size_t>(t) * H;
+            continue;
+        }
+        const int r = m->hid_rows.empty() ? t : (t < static_cast<int>(m->hid_rows.size()) ? m->hid_rows[static_cast<size_t>(t)] : -1);
+        if (r < 0 || static_cast<size_t>(r + 1) * H > m->hid.size()) return -1;
+        hs[static_cast<size_t>(t)] = m->hid.data() + static_cast<size_t>(r) * H;
+    }
+    // the layer's input: [RMSNorm(embedding of the next token; 1 + pre_e) | RMSNorm(hidden; 1 + pre_h)], then fc
+    std::vector<float> in(static_cast<size_t>(n) * 2 * H), e(static_cast<size_t>(H));
+    for (int t = 0; t < n; ++t) {
+        float *row = in.data() + static_cast<size_t>(t) * 2 * H;
+        orc_dequant_rows(m->embed.data() + static_cast<size_t>(toks[t]) * q4_row_bytes(H), 1, H, m->g_embed, e.data());
+        rmsnorm(e.data(), m->mtp_pre_e.data(), row, H, c.eps, true);
+        rmsnorm(hs[static_cast<size_t>(t)], m->mtp_pre_h.data(), row + H, H, c.eps, true);
+    }
+    std::vector<float> x(static_cast<size_t>(n) * H), h(x.size()), mix(x.size());
+    {
+        const auto ins = crow_ptrs(in.data(), n, static_cast<size_t>(2 * H));
+        auto xs = row_ptrs(x.data(), n, static_cast<size_t>(H));
+        matmul(m->mtp_fc.data(), H, 2 * H, m->g_fc, n, ins.data(), xs.data(), mode);
+    }
+    // the decoder layer: attention over the MTP layer's own positions (slots pos..), then its MoE
+    Layer &L = m->layers[static_cast<size_t>(c.n_layers)];
+    for (int t = 0; t < n; ++t)
+        rmsnorm(x.data() + static_cast<size_t>(t) * H, L.in_norm.data(), h.data() + static_cast<size_t>(t) * H, H, c.eps, true);
+    attention(*m, L, n, h.data(), pos, nullptr, mode, mix.data());
+    for (int t = 0; t < n; ++t) {
+        float *xr = x.data() + static_cast<size_t>(t) * H;
+        const float *mr = mix.data() + static_cast<size_t>(t) * H;
+        for (int i = 0; i < H; ++i) xr[i] += mr[i];
+        rmsnorm(xr, L.post_norm.data(), h.data() + static_cast<size_t>(t) * H, H, c.eps, true);
+    }
+    std::vector<int> ids(static_cast<size_t>(n) * c.top_k);
+    const orc_moe_weights w = moe_view(*m, L);
+    moe_layer(w, n, h.data(), nullptr, mode, mix.data(), ids.data(), nullptr, nullptr);
+    for (size_t i = 0; i < x.size(); ++i) x[i] += mix[i];
+    if (!logits) return 0;
+    // the last row: mtp.norm, then lm_head (or the draft head)
+    m->mtp_out.resize(static_cast<size_t>(H));
+    rmsnorm(x.data() + static_cast<size_t>(n - 1) * H, m->mtp_norm.data(), m->mtp_out.data(), H, c.eps, true);
+    const bool sub = !m->draft_ids.empty();
+    const float *hp = m->mtp_out.data();
+    matmul(sub ? m->draft_head.data() : m->lm_head.data(), sub ? static_cast<int64_t>(m->draft_ids.size()) : c.vocab, H,
+           m->g_lm, 1, &hp, &logits, mode);
+    return 0;
+}
+
+namespace {
+// argmax (the first maximum, as std::max_element) and softmax_at (model.cpp:1286-1292): 1 / sum exp(double(l - max))
+void pick_draft(const orc_model *m, const float *lg, int32_t *draft, float *prob) {
+    const int rows = m->draft_ids.empty() ? m->c.vocab : static_cast<int>(m->draft_ids.size());
+    int best = 0;
+    for (int i = 1; i < rows; ++i)
+        if (lg[i] > lg[best]) best = i;
+    double sum = 0.0;
+    for (int i = 0; i < rows; ++i) sum += std::exp(static_cast<double>(lg[i] - lg[best]));
+    if (draft) *draft = m->draft_ids.empty() ? best : m->draft_ids[static_cast<size_t>(best)];
+    if (prob) *prob = static_cast<float>(1.0 / sum);
+}
+}  // namespace
+
+int orc_model_draft(orc_model *m, const int32_t *toks, int n, int pos, const float *hidden, int mode, float *logits,
+                    int32_t *draft, float *prob) {
+    std::vector<float> lg(static_cast<size_t>(m->c.vocab));
+    if (orc_model_mtp(m, toks, n, pos, hidden, mode, lg.data()) != 0) return -1;
+    pick_draft(m, lg.data(), draft, prob);
+    const int rows = m->draft_ids.empty() ? m->c.vocab : static_cast<int>(m->draft_ids.size());
+    if (logits) std::copy(lg.begin(), lg.begin() + rows, logits);
+    return 0;
+}
+
+int orc_model_draft_next(orc_model *m, int32_t tok, int pos, int mode, float *logits, int32_t *draft, float *prob) {
+    if (m->mtp_out.empty()) return -1;   // no MTP pass to go on from
+    const std::vector<float> h = m->mtp_out;
+    return orc_model_draft(m, &tok, 1, pos, h.data(), mode, logits, draft, prob);
 }
 
 void orc_model_last_times(const orc_model *m, double *t_layers, double *t_head) {

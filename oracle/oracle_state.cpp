@@ -110,9 +110,10 @@ View view_of(orc_model *m) {
     v.conv_per = static_cast<size_t>(2 * c.gdn_k_heads * c.gdn_k_dim + c.gdn_v_heads * c.gdn_v_dim) *
                  static_cast<size_t>(c.conv_kernel > 0 ? c.conv_kernel - 1 : 0);
     v.s_per = static_cast<size_t>(c.gdn_v_heads) * c.gdn_k_dim * c.gdn_v_dim;
-    for (int l = 0; l < v.c.n_layers; ++l) {
+    // (the MTP layer's KV after the main layers', model.cpp:351)
+    for (int l = 0; l < v.c.n_layers + (c.mtp ? 1 : 0); ++l) {
         int64_t bytes = 0;
-        if (c.gdn_v_heads > 0 && c.gdn_layers[l]) {
+        if (c.gdn_v_heads > 0 && l < c.n_layers && c.gdn_layers[l]) {
             v.conv.push_back(reinterpret_cast<float *>(orc_model_tensor(m, ORC_GDN_CONV_ST, l, 0, &bytes, nullptr)));
             v.S.push_back(reinterpret_cast<float *>(orc_model_tensor(m, ORC_GDN_S, l, 0, &bytes, nullptr)));
             continue;
@@ -169,7 +170,7 @@ float *scale_at(const View &v, int l, int which, int p) {
 uint64_t fingerprint(const View &v, const orc_state_info &info) {   // state.cpp:227-245
     const uint64_t shapes[] = {kVersion, v.elem, static_cast<uint64_t>(v.n_attn), static_cast<uint64_t>(v.c.n_kv_heads),
                                v.kv_row, v.conv_n, v.gdn_n, static_cast<uint64_t>(v.c.hidden),
-                               static_cast<uint64_t>(v.c.n_layers), info.has_mtp ? 1u : 0u, info.has_vision ? 1u : 0u};
+                               static_cast<uint64_t>(v.c.n_layers), info.has_mtp || v.c.mtp ? 1u : 0u, info.has_vision ? 1u : 0u};
     return fnv(shapes, sizeof shapes, info.pack_print ? info.pack_print : 1);
 }
 
@@ -206,7 +207,7 @@ int orc_state_save(orc_model *m, const char *path, int append, const orc_state_i
     h.kv_heads = static_cast<uint32_t>(v.c.n_kv_heads);
     h.kv_row = static_cast<uint32_t>(v.kv_row);
     h.hidden = static_cast<uint32_t>(v.c.hidden);
-    h.has_hidden = info->has_mtp && pos > 0 && info->hidden ? 1 : 0;
+    h.has_hidden = (info->has_mtp || v.c.mtp) && pos > 0 && info->hidden ? 1 : 0;
     h.block = kStateBlock;
     h.conv_n = v.conv_n;
     h.gdn_n = v.gdn_n;

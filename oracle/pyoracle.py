@@ -30,7 +30,7 @@ class Config(_c.Structure):
                [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int), ("attn_block", _c.c_int),
                 ("kv_int8", _c.c_int)] + \
                [(n, _c.c_int) for n in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")] + \
-               [("gdn_layers", _c.c_ubyte * 256)]
+               [("gdn_layers", _c.c_ubyte * 256), ("mtp", _c.c_int)]
 
 
 class MoeWeights(_c.Structure):
@@ -43,6 +43,7 @@ class MoeWeights(_c.Structure):
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, Q, K, V, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, SH_GATE, \
     SH_UP, SH_DOWN, KV, KV8, KVS = range(20)
 GDN_QKV, GDN_Z, GDN_OUT, GDN_A, GDN_B, GDN_ALOG, GDN_DTB, GDN_CONV, GDN_NORM, GDN_CONV_ST, GDN_S = range(20, 31)
+MTP_FC, MTP_NORM, MTP_PRE_E, MTP_PRE_H = range(31, 35)
 
 
 class StateInfo(_c.Structure):
@@ -90,6 +91,11 @@ def _load():
         "orc_model_verify_trace": (_c.c_int, [_P, _P, _c.c_int, _P, _c.c_int, _P, _P, _P]),
         "orc_model_keep": (_c.c_int, [_P, _c.c_int, _P]),
         "orc_model_last_times": (None, [_P, _P, _P]),
+        "orc_model_hidden": (_c.c_int, [_P, _P, _c.c_int]),
+        "orc_model_mtp": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _P, _c.c_int, _P]),
+        "orc_model_draft": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _P, _c.c_int, _P, _P, _P]),
+        "orc_model_draft_next": (_c.c_int, [_P, _c.c_int32, _c.c_int, _c.c_int, _P, _P, _P]),
+        "orc_model_set_draft_vocab": (_c.c_int, [_P, _P, _c.c_int]),
         "orc_sample": (_c.c_int, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _c.c_double]),
         "orc_sample_seeded": (None, [_P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_uint64, _c.c_int, _P]),
         "orc_accept_match": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int, _c.c_int, _P,
@@ -395,6 +401,51 @@ class Model:
         p = np.ascontiguousarray(path, np.int32) if path is not None else None
         if lib.orc_model_keep(self.h, kept, _ptr(p)) != 0:
             raise ValueError("orc_model_keep failed")
+
+    def hidden(self):
+        """the last verify's rows after the final norm [n][hidden] (the MTP layer's input)"""
+        rows = self.cfg.get("max_rows", 32)
+        out = np.empty((rows, self.cfg["hidden"]), np.float32)
+        n = lib.orc_model_hidden(self.h, _ptr(out), rows)
+        return out[:n].copy()
+
+    def _draft_rows(self):
+        return len(self._draft_ids) if getattr(self, "_draft_ids", None) is not None else self.cfg["vocab"]
+
+    def set_draft_vocab(self, ids):
+        """the draft head: lm_head's rows of ids (None or empty: the whole vocabulary)"""
+        a = np.ascontiguousarray(ids if ids is not None else [], np.int32)
+        if lib.orc_model_set_draft_vocab(self.h, _ptr(a), a.size) != 0:
+            raise ValueError("orc_model_set_draft_vocab failed")
+        self._draft_ids = a if a.size else None
+
+    def mtp(self, tokens, pos, hidden=None, mode=0, logits=True):
+        """forward_mtp: the last row's logits over the draft head (None when logits=False: the KV only)"""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        hid = np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
+        lg = np.empty(self._draft_rows(), np.float32) if logits else None
+        if lib.orc_model_mtp(self.h, _ptr(tokens), tokens.size, pos, _ptr(hid), mode, _ptr(lg)) != 0:
+            raise ValueError("orc_model_mtp failed")
+        return lg
+
+    def draft(self, tokens, pos, hidden=None, mode=0):
+        """Model::draft: (draft token, its probability, the last row's logits)"""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        hid = np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
+        lg = np.empty(self._draft_rows(), np.float32)
+        d, p = _c.c_int32(0), _c.c_float(0)
+        if lib.orc_model_draft(self.h, _ptr(tokens), tokens.size, pos, _ptr(hid), mode, _ptr(lg), _c.byref(d),
+                               _c.byref(p)) != 0:
+            raise ValueError("orc_model_draft failed")
+        return d.value, p.value, lg
+
+    def draft_next(self, token, pos, mode=0):
+        """Model::draft_next: (draft token, its probability, logits) from the last MTP pass's output"""
+        lg = np.empty(self._draft_rows(), np.float32)
+        d, p = _c.c_int32(0), _c.c_float(0)
+        if lib.orc_model_draft_next(self.h, int(token), pos, mode, _ptr(lg), _c.byref(d), _c.byref(p)) != 0:
+            raise ValueError("orc_model_draft_next failed")
+        return d.value, p.value, lg
 
     def save_state(self, path, append=False, *, pack_print=0, conv_id=0, extra=0, rope_delta=0, has_mtp=False,
                    has_vision=False, hidden=None):

@@ -93,46 +93,57 @@ class F64Model:
         self.embed = q4(po.EMBED, V, H)
         self.lm = q4(po.LM_HEAD, V, H)
         self.final_norm = om.tensor(po.FINAL_NORM)[0].view(np.float32).astype(np.float64)
-        self.layers = []
+        self.q4 = q4
+        self.layers = [self._layer(l) for l in range(c["n_layers"])]
+        self.mtp_layer = None
+        if c.get("mtp"):   # the MTP layer (model.cpp:175-191): fc, its norms, a decoder layer at index n_layers
+            self.mtp_layer = self._layer(c["n_layers"])
+            self.mtp_fc = q4(po.MTP_FC, H, 2 * H)
+            f32 = lambda kind: om.tensor(kind)[0].view(np.float32).astype(np.float64)   # noqa: E731
+            self.mtp_norm, self.pre_e, self.pre_h = f32(po.MTP_NORM), f32(po.MTP_PRE_E), f32(po.MTP_PRE_H)
+            self.mtp_out = None
+
+    def _layer(self, l):
+        c, om, q4 = self.c, self.om, self.q4
+        H, F, hd, nh, nkv = c["hidden"], c["moe_ff"], c["head_dim"], c["n_heads"], c["n_kv_heads"]
         gu_bytes = 2 * F * po.q4_row_bytes(H)
-        for l in range(c["n_layers"]):
-            L = {}
-            for k, name in ((po.IN_NORM, "in"), (po.POST_NORM, "post"), (po.Q_NORM, "qn"), (po.K_NORM, "kn")):
-                L[name] = om.tensor(k, l)[0].view(np.float32).astype(np.float64)
-            L["q"] = q4(po.Q, nh * 2 * hd, H, l)
-            L["k"] = q4(po.K, nkv * hd, H, l)
-            L["v"] = q4(po.V, nkv * hd, H, l)
-            L["o"] = q4(po.O, H, nh * hd, l)
-            L["router"] = _bf16(om.tensor(po.ROUTER, l)[0].view(np.uint16)).reshape(c["n_experts"], H)
-            L["sgate"] = _bf16(om.tensor(po.SHARED_GATE, l)[0].view(np.uint16))
-            gu, dn = [], []
-            for e in range(c["n_experts"]):
-                blk, g = om.tensor(po.EXPERT, l, e)
-                gu.append(po.dequant(blk[:gu_bytes].reshape(2 * F, -1), H, float(g[0])).astype(np.float64))
-                dn.append(po.dequant(blk[gu_bytes:].reshape(H, -1), F, float(g[1])).astype(np.float64))
-            L["gu"], L["dn"] = np.stack(gu), np.stack(dn)
-            SF = c["shared_ff"]
-            L["sg"] = q4(po.SH_GATE, SF, H, l)
-            L["su"] = q4(po.SH_UP, SF, H, l)
-            L["sd"] = q4(po.SH_DOWN, H, SF, l)
-            kv = om.tensor(po.KV, l)[0].view(np.float16).astype(np.float64).reshape(2, c["max_ctx"], nkv * hd)
-            L["kcache"], L["vcache"] = kv[0].copy(), kv[1].copy()
-            L["gdn"] = bool(c.get("gdn_layers") and c["gdn_layers"][l])
-            if L["gdn"]:
-                nk, nv, dk, dv, K = (c["gdn_k_heads"], c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"],
-                                     c["conv_kernel"])
-                cd, vd = 2 * nk * dk + nv * dv, nv * dv
-                f32 = lambda kind: om.tensor(kind, l)[0].view(np.float32).astype(np.float64)   # noqa: E731
-                L["gqkv"] = q4(po.GDN_QKV, cd, H, l)
-                L["gz"] = q4(po.GDN_Z, vd, H, l)
-                L["gout"] = q4(po.GDN_OUT, H, vd, l)
-                L["ga"] = _bf16(om.tensor(po.GDN_A, l)[0].view(np.uint16)).reshape(nv, H)
-                L["gb"] = _bf16(om.tensor(po.GDN_B, l)[0].view(np.uint16)).reshape(nv, H)
-                L["alog"], L["dtb"], L["gnorm"] = f32(po.GDN_ALOG), f32(po.GDN_DTB), f32(po.GDN_NORM)
-                L["convw"] = f32(po.GDN_CONV).reshape(cd, K)
-                L["conv"] = f32(po.GDN_CONV_ST).reshape(cd, K - 1)
-                L["S"] = f32(po.GDN_S).reshape(nv, dk, dv)
-            self.layers.append(L)
+        L = {}
+        for k, name in ((po.IN_NORM, "in"), (po.POST_NORM, "post"), (po.Q_NORM, "qn"), (po.K_NORM, "kn")):
+            L[name] = om.tensor(k, l)[0].view(np.float32).astype(np.float64)
+        L["q"] = q4(po.Q, nh * 2 * hd, H, l)
+        L["k"] = q4(po.K, nkv * hd, H, l)
+        L["v"] = q4(po.V, nkv * hd, H, l)
+        L["o"] = q4(po.O, H, nh * hd, l)
+        L["router"] = _bf16(om.tensor(po.ROUTER, l)[0].view(np.uint16)).reshape(c["n_experts"], H)
+        L["sgate"] = _bf16(om.tensor(po.SHARED_GATE, l)[0].view(np.uint16))
+        gu, dn = [], []
+        for e in range(c["n_experts"]):
+            blk, g = om.tensor(po.EXPERT, l, e)
+            gu.append(po.dequant(blk[:gu_bytes].reshape(2 * F, -1), H, float(g[0])).astype(np.float64))
+            dn.append(po.dequant(blk[gu_bytes:].reshape(H, -1), F, float(g[1])).astype(np.float64))
+        L["gu"], L["dn"] = np.stack(gu), np.stack(dn)
+        SF = c["shared_ff"]
+        L["sg"] = q4(po.SH_GATE, SF, H, l)
+        L["su"] = q4(po.SH_UP, SF, H, l)
+        L["sd"] = q4(po.SH_DOWN, H, SF, l)
+        kv = om.tensor(po.KV, l)[0].view(np.float16).astype(np.float64).reshape(2, c["max_ctx"], nkv * hd)
+        L["kcache"], L["vcache"] = kv[0].copy(), kv[1].copy()
+        L["gdn"] = bool(c.get("gdn_layers") and l < c["n_layers"] and c["gdn_layers"][l])
+        if L["gdn"]:
+            nk, nv, dk, dv, K = (c["gdn_k_heads"], c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"],
+                                 c["conv_kernel"])
+            cd, vd = 2 * nk * dk + nv * dv, nv * dv
+            f32 = lambda kind: om.tensor(kind, l)[0].view(np.float32).astype(np.float64)   # noqa: E731
+            L["gqkv"] = q4(po.GDN_QKV, cd, H, l)
+            L["gz"] = q4(po.GDN_Z, vd, H, l)
+            L["gout"] = q4(po.GDN_OUT, H, vd, l)
+            L["ga"] = _bf16(om.tensor(po.GDN_A, l)[0].view(np.uint16)).reshape(nv, H)
+            L["gb"] = _bf16(om.tensor(po.GDN_B, l)[0].view(np.uint16)).reshape(nv, H)
+            L["alog"], L["dtb"], L["gnorm"] = f32(po.GDN_ALOG), f32(po.GDN_DTB), f32(po.GDN_NORM)
+            L["convw"] = f32(po.GDN_CONV).reshape(cd, K)
+            L["conv"] = f32(po.GDN_CONV_ST).reshape(cd, K - 1)
+            L["S"] = f32(po.GDN_S).reshape(nv, dk, dv)
+        return L
 
     def _mm(self, W, x, mode):
         return (_quant(x) if mode == 0 else np.asarray(x, np.float32).astype(np.float64)) @ W.T
@@ -300,7 +311,39 @@ class F64Model:
             all_p.append(p)
             x = x + o
         hf = _rms(x, self.final_norm, c["eps"])
+        self.hid = hf   # the MTP layer's input rows
         return self._mm(self.lm, hf, mode), np.array(all_ids), np.array(all_p)
+
+
+MTP_MISTAKES = (
+    "mtp_concat_swapped",   # fc's input [hidden | embedding] instead of [embedding | hidden]
+    "mtp_pre_plain_w",      # the two input norms scaled by w instead of (1 + w)
+    "mtp_no_norm",          # lm_head on the layer's output without mtp.norm
+    "mtp_rope_next",        # the MTP rows rotated at pos + 1 + t (the token's position) instead of pos + t
+    "mtp_first_row",        # the logits of the first row instead of the last
+)
+
+
+def mtp_pass(fm, tokens, pos, hidden, mode=1, mistakes=(), logits=True):
+    """Model::forward_mtp (model.cpp:4965-5039) in float64: row t = (hidden row t, the token after it); the MTP
+    layer's KV written at pos..; the last row's logits (and its mtp.norm output kept for a chained draft)"""
+    c = fm.c
+    emb = fm.embed[np.asarray(tokens)]
+    plain = "mtp_pre_plain_w" in mistakes
+    e = _rms(emb, fm.pre_e, c["eps"], plain)
+    h = _rms(np.asarray(hidden, np.float64), fm.pre_h, c["eps"], plain)
+    x = fm._mm(fm.mtp_fc, np.concatenate([h, e] if "mtp_concat_swapped" in mistakes else [e, h], axis=1), mode)
+    L = fm.mtp_layer
+    hin = _rms(x, L["in"], c["eps"])
+    x = x + fm.attention(L, hin, pos + (1 if "mtp_rope_next" in mistakes else 0), None, mode)
+    o, _, _, _ = fm.moe(L, _rms(x, L["post"], c["eps"]), mode)
+    x = x + o
+    if not logits:
+        return None
+    last = x[0] if "mtp_first_row" in mistakes else x[-1]
+    hn = last if "mtp_no_norm" in mistakes else _rms(last, fm.mtp_norm, c["eps"])
+    fm.mtp_out = hn
+    return fm._mm(fm.lm, hn[None], mode)[0]
 
 
 def topk_margin(p, K):

@@ -26,7 +26,7 @@ def _rows(om):
     c = om.cfg
     kv_row = c["n_kv_heads"] * c["head_dim"]
     rows, scales = [], []
-    for l in range(c["n_layers"]):
+    for l in range(c["n_layers"] + (1 if c.get("mtp") else 0)):   # (an MTP layer's KV after the main layers')
         if c.get("kv_int8"):
             rows.append(om.tensor(po.KV8, l)[0].view(np.int8).reshape(2, c["max_ctx"], kv_row))
             scales.append(om.tensor(po.KVS, l)[0].view(np.float32).reshape(2, c["max_ctx"], c["n_kv_heads"]))
@@ -185,6 +185,22 @@ def test_hidden_only_with_mtp_and_a_position(tmp_path):
     om.save_state(path, has_mtp=True, hidden=np.ones(CFG["hidden"], np.float32))
     assert sf.read_header(open(path, "rb").read())["has_hidden"] == 1
     assert om.load_state(path, has_mtp=True)["hidden"].tolist() == [1.0] * CFG["hidden"]
+
+
+@pytest.mark.parametrize("kv_int8", [0, 1])
+def test_mtp_layer_kv_in_the_file(tmp_path, kv_int8):
+    """an MTP layer's KV goes after the main layers' (model.cpp:351: n_attn counts it), the fingerprint carries its
+    flag; a model without one refuses the file"""
+    om = po.Model(dict(CFG, kv_int8=kv_int8, mtp=1), seed=3, ctx=CTX)
+    hidden = po.normal(7, CFG["hidden"])
+    path = str(tmp_path / "s.geode")
+    om.save_state(path, pack_print=9, hidden=hidden)
+    rows, scales = _rows(om)
+    assert len(rows) == CFG["n_layers"] + 1
+    want = sf.state_bytes(om.cfg, rows, scales, CTX, pack_print=9, has_mtp=True, hidden=hidden)
+    assert open(path, "rb").read() == want
+    with pytest.raises(ValueError):
+        _model(kv_int8).load_state(path, pack_print=9, has_mtp=True)
 
 
 # a model of two Gated DeltaNet layers and an attention layer: its states go in the fixed part (each GDN layer's conv
