@@ -26,12 +26,13 @@ class GvModelConfig(_c.Structure):
                [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int32), ("max_rows", _c.c_int32),
                 ("kv_int8", _c.c_int32)] + \
                [(n, _c.c_int32) for n in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")] + \
-               [("gdn_layers", _c.c_uint8 * 256)]
+               [("gdn_layers", _c.c_uint8 * 256), ("mtp", _c.c_int32)]
 
     @classmethod
     def of(cls, cfg):
-        """the C struct of a config dict (kv_int8 and the Gated DeltaNet fields optional, gdn_layers a list of flags)"""
-        optional = ("kv_int8", "gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")
+        """the C struct of a config dict (kv_int8, the Gated DeltaNet fields and mtp optional, gdn_layers a list of
+        flags)"""
+        optional = ("kv_int8", "gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel", "mtp")
         c = cls(**{k: cfg.get(k, 0) if k in optional else cfg[k] for k, _ in cls._fields_ if k != "gdn_layers"})
         for l, g in enumerate(cfg.get("gdn_layers", ())):
             c.gdn_layers[l] = 1 if g else 0
@@ -58,6 +59,7 @@ class GvStateInfo(_c.Structure):
 EMBED, LM_HEAD, FINAL_NORM, IN_NORM, POST_NORM, QKV, O, Q_NORM, K_NORM, ROUTER, SHARED_GATE, EXPERT, \
     SHARED_EXPERT, KV, KV_I8 = 0, 1, 2, 3, 4, 5, 8, 9, 10, 11, 12, 13, 14, 17, 18
 GDN_QKV, GDN_Z, GDN_OUT, GDN_A, GDN_B, GDN_ALOG, GDN_DTB, GDN_CONV, GDN_NORM, GDN_CONV_ST, GDN_S = range(20, 31)
+MTP_FC, MTP_NORM, MTP_PRE_E, MTP_PRE_H = range(31, 35)
 
 # every symbol include/geode_verify.h declares, with its signature
 SIGNATURES = {
@@ -109,6 +111,13 @@ SIGNATURES = {
     "gv_model_moe_replay": (_c.c_int, [_P, _c.c_int, _P]),
     "gv_model_layer": (_c.c_int, [_P, _c.c_int, _P, _c.c_int, _P, _P, _P, _P]),
     "gv_model_gdn_state": (_c.c_int, [_P, _c.c_int, _P, _P]),
+    "gv_model_draft": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _P, _P, _P]),
+    "gv_model_draft_next": (_c.c_int, [_P, _c.c_int32, _c.c_int, _P, _P]),
+    "gv_model_draft_chain": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _P, _c.c_int, _c.c_float, _P, _P, _P]),
+    "gv_model_mtp_fill": (_c.c_int, [_P, _P, _c.c_int, _c.c_int, _P]),
+    "gv_model_set_draft_vocab": (_c.c_int, [_P, _P, _c.c_int]),
+    "gv_model_hidden": (_c.c_int, [_P, _P, _c.c_int]),
+    "gv_model_draft_logits": (_c.c_int, [_P, _P]),
     "gv_pack_open": (_P, [_c.c_char_p, _c.c_char_p, _c.c_int]),
     "gv_pack_close": (None, [_P]),
     "gv_pack_print": (_c.c_uint64, [_P]),
@@ -459,6 +468,67 @@ class VerifyModel:
         check(_lib().gv_model_gdn_state(self.h, layer, conv.ctypes.data_as(_P), S.ctypes.data_as(_P)),
               "gv_model_gdn_state")
         return conv, S
+
+    # ---- the MTP draft layer (a model made with mtp = 1)
+    @staticmethod
+    def _hid(hidden):
+        return np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
+
+    def draft(self, tokens, pos, hidden=None):
+        """gv_model_draft: (draft token, its probability); hidden None = the last verify's final-normed rows"""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        hid = self._hid(hidden)
+        d, p = _c.c_int32(0), _c.c_float(0)
+        check(_lib().gv_model_draft(self.h, tokens.ctypes.data_as(_P), tokens.size, pos,
+                                    hid.ctypes.data_as(_P) if hid is not None else None, _c.byref(d), _c.byref(p)),
+              "gv_model_draft")
+        return d.value, p.value
+
+    def draft_next(self, token, pos):
+        """gv_model_draft_next: (draft token, its probability) from the last MTP pass's output"""
+        d, p = _c.c_int32(0), _c.c_float(0)
+        check(_lib().gv_model_draft_next(self.h, int(token), pos, _c.byref(d), _c.byref(p)), "gv_model_draft_next")
+        return d.value, p.value
+
+    def draft_chain(self, tokens, pos, kmax, pmin=0.8, hidden=None):
+        """gv_model_draft_chain: (drafts, probabilities) by the generate loop's rule"""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        hid = self._hid(hidden)
+        d = np.zeros(max(1, kmax - 1), np.int32)
+        p = np.zeros(max(1, kmax - 1), np.float32)
+        cnt = _c.c_int(0)
+        check(_lib().gv_model_draft_chain(self.h, tokens.ctypes.data_as(_P), tokens.size, pos,
+                                          hid.ctypes.data_as(_P) if hid is not None else None, kmax, pmin,
+                                          d.ctypes.data_as(_P), p.ctypes.data_as(_P), _c.byref(cnt)),
+              "gv_model_draft_chain")
+        return d[:cnt.value].copy(), p[:cnt.value].copy()
+
+    def mtp_fill(self, tokens, pos, hidden=None):
+        """gv_model_mtp_fill: the MTP layer's KV of a prompt's rows (no logits)"""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        hid = self._hid(hidden)
+        check(_lib().gv_model_mtp_fill(self.h, tokens.ctypes.data_as(_P), tokens.size, pos,
+                                       hid.ctypes.data_as(_P) if hid is not None else None), "gv_model_mtp_fill")
+
+    def set_draft_vocab(self, ids):
+        a = np.ascontiguousarray(ids if ids is not None else [], np.int32)
+        check(_lib().gv_model_set_draft_vocab(self.h, a.ctypes.data_as(_P), a.size), "gv_model_set_draft_vocab")
+
+    def hidden(self):
+        """the last verify's rows after the final norm [n][hidden]"""
+        out = np.empty((self.cfg["max_rows"], self.cfg["hidden"]), np.float32)
+        n = _lib().gv_model_hidden(self.h, out.ctypes.data_as(_P), out.shape[0])
+        if n < 0:
+            check(n, "gv_model_hidden")
+        return out[:n].copy()
+
+    def draft_logits(self):
+        """the last MTP pass's logits (its last row, over the draft head)"""
+        out = np.empty(self.cfg["vocab"], np.float32)
+        n = _lib().gv_model_draft_logits(self.h, out.ctypes.data_as(_P))
+        if n < 0:
+            check(n, "gv_model_draft_logits")
+        return out[:n].copy()
 
     def time_kernel(self, cls):
         """events around every launch of kernel class cls (an index into KERNEL_CLASSES; -1 off) from now on"""

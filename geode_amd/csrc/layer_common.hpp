@@ -21,6 +21,30 @@ __device__ __host__ inline int64_t v_index(int64_t slots, int hd, int nkv, int k
            ((static_cast<int64_t>(kh) * (slots / kAttnBlock) + slot / kAttnBlock) * hd + d) * kAttnBlock + slot % kAttnBlock;
 }
 
+// Row r of a tile-layout q4 matrix dequantized as dequant_row does (pack.cpp:356-366; level x E4M3 x global, bit for
+// bit) into the registers norm_quant_regs takes (thread i: the 8-value groups i, i + blockDim, ..., zeros past the
+// row), and to out (fp32, may be null). cols at most 32 x blockDim.
+__device__ inline void dequant_row_regs(const Q4 &w, int64_t r, float (&v)[4][8], float *out) {
+    const int ng = static_cast<int>(w.cols / 8);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * blockDim.x;   // the row's code word g (tile layout)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) v[q][b] = 0.0f;
+        if (g >= ng) continue;
+        uint32_t word, sb;
+        tq4_word(w, r, g, word, sb);
+        const float s = __fmul_rn(e4m3_to_f32(sb), w.global);
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            v[q][b] = __fmul_rn(static_cast<float>(2 * static_cast<int>((word >> (4 * b)) & 15u) - 15), s);
+        if (out) {
+            *reinterpret_cast<float4 *>(out + g * 8) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+            *reinterpret_cast<float4 *>(out + g * 8 + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+        }
+    }
+}
+
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));

@@ -30,26 +30,9 @@ __global__ __launch_bounds__(256) void embed_kernel(Q4 w, const StepParams *__re
     __shared__ double red[16];
     const int t = blockIdx.x;
     if (t >= sp->M) return;
-    const int64_t r = sp->tokens[t];
-    const int ng = static_cast<int>(w.cols / 8);
     float v[4][8];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int g = threadIdx.x + q * blockDim.x;   // the row's code word g (tile layout)
-#pragma unroll
-        for (int b = 0; b < 8; ++b) v[q][b] = 0.0f;
-        if (g >= ng) continue;
-        uint32_t word, sb;
-        tq4_word(w, r, g, word, sb);
-        const float s = __fmul_rn(e4m3_to_f32(sb), w.global);
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-            v[q][b] = __fmul_rn(static_cast<float>(2 * static_cast<int>((word >> (4 * b)) & 15u) - 15), s);
-        float *o = x + static_cast<int64_t>(t) * w.cols + g * 8;
-        *reinterpret_cast<float4 *>(o) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
-        *reinterpret_cast<float4 *>(o + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
-    }
-    norm_quant_regs(v, ng * 8, norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
+    dequant_row_regs(w, sp->tokens[t], v, x + static_cast<int64_t>(t) * w.cols);
+    norm_quant_regs(v, static_cast<int>(w.cols), norm_w, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
 }
 
 // quant_kv_row (model.cpp:3766-3774) of a row held one value a thread (256 threads; threads past the row: live
@@ -963,7 +946,8 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
 // and its operands; a workgroup per row
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K, const MixView mix,
                                                       int M, float *__restrict__ x, const float *__restrict__ norm_w,
-                                                      float eps, _Float16 *__restrict__ act, int64_t act_stride) {
+                                                      float eps, _Float16 *__restrict__ act, int64_t act_stride,
+                                                      float *__restrict__ hout) {
     __shared__ double red[16];
     const int t = blockIdx.x;
     if (t >= M) return;
@@ -1037,12 +1021,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
             *reinterpret_cast<float4 *>(xr + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
         }
     }
-    if (act) norm_quant_regs_w(v, H, norm_w != nullptr, w1, eps, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
+    if (act)
+        norm_quant_regs_w(v, H, norm_w != nullptr, w1, eps, act + static_cast<int64_t>(t) * act_stride,
+                          hout ? hout + static_cast<int64_t>(t) * H : nullptr, red);
 }
 
+// (hout: the normalized rows in fp32 too, [M][H], or null)
 inline int combine_launch(const float *y, int H, int K, const MixView &mix, int M, float *x, const float *norm_w,
-                          float eps, _Float16 *act, int64_t act_stride, hipStream_t st) {
-    hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, y, H, K, mix, M, x, norm_w, eps, act, act_stride);
+                          float eps, _Float16 *act, int64_t act_stride, hipStream_t st, float *hout = nullptr) {
+    hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, y, H, K, mix, M, x, norm_w, eps, act, act_stride,
+                       hout);
     return 0;
 }
 
@@ -1593,11 +1581,21 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         return 0;
     case GV_K_MOE_DOWN:
         return m.moe_dec ? moe_dec(m, L, M, false, st) : moe_products(m, L, M, false, st);
-    case GV_K_COMBINE: {   // the residual add, then the next layer's input RMSNorm (after the last: the final norm)
-        const float *next_norm = m.moe_only                ? nullptr
-                                 : l + 1 < c.n_layers ? m.layers[static_cast<size_t>(l) + 1].in_norm
-                                                      : m.final_norm;
-        combine_launch(m.y, H, c.top_k, route_mix(m.route + l, m.moe_dec), M, m.x, next_norm, c.eps, m.act_h, abH, st);
+    case GV_K_COMBINE: {   // the residual add, then the next layer's input RMSNorm (after the last: the final norm;
+                           // after the MTP layer: mtp.norm)
+        const bool mtp_layer = l == c.n_layers;
+        const float *next_norm = m.moe_only              ? nullptr
+                                 : mtp_layer             ? m.mtp_norm
+                                 : l + 1 < c.n_layers    ? m.layers[static_cast<size_t>(l) + 1].in_norm
+                                                         : m.final_norm;
+        // a model with an MTP layer keeps the normalized rows it drafts from: the last layer's (the verify's hidden
+        // rows) and the MTP layer's own (a chained draft's)
+        float *hout = !m.has_mtp || m.moe_only ? nullptr
+                      : mtp_layer             ? m.hbuf + static_cast<int64_t>(c.max_rows) * H
+                      : l + 1 == c.n_layers   ? m.hbuf
+                                              : nullptr;
+        combine_launch(m.y, H, c.top_k, route_mix(m.route + l, m.moe_dec), M, m.x, next_norm, c.eps, m.act_h, abH, st,
+                       hout);
         return 0;
     }
     case GV_K_LM_HEAD:
@@ -1608,14 +1606,14 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
 }
 
 // (an attention layer skips the GV_K_GDN_* classes, a Gated DeltaNet layer GV_K_ROPE, GV_K_ATTN and GV_K_MERGE)
-constexpr int kLayerClasses[] = {GV_K_QKV,      GV_K_GDN_AB, GV_K_GDN_CONV, GV_K_GDN_CORE, GV_K_GDN_NORM,
-                                 GV_K_ROPE,     GV_K_ATTN,   GV_K_MERGE,    GV_K_O,        GV_K_ROUTER,
-                                 GV_K_ROUTE,    GV_K_MOE_UP, GV_K_SWIGLU,   GV_K_MOE_DOWN, GV_K_COMBINE};
+constexpr int kLayerClassList[] = {GV_K_QKV,    GV_K_GDN_AB, GV_K_GDN_CONV, GV_K_GDN_CORE, GV_K_GDN_NORM,
+                                      GV_K_ROPE,   GV_K_ATTN,   GV_K_MERGE,    GV_K_O,        GV_K_ROUTER,
+                                      GV_K_ROUTE,  GV_K_MOE_UP, GV_K_SWIGLU,   GV_K_MOE_DOWN, GV_K_COMBINE};
 
 int run_layers(Model &m, int M, hipStream_t st) {
     if (launch_class(m, GV_K_EMBED, 0, M, st) != 0) return -1;
     for (int l = 0; l < m.c.n_layers; ++l)
-        for (int cls : kLayerClasses)
+        for (int cls : kLayerClassList)
             if (launch_class(m, cls, l, M, st) != 0) return -1;
     if (launch_class(m, GV_K_LM_HEAD, 0, M, st) != 0) return -1;
     GV_CHECK_HIP(hipGetLastError());
@@ -1764,6 +1762,12 @@ int64_t qkv_rows(const gv_model_config &c) {
 
 }  // namespace
 
+int run_class(Model &m, int cls, int l, int M, hipStream_t st) { return launch_class(m, cls, l, M, st); }
+const int *layer_classes(int &count) {
+    count = static_cast<int>(sizeof(kLayerClassList) / sizeof(kLayerClassList[0]));
+    return kLayerClassList;
+}
+
 }  // namespace gv
 
 using namespace gv;
@@ -1834,6 +1838,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     if (c.n_experts <= 0 || c.n_experts > 256 || c.top_k <= 0 || c.top_k > 16 || c.top_k > c.n_experts)
         return fail("1 <= top_k <= 16, top_k <= n_experts <= 256");
     if (c.max_rows <= 0 || c.max_rows > kMaxRows) return fail("max_rows must be 1..32");
+    if (c.mtp != 0 && (c.mtp != 1 || c.hidden > 8192)) return fail("mtp must be 0 or 1 (an MTP layer: hidden at most 8192)");
     if (c.vocab <= 0 || c.n_layers <= 0 || c.max_ctx <= c.max_rows) return fail("vocab, n_layers, max_ctx");
     {
         std::string why;
@@ -1865,13 +1870,16 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     m.kv_i8 = c.kv_int8 != 0;
     m.kv_layer_bytes = m.kv_i8 ? kv_layer + 2 * static_cast<size_t>(nkv) * m.slots * 4 : kv_layer * 2;
     m.kv_layer_bytes = (m.kv_layer_bytes + 255) / 256 * 256;
-    m.kv_all = static_cast<_Float16 *>(dalloc(m, static_cast<size_t>(c.n_layers) * m.kv_layer_bytes));
+    // the layers: the main ones, then the MTP layer's (index n_layers: an attention layer, its KV after theirs)
+    m.has_mtp = c.mtp != 0;
+    const int NL = c.n_layers + (m.has_mtp ? 1 : 0);
+    m.kv_all = static_cast<_Float16 *>(dalloc(m, static_cast<size_t>(NL) * m.kv_layer_bytes));
     ok = ok && m.kv_all;
-    m.layers.resize(static_cast<size_t>(c.n_layers));
+    m.layers.resize(static_cast<size_t>(NL));
     const int64_t gconv = gdn_conv_dim(c), gvd = static_cast<int64_t>(c.gdn_v_heads) * c.gdn_v_dim;
-    for (int l = 0; ok && l < c.n_layers; ++l) {
+    for (int l = 0; ok && l < NL; ++l) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
-        L.gdn = c.gdn_v_heads > 0 && l < 256 && c.gdn_layers[l] != 0;
+        L.gdn = c.gdn_v_heads > 0 && l < c.n_layers && l < 256 && c.gdn_layers[l] != 0;
         if (L.gdn) {   // in_proj_qkv | in_proj_z, out_proj, the bf16 a / b rows, the small tensors, the state slots
             const int64_t nv = c.gdn_v_heads, K = c.conv_kernel, Mx2 = 2 * static_cast<int64_t>(c.max_rows);
             ok = alloc_q4(m, L.qkv, gconv + gvd, H) && alloc_q4(m, L.o, H, gvd);
@@ -1906,7 +1914,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
             L.kv = reinterpret_cast<_Float16 *>(kb);
         }
     }
-    for (int l = 0; l < c.n_layers; ++l) (m.layers[static_cast<size_t>(l)].gdn ? m.gdn_layers : m.attn_layers).push_back(l);
+    for (int l = 0; l < NL; ++l) (m.layers[static_cast<size_t>(l)].gdn ? m.gdn_layers : m.attn_layers).push_back(l);
     ok = ok && (m.attn_index = static_cast<int *>(dalloc(m, std::max<size_t>(1, m.attn_layers.size()) * 4)));
     ok = ok && (m.attn_layers.empty() || hipMemcpy(m.attn_index, m.attn_layers.data(), m.attn_layers.size() * 4,
                                                    hipMemcpyHostToDevice) == hipSuccess);
@@ -1916,13 +1924,13 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     m.max_picks = Mx * (K + 1);
     m.kv_blocks = (c.max_ctx + kAttnBlock - 1) / kAttnBlock;
     ok = ok && (m.sp = static_cast<StepParams *>(dalloc(m, sizeof(StepParams))));
-    ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * c.n_layers)));
+    ok = ok && (m.route = static_cast<RouteState *>(dalloc(m, sizeof(RouteState) * NL)));
     ok = ok && (m.counter = static_cast<int *>(dalloc(m, 64)));
     ok = ok && hipMemset(m.counter, 0, 64) == hipSuccess;
-    const size_t ctr_bytes = static_cast<size_t>(c.n_layers) * kFlagsPerLayer * 4 + 256;   // the fused launches' flags, err
+    const size_t ctr_bytes = static_cast<size_t>(NL) * kFlagsPerLayer * 4 + 256;   // the fused launches' flags, err
     ok = ok && (m.ctr = static_cast<int *>(dalloc(m, ctr_bytes)));
     ok = ok && hipMemset(m.ctr, 0, ctr_bytes) == hipSuccess;
-    if (ok) m.err = m.ctr + static_cast<size_t>(c.n_layers) * kFlagsPerLayer;
+    if (ok) m.err = m.ctr + static_cast<size_t>(NL) * kFlagsPerLayer;
     {
         int kwu, kwd, waves;
         m.moe_dec = moe_dec_shape(c, kwu, kwd, waves);
@@ -1962,7 +1970,8 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     }
     ok = ok && (m.q16 = static_cast<_Float16 *>(dalloc(m, 2 * Mx * nh * hd * 2)));
     ok = ok && (m.gu_out = static_cast<float *>(dalloc(m, static_cast<size_t>(m.max_picks) * 2 * F * 4)));
-    ok = ok && (m.route_ids = static_cast<int32_t *>(dalloc(m, static_cast<size_t>(c.n_layers) * Mx * K * 4)));
+    ok = ok && (m.route_ids = static_cast<int32_t *>(dalloc(m, static_cast<size_t>(NL) * Mx * K * 4)));
+    ok = ok && (!m.has_mtp || mtp_alloc(m) == 0);
     const int half = c.rope_dim / 2;
     const int npos = c.max_ctx + kMaxRows;
     ok = ok && (m.rope_cos = static_cast<float *>(dalloc(m, static_cast<size_t>(npos) * std::max(1, half) * 4)));
@@ -1982,7 +1991,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         (hipMemcpy(m.rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
          hipMemcpy(m.rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess))
         return fail("gv_model_create: rope table copy failed");
-    if (hipMemset(m.kv_all, 0, static_cast<size_t>(c.n_layers) * m.kv_layer_bytes) != hipSuccess)
+    if (hipMemset(m.kv_all, 0, static_cast<size_t>(NL) * m.kv_layer_bytes) != hipSuccess)
         return fail("gv_model_create: memset failed");
     return g.release();
 }
@@ -1992,6 +2001,7 @@ void gv_model_free(gv_model *g) {
     (void)hipStreamSynchronize(stream());
     for (auto &ge : g->m.graphs)
         if (ge) (void)hipGraphExecDestroy(ge);
+    mtp_free(g->m);
     for (void *p : g->m.allocs) (void)hipFree(p);
     for (void *p : g->m.pf.allocs) (void)hipFree(p);
     if (g->m.trace) {   // the kernels stop stamping before the buffer goes
@@ -2010,8 +2020,11 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
     Model &m = g->m;
     const auto &c = m.c;
     const int64_t H = c.hidden, F = c.moe_ff, V = c.vocab, nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
-    const bool per_layer = kind != GV_EMBED && kind != GV_LM_HEAD && kind != GV_FINAL_NORM;
-    GV_REQUIRE(!per_layer || (layer >= 0 && layer < c.n_layers), "gv_model_adopt: no such layer");
+    const bool mtp_kind = kind >= GV_MTP_FC && kind <= GV_MTP_PRE_H;
+    GV_REQUIRE(!mtp_kind || m.has_mtp, "gv_model_adopt: an MTP tensor for a model without an MTP layer");
+    const bool per_layer = kind != GV_EMBED && kind != GV_LM_HEAD && kind != GV_FINAL_NORM && !mtp_kind;
+    GV_REQUIRE(!per_layer || (layer >= 0 && layer < static_cast<int>(m.layers.size())),
+               "gv_model_adopt: no such layer (n_layers: the MTP layer's)");
     LayerW *L = per_layer ? &m.layers[static_cast<size_t>(layer)] : nullptr;
     auto q4_size = [](int64_t r, int64_t cc) { return r * (cc / 16) * 9; };
     auto copy = [&](void *dst, int64_t want) -> int {
@@ -2063,6 +2076,13 @@ int gv_model_adopt(gv_model *g, int kind, int layer, int expert, const void *dat
                          globals[0], q);
     }
     case GV_FINAL_NORM: return copy(m.final_norm, H * 4);
+    case GV_MTP_FC:
+        GV_REQUIRE(globals && bytes == q4_size(H, 2 * H), "gv_model_adopt: mtp.fc size");
+        return upload_q4(data, false, H, 2 * H, const_cast<uint8_t *>(m.mtp_fc.codes),
+                         const_cast<uint8_t *>(m.mtp_fc.scales), globals[0], m.mtp_fc);
+    case GV_MTP_NORM: return copy(m.mtp_norm, H * 4);
+    case GV_MTP_PRE_E: return copy(m.mtp_pre_e, H * 4);
+    case GV_MTP_PRE_H: return copy(m.mtp_pre_h, H * 4);
     case GV_IN_NORM: return copy(L->in_norm, H * 4);
     case GV_POST_NORM: return copy(L->post_norm, H * 4);
     case GV_Q_NORM: return copy(L->q_norm, hd * 4);
@@ -2192,7 +2212,14 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
     rc |= make_q4(tseed(GV_LM_HEAD, 0, 0), V, H, const_cast<uint8_t *>(m.lm_head.codes),
                   const_cast<uint8_t *>(m.lm_head.scales), &m.lm_head.global, nullptr);
     rc |= make_f32(tseed(GV_FINAL_NORM, 0, 0), H, 0.02f, m.final_norm);
-    for (int l = 0; l < c.n_layers && rc == 0; ++l) {
+    if (m.has_mtp) {   // the MTP layer's fc and norms (its decoder layer: layer n_layers below)
+        rc |= make_q4(tseed(GV_MTP_FC, 0, 0), H, 2 * H, const_cast<uint8_t *>(m.mtp_fc.codes),
+                      const_cast<uint8_t *>(m.mtp_fc.scales), &m.mtp_fc.global, nullptr);
+        rc |= make_f32(tseed(GV_MTP_NORM, 0, 0), H, 0.02f, m.mtp_norm);
+        rc |= make_f32(tseed(GV_MTP_PRE_E, 0, 0), H, 0.02f, m.mtp_pre_e);
+        rc |= make_f32(tseed(GV_MTP_PRE_H, 0, 0), H, 0.02f, m.mtp_pre_h);
+    }
+    for (int l = 0; l < static_cast<int>(m.layers.size()) && rc == 0; ++l) {
         LayerW &L = m.layers[static_cast<size_t>(l)];
         rc |= make_f32(tseed(GV_IN_NORM, l, 0), H, 0.02f, L.in_norm);
         rc |= make_f32(tseed(GV_POST_NORM, l, 0), H, 0.02f, L.post_norm);
@@ -2360,6 +2387,8 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     m.last_n = n;
     m.pos += n;
     m.gdn_base = sp.gdn_wset + n - 1;   // (a chain's states as after its last row)
+    m.hid_n = m.has_mtp ? n : 0;        // the final-normed rows the MTP layer drafts from
+    m.keep_rows.clear();
     return 0;
 }
 
@@ -2396,6 +2425,8 @@ int gv_verify_keep(gv_model *g, int kept, const int32_t *path) {
     m.pos = m.last_pos + kept;
     m.gdn_base = m.host_sp.gdn_wset + (path ? path[kept - 1] : kept - 1);   // the states as after the last kept row
     m.last_n = 0;
+    m.keep_rows.clear();
+    if (path) m.keep_rows.assign(path, path + kept);   // (the MTP layer's hidden rows: the path's)
     return 0;
 }
 

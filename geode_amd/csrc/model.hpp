@@ -24,6 +24,7 @@ struct StepParams {
     uint32_t vis[kMaxRows];
     int gdn_base;   // the Gated DeltaNet layers' slot holding the states the rows start from
     int gdn_wset;   // the first slot of the set the rows' states go to (the set without gdn_base)
+    int hrow[kMaxRows];   // an MTP pass: row t's hidden row in Model::hbuf
 };
 
 // Routing of one layer, written by the route kernel: slots are runs of at most kSlotRows picks (token, rank) of one
@@ -148,6 +149,23 @@ struct Model {
     int gdn_base = 0;            // the Gated DeltaNet layers' base slot (StepParams::gdn_base)
     std::vector<int> attn_layers, gdn_layers;   // the attention / Gated DeltaNet layers' indices, in order
     int *attn_index = nullptr;   // device copy of attn_layers
+    // the MTP draft layer (mtp.hip): layers[n_layers] is its decoder layer, its KV after the main layers'
+    bool has_mtp = false;
+    Q4 mtp_fc;                                            // [H x 2 H]
+    float *mtp_norm = nullptr, *mtp_pre_e = nullptr, *mtp_pre_h = nullptr;
+    float *hbuf = nullptr;        // [3][max_rows][H]: the last verify's final-normed rows, the last MTP pass's
+                                  // mtp.norm rows, rows given by the caller
+    int hid_n = 0;                // rows of the first part the last verify wrote
+    std::vector<int> keep_rows;   // after a keep with a path: the kept rows (an MTP row t's hidden: keep_rows[t])
+    _Float16 *mtp_act = nullptr;  // [max_rows] fc's operands (2 H values a row)
+    float *mtp_logits = nullptr;  // [vocab] the last MTP pass's last row
+    StepParams *sp_mtp = nullptr;
+    StepParams host_sp_mtp{};
+    int mtp_last_n = 0;           // rows of the last MTP pass with logits (0: none yet)
+    Q4 draft_head;                // lm_head's rows of the draft vocabulary (rows 0: the whole vocabulary)
+    int32_t *draft_ids = nullptr; // device [draft_head.rows]
+    uint8_t *draft_mem = nullptr;
+    void *pick = nullptr;         // the draft pick's partials and result (mtp.hip)
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
@@ -166,5 +184,12 @@ int64_t gdn_c_floats(const gv_model_config &c);   // a slot's conv state
 int gdn_launch(Model &m, LayerW &L, int l, int M, bool ab_given, hipStream_t st);
 int gdn_put_state(Model &m, LayerW &L, int slot, const float *conv, const float *S);
 int gdn_get_state(const Model &m, const LayerW &L, int slot, float *conv, float *S);
+
+// the verify step's launches (model.hip): one kernel class of layer l for M rows, and a layer's classes in order
+int run_class(Model &m, int cls, int l, int M, hipStream_t st);
+const int *layer_classes(int &count);
+// the MTP layer's buffers (mtp.hip), at gv_model_create
+int mtp_alloc(Model &m);
+void mtp_free(Model &m);
 
 }  // namespace gv

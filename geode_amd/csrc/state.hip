@@ -105,7 +105,7 @@ uint64_t fingerprint_of(const Model &m, const gv_state_info &info) {
                                gdn_n_of(m),
                                static_cast<uint64_t>(c.hidden),
                                static_cast<uint64_t>(c.n_layers),
-                               info.has_mtp ? 1u : 0u,
+                               info.has_mtp || m.has_mtp ? 1u : 0u,
                                info.has_vision ? 1u : 0u};
     return fnv(shapes, sizeof shapes, info.pack_print ? info.pack_print : 1);
 }
@@ -306,7 +306,7 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
     h.kv_heads = static_cast<uint32_t>(c.n_kv_heads);
     h.kv_row = s.kv_row;
     h.hidden = static_cast<uint32_t>(c.hidden);
-    h.has_hidden = info->hidden && info->has_mtp && m.pos > 0 ? 1 : 0;
+    h.has_hidden = info->hidden && (info->has_mtp || m.has_mtp) && m.pos > 0 ? 1 : 0;
     h.block = kStateBlock;
     h.conv_n = conv_n_of(m);
     h.gdn_n = gdn_n_of(m);

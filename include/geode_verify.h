@@ -119,6 +119,10 @@ typedef struct gv_model_config {
      * nv x dv a multiple of 128), causal conv of conv_kernel taps (2 .. 8). */
     int32_t gdn_k_heads, gdn_v_heads, gdn_k_dim, gdn_v_dim, conv_kernel;
     uint8_t gdn_layers[256];
+    /* 1: an MTP draft layer (ModelConfig::mtp_layers, engine/src/model.cpp:175-191): a full-attention layer at index
+     * n_layers (its tensors adopted with the per-layer kinds at that index, its KV after the main layers') behind
+     * mtp.fc, with its own norms (GV_MTP_*); hidden at most 8192 */
+    int32_t mtp;
 } gv_model_config;
 
 /* tensor kinds for gv_model_adopt (numbered as the CPU oracle's) */
@@ -152,7 +156,12 @@ enum {
     GV_GDN_CONV = 27,     /* f32 conv1d [2 kd + vd][conv_kernel] */
     GV_GDN_NORM = 28,     /* f32 norm [dv] (the gated RMSNorm's weight as it is: no 1 + w) */
     GV_GDN_CONV_ST = 29,  /* f32 the conv's state [2 kd + vd][conv_kernel - 1], the last inputs oldest first */
-    GV_GDN_S = 30         /* f32 the recurrent state [nv][dk][dv] */
+    GV_GDN_S = 30,        /* f32 the recurrent state [nv][dk][dv] */
+    /* the MTP layer's own tensors (engine/src/model.cpp:178-190; layer ignored) */
+    GV_MTP_FC = 31,       /* q4 mtp.fc.weight [hidden x 2 hidden], globals[0] */
+    GV_MTP_NORM = 32,     /* f32 mtp.norm.weight [hidden] */
+    GV_MTP_PRE_E = 33,    /* f32 mtp.pre_fc_norm_embedding.weight [hidden] */
+    GV_MTP_PRE_H = 34     /* f32 mtp.pre_fc_norm_hidden.weight [hidden] */
 };
 
 typedef struct gv_model gv_model;
@@ -233,6 +242,33 @@ int gv_model_layer(gv_model *m, int layer, const float *x_in, int n, const int32
  * after the last kept row, model.cpp:1617-1633): conv [2 kd + vd][conv_kernel - 1] and S [nv][dk][dv], host (either
  * may be NULL). gv_model_layer reads the states and leaves them as they were. */
 int gv_model_gdn_state(const gv_model *m, int layer, float *conv, float *S);
+
+/* ---- the MTP draft layer on the GPU (a model made with mtp = 1) ----
+ * Model::draft (engine/src/model.cpp:1295-1432): the MTP pass (Model::forward_mtp, :4965-5039) over n rows at MTP
+ * positions pos..pos+n-1, row t the pair (hidden row t, toks[t]: the token after it), the layer's keys and values to
+ * its own cache at those positions; *draft = the first maximum of the last row's logits (through the draft
+ * vocabulary when one is set), *prob = its softmax probability, 1 / sum exp(double(l - max)) (softmax_at, :1286-1292).
+ * hidden: host [n][hidden], or NULL for the last verify's rows after the final norm (rows 0..n-1; after a keep with a
+ * path, the path's rows). 1 <= n <= max_rows. */
+int gv_model_draft(gv_model *m, const int32_t *toks, int n, int pos, const float *hidden, int32_t *draft, float *prob);
+/* Model::draft_next (model.cpp:1434-1479): one MTP row at position pos from the last MTP pass's output after mtp.norm
+ * (its last row) and tok (the draft it made) */
+int gv_model_draft_next(gv_model *m, int32_t tok, int pos, int32_t *draft, float *prob);
+/* The generate loop's drafting (engine/src/geode.cpp:301-317) in one call: gv_model_draft, then chained drafts
+ * while the last one's probability is at least pmin, at most kmax - 1 drafts in all and while the verify batch (the
+ * token and the drafts) still fits the context after the model's position. drafts / probs [kmax - 1]. */
+int gv_model_draft_chain(gv_model *m, const int32_t *toks, int n, int pos, const float *hidden, int kmax, float pmin,
+                         int32_t *drafts, float *probs, int *count);
+/* forward_mtp without logits (a prompt's pass, model.cpp:4985: only the layer's keys and values); n rows, in chunks
+ * of max_rows; hidden NULL only for n within the last verify's rows */
+int gv_model_mtp_fill(gv_model *m, const int32_t *toks, int n, int pos, const float *hidden);
+/* The draft head (model.cpp:803-827, draft_vocab.bin): lm_head's rows of ids[0..n), a draft is one of them; n = 0:
+ * the whole vocabulary again */
+int gv_model_set_draft_vocab(gv_model *m, const int32_t *ids, int n);
+/* The last verify's rows after the final norm (the MTP layer's input), host [rows][hidden]; returns the rows copied */
+int gv_model_hidden(const gv_model *m, float *out, int max_rows);
+/* The last MTP pass's logits (its last row, over the draft head's rows), host; returns their count */
+int gv_model_draft_logits(const gv_model *m, float *out);
 /* Re-run the last gv_model_moe call's block on its device-staged rows and logits reps times back to back, run i on
  * layer (layer + i) mod n_layers (so that a model of several layers rotates through distinct expert weights), and
  * return the mean milliseconds a block (device work only); a measurement aid with no reference counterpart. */

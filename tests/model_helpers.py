@@ -36,7 +36,12 @@ def adopt_oracle_model(gm, om, ctx):
     gm.adopt(g.LM_HEAD, t, globals_=gl[:1])
     gm.adopt(g.FINAL_NORM, om.tensor(po.FINAL_NORM)[0])
     gdn = c.get("gdn_layers", ())
-    for l in range(c["n_layers"]):
+    if c.get("mtp"):   # the MTP layer's own tensors; its decoder layer is layer n_layers below
+        t, gl = om.tensor(po.MTP_FC)
+        gm.adopt(g.MTP_FC, t, globals_=gl[:1])
+        for k_o, k_g in ((po.MTP_NORM, g.MTP_NORM), (po.MTP_PRE_E, g.MTP_PRE_E), (po.MTP_PRE_H, g.MTP_PRE_H)):
+            gm.adopt(k_g, om.tensor(k_o)[0])
+    for l in range(c["n_layers"] + (1 if c.get("mtp") else 0)):
         for k_o, k_g in ((po.IN_NORM, g.IN_NORM), (po.POST_NORM, g.POST_NORM), (po.ROUTER, g.ROUTER),
                          (po.SHARED_GATE, g.SHARED_GATE)):
             gm.adopt(k_g, om.tensor(k_o, l)[0], layer=l)

@@ -234,3 +234,51 @@ def test_gdn_refused_load_leaves_zero_states(gv, gdn_pair, tmp_path):
         conv, S = g2.gdn_state(l)
         assert not conv.any() and not S.any()
     g2.close()
+
+
+@pytest.mark.parametrize("kv_int8", [0, 1])
+def test_mtp_save_equals_the_oracles(gv, tmp_path, kv_int8):
+    """a model with an MTP layer: its KV after the main layers' in every block (model.cpp:351), the fingerprint's MTP
+    flag from the model; the GPU's file equals the oracle's byte for byte after an MTP pass on both, and it loads into a
+    fresh GPU model whose next draft equals the original's"""
+    cfg = dict(CFG, kv_int8=kv_int8, mtp=1, max_ctx=400)
+    om = po.Model(cfg, seed=13, router_sigma=SMALL_ROUTER_SIGMA, ctx=300)
+    gm = gv.VerifyModel(cfg)
+    g2 = None
+    try:
+        adopt_oracle_model(gm, om, 300)
+        rng = np.random.default_rng(4)
+        toks = rng.integers(0, cfg["vocab"], 3).astype(np.int32)
+        hid = rng.normal(0, 1, (3, cfg["hidden"])).astype(np.float32)
+        om.mtp(toks, 280, hid, logits=False)
+        gm.mtp_fill(toks, 280, hid)
+        om.position = gm.position = 300
+        meta = dict(META, has_mtp=False)   # (the model's own MTP layer sets the flag)
+        om.save_state(str(tmp_path / "o.geode"), **meta)
+        gm.save_state(str(tmp_path / "g.geode"), **meta)
+        got, want = open(tmp_path / "g.geode", "rb").read(), open(tmp_path / "o.geode", "rb").read()
+        assert len(got) == len(want) and got[:4096] == want[:4096]   # the header: n_attn 3, the MTP flag
+        assert sf.read_header(got)["n_attn"] == cfg["n_layers"] + 1
+        # the KV blocks: every row equal but the MTP pass's own (positions 280..282 of the MTP layer's, where the
+        # two paths' products may differ in the last bits)
+        gr, gs = sf.kv_rows(cfg, got)
+        orr, os_ = sf.kv_rows(cfg, want)
+        for l in range(cfg["n_layers"] + 1):
+            live = np.ones(300, bool)
+            if l == cfg["n_layers"]:
+                live[280:283] = False
+            assert np.array_equal(gr[l][:, live], orr[l][:, live]), f"attention layer {l}"
+            if kv_int8:
+                assert np.array_equal(gs[l][:, live], os_[l][:, live])
+        g2 = _fresh(gv, om, cfg)
+        g2.load_state(str(tmp_path / "g.geode"), pack_print=meta["pack_print"])
+        t2 = np.array([5, 6], np.int32)
+        h2 = rng.normal(0, 1, (2, cfg["hidden"])).astype(np.float32)
+        a = gm.draft(t2, 300, h2)
+        la = gm.draft_logits()
+        b = g2.draft(t2, 300, h2)
+        assert a == b and np.array_equal(la, g2.draft_logits())
+    finally:
+        gm.close()
+        if g2 is not None:
+            g2.close()
