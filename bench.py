@@ -30,7 +30,7 @@ C4 = dict(hidden=2048, vocab=151936, n_layers=40, n_experts=256, top_k=8, moe_ff
 # the real model (Qwen3.6-35B-A3B, engine/src/gpu_check.cpp:277-281): 30 Gated DeltaNet layers (16 key heads, 32 value
 # heads, 128-wide, conv of 4) and 10 gated-attention layers (every fourth), vocab 248,320, the int8 KV cache
 REAL = dict(C4, vocab=248320, kv_int8=1, gdn_k_heads=16, gdn_v_heads=32, gdn_k_dim=128, gdn_v_dim=128, conv_kernel=4,
-            gdn_layers=[0 if l % 4 == 3 else 1 for l in range(40)])
+            gdn_layers=[0 if l % 4 == 3 else 1 for l in range(40)], mtp=1)
 CTX = 8192
 SEED = 20261201
 PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s
@@ -249,8 +249,36 @@ def bench_real(g, args):
                         "kernel_ms_per_step": per_class,
                         "gdn_core": {"avg_launch_us": core_s * 1e6, "bytes_per_launch": core_b,
                                      "achieved_gbs": core_b / core_s / 1e9, "frac": core_b / core_s / PEAK_HBM}}
+    out["mtp"] = bench_drafts(g, m, args)
     m.close()
     return out
+
+
+def bench_drafts(g, m, args):
+    """The MTP draft layer after a chain verify (wall clock of the synchronous calls, each returning its token): a
+    draft from the verify's 5 rows, a chained draft, the generate loop's chain of 4 drafts (pmin 0: all four), over
+    the whole vocabulary and over a 32,768-token draft head (an example size of draft_vocab.bin)"""
+    toks = np.array([(7 + 1000 * i) % REAL["vocab"] for i in range(5)], np.int32)
+    m.position = CTX
+    m.verify(toks, want_logits=False)
+    res = {}
+    for name, ids in (("whole_vocab", None), ("draft_vocab_32768", np.arange(0, REAL["vocab"], 7)[:32768])):
+        m.set_draft_vocab(ids)
+
+        def timed(fn, reps=max(5, args.steps)):
+            for _ in range(2):
+                fn()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            return (time.perf_counter() - t0) / reps * 1e3
+
+        d = m.draft(toks, CTX)[0]
+        res[name] = {"ms_draft_5_rows": timed(lambda: m.draft(toks, CTX)),
+                     "ms_draft_next": timed(lambda: m.draft_next(d, CTX + 5)),
+                     "ms_chain_4_drafts": timed(lambda: m.draft_chain(toks, CTX, 5, 0.0))}
+    m.set_draft_vocab(None)
+    return res
 
 
 def main_config(args):

@@ -27,6 +27,7 @@
 
 #include "../../include/geode_verify.h"
 #include "common.hpp"
+#include "model.hpp"
 
 namespace gv {
 namespace {
@@ -624,6 +625,7 @@ int gv_pack_model_config(const gv_pack *p, int max_ctx, int max_rows, int kv_int
     c.max_ctx = max_ctx;
     c.max_rows = max_rows;
     c.kv_int8 = kv_int8;
+    c.mtp = p->mtp ? 1 : 0;   // ModelConfig::mtp_layers (pack.cpp:303-305); a caller may set it to 0 (no drafting)
     if (any_gdn) {   // ModelConfig's Gated DeltaNet shape (pack.cpp:96-100), the layers not "full_attention"
         c.gdn_k_heads = p->gdn_k_heads;
         c.gdn_v_heads = p->gdn_v_heads;
@@ -715,8 +717,8 @@ int gv_model_load_pack(gv_model *g, const gv_pack *p) {
         return -1;
     const int64_t nk = p->gdn_k_heads, nv = p->gdn_v_heads, dk = p->gdn_k_dim, dv = p->gdn_v_dim, K = p->conv_kernel;
     const int64_t conv_dim = 2 * nk * dk + nv * dv, vd = nv * dv;
-    for (int l = 0; l < p->n_layers; ++l) {
-        const std::string pre = "layers." + std::to_string(l) + ".";
+    // a decoder layer's tensors under `pre` (the MTP layer's: "mtp.layers.0.", layer index n_layers, attention)
+    auto load_layer = [&](int l, const std::string &pre, bool attention) -> int {
         struct F32 {
             const char *name;
             int kind;
@@ -726,7 +728,7 @@ int gv_model_load_pack(gv_model *g, const gv_pack *p) {
             if (get_f32(pre + f.name, f.n, t) != 0 || adopt(f.kind, l, 0, buf.data(), buf.size(), nullptr) != 0)
                 return -1;
         float gl[3];
-        if (!p->attention[static_cast<size_t>(l)]) {   // a Gated DeltaNet layer (model.cpp:136-146)
+        if (!attention) {   // a Gated DeltaNet layer (model.cpp:136-146)
             struct Q {
                 const char *name;
                 int kind;
@@ -807,6 +809,28 @@ int gv_model_load_pack(gv_model *g, const gv_pack *p) {
             }
             if (adopt(GV_EXPERT, l, ex, src, blk.size(), &scales[static_cast<size_t>(2 * ex)]) != 0) return -1;
         }
+        return 0;
+    };
+    for (int l = 0; l < p->n_layers; ++l)
+        if (load_layer(l, "layers." + std::to_string(l) + ".", p->attention[static_cast<size_t>(l)]) != 0) return -1;
+    if (gv::model_of(g).has_mtp) {   // the MTP layer (model.cpp:175-191): its decoder layer, fc and norms, the draft head
+        GV_REQUIRE(p->mtp, "gv_model_load_pack: the model has an MTP layer and the pack none");
+        if (load_layer(p->n_layers, "mtp.layers.0.", true) != 0) return -1;
+        if (get("mtp.fc.weight", T_Q4, H, 2 * H, t) != 0 || adopt(GV_MTP_FC, 0, 0, buf.data(), buf.size(), &t->global) != 0)
+            return -1;
+        for (const auto &[name, kind] : {std::make_pair("mtp.norm.weight", GV_MTP_NORM),
+                                         std::make_pair("mtp.pre_fc_norm_embedding.weight", GV_MTP_PRE_E),
+                                         std::make_pair("mtp.pre_fc_norm_hidden.weight", GV_MTP_PRE_H)})
+            if (get_f32(name, H, t) != 0 || adopt(kind, 0, 0, buf.data(), buf.size(), nullptr) != 0) return -1;
+        // draft_vocab.bin (model.cpp:806-811): int32 token ids, those outside the vocabulary skipped
+        std::vector<int32_t> ids;
+        if (std::FILE *f = std::fopen((p->dir + "/draft_vocab.bin").c_str(), "rb")) {
+            int32_t id;
+            while (std::fread(&id, 4, 1, f) == 1)
+                if (id >= 0 && id < p->vocab) ids.push_back(id);
+            std::fclose(f);
+        }
+        if (gv_model_set_draft_vocab(g, ids.data(), static_cast<int>(ids.size())) != 0) return -1;
     }
     return gv_model_set_position(g, 0);
 }

@@ -65,9 +65,10 @@ class _Bin:
                 f.write(p)
 
 
-def write_pack(om, directory, tile8=False, extra_config=None, mutate=None):
+def write_pack(om, directory, tile8=False, extra_config=None, mutate=None, draft_vocab=None):
     """The oracle model om as a pack in directory; returns the manifest (dict). mutate(manifest) may damage it before
-    it is written (the refusal tests)."""
+    it is written (the refusal tests). A model with an MTP layer: its tensors under mtp.* (model.cpp:175-191) and the
+    manifest's "mtp" object with its experts (pack.cpp:303-305); draft_vocab: token ids for draft_vocab.bin."""
     os.makedirs(directory, exist_ok=True)
     c = om.cfg
     H, V, L, E = c["hidden"], c["vocab"], c["n_layers"], c["n_experts"]
@@ -88,11 +89,11 @@ def write_pack(om, directory, tile8=False, extra_config=None, mutate=None):
     put("norm.weight", "f32", (H,), om.tensor(po.FINAL_NORM)[0])
     layers = []
     gdn = c.get("gdn_layers", ())
-    for l in range(L):
-        p = f"layers.{l}."
+
+    def layer(l, p):
         put(p + "input_layernorm.weight", "f32", (H,), om.tensor(po.IN_NORM, l)[0])
         put(p + "post_attention_layernorm.weight", "f32", (H,), om.tensor(po.POST_NORM, l)[0])
-        if l < len(gdn) and gdn[l]:   # a Gated DeltaNet layer (Model::bind_layer, model.cpp:136-146)
+        if l < L and l < len(gdn) and gdn[l]:   # a Gated DeltaNet layer (Model::bind_layer, model.cpp:136-146)
             nk, nv, dk, dv, K = c["gdn_k_heads"], c["gdn_v_heads"], c["gdn_k_dim"], c["gdn_v_dim"], c["conv_kernel"]
             conv_dim, vd = 2 * nk * dk + nv * dv, nv * dv
             for kind, name, shape in ((po.GDN_QKV, "in_proj_qkv", (conv_dim, H)), (po.GDN_Z, "in_proj_z", (vd, H)),
@@ -132,8 +133,21 @@ def write_pack(om, directory, tile8=False, extra_config=None, mutate=None):
             off = experts.add(blk)
             first = off if first is None else first
         stride = (gu_bytes + H * (F // 16 * 9) + 63) // 64 * 64
-        layers.append({"file": "experts.bin", "offset": first, "stride": stride, "format": "q4"})
         put(p + "mlp.experts.scales", "f32", (E, 2), scales)
+        return {"file": "experts.bin", "offset": first, "stride": stride, "format": "q4"}
+
+    for l in range(L):
+        layers.append(layer(l, f"layers.{l}."))
+    mtp = None
+    if c.get("mtp"):
+        mtp = {"experts": layer(L, "mtp.layers.0.")}
+        t, g = om.tensor(po.MTP_FC)
+        put("mtp.fc.weight", "q4", (H, 2 * H), t, g[0])
+        for kind, name in ((po.MTP_NORM, "norm"), (po.MTP_PRE_E, "pre_fc_norm_embedding"),
+                           (po.MTP_PRE_H, "pre_fc_norm_hidden")):
+            put(f"mtp.{name}.weight", "f32", (H,), om.tensor(kind)[0])
+    if draft_vocab is not None:
+        np.asarray(draft_vocab, "<i4").tofile(os.path.join(directory, "draft_vocab.bin"))
     config = {"hidden_size": H, "num_hidden_layers": L, "vocab_size": V, "rms_norm_eps": c["eps"],
               "num_attention_heads": nh, "num_key_value_heads": nkv, "head_dim": hd,
               "rope_parameters": {"rope_theta": c["rope_theta"], "partial_rotary_factor": c["rope_dim"] / hd},
@@ -151,6 +165,8 @@ def write_pack(om, directory, tile8=False, extra_config=None, mutate=None):
          "files": [{"name": "dense.bin", "size": dense.size}, {"name": "experts.bin", "size": experts.size}],
          "config": config, "tensors": tensors, "experts": {"layers": layers},
          "formats": {"q4": {"layout": "tile8" if tile8 else "rows"}}}
+    if mtp:
+        m["mtp"] = mtp
     if mutate:
         mutate(m)
     with open(os.path.join(directory, "geode.json"), "w") as f:

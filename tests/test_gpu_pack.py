@@ -84,3 +84,37 @@ def test_gdn_pack_loads_as_the_direct_adoption(gv, tmp_path, tile8):
             np.testing.assert_array_equal(x, y)
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("vocab", [None, "draft"], ids=["whole", "draft_vocab"])
+def test_mtp_pack_loads_as_the_direct_adoption(gv, tmp_path, vocab):
+    """a pack with an MTP layer (mtp.* tensors, the manifest's "mtp" experts) and optionally a draft_vocab.bin (ids
+    outside the vocabulary skipped, model.cpp:806-811): the config's mtp flag, and the drafts and their logits after
+    a verify bit-identical to the direct adoption with the same draft vocabulary"""
+    cfg0 = dict(SMALL, mtp=1)
+    om = po.Model(cfg0, seed=23, router_sigma=SMALL_ROUTER_SIGMA, ctx=0)
+    ids = None if vocab is None else [5, 300, -1, 17, SMALL["vocab"], 260, 4, 99]
+    write_pack(om, str(tmp_path), draft_vocab=ids)
+    pack = gv.Pack(str(tmp_path))
+    cfg = pack.model_config(max_ctx=SMALL["max_ctx"], max_rows=SMALL["max_rows"])
+    assert cfg["mtp"] == 1
+    a = gv.VerifyModel(cfg0)
+    adopt_oracle_model(a, om, 0)
+    if ids is not None:
+        a.set_draft_vocab([i for i in ids if 0 <= i < SMALL["vocab"]])
+    b = gv.VerifyModel(cfg)
+    b.load_pack(pack)
+    try:
+        toks = np.array([3, 77, 410, 9, 200], np.int32)
+        np.testing.assert_array_equal(b.verify(toks), a.verify(toks))
+        nxt = np.array([77, 410, 9, 200, 12], np.int32)
+        assert a.draft(nxt, 0) == b.draft(nxt, 0)
+        np.testing.assert_array_equal(a.draft_logits(), b.draft_logits())
+        if ids is not None:
+            assert a.draft_logits().size == 6
+        d, _ = a.draft(nxt, 0)
+        assert a.draft_next(d, 5) == b.draft_next(d, 5)
+        np.testing.assert_array_equal(a.draft_logits(), b.draft_logits())
+    finally:
+        a.close()
+        b.close()

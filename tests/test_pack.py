@@ -70,6 +70,21 @@ def test_open_reads_the_tables(gv, om, tmp_path, tile8):
               "head_dim", "rope_dim"):
         assert cfg[k] == CFG[k], k
     assert cfg["rope_theta"] == np.float32(CFG["rope_theta"]) and cfg["eps"] == np.float32(CFG["eps"])
+    assert cfg["mtp"] == 0
+
+
+def test_mtp_pack_tables(gv, tmp_path):
+    """a pack with an MTP layer: the manifest's "mtp" experts are expert layer n_layers (pack.cpp:303-305, Pack::expert
+    past the main layers), its tensors are in the table, and the config asks for the MTP layer"""
+    om = po.Model(dict(CFG, mtp=1), seed=4)
+    m = write_pack(om, str(tmp_path))
+    p = gv.Pack(str(tmp_path))
+    files = [f["name"] for f in m["files"]]
+    for e in (0, CFG["n_experts"] - 1):
+        assert p.expert(CFG["n_layers"], e) == (files.index("experts.bin"),
+                                                m["mtp"]["experts"]["offset"] + e * m["mtp"]["experts"]["stride"], "q4")
+    assert p.tensor("mtp.fc.weight")["cols"] == 2 * CFG["hidden"]
+    assert p.model_config(96)["mtp"] == 1
 
 
 def _damage(what):
