@@ -1818,6 +1818,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
     Model *made = nullptr;   // once set, a failure frees what it allocated
     auto fail = [&](const std::string &msg) -> gv_model * {
         if (made) {
+            mtp_release(*made);
             for (void *p : made->allocs) (void)hipFree(p);
             made->allocs.clear();
         }
@@ -2001,7 +2002,7 @@ void gv_model_free(gv_model *g) {
     (void)hipStreamSynchronize(stream());
     for (auto &ge : g->m.graphs)
         if (ge) (void)hipGraphExecDestroy(ge);
-    mtp_free(g->m);
+    mtp_release(g->m);
     for (void *p : g->m.allocs) (void)hipFree(p);
     for (void *p : g->m.pf.allocs) (void)hipFree(p);
     if (g->m.trace) {   // the kernels stop stamping before the buffer goes

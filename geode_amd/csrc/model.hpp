@@ -166,6 +166,10 @@ struct Model {
     int32_t *draft_ids = nullptr; // device [draft_head.rows]
     uint8_t *draft_mem = nullptr;
     void *pick = nullptr;         // the draft pick's partials and result (mtp.hip)
+    int *pick_host = nullptr;     // pinned: the pick's draft and probability, and the fused launches' error flag
+    // an MTP pass as a HIP graph per (rows, with head), captured on its second use like the verify step's
+    hipGraphExec_t mtp_graphs[kMaxRows + 1][2] = {};
+    bool mtp_seen[kMaxRows + 1][2] = {};
 };
 
 constexpr int kAttnBlock = 64;   // positions an attention workgroup takes
@@ -190,6 +194,7 @@ int run_class(Model &m, int cls, int l, int M, hipStream_t st);
 const int *layer_classes(int &count);
 // the MTP layer's buffers (mtp.hip), at gv_model_create
 int mtp_alloc(Model &m);
-void mtp_free(Model &m);
+void mtp_free(Model &m);      // the draft head
+void mtp_release(Model &m);   // everything the MTP layer holds outside Model::allocs (at gv_model_free)
 
 }  // namespace gv

@@ -235,30 +235,62 @@ int mtp_launches(Model &m, int n, bool head, hipStream_t st) {
     return 0;
 }
 
-int mtp_pass(Model &m, int n, bool head) {
-    hipStream_t st = stream();
+// the pass's launches with the MTP step parameters swapped in: directly, or as the (rows, head) graph (captured on
+// the second use; every parameter is read from device memory, so one graph serves every position and token)
+int mtp_run(Model &m, int n, bool head, hipStream_t st) {
     StepParams *saved = m.sp;
     m.sp = m.sp_mtp;
-    const int rc = mtp_launches(m, n, head, st);
+    int rc = 0;
+    bool &seen = m.mtp_seen[n][head ? 1 : 0];
+    hipGraphExec_t &ge = m.mtp_graphs[n][head ? 1 : 0];
+    if (!m.use_graphs || m.timed_class >= 0 || !seen) {
+        seen = true;
+        rc = mtp_launches(m, n, head, st);
+    } else {
+        if (!ge) {
+            hipGraph_t graph = nullptr;
+            if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+                m.sp = saved;
+                GV_REQUIRE(false, "MTP pass: graph capture failed to start");
+            }
+            rc = mtp_launches(m, n, head, st);
+            const hipError_t e = hipStreamEndCapture(st, &graph);
+            if (rc == 0 && (e != hipSuccess || !graph)) rc = -1, set_error("MTP pass: graph capture failed");
+            if (rc == 0 && hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0) != hipSuccess)
+                rc = -1, ge = nullptr, set_error("MTP pass: graph instantiate failed");
+            if (graph) (void)hipGraphDestroy(graph);
+        }
+        if (rc == 0 && hipGraphLaunch(ge, st) != hipSuccess) rc = -1, set_error("MTP pass: graph launch failed");
+    }
     m.sp = saved;
-    if (rc != 0) return -1;
-    int err = 0;
-    GV_CHECK_HIP(hipMemcpyAsync(&err, m.err, 4, hipMemcpyDeviceToHost, st));
+    return rc;
+}
+
+// the pass, then its result (the draft and its probability, with the fused launches' error flag) in one wait
+int mtp_pass(Model &m, int n, bool head) {
+    hipStream_t st = stream();
+    if (mtp_run(m, n, head, st) != 0) return -1;
+    const auto *pa = static_cast<const PickArea *>(m.pick);
+    if (head) GV_CHECK_HIP(hipMemcpyAsync(m.pick_host, &pa->draft, 8, hipMemcpyDeviceToHost, st));
+    GV_CHECK_HIP(hipMemcpyAsync(m.pick_host + 2, m.err, 4, hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
-    GV_REQUIRE(err == 0, "MTP pass: a fused launch's wait for its producers ran out (the results are invalid)");
+    GV_REQUIRE(m.pick_host[2] == 0, "MTP pass: a fused launch's wait for its producers ran out (the results are invalid)");
     if (head) m.mtp_last_n = n;
     return 0;
 }
 
 int mtp_result(Model &m, int32_t *draft, float *prob) {
-    const auto *pa = static_cast<const PickArea *>(m.pick);
-    int32_t d = 0;
-    float p = 0.0f;
-    GV_CHECK_HIP(hipMemcpy(&d, &pa->draft, 4, hipMemcpyDeviceToHost));
-    GV_CHECK_HIP(hipMemcpy(&p, &pa->prob, 4, hipMemcpyDeviceToHost));
-    if (draft) *draft = d;
-    if (prob) *prob = p;
+    if (draft) *draft = m.pick_host[0];
+    if (prob) *prob = __builtin_bit_cast(float, m.pick_host[1]);
     return 0;
+}
+
+void drop_head_graphs(Model &m) {   // (the head changed: the passes with a head are captured again)
+    for (int n = 0; n <= kMaxRows; ++n) {
+        if (m.mtp_graphs[n][1]) (void)hipGraphExecDestroy(m.mtp_graphs[n][1]);
+        m.mtp_graphs[n][1] = nullptr;
+        m.mtp_seen[n][1] = false;
+    }
 }
 
 }  // namespace
@@ -273,6 +305,7 @@ int mtp_alloc(Model &m) {
     m.sp_mtp = static_cast<StepParams *>(mtp_dalloc(m, sizeof(StepParams)));
     m.pick = mtp_dalloc(m, sizeof(PickArea));
     if (!fc || !f || !m.mtp_act || !m.mtp_logits || !m.sp_mtp || !m.pick) return -1;
+    if (hipHostMalloc(reinterpret_cast<void **>(&m.pick_host), 16, hipHostMallocDefault) != hipSuccess) return -1;
     m.mtp_fc.codes = fc;
     m.mtp_fc.scales = fc + q4_code_bytes(H, 2 * H);
     m.mtp_fc.rows = H;
@@ -287,6 +320,15 @@ int mtp_alloc(Model &m) {
 void mtp_free(Model &m) {
     if (m.draft_mem) (void)hipFree(m.draft_mem);
     m.draft_mem = nullptr;
+}
+
+void mtp_release(Model &m) {
+    mtp_free(m);
+    for (auto &row : m.mtp_graphs)
+        for (auto &ge : row)
+            if (ge) (void)hipGraphExecDestroy(ge), ge = nullptr;
+    if (m.pick_host) (void)hipHostFree(m.pick_host);
+    m.pick_host = nullptr;
 }
 
 }  // namespace gv
@@ -369,6 +411,7 @@ int gv_model_set_draft_vocab(gv_model *g, const int32_t *ids, int n) {
     for (int i = 0; i < n; ++i) GV_REQUIRE(ids[i] >= 0 && ids[i] < c.vocab, "gv_model_set_draft_vocab: id out of range");
     GV_CHECK_HIP(hipStreamSynchronize(stream()));
     mtp_free(m);
+    drop_head_graphs(m);
     m.draft_head = Q4{};
     m.draft_ids = nullptr;
     if (n == 0) return 0;

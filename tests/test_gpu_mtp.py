@@ -242,3 +242,29 @@ def test_refusals(gv, pair):
         gm.draft(np.array([ATTN["vocab"]], np.int32), 0, hid[:1])
     with pytest.raises(gv.GeodeError):
         gm.set_draft_vocab([ATTN["vocab"]])
+
+
+def test_graph_replays_match_direct_launches(gv, pair):
+    """the MTP passes replayed from their graphs (captured on the second use of a row count) against direct launches:
+    four rounds of a draft and two chained drafts at moving positions, bit for bit, the draft head switched after the
+    second round (its graphs captured again)"""
+    gm = pair.gm
+    res = {}
+    for graphs in (True, False):
+        gm.set_graphs(graphs)
+        out = []
+        for r in range(4):
+            if r in (0, 2):
+                gm.set_draft_vocab(None if r == 0 else np.arange(3, 300, 2, dtype=np.int32))
+            toks, hid = _inputs(3, seed=100 + r)
+            pos = CTX + 4 * r
+            out.append((gm.draft(toks, pos, hid), gm.draft_logits().copy()))
+            d = out[-1][0][0]
+            for q in range(2):
+                out.append((gm.draft_next(d, pos + 3 + q), gm.draft_logits().copy()))
+                d = out[-1][0][0]
+        res[graphs] = out
+    gm.set_graphs(True)
+    gm.set_draft_vocab(None)
+    for (a, la), (b, lb) in zip(res[True], res[False]):
+        assert a == b and np.array_equal(la, lb)
