@@ -26,13 +26,13 @@ class GvModelConfig(_c.Structure):
                [("rope_theta", _c.c_float), ("eps", _c.c_float), ("max_ctx", _c.c_int32), ("max_rows", _c.c_int32),
                 ("kv_int8", _c.c_int32)] + \
                [(n, _c.c_int32) for n in ("gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel")] + \
-               [("gdn_layers", _c.c_uint8 * 256), ("mtp", _c.c_int32)]
+               [("gdn_layers", _c.c_uint8 * 256), ("mtp", _c.c_int32), ("exact", _c.c_int32)]
 
     @classmethod
     def of(cls, cfg):
         """the C struct of a config dict (kv_int8, the Gated DeltaNet fields and mtp optional, gdn_layers a list of
         flags)"""
-        optional = ("kv_int8", "gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel", "mtp")
+        optional = ("kv_int8", "gdn_k_heads", "gdn_v_heads", "gdn_k_dim", "gdn_v_dim", "conv_kernel", "mtp", "exact")
         c = cls(**{k: cfg.get(k, 0) if k in optional else cfg[k] for k, _ in cls._fields_ if k != "gdn_layers"})
         for l, g in enumerate(cfg.get("gdn_layers", ())):
             c.gdn_layers[l] = 1 if g else 0

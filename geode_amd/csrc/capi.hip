@@ -23,6 +23,7 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 struct Runtime {
     int device = -1;
     hipStream_t stream = nullptr;
+    int act_exact = 0;   // the products' operands now in every source file's g_act_exact
     std::vector<hipEvent_t> events;
     void *scratch_dev[kMaxDevices] = {};   // scratch's device address on each device (set by gv_init)
 };
@@ -33,6 +34,21 @@ Runtime &rt() {
 }
 
 hipStream_t stream() { return rt().stream; }
+
+// Every source file's copy of the operands' mode to `exact`, when it differs: the device idle before (no kernel may
+// read a copy while it changes) and after
+int use_act_mode(int exact) {
+    exact = exact ? 1 : 0;
+    if (rt().act_exact == exact) return 0;
+    GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    GV_CHECK_HIP(hipDeviceSynchronize());
+    if (act_mode_set_model(exact) != 0 || act_mode_set_q4(exact) != 0 || act_mode_set_gdn(exact) != 0 ||
+        act_mode_set_mtp(exact) != 0)
+        return -1;
+    GV_CHECK_HIP(hipDeviceSynchronize());
+    rt().act_exact = exact;
+    return 0;
+}
 
 int ensure_init() {
     if (rt().stream) return 0;
@@ -223,7 +239,7 @@ size_t gv_act_bytes(int64_t cols) { return act_bytes(cols); }
 
 int gv_quantize(const float *x, int64_t ldx, int M, int cols, const float *norm_w, float eps, uint8_t *act,
                 float *h_out) {
-    if (ensure_init() != 0) return -1;
+    if (ensure_init() != 0 || use_act_mode(0) != 0) return -1;
     return quantize_act(x, ldx, M, cols, norm_w, eps, reinterpret_cast<_Float16 *>(act), act_halves(cols), h_out, cols,
                         stream());
 }
@@ -242,13 +258,13 @@ size_t gv_ffn_workspace_bytes(int64_t hidden, int64_t ff, int M) {
 
 int gv_ffn_swiglu(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16, float *y,
                   void *ws) {
-    if (ensure_init() != 0) return -1;
+    if (ensure_init() != 0 || use_act_mode(0) != 0) return -1;
     return ffn_swiglu_ws(gate, up, down, M, x_f16, y, ws);
 }
 
 int gv_ffn_swiglu_noalloc(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, const uint16_t *x_f16,
                           float *y) {
-    if (ensure_init() != 0) return -1;
+    if (ensure_init() != 0 || use_act_mode(0) != 0) return -1;
     GV_REQUIRE(gate && up && down, "gv_ffn_swiglu_noalloc: null pointer");
     GV_REQUIRE(M >= 1 && M <= kMaxRows, "gv_ffn_swiglu_noalloc: 1 <= M <= 32");
     const size_t need = gv_ffn_workspace_bytes(gate->cols, gate->rows, M);
@@ -351,6 +367,7 @@ int gv_adopt_q4(gv_ctx *g, const uint8_t *data, int64_t rows, int64_t cols, size
 
 int gv_gemm(gv_ctx *g, int id, int n, const float *const *xs, float *const *ys) {
     GV_REQUIRE(g && id >= 0 && id < static_cast<int>(g->mats.size()) && n >= 0, "gv_gemm: bad arguments");
+    if (use_act_mode(0) != 0) return -1;   // the plugin's products: the int8 path
     const Q4 &q = g->mats[static_cast<size_t>(id)].q;
     hipStream_t st = stream();
     for (int t0 = 0; t0 < n; t0 += kMaxRows) {
@@ -382,6 +399,7 @@ int gv_mlp(gv_ctx *g, int gate, int up, int n_down, const int *downs, int act, i
     GV_REQUIRE(g && gate >= 0 && gate < nm && up >= 0 && up < nm && n_down >= 1 && downs && n >= 0,
                "gv_mlp: bad arguments");
     GV_REQUIRE(act == 1, "gv_mlp: only act 1 (silu) is supported");
+    if (use_act_mode(0) != 0) return -1;
     const Q4 &qg = g->mats[static_cast<size_t>(gate)].q, &qu = g->mats[static_cast<size_t>(up)].q;
     GV_REQUIRE(qg.rows == qu.rows && qg.cols == qu.cols, "gv_mlp: gate and up differ");
     const int64_t H = qg.cols, F = qg.rows;

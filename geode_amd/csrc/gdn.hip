@@ -539,6 +539,8 @@ int gdn_get_state(const Model &m, const LayerW &L, int slot, float *conv, float 
     return 0;
 }
 
+GV_ACT_MODE_SETTER(act_mode_set_gdn)
+
 int trace_set_gdn(uint64_t *p) {
     GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));
     return 0;

@@ -56,6 +56,13 @@ int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm
                  int64_t act_stride, float *h_out, int64_t ldh, hipStream_t st);
 int trace_set_q4(uint64_t *p);   // the gemv kernels' g_trace (q4.hip)
 int trace_set_gdn(uint64_t *p);  // the Gated DeltaNet kernel's g_trace (gdn.hip)
+// the products' operands of every source file's kernels: the int8 path's (0) or the exact path's (1) (mfma_gemv.hpp
+// g_act_exact); use_act_mode switches them all when the mode differs from the current one, waiting for the device
+int act_mode_set_model(int exact);
+int act_mode_set_q4(int exact);
+int act_mode_set_gdn(int exact);
+int act_mode_set_mtp(int exact);
+int use_act_mode(int exact);
 int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st);
 // the waves a product's K (a multiple of 128) splits over and the 32-value chunks each takes, for ntt 16-row tiles
 // of activations; 0 when one launch cannot take K (more than 8 waves)

@@ -47,9 +47,31 @@ inline size_t act16_row_bytes(int64_t cols) { return static_cast<size_t>(cols) *
 // engine/src/kernels.cpp:1254-1295, bit for bit) written as hi + lo halves at the group's 32 bytes. The 16-value
 // block is the groups g and g ^ 1, held by lanes l and l ^ 1: every lane of the wave calls this (live = false: a lane
 // past the row's end, which stores nothing).
-// 8 values of a 16-value block with the block's amax into their operands: q x (amax / 127) as hi + lo halves in
-// the slot order (0 4 1 5 2 6 3 7)
+// The products' operands are the int8 path's values (0, the reference's default) or the fp32 values themselves (1:
+// the exact path, ModelOptions::exact, engine/src/model.cpp:3337-3361 with kernels.cpp:1230-1250: fp32 activations
+// against the dequantized weights), both written as hi + lo halves (hi + lo = the value to 2^-22). Each source
+// file's kernels read their own copy; the act_mode_set_* functions set them (between launches only).
+static __constant__ int g_act_exact;
+#define GV_ACT_MODE_SETTER(name)                                                   \
+    int name(int exact) {                                                          \
+        GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_act_exact), &exact, sizeof exact)); \
+        return 0;                                                                  \
+    }
+
+// 8 values of a 16-value block with the block's amax into their operands: q x (amax / 127) (the exact path: the
+// values) as hi + lo halves in the slot order (0 4 1 5 2 6 3 7)
 __device__ inline void act16_operands(const float (&v)[8], float amax, h8 &hi, h8 &lo) {
+    if (g_act_exact) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int slot = i < 4 ? 2 * i : 2 * (i - 4) + 1;
+            _Float16 yh, yl;
+            split_f16(v[i], yh, yl);
+            hi[slot] = yh;
+            lo[slot] = yl;
+        }
+        return;
+    }
     const float s = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

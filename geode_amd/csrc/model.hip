@@ -870,8 +870,9 @@ __global__ __launch_bounds__(512) void moe_up_kernel(const MoeArgsDec a) {
             _Float16 h0, l0, h1, l1;
             const int q0 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r], qi))), -127), 127);
             const int q1 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r + 1], qi))), -127), 127);
-            split_f16(__fmul_rn(static_cast<float>(q0), sc), h0, l0);
-            split_f16(__fmul_rn(static_cast<float>(q1), sc), h1, l1);
+            const bool ex = g_act_exact != 0;   // (the exact path: the SwiGLU values themselves)
+            split_f16(ex ? mv[r] : __fmul_rn(static_cast<float>(q0), sc), h0, l0);
+            split_f16(ex ? mv[r + 1] : __fmul_rn(static_cast<float>(q1), sc), h1, l1);
             hw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
                         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
             lw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
@@ -1763,6 +1764,7 @@ int64_t qkv_rows(const gv_model_config &c) {
 }  // namespace
 
 int run_class(Model &m, int cls, int l, int M, hipStream_t st) { return launch_class(m, cls, l, M, st); }
+GV_ACT_MODE_SETTER(act_mode_set_model)
 const int *layer_classes(int &count) {
     count = static_cast<int>(sizeof(kLayerClassList) / sizeof(kLayerClassList[0]));
     return kLayerClassList;
@@ -1840,6 +1842,7 @@ gv_model *gv_model_create(const gv_model_config *cfg, char *err, int err_len) {
         return fail("1 <= top_k <= 16, top_k <= n_experts <= 256");
     if (c.max_rows <= 0 || c.max_rows > kMaxRows) return fail("max_rows must be 1..32");
     if (c.mtp != 0 && (c.mtp != 1 || c.hidden > 8192)) return fail("mtp must be 0 or 1 (an MTP layer: hidden at most 8192)");
+    if (c.exact != 0 && (c.exact != 1 || c.kv_int8 != 0)) return fail("exact must be 0 or 1, and the exact path takes no int8 cache");
     if (c.vocab <= 0 || c.n_layers <= 0 || c.max_ctx <= c.max_rows) return fail("vocab, n_layers, max_ctx");
     {
         std::string why;
@@ -2356,6 +2359,7 @@ int gv_model_position(const gv_model *g) { return g ? g->m.pos : -1; }
 int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents, float *logits) {
     GV_REQUIRE(g && tokens, "gv_verify: null pointer");
     Model &m = g->m;
+    if (use_act_mode(m.c.exact) != 0) return -1;
     const auto &c = m.c;
     GV_REQUIRE(n >= 1 && n <= c.max_rows, "gv_verify: 1 <= n <= max_rows");
     GV_REQUIRE(m.pos + n <= c.max_ctx, "gv_verify: the context is full");
@@ -2445,6 +2449,7 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
     GV_REQUIRE(g && ms_per_launch && cls >= 0 && cls < GV_K_COUNT && cls != GV_K_QUANT && reps >= 1,
                "gv_model_replay: bad arguments");
     Model &m = g->m;
+    if (use_act_mode(m.c.exact) != 0) return -1;
     GV_REQUIRE(layer >= 0 && layer < m.c.n_layers, "gv_model_replay: no such layer");
     GV_REQUIRE(m.last_n > 0, "gv_model_replay: no verify yet");
     const hipStream_t st = stream();
@@ -2515,6 +2520,7 @@ int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *rou
                  int32_t *ids, float *weights) {
     GV_REQUIRE(g && h && out, "gv_model_moe: null pointer");
     Model &m = g->m;
+    if (use_act_mode(m.c.exact) != 0) return -1;
     const auto &c = m.c;
     GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_moe: no such layer");
     GV_REQUIRE(M >= 1 && M <= 16384, "gv_model_moe: 1 <= M <= 16384");
@@ -2555,6 +2561,7 @@ int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32
                    float *x_out, int32_t *ids) {
     GV_REQUIRE(g && x_in, "gv_model_layer: null pointer");
     Model &m = g->m;
+    if (use_act_mode(m.c.exact) != 0) return -1;
     const auto &c = m.c;
     GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_layer: no such layer");
     GV_REQUIRE(n >= 1 && n <= c.max_rows && m.pos + n <= c.max_ctx, "gv_model_layer: 1 <= n <= max_rows, in context");
@@ -2606,6 +2613,7 @@ int gv_model_gdn_state(const gv_model *g, int layer, float *conv, float *S) {
 int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
     GV_REQUIRE(g && ms_per_block && reps >= 1, "gv_model_moe_replay: bad arguments");
     Model &m = g->m;
+    if (use_act_mode(m.c.exact) != 0) return -1;
     GV_REQUIRE(m.pf.M > 0, "gv_model_moe_replay: no gv_model_moe call to replay");
     const hipStream_t st = stream();
     if (moe_block(m, m.pf.layer, m.pf.M, m.pf.given, st) != 0) return -1;   // warm

@@ -269,6 +269,7 @@ int mtp_run(Model &m, int n, bool head, hipStream_t st) {
 // the pass, then its result (the draft and its probability, with the fused launches' error flag) in one wait
 int mtp_pass(Model &m, int n, bool head) {
     hipStream_t st = stream();
+    if (use_act_mode(m.c.exact) != 0) return -1;
     if (mtp_run(m, n, head, st) != 0) return -1;
     const auto *pa = static_cast<const PickArea *>(m.pick);
     if (head) GV_CHECK_HIP(hipMemcpyAsync(m.pick_host, &pa->draft, 8, hipMemcpyDeviceToHost, st));
@@ -294,6 +295,8 @@ void drop_head_graphs(Model &m) {   // (the head changed: the passes with a head
 }
 
 }  // namespace
+
+GV_ACT_MODE_SETTER(act_mode_set_mtp)
 
 int mtp_alloc(Model &m) {
     const auto &c = m.c;

@@ -278,6 +278,8 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     if (tc >= 0) trace(tc, 3);
 }
 
+GV_ACT_MODE_SETTER(act_mode_set_q4)
+
 int trace_set_q4(uint64_t *p) {
     GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));
     return 0;

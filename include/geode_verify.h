@@ -123,6 +123,10 @@ typedef struct gv_model_config {
      * n_layers (its tensors adopted with the per-layer kinds at that index, its KV after the main layers') behind
      * mtp.fc, with its own norms (GV_MTP_*); hidden at most 8192 */
     int32_t mtp;
+    /* 1: the exact path (ModelOptions::exact, GEODE_EXACT=1; engine/src/model.cpp:3337-3361): every product takes
+     * the fp32 activations instead of the int8 path's quantized ones (kv_int8 must be 0; the cache stays fp16, where
+     * the reference's exact path keeps fp32) */
+    int32_t exact;
 } gv_model_config;
 
 /* tensor kinds for gv_model_adopt (numbered as the CPU oracle's) */
