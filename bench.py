@@ -151,6 +151,53 @@ def bench_moe_block(g, M, reps):
     return ms, touched, byts, flops
 
 
+def bench_c1(g, reps=240, copies=48):
+    """C1: the dense SwiGLU FFN 2048 -> 6144 -> 2048 (gate, up [6144 x 2048], down [2048 x 6144], weights N(0, 0.02)
+    packed by the library's own packer on the device), x fp16 N(0, 1) [5 x 2048]; device time of gv_ffn_swiglu cycling
+    through `copies` copies of the weights at distinct addresses (48 x 21.2 MB = 1.02 GB > the 256 MB Infinity
+    Cache), hipEvents around `reps` back-to-back calls"""
+    import ctypes as C
+    H, F, M = 2048, 6144, 5
+    rng = np.random.default_rng(SEED + 1)
+    glob = g.DeviceBuffer(16)
+    mats = []
+    for i, (rows, cols) in enumerate(((F, H), (F, H), (H, F))):   # gate, up, down: packed once, copied
+        w = g.DeviceBuffer.from_array(rng.normal(0.0, 0.02, (rows, cols)).astype(np.float32))
+        pack = g.DeviceBuffer(rows * Q4_ROW(cols))
+        g.check(g.lib.gv_q4_pack(w.ptr, rows, cols, pack.ptr, glob.ptr), "gv_q4_pack")
+        gl = float(glob.download(np.float32, (1,))[0])
+        w.free()
+        mats.append((rows, cols, pack, gl))
+    sets, bufs = [], []
+    for _ in range(copies):
+        one = []
+        for rows, cols, pack, gl in mats:
+            buf = g.DeviceBuffer(g.lib.gv_q4_device_bytes(rows, cols))
+            d = g.GvQ4()
+            g.check(g.lib.gv_q4_from_pack(pack.ptr, rows, cols, gl, buf.ptr, C.byref(d)), "gv_q4_from_pack")
+            bufs.append(buf)
+            one.append(d)
+        sets.append(one)
+    x = g.DeviceBuffer.from_array(rng.standard_normal((M, H)).astype(np.float16))
+    y = g.DeviceBuffer(M * H * 4)
+    ws = g.DeviceBuffer(g.lib.gv_ffn_workspace_bytes(H, F, M))
+
+    def call(i):
+        a, b, d = sets[i % copies]
+        g.check(g.lib.gv_ffn_swiglu(C.byref(a), C.byref(b), C.byref(d), M, x.ptr, y.ptr, ws.ptr), "gv_ffn_swiglu")
+
+    for i in range(copies):
+        call(i)
+    g.check(g.lib.gv_synchronize(), "sync")
+    e0 = g.lib.gv_event_record()
+    for i in range(reps):
+        call(i)
+    e1 = g.lib.gv_event_record()
+    us = g.lib.gv_event_elapsed_ms(e0, e1) / reps * 1e3
+    byts = 2 * F * Q4_ROW(H) + H * Q4_ROW(F) + M * H * 2 + M * H * 4   # 21,295,104 B (fp16 in, fp32 out)
+    return us, byts
+
+
 def bench_c2(g, trials):
     """C2: target logits [5 x V] ~ N(0, 3), draft [4 x V] = target rows 0..3 + N(0, 0.5), T 0.7, top-p 0.95; the
     textbook rule per trial (seeded uniforms), stochastic and greedy, and sample-and-match of the 5 rows; logits
@@ -295,6 +342,18 @@ def main_config(args):
                                                  "vocab 248320, int8 KV, ctx 8192; chain M=5 and tree M=17"},
                           "detail": r}))
         return
+    if args.config == "c1":
+        us, byts = bench_c1(g)
+        print(json.dumps({"metric": "C1 dense SwiGLU FFN: HBM GB/s vs peak", "value": byts / (us / 1e6) / 1e9,
+                          "unit": "GB/s", "n_gpus": 1, "steps": 240, "warmup": 48, "us_per_call": us,
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+                          "data": "synthetic",
+                          "config": {"workload": "C1: 2048 -> 6144 -> 2048 SwiGLU FFN, M=5, x fp16 N(0,1), weights "
+                                                 "N(0,0.02) q4, 48 weight copies rotated (1.02 GB)"},
+                          "bytes_per_call": byts,
+                          "roofline": {"bound": "hbm", "achieved": byts / (us / 1e6) / 1e9, "peak": PEAK_HBM / 1e9,
+                                       "unit": "GB/s", "frac": byts / (us / 1e6) / PEAK_HBM, "traffic": None}}))
+        return
     if args.config in ("c3", "c5"):
         M = 5 if args.config == "c3" else 512
         ms, touched, byts, flops = bench_moe_block(g, M, 20 if M > 5 else 100)
@@ -328,9 +387,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a 256 MiB device copy, three times: the known traffic that scales HBM byte counters")
-    ap.add_argument("--config", choices=["c4", "c2", "c3", "c5", "real"], default="c4",
-                    help="c4 (default): the verify step; c2 / c3 / c5: the acceptance rules / one MoE block; real: "
-                         "the real model's shape with its Gated DeltaNet layers")
+    ap.add_argument("--config", choices=["c4", "c1", "c2", "c3", "c5", "real"], default="c4",
+                    help="c4 (default): the verify step; c1: the dense SwiGLU FFN; c2 / c3 / c5: the acceptance rules "
+                         "/ one MoE block; real: the real model's shape with its Gated DeltaNet layers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the verify step on one GPU only: the step of one sequence does not shard "

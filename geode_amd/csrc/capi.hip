@@ -293,8 +293,17 @@ int ffn_swiglu_ws(const gv_q4 *gate, const gv_q4 *up, const gv_q4 *down, int M, 
     float *m = u + static_cast<size_t>(M) * F;
     _Float16 *act = reinterpret_cast<_Float16 *>(m + static_cast<size_t>(M) * F);
     hipStream_t st = stream();
-    if (f16_to_f32(x_f16, static_cast<int64_t>(M) * H, x, st) != 0) return -1;
     const int64_t ab_h = act_halves(H), ab_f = act_halves(F);
+    int waves = 0, kw = 0;
+    if (M <= 8 && F % 16 == 0 && H <= 8192 && mfma_split(H, 1, waves, kw) && waves <= 4) {
+        // three launches: x's operands (in x's place: M act rows of H fit its M x H floats), gate | up with the
+        // SwiGLU and its quantization (act), down
+        _Float16 *act_x = reinterpret_cast<_Float16 *>(x);
+        if (quantize_f16(x_f16, M, static_cast<int>(H), act_x, ab_h, st) != 0) return -1;
+        if (ffn_up(to_q4(*gate), to_q4(*up), act_x, ab_h, M, act, ab_f, st) != 0) return -1;
+        return gemv_q4(to_q4(*down), act, ab_f, M, gemv_out(y, H, down->global), st);
+    }
+    if (f16_to_f32(x_f16, static_cast<int64_t>(M) * H, x, st) != 0) return -1;
     if (quantize_act(x, H, M, static_cast<int>(H), nullptr, 0.0f, act, ab_h, nullptr, 0, st) != 0) return -1;
     if (gemv_q4(to_q4(*gate), act, ab_h, M, gemv_out(g, F, gate->global), st) != 0) return -1;
     if (gemv_q4(to_q4(*up), act, ab_h, M, gemv_out(u, F, up->global), st) != 0) return -1;

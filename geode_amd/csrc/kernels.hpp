@@ -64,6 +64,10 @@ int act_mode_set_gdn(int exact);
 int act_mode_set_mtp(int exact);
 int use_act_mode(int exact);
 int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st);
+// C1's dense FFN pieces: fp16 rows to operands; gate and up with the SwiGLU and its quantization (M <= 8)
+int quantize_f16(const uint16_t *x, int M, int cols, _Float16 *act, int64_t act_stride, hipStream_t st);
+int ffn_up(const Q4 &gate, const Q4 &up, const _Float16 *act, int64_t act_stride, int M, _Float16 *act_m,
+           int64_t act_m_stride, hipStream_t st);
 // the waves a product's K (a multiple of 128) splits over and the 32-value chunks each takes, for ntt 16-row tiles
 // of activations; 0 when one launch cannot take K (more than 8 waves)
 int mfma_split(int64_t K, int ntt, int &waves, int &kw);

@@ -279,6 +279,122 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
 }
 
 GV_ACT_MODE_SETTER(act_mode_set_q4)
+// ---------------------------------------------------------------- the dense SwiGLU FFN (C1) in three launches
+// x fp16 rows to the products' operands (the int8 path's quantization of the fp32 values, which fp16 converts to
+// exactly): a workgroup a row
+__global__ __launch_bounds__(256) void quantize_f16_kernel(const uint16_t *__restrict__ x, int cols,
+                                                           _Float16 *__restrict__ act, int64_t act_stride) {
+    __shared__ double red[16];
+    const int t = blockIdx.x, ng = cols / 8;
+    float v[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int g = threadIdx.x + q * blockDim.x;
+        uint4 w = make_uint4(0, 0, 0, 0);
+        if (g < ng) w = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(t) * cols + g * 8);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[q][2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u[i] & 0xFFFFu)));
+            v[q][2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u[i] >> 16)));
+        }
+    }
+    norm_quant_regs(v, cols, nullptr, 0.0f, act + static_cast<int64_t>(t) * act_stride, nullptr, red);
+}
+
+// The gate and up products with the SwiGLU and its quantization in one launch: a workgroup per 16-row tile pair
+// (gate tile p, up tile p), its waves splitting K as the skinny product does (the same sums, in the same order); the
+// 16 values m = silu(g) x u of a row and tile are one quantization block, so the down product's operands are the
+// workgroup's own (at most 8 rows: the rows' hi and lo halves in the MFMA's columns).
+template <int KW>
+__global__ __launch_bounds__(256) void ffn_up_kernel(Q4 gate, Q4 up, const _Float16 *__restrict__ act,
+                                                     int64_t act_stride, int M, _Float16 *__restrict__ act_m,
+                                                     int64_t act_m_stride) {
+    extern __shared__ f4 part_lds[];
+    __shared__ uint2 tab[256];
+    const int p = blockIdx.x, W = blockDim.x / 64, lane = threadIdx.x % 64;
+    const int nsc = static_cast<int>(gate.cols / kSuperK);
+    auto rowp = [&](int j) { return act + static_cast<int64_t>(min(j, M - 1)) * act_stride; };
+    auto tile = [&](int) -> int64_t { return p; };
+    mfma_tiles<KW, 1, kKeepParts, 1, 2, true>(gate.codes, gate.scales, gate.rows, nsc, 0, 1, M, rowp,
+                                              [](int64_t, int, float) {}, part_lds, tab, tile);
+    mfma_tiles<KW, 1, kKeepParts, 1, 2, true>(up.codes, up.scales, up.rows, nsc, 0, 1, M, rowp,
+                                              [](int64_t, int, float) {}, part_lds + W * 64, tab, tile);
+    if (threadIdx.x >= 64) return;
+    // the waves' sums in wave order x global (the products' put), m = silu(g) x u (swiglu's arithmetic), the block's
+    // operands (quantize_activation); lane (j = lane % 16, lg = lane / 16): rows 4 lg .. 4 lg + 3 of the tile, row j
+    const int j = lane % 16, lg = lane / 16;
+    f4 gs = part_lds[lane], us = part_lds[W * 64 + lane];
+    for (int w2 = 1; w2 < W; ++w2) {
+        gs += part_lds[w2 * 64 + lane];
+        us += part_lds[(W + w2) * 64 + lane];
+    }
+    float mv[4], amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = gs[r] * gate.global, uv = us[r] * up.global;
+        mv[r] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), uv);
+        amax = fmaxf(amax, fabsf(mv[r]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const float sc = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    uint32_t hw[2], lw[2];
+#pragma unroll
+    for (int r = 0; r < 4; r += 2) {
+        _Float16 h0, l0, h1, l1;
+        const int q0 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r], qi))), -127), 127);
+        const int q1 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r + 1], qi))), -127), 127);
+        const bool ex = g_act_exact != 0;   // (the exact path: the SwiGLU values themselves)
+        split_f16(ex ? mv[r] : __fmul_rn(static_cast<float>(q0), sc), h0, l0);
+        split_f16(ex ? mv[r + 1] : __fmul_rn(static_cast<float>(q1), sc), h1, l1);
+        hw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                    (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+        lw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
+                    (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+    }
+    // k-group 2 p + lg / 2 holds values 0..3 (lane lg even) and 4..7 (lane lg + 1) in the slot order
+    // (0 4 1 5 2 6 3 7): the even lane takes its partner's four and writes the group
+    uint32_t ph[2], pl[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        ph[k] = __shfl_xor(hw[k], 16, 64);
+        pl[k] = __shfl_xor(lw[k], 16, 64);
+    }
+    if ((lg & 1) == 0 && j < M) {
+        auto inter = [](uint32_t mine, uint32_t other) {
+            return make_uint2((mine & 0xFFFFu) | (other << 16), (mine >> 16) | (other & 0xFFFF0000u));
+        };
+        const uint2 h01 = inter(hw[0], ph[0]), h23 = inter(hw[1], ph[1]);
+        const uint2 l01 = inter(lw[0], pl[0]), l23 = inter(lw[1], pl[1]);
+        uint4 *dst = reinterpret_cast<uint4 *>(act_m + j * act_m_stride + static_cast<int64_t>(2 * p + lg / 2) * 16);
+        dst[0] = make_uint4(h01.x, h01.y, h23.x, h23.y);
+        dst[1] = make_uint4(l01.x, l01.y, l23.x, l23.y);
+    }
+}
+
+int quantize_f16(const uint16_t *x, int M, int cols, _Float16 *act, int64_t act_stride, hipStream_t st) {
+    GV_REQUIRE(cols % 16 == 0 && cols <= 8192 && M > 0, "quantize_f16: cols must be a multiple of 16, at most 8192");
+    hipLaunchKernelGGL(quantize_f16_kernel, dim3(M), dim3(256), 0, st, x, cols, act, act_stride);
+    GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+int ffn_up(const Q4 &gate, const Q4 &up, const _Float16 *act, int64_t act_stride, int M, _Float16 *act_m,
+           int64_t act_m_stride, hipStream_t st) {
+    int waves = 0, kw = 0;
+    GV_REQUIRE(M >= 1 && M <= 8 && gate.rows == up.rows && gate.cols == up.cols && gate.rows % kTileR == 0 &&
+                   mfma_split(gate.cols, 1, waves, kw) && waves <= 4,
+               "ffn_up: 1 <= M <= 8, gate and up alike, whole row tiles, K split over at most 4 waves");
+    const dim3 grid(static_cast<unsigned>(gate.rows / kTileR)), block(static_cast<unsigned>(64 * waves));
+    const size_t lds = static_cast<size_t>(2 * waves) * 1024;
+    if (kw == 16) hipLaunchKernelGGL(ffn_up_kernel<16>, grid, block, lds, st, gate, up, act, act_stride, M, act_m, act_m_stride);
+    else if (kw == 8) hipLaunchKernelGGL(ffn_up_kernel<8>, grid, block, lds, st, gate, up, act, act_stride, M, act_m, act_m_stride);
+    else hipLaunchKernelGGL(ffn_up_kernel<4>, grid, block, lds, st, gate, up, act, act_stride, M, act_m, act_m_stride);
+    GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
 
 int trace_set_q4(uint64_t *p) {
     GV_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p));

@@ -119,9 +119,11 @@ def test_gemv_accumulate(gv):
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
 
 
-def test_c1_ffn_swiglu(gv):
-    """C1: hidden 2048 -> 6144 -> 2048 SwiGLU, weights N(0, 0.02) packed, x fp16 N(0,1) at M = 5."""
-    H, F, M = 2048, 6144, 5
+@pytest.mark.parametrize("M", [5, 8, 9, 17])
+def test_c1_ffn_swiglu(gv, M):
+    """C1: hidden 2048 -> 6144 -> 2048 SwiGLU, weights N(0, 0.02) packed, x fp16 N(0,1) at M = 5 (and 8: the fused
+    three-launch path; 9, 17: the general one)."""
+    H, F = 2048, 6144
     gq, gg = po.q4_random(1001, F, H)
     uq, ug = po.q4_random(1002, F, H)
     dq, dg = po.q4_random(1003, H, F)
