@@ -488,6 +488,126 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     trace(GV_K_MERGE, 3);
 }
 
+// attn_merge_kernel's arithmetic with the head's dims split over workgroups (head_dim a multiple of 64): a workgroup
+// per (row, head, 64 dims), four times the workgroups with a quarter of the loads each at head_dim 256. Lane
+// (phase ph = 4 wave + lane / 16, dims 4 (lane % 16) .. + 3 of the part) adds the blocks b = ph mod 16 in order; the
+// sixteen phases' sums are then added in a fixed order (lanes by xor 16 then 32, the waves in order).
+__global__ __launch_bounds__(256) void attn_merge64_kernel(const float *__restrict__ parts, const float *__restrict__ qkv,
+                                                           int64_t ldq, int nh, int hd, int nb_max,
+                                                           const StepParams *__restrict__ sp,
+                                                           _Float16 *__restrict__ act, int64_t act_stride) {
+    __shared__ float fw[1024];
+    __shared__ float red[2][4];
+    __shared__ float4 osum[4][16];
+    trace(GV_K_MERGE, 0);
+    const int t = blockIdx.x, h = blockIdx.y, part = blockIdx.z;
+    if (t >= sp->M) return;
+    const int nbw = (sp->pos + sp->M + kAttnBlock - 1) / kAttnBlock;
+    const int ld = hd + 2;
+    const float *base = parts + ((static_cast<int64_t>(t) * nh + h) * nb_max) * ld;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ph = 4 * wave + lane / 16, dq = lane % 16;
+    const int d0 = part * 64 + 4 * dq;
+    // every load of the first pass at once (indices clamped as in attn_merge_kernel): the blocks' maxima and sums,
+    // the phase's first kB blocks' four dims, the gate values of wave 0's groups
+    float bm[4], bs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int bb = min(static_cast<int>(threadIdx.x) + 256 * k, nbw - 1);
+        bm[k] = base[bb * ld + hd];
+        bs[k] = base[bb * ld + hd + 1];
+    }
+    constexpr int kB = 9;   // blocks a phase (144 blocks a workgroup: 9216 positions)
+    float4 pv[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) pv[u] = *reinterpret_cast<const float4 *>(base + min(ph + 16 * u, nbw - 1) * ld + d0);
+    const int g = min(lane, 7);   // wave 0: lane g < 8 takes group part * 8 + g (8 dims)
+    float gate[8];
+    {
+        const float *gp = qkv + t * ldq + static_cast<int64_t>(h) * 2 * hd + hd + part * 64 + 8 * g;
+        const float4 a = *reinterpret_cast<const float4 *>(gp), b = *reinterpret_cast<const float4 *>(gp + 4);
+        const float g8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) gate[i] = g8[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float mx = fmaxf(fmaxf(bm[0], bm[1]), fmaxf(bm[2], bm[3]));
+    mx = wave_max(mx);
+    if (lane == 0) red[0][wave] = mx;
+    __syncthreads();
+    trace(GV_K_MERGE, 1);
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float l = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int bb = threadIdx.x + 256 * k;
+        if (bb >= nbw) break;
+        const float f = bm[k] == -__builtin_inff() ? 0.0f : expf(__fsub_rn(bm[k], mx));
+        fw[bb] = f;
+        l = __builtin_fmaf(bs[k], f, l);
+    }
+    l = static_cast<float>(wave_sum(static_cast<double>(l)));
+    if (lane == 0) red[1][wave] = l;
+    __syncthreads();
+    const float inv = __fdiv_rn(1.0f, ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3]);
+    float4 o = make_float4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+        const int bb = ph + 16 * u;
+        const float f = bb < nbw ? fw[bb] : 0.0f;   // (a clamped block: weight 0)
+        o.x = __builtin_fmaf(pv[u].x, f, o.x);
+        o.y = __builtin_fmaf(pv[u].y, f, o.y);
+        o.z = __builtin_fmaf(pv[u].z, f, o.z);
+        o.w = __builtin_fmaf(pv[u].w, f, o.w);
+    }
+    for (int b = ph + 16 * kB; b < nbw; b += 16 * 8) {   // longer contexts: eight blocks a phase at a time
+        float4 w4[8];
+        float f[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const bool in = b + 16 * u < nbw;
+            w4[u] = in ? *reinterpret_cast<const float4 *>(base + (b + 16 * u) * ld + d0) : make_float4(0, 0, 0, 0);
+            f[u] = in ? fw[b + 16 * u] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            o.x = __builtin_fmaf(w4[u].x, f[u], o.x);
+            o.y = __builtin_fmaf(w4[u].y, f[u], o.y);
+            o.z = __builtin_fmaf(w4[u].z, f[u], o.z);
+            o.w = __builtin_fmaf(w4[u].w, f[u], o.w);
+        }
+    }
+#pragma unroll
+    for (int x = 16; x <= 32; x *= 2) {   // the wave's four phases: (p0 + p1) + (p2 + p3) on every lane
+        o.x += __shfl_xor(o.x, x, 64);
+        o.y += __shfl_xor(o.y, x, 64);
+        o.z += __shfl_xor(o.z, x, 64);
+        o.w += __shfl_xor(o.w, x, 64);
+    }
+    if (lane < 16) osum[wave][lane] = o;
+    __syncthreads();
+    trace(GV_K_MERGE, 2);
+    if (wave == 0) {   // the gated output of the part's 8 groups (a k-group of the projection's operands a lane)
+        float v[8];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            float4 s4 = osum[0][2 * g + half];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) {
+                const float4 a = osum[w][2 * g + half];
+                s4.x += a.x, s4.y += a.y, s4.z += a.z, s4.w += a.w;
+            }
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gate[4 * half + i])));
+                v[4 * half + i] = __fmul_rn(__fmul_rn(sv[i], inv), sig);
+            }
+        }
+        act16_group(v, h * (hd / 8) + part * 8 + g, lane < 8, act + static_cast<int64_t>(t) * act_stride);
+    }
+    trace(GV_K_MERGE, 3);
+}
+
 // the route alone (rows' logits given after the router: the MoE block entry point)
 __global__ __launch_bounds__(1024) void route_kernel(const float *__restrict__ logits, int E, int K,
                                                     const StepParams *__restrict__ sp, RouteState *__restrict__ rs,
@@ -1538,8 +1658,12 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         return launch_attn(m, L, st);
     }
     case GV_K_MERGE:
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
-                           m.kv_blocks, m.sp, m.act_core, abC);
+        if (hd % 64 == 0)
+            hipLaunchKernelGGL(attn_merge64_kernel, dim3(M, nh, hd / 64), dim3(256), 0, st, m.parts, m.qkv_out,
+                               L.qkv.rows, nh, hd, m.kv_blocks, m.sp, m.act_core, abC);
+        else
+            hipLaunchKernelGGL(attn_merge_kernel, dim3(M, nh), dim3(256), 0, st, m.parts, m.qkv_out, L.qkv.rows, nh, hd,
+                               m.kv_blocks, m.sp, m.act_core, abC);
         return 0;
     case GV_K_O: {   // the residual add is the product's accumulate
         if (mixout) return launch_mixout(m, L, l, M, mix_kw, st);   // with the router and the route
