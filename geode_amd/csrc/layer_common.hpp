@@ -157,9 +157,9 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
     const int E1 = E + 1;
     trace(GV_K_ROUTE, 0);
     for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
-    if (M <= waves) {   // a row a wave
-        if (wave < M) {
-            const int t0 = wave;
+    if (M < 2 * waves) {   // a row a wave (the first M - waves waves a second one after it: a pair in every wave
+                           // would run the second row's instructions, masked, in all of them)
+        for (int t0 = wave; t0 < M; t0 += waves) {
             const float *const lg[1] = {logits + static_cast<int64_t>(t0) * E1};
             const bool live[1] = {true};
             int *const ids[1] = {&r.ids[t0 * 16]};
