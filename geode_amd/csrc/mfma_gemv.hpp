@@ -288,16 +288,19 @@ enum TilesMode { kSplitK = 0, kKeepParts = 1, kWaveTiles = 2 };
 // halves (8..15), so one MFMA chain makes both products (each column's sum is the one the unpacked form makes) and a
 // lane swap adds them; else the hi and lo halves are two chains. put(row, j, v) takes the fp32 sum (before global).
 // part: LDS of max(nt, NT) * W * NTT KB for the waves' partial sums (kSplitK, kKeepParts: part[((i W + w) NTT + tt)
-// 64 + lane], left there after a workgroup barrier in kKeepParts); tab: LDS for fill_e4m3_table, filled here. hook()
+// 64 + lane], left there after a workgroup barrier in kKeepParts); FLUSH > 0 (kSplitK, runtime loop): the sums of
+// every FLUSH tiles are put as soon as those tiles are done, so part holds FLUSH * W * NTT KB whatever nt is (the
+// activations stay in registers over many tiles); tab: LDS for fill_e4m3_table, filled here. hook()
 // runs after the first tiles' loads are issued and before the activations are loaded (a wait for them); ready() once
 // the activations and the first tiles are in registers. Every thread of the workgroup calls this.
-template <int KW, int NTT, int MODE, int NT = 0, int DEPTH = 3, bool PACK = false, typename RowFn, typename PutFn,
-          typename MapFn = TileRun, typename HookFn = NoHook, typename ReadyFn = NoHook>
+template <int KW, int NTT, int MODE, int NT = 0, int DEPTH = 3, bool PACK = false, int FLUSH = 0, typename RowFn,
+          typename PutFn, typename MapFn = TileRun, typename HookFn = NoHook, typename ReadyFn = NoHook>
 __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, int64_t rows,
                                   int nsc, int sc0, int nt, int M, RowFn rowp, PutFn put, f4 *part, uint2 *tab,
                                   MapFn tmap, HookFn hook = HookFn{}, ReadyFn ready = ReadyFn{}) {
-    static_assert(DEPTH >= 2 && (NT > 0 || DEPTH == 3), "the runtime loop is a ring of three");
+    static_assert(DEPTH >= 2 && (NT > 0 || DEPTH >= 3), "the runtime loop is a ring of at least three");
     static_assert(!PACK || NTT == 1, "packed hi | lo columns take one 16-row tile of at most 8 rows");
+    static_assert(FLUSH == 0 || (MODE == kSplitK && NT == 0), "the flushed split-K runs the runtime tile loop");
     constexpr int NB = PACK ? 1 : 2;   // operand arrays: hi | lo packed, or hi and lo
     const int W = MODE == kWaveTiles ? 1 : static_cast<int>(blockDim.x / 64);
     const int w = MODE == kWaveTiles ? 0 : static_cast<int>(threadIdx.x / 64);
@@ -402,7 +405,7 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
         f4 (&res)[NTT] = acc[0];
         if (MODE != kWaveTiles) {
 #pragma unroll
-            for (int tt = 0; tt < NTT; ++tt) part[((i * W + w) * NTT + tt) * 64 + l] = res[tt];
+            for (int tt = 0; tt < NTT; ++tt) part[(((FLUSH ? i % FLUSH : i) * W + w) * NTT + tt) * 64 + l] = res[tt];
         } else if (i < nt) {
             const int64_t T = tmap(i);
 #pragma unroll
@@ -416,6 +419,24 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             }
         }
     };
+    // the waves' partial sums of tiles [i0, i1) (at i - i0 in part, or i when every tile's are kept) added in wave
+    // order, each output by one thread
+    auto split_k_out = [&](int i0, int i1) {
+        __syncthreads();
+        for (int o = threadIdx.x; o < (i1 - i0) * NTT * 64; o += blockDim.x) {
+            const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+            f4 sum = part[((i * W + 0) * NTT + tt) * 64 + ll];
+            for (int w2 = 1; w2 < W; ++w2) sum += part[((i * W + w2) * NTT + tt) * 64 + ll];
+            const int j = tt * 16 + ll % 16;
+            const int64_t T = tmap(i0 + i);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = T * kTileR + 4 * (ll / 16) + r;
+                if (j < M && row < rows) put(row, j, sum[r]);
+            }
+        }
+        if (FLUSH) __syncthreads();   // (the next tiles write the same LDS)
+    };
     if constexpr (NT > 0) {
         ready();
         // straight-line: tile i + DEPTH - 1's loads go to the slot tile i - 1 used, then tile i is computed
@@ -425,42 +446,30 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
             tile(i, cw[i % DEPTH], sw[i % DEPTH]);
         }
     } else {
-        // a ring of three tiles' loads: two in flight while one is computed. Everything loaded so far (the
-        // activations, the first two tiles) is waited for here, once: the loop then starts from the state its back
-        // edge has (two tiles in flight).
+        // a ring of DEPTH tiles' loads: DEPTH - 1 in flight while one is computed. Everything loaded so far (the
+        // activations, the first DEPTH - 1 tiles) is waited for here, once: the loop then starts from the state its
+        // back edge has (DEPTH - 1 tiles in flight). Tile i + d is computed from slot d, its slot then refilled with
+        // tile i + d + DEPTH ... by the load issued just before it (slot (d + DEPTH - 1) % DEPTH).
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0) (expcnt, lgkmcnt: no wait)
         ready();
-        for (int i = 0; i < nt; i += 3) {
-            load(i + 2, cw[2], sw[2]);
-            tile(i, cw[0], sw[0]);
-            if (i + 1 >= nt) break;
-            load(i + 3, cw[0], sw[0]);
-            tile(i + 1, cw[1], sw[1]);
-            if (i + 2 >= nt) break;
-            load(i + 4, cw[1], sw[1]);
-            tile(i + 2, cw[2], sw[2]);
+        for (int i = 0; i < nt; i += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                if (i + d >= nt) break;
+                load(i + d + DEPTH - 1, cw[(d + DEPTH - 1) % DEPTH], sw[(d + DEPTH - 1) % DEPTH]);
+                tile(i + d, cw[d], sw[d]);
+                if constexpr (FLUSH > 0) {   // every FLUSH tiles (and the last): their sums out, the LDS free again
+                    const int done = i + d + 1;
+                    if (done % FLUSH == 0 || done == nt) split_k_out(done - 1 - (done - 1) % FLUSH, done);
+                }
+            }
         }
     }
     if (MODE == kKeepParts) {
         __syncthreads();
         return;
     }
-    // the waves' partial sums added in wave order, each output by one thread
-    if (MODE == kSplitK) {
-        __syncthreads();
-        for (int o = threadIdx.x; o < nt * NTT * 64; o += blockDim.x) {
-            const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
-            f4 sum = part[((i * W + 0) * NTT + tt) * 64 + ll];
-            for (int w2 = 1; w2 < W; ++w2) sum += part[((i * W + w2) * NTT + tt) * 64 + ll];
-            const int j = tt * 16 + ll % 16;
-            const int64_t T = tmap(i);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = T * kTileR + 4 * (ll / 16) + r;
-                if (j < M && row < rows) put(row, j, sum[r]);
-            }
-        }
-    }
+    if (MODE == kSplitK && FLUSH == 0) split_k_out(0, nt);
 }
 
 }  // namespace gv

@@ -875,6 +875,8 @@ __global__ __launch_bounds__(512) void mixout_kernel(const MixOutArgs a) {
 // The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
 // the post-norm rows of the slot's tokens, DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each
 // pick's rows go to out [pick][rows].
+constexpr int kMoeFlush = 4;   // tiles whose partial sums an expert workgroup holds at once
+
 template <int KW, int NTT, int WMAX, bool UP>
 __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
                                                         size_t code_stride, size_t scale_stride, int64_t rows, int K,
@@ -894,7 +896,7 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
     if (t0 >= ntiles) return;
     const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
-    mfma_tiles<KW, NTT, kSplitK>(
+    mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
         codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
         K / kSuperK, 0, static_cast<int>(t1 - t0),
         cnt,
@@ -1274,10 +1276,13 @@ struct MoeArgs {
 template <int KW, int NTT, int WMAX, bool UP>
 int launch_moe_raw(const MoeArgs &a, int waves, hipStream_t st) {
     const int64_t ntiles = tiles_rows(a.rows);
-    // the slots' tiles over about as many workgroups as the chip holds at once
-    const int per = static_cast<int>(tiles_per_wg(ntiles * a.slots, waves, NTT));
+    // the slots' tiles over about four times as many workgroups as the chip holds at once (each workgroup loads its
+    // rows' activations once for all its tiles, so longer runs a workgroup read them fewer times)
+    const int64_t resident = 256 * std::max(1, 8 / waves);
+    const int per = static_cast<int>(
+        std::min<int64_t>(ntiles, std::max<int64_t>(kMoeFlush, (ntiles * a.slots + 4 * resident - 1) / (4 * resident))));
     const int tiles = static_cast<int>((ntiles + per - 1) / per);
-    const size_t lds = static_cast<size_t>(per) * waves * NTT * 1024;   // the waves' partial sums
+    const size_t lds = static_cast<size_t>(kMoeFlush) * waves * NTT * 1024;   // the waves' partial sums
     static int granted = 0;
     if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 76 * 1024, granted) != 0)
         return -1;
