@@ -176,6 +176,17 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
     };
     trace(GV_K_GDN_CORE, 0);
     load(base);
+    // the conv weights of the thread's channels (tid, tid + 256, ..: conv_w [ch][K]) and the rows' masks, loaded with
+    // the inputs below (one round trip for all; indices clamped, no branch around a load)
+    constexpr int kWch = 3;   // channel runs of 256 (nch = 2 dk + 16 <= 768: dk <= 256)
+    float wr[kWch][kMaxConvK];
+#pragma unroll
+    for (int c = 0; c < kWch; ++c) {
+        const float *src = a.conv_w + static_cast<int64_t>(gch(min(tid + c * kGdnThreads, nch - 1))) * K;
+#pragma unroll
+        for (int k = 0; k < kMaxConvK; ++k) wr[c][k] = src[min(k, K - 1)];
+    }
+    const uint32_t vis_r = sp->vis[min(tid, M - 1)];
     // 1. the raw inputs (rows 0 .. M - 1) and the base conv state (K - 1 rows of conv_dim) in 16-byte pieces: a thread
     // piece c4 of rows r, r + rstep, .. (pieces a row padded to a power of two, so no division), eight loads issued
     // before their LDS stores; then the conv weights, a thread a channel
@@ -200,15 +211,14 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
                 }
             }
         }
-        if (tid < M) vis[tid] = sp->vis[tid];
-        for (int lc = tid; lc < nch; lc += kGdnThreads) {   // conv_w [ch][K] to cw [k][lc]
-            const float *src = a.conv_w + static_cast<int64_t>(gch(lc)) * K;
-            float r[kMaxConvK];
+        if (tid < M) vis[tid] = vis_r;
 #pragma unroll
-            for (int k = 0; k < kMaxConvK; ++k) r[k] = src[min(k, K - 1)];
+        for (int c = 0; c < kWch; ++c) {   // conv_w [ch][K] to cw [k][lc]
+            const int lc = tid + c * kGdnThreads;
+            if (lc < nch)
 #pragma unroll
-            for (int k = 0; k < kMaxConvK; ++k)
-                if (k < K) cw[k * nch + lc] = r[k];
+                for (int k = 0; k < kMaxConvK; ++k)
+                    if (k < K) cw[k * nch + lc] = wr[c][k];
         }
     }
     __syncthreads();
@@ -234,19 +244,25 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
     // v channels as (row, column) pairs over every thread; each (row, channel) w . window in order, silu; the conv
     // state's slots written by one workgroup a channel (q and k: the key head's first value head's first workgroup)
     const bool qk_writer = vh % (a.nv / a.nk) == 0 && j0 == 0;
-    auto conv_one = [&](int t, int lc, bool writer) {
-        float *dst = a.c_slots + (wset + t) * a.c_slot_floats + gch(lc);
+    auto conv_one = [&](int t, int lc) {
         float acc = 0.0f;   // w . window (oldest first: the (K - 1 - k)-th newest before row t), then the input
         for (int k = 0; k < K1; ++k) {
             const int code = anc[t * (kMaxConvK - 1) + (K1 - 1 - k)];
             const float v = code >= 0 ? cv[code * nch + lc] : bs[(-1 - code) * nch + lc];
             acc = __fadd_rn(acc, __fmul_rn(cw[k * nch + lc], v));
-            if (writer && k > 0) dst[static_cast<int64_t>(k - 1) * a.conv_dim] = v;   // the state after the row
         }
-        const float in = cv[t * nch + lc];
-        acc = __fadd_rn(acc, __fmul_rn(cw[K1 * nch + lc], in));
-        if (writer) dst[static_cast<int64_t>(K1 - 1) * a.conv_dim] = in;
+        acc = __fadd_rn(acc, __fmul_rn(cw[K1 * nch + lc], cv[t * nch + lc]));
         co[t * nch + lc] = silu_fast(acc);
+    };
+    // the conv state after row t (its window's newest K - 1 entries, the row's own input last) to its slot: stored
+    // after the delta rule, so that no workgroup barrier before then waits for these stores to complete
+    auto conv_state_one = [&](int t, int lc) {
+        float *dst = a.c_slots + (wset + t) * a.c_slot_floats + gch(lc);
+        for (int k = 1; k < K1; ++k) {
+            const int code = anc[t * (kMaxConvK - 1) + (K1 - 1 - k)];
+            dst[static_cast<int64_t>(k - 1) * a.conv_dim] = code >= 0 ? cv[code * nch + lc] : bs[(-1 - code) * nch + lc];
+        }
+        dst[static_cast<int64_t>(K1 - 1) * a.conv_dim] = cv[t * nch + lc];
     };
     {
         const int qk = 2 * dk, lg = 31 - __clz(qk);   // (a power of two: 64 .. 512)
@@ -258,7 +274,7 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int t = t0 + u * t_step;
-                    if (t < M) conv_one(t, lc, qk_writer);
+                    if (t < M) conv_one(t, lc);
                 }
             }
         }
@@ -266,7 +282,7 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int p = p0 + u * kGdnThreads;
-                if (p < 16 * M) conv_one(p >> 4, qk + (p & 15), true);
+                if (p < 16 * M) conv_one(p >> 4, qk + (p & 15));
             }
         }
     }
@@ -341,6 +357,13 @@ __device__ void gdn_core_role(const GdnArgs &a, int w, float *lds) {
     trace(GV_K_GDN_CORE, 5);
     signal_done(a.flags + a.n_ab + w);
     trace(GV_K_GDN_CORE, 6);
+    // then the conv states (q and k channels: the key head's first workgroup; the 16 v channels: every workgroup),
+    // the (row, channel) pairs over the threads: no consumer in this launch waits for them
+    const int per_row = qk_writer ? 2 * dk + 16 : 16;
+    for (int p = tid; p < per_row * M; p += kGdnThreads) {
+        const int t = p / per_row, c = p % per_row;
+        conv_state_one(t, qk_writer ? c : 2 * dk + c);
+    }
 }
 
 // A norm workgroup, row t: once every core workgroup is done, the gated RMSNorm per value head (model.cpp:3670-3682):
