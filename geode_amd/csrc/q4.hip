@@ -278,6 +278,27 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     if (tc >= 0) trace(tc, 3);
 }
 
+// The skinny product over many row tiles a workgroup at 17..32 rows (two 16-column tiles: a K range's activations
+// take half the registers, so the kept-parts form above holds only 4 tiles' partial sums and each workgroup reloads
+// the rows' activations every 4 tiles): the waves' sums put every kGemvFlush tiles (mfma_tiles FLUSH), the same
+// sums in the same order as gemv_q4_kernel, so a workgroup takes ~19 tiles with one load of the activations.
+constexpr int kGemvFlush = 4;
+template <int KW, int WMAX>
+__global__ __launch_bounds__(64 * WMAX) void gemv_q4_flush_kernel(Q4 w, const _Float16 *__restrict__ act,
+                                                                  int64_t act_stride, int M, int sc0, int tiles_per_wg,
+                                                                  GemvOut out) {
+    extern __shared__ f4 part_lds[];
+    __shared__ uint2 tab[256];
+    const int64_t ntiles = tiles_rows(w.rows);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
+    if (t0 >= ntiles) return;
+    const int nt = static_cast<int>(std::min<int64_t>(tiles_per_wg, ntiles - t0));
+    mfma_tiles<KW, 2, kSplitK, 0, 3, false, kGemvFlush>(
+        w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, nt, M,
+        [&](int j) { return act + j * act_stride; }, [&](int64_t row, int j, float v) { out.put(row, j, v); },
+        part_lds, tab, TileRun{t0});
+}
+
 GV_ACT_MODE_SETTER(act_mode_set_q4)
 // ---------------------------------------------------------------- the dense SwiGLU FFN (C1) in three launches
 // x fp16 rows to the products' operands (the int8 path's quantization of the fp32 values, which fp16 converts to
@@ -422,6 +443,22 @@ static int launch_gemv(const Q4 &w, const _Float16 *act, int64_t act_stride, int
                        const GemvOut &out, hipStream_t st) {
     const int64_t ntiles = tiles_rows(w.rows);
     const int64_t per = tiles_per_wg(ntiles, waves, NTT);
+    if constexpr (NTT == 2 && !PACK) {
+        // a matrix whose tiles outnumber 4 a workgroup of the chip's resident ones (the head at a tree's 17 rows):
+        // the flushed form, ~2 workgroups a CU's worth of tiles each
+        const int64_t resident = 256 * std::max(1, 8 / waves);
+        if (ntiles > per * resident) {
+            const int64_t pf = std::max<int64_t>(kGemvFlush, (ntiles + 2 * resident - 1) / (2 * resident));
+            const int64_t wgf = (ntiles + pf - 1) / pf;
+            const size_t ldsf = static_cast<size_t>(kGemvFlush) * waves * NTT * 1024;
+            static int granted_f = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_flush_kernel<KW, WMAX>), 76 * 1024, granted_f) != 0)
+                return -1;
+            hipLaunchKernelGGL((gemv_q4_flush_kernel<KW, WMAX>), dim3(static_cast<unsigned>(wgf)), dim3(64 * waves), ldsf,
+                               st, w, act, act_stride, M, sc0, static_cast<int>(pf), out);
+            return 0;
+        }
+    }
     const int64_t wg = (ntiles + per - 1) / per;
     const size_t lds = static_cast<size_t>(per) * waves * NTT * 1024;   // the waves' partial sums
     static int granted = 0;
