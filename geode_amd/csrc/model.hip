@@ -1459,10 +1459,11 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids
 
 // The picks of expert blockIdx.x in (token, rank) order, by ordered compaction over ids [M][K]: their rows and,
 // per (row, rank), where the pick went; the shared expert (E) takes row t at start + t.
+constexpr int kFillBatch = 16;
 __global__ __launch_bounds__(256) void fill_picks_kernel(const int *__restrict__ ids, int M, int K, int E,
                                                          const int *__restrict__ start, int *__restrict__ pick_token,
                                                          int *__restrict__ pick_of) {
-    __shared__ int wt[4];
+    __shared__ int wt[kFillBatch][4];
     const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int s0 = start[e];
     if (e == E) {
@@ -1472,23 +1473,36 @@ __global__ __launch_bounds__(256) void fill_picks_kernel(const int *__restrict__
         }
         return;
     }
+    // kFillBatch chunks of 256 ids at a time: every id of the batch loaded at once, each chunk's matches counted per
+    // wave, one barrier, then each match placed after the earlier chunks' and waves' (the same order as one chunk at
+    // a time)
     int base = 0;
-    for (int c0 = 0; c0 < M * K; c0 += blockDim.x) {
-        const int i = c0 + tid;
-        const bool match = i < M * K && ids[i] == e;
-        const uint64_t b = __ballot(match);
-        const int rank = __popcll(b & ((1ull << lane) - 1ull));
-        if (lane == 0) wt[wave] = __popcll(b);
-        __syncthreads();
-        int wb = base;
-        for (int w2 = 0; w2 < wave; ++w2) wb += wt[w2];
-        if (match) {
-            const int p = s0 + wb + rank, t = i / K, k = i % K;
-            pick_token[p] = t;
-            pick_of[t * (K + 1) + k] = p;
+    for (int c0 = 0; c0 < M * K; c0 += kFillBatch * 256) {
+        int idv[kFillBatch];
+#pragma unroll
+        for (int u = 0; u < kFillBatch; ++u) idv[u] = ids[min(c0 + u * 256 + tid, M * K - 1)];
+        uint64_t bal[kFillBatch];
+#pragma unroll
+        for (int u = 0; u < kFillBatch; ++u) {
+            bal[u] = __ballot(c0 + u * 256 + tid < M * K && idv[u] == e);
+            if (lane == 0) wt[u][wave] = __popcll(bal[u]);
         }
-        base += wt[0] + wt[1] + wt[2] + wt[3];
         __syncthreads();
+        int run = base;
+#pragma unroll
+        for (int u = 0; u < kFillBatch; ++u) {
+            int wb = run;
+            for (int w2 = 0; w2 < wave; ++w2) wb += wt[u][w2];
+            if ((bal[u] >> lane) & 1ull) {
+                const int i = c0 + u * 256 + tid;
+                const int p = s0 + wb + __popcll(bal[u] & ((1ull << lane) - 1ull)), t = i / K, k = i % K;
+                pick_token[p] = t;
+                pick_of[t * (K + 1) + k] = p;
+            }
+            run += wt[u][0] + wt[u][1] + wt[u][2] + wt[u][3];
+        }
+        base = run;
+        __syncthreads();   // (wt is the next batch's)
     }
 }
 
