@@ -1070,7 +1070,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *__restri
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, int H, int K, const MixView mix,
                                                       int M, float *__restrict__ x, const float *__restrict__ norm_w,
                                                       float eps, _Float16 *__restrict__ act, int64_t act_stride,
-                                                      float *__restrict__ hout) {
+                                                      float *__restrict__ hout, int residual) {
     __shared__ double red[16];
     const int t = blockIdx.x;
     if (t >= M) return;
@@ -1110,7 +1110,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
             yb[u] = *reinterpret_cast<const float4 *>(yk + 4);
         }
         float *xr = x + static_cast<int64_t>(t) * H + gc * 8;
-        const float4 xa = *reinterpret_cast<const float4 *>(xr), xb = *reinterpret_cast<const float4 *>(xr + 4);
+        const float *xs = residual ? xr : zero + gc * 8;   // (no residual: the block's output alone, x + 0)
+        const float4 xa = *reinterpret_cast<const float4 *>(xs), xb = *reinterpret_cast<const float4 *>(xs + 4);
         __builtin_amdgcn_sched_barrier(0);
         float o[8];
         {
@@ -1150,10 +1151,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 }
 
 // (hout: the normalized rows in fp32 too, [M][H], or null)
+// (residual false: x is written, not read: the block's output without a residual)
 inline int combine_launch(const float *y, int H, int K, const MixView &mix, int M, float *x, const float *norm_w,
-                          float eps, _Float16 *act, int64_t act_stride, hipStream_t st, float *hout = nullptr) {
+                          float eps, _Float16 *act, int64_t act_stride, hipStream_t st, float *hout = nullptr,
+                          bool residual = true) {
     hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, y, H, K, mix, M, x, norm_w, eps, act, act_stride,
-                       hout);
+                       hout, residual ? 1 : 0);
     return 0;
 }
 
@@ -1386,17 +1389,48 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
 __global__ __launch_bounds__(256) void gate_rows_kernel(const uint16_t *__restrict__ wrow, int H,
                                                         const float *__restrict__ h, int M, float *__restrict__ logits,
                                                         int E1) {
-    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // LDS: the gate row as fp32 [H], then the waves' rows [4][H]. Every global load is issued before the first store
+    // to the LDS (the gate row 8 values a thread, the wave's row 4 values a lane, 2048 values a pass), then the eight
+    // fixed-order chains run from the LDS.
+    extern __shared__ float gr_lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = blockIdx.x * 4 + wave;
+    float *ws = gr_lds, *hs = gr_lds + H + wave * H;
+    const float *hr = h + static_cast<int64_t>(min(t, M - 1)) * H;
+    for (int p0 = 0; p0 < H; p0 += 2048) {
+        uint4 wv = make_uint4(0, 0, 0, 0);
+        const int iw = p0 + static_cast<int>(threadIdx.x) * 8;
+        if (iw < H) wv = *reinterpret_cast<const uint4 *>(wrow + iw);
+        float4 hv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int ih = min(p0 + u * 256 + lane * 4, H - 4);
+            hv[u] = *reinterpret_cast<const float4 *>(hr + ih);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (iw < H) {
+            const uint32_t wu[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                ws[iw + 2 * k] = __uint_as_float(wu[k] << 16);
+                ws[iw + 2 * k + 1] = __uint_as_float(wu[k] & 0xFFFF0000u);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int ih = p0 + u * 256 + lane * 4;
+            if (ih < H) *reinterpret_cast<float4 *>(hs + ih) = hv[u];
+        }
+    }
+    __syncthreads();
     if (t >= M) return;
-    const float *hr = h + static_cast<int64_t>(t) * H;
     float a = 0.0f;
     if (lane < 8)
-        for (int c0 = lane; c0 < H; c0 += 8 * 16) {
+        for (int c0 = lane; c0 < H; c0 += 8 * 16) {   // 16 steps' operands read ahead of their sums
             float hv[16], wv[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-                hv[u] = hr[c0 + 8 * u];
-                wv[u] = __uint_as_float(static_cast<uint32_t>(wrow[c0 + 8 * u]) << 16);
+                hv[u] = hs[c0 + 8 * u];
+                wv[u] = ws[c0 + 8 * u];
             }
 #pragma unroll
             for (int u = 0; u < 16; ++u) a = __fadd_rn(a, __fmul_rn(wv[u], hv[u]));
@@ -1739,7 +1773,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
                       : l + 1 == c.n_layers   ? m.hbuf
                                               : nullptr;
         combine_launch(m.y, H, c.top_k, route_mix(m.route + l, m.moe_dec), M, m.x, next_norm, c.eps, m.act_h, abH, st,
-                       hout);
+                       hout, !m.moe_only);
         return 0;
     }
     case GV_K_LM_HEAD:
@@ -1855,8 +1889,13 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     LayerW &L = m.layers[static_cast<size_t>(layer)];
     if (quantize_act(pf.h, H, M, H, nullptr, 0.0f, pf.act, act_halves(H), nullptr, 0, st) != 0) return -1;
     const int wg4 = (M + 3) / 4;
-    hipLaunchKernelGGL(gate_rows_kernel, dim3(wg4), dim3(256), 0, st, L.router + static_cast<int64_t>(E) * H, H, pf.h,
-                       M, pf.logits, m.E1);
+    {
+        const size_t lds = static_cast<size_t>(5) * H * 4;   // the gate row and the 4 waves' rows as fp32
+        static int granted = 0;
+        if (lds_grant(reinterpret_cast<const void *>(&gate_rows_kernel), lds, granted) != 0) return -1;
+        hipLaunchKernelGGL(gate_rows_kernel, dim3(wg4), dim3(256), lds, st, L.router + static_cast<int64_t>(E) * H, H,
+                           pf.h, M, pf.logits, m.E1);
+    }
     hipLaunchKernelGGL(route_rows_kernel, dim3(wg4), dim3(256), 0, st, pf.logits, E, K, M, pf.ids, pf.w, pf.gate);
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, pf.start, pf.n_slots,
                        pf.slot_expert, pf.slot_start, pf.slot_count, pf.n_picks);
@@ -1870,8 +1909,8 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     hipLaunchKernelGGL(swiglu_quant_kernel, dim3(picks), dim3(256), static_cast<size_t>(F) * 4, st, pf.gu, F,
                        pf.n_picks, pf.act_m);
     if (moe_run(m, L, false, 32, pf.act_m, pf.gu, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
-    GV_CHECK_HIP(hipMemsetAsync(pf.out, 0, static_cast<size_t>(M) * H * 4, st));
-    combine_launch(pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M, pf.out, nullptr, 0.0f, nullptr, 0, st);
+    combine_launch(pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M, pf.out, nullptr, 0.0f, nullptr, 0, st, nullptr,
+                   false);
     GV_CHECK_HIP(hipGetLastError());
     pf.M = M;
     return 0;
@@ -2650,7 +2689,6 @@ int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
                               static_cast<size_t>(E) * 4, M, hipMemcpyDeviceToDevice, st) == hipSuccess ? 0 : -1;
     for (int cls : {GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN})
         if (rc == 0) rc = launch_class(m, cls, layer, M, st);
-    if (rc == 0) rc = hipMemsetAsync(m.x, 0, static_cast<size_t>(M) * H * 4, st) == hipSuccess ? 0 : -1;
     if (rc == 0) rc = launch_class(m, GV_K_COMBINE, layer, M, st);   // the block's output, no residual
     m.moe_only = false;
     return rc;
