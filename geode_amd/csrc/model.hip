@@ -626,12 +626,15 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
                                                      float *__restrict__ logits, _Float16 *__restrict__ act,
                                                      int64_t act_stride, int route, int E, int K,
                                                      RouteState *__restrict__ rs, int32_t *__restrict__ ids_out,
-                                                     int *__restrict__ counter, int n_dg) {
+                                                     int *__restrict__ counter, int n_dg, int shared_dg) {
     // workgroup b: router rows 4 (b % n_dg) .., token group b / n_dg; it writes the experts' operands of row
-    // (b / n_dg) TG + b % n_dg (when b % n_dg < TG: every row's by one workgroup, n_dg >= min(M, TG))
+    // (b / n_dg) TG + b % n_dg (when b % n_dg < TG: every row's by one workgroup, n_dg >= min(M, TG)).
+    // shared_dg >= 0 (the routed logits given): the last row group of each token group is shared_dg instead, the one
+    // holding the shared expert's gate row; the others then only make the operands (and logits that are replaced)
     extern __shared__ float lds_f[];
     constexpr int TG = GPT == 1 ? 8 : 4;
-    const int dg = static_cast<int>(blockIdx.x) % n_dg, tg = static_cast<int>(blockIdx.x) / n_dg;
+    const int dg0 = static_cast<int>(blockIdx.x) % n_dg, tg = static_cast<int>(blockIdx.x) / n_dg;
+    const int dg = shared_dg >= 0 && dg0 == n_dg - 1 ? shared_dg : dg0;
     router_rows<GPT>(dg, tg, 0x7FFF, w, E1, H, x, norm_w, eps, sp, logits, false, act, dg < TG ? tg * TG + dg : -1,
                      act_stride, lds_f);
     if (!route) return;
@@ -1689,13 +1692,13 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.gdn_ab, E1, H, m.x,
                                L.in_norm, c.eps, m.sp, m.rlogits, nullptr, 0, 0, c.n_experts, c.top_k, m.route + l,
-                               nullptr, m.counter, n_dg);
+                               nullptr, m.counter, n_dg, -1);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.gdn_ab, E1, H, m.x,
                                L.in_norm, c.eps, m.sp, m.rlogits, nullptr, 0, 0, c.n_experts, c.top_k, m.route + l,
-                               nullptr, m.counter, n_dg);
+                               nullptr, m.counter, n_dg, -1);
         }
         GV_CHECK_HIP(hipGetLastError());
         return 0;
@@ -1726,7 +1729,10 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
     }
     case GV_K_ROUTER: {   // workgroups: (router row group, token group), each row's operands by one of them
         const int TG = router_tokens(H);
-        const int n_dg = std::max((m.E1 + kRouterRows - 1) / kRouterRows, std::min(M, TG));
+        // (the MoE block with its routed logits given: only the operands' row groups and the shared expert's)
+        const bool shared_only = m.moe_only && m.router_shared_only && (m.E1 - 1) / kRouterRows >= std::min(M, TG);
+        const int shared_dg = shared_only ? (m.E1 - 1) / kRouterRows : -1;
+        const int n_dg = shared_only ? std::min(M, TG) + 1 : std::max((m.E1 + kRouterRows - 1) / kRouterRows, std::min(M, TG));
         const int wgs = n_dg * ((M + TG - 1) / TG);
         if (H <= 2048) {
             static int granted = 0;
@@ -1734,14 +1740,16 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
             hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
                                m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
-                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg);
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg,
+                               shared_dg);
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
             hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
                                m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
-                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg);
+                               m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg,
+                               shared_dg);
         }
         return 0;
     }
@@ -2683,7 +2691,9 @@ int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
     Prefill &pf = m.pf;
     GV_CHECK_HIP(hipMemcpyAsync(m.x, pf.h, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToDevice, st));
     m.moe_only = true;
+    m.router_shared_only = given;
     int rc = launch_class(m, GV_K_ROUTER, layer, M, st);   // the shared expert's gate logit and the operands
+    m.router_shared_only = false;
     if (rc == 0 && given)                                  // the routed logits as given
         rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, pf.logits, static_cast<size_t>(m.E1) * 4,
                               static_cast<size_t>(E) * 4, M, hipMemcpyDeviceToDevice, st) == hipSuccess ? 0 : -1;

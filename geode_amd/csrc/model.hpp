@@ -132,6 +132,7 @@ struct Model {
     int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
     bool moe_dec = false;          // the decode MoE kernels (moe_up_kernel, moe_down_kernel), where the shapes fit
     bool fused = true;             // dependent phases chained within one launch where the shapes fit (gv_model_set_fused)
+    bool router_shared_only = false;   // the MoE block's router launch with the routed logits given (gv_model_moe)
     int *ctr = nullptr;            // [n_layers][kFlagsPerLayer] the fused launches' flags (each launch clears its own)
     int *err = nullptr;            // set by a fused launch whose wait ran out (read back by gv_verify)
     uint64_t *trace = nullptr;     // gv_model_trace's stamps [GV_K_COUNT][8192 workgroups][8] (allocated when on)
