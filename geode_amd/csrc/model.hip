@@ -2534,6 +2534,7 @@ int gv_model_randomize(gv_model *g, uint64_t seed, float sigma, float router_sig
     GV_CHECK_HIP(hipGetLastError());
     GV_REQUIRE(rc == 0, std::string("gv_model_randomize: ") + last_error());
     m.pos = ctx;
+    m.mtp_last_n = 0;
     return 0;
 }
 
@@ -2541,6 +2542,7 @@ int gv_model_set_position(gv_model *g, int pos) {
     GV_REQUIRE(g && pos >= 0 && pos + g->m.c.max_rows <= g->m.c.max_ctx, "gv_model_set_position: out of range");
     g->m.pos = pos;
     g->m.last_n = 0;
+    g->m.mtp_last_n = 0;   // a draft then starts from a new MTP pass, not the previous conversation's
     return 0;
 }
 
@@ -2673,7 +2675,7 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     m.timed_class = saved;
-    if (rc != 0) return -1;
+    if (rc != 0 || check_wait_flag(m, st) != 0) return -1;
     *ms_per_launch = ms / reps;
     return 0;
 }
@@ -2743,7 +2745,7 @@ int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *rou
     if (weights)
         GV_CHECK_HIP(hipMemcpyAsync(weights, big ? pf.w : m.route[layer].weight, static_cast<size_t>(M) * K * 4,
                                     hipMemcpyDeviceToHost, st));
-    GV_CHECK_HIP(hipStreamSynchronize(st));
+    if (check_wait_flag(m, st) != 0) return -1;   // (synchronizes the stream)
     m.last_n = 0;   // the step's state is this block's, not a verify's
     return 0;
 }
@@ -2821,7 +2823,7 @@ int gv_model_moe_replay(gv_model *g, int reps, float *ms_per_block) {
     GV_CHECK_HIP(hipEventElapsedTime(&ms, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    if (rc != 0) return -1;
+    if (rc != 0 || check_wait_flag(m, st) != 0) return -1;
     *ms_per_block = ms / reps;
     return 0;
 }

@@ -43,6 +43,7 @@ constexpr int kPass = 256;        // threads of a row-pass workgroup
 constexpr int kLoads = 16;        // values a thread holds in a pass
 constexpr int kChunk = kPass * kLoads;   // values a row-pass workgroup takes at most
 constexpr int kMaxChunks = 64;    // workgroups a row at most (a vocabulary up to 262,144)
+constexpr int kMaxVocab = kMaxChunks * kChunk;   // the entry points refuse a larger vocabulary before any work
 constexpr int kBins = 2048;       // bins of a histogram level (the last level uses 1024)
 constexpr int kSortThreads = 1024;
 constexpr int kMaxCand = 16384;   // top-K candidates a row can keep (the full-vocabulary nucleus has no limit)
@@ -1107,6 +1108,7 @@ extern "C" {
 
 int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float temperature, float top_p, int top_k,
                    int cap, const double *u, int32_t *out) {
+    GV_REQUIRE(V <= kMaxVocab, "gv_sample_rows: a vocabulary of at most 262,144 tokens");
     if (ensure_init() != 0) return -1;
     GV_REQUIRE(logits && out && rows >= 1 && rows <= kSampleRows && V >= 1 && ld >= V, "gv_sample_rows: bad arguments");
     GV_REQUIRE(temperature <= 0.0f || u, "gv_sample_rows: uniforms needed when temperature > 0");
@@ -1137,6 +1139,7 @@ int gv_accept_match(const float *logits, int64_t ld, int V, const int32_t *batch
 int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, int n, float temperature, float top_p,
                        int top_k, int cap, const double *u, const int32_t *seen, int n_seen, float presence_penalty,
                        const int32_t *stop, int n_stop, int32_t *out, int *kept) {
+    GV_REQUIRE(V <= kMaxVocab, "gv_accept_match: a vocabulary of at most 262,144 tokens");
     if (ensure_init() != 0) return -1;
     GV_REQUIRE(logits && batch && out && n >= 1 && n <= 32 && V >= 1 && ld >= V, "gv_accept_match: bad arguments");
     GV_REQUIRE(temperature <= 0.0f || u, "gv_accept_match: uniforms needed when temperature > 0");
@@ -1195,6 +1198,7 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
 
 int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int V, int k, float temperature,
                        float top_p, int greedy, const float *u_draft, const float *u_acc, float u_res, int32_t *out) {
+    GV_REQUIRE(V <= kMaxVocab, "gv_accept_textbook: a vocabulary of at most 262,144 tokens");
     if (ensure_init() != 0) return -1;
     GV_REQUIRE(target && draft && out && k >= 1 && k <= 31 && V >= 1 && ld >= V, "gv_accept_textbook: bad arguments");
     GV_REQUIRE(greedy || (u_draft && u_acc && temperature > 0.0f), "gv_accept_textbook: uniforms and T > 0 needed");

@@ -400,6 +400,7 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
     auto reset = [&] {
         m.pos = 0;
         m.last_n = 0;
+        m.mtp_last_n = 0;   // no MTP pass of the loaded conversation exists yet
         info->has_hidden = 0;
         return gdn_zero(m);
     };

@@ -36,3 +36,28 @@ def test_python_binding_covers_the_header():
 
     assert set(declared_functions()) <= set(geode_amd.SIGNATURES), \
         set(declared_functions()) - set(geode_amd.SIGNATURES)
+
+
+def test_sampler_refuses_a_vocabulary_past_its_chunk_table():
+    """the sampler's work buffers hold 64 chunks of 4096 values a row: every entry point refuses a larger vocabulary
+    before any device work (checked here without a GPU: the refusal comes before the library's init)"""
+    import ctypes
+
+    import geode_amd
+
+    lib = geode_amd.lib
+    V = 64 * 4096 + 1
+    logits = (ctypes.c_float * 4)()
+    out = (ctypes.c_int32 * 32)()
+    batch = (ctypes.c_int32 * 2)(0, 1)
+    kept = ctypes.c_int(0)
+    u = (ctypes.c_double * 2)(0.5, 0.5)
+    uf = (ctypes.c_float * 2)(0.5, 0.5)
+    rcs = {
+        "gv_sample_rows": lib.gv_sample_rows(logits, V, 1, V, 0.0, 1.0, 0, 0, u, out),
+        "gv_accept_match": lib.gv_accept_match(logits, V, V, batch, 2, 0.0, 1.0, 0, 0, u, out, ctypes.byref(kept)),
+        "gv_accept_textbook": lib.gv_accept_textbook(logits, logits, V, V, 1, 0.7, 0.95, 0, uf, uf, 0.5, out),
+    }
+    for name, rc in rcs.items():
+        assert rc == -1, name
+    assert "262,144" in lib.gv_last_error().decode()
