@@ -10,8 +10,9 @@
 // "tile8" layout (formats.q4.layout, kernels.hpp:49-56) has them turned back into rows here (the inverse of
 // to_tile8, kernels.cpp:971-991) before the device makes its own layout of them.
 //
-// Host code only: the JSON reader, the table and the file reads; the bytes go to the device through
-// gv_model_adopt.
+// Host code only: a JSON reader (RFC 8259, parsed into a flat tape), the staged manifest checks, the table and the
+// file reads; the bytes go to the device through gv_model_adopt. The architectures read are qwen35moe (the GPU
+// model's) and qwen35 (dense; its table is readable, the GPU model refuses it).
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -32,212 +33,282 @@
 namespace gv {
 namespace {
 
-// ---------------------------------------------------------------- JSON (the manifest's subset: all of RFC 8259)
-struct Json {
-    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
-    bool b = false;
-    double num = 0.0;
-    std::string s;
-    std::vector<Json> a;
-    std::map<std::string, Json> o;
-
-    const Json &operator[](const std::string &key) const {
-        static const Json none;
-        if (kind != Obj) return none;
-        const auto it = o.find(key);
-        return it == o.end() ? none : it->second;
-    }
-    const Json &at(size_t i) const {
-        static const Json none;
-        return kind == Arr && i < a.size() ? a[i] : none;
-    }
-    size_t size() const { return kind == Arr ? a.size() : kind == Obj ? o.size() : 0; }
-    std::string str(const std::string &fallback = "") const { return kind == Str ? s : fallback; }
-    int64_t i64(int64_t fallback = 0) const { return kind == Num ? static_cast<int64_t>(num) : fallback; }
-    double f64(double fallback = 0.0) const { return kind == Num ? num : fallback; }
-};
-
-class JsonReader {
+// ---------------------------------------------------------------- JSON (RFC 8259), read into a flat tape
+// The document is parsed once, without recursion, into `nodes` in document order: a scalar is one node; an array or
+// an object is a node whose `skip` is the index one past its last descendant, so its children are reached by jumping
+// from one child to the next child's index. An object's children come in pairs, a key (a string node) then its value.
+// Strings are decoded (escapes, UTF-16 surrogate pairs to UTF-8) into one byte arena; numbers follow the RFC's
+// grammar exactly and are converted with strtod. Lookups walk a container's children (manifests are small).
+class JsonTape {
 public:
-    JsonReader(const char *p, size_t n) : p_(p), begin_(p), end_(p + n) {}
-    bool read(Json &out, std::string &err) {
-        if (!value(out, 0) || (skip(), p_ != end_)) {
-            if (err_.empty()) err_ = "trailing characters";
-            err = err_ + " at byte " + std::to_string(p_ - begin_);
-            return false;
+    enum Kind : uint8_t { kNull, kTrue, kFalse, kNumber, kString, kArray, kObject };
+    struct Node {
+        Kind kind;
+        uint32_t skip;     // containers: one past the last descendant; scalars: own index + 1
+        uint32_t off, len; // strings: the decoded bytes in the arena
+        double number;
+    };
+
+    // a position in the tape; an absent member or element is the null view (kind() == kNull, valid() false)
+    class View {
+    public:
+        View() = default;
+        View(const JsonTape *t, uint32_t i) : t_(t), i_(i) {}
+        bool valid() const { return t_ != nullptr; }
+        Kind kind() const { return t_ ? t_->nodes_[i_].kind : kNull; }
+        bool is(Kind k) const { return kind() == k; }
+        // members and elements
+        View member(const char *key) const {
+            if (!is(kObject)) return {};
+            const size_t kl = std::strlen(key);
+            for (uint32_t c = i_ + 1; c < node().skip; c = t_->nodes_[c + 1].skip)
+                if (t_->nodes_[c].len == kl && std::memcmp(t_->arena_.data() + t_->nodes_[c].off, key, kl) == 0)
+                    return View(t_, c + 1);
+            return {};
         }
+        View operator[](const char *key) const { return member(key); }
+        size_t count() const {
+            if (!is(kArray) && !is(kObject)) return 0;
+            size_t n = 0;
+            for (uint32_t c = i_ + 1; c < node().skip; c = t_->nodes_[c].skip) ++n;
+            return is(kObject) ? n / 2 : n;
+        }
+        View element(size_t k) const {
+            if (!is(kArray)) return {};
+            uint32_t c = i_ + 1;
+            for (size_t j = 0; j < k && c < node().skip; ++j) c = t_->nodes_[c].skip;
+            return c < node().skip ? View(t_, c) : View();
+        }
+        template <typename F> void each_member(F &&f) const {   // f(key, value)
+            if (!is(kObject)) return;
+            for (uint32_t c = i_ + 1; c < node().skip; c = t_->nodes_[c + 1].skip)
+                f(std::string(t_->arena_.data() + t_->nodes_[c].off, t_->nodes_[c].len), View(t_, c + 1));
+        }
+        // scalars
+        std::string text(const char *fallback = "") const {
+            return is(kString) ? std::string(t_->arena_.data() + node().off, node().len) : std::string(fallback);
+        }
+        double number(double fallback) const { return is(kNumber) ? node().number : fallback; }
+        // an integral number in [lo, hi] (false: absent, not a number, fractional or out of range)
+        bool integer(int64_t lo, int64_t hi, int64_t &out) const {
+            if (!is(kNumber)) return false;
+            const double v = node().number;
+            if (!(v >= static_cast<double>(lo) && v <= static_cast<double>(hi)) || v != std::floor(v)) return false;
+            out = static_cast<int64_t>(v);
+            return true;
+        }
+        bool flag() const { return is(kTrue); }
+
+    private:
+        const Node &node() const { return t_->nodes_[i_]; }
+        const JsonTape *t_ = nullptr;
+        uint32_t i_ = 0;
+    };
+
+    View root() const { return nodes_.empty() ? View() : View(this, 0); }
+
+    // false with a message naming the byte offset and what was wrong
+    bool parse(const char *text, size_t n, std::string &err) {
+        nodes_.clear();
+        arena_.clear();
+        s_ = text;
+        e_ = text + n;
+        p_ = text;
+        std::vector<uint32_t> open;   // indices of the containers not yet closed
+        bool want_value = true;       // a value may (must) come next
+        for (;;) {
+            blanks();
+            if (want_value) {
+                if (p_ == e_) return bad("the text ends where a value is expected", err);
+                const char c = *p_;
+                if (c == ']' && !open.empty() && nodes_[open.back()].kind == kArray &&
+                    nodes_.size() == open.back() + size_t{1}) {   // an empty array (no element pushed yet)
+                    ++p_;
+                    close(open);
+                    want_value = false;
+                } else if (c == '[' || c == '{') {
+                    ++p_;
+                    open.push_back(push(c == '[' ? kArray : kObject));
+                    blanks();
+                    if (c == '{') {
+                        if (p_ < e_ && *p_ == '}') {
+                            ++p_;
+                            close(open);
+                            want_value = false;
+                        } else if (!key(err)) {
+                            return false;
+                        }
+                    }
+                    // an array: its first value (or ']') comes next; want_value stays true
+                } else {
+                    if (!scalar(err)) return false;
+                    want_value = false;
+                }
+                if (!want_value && open.empty()) break;
+                continue;
+            }
+            // after a value: a separator or the end of the enclosing container
+            if (p_ == e_) return bad("the text ends inside an array or object", err);
+            const Kind in = nodes_[open.back()].kind;
+            const char c = *p_++;
+            if (c == ',') {
+                blanks();
+                if (in == kObject && !key(err)) return false;
+                want_value = true;
+            } else if ((c == ']' && in == kArray) || (c == '}' && in == kObject)) {
+                close(open);
+                if (open.empty()) break;
+            } else {
+                --p_;
+                return bad(in == kArray ? "',' or ']' expected after an array element"
+                                        : "',' or '}' expected after an object member", err);
+            }
+        }
+        blanks();
+        if (p_ != e_) return bad("more text after the document's value", err);
         return true;
     }
 
 private:
-    const char *p_, *begin_, *end_;
-    std::string err_;
-
-    bool fail(const char *what) {
-        if (err_.empty()) err_ = what;
+    uint32_t push(Kind k) {
+        const uint32_t i = static_cast<uint32_t>(nodes_.size());
+        nodes_.push_back(Node{k, i + 1, 0, 0, 0.0});
+        return i;
+    }
+    void close(std::vector<uint32_t> &open) {
+        nodes_[open.back()].skip = static_cast<uint32_t>(nodes_.size());
+        open.pop_back();
+    }
+    void blanks() {
+        while (p_ < e_ && (*p_ == ' ' || *p_ == '\n' || *p_ == '\r' || *p_ == '\t')) ++p_;
+    }
+    bool bad(const char *what, std::string &err) {
+        err = std::string(what) + " (byte " + std::to_string(p_ - s_) + ")";
         return false;
     }
-    void skip() {
-        while (p_ < end_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) ++p_;
-    }
-    bool literal(const char *w) {
-        const size_t n = std::strlen(w);
-        if (static_cast<size_t>(end_ - p_) < n || std::memcmp(p_, w, n) != 0) return fail("unexpected characters");
-        p_ += n;
-        return true;
-    }
-    static void utf8(uint32_t cp, std::string &out) {
-        if (cp < 0x80) {
-            out += static_cast<char>(cp);
-        } else if (cp < 0x800) {
-            out += static_cast<char>(0xC0 | (cp >> 6));
-            out += static_cast<char>(0x80 | (cp & 0x3F));
-        } else if (cp < 0x10000) {
-            out += static_cast<char>(0xE0 | (cp >> 12));
-            out += static_cast<char>(0x80 | ((cp >> 6) & 0x3F));
-            out += static_cast<char>(0x80 | (cp & 0x3F));
-        } else {
-            out += static_cast<char>(0xF0 | (cp >> 18));
-            out += static_cast<char>(0x80 | ((cp >> 12) & 0x3F));
-            out += static_cast<char>(0x80 | ((cp >> 6) & 0x3F));
-            out += static_cast<char>(0x80 | (cp & 0x3F));
-        }
-    }
-    bool hex4(uint32_t &v) {
-        if (end_ - p_ < 4) return fail("a short \\u escape");
-        v = 0;
-        for (int i = 0; i < 4; ++i) {
-            const char c = *p_++;
-            v <<= 4;
-            if (c >= '0' && c <= '9') v |= static_cast<uint32_t>(c - '0');
-            else if (c >= 'a' && c <= 'f') v |= static_cast<uint32_t>(c - 'a' + 10);
-            else if (c >= 'A' && c <= 'F') v |= static_cast<uint32_t>(c - 'A' + 10);
-            else return fail("a bad \\u escape");
-        }
-        return true;
-    }
-    bool string(std::string &out) {
-        ++p_;   // the opening quote
-        while (p_ < end_ && *p_ != '"') {
-            const unsigned char c = static_cast<unsigned char>(*p_);
-            if (c < 0x20) return fail("a control character in a string");
-            if (c != '\\') {
-                out += *p_++;
-                continue;
-            }
-            if (++p_ == end_) break;
-            const char e = *p_++;
-            switch (e) {
-            case '"': out += '"'; break;
-            case '\\': out += '\\'; break;
-            case '/': out += '/'; break;
-            case 'b': out += '\b'; break;
-            case 'f': out += '\f'; break;
-            case 'n': out += '\n'; break;
-            case 'r': out += '\r'; break;
-            case 't': out += '\t'; break;
-            case 'u': {
-                uint32_t cp;
-                if (!hex4(cp)) return false;
-                if (cp >= 0xD800 && cp < 0xDC00 && end_ - p_ >= 6 && p_[0] == '\\' && p_[1] == 'u') {
-                    const char *save = p_;
-                    p_ += 2;
-                    uint32_t lo;
-                    if (!hex4(lo)) return false;
-                    if (lo >= 0xDC00 && lo < 0xE000) cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
-                    else p_ = save;
-                }
-                utf8(cp, out);
-                break;
-            }
-            default: return fail("a bad escape");
-            }
-        }
-        if (p_ == end_) return fail("an unterminated string");
+    // an object member's key and the ':' after it
+    bool key(std::string &err) {
+        if (p_ == e_ || *p_ != '"') return bad("an object member must start with a quoted key", err);
+        if (!string_node(err)) return false;
+        blanks();
+        if (p_ == e_ || *p_ != ':') return bad("':' expected after an object key", err);
         ++p_;
         return true;
     }
-    bool number(double &out) {
-        const char *s = p_;
-        if (p_ < end_ && *p_ == '-') ++p_;
-        if (p_ == end_ || !((*p_ >= '0' && *p_ <= '9'))) return fail("a bad number");
-        while (p_ < end_ && ((*p_ >= '0' && *p_ <= '9') || *p_ == '.' || *p_ == 'e' || *p_ == 'E' || *p_ == '+' ||
-                             *p_ == '-'))
+    bool scalar(std::string &err) {
+        const char c = *p_;
+        if (c == '"') return string_node(err);
+        if (c == '-' || (c >= '0' && c <= '9')) return number_node(err);
+        static const struct { const char *word; Kind kind; } words[] = {{"null", kNull}, {"true", kTrue}, {"false", kFalse}};
+        for (const auto &w : words) {
+            const size_t wl = std::strlen(w.word);
+            if (static_cast<size_t>(e_ - p_) >= wl && std::memcmp(p_, w.word, wl) == 0) {
+                p_ += wl;
+                push(w.kind);
+                return true;
+            }
+        }
+        return bad("a value is expected (object, array, string, number, true, false or null)", err);
+    }
+    // RFC 8259 section 6: -? (0 | [1-9][0-9]*) (. [0-9]+)? ([eE] [+-]? [0-9]+)?
+    bool number_node(std::string &err) {
+        const char *b = p_;
+        auto digits = [&] {
+            const char *d = p_;
+            while (p_ < e_ && *p_ >= '0' && *p_ <= '9') ++p_;
+            return p_ > d;
+        };
+        if (*p_ == '-') ++p_;
+        if (p_ < e_ && *p_ == '0') ++p_;
+        else if (!digits()) return bad("a number needs a digit after its sign", err);
+        if (p_ < e_ && *p_ == '.') {
             ++p_;
-        const std::string text(s, p_);
-        char *stop = nullptr;
-        out = std::strtod(text.c_str(), &stop);
-        if (!stop || *stop != '\0') return fail("a bad number");
+            if (!digits()) return bad("a number needs digits after its decimal point", err);
+        }
+        if (p_ < e_ && (*p_ == 'e' || *p_ == 'E')) {
+            ++p_;
+            if (p_ < e_ && (*p_ == '+' || *p_ == '-')) ++p_;
+            if (!digits()) return bad("a number needs digits in its exponent", err);
+        }
+        char buf[64];
+        const size_t n = static_cast<size_t>(p_ - b);
+        if (n >= sizeof buf) return bad("a number longer than 63 characters", err);
+        std::memcpy(buf, b, n);
+        buf[n] = '\0';
+        const uint32_t i = push(kNumber);
+        nodes_[i].number = std::strtod(buf, nullptr);
         return true;
     }
-    bool value(Json &v, int depth) {
-        if (depth > 64) return fail("nested too deeply");
-        skip();
-        if (p_ == end_) return fail("unexpected end");
-        switch (*p_) {
-        case '{': {
-            ++p_;
-            v.kind = Json::Obj;
-            skip();
-            if (p_ < end_ && *p_ == '}') {
-                ++p_;
-                return true;
-            }
-            while (true) {
-                skip();
-                if (p_ == end_ || *p_ != '"') return fail("a key expected");
-                std::string key;
-                if (!string(key)) return false;
-                skip();
-                if (p_ == end_ || *p_ != ':') return fail("':' expected");
-                ++p_;
-                Json item;
-                if (!value(item, depth + 1)) return false;
-                v.o[key] = std::move(item);
-                skip();
-                if (p_ < end_ && *p_ == ',') {
-                    ++p_;
-                    continue;
-                }
-                if (p_ < end_ && *p_ == '}') {
-                    ++p_;
-                    return true;
-                }
-                return fail("',' or '}' expected");
-            }
-        }
-        case '[': {
-            ++p_;
-            v.kind = Json::Arr;
-            skip();
-            if (p_ < end_ && *p_ == ']') {
-                ++p_;
-                return true;
-            }
-            while (true) {
-                Json item;
-                if (!value(item, depth + 1)) return false;
-                v.a.push_back(std::move(item));
-                skip();
-                if (p_ < end_ && *p_ == ',') {
-                    ++p_;
-                    continue;
-                }
-                if (p_ < end_ && *p_ == ']') {
-                    ++p_;
-                    return true;
-                }
-                return fail("',' or ']' expected");
-            }
-        }
-        case '"': v.kind = Json::Str; return string(v.s);
-        case 't': v.kind = Json::Bool, v.b = true; return literal("true");
-        case 'f': v.kind = Json::Bool, v.b = false; return literal("false");
-        case 'n': v.kind = Json::Null; return literal("null");
-        default: v.kind = Json::Num; return number(v.num);
-        }
+    static int hexval(char c) {
+        return c >= '0' && c <= '9' ? c - '0' : c >= 'a' && c <= 'f' ? c - 'a' + 10 : c >= 'A' && c <= 'F' ? c - 'A' + 10 : -1;
     }
+    bool unit16(uint32_t &u) {   // the four hex digits of a \u escape, p_ past the 'u'
+        if (e_ - p_ < 4) return false;
+        u = 0;
+        for (int k = 0; k < 4; ++k) {
+            const int h = hexval(p_[k]);
+            if (h < 0) return false;
+            u = u * 16 + static_cast<uint32_t>(h);
+        }
+        p_ += 4;
+        return true;
+    }
+    void put_code_point(uint32_t cp) {   // UTF-8: 1 to 4 bytes
+        char b[4];
+        int n;
+        if (cp < 0x80) {
+            b[0] = static_cast<char>(cp);
+            n = 1;
+        } else {
+            n = cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
+            for (int k = n - 1; k > 0; --k, cp >>= 6) b[k] = static_cast<char>(0x80 | (cp & 0x3F));
+            static const uint8_t lead[5] = {0, 0, 0xC0, 0xE0, 0xF0};
+            b[0] = static_cast<char>(lead[n] | cp);
+        }
+        arena_.append(b, static_cast<size_t>(n));
+    }
+    bool string_node(std::string &err) {
+        ++p_;   // the opening quote
+        const uint32_t i = push(kString);
+        nodes_[i].off = static_cast<uint32_t>(arena_.size());
+        for (;;) {
+            const char *run = p_;   // a run of plain bytes copied at once
+            while (p_ < e_ && *p_ != '"' && *p_ != '\\' && static_cast<unsigned char>(*p_) >= 0x20) ++p_;
+            arena_.append(run, static_cast<size_t>(p_ - run));
+            if (p_ == e_) return bad("a string is not closed", err);
+            if (*p_ == '"') break;
+            if (*p_ != '\\') return bad("a control byte inside a string must be escaped", err);
+            if (++p_ == e_) return bad("a string ends inside an escape", err);
+            const char esc = *p_++;
+            const char *plain = std::strchr("\"\\/bfnrt", esc);
+            if (esc != '\0' && plain) {
+                static const char decoded[] = "\"\\/\b\f\n\r\t";
+                arena_.push_back(decoded[plain - "\"\\/bfnrt"]);
+                continue;
+            }
+            if (esc != 'u') return bad("an unknown escape in a string", err);
+            uint32_t u;
+            if (!unit16(u)) return bad("\\u needs four hex digits", err);
+            if (u >= 0xDC00 && u <= 0xDFFF) return bad("a low surrogate without its high surrogate", err);
+            if (u >= 0xD800 && u <= 0xDBFF) {   // a pair: the low surrogate must follow as \uDC00..\uDFFF
+                uint32_t lo;
+                if (e_ - p_ < 2 || p_[0] != '\\' || p_[1] != 'u') return bad("a high surrogate without its pair", err);
+                p_ += 2;
+                if (!unit16(lo) || lo < 0xDC00 || lo > 0xDFFF) return bad("a high surrogate without its pair", err);
+                u = 0x10000 + ((u - 0xD800) << 10) + (lo - 0xDC00);
+            }
+            put_code_point(u);
+        }
+        ++p_;   // the closing quote
+        nodes_[i].len = static_cast<uint32_t>(arena_.size()) - nodes_[i].off;
+        return true;
+    }
+
+    std::vector<Node> nodes_;
+    std::string arena_;
+    const char *s_ = nullptr, *e_ = nullptr, *p_ = nullptr;
 };
+using JView = JsonTape::View;
 
 // ---------------------------------------------------------------- the table (kernels.cpp:858-902)
 enum Type { T_F32 = 0, T_BF16 = 1, T_Q2 = 2, T_Q3 = 3, T_NVFP4 = 4, T_Q8 = 5, T_Q4 = 6, T_UNKNOWN = 7, T_Q4I = 8 };
@@ -325,7 +396,7 @@ using namespace gv;
 
 struct gv_pack {
     std::string dir;
-    Json m;
+    JsonTape doc;        // geode.json
     uint64_t print = 1;
     std::string arch;
     // the geometry (pack.cpp:90-160)
@@ -354,172 +425,262 @@ struct gv_pack {
 namespace gv {
 namespace {
 
-int geti(const Json &v, const char *key, int fallback = 0) { return static_cast<int>(v[key].i64(fallback)); }
+// Opening a pack: the manifest is read into gv_pack in stages, each checking what the later stages and the loads rely
+// on, and a refusal names the entry at fault. What is checked follows Pack::open (pack.cpp:39-308) — the format and
+// version, the architecture, every listed file present at its listed size (an optional one may be absent: its tensors
+// are then skipped), the geometry, each tensor's type, shape and byte extent inside its file, dense.bin in use, the
+// embedding, the expert table covering every layer with its scales, q3's bit order — but dense.bin is not read into
+// memory: the tensors are read from their files when a model adopts them. Integers in the manifest must be integral
+// JSON numbers in range; a tensor's dimensions are at most 2^32 and its element count at most 2^48 (byte counts stay
+// far inside 64 bits).
+class PackOpener {
+public:
+    PackOpener(gv_pack &P, std::string &err) : P_(P), err_(err) {}
 
-// Pack::open (pack.cpp:39-308) without reading dense.bin into memory: the tensors are read from their files when
-// adopted
-bool open_pack(gv_pack &P, const std::string &dir, std::string &err) {
-    P.dir = dir;
-    const std::string mpath = dir + "/geode.json";
-    std::string text;
-    {
-        std::FILE *f = std::fopen(mpath.c_str(), "rb");
-        if (!f) return err = "no geode.json in " + dir, false;
-        char buf[1 << 16];
-        size_t n;
-        while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, n);
-        std::fclose(f);
+    bool run(const std::string &dir) {
+        P_.dir = dir;
+        return read_manifest() && check_format() && check_files() && read_geometry() && read_tensors() &&
+               read_expert_table() && read_formats();
     }
-    const uint64_t h = fnv(text.data(), text.size());   // Model::fingerprint's pack print (state.cpp:227-238)
-    P.print = h ? h : 1;
-    std::string perr;
-    if (!JsonReader(text.data(), text.size()).read(P.m, perr)) return err = "geode.json: " + perr, false;
-    const Json &m = P.m;
-    if (m["format"].str() != "geode-pack" || m["version"].i64() != 1)
-        return err = "not a geode-pack v1 (format '" + m["format"].str() + "')", false;
-    P.arch = m["arch"].str();
-    const bool gemma = P.arch == "gemma4";
-    if (P.arch != "qwen35moe" && P.arch != "qwen35" && !gemma) return err = "unknown architecture '" + P.arch + "'", false;
 
-    // the files: present at their sizes; an optional one may be missing, its tensors then absent
-    const Json &files = m["files"];
-    std::vector<std::string> missing;
-    for (size_t i = 0; i < files.size(); ++i) {
-        const Json &f = files.at(i);
-        const std::string name = f["name"].str();
+private:
+    static constexpr int64_t kMaxDim = int64_t{1} << 32;
+    static constexpr int64_t kMaxElements = int64_t{1} << 48;
+
+    bool refuse(const std::string &why) {
+        err_ = why;
+        return false;
+    }
+    static std::string number_text(double v) {
+        char b[32];
+        std::snprintf(b, sizeof b, "%g", v);
+        return b;
+    }
+    JView manifest() const { return P_.doc.root(); }
+
+    bool read_manifest() {
+        const std::string path = P_.dir + "/geode.json";
         uint64_t size = 0;
-        const bool there = file_size(dir + "/" + name, size);
-        if (f["optional"].kind == Json::Bool && f["optional"].b && !there) {
-            missing.push_back(name);
-            continue;
-        }
-        if (!there) return err = "cannot open " + dir + "/" + name, false;
-        if (static_cast<int64_t>(size) != f["size"].i64())
-            return err = name + ": " + std::to_string(size) + " bytes, expected " + std::to_string(f["size"].i64()), false;
-        P.files.push_back(name);
-        P.sizes.push_back(size);
+        ReadFile f;
+        if (!file_size(path, size) || !f.open(path)) return refuse("cannot read " + path);
+        std::string text(static_cast<size_t>(size), '\0');
+        if (size && !f.read(0, text.data(), text.size())) return refuse("cannot read " + path);
+        const uint64_t h = fnv(text.data(), text.size());   // the pack print a state file carries (state.cpp:227-238)
+        P_.print = h ? h : 1;
+        std::string why;
+        if (!P_.doc.parse(text.data(), text.size(), why)) return refuse("geode.json is not valid JSON: " + why);
+        if (!manifest().is(JsonTape::kObject)) return refuse("geode.json must hold a JSON object");
+        return true;
     }
 
-    // the geometry
-    const Json &c = m["config"];
-    P.hidden = geti(c, "hidden_size");
-    P.n_layers = geti(c, "num_hidden_layers");
-    P.vocab = geti(c, "vocab_size");
-    P.eps = static_cast<float>(c["rms_norm_eps"].f64(1e-6));
-    P.n_heads = geti(c, "num_attention_heads");
-    P.n_kv_heads = geti(c, "num_key_value_heads");
-    P.head_dim = geti(c, "head_dim");
-    const Json &rope = c["rope_parameters"];
-    P.rope_theta = static_cast<float>(rope["rope_theta"].f64(10000.0));
-    P.rope_dim = static_cast<int>(P.head_dim * rope["partial_rotary_factor"].f64(1.0));
-    P.gdn_k_heads = geti(c, "linear_num_key_heads");
-    P.gdn_v_heads = geti(c, "linear_num_value_heads");
-    P.gdn_k_dim = geti(c, "linear_key_head_dim");
-    P.gdn_v_dim = geti(c, "linear_value_head_dim");
-    P.conv_kernel = geti(c, "linear_conv_kernel_dim");
-    P.dense = P.arch == "qwen35" || gemma;
-    P.n_experts = gemma ? 0 : geti(c, "num_experts");
-    P.top_k = gemma ? 0 : geti(c, "num_experts_per_tok");
-    P.moe_ff = gemma ? 0 : geti(c, "moe_intermediate_size");
-    P.shared_ff = geti(c, P.arch == "qwen35" ? "intermediate_size" : "shared_expert_intermediate_size");
-    const Json &types = c["layer_types"];
-    if (P.n_layers <= 0 || P.n_layers > 1024 || static_cast<int>(types.size()) != P.n_layers)
-        return err = "geode.json: layer_types does not match num_hidden_layers", false;
-    for (int l = 0; l < P.n_layers; ++l) P.attention.push_back(types.at(static_cast<size_t>(l)).str() == "full_attention");
-    const bool moe_ok = P.dense ? P.n_experts == 0 && (gemma || (P.shared_ff > 0 && P.shared_ff % 16 == 0))
-                                : P.top_k > 0 && P.top_k <= P.n_experts;
-    if (P.hidden <= 0 || P.hidden % 16 || !moe_ok || P.gdn_v_heads % std::max(1, P.gdn_k_heads) ||
-        P.n_heads % std::max(1, P.n_kv_heads) || P.rope_dim % 2)
-        return err = "geode.json: inconsistent model geometry", false;
+    bool check_format() {
+        const JView m = manifest();
+        int64_t version = 0;
+        if (m["format"].text() != "geode-pack" || !m["version"].integer(1, 1, version))
+            return refuse("geode.json describes format '" + m["format"].text("(none)") + "' version " +
+                          (m["version"].is(JsonTape::kNumber) ? number_text(m["version"].number(0)) : "(none)") +
+                          "; this reader takes geode-pack version 1");
+        P_.arch = m["arch"].text();
+        if (P_.arch != "qwen35moe" && P_.arch != "qwen35")
+            return refuse("architecture '" + P_.arch + "' is not one this library loads (qwen35moe, qwen35)");
+        P_.dense = P_.arch == "qwen35";
+        return true;
+    }
 
-    // the tensor table: every shape and extent checked before anything is read
-    const Json &tensors = m["tensors"];
-    if (tensors.kind != Json::Obj) return err = "geode.json: no tensor table", false;
-    bool any_dense = false;
-    for (const auto &[name, t] : tensors.o) {
-        if (std::find(missing.begin(), missing.end(), t["file"].str()) != missing.end()) continue;
-        Tensor x;
-        x.type = type_of(t["type"].str());
-        if (x.type == T_UNKNOWN) return err = name + ": unknown type '" + t["type"].str() + "'", false;
-        bool shape_ok = true;
-        for (size_t i = 0; i < t["shape"].size(); ++i) {
-            const int64_t d = t["shape"].at(i).i64();
-            shape_ok &= d > 0 && d < (int64_t{1} << 31);
+    bool check_files() {
+        const JView list = manifest()["files"];
+        for (size_t k = 0; k < list.count(); ++k) {
+            const JView entry = list.element(k);
+            const std::string name = entry["name"].text();
+            int64_t listed = 0;
+            if (name.empty() || !entry["size"].integer(0, INT64_MAX, listed))
+                return refuse("geode.json files[" + std::to_string(k) + "] needs a name and a byte size");
+            uint64_t have = 0;
+            if (!file_size(P_.dir + "/" + name, have)) {
+                if (entry["optional"].flag()) {
+                    absent_.push_back(name);
+                    continue;
+                }
+                return refuse(name + " is listed in geode.json but missing from " + P_.dir);
+            }
+            if (have != static_cast<uint64_t>(listed))
+                return refuse(name + " holds " + std::to_string(have) + " bytes; geode.json lists " + std::to_string(listed));
+            P_.files.push_back(name);
+            P_.sizes.push_back(have);
+        }
+        return true;
+    }
+
+    // an optional integer of the config (absent: 0), refused when present but not an integer in [0, 2^31)
+    bool config_int(const char *key, int &out) {
+        const JView v = manifest()["config"][key];
+        int64_t x = 0;
+        if (v.valid() && !v.integer(0, INT32_MAX, x)) return refuse(std::string("config.") + key + " is not a count");
+        out = static_cast<int>(x);
+        return true;
+    }
+
+    bool read_geometry() {
+        const JView c = manifest()["config"];
+        gv_pack &P = P_;
+        const char *ff_key = P.dense ? "intermediate_size" : "shared_expert_intermediate_size";
+        const std::pair<const char *, int *> ints[] = {
+            {"hidden_size", &P.hidden}, {"num_hidden_layers", &P.n_layers}, {"vocab_size", &P.vocab},
+            {"num_attention_heads", &P.n_heads}, {"num_key_value_heads", &P.n_kv_heads}, {"head_dim", &P.head_dim},
+            {"linear_num_key_heads", &P.gdn_k_heads}, {"linear_num_value_heads", &P.gdn_v_heads},
+            {"linear_key_head_dim", &P.gdn_k_dim}, {"linear_value_head_dim", &P.gdn_v_dim},
+            {"linear_conv_kernel_dim", &P.conv_kernel}, {"num_experts", &P.n_experts},
+            {"num_experts_per_tok", &P.top_k}, {"moe_intermediate_size", &P.moe_ff}, {ff_key, &P.shared_ff}};
+        for (const auto &[key, dst] : ints)
+            if (!config_int(key, *dst)) return false;
+        P.eps = static_cast<float>(c["rms_norm_eps"].number(1e-6));
+        const JView rope = c["rope_parameters"];
+        P.rope_theta = static_cast<float>(rope["rope_theta"].number(10000.0));
+        P.rope_dim = static_cast<int>(P.head_dim * rope["partial_rotary_factor"].number(1.0));
+        const std::string g = "model geometry: ";
+        if (P.n_layers < 1 || P.n_layers > 1024) return refuse(g + "num_hidden_layers must be 1..1024");
+        const JView types = c["layer_types"];
+        if (types.count() != static_cast<size_t>(P.n_layers))
+            return refuse(g + "config.layer_types lists " + std::to_string(types.count()) + " layers for num_hidden_layers " +
+                          std::to_string(P.n_layers));
+        P.attention.clear();
+        for (int l = 0; l < P.n_layers; ++l)
+            P.attention.push_back(types.element(static_cast<size_t>(l)).text() == "full_attention");
+        if (P.hidden <= 0 || P.hidden % 16)
+            return refuse(g + "hidden_size " + std::to_string(P.hidden) + " is not a positive multiple of 16");
+        if (P.dense && (P.n_experts != 0 || P.shared_ff <= 0 || P.shared_ff % 16))
+            return refuse(g + "a dense model needs no experts and an intermediate_size that is a multiple of 16");
+        if (!P.dense && (P.top_k < 1 || P.top_k > P.n_experts))
+            return refuse(g + "num_experts_per_tok must be 1..num_experts");
+        if (P.gdn_v_heads % std::max(1, P.gdn_k_heads))
+            return refuse(g + "linear_num_value_heads is not a multiple of linear_num_key_heads");
+        if (P.n_heads % std::max(1, P.n_kv_heads))
+            return refuse(g + "num_attention_heads is not a multiple of num_key_value_heads");
+        if (P.rope_dim % 2) return refuse(g + "the rotary dimensions are odd");
+        return true;
+    }
+
+    // a tensor's entry; false with the refusal set; skip set when its file is an absent optional one
+    bool tensor_entry(const std::string &name, const JView &e, Tensor &x, bool &skip) {
+        const std::string file = e["file"].text();
+        skip = std::find(absent_.begin(), absent_.end(), file) != absent_.end();
+        if (skip) return true;
+        const std::string at = "tensor " + name + ": ";
+        x.type = type_of(e["type"].text());
+        if (x.type == T_UNKNOWN) return refuse(at + "type '" + e["type"].text() + "' is not a known tensor type");
+        const JView shape = e["shape"];
+        int64_t elements = 1, offset = 0;
+        bool in_range = e["offset"].integer(0, kMaxElements, offset);
+        for (size_t i = 0; i < shape.count() && in_range; ++i) {
+            int64_t d = 0;
+            in_range = shape.element(i).integer(1, kMaxDim, d) && elements <= kMaxElements / d;
+            elements *= d;
             x.shape.push_back(d);
         }
-        if (x.shape.empty()) x.shape.push_back(1);
-        x.rows = x.shape[0];
-        x.cols = 1;
-        for (size_t i = 1; i < x.shape.size() && shape_ok; ++i) {
-            x.cols *= x.shape[i];
-            shape_ok &= x.cols < (int64_t{1} << 40);
-        }
-        if (x.shape.size() == 1) {
-            x.cols = x.rows;
-            x.rows = 1;
-        }
-        const int64_t off = t["offset"].i64();
-        if (!shape_ok || off < 0 || static_cast<double>(x.rows) * static_cast<double>(x.cols) > 1099511627776.0)
-            return err = name + ": a shape or an offset out of range", false;
-        x.file = P.file_index(t["file"].str());
-        if (x.file < 0) return err = "geode.json names a file it does not list: " + t["file"].str(), false;
-        x.offset = static_cast<uint64_t>(off);
-        x.global = static_cast<float>(t["global"].f64(1.0));
-        if (quantized(x.type) && x.cols % 16) return err = name + ": columns not a multiple of 16", false;
-        const uint64_t fsize = P.sizes[static_cast<size_t>(x.file)];
-        if (x.offset > fsize || x.bytes() > fsize - x.offset) return err = name + ": runs past the end of " + t["file"].str(), false;
-        any_dense |= t["file"].str() == "dense.bin";
-        P.tensors.emplace(name, std::move(x));
-    }
-    if (!any_dense) return err = "geode.json: no tensors in dense.bin", false;
-    const Tensor *embed = P.find("embed_tokens.weight");
-    if (!embed || !quantized(embed->type) || embed->cols != P.hidden) return err = "geode.json: no usable embed_tokens.weight", false;
-
-    // the experts
-    const Json &el = m["experts"]["layers"];
-    if (static_cast<int>(el.size()) != (P.dense ? 0 : P.n_layers))
-        return err = "geode.json: the expert table does not cover every layer", false;
-    auto expert_layer = [&](const Json &e, int l) -> bool {
-        ExpertLayer x;
-        x.file = P.file_index(e["file"].str());
-        if (x.file < 0) return err = "geode.json names a file it does not list: " + e["file"].str(), false;
-        x.offset = static_cast<uint64_t>(e["offset"].i64());
-        if (e["stride"].kind == Json::Num) {
-            x.stride = static_cast<uint64_t>(e["stride"].i64());
-            x.type = type_of(e["format"].str());
-        } else {
-            for (size_t i = 0; i < e["offsets"].size(); ++i) {
-                x.offsets.push_back(static_cast<uint64_t>(e["offsets"].at(i).i64()));
-                x.types.push_back(type_of(e["formats"].at(i).str()));
-            }
-            if (static_cast<int>(x.offsets.size()) != P.n_experts)
-                return err = "geode.json: layer " + std::to_string(l) + " lists the wrong number of experts", false;
-        }
-        P.experts.push_back(std::move(x));
-        const std::string scales = l < P.n_layers ? "layers." + std::to_string(l) + ".mlp.experts.scales"
-                                                  : "mtp.layers.0.mlp.experts.scales";
-        const Tensor *s = P.find(scales);
-        if (!s || s->type != T_F32 || s->rows != P.n_experts || s->cols != 2)
-            return err = "geode.json: no expert scales for layer " + std::to_string(l), false;
+        if (!in_range) return refuse(at + "its shape or offset is outside what a pack can hold");
+        // rows and columns: [d0, d1 x d2 x ...]; a vector is one row; no dimension at all, one value
+        x.rows = x.shape.size() >= 2 ? x.shape[0] : 1;
+        x.cols = x.shape.empty() ? 1 : elements / x.rows;
+        x.file = P_.file_index(file);
+        if (x.file < 0) return refuse(at + "file '" + file + "' is not one of geode.json's files");
+        x.offset = static_cast<uint64_t>(offset);
+        x.global = static_cast<float>(e["global"].number(1.0));
+        if (quantized(x.type) && x.cols % 16)
+            return refuse(at + "a quantized tensor needs a multiple of 16 columns (it has " + std::to_string(x.cols) + ")");
+        const uint64_t fsize = P_.sizes[static_cast<size_t>(x.file)];
+        if (x.offset > fsize || x.bytes() > fsize - x.offset) return refuse(at + "its bytes run past the end of " + file);
         return true;
-    };
-    for (int l = 0; l < (P.dense ? 0 : P.n_layers); ++l)
-        if (!expert_layer(el.at(static_cast<size_t>(l)), l)) return false;
-    bool any_q3 = false;
-    for (const auto &[name, t] : P.tensors) any_q3 |= t.type == T_Q3;
-    for (const auto &x : P.experts) {
-        any_q3 |= x.type == T_Q3;
-        for (int t : x.types) any_q3 |= t == T_Q3;
     }
-    if (any_q3 && m["formats"]["q3"]["high_bits"].str() != "value order")
-        return err = "geode.json: q3 with the old bit planes", false;
-    P.tile8 = m["formats"]["q4"]["layout"].str() == "tile8";
-    if (m["mtp"].kind == Json::Obj) {
-        if (!P.dense && !expert_layer(m["mtp"]["experts"], P.n_layers)) return false;
-        P.mtp = true;
+
+    bool read_tensors() {
+        const JView table = manifest()["tensors"];
+        if (!table.is(JsonTape::kObject)) return refuse("geode.json has no tensor table (\"tensors\")");
+        bool ok = true, in_dense = false;
+        table.each_member([&](const std::string &name, const JView &e) {
+            if (!ok) return;
+            Tensor x;
+            bool skip = false;
+            ok = tensor_entry(name, e, x, skip);
+            if (!ok || skip) return;
+            in_dense = in_dense || P_.files[static_cast<size_t>(x.file)] == "dense.bin";
+            P_.tensors[name] = std::move(x);
+        });
+        if (!ok) return false;
+        if (!in_dense) return refuse("geode.json places no tensor in dense.bin");
+        const Tensor *embed = P_.find("embed_tokens.weight");
+        if (!embed || !quantized(embed->type) || embed->cols != P_.hidden)
+            return refuse("embed_tokens.weight must be a quantized [vocab, hidden_size] tensor");
+        return true;
     }
-    return true;
-}
+
+    // expert layer l's entry (l = n_layers: the MTP layer's) and its scales tensor
+    bool expert_layer(const JView &e, int l) {
+        const std::string at = "experts, layer " + std::to_string(l) + ": ";
+        ExpertLayer x;
+        x.file = P_.file_index(e["file"].text());
+        if (x.file < 0) return refuse(at + "file '" + e["file"].text() + "' is not one of geode.json's files");
+        int64_t v = 0;
+        if (e["stride"].is(JsonTape::kNumber)) {   // one format, expert i at offset + i x stride
+            if (!e["offset"].integer(0, kMaxElements, v)) return refuse(at + "the offset is not a byte position");
+            x.offset = static_cast<uint64_t>(v);
+            if (!e["stride"].integer(0, kMaxElements, v)) return refuse(at + "the stride is not a byte count");
+            x.stride = static_cast<uint64_t>(v);
+            x.type = type_of(e["format"].text());
+        } else {                                   // per-expert offsets and formats
+            const JView offs = e["offsets"], fmts = e["formats"];
+            if (offs.count() != static_cast<size_t>(P_.n_experts) || fmts.count() != offs.count())
+                return refuse(at + std::to_string(offs.count()) + " experts listed, config.num_experts is " +
+                              std::to_string(P_.n_experts));
+            for (size_t i = 0; i < offs.count(); ++i) {
+                if (!offs.element(i).integer(0, kMaxElements, v)) return refuse(at + "an offset is not a byte position");
+                x.offsets.push_back(static_cast<uint64_t>(v));
+                x.types.push_back(type_of(fmts.element(i).text()));
+            }
+        }
+        P_.experts.push_back(std::move(x));
+        const std::string scales = l < P_.n_layers ? "layers." + std::to_string(l) + ".mlp.experts.scales"
+                                                   : "mtp.layers.0.mlp.experts.scales";
+        const Tensor *s = P_.find(scales);
+        if (!s || s->type != T_F32 || s->rows != P_.n_experts || s->cols != 2)
+            return refuse(at + "the scales tensor " + scales + " is missing or not f32 [num_experts, 2]");
+        return true;
+    }
+
+    bool read_expert_table() {
+        const JView layers = manifest()["experts"]["layers"];
+        const size_t want = P_.dense ? 0 : static_cast<size_t>(P_.n_layers);
+        if (layers.count() != want)
+            return refuse("geode.json's expert table has " + std::to_string(layers.count()) + " layers; the model has " +
+                          std::to_string(want) + " MoE layers");
+        for (size_t l = 0; l < want; ++l)
+            if (!expert_layer(layers.element(l), static_cast<int>(l))) return false;
+        const JView mtp = manifest()["mtp"];
+        if (mtp.is(JsonTape::kObject)) {
+            if (!P_.dense && !expert_layer(mtp["experts"], P_.n_layers)) return false;
+            P_.mtp = true;
+        }
+        return true;
+    }
+
+    bool read_formats() {
+        const JView formats = manifest()["formats"];
+        bool q3 = false;
+        for (const auto &kv : P_.tensors) q3 = q3 || kv.second.type == T_Q3;
+        for (const auto &x : P_.experts) {
+            q3 = q3 || x.type == T_Q3;
+            q3 = q3 || std::find(x.types.begin(), x.types.end(), static_cast<int>(T_Q3)) != x.types.end();
+        }
+        // q3 packs written before the values' high bits went in value order are not readable (kernels.hpp's q3)
+        if (q3 && formats["q3"]["high_bits"].text() != "value order")
+            return refuse("q3 tensors need formats.q3.high_bits = \"value order\"");
+        P_.tile8 = formats["q4"]["layout"].text() == "tile8";
+        return true;
+    }
+
+    gv_pack &P_;
+    std::string &err_;
+    std::vector<std::string> absent_;   // optional files not present
+};
 
 // tile8 (kernels.cpp:971-991) back to the pack's rows: per 32-row tile, code word j of chunk c of quad i (four rows'
 // 32-bit words, affine codes) at ((c * 8 + j) * 8 + i) * 16 + 4 r, then the scales, block b of chunk c of row r of
@@ -589,7 +750,7 @@ gv_pack *gv_pack_open(const char *dir, char *err, int err_len) {
     }
     auto P = std::make_unique<gv_pack>();
     std::string e;
-    if (!open_pack(*P, dir, e)) {
+    if (!PackOpener(*P, e).run(dir)) {
         put(e);
         return nullptr;
     }

@@ -220,51 +220,54 @@ void launch_blocks(Model &m, int B, int b0, int nb, int position, uint8_t *dev_f
                            m.attn_index, n_attn, c.n_kv_heads, c.head_dim, m.slots, B, b0, nb, position, dev_file);
 }
 
-// a file read and written at offsets, in pieces of at most 1 GB
-struct StateFile {
-    int fd = -1;
-    ~StateFile() { close(); }
-    bool open(const std::string &path, bool write, bool create) {
-        int flags = O_CLOEXEC | (write ? O_RDWR : O_RDONLY);
-        if (create) flags |= O_CREAT | O_TRUNC;
-        fd = ::open(path.c_str(), flags, 0600);
-        return fd >= 0;
+// The state file's I/O: positioned transfers (pread / pwrite in pieces of at most 1 GB, resumed after a short one),
+// its length, and fsync, which orders a save's parts on the disk (a header is never written ahead of what it names).
+class StateIo {
+public:
+    enum Mode { kRead, kUpdate, kCreate };   // read only; read and write in place; a new file (truncated)
+    ~StateIo() { shut(); }
+    bool open(const std::string &path, Mode mode) {
+        const int how = mode == kRead ? O_RDONLY : mode == kUpdate ? O_RDWR : (O_RDWR | O_CREAT | O_TRUNC);
+        fd_ = ::open(path.c_str(), how | O_CLOEXEC, 0600);
+        return fd_ >= 0;
     }
-    void close() {
-        if (fd >= 0) ::close(fd);
-        fd = -1;
+    void shut() {
+        if (fd_ >= 0) ::close(fd_);
+        fd_ = -1;
     }
-    uint64_t size() const {
-        struct stat s {};
-        return fstat(fd, &s) == 0 ? static_cast<uint64_t>(s.st_size) : 0;
+    uint64_t length() const {
+        struct stat st {};
+        return fd_ >= 0 && fstat(fd_, &st) == 0 ? static_cast<uint64_t>(st.st_size) : 0;
     }
-    bool write(uint64_t off, const void *data, size_t n) {
-        const auto *p = static_cast<const uint8_t *>(data);
-        while (n > 0) {
-            const ssize_t w = ::pwrite(fd, p, std::min<size_t>(n, size_t{1} << 30), static_cast<off_t>(off));
-            if (w <= 0) return false;
-            p += w, off += static_cast<uint64_t>(w), n -= static_cast<size_t>(w);
+    bool put(uint64_t at, const void *src, size_t n) { return transfer(at, const_cast<void *>(src), n, true); }
+    bool get(uint64_t at, void *dst, size_t n) { return transfer(at, dst, n, false); }
+    bool flush() { return fd_ >= 0 && ::fsync(fd_) == 0; }
+
+private:
+    bool transfer(uint64_t at, void *buf, size_t n, bool out) {
+        auto *p = static_cast<uint8_t *>(buf);
+        for (size_t left = n; left > 0;) {
+            const size_t piece = std::min<size_t>(left, size_t{1} << 30);
+            const ssize_t moved = out ? ::pwrite(fd_, p, piece, static_cast<off_t>(at))
+                                      : ::pread(fd_, p, piece, static_cast<off_t>(at));
+            if (moved <= 0) return false;
+            p += moved;
+            at += static_cast<uint64_t>(moved);
+            left -= static_cast<size_t>(moved);
         }
         return true;
     }
-    bool read(uint64_t off, void *data, size_t n) {
-        auto *p = static_cast<uint8_t *>(data);
-        while (n > 0) {
-            const ssize_t r = ::pread(fd, p, std::min<size_t>(n, size_t{1} << 30), static_cast<off_t>(off));
-            if (r <= 0) return false;
-            p += r, off += static_cast<uint64_t>(r), n -= static_cast<size_t>(r);
-        }
-        return true;
-    }
-    bool sync() { return ::fsync(fd) == 0; }
+    int fd_ = -1;
 };
 
-bool read_header(StateFile &f, StateHeader &h, std::string &err) {
-    if (!f.read(0, &h, sizeof h)) return err = "not a saved conversation (too short)", false;
-    if (std::memcmp(h.magic, kMagic, sizeof kMagic) != 0) return err = "not a saved conversation", false;
+// the header read and checked in the order a reader relies on it: present, the format's magic, its version and
+// size, then its checksum over every byte before the checksum field
+bool read_header(StateIo &f, StateHeader &h, std::string &err) {
+    if (!f.get(0, &h, sizeof h)) return err = "the file is shorter than a state header", false;
+    if (std::memcmp(h.magic, kMagic, sizeof kMagic) != 0) return err = "the file has no state-file magic", false;
     if (h.version != kVersion || h.header_size != sizeof(StateHeader))
-        return err = "a saved conversation of another version (" + std::to_string(h.version) + ")", false;
-    if (h.checksum != header_checksum(h)) return err = "the saved conversation's header is damaged", false;
+        return err = "state format version " + std::to_string(h.version) + " (this library reads version 1)", false;
+    if (h.checksum != header_checksum(h)) return err = "the header's checksum does not match its bytes", false;
     return true;
 }
 
@@ -317,10 +320,10 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
     int first_block = 0;
     bool in_place = false;
     if (append) {
-        StateFile f;
+        StateIo f;
         StateHeader old{};
         std::string e;
-        if (f.open(path, false, false) && read_header(f, old, e) && old.fingerprint == h.fingerprint &&
+        if (f.open(path, StateIo::kRead) && read_header(f, old, e) && old.fingerprint == h.fingerprint &&
             old.conv_id == h.conv_id && old.position <= h.position && h.n_images <= old.image_cap &&
             old.block == h.block && old.block_bytes == h.block_bytes && old.fixed_offset == h.fixed_offset) {
             h.image_cap = old.image_cap;
@@ -335,13 +338,13 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
     h.checksum = header_checksum(h);
 
     const std::string target = in_place ? std::string(path) : std::string(path) + ".tmp";
-    StateFile f;
-    if (!f.open(target, true, !in_place)) {
+    StateIo f;
+    if (!f.open(target, in_place ? StateIo::kUpdate : StateIo::kCreate)) {
         set_error("gv_model_save_state: cannot write " + target);
         return GV_STATE_E_IO;
     }
     auto fail = [&](int code, const char *what) {
-        f.close();
+        f.shut();
         if (!in_place) std::remove(target.c_str());
         set_error(std::string("gv_model_save_state: ") + what + " (" + target + ")");
         return code;
@@ -352,9 +355,9 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
         if (h.has_hidden) std::memcpy(head.data() + (L.hidden - h.fixed_offset), info->hidden, size_t{h.hidden} * 4);
         std::vector<float> conv, rec;
         if (gdn_states_io(m, conv, rec, true) != 0) return fail(GV_STATE_E_IO, "cannot read the layers' states");
-        if (!f.write(h.fixed_offset, head.data(), head.size()) || !f.write(L.conv, conv.data(), conv.size() * 4) ||
-            !f.write(L.gdn, rec.data(), rec.size() * 4) || !f.sync() || !f.write(L.trail, &h.gen, sizeof h.gen))
-            return fail(GV_STATE_E_IO, "cannot write the conversation's states");
+        if (!f.put(h.fixed_offset, head.data(), head.size()) || !f.put(L.conv, conv.data(), conv.size() * 4) ||
+            !f.put(L.gdn, rec.data(), rec.size() * 4) || !f.flush() || !f.put(L.trail, &h.gen, sizeof h.gen))
+            return fail(GV_STATE_E_IO, "writing the fixed part (generation, hidden row, layer states) failed");
     }
     const int blocks = (m.pos + kStateBlock - 1) / kStateBlock;
     if (blocks > first_block) {
@@ -375,13 +378,13 @@ int gv_model_save_state(gv_model *g, const char *path, int append, const gv_stat
                 hipMemcpyAsync(buf.data(), dbuf.p, static_cast<size_t>(nb) * bb, hipMemcpyDeviceToHost, st) != hipSuccess ||
                 hipStreamSynchronize(st) != hipSuccess)
                 return fail(GV_STATE_E_IO, "cannot read the KV cache from the device");
-            if (!f.write(h.kv_offset + static_cast<uint64_t>(b0) * h.block_bytes, buf.data(), static_cast<size_t>(nb) * bb))
-                return fail(GV_STATE_E_IO, "cannot write the conversation's KV cache");
+            if (!f.put(h.kv_offset + static_cast<uint64_t>(b0) * h.block_bytes, buf.data(), static_cast<size_t>(nb) * bb))
+                return fail(GV_STATE_E_IO, "writing the KV blocks failed");
         }
     }
-    if (!f.sync() || !f.write(0, &h, sizeof h) || !f.sync())   // the header last, once what it names is written
-        return fail(GV_STATE_E_IO, "cannot write the conversation's header");
-    f.close();
+    if (!f.flush() || !f.put(0, &h, sizeof h) || !f.flush())   // the header last, once what it names is written
+        return fail(GV_STATE_E_IO, "writing the header failed");
+    f.shut();
     if (!in_place && std::rename(target.c_str(), path) != 0) {
         std::remove(target.c_str());
         set_error(std::string("gv_model_save_state: cannot move ") + target + " to " + path);
@@ -410,8 +413,8 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
         set_error("gv_model_load_state: " + e);
         return code;
     };
-    StateFile f;
-    if (!f.open(path, false, false)) return refuse(GV_STATE_E_IO, std::string("cannot open ") + path);
+    StateIo f;
+    if (!f.open(path, StateIo::kRead)) return refuse(GV_STATE_E_IO, std::string("cannot open ") + path);
     StateHeader h{};
     std::string e;
     if (!read_header(f, h, e)) return refuse(GV_STATE_E_FORMAT, e);
@@ -420,29 +423,30 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
         h.n_attn != static_cast<uint32_t>(m.attn_layers.size()) || h.kv_heads != static_cast<uint32_t>(c.n_kv_heads) ||
         h.kv_row != s.kv_row || h.hidden != static_cast<uint32_t>(c.hidden) || h.conv_n != conv_n_of(m) ||
         h.gdn_n != gdn_n_of(m) || h.block == 0 || h.block > (1u << 24))
-        return refuse(GV_STATE_E_FORMAT, "the conversation was saved by another model or another KV cache format");
+        return refuse(GV_STATE_E_FORMAT, "the file's model fingerprint, layer shapes or KV element type differ from "
+                                         "this model's");
     if (h.position < 0 || h.position >= c.max_ctx)
-        return refuse(GV_STATE_E_ARG, "the saved conversation (" + std::to_string(h.position) +
-                                          " tokens) is longer than this context (" + std::to_string(c.max_ctx) + ")");
+        return refuse(GV_STATE_E_ARG, "the file holds " + std::to_string(h.position) + " positions; this model's "
+                                          "context is " + std::to_string(c.max_ctx));
     const Layout L = layout_of(h);
     const uint64_t B = h.block;
     const int blocks = static_cast<int>((static_cast<uint64_t>(h.position) + B - 1) / B);
     if (L.fixed_bytes != h.fixed_bytes || L.kv_offset != h.kv_offset || h.n_images > h.image_cap ||
         h.block_bytes != 2 * static_cast<uint64_t>(m.attn_layers.size()) * B * (uint64_t{s.kv_row} * s.elem + s.scale_bytes) ||
-        f.size() < h.kv_offset + static_cast<uint64_t>(blocks) * h.block_bytes)
-        return refuse(GV_STATE_E_IO, "the saved conversation is cut short");
+        f.length() < h.kv_offset + static_cast<uint64_t>(blocks) * h.block_bytes)
+        return refuse(GV_STATE_E_IO, "the file ends before the parts its header names");
     uint64_t lead = 0, trail = 0;
-    if (!f.read(h.fixed_offset, &lead, 8) || !f.read(L.trail, &trail, 8) || lead != h.gen || trail != h.gen)
-        return refuse(GV_STATE_E_IO, "the saved conversation is incomplete (its save was interrupted)");
+    if (!f.get(h.fixed_offset, &lead, 8) || !f.get(L.trail, &trail, 8) || lead != h.gen || trail != h.gen)
+        return refuse(GV_STATE_E_IO, "the fixed part's generation marks disagree with the header (a save did not finish)");
     // images need a vision encoder's rotary positions, which this model does not compute
     if (h.n_images != 0)
-        return refuse(GV_STATE_E_FORMAT, "the saved conversation holds images (this model has no vision encoder)");
-    if (h.has_hidden && info->hidden && !f.read(L.hidden, info->hidden, size_t{h.hidden} * 4))
-        return refuse(GV_STATE_E_IO, "cannot read the last hidden state");
+        return refuse(GV_STATE_E_FORMAT, "the file holds image positions; this model has no vision encoder");
+    if (h.has_hidden && info->hidden && !f.get(L.hidden, info->hidden, size_t{h.hidden} * 4))
+        return refuse(GV_STATE_E_IO, "reading the hidden row failed");
     {
         std::vector<float> conv(static_cast<size_t>(h.conv_n)), rec(static_cast<size_t>(h.gdn_n));
-        if (!f.read(L.conv, conv.data(), conv.size() * 4) || !f.read(L.gdn, rec.data(), rec.size() * 4))
-            return refuse(GV_STATE_E_IO, "cannot read the layers' states");
+        if (!f.get(L.conv, conv.data(), conv.size() * 4) || !f.get(L.gdn, rec.data(), rec.size() * 4))
+            return refuse(GV_STATE_E_IO, "reading the layer states failed");
         if (gdn_states_io(m, conv, rec, false) != 0) return refuse(GV_STATE_E_IO, "cannot copy the layers' states");
     }
     if (blocks > 0) {
@@ -458,8 +462,8 @@ int gv_model_load_state(gv_model *g, const char *path, gv_state_info *info) {
         const hipStream_t st = stream();
         for (int b0 = 0; b0 < blocks; b0 += per) {
             const int nb = std::min(per, blocks - b0);
-            if (!f.read(h.kv_offset + static_cast<uint64_t>(b0) * h.block_bytes, buf.data(), static_cast<size_t>(nb) * bb))
-                return refuse(GV_STATE_E_IO, "cannot read the KV cache");
+            if (!f.get(h.kv_offset + static_cast<uint64_t>(b0) * h.block_bytes, buf.data(), static_cast<size_t>(nb) * bb))
+                return refuse(GV_STATE_E_IO, "reading the KV blocks failed");
             if (hipMemcpyAsync(dbuf.p, buf.data(), static_cast<size_t>(nb) * bb, hipMemcpyHostToDevice, st) != hipSuccess)
                 return refuse(GV_STATE_E_IO, "cannot copy the KV cache to the device");
             launch_blocks<false>(m, static_cast<int>(B), b0, nb, h.position, dbuf.p, st);

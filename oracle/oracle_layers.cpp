@@ -488,12 +488,15 @@ float fill_q4(std::vector<uint8_t> &dst, int64_t rows, int64_t cols, uint64_t se
     if (fast) {
         const int64_t nb = cols / 16;
         const size_t rb = q4_row_bytes(cols);
+        // (eight code bytes a hash; each scale byte from a byte of a hash: 0x30 + b % 25, exponents 6..9)
         par(rows, 64, [&](int64_t a, int64_t b) {
             for (int64_t r = a; r < b; ++r) {
                 uint8_t *row = dst.data() + static_cast<size_t>(r) * rb;
-                for (int64_t i = 0; i < nb * 8; ++i) row[i] = static_cast<uint8_t>(orc_hash(seed, static_cast<uint64_t>(r * rb + i)));
-                for (int64_t i = 0; i < nb; ++i)
-                    row[nb * 8 + i] = static_cast<uint8_t>(0x30 + orc_hash(seed ^ 1, static_cast<uint64_t>(r * nb + i)) % 25);
+                for (int64_t i = 0; i < nb; ++i) {
+                    const uint64_t h = orc_hash(seed, static_cast<uint64_t>(r * nb + i));
+                    std::memcpy(row + 8 * i, &h, 8);
+                    row[nb * 8 + i] = static_cast<uint8_t>(0x30 + ((orc_hash(seed ^ 1, static_cast<uint64_t>(r * nb + i)) >> 24) & 0xFF) % 25);
+                }
             }
         });
         return 1.0f / 448.0f;
@@ -590,15 +593,17 @@ void orc_model_fill(orc_model *m, uint64_t seed, float sigma, float router_sigma
         const size_t eb = expert_block_bytes(c), gu = static_cast<size_t>(2 * F) * q4_row_bytes(H);
         L.experts.resize(eb * static_cast<size_t>(E));
         L.expert_globals.resize(static_cast<size_t>(2 * E));
-        std::vector<uint8_t> tmp;
-        for (int e = 0; e < E; ++e) {
-            L.expert_globals[static_cast<size_t>(2 * e)] =
-                fill_q4(tmp, 2 * F, H, tensor_seed(seed, ORC_EXPERT, l, 2 * e), sigma, fast);
-            std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e));
-            L.expert_globals[static_cast<size_t>(2 * e + 1)] =
-                fill_q4(tmp, H, F, tensor_seed(seed, ORC_EXPERT, l, 2 * e + 1), sigma, fast);
-            std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e + gu));
-        }
+        par(E, 1, [&](int64_t e0, int64_t e1) {   // experts on the pool's threads (each fill then runs in its thread)
+            std::vector<uint8_t> tmp;
+            for (int64_t e = e0; e < e1; ++e) {
+                L.expert_globals[static_cast<size_t>(2 * e)] =
+                    fill_q4(tmp, 2 * F, H, tensor_seed(seed, ORC_EXPERT, l, static_cast<int>(2 * e)), sigma, fast);
+                std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e));
+                L.expert_globals[static_cast<size_t>(2 * e + 1)] =
+                    fill_q4(tmp, H, F, tensor_seed(seed, ORC_EXPERT, l, static_cast<int>(2 * e + 1)), sigma, fast);
+                std::copy(tmp.begin(), tmp.end(), L.experts.begin() + static_cast<ptrdiff_t>(eb * e + gu));
+            }
+        });
         L.gdn = c.gdn_v_heads > 0 && l < c.n_layers && c.gdn_layers[l] != 0;
         if (L.gdn) {   // the GDN layer's weights, then (a context) its states
             const int nk = c.gdn_k_heads, nv = c.gdn_v_heads, dk = c.gdn_k_dim, dv = c.gdn_v_dim, K = c.conv_kernel;

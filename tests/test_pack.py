@@ -127,12 +127,15 @@ def _damage(what):
 
 
 @pytest.mark.parametrize("what,message", [
-    ("format", "not a geode-pack v1"), ("version", "not a geode-pack v1"), ("arch", "unknown architecture"),
-    ("size", "bytes, expected"), ("layers", "layer_types"), ("geometry", "inconsistent model geometry"),
-    ("type", "unknown type"), ("past_end", "runs past the end"), ("negative", "out of range"),
-    ("cols", "not a multiple of 16"), ("unlisted", "does not list"), ("no_dense", "no tensors in dense.bin"),
-    ("embed", "embed_tokens"), ("experts", "does not cover every layer"), ("scales", "no expert scales"),
-    ("expert_count", "wrong number of experts")])
+    ("format", "format 'other' version 1; this reader takes geode-pack version 1"),
+    ("version", "format 'geode-pack' version 2;"), ("arch", "architecture 'llama' is not one this library loads"),
+    ("size", "bytes; geode.json lists"), ("layers", "layer_types lists 1 layers"),
+    ("geometry", "model geometry: hidden_size 130"), ("type", "type 'f64' is not a known tensor type"),
+    ("past_end", "its bytes run past the end of dense.bin"), ("negative", "outside what a pack can hold"),
+    ("cols", "needs a multiple of 16 columns"), ("unlisted", "file 'other.bin' is not one of geode.json's files"),
+    ("no_dense", "no tensor in dense.bin"), ("embed", "embed_tokens.weight must be"),
+    ("experts", "expert table has 1 layers; the model has 2"), ("scales", "layer 1: the scales tensor"),
+    ("expert_count", "3 experts listed, config.num_experts is 8")])
 def test_open_refuses(gv, om, tmp_path, what, message):
     write_pack(om, str(tmp_path), mutate=_damage(what))
     with pytest.raises(gv.GeodeError, match=message):
@@ -179,3 +182,19 @@ def test_gated_deltanet_pack(gv, tmp_path):
     assert got["global"] == np.float32(om.tensor(po.GDN_QKV, 2)[1][0])
     with pytest.raises(gv.GeodeError, match="no layers.0.self_attn"):
         p.tensor("layers.0.self_attn.q_proj.weight")
+
+
+@pytest.mark.parametrize("text,valid", [
+    ('{"a": [1, 2,]}', False), ('{"a": 01}', False), ('{"a": 1.}', False), ('{"a": -}', False),
+    ('{"a": "\\ud800"}', False), ('{"a": "\\udc00\\ud800"}', False), ('{"a": "x\ty"}', False),
+    ('{"a": "\\x"}', False), ('{"a" 1}', False), ('{"a": 1} {}', False), ('{"a": [1 2]}', False),
+    ('{"a": tru}', False), ('{"a": "open}', False), ('[', False), ('', False),
+    ('{"a": [], "b": {}, "c": [[], {}], "d": -0, "e": 1E+2, "f": 0.5e-3, "g": "\\ud83d\\ude00", "h": null}', True),
+    ('  {"format": "geode-pack", "version": 1}\n', True)])
+def test_json_reader_follows_rfc_8259(gv, tmp_path, text, valid):
+    """the manifest reader accepts RFC 8259's grammar and nothing else: a document it refuses is reported as invalid
+    JSON; one it accepts goes on to the manifest's own checks (which these minimal documents then fail)"""
+    (tmp_path / "geode.json").write_text(text, encoding="utf-8")
+    with pytest.raises(gv.GeodeError) as e:
+        gv.Pack(str(tmp_path))
+    assert ("is not valid JSON" in str(e.value)) != valid, str(e.value)
