@@ -2555,7 +2555,9 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
     const auto &c = m.c;
     GV_REQUIRE(n >= 1 && n <= c.max_rows, "gv_verify: 1 <= n <= max_rows");
     GV_REQUIRE(m.pos + n <= c.max_ctx, "gv_verify: the context is full");
-    StepParams &sp = m.host_sp;
+    // the step's parameters made and checked apart from the model's: a refused call leaves the last verify's
+    // (which gv_verify_keep reads) and everything else as they were
+    StepParams sp;
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;
     sp.M = n;
@@ -2573,8 +2575,9 @@ int gv_verify(gv_model *g, const int32_t *tokens, int n, const int32_t *parents,
             sp.vis[i] = (i == 31) ? 0xFFFFFFFFu : ((1u << (i + 1)) - 1u);
         }
     }
+    m.host_sp = sp;
     hipStream_t st = stream();
-    GV_CHECK_HIP(hipMemcpyAsync(m.sp, &sp, sizeof sp, hipMemcpyHostToDevice, st));
+    GV_CHECK_HIP(hipMemcpyAsync(m.sp, &m.host_sp, sizeof sp, hipMemcpyHostToDevice, st));
     if (run_step(m, n, st) != 0) return -1;
     if (logits) {
         GV_CHECK_HIP(hipMemcpyAsync(logits, m.logits, static_cast<size_t>(n) * c.vocab * 4, hipMemcpyDeviceToHost, st));
@@ -2722,6 +2725,7 @@ int gv_model_moe(gv_model *g, int layer, const float *h, int M, const float *rou
     const hipStream_t st = stream();
     if (prefill_alloc(m, M) != 0) return -1;
     Prefill &pf = m.pf;
+    m.last_n = 0;   // (the last verify's parameters are replaced below: nothing is left to keep, failed or not)
     StepParams &sp = m.host_sp;
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;
@@ -2758,6 +2762,7 @@ int gv_model_layer(gv_model *g, int layer, const float *x_in, int n, const int32
     const auto &c = m.c;
     GV_REQUIRE(layer >= 0 && layer < c.n_layers, "gv_model_layer: no such layer");
     GV_REQUIRE(n >= 1 && n <= c.max_rows && m.pos + n <= c.max_ctx, "gv_model_layer: 1 <= n <= max_rows, in context");
+    m.last_n = 0;   // (the last verify's parameters are replaced below: nothing is left to keep, failed or not)
     StepParams &sp = m.host_sp;
     std::memset(&sp, 0, sizeof sp);
     sp.pos = m.pos;

@@ -51,7 +51,7 @@ def test_state_carries_the_pack_print(gv, om, tmp_path):
     m.verify(np.array([1, 2, 3], np.int32))
     path = str(tmp_path / "s.geode")
     m.save_state(path, pack_print=pack.print)
-    with pytest.raises(gv.StateError, match="another model"):
+    with pytest.raises(gv.StateError, match="model fingerprint"):
         m.load_state(path, pack_print=pack.print ^ 1)
     assert m.load_state(path, pack_print=pack.print)["conv_id"] == 0 and m.position == 3
 
