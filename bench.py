@@ -100,33 +100,55 @@ def step_bytes(c, M, uniq_per_layer, ctx):
     return tot
 
 
-def cpu_baseline(M, threads, kv_int8=False):
-    """The oracle (the reference's CPU arithmetic restated, int8 path; g++ -O3 -march=x86-64-v3, rows split over
-    `threads` in chunks of 16 as ThreadPool::parallel_for) on the host cores: a bounded sample of the same workload,
-    1 of the 40 layers plus the final norm and lm_head at full shapes (timing-only random q4 bytes); the step time
-    is extrapolated as t_head + 40 x t_layer."""
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as po
+    return po
 
+
+def cpu_baseline(M, threads, kv_int8=False, budget_s=30.0):
+    """The oracle (the reference's CPU arithmetic restated, int8 path; g++ -O3 -march=x86-64-v3, rows split over
+    `threads` in chunks of 16 as ThreadPool::parallel_for) on the host cores: whole 40-layer verify steps of the same
+    workload (full shapes, ctx 8192, timing-only random q4 bytes, every layer its own weights: ~20 GB of host memory),
+    the best of the steps that fit the time budget (at least one)."""
+    po = _oracle()
     po.lib.orc_set_threads(threads)
     cfg = dict(C4, kv_int8=int(kv_int8))
-    cfg["n_layers"] = 1
+    om = po.Model(cfg, seed=SEED, ctx=CTX, fast=True)
+    toks = (np.arange(M) * 1000 + 7).astype(np.int32)
+    times = []
+    t_start = time.time()
+    while not times or (time.time() - t_start + times[-1] < budget_s and len(times) < 3):
+        om.position = CTX
+        t0 = time.perf_counter()
+        om.verify(toks)
+        times.append(time.perf_counter() - t0)
+    del om
+    best = min(times)
+    return {"value": M / best, "unit": "tok/s", "cores": threads, "kind": "port",
+            "verify_steps_per_s": 1.0 / best,
+            "sample": f"whole 40-layer verify steps at full shapes, M={M}, ctx {CTX}, int8 path, "
+                      f"{'int8' if kv_int8 else 'fp16'} KV; best of {len(times)}: {best * 1e3:.0f} ms a step"}
+
+
+def cpu_baseline_one_core(M, kv_int8=False):
+    """one core: a bounded sample (one of the 40 layers plus the final norm and lm_head at full shapes, the step
+    extrapolated as t_head + 40 x t_layer; a whole step on one core takes ~1.5 minutes)"""
+    po = _oracle()
+    po.lib.orc_set_threads(1)
+    cfg = dict(C4, kv_int8=int(kv_int8), n_layers=1)
     om = po.Model(cfg, seed=SEED, ctx=CTX, fast=True)
     toks = (np.arange(M) * 1000 + 7).astype(np.int32)
     best = None
-    t_start = time.time()
-    reps = 0
-    while reps < 2 or (time.time() - t_start < 8 and reps < 4):
+    for _ in range(2):
         om.position = CTX
         om.verify(toks)
         tl, th = om.last_times()
         est = th + C4["n_layers"] * tl
         best = est if best is None else min(best, est)
-        reps += 1
-    return {"value": M / best, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"1 of 40 layers + final norm + lm_head at full shapes, M={M}, ctx {CTX}, int8 path, "
-                      f"{'int8' if kv_int8 else 'fp16'} KV, "
-                      f"best of {reps}; step = t_head + 40 x t_layer = {best * 1e3:.1f} ms"}
+    return {"value": M / best, "unit": "tok/s", "cores": 1,
+            "sample": f"1 of 40 layers + final norm + lm_head at full shapes, M={M}; step = t_head + 40 x t_layer = "
+                      f"{best * 1e3:.0f} ms"}
 
 
 def bench_moe_block(g, M, reps):
@@ -558,6 +580,8 @@ def main():
                                 f", ctx {CTX}, vocab 151936, q4 weights, {'int8' if args.kv_int8 else 'fp16'} KV, int8-path products"),
                    "rows": M, "tokens_emitted_per_step": emitted, "acceptance": "greedy sample-and-match on the "
                    "step's logits; drafts = the target's own greedy chain" if not args.tree else "greedy tree walk"},
+        "value_note": "tok/s with every draft accepted (the drafts are the target's own greedy chain): the ceiling "
+                      "of acceptance; verify_steps_per_s is the step rate that does not depend on it",
         "verify_steps_per_s": verify_steps_s,
         "ms_per_verify": ms_verify,
         "ms_per_step_device_events": ms_events,
@@ -578,11 +602,13 @@ def main():
     if tree:
         out["tree_m17"] = tree
     if not args.no_cpu:
-        # the box's CPU share for one GPU is 16 threads (whatever os.cpu_count() shows there), and one core
-        threads = min(16, os.cpu_count() or 1)
+        # the host's threads as the process may use them, within the box's CPU share for one GPU (16 threads,
+        # whatever os.cpu_count() shows there); and one core
+        host = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+        threads = min(16, host)
         out["cpu_baseline"] = cpu_baseline(M, threads, args.kv_int8)
-        one = cpu_baseline(M, 1, args.kv_int8)
-        out["cpu_baseline"]["one_core"] = {"value": one["value"], "unit": one["unit"], "sample": one["sample"]}
+        out["cpu_baseline"]["host_threads"] = os.cpu_count()
+        out["cpu_baseline"]["one_core"] = cpu_baseline_one_core(M, args.kv_int8)
     print(json.dumps(out))
 
 
