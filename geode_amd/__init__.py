@@ -545,8 +545,9 @@ class VerifyModel:
         check(_lib().gv_model_set_graphs(self.h, 1 if on else 0), "gv_model_set_graphs")
 
     def set_fused(self, on):
-        """dependent phases chained within one launch where the shapes fit (default) or one launch a phase"""
-        check(_lib().gv_model_set_fused(self.h, 1 if on else 0), "gv_model_set_fused")
+        """dependent phases chained within one launch where the shapes fit (True / 1, the default: with the rows
+        routed by the experts' up launch; 2: routed by the output projection's launch) or one launch a phase (0)"""
+        check(_lib().gv_model_set_fused(self.h, int(on)), "gv_model_set_fused")
 
     def trace(self, on):
         """workgroup clock stamps of the traced kernels on or off (a measurement aid)"""

@@ -252,6 +252,21 @@ __device__ inline int wave_incl_scan(int v) {
 }
 
 // the maximum over the wave's 64 lanes, a uniform value
+// The wave's largest of int keys, in every lane: four DPP steps within each 16-lane row (pairs, quads, eights,
+// sixteens), then gfx950's row swaps (rows 0 <-> 1 and 2 <-> 3, then the halves), no lane read back. For non-negative
+// floats the keys are their bits (the order is the same).
+__device__ inline int wave_max_all_i(int v) {
+    // (every lane's source is a lane of its own row: no bound is hit; each step becomes one v_max_i32_dpp)
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true));    // quad_perm [1, 0, 3, 2]
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true));    // quad_perm [2, 3, 0, 1]
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true));   // row_half_mirror
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true));   // row_mirror
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);      // {rows 0 0 2 2, rows 1 1 3 3}
+    v = max(static_cast<int>(r[0]), static_cast<int>(r[1]));
+    const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);      // {low half twice, high half twice}
+    return max(static_cast<int>(h[0]), static_cast<int>(h[1]));
+}
+
 __device__ inline float wave_max(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));

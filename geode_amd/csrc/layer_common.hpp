@@ -61,7 +61,8 @@ inline size_t attn_lds(int hd) { return (static_cast<size_t>(kAttnBlock) * attn_
 // so, their order (the picks) not at all. live[r] false: row r is skipped (its outputs untouched).
 template <int NR>
 __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&live)[NR], int E, int K,
-                                  int *const (&ids)[NR], float *const (&w)[NR], float *const (&gate)[NR]) {
+                                  int *const (&ids)[NR], float *const (&w)[NR], float *const (&gate)[NR],
+                                  bool keep = true) {
     const int lane = threadIdx.x & 63;
     float pv[NR][4], sum[NR], raw[NR][4], lge[NR];
     // every logit up front (indices clamped, no branch around a load), the shared expert's gate logit too
@@ -100,21 +101,27 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
         }
     trace(GV_K_ROUTE, 6);
     float top[NR], mine[NR];
+    int key[NR][4];   // the probabilities' bits (non-negative: ordered as ints); taken and past E: -1.0f's (negative)
 #pragma unroll
-    for (int r = 0; r < NR; ++r) top[r] = mine[r] = 0.0f;
+    for (int r = 0; r < NR; ++r) {
+        top[r] = mine[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) key[r][i] = __float_as_int(pv[r][i]);
+    }
     for (int k = 0; k < K; ++k) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            const float bv = wave_max(fmaxf(fmaxf(pv[r][0], pv[r][1]), fmaxf(pv[r][2], pv[r][3])));
-            int bi = E;
+            const int bk = wave_max_all_i(max(max(key[r][0], key[r][1]), max(key[r][2], key[r][3])));
+            const float bv = __int_as_float(bk);
+            int bi = E;   // the lowest index holding it: slot i first, then the lane
 #pragma unroll
             for (int i = 3; i >= 0; --i) {
-                const uint64_t hit = __ballot(pv[r][i] == bv);
+                const uint64_t hit = __ballot(key[r][i] == bk);
                 if (hit) bi = 64 * i + __builtin_ctzll(hit);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i == bi) pv[r][i] = -1.0f;   // taken
+                if (lane + 64 * i == bi) key[r][i] = __float_as_int(-1.0f);   // taken
             if (lane == k) mine[r] = bv;
             if (lane == 0 && live[r]) ids[r][k] = bi;
             top[r] = __fadd_rn(top[r], bv);   // rank order
@@ -123,7 +130,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
     trace(GV_K_ROUTE, 7);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (!live[r]) continue;
+        if (!live[r] || !keep) continue;   // (keep false: the ids alone)
         if (lane < K) w[r][lane] = __fdiv_rn(mine[r], top[r]);
         if (lane == 0) *gate[r] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lge[r])));
     }
@@ -151,21 +158,26 @@ struct RouteLds {
     int (*wtot)[16];
 };
 
-__device__ inline void route_all(const float *__restrict__ logits, int E, int K, int M, RouteState *__restrict__ rs,
-                                 int32_t *__restrict__ ids_out, const RouteLds &r) {
+// The route's part every caller shares (the whole workgroup calls it): the rows' top-K into r.ids (route_rows; the
+// weights and the shared gate to weight [M][K] / gate [M] when not null), each expert's pick count and row mask, then
+// the exclusive scans: r.start[e] (its first pick), r.slot_of[e] (its first slot, -1: none), and the slot and pick
+// totals in r.wtot[0][15] / r.wtot[1][15]. Every result is the same whatever the timing (counts, masks and scans).
+__device__ inline void route_core(const float *__restrict__ logits, int E, int K, int M, float *weight, float *gate,
+                                  const RouteLds &r) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
     const int E1 = E + 1;
     trace(GV_K_ROUTE, 0);
     for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
+    float wdummy[1], gdummy[1];   // (weights not kept: written to registers that go nowhere)
     if (M < 2 * waves) {   // a row a wave (the first M - waves waves a second one after it: a pair in every wave
                            // would run the second row's instructions, masked, in all of them)
         for (int t0 = wave; t0 < M; t0 += waves) {
             const float *const lg[1] = {logits + static_cast<int64_t>(t0) * E1};
             const bool live[1] = {true};
             int *const ids[1] = {&r.ids[t0 * 16]};
-            float *const w[1] = {rs->weight + t0 * K};
-            float *const gate[1] = {rs->gate + t0};
-            route_rows<1>(lg, live, E, K, ids, w, gate);
+            float *const w[1] = {weight ? weight + t0 * K : wdummy};
+            float *const g[1] = {gate ? gate + t0 : gdummy};
+            route_rows<1>(lg, live, E, K, ids, w, g, weight != nullptr);
         }
     } else {
         for (int t0 = wave; t0 < M; t0 += 2 * waves) {   // rows t0 and t0 + waves
@@ -176,16 +188,15 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
                                         logits + static_cast<int64_t>(t1c) * E1};
             const bool live[2] = {true, l1};
             int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
-            float *const w[2] = {rs->weight + t0 * K, rs->weight + t1c * K};
-            float *const gate[2] = {rs->gate + t0, rs->gate + t1c};
-            route_rows<2>(lg, live, E, K, ids, w, gate);
+            float *const w[2] = {weight ? weight + t0 * K : wdummy, weight ? weight + t1c * K : wdummy};
+            float *const g[2] = {gate ? gate + t0 : gdummy, gate ? gate + t1c : gdummy};
+            route_rows<2>(lg, live, E, K, ids, w, g, weight != nullptr);
         }
     }
     __syncthreads();
     trace(GV_K_ROUTE, 1);
     for (int i = tid; i < M * K; i += blockDim.x) {
         const int t = i / K, e = r.ids[t * 16 + i % K];
-        ids_out[i] = e;
         atomicAdd(&r.cnt[e], 1);
         atomicOr(&r.rows[e], 1u << t);
     }
@@ -205,16 +216,27 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         if (e0 <= E) {
             r.start[e0] = xc;
             r.slot_of[e0] = u0 ? xu : -1;   // the expert's first slot
-            if (e0 == E) rs->n_slots = xu + u0, rs->n_picks = xc + c0;
         }
         if (e1 <= E) {
             r.start[e1] = xc + c0;
             r.slot_of[e1] = u1 ? xu + u0 : -1;
-            if (e1 == E) rs->n_slots = xu + u0 + u1, rs->n_picks = xc + c0 + c1;
+        }
+        __syncthreads();   // (every wave has read the totals)
+        if (e0 == E || e1 == E) {   // the totals, for the callers
+            r.wtot[1][15] = xu + u0 + (e1 == E ? u1 : 0);
+            r.wtot[0][15] = xc + c0 + (e1 == E ? c1 : 0);
         }
     }
     __syncthreads();
     trace(GV_K_ROUTE, 3);
+}
+
+// The slot tables of the route in LDS (route_core's) written to the route state, with the ids (route_all's tail)
+__device__ inline void route_tables(int E, int K, int M, RouteState *__restrict__ rs, int32_t *__restrict__ ids_out,
+                                    const RouteLds &r) {
+    const int tid = threadIdx.x;
+    if (tid == 0) rs->n_slots = r.wtot[1][15], rs->n_picks = r.wtot[0][15];
+    for (int i = tid; i < M * K; i += blockDim.x) ids_out[i] = r.ids[(i / K) * 16 + i % K];
     for (int e = tid; e <= E; e += blockDim.x)
         if (r.slot_of[e] >= 0)
             for (int k = 0; k * kSlotRows < r.cnt[e]; ++k) {
@@ -244,6 +266,46 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
         }
     }
     trace(GV_K_ROUTE, 4);
+}
+
+// The route of the step's rows (route_rows, two rows a wave); then the slots and their picks ordered by (expert,
+// token, rank), each pick placed by counting (the rows before it that picked the same expert: a bit mask per expert),
+// so the order never depends on timing. A slot is a run of at most kSlotRows picks of one expert: the distinct
+// experts ascending, the shared one last (index E), an expert with more picks taking consecutive slots. The whole
+// workgroup (blockDim a multiple of 64, at least 256) calls this; LDS: ids [M][16], cnt / start / slot_of / rows
+// [E + 1], wtot [2][16].
+__device__ inline void route_all(const float *__restrict__ logits, int E, int K, int M, RouteState *__restrict__ rs,
+                                 int32_t *__restrict__ ids_out, const RouteLds &r) {
+    route_core(logits, E, K, M, rs->weight, rs->gate, r);
+    route_tables(E, K, M, rs, ids_out, r);
+}
+
+// Slot u of the route in LDS (route_core's): its expert, first pick, pick count and the row of pick j of the slot
+// (past the count: the slot's first pick's row), as route_tables writes them; false when u is past the slots. The
+// whole workgroup calls it (one barrier); sel: two ints of LDS.
+__device__ inline bool route_slot(const RouteLds &r, int E, int u, int j, int *sel, int &e, int &start, int &cnt,
+                                  int &tok) {
+    if (threadIdx.x == 0) sel[0] = -1;
+    __syncthreads();
+    for (int x = threadIdx.x; x <= E; x += blockDim.x)
+        if (r.slot_of[x] >= 0 && u >= r.slot_of[x] && (u - r.slot_of[x]) * kSlotRows < r.cnt[x])
+            sel[0] = x, sel[1] = u - r.slot_of[x];
+    __syncthreads();
+    e = sel[0];
+    if (e < 0) return false;
+    const int k = sel[1];
+    start = r.start[e] + k * kSlotRows;
+    cnt = min(kSlotRows, r.cnt[e] - k * kSlotRows);
+    const int jj = j < cnt ? j : 0;
+    const int nth = k * kSlotRows + jj;   // the pick's index among the expert's picks: its row's rank among the rows
+    if (e == E) {
+        tok = nth;   // (the shared expert: every row, in order)
+    } else {
+        uint32_t m = r.rows[e];
+        for (int i = 0; i < nth; ++i) m &= m - 1u;   // drop the lowest set bits
+        tok = __builtin_ctz(m);
+    }
+    return true;
 }
 
 // The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A

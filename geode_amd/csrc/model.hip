@@ -271,18 +271,37 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
         const bool qvalid = qi < NQ;
         const int tq = qvalid ? qi / group : 0, hq = kh * group + (qvalid ? qi % group : 0);
         const uint32_t vis = qvalid ? (qt == wave ? vis_first : vis_of(qt)) : 0u;
-        // the four 16-position tiles' scores, hi and lo products apart: eight independent MFMA chains
+        // the four 16-position tiles' scores, hi and lo products apart: eight independent MFMA chains. The keys'
+        // operands come from LDS a group of KG chunks at a time, the next group's reads issued before the current
+        // group's products (double-buffered), so that no product waits for a read issued just before it
+        constexpr int KG = 2, NKG = (NCH + KG - 1) / KG;
         float4v ch_[4], cl_[4];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) ch_[pt] = cl_[pt] = float4v{0, 0, 0, 0};
+        half8 kb[2][KG][4];
+        auto load_k = [&](int g, half8 (&dst)[KG][4]) {
 #pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) {
+            for (int c = 0; c < KG; ++c)
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-                const half8 a = *reinterpret_cast<const half8 *>(ks + (pt * 16 + lq) * kld + 8 * lg + ch * 32);
-                ch_[pt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ch], ch_[pt], 0, 0, 0);
-                cl_[pt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ch], cl_[pt], 0, 0, 0);
-            }
+                for (int pt = 0; pt < 4; ++pt)
+                    if (g * KG + c < NCH)   // (compile time: the loops are unrolled)
+                        dst[c][pt] = *reinterpret_cast<const half8 *>(ks + (pt * 16 + lq) * kld + 8 * lg + (g * KG + c) * 32);
+        };
+        load_k(0, kb[0]);
+#pragma unroll
+        for (int g = 0; g < NKG; ++g) {
+            if (g + 1 < NKG) load_k(g + 1, kb[(g + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < KG; ++c)
+#pragma unroll
+                for (int pt = 0; pt < 4; ++pt) {
+                    const int ch = g * KG + c;
+                    if (ch >= NCH) break;
+                    ch_[pt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[g & 1][c][pt], qb[ch], ch_[pt], 0, 0, 0);
+                    cl_[pt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[g & 1][c][pt], ql[ch], cl_[pt], 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
         }
         float sc[4][4];
         float mx = -__builtin_inff();
@@ -328,8 +347,27 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
             }
         float *dst = parts + ((static_cast<int64_t>(tq) * nh + hq) * nb_max + b) * (hd + 2);
         constexpr int NDT = hd / 16;   // 16-dim tiles of the head (2 NCH: not always a multiple of four)
+        constexpr int NVG = (NDT + 3) / 4;
+        // the values' operands of four 16-dim tiles (both 32-position chunks), read a group ahead like the keys'
+        half8 vb[2][2][4];
+        auto load_v = [&](int vg, half8 (&dstv)[2][4]) {
 #pragma unroll
-        for (int dt0 = 0; dt0 < NDT; dt0 += 4) {   // four 16-dim tiles at a time, hi and lo apart
+            for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (4 * vg + k < NDT) {   // (compile time)
+                        const _Float16 *vrow = vs + ((4 * vg + k) * 16 + lq) * kAttnVld;
+                        const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
+                        const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
+                        dstv[kc][k] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    }
+        };
+        load_v(0, vb[0]);
+#pragma unroll
+        for (int vg = 0; vg < NVG; ++vg) {   // four 16-dim tiles at a time, hi and lo apart
+            const int dt0 = 4 * vg;
+            if (vg + 1 < NVG) load_v(vg + 1, vb[(vg + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
             float4v oh[4], ol[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) oh[k] = ol[k] = float4v{0, 0, 0, 0};
@@ -338,12 +376,8 @@ __global__ __launch_bounds__(256) void attn_block_kernel(const _Float16 *__restr
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     if (dt0 + k >= NDT) break;   // (compile time: the loops are unrolled)
-                    const _Float16 *vrow = vs + ((dt0 + k) * 16 + lq) * kAttnVld;
-                    const half4 lo = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 4 * lg);
-                    const half4 hi = *reinterpret_cast<const half4 *>(vrow + kc * 32 + 16 + 4 * lg);
-                    const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    oh[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[kc], oh[k], 0, 0, 0);
-                    ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pbl[kc], ol[k], 0, 0, 0);
+                    oh[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[vg & 1][kc][k], pb[kc], oh[k], 0, 0, 0);
+                    ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[vg & 1][kc][k], pbl[kc], ol[k], 0, 0, 0);
                 }
             // O^T[dim dt*16 + 4 lg + r][query lq]
             if (qvalid)
@@ -686,6 +720,8 @@ struct MixOutArgs {
     int *ctr;                   // flags: [0, n_o) a projection workgroup done, [n_o, n_o + n_r) a router workgroup
     int *err;
     int n_o, n_r;
+    int route_role;             // 1: the launch's last workgroup routes; 0: the experts' up launch routes the rows
+                                // itself (and clears these flags)
 };
 
 template <int KW>
@@ -872,7 +908,7 @@ __global__ __launch_bounds__(512) void mixout_kernel(const MixOutArgs a) {
     const int b = blockIdx.x;
     if (b < a.n_o) mixout_o<KW>(a, b, reinterpret_cast<f4 *>(mix_lds), tab);
     else if (b < a.n_o + a.n_r) mixout_router(a, b - a.n_o, reinterpret_cast<float *>(mix_lds), red);
-    else mixout_route(a, reinterpret_cast<float *>(mix_lds));
+    else if (a.route_role) mixout_route(a, reinterpret_cast<float *>(mix_lds));
 }
 
 // The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
@@ -935,6 +971,16 @@ struct MoeArgsDec {
     float *y;                             // [pick][H]
     Slots sl;
     int groups, E1, max_picks;
+    // the route made by the up launch itself (moe_up_kernel<KWU, true>): the rows' router logits [M][E1], the route
+    // state its workgroup 0 writes for the launches after it, the routed ids out, and the previous launch's flags
+    // (the fused output projection / router's) that workgroup 0 clears for the next step
+    const float *logits;
+    int E, K;
+    RouteState *rs;
+    int32_t *ids_out;
+    const StepParams *sp;
+    int *flags;
+    int n_flags;
 };
 
 // the slot of this workgroup (blockIdx / groups) and its expert, first pick and pick count, and the lane's pick's
@@ -948,14 +994,34 @@ __device__ inline bool moe_slot(const MoeArgsDec &a, int u, int &e, int &start, 
            tok >= 0 && tok < kMaxRows;
 }
 
-template <int KWU>
+// ROUTE: the launch routes the rows itself (at most kMaxRowsMixOut of them): every workgroup runs the route on the
+// router's logits into its LDS (route_core: the same ids, counts and scans whichever workgroup runs it) and takes its
+// slot from there, so that no route launch or hand-off sits between the router and the experts; workgroup 0 also
+// writes the route state (the down products, the combine and the ids read it after this launch) and clears the
+// router launch's flags. Otherwise the slot comes from the route state the route launch wrote.
+template <int KWU, bool ROUTE>
 __global__ __launch_bounds__(512) void moe_up_kernel(const MoeArgsDec a) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
     trace(GV_K_MOE_UP, 0);
     const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
     int e, start, cnt, tok;
-    if (!__builtin_amdgcn_readfirstlane(moe_slot(a, u, e, start, cnt, tok))) return;
+    if constexpr (ROUTE) {
+        __shared__ int r_ids[kMaxRowsMixOut * 16], r_cnt[260], r_start[260], r_slot[260], r_sel[2];
+        __shared__ unsigned r_rows[260];
+        __shared__ int r_wtot[2][16];
+        const RouteLds r{r_ids, r_cnt, r_start, r_slot, r_rows, r_wtot};
+        const bool writer = blockIdx.x == 0;
+        const int M = a.sp->M;
+        route_core(a.logits, a.E, a.K, M, writer ? a.rs->weight : nullptr, writer ? a.rs->gate : nullptr, r);
+        if (writer) {
+            route_tables(a.E, a.K, M, a.rs, a.ids_out, r);
+            clear_flags(a.flags, a.n_flags);   // (every workgroup of the router's launch is done: it came before)
+        }
+        if (!route_slot(r, a.E, u, (threadIdx.x % 64) % 8, r_sel, e, start, cnt, tok)) return;
+    } else {
+        if (!__builtin_amdgcn_readfirstlane(moe_slot(a, u, e, start, cnt, tok))) return;
+    }
     trace(GV_K_MOE_UP, 4);
     const int F = a.F, W = blockDim.x / 64, lane = threadIdx.x % 64;
     const int64_t act_m_stride = act_halves(F);
@@ -1174,6 +1240,13 @@ inline bool mixout_fits(const Model &m, int M, int64_t o_cols, int &kw) {
     return kw == 16 || kw == 8 || kw == 4;
 }
 
+// the flags of the fused output projection / router launch: its projection workgroups' and its router workgroups'
+inline int mixout_flags(const Model &m) {
+    const int64_t ntiles = tiles_rows(m.c.hidden);
+    const int64_t per = tiles_per_wg(ntiles, 8, 1);
+    return static_cast<int>((ntiles + per - 1) / per) + (m.E1 + 3) / 4;
+}
+
 inline size_t mixout_lds(int M, int E1, int o_per) {
     const size_t router = static_cast<size_t>(M + 4) * 8 * kRT * 4;
     const size_t route = (static_cast<size_t>(M) * E1 + kMaxRows * 16 + 4 * 260) * 4;
@@ -1351,9 +1424,24 @@ bool moe_dec_shape(const gv_model_config &c, int &kwu, int &kwd, int &waves) {
     return (kwu == 16 && kwd == 16) || (kwu == 4 && kwd == 4);
 }
 
-int moe_dec(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
+// the decode up launch's threads (moe_dec's choice below)
+int moe_up_threads(const gv_model_config &c) {
+    int kwu, kwd, waves;
+    if (!moe_dec_shape(c, kwu, kwd, waves)) return 0;
+    return kwu == 16 && waves <= 4 ? 128 * waves : 64 * waves;
+}
+
+// whether the experts' up launch after the fused output projection / router launch routes the rows itself (the decode
+// variant, its scan of the E + 1 counters two a thread, not a replay of one launch alone); otherwise the fused launch
+// keeps its route workgroup
+inline bool up_routes(const Model &m, bool mixout) {
+    return mixout && m.route_in_up && m.moe_dec && !m.replaying && 2 * moe_up_threads(m.c) >= m.E1;
+}
+
+int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStream_t st) {
     int kwu, kwd, waves;
     GV_REQUIRE(moe_dec_shape(m.c, kwu, kwd, waves), "moe: no decode variant for this shape");
+    GV_REQUIRE(!route || (up && M <= kMaxRowsMixOut), "moe: the up launch routes at most kMaxRowsMixOut rows");
     MoeArgsDec a{};
     a.gu_codes = L.gu_codes, a.gu_scales = L.gu_scales, a.dn_codes = L.dn_codes, a.dn_scales = L.dn_scales;
     a.gu_cstride = m.gu_code_stride, a.gu_sstride = m.gu_scale_stride;
@@ -1363,19 +1451,32 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, hipStream_t st) {
     a.act = m.act_h, a.act_stride = act_halves(m.c.hidden);
     a.act_m = m.act_m;
     a.y = m.y;
-    a.sl = route_slots(m.route + (&L - &m.layers[0]));
+    const int64_t l = &L - &m.layers[0];
+    a.sl = route_slots(m.route + l);
     a.E1 = m.E1, a.max_picks = m.max_picks;
+    a.logits = m.rlogits, a.E = m.c.n_experts, a.K = m.c.top_k;
+    a.rs = m.route + l;
+    a.ids_out = m.route_ids + l * m.c.max_rows * m.c.top_k;
+    a.sp = m.sp;
+    a.flags = m.ctr + l * kFlagsPerLayer;
+    a.n_flags = mixout_flags(m);
     const int slots = moe_slots(m, M);
     if (up) {
         a.groups = (a.F / kTileR + kMoePairs - 1) / kMoePairs;
         const dim3 grid(static_cast<unsigned>(slots * a.groups));
         if (kwu == 16 && waves <= 4) {   // eight waves, each half the K range
             const size_t lds = static_cast<size_t>(2 * kMoePairs) * (2 * waves) * 1024;
-            hipLaunchKernelGGL(moe_up_kernel<8>, grid, dim3(128 * waves), lds, st, a);
+            if (route) hipLaunchKernelGGL((moe_up_kernel<8, true>), grid, dim3(128 * waves), lds, st, a);
+            else hipLaunchKernelGGL((moe_up_kernel<8, false>), grid, dim3(128 * waves), lds, st, a);
         } else {
             const size_t lds = static_cast<size_t>(2 * kMoePairs) * waves * 1024;
-            if (kwu == 16) hipLaunchKernelGGL(moe_up_kernel<16>, grid, dim3(64 * waves), lds, st, a);
-            else hipLaunchKernelGGL(moe_up_kernel<4>, grid, dim3(64 * waves), lds, st, a);
+            if (kwu == 16) {
+                if (route) hipLaunchKernelGGL((moe_up_kernel<16, true>), grid, dim3(64 * waves), lds, st, a);
+                else hipLaunchKernelGGL((moe_up_kernel<16, false>), grid, dim3(64 * waves), lds, st, a);
+            } else {
+                if (route) hipLaunchKernelGGL((moe_up_kernel<4, true>), grid, dim3(64 * waves), lds, st, a);
+                else hipLaunchKernelGGL((moe_up_kernel<4, false>), grid, dim3(64 * waves), lds, st, a);
+            }
         }
     } else {
         a.groups = (a.H / kTileR + waves * kMoeDnTiles - 1) / (waves * kMoeDnTiles);
@@ -1635,11 +1736,16 @@ int launch_mixout_t(Model &m, LayerW &L, int l, int M, hipStream_t st) {
     a.err = m.err;
     a.n_o = static_cast<int>((ntiles + a.o_per - 1) / a.o_per);
     a.n_r = (m.E1 + 3) / 4;
+    // (the decode experts' up launch routes the rows itself and clears this launch's flags; a replay of this launch
+    // alone keeps its own route workgroup, which clears them)
+    a.route_role = up_routes(m, true) ? 0 : 1;
     GV_REQUIRE(a.n_o + a.n_r <= kGdnFlagBase, "mixout: more flags than the launch's share of the layer's");
+    GV_REQUIRE(a.n_o + a.n_r == mixout_flags(m), "mixout: the flag count differs from the one the up launch clears");
     const size_t lds = mixout_lds(M, m.E1, a.o_per);
     static int granted = 0;
     if (lds_grant(reinterpret_cast<const void *>(&mixout_kernel<KW>), lds, granted) != 0) return -1;
-    hipLaunchKernelGGL(mixout_kernel<KW>, dim3(static_cast<unsigned>(a.n_o + a.n_r + 1)), dim3(512), lds, st, a);
+    hipLaunchKernelGGL(mixout_kernel<KW>, dim3(static_cast<unsigned>(a.n_o + a.n_r + a.route_role)), dim3(512), lds,
+                       st, a);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -1758,15 +1864,17 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         hipLaunchKernelGGL(route_kernel, dim3(1), dim3(1024), 0, st, m.rlogits, c.n_experts, c.top_k, m.sp, m.route + l,
                            m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k);
         return 0;
-    case GV_K_MOE_UP:   // with the SwiGLU and its quantization (moe_up_kernel) where the decode variant fits
-        return m.moe_dec ? moe_dec(m, L, M, true, st) : moe_products(m, L, M, true, st);
+    case GV_K_MOE_UP:   // with the SwiGLU and its quantization (moe_up_kernel) where the decode variant fits; after
+                        // the fused output projection / router launch it also routes the rows
+        // (a replay of this launch alone: the slots the step's own route left in the layer's route state)
+        return m.moe_dec ? moe_dec(m, L, M, true, up_routes(m, mixout), st) : moe_products(m, L, M, true, st);
     case GV_K_SWIGLU:
         if (m.moe_dec) return 0;
         hipLaunchKernelGGL(swiglu_quant_kernel, dim3(M * (c.top_k + 1)), dim3(256), static_cast<size_t>(c.moe_ff) * 4,
                            st, m.gu_out, c.moe_ff, &m.route[l].n_picks, m.act_m);
         return 0;
     case GV_K_MOE_DOWN:
-        return m.moe_dec ? moe_dec(m, L, M, false, st) : moe_products(m, L, M, false, st);
+        return m.moe_dec ? moe_dec(m, L, M, false, false, st) : moe_products(m, L, M, false, st);
     case GV_K_COMBINE: {   // the residual add, then the next layer's input RMSNorm (after the last: the final norm;
                            // after the MTP layer: mtp.norm)
         const bool mtp_layer = l == c.n_layers;
@@ -2664,6 +2772,11 @@ int gv_model_replay(gv_model *g, int cls, int layer, int reps, float *ms_per_lau
         if (!(gdn_cls && !gdn) && !(attn_cls && gdn)) on.push_back(l);
     }
     GV_REQUIRE(!on.empty(), "gv_model_replay: no layer has this kernel class");
+    m.replaying = true;
+    struct Done {   // (however this ends)
+        Model &m;
+        ~Done() { m.replaying = false; }
+    } done{m};
     if (launch_class(m, cls, on[0], m.last_n, st) != 0) return -1;   // warm
     hipEvent_t e0, e1;
     GV_CHECK_HIP(hipEventCreate(&e0));
@@ -2871,7 +2984,9 @@ int gv_model_set_fused(gv_model *g, int on) {
     GV_REQUIRE(g, "gv_model_set_fused: null model");
     Model &m = g->m;
     GV_CHECK_HIP(hipStreamSynchronize(stream()));
+    GV_REQUIRE(on >= 0 && on <= 2, "gv_model_set_fused: 0, 1 or 2");
     m.fused = on != 0;
+    m.route_in_up = on == 1;
     for (auto &ge : m.graphs)   // the graphs hold the other launches: captured again on the next steps
         if (ge) {
             (void)hipGraphExecDestroy(ge);

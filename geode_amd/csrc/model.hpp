@@ -132,6 +132,7 @@ struct Model {
     int *counter = nullptr;        // the router's finished-workgroup count (zero between launches)
     bool moe_dec = false;          // the decode MoE kernels (moe_up_kernel, moe_down_kernel), where the shapes fit
     bool fused = true;             // dependent phases chained within one launch where the shapes fit (gv_model_set_fused)
+    bool route_in_up = true;       // (fused) the experts' up launch routes the rows itself (gv_model_set_fused 2: off)
     bool router_shared_only = false;   // the MoE block's router launch with the routed logits given (gv_model_moe)
     int *ctr = nullptr;            // [n_layers][kFlagsPerLayer] the fused launches' flags (each launch clears its own)
     int *err = nullptr;            // set by a fused launch whose wait ran out (read back by gv_verify)
@@ -163,6 +164,7 @@ struct Model {
     StepParams *sp_mtp = nullptr;
     StepParams host_sp_mtp{};
     int mtp_last_n = 0;           // rows of the last MTP pass with logits (0: none yet)
+    bool replaying = false;       // gv_model_replay's launches: each fused launch clears its own flags
     Q4 draft_head;                // lm_head's rows of the draft vocabulary (rows 0: the whole vocabulary)
     int32_t *draft_ids = nullptr; // device [draft_head.rows]
     uint8_t *draft_mem = nullptr;

@@ -208,7 +208,9 @@ enum {
 int gv_model_set_graphs(gv_model *m, int on);
 /* on (the default): dependent phases of a layer chained within one launch where the shapes fit (the output
  * projection, the post-attention RMSNorm + router and the route: workgroups of each phase wait for the previous
- * phase's counter instead of a kernel boundary); off: one launch a phase. The same results bit for bit (no reference
+ * phase's counter instead of a kernel boundary), and the experts' up launch routing the rows itself (no route
+ * launch or hand-off between the router and the experts); 2: the same but with the route as the last phase of the
+ * output projection's launch (a measurement aid); 0: one launch a phase. The same results bit for bit (no reference
  * counterpart). */
 int gv_model_set_fused(gv_model *m, int on);
 /* A measurement aid with no reference counterpart: with on = 1, thread 0 of every workgroup of the traced kernels

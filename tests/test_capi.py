@@ -61,3 +61,16 @@ def test_sampler_refuses_a_vocabulary_past_its_chunk_table():
     for name, rc in rcs.items():
         assert rc == -1, name
     assert "262,144" in lib.gv_last_error().decode()
+
+
+def test_library_leaves_none_of_its_own_symbols_undefined():
+    """every function of the library's own namespace is defined in it (a declaration without a definition in the
+    same namespace would surface only when a GPU call reaches it)"""
+    import subprocess
+
+    import geode_amd
+
+    out = subprocess.run(["nm", "-D", "--undefined-only", geode_amd.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    own = [line.split()[-1] for line in out.splitlines() if "_ZN2gv" in line or " gv_" in line]
+    assert not own, f"undefined: {own}"

@@ -79,10 +79,12 @@ def test_repeated_steps_identical(models):
         assert np.array_equal(again.view(np.uint32), first.view(np.uint32))
 
 
+@pytest.mark.parametrize("level", [1, 2])
 @pytest.mark.parametrize("tree", [False, True])
-def test_fused_launches_match_separate_kernels(models, tree):
-    """the dependent phases chained within one launch (the default where the shapes fit) against one launch a phase:
-    the same arithmetic in the same order, so the same bits; several steps in a row (graph replays after the second)"""
+def test_fused_launches_match_separate_kernels(models, tree, level):
+    """the dependent phases chained within one launch (the default where the shapes fit; level 1: the rows routed by
+    the experts' up launch, 2: by the output projection's launch) against one launch a phase: the same arithmetic in
+    the same order, so the same bits; several steps in a row (graph replays after the second)"""
     om, gm = models
     parents = tree_parents((4, 3)) if tree else None
     n = 17 if tree else 5
@@ -91,9 +93,12 @@ def test_fused_launches_match_separate_kernels(models, tree):
     gm.position = CTX
     want = gm.verify(toks, parents=parents)
     want_ids = gm.route_ids(n)
-    gm.set_fused(True)
-    for _ in range(5):
-        gm.position = CTX
-        got = gm.verify(toks, parents=parents)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-        assert np.array_equal(gm.route_ids(n), want_ids)
+    gm.set_fused(level)
+    try:
+        for _ in range(5):
+            gm.position = CTX
+            got = gm.verify(toks, parents=parents)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+            assert np.array_equal(gm.route_ids(n), want_ids)
+    finally:
+        gm.set_fused(True)
