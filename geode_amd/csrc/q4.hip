@@ -221,7 +221,9 @@ int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm
 // ---------------------------------------------------------------- the skinny GEMM (mfma_gemv.hpp)
 // WMAX: the most waves a launch of the instance takes (8: a budget of 256 VGPRs a lane)
 // PACK: at most 8 rows, their hi and lo halves in the MFMA's two column halves (mfma_tiles)
-template <int KW, int NTT, int WMAX, bool PACK>
+// NT > 0 (a launch of at most NT tiles a workgroup): the tile loop straight-line, every tile's loads issued before
+// the first tile is computed (NT <= the ring's depth); 0: the ring of three over any number of tiles
+template <int KW, int NTT, int WMAX, bool PACK, int NT = 0>
 __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16 *__restrict__ act,
                                                             int64_t act_stride, int M, int sc0, int tiles_per_wg,
                                                             GemvOut out) {
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
 #pragma unroll
         for (int r = 0; r < 4; ++r) old[r] = p[min(row0 + r, w.rows - 1)];   // (clamped: always a valid address)
     };
-    mfma_tiles<KW, NTT, kKeepParts, 0, 3, PACK>(
+    mfma_tiles<KW, NTT, kKeepParts, NT, (NT > 0 ? NT : 3), PACK>(
         w.codes, w.scales, w.rows, static_cast<int>(w.cols / kSuperK), sc0, nt, M,
         [&](int j) { return act + j * act_stride; }, [](int64_t, int, float) {}, part_lds, tab, TileRun{t0}, prefetch,
         [&] { if (tc >= 0) trace(tc, 5); });
@@ -461,6 +463,15 @@ static int launch_gemv(const Q4 &w, const _Float16 *act, int64_t act_stride, int
     }
     const int64_t wg = (ntiles + per - 1) / per;
     const size_t lds = static_cast<size_t>(per) * waves * NTT * 1024;   // the waves' partial sums
+    if (per <= 3 && per > 1) {   // a few tiles a workgroup (q|k|v): all of them in flight at once
+        static int granted3 = 0;
+        if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX, PACK, 3>), 76 * 1024, granted3) != 0)
+            return -1;
+        hipLaunchKernelGGL((gemv_q4_kernel<KW, NTT, WMAX, PACK, 3>), dim3(static_cast<unsigned>(wg)), dim3(64 * waves),
+                           static_cast<size_t>(3) * waves * NTT * 1024, st, w, act, act_stride, M, sc0,
+                           static_cast<int>(per), out);
+        return 0;
+    }
     static int granted = 0;
     if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<KW, NTT, WMAX, PACK>), 76 * 1024, granted) != 0)
         return -1;
