@@ -251,7 +251,6 @@ __device__ inline int wave_incl_scan(int v) {
     return v;
 }
 
-// the maximum over the wave's 64 lanes, a uniform value
 // The wave's largest of int keys, in every lane: four DPP steps within each 16-lane row (pairs, quads, eights,
 // sixteens), then gfx950's row swaps (rows 0 <-> 1 and 2 <-> 3, then the halves), no lane read back. For non-negative
 // floats the keys are their bits (the order is the same).
@@ -267,6 +266,15 @@ __device__ inline int wave_max_all_i(int v) {
     return max(static_cast<int>(h[0]), static_cast<int>(h[1]));
 }
 
+// the largest float over the wave's 64 lanes, in every lane (signed floats as order-preserving int keys: a negative
+// value's magnitude bits flipped)
+__device__ inline float wave_max_all_f(float v) {
+    const int b = __float_as_int(v);
+    const int k = wave_max_all_i(b < 0 ? b ^ 0x7FFFFFFF : b);
+    return __int_as_float(k < 0 ? k ^ 0x7FFFFFFF : k);
+}
+
+// the maximum over the wave's 64 lanes, a uniform value
 __device__ inline float wave_max(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));

@@ -84,7 +84,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
             mx = fmaxf(mx, v[i]);
         }
         if (r == 0) trace(GV_K_ROUTE, 5);
-        mx = wave_max(mx);
+        mx = wave_max_all_f(mx);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = lane + 64 * i;
@@ -280,32 +280,83 @@ __device__ inline void route_all(const float *__restrict__ logits, int E, int K,
     route_tables(E, K, M, rs, ids_out, r);
 }
 
-// Slot u of the route in LDS (route_core's): its expert, first pick, pick count and the row of pick j of the slot
-// (past the count: the slot's first pick's row), as route_tables writes them; false when u is past the slots. The
-// whole workgroup calls it (one barrier); sel: two ints of LDS.
-__device__ inline bool route_slot(const RouteLds &r, int E, int u, int j, int *sel, int &e, int &start, int &cnt,
-                                  int &tok) {
-    if (threadIdx.x == 0) sel[0] = -1;
-    __syncthreads();
-    for (int x = threadIdx.x; x <= E; x += blockDim.x)
-        if (r.slot_of[x] >= 0 && u >= r.slot_of[x] && (u - r.slot_of[x]) * kSlotRows < r.cnt[x])
-            sel[0] = x, sel[1] = u - r.slot_of[x];
-    __syncthreads();
-    e = sel[0];
-    if (e < 0) return false;
-    const int k = sel[1];
-    start = r.start[e] + k * kSlotRows;
-    cnt = min(kSlotRows, r.cnt[e] - k * kSlotRows);
-    const int jj = j < cnt ? j : 0;
-    const int nth = k * kSlotRows + jj;   // the pick's index among the expert's picks: its row's rank among the rows
-    if (e == E) {
-        tok = nth;   // (the shared expert: every row, in order)
+// The route of at most 8 rows of at most 8 picks (M K <= 64, E <= 256) for one workgroup of the experts' up launch:
+// route_core's results in LDS (the same ids, counts, row masks, starts and slot numbers: its top-K branch, then the
+// counts and both scans by one wave, an expert's count being at most M <= kSlotRows so one slot at most), and slot
+// u's expert, first pick, pick count and row mask in sel[0..3] (sel[0] = -1: u is past the slots). Two barriers.
+__device__ inline void route_small(const float *__restrict__ logits, int E, int K, int M, float *weight, float *gate,
+                                   const RouteLds &r, int u, int *sel) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    const int E1 = E + 1;
+    trace(GV_K_ROUTE, 0);
+    for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
+    float wdummy[1], gdummy[1];
+    if (M < 2 * waves) {   // (route_core's branches: the same rows on the same arithmetic)
+        for (int t0 = wave; t0 < M; t0 += waves) {
+            const float *const lg[1] = {logits + static_cast<int64_t>(t0) * E1};
+            const bool live[1] = {true};
+            int *const ids[1] = {&r.ids[t0 * 16]};
+            float *const w[1] = {weight ? weight + t0 * K : wdummy};
+            float *const g[1] = {gate ? gate + t0 : gdummy};
+            route_rows<1>(lg, live, E, K, ids, w, g, weight != nullptr);
+        }
     } else {
-        uint32_t m = r.rows[e];
-        for (int i = 0; i < nth; ++i) m &= m - 1u;   // drop the lowest set bits
-        tok = __builtin_ctz(m);
+        for (int t0 = wave; t0 < M; t0 += 2 * waves) {
+            const int t1 = t0 + waves;
+            const bool l1 = t1 < M;
+            const int t1c = l1 ? t1 : t0;
+            const float *const lg[2] = {logits + static_cast<int64_t>(t0) * E1,
+                                        logits + static_cast<int64_t>(t1c) * E1};
+            const bool live[2] = {true, l1};
+            int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
+            float *const w[2] = {weight ? weight + t0 * K : wdummy, weight ? weight + t1c * K : wdummy};
+            float *const g[2] = {gate ? gate + t0 : gdummy, gate ? gate + t1c : gdummy};
+            route_rows<2>(lg, live, E, K, ids, w, g, weight != nullptr);
+        }
     }
-    return true;
+    __syncthreads();
+    trace(GV_K_ROUTE, 1);
+    if (wave == 0) {
+        const int np = M * K;
+        if (lane < np) {   // (one wave's LDS operations complete in order: the reads below see every count)
+            const int t = lane / K, e = r.ids[t * 16 + lane % K];
+            atomicAdd(&r.cnt[e], 1);
+            atomicOr(&r.rows[e], 1u << t);
+        }
+        int c[4], n = 0, s = 0;   // experts 4 lane .. 4 lane + 3: their picks and slots
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            c[j] = e < E ? r.cnt[e] : 0;
+            n += c[j];
+            s += c[j] > 0 ? 1 : 0;
+        }
+        const int is = wave_incl_scan(s), in = wave_incl_scan(n);
+        const int U = __builtin_amdgcn_readlane(is, 63);   // the routed experts' slots (the shared one's is U)
+        int sl = is - s, st = in - n;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            if (e < E) {
+                r.start[e] = st;
+                r.slot_of[e] = c[j] ? sl : -1;
+                if (c[j] && sl == u) sel[0] = e, sel[1] = st, sel[2] = c[j], sel[3] = static_cast<int>(r.rows[e]);
+            }
+            st += c[j];
+            sl += c[j] > 0 ? 1 : 0;
+        }
+        if (lane == 0) {
+            r.cnt[E] = M;
+            r.start[E] = np;
+            r.slot_of[E] = U;
+            r.wtot[0][15] = np + M;   // (the totals, as route_core leaves them)
+            r.wtot[1][15] = U + 1;
+            if (u == U) sel[0] = E, sel[1] = np, sel[2] = M, sel[3] = static_cast<int>((1u << M) - 1u);
+            else if (u > U) sel[0] = -1;
+        }
+    }
+    __syncthreads();
+    trace(GV_K_ROUTE, 3);
 }
 
 // The post-attention RMSNorm (none when norm_w is null: the rows are used as they are) and the router logits. A

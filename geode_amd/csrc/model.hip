@@ -1007,18 +1007,29 @@ __global__ __launch_bounds__(512) void moe_up_kernel(const MoeArgsDec a) {
     const int u = static_cast<int>(blockIdx.x) / a.groups, grp = static_cast<int>(blockIdx.x) % a.groups;
     int e, start, cnt, tok;
     if constexpr (ROUTE) {
-        __shared__ int r_ids[kMaxRowsMixOut * 16], r_cnt[260], r_start[260], r_slot[260], r_sel[2];
+        __shared__ int r_ids[kMaxRowsMixOut * 16], r_cnt[260], r_start[260], r_slot[260], r_sel[4];
         __shared__ unsigned r_rows[260];
         __shared__ int r_wtot[2][16];
         const RouteLds r{r_ids, r_cnt, r_start, r_slot, r_rows, r_wtot};
         const bool writer = blockIdx.x == 0;
         const int M = a.sp->M;
-        route_core(a.logits, a.E, a.K, M, writer ? a.rs->weight : nullptr, writer ? a.rs->gate : nullptr, r);
+        route_small(a.logits, a.E, a.K, M, writer ? a.rs->weight : nullptr, writer ? a.rs->gate : nullptr, r, u,
+                    r_sel);
         if (writer) {
             route_tables(a.E, a.K, M, a.rs, a.ids_out, r);
             clear_flags(a.flags, a.n_flags);   // (every workgroup of the router's launch is done: it came before)
         }
-        if (!route_slot(r, a.E, u, (threadIdx.x % 64) % 8, r_sel, e, start, cnt, tok)) return;
+        e = r_sel[0];
+        if (e < 0) return;   // (uniform: LDS)
+        start = r_sel[1], cnt = r_sel[2];
+        const int j = (threadIdx.x % 64) % 8, nth = j < cnt ? j : 0;   // the lane's pick (past the count: the first)
+        if (e == a.E) {
+            tok = nth;   // (the shared expert: every row, in order)
+        } else {
+            uint32_t mk = static_cast<uint32_t>(r_sel[3]);
+            for (int i = 0; i < nth; ++i) mk &= mk - 1u;   // the nth-lowest set bit: the rows in order
+            tok = __builtin_ctz(mk);
+        }
     } else {
         if (!__builtin_amdgcn_readfirstlane(moe_slot(a, u, e, start, cnt, tok))) return;
     }
@@ -1432,10 +1443,11 @@ int moe_up_threads(const gv_model_config &c) {
 }
 
 // whether the experts' up launch after the fused output projection / router launch routes the rows itself (the decode
-// variant, its scan of the E + 1 counters two a thread, not a replay of one launch alone); otherwise the fused launch
-// keeps its route workgroup
+// variant; route_small's bounds: at most 8 picks a row, 256 experts; not a replay of one launch alone); otherwise the
+// fused launch keeps its route workgroup
 inline bool up_routes(const Model &m, bool mixout) {
-    return mixout && m.route_in_up && m.moe_dec && !m.replaying && 2 * moe_up_threads(m.c) >= m.E1;
+    return mixout && m.route_in_up && m.moe_dec && !m.replaying && m.c.top_k <= 8 && m.c.n_experts <= 256 &&
+           moe_up_threads(m.c) >= 64;
 }
 
 int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStream_t st) {
