@@ -54,11 +54,13 @@ constexpr int kAttnVld = kAttnBlock + 8;                              // halves 
 inline size_t attn_lds(int hd) { return (static_cast<size_t>(kAttnBlock) * attn_k_ld(hd) + hd * kAttnVld) * 2; }
 
 // route_topk (model.cpp:4021-4065) of NR rows by one wave, the rows' dependency chains interleaved: softmax over the
-// E <= 256 experts (max, expf, the sum, divide), the top K by probability with ties to the lower index (a wave max,
-// then ballots), the weights p / (their sum in rank order) to w[r][0..K), the ids to ids[r][0..K) (lane 0), the
-// shared expert's gate sigmoid(lg[E]) to gate[r]. The softmax denominator is a fixed tree (each lane's four values,
-// then the lanes: wave_sum_f), not the reference's index-order loop: the probabilities differ from it by an ulp or
-// so, their order (the picks) not at all. live[r] false: row r is skipped (its outputs untouched).
+// E <= 256 experts (max, expf, the sum, divide), the top K by probability with ties to the lower index, the weights
+// p / (their sum in rank order) to w[r][0..K), the ids to ids[r][0..K) (lane 0), the shared expert's gate
+// sigmoid(lg[E]) to gate[r]. Lane l holds experts 4 l .. 4 l + 3, so a pick is a wave max of the lanes' largest, one
+// ballot (the lowest lane holding it) and that lane's first slot holding it: the lowest index. The softmax
+// denominator is a fixed tree (each lane's four values, then the lanes: wave_sum_f), not the reference's index-order
+// loop: the probabilities differ from it by an ulp or so, their order (the picks) not at all. live[r] false: row r
+// is skipped (its outputs untouched).
 template <int NR>
 __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&live)[NR], int E, int K,
                                   int *const (&ids)[NR], float *const (&w)[NR], float *const (&gate)[NR],
@@ -69,7 +71,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) raw[r][i] = lg[r][min(lane + 64 * i, E - 1)];
+        for (int i = 0; i < 4; ++i) raw[r][i] = lg[r][min(4 * lane + i, E - 1)];
         lge[r] = lg[r][E];
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -79,7 +81,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
         float mx = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
+            const int e = 4 * lane + i;
             v[i] = live[r] && e < E ? raw[r][i] : -__builtin_inff();
             mx = fmaxf(mx, v[i]);
         }
@@ -87,7 +89,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
         mx = wave_max_all_f(mx);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
+            const int e = 4 * lane + i;
             pv[r][i] = live[r] && e < E ? expf(__fsub_rn(v[i], mx)) : 0.0f;
         }
         sum[r] = wave_sum_f(__fadd_rn(__fadd_rn(pv[r][0], pv[r][1]), __fadd_rn(pv[r][2], pv[r][3])));
@@ -96,7 +98,7 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
     for (int r = 0; r < NR; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
+            const int e = 4 * lane + i;
             pv[r][i] = live[r] && e < E ? __fdiv_rn(pv[r][i], sum[r]) : -1.0f;
         }
     trace(GV_K_ROUTE, 6);
@@ -111,17 +113,17 @@ __device__ inline void route_rows(const float *const (&lg)[NR], const bool (&liv
     for (int k = 0; k < K; ++k) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            const int bk = wave_max_all_i(max(max(key[r][0], key[r][1]), max(key[r][2], key[r][3])));
+            const int lm = max(max(key[r][0], key[r][1]), max(key[r][2], key[r][3]));
+            const int bk = wave_max_all_i(lm);
             const float bv = __int_as_float(bk);
-            int bi = E;   // the lowest index holding it: slot i first, then the lane
-#pragma unroll
-            for (int i = 3; i >= 0; --i) {
-                const uint64_t hit = __ballot(key[r][i] == bk);
-                if (hit) bi = 64 * i + __builtin_ctzll(hit);
-            }
+            // the lowest index holding it: the lowest lane (a valid probability is >= 0 > the taken keys, so some
+            // lane holds it), then that lane's first slot
+            const int L = __builtin_ctzll(__ballot(lm == bk));
+            const int li = key[r][0] == bk ? 0 : key[r][1] == bk ? 1 : key[r][2] == bk ? 2 : 3;
+            const int bi = 4 * L + __builtin_amdgcn_readlane(li, L);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i == bi) key[r][i] = __float_as_int(-1.0f);   // taken
+                if (lane == L && li == i) key[r][i] = __float_as_int(-1.0f);   // taken
             if (lane == k) mine[r] = bv;
             if (lane == 0 && live[r]) ids[r][k] = bi;
             top[r] = __fadd_rn(top[r], bv);   // rank order
@@ -168,15 +170,15 @@ __device__ inline void route_core(const float *__restrict__ logits, int E, int K
     const int E1 = E + 1;
     trace(GV_K_ROUTE, 0);
     for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
-    float wdummy[1], gdummy[1];   // (weights not kept: written to registers that go nowhere)
+    // (no weight: route_rows writes the ids alone, never w or g)
     if (M < 2 * waves) {   // a row a wave (the first M - waves waves a second one after it: a pair in every wave
                            // would run the second row's instructions, masked, in all of them)
         for (int t0 = wave; t0 < M; t0 += waves) {
             const float *const lg[1] = {logits + static_cast<int64_t>(t0) * E1};
             const bool live[1] = {true};
             int *const ids[1] = {&r.ids[t0 * 16]};
-            float *const w[1] = {weight ? weight + t0 * K : wdummy};
-            float *const g[1] = {gate ? gate + t0 : gdummy};
+            float *const w[1] = {weight ? weight + t0 * K : nullptr};
+            float *const g[1] = {gate ? gate + t0 : nullptr};
             route_rows<1>(lg, live, E, K, ids, w, g, weight != nullptr);
         }
     } else {
@@ -188,8 +190,8 @@ __device__ inline void route_core(const float *__restrict__ logits, int E, int K
                                         logits + static_cast<int64_t>(t1c) * E1};
             const bool live[2] = {true, l1};
             int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
-            float *const w[2] = {weight ? weight + t0 * K : wdummy, weight ? weight + t1c * K : wdummy};
-            float *const g[2] = {gate ? gate + t0 : gdummy, gate ? gate + t1c : gdummy};
+            float *const w[2] = {weight ? weight + t0 * K : nullptr, weight ? weight + t1c * K : nullptr};
+            float *const g[2] = {gate ? gate + t0 : nullptr, gate ? gate + t1c : nullptr};
             route_rows<2>(lg, live, E, K, ids, w, g, weight != nullptr);
         }
     }
@@ -290,14 +292,14 @@ __device__ inline void route_small(const float *__restrict__ logits, int E, int 
     const int E1 = E + 1;
     trace(GV_K_ROUTE, 0);
     for (int e = tid; e <= E; e += blockDim.x) r.cnt[e] = 0, r.rows[e] = 0;
-    float wdummy[1], gdummy[1];
+    // (no weight: route_rows writes the ids alone, never w or g)
     if (M < 2 * waves) {   // (route_core's branches: the same rows on the same arithmetic)
         for (int t0 = wave; t0 < M; t0 += waves) {
             const float *const lg[1] = {logits + static_cast<int64_t>(t0) * E1};
             const bool live[1] = {true};
             int *const ids[1] = {&r.ids[t0 * 16]};
-            float *const w[1] = {weight ? weight + t0 * K : wdummy};
-            float *const g[1] = {gate ? gate + t0 : gdummy};
+            float *const w[1] = {weight ? weight + t0 * K : nullptr};
+            float *const g[1] = {gate ? gate + t0 : nullptr};
             route_rows<1>(lg, live, E, K, ids, w, g, weight != nullptr);
         }
     } else {
@@ -309,8 +311,8 @@ __device__ inline void route_small(const float *__restrict__ logits, int E, int 
                                         logits + static_cast<int64_t>(t1c) * E1};
             const bool live[2] = {true, l1};
             int *const ids[2] = {&r.ids[t0 * 16], &r.ids[t1c * 16]};
-            float *const w[2] = {weight ? weight + t0 * K : wdummy, weight ? weight + t1c * K : wdummy};
-            float *const g[2] = {gate ? gate + t0 : gdummy, gate ? gate + t1c : gdummy};
+            float *const w[2] = {weight ? weight + t0 * K : nullptr, weight ? weight + t1c * K : nullptr};
+            float *const g[2] = {gate ? gate + t0 : nullptr, gate ? gate + t1c : nullptr};
             route_rows<2>(lg, live, E, K, ids, w, g, weight != nullptr);
         }
     }
