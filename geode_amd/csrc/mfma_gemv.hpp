@@ -273,6 +273,20 @@ struct TileRun {
 struct NoHook {
     __device__ void operator()() const {}
 };
+// a call's own output of the flushed tiles (mfma_tiles, kSplitK with FLUSH): flush(i0, i1, part, W) takes tiles
+// [i0, i1)'s waves' partial sums (part[((i - i0) W + w) NTT + tt) 64 + lane]) instead of put; active false: put
+struct NoFlush {
+    static constexpr bool active = false;
+    __device__ void operator()(int, int, const f4 *, int) const {}
+};
+template <typename F>
+struct FlushWith {
+    static constexpr bool active = true;
+    F f;
+    __device__ void operator()(int i0, int i1, const f4 *part, int W) const { f(i0, i1, part, W); }
+};
+template <typename F>
+__device__ inline FlushWith<F> flush_with(F f) { return FlushWith<F>{f}; }
 
 // How a call's waves share the work: kSplitK - the workgroup's waves split the K range of every tile, their partial
 // sums added in wave order at the end (then put); kKeepParts - the same, the partial sums left in LDS for the caller;
@@ -294,10 +308,12 @@ enum TilesMode { kSplitK = 0, kKeepParts = 1, kWaveTiles = 2 };
 // runs after the first tiles' loads are issued and before the activations are loaded (a wait for them); ready() once
 // the activations and the first tiles are in registers. Every thread of the workgroup calls this.
 template <int KW, int NTT, int MODE, int NT = 0, int DEPTH = 3, bool PACK = false, int FLUSH = 0, typename RowFn,
-          typename PutFn, typename MapFn = TileRun, typename HookFn = NoHook, typename ReadyFn = NoHook>
+          typename PutFn, typename MapFn = TileRun, typename HookFn = NoHook, typename ReadyFn = NoHook,
+          typename FlushFn = NoFlush>
 __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, int64_t rows,
                                   int nsc, int sc0, int nt, int M, RowFn rowp, PutFn put, f4 *part, uint2 *tab,
-                                  MapFn tmap, HookFn hook = HookFn{}, ReadyFn ready = ReadyFn{}) {
+                                  MapFn tmap, HookFn hook = HookFn{}, ReadyFn ready = ReadyFn{},
+                                  FlushFn flush = FlushFn{}) {
     static_assert(DEPTH >= 2 && (NT > 0 || DEPTH >= 3), "the runtime loop is a ring of at least three");
     static_assert(!PACK || NTT == 1, "packed hi | lo columns take one 16-row tile of at most 8 rows");
     static_assert(FLUSH == 0 || (MODE == kSplitK && NT == 0), "the flushed split-K runs the runtime tile loop");
@@ -423,6 +439,11 @@ __device__ inline void mfma_tiles(const uint8_t *__restrict__ codes, const uint8
     // order, each output by one thread
     auto split_k_out = [&](int i0, int i1) {
         __syncthreads();
+        if constexpr (FlushFn::active) {
+            flush(i0, i1, part, W);
+            if (FLUSH) __syncthreads();
+            return;
+        }
         for (int o = threadIdx.x; o < (i1 - i0) * NTT * 64; o += blockDim.x) {
             const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
             f4 sum = part[((i * W + 0) * NTT + tt) * 64 + ll];

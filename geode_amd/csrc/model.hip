@@ -916,14 +916,70 @@ __global__ __launch_bounds__(512) void mixout_kernel(const MixOutArgs a) {
 // pick's rows go to out [pick][rows].
 constexpr int kMoeFlush = 4;   // tiles whose partial sums an expert workgroup holds at once
 
-template <int KW, int NTT, int WMAX, bool UP>
+// The SwiGLU of a matched gate / up tile pair's sums for F tile p (gs, us: the lane's rows 4 lg .. 4 lg + 3 of its
+// column; x their globals g0, g1), m = silu(gate) x up (swiglu_quant_kernel's arithmetic), quantized per 16-value
+// block (the pair's 16 rows: the column's four lanes) into the act16 operands of the column's row (live: the column
+// is a pick). Every lane of the wave calls it (lane shuffles).
+__device__ inline void swiglu_pair_out(f4 gs, f4 us, float g0, float g1, int p, bool live, _Float16 *row) {
+    const int lg = (threadIdx.x % 64) / 16;
+    float mv[4], amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = gs[r] * g0, uv = us[r] * g1;
+        mv[r] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), uv);
+        amax = fmaxf(amax, fabsf(mv[r]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const float sc = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    uint32_t hw[2], lw[2];   // this lane's 4 values (rows 4 lg .. 4 lg + 3 of the pair): hi, lo halves
+#pragma unroll
+    for (int r = 0; r < 4; r += 2) {
+        _Float16 h0, l0, h1, l1;
+        const int q0 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r], qi))), -127), 127);
+        const int q1 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r + 1], qi))), -127), 127);
+        const bool ex = g_act_exact != 0;   // (the exact path: the SwiGLU values themselves)
+        split_f16(ex ? mv[r] : __fmul_rn(static_cast<float>(q0), sc), h0, l0);
+        split_f16(ex ? mv[r + 1] : __fmul_rn(static_cast<float>(q1), sc), h1, l1);
+        hw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                    (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+        lw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
+                    (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+    }
+    // k-group 2 p + lg / 2 holds values 0..3 (lane lg even) and 4..7 (lane lg + 1) in the slot order
+    // (0 4 1 5 2 6 3 7): the even lane takes its partner's four and writes the group
+    uint32_t ph[2], pl[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        ph[k] = __shfl_xor(hw[k], 16, 64);
+        pl[k] = __shfl_xor(lw[k], 16, 64);
+    }
+    if ((lg & 1) == 0 && live) {
+        auto inter = [](uint32_t mine, uint32_t other) {   // (m0, o0), (m1, o1) as two words
+            return make_uint2((mine & 0xFFFFu) | (other << 16), (mine >> 16) | (other & 0xFFFF0000u));
+        };
+        const uint2 h01 = inter(hw[0], ph[0]), h23 = inter(hw[1], ph[1]);
+        const uint2 l01 = inter(lw[0], pl[0]), l23 = inter(lw[1], pl[1]);
+        const int gi = 2 * p + lg / 2;
+        uint4 *dst = reinterpret_cast<uint4 *>(row + static_cast<int64_t>(gi) * 16);
+        dst[0] = make_uint4(h01.x, h01.y, h23.x, h23.y);
+        dst[1] = make_uint4(l01.x, l01.y, l23.x, l23.y);
+    }
+}
+
+// SW (UP): the workgroup's tiles are matched gate / up pairs (gate tile p, up tile F / 16 + p: the tile loop takes
+// them in turns, tiles_per_wg even), and each flush of two pairs writes their SwiGLU's operands for down
+// (swiglu_pair_out) to sw_out [pick] instead of the products to out: no gate|up buffer, no SwiGLU launch.
+template <int KW, int NTT, int WMAX, bool UP, bool SW = false>
 __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
                                                         size_t code_stride, size_t scale_stride, int64_t rows, int K,
                                                         const float *__restrict__ globals, int half_rows,
                                                         const _Float16 *__restrict__ act, int64_t act_stride,
                                                         const float *__restrict__ gu, const Slots sl,
                                                         float *__restrict__ out, int tiles_per_wg, int E1,
-                                                        int max_picks) {
+                                                        int max_picks, _Float16 *__restrict__ sw_out,
+                                                        int64_t sw_stride) {
+    static_assert(!SW || (UP && kMoeFlush % 2 == 0), "pairs: the up products, whole pairs a flush");
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
     const int u = blockIdx.x;
@@ -931,10 +987,34 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
     const int e = sl.expert[u], start = sl.start[u], cnt = sl.count[u];
     if (e < 0 || e >= E1 || cnt < 1 || cnt > kMaxRows || start < 0 || start + cnt > max_picks) return;   // no slot
     const int64_t ntiles = tiles_rows(rows);
+    const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
+    if constexpr (SW) {
+        const int npair = static_cast<int>(ntiles / 2), ppw = tiles_per_wg / 2;
+        const int P0 = static_cast<int>(blockIdx.y) * ppw, P1 = min(P0 + ppw, npair);
+        if (P0 >= npair) return;
+        mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
+            codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
+            K / kSuperK, 0, 2 * (P1 - P0), cnt,
+            [&](int j) { return act + static_cast<int64_t>(sl.pick_token[start + j]) * act_stride; },
+            [](int64_t, int, float) {}, part_lds, tab,
+            [&](int i) -> int64_t { return (i & 1) ? npair + P0 + (i >> 1) : P0 + (i >> 1); }, NoHook{}, NoHook{},
+            flush_with([&](int i0, int i1, const f4 *part, int W) {   // a pair and column tile a wave: sums in wave order
+                for (int o = threadIdx.x; o < (i1 - i0) / 2 * NTT * 64; o += blockDim.x) {
+                    const int q = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+                    f4 gs = part[((2 * q * W) * NTT + tt) * 64 + ll], us = part[(((2 * q + 1) * W) * NTT + tt) * 64 + ll];
+                    for (int w2 = 1; w2 < W; ++w2) {
+                        gs += part[(((2 * q) * W + w2) * NTT + tt) * 64 + ll];
+                        us += part[(((2 * q + 1) * W + w2) * NTT + tt) * 64 + ll];
+                    }
+                    const int j = tt * 16 + ll % 16;
+                    swiglu_pair_out(gs, us, g0, g1, P0 + (i0 >> 1) + q, j < cnt, sw_out + (start + j) * sw_stride);
+                }
+            }));
+        return;
+    }
     const int64_t t0 = static_cast<int64_t>(blockIdx.y) * tiles_per_wg;
     const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
     if (t0 >= ntiles) return;
-    const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
     mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
         codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
         K / kSuperK, 0, static_cast<int>(t1 - t0),
@@ -1056,49 +1136,7 @@ __global__ __launch_bounds__(512) void moe_up_kernel(const MoeArgsDec a) {
             gs += part_lds[(2 * q * W + w2) * 64 + lane];
             us += part_lds[((2 * q + 1) * W + w2) * 64 + lane];
         }
-        float mv[4], amax = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float x = gs[r] * g0, uv = us[r] * g1;
-            mv[r] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), uv);
-            amax = fmaxf(amax, fabsf(mv[r]));
-        }
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-        const float sc = __fdiv_rn(amax, 127.0f), qi = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-        uint32_t hw[2], lw[2];   // this lane's 4 values (rows 4 lg .. 4 lg + 3 of the pair): hi, lo halves
-#pragma unroll
-        for (int r = 0; r < 4; r += 2) {
-            _Float16 h0, l0, h1, l1;
-            const int q0 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r], qi))), -127), 127);
-            const int q1 = min(max(static_cast<int>(rintf(__fmul_rn(mv[r + 1], qi))), -127), 127);
-            const bool ex = g_act_exact != 0;   // (the exact path: the SwiGLU values themselves)
-            split_f16(ex ? mv[r] : __fmul_rn(static_cast<float>(q0), sc), h0, l0);
-            split_f16(ex ? mv[r + 1] : __fmul_rn(static_cast<float>(q1), sc), h1, l1);
-            hw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
-                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
-            lw[r / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
-                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
-        }
-        // k-group 2 (p0 + q) + lg / 2 holds values 0..3 (lane lg even) and 4..7 (lane lg + 1) in the slot order
-        // (0 4 1 5 2 6 3 7): the even lane takes its partner's four and writes the group
-        uint32_t ph[2], pl[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            ph[k] = __shfl_xor(hw[k], 16, 64);
-            pl[k] = __shfl_xor(lw[k], 16, 64);
-        }
-        if ((lg & 1) == 0 && j < cnt) {
-            auto inter = [](uint32_t mine, uint32_t other) {   // (m0, o0), (m1, o1) as two words
-                return make_uint2((mine & 0xFFFFu) | (other << 16), (mine >> 16) | (other & 0xFFFF0000u));
-            };
-            const uint2 h01 = inter(hw[0], ph[0]), h23 = inter(hw[1], ph[1]);
-            const uint2 l01 = inter(lw[0], pl[0]), l23 = inter(lw[1], pl[1]);
-            const int gi = 2 * (p0 + q) + lg / 2;
-            uint4 *dst = reinterpret_cast<uint4 *>(a.act_m + (start + j) * act_m_stride + static_cast<int64_t>(gi) * 16);
-            dst[0] = make_uint4(h01.x, h01.y, h23.x, h23.y);
-            dst[1] = make_uint4(l01.x, l01.y, l23.x, l23.y);
-        }
+        swiglu_pair_out(gs, us, g0, g1, p0 + q, j < cnt, a.act_m + (start + j) * act_m_stride);
     }
     trace(GV_K_MOE_UP, 3);
 }
@@ -1361,42 +1399,46 @@ struct MoeArgs {
     float *out;            // [pick][rows]
     int slots;             // a bound on the slot count (the grid)
     int E1, max_picks;
+    _Float16 *sw_out;      // UP with the SwiGLU in the launch: the picks' down operands (act16 rows of F), else null
 };
 
-template <int KW, int NTT, int WMAX, bool UP>
+template <int KW, int NTT, int WMAX, bool UP, bool SW>
 int launch_moe_raw(const MoeArgs &a, int waves, hipStream_t st) {
     const int64_t ntiles = tiles_rows(a.rows);
     // the slots' tiles over about four times as many workgroups as the chip holds at once (each workgroup loads its
-    // rows' activations once for all its tiles, so longer runs a workgroup read them fewer times)
+    // rows' activations once for all its tiles, so longer runs a workgroup read them fewer times); SW: whole pairs
     const int64_t resident = 256 * std::max(1, 8 / waves);
-    const int per = static_cast<int>(
+    int per = static_cast<int>(
         std::min<int64_t>(ntiles, std::max<int64_t>(kMoeFlush, (ntiles * a.slots + 4 * resident - 1) / (4 * resident))));
+    if (SW) per += per % 2;
     const int tiles = static_cast<int>((ntiles + per - 1) / per);
     const size_t lds = static_cast<size_t>(kMoeFlush) * waves * NTT * 1024;   // the waves' partial sums
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP>), 76 * 1024, granted) != 0)
+    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP, SW>), 76 * 1024, granted) != 0)
         return -1;
-    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP>), dim3(a.slots, tiles), dim3(64 * waves), lds, st, a.codes,
-                       a.scales, a.code_stride, a.scale_stride, a.rows, static_cast<int>(a.cols), a.globals, a.F, a.act,
-                       act_halves(a.cols), a.gu, a.sl, a.out, per, a.E1, a.max_picks);
+    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP, SW>), dim3(a.slots, tiles), dim3(64 * waves), lds, st,
+                       a.codes, a.scales, a.code_stride, a.scale_stride, a.rows, static_cast<int>(a.cols), a.globals,
+                       a.F, a.act, act_halves(a.cols), a.gu, a.sl, a.out, per, a.E1, a.max_picks, a.sw_out,
+                       act_halves(a.F));
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-template <bool UP>
+template <bool UP, bool SW = false>
 int moe_launch(const MoeArgs &a, int ntt, int kw, int waves, hipStream_t st) {
     if (ntt == 1) {
-        if (kw == 16) return launch_moe_raw<16, 1, 8, UP>(a, waves, st);
-        if (kw == 8) return launch_moe_raw<8, 1, 8, UP>(a, waves, st);
-        return launch_moe_raw<4, 1, 8, UP>(a, waves, st);
+        if (kw == 16) return launch_moe_raw<16, 1, 8, UP, SW>(a, waves, st);
+        if (kw == 8) return launch_moe_raw<8, 1, 8, UP, SW>(a, waves, st);
+        return launch_moe_raw<4, 1, 8, UP, SW>(a, waves, st);
     }
-    if (kw == 8) return launch_moe_raw<8, 2, 8, UP>(a, waves, st);
-    return launch_moe_raw<4, 2, 8, UP>(a, waves, st);
+    if (kw == 8) return launch_moe_raw<8, 2, 8, UP, SW>(a, waves, st);
+    return launch_moe_raw<4, 2, 8, UP, SW>(a, waves, st);
 }
 
 // the experts' products of layer L: gate|up (up) or down, over slots of at most `rows_max` rows each
+// (sw_out: up with the SwiGLU in the launch, its operands for down to sw_out; null: the products to out)
 int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float16 *act, const float *gu,
-            const Slots &sl, float *out, int slots, int max_picks, hipStream_t st) {
+            const Slots &sl, float *out, int slots, int max_picks, hipStream_t st, _Float16 *sw_out = nullptr) {
     const int64_t H = m.c.hidden, F = m.c.moe_ff;
     const int ntt = rows_max <= 16 ? 1 : 2;
     int waves, kw;
@@ -1415,7 +1457,9 @@ int moe_run(const Model &m, const LayerW &L, bool up, int rows_max, const _Float
               out,
               slots,
               m.E1,
-              max_picks};
+              max_picks,
+              sw_out};
+    if (up && sw_out) return moe_launch<true, true>(a, ntt, kw, waves, st);
     return up ? moe_launch<true>(a, ntt, kw, waves, st) : moe_launch<false>(a, ntt, kw, waves, st);
 }
 
@@ -2033,9 +2077,8 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks, nullptr,
                    nullptr};
     const int picks = M * (K + 1);
-    if (moe_run(m, L, true, 32, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st) != 0) return -1;
-    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(picks), dim3(256), static_cast<size_t>(F) * 4, st, pf.gu, F,
-                       pf.n_picks, pf.act_m);
+    // gate|up with the SwiGLU and its quantization in the launch (matched tile pairs), then down
+    if (moe_run(m, L, true, 32, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st, pf.act_m) != 0) return -1;
     if (moe_run(m, L, false, 32, pf.act_m, pf.gu, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
     combine_launch(pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M, pf.out, nullptr, 0.0f, nullptr, 0, st, nullptr,
                    false);
