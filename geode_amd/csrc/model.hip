@@ -914,7 +914,6 @@ __global__ __launch_bounds__(512) void mixout_kernel(const MixOutArgs a) {
 // The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
 // the post-norm rows of the slot's tokens, DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each
 // pick's rows go to out [pick][rows].
-constexpr int kPrefillRun = 16;   // picks a prefill slot holds at most (one 16-column MFMA tile)
 constexpr int kMoeFlush = 4;   // tiles whose partial sums an expert workgroup holds at once
 
 // The SwiGLU of a matched gate / up tile pair's sums for F tile p (gs, us: the lane's rows 4 lg .. 4 lg + 3 of its
@@ -1614,7 +1613,7 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const float *__restrict
 
 // The picks per expert (the shared one, E, takes every row), their starts, and the slots: each expert's picks in
 // runs of at most 32 (the products' row tiles), experts ascending. One workgroup of 1024 threads (E + 1 <= 257).
-__global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids, int M, int K, int E, int run,
+__global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids, int M, int K, int E,
                                                      int *__restrict__ start_out, int *__restrict__ n_slots,
                                                      int *__restrict__ slot_expert, int *__restrict__ slot_start,
                                                      int *__restrict__ slot_count, int *__restrict__ n_picks) {
@@ -1626,7 +1625,7 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids
     for (int i = tid; i < M * K; i += blockDim.x) atomicAdd(&cnt[ids[i]], 1);
     if (tid == 0) cnt[E] = M;
     __syncthreads();
-    const int c = tid <= E ? cnt[tid] : 0, ns = (c + run - 1) / run;
+    const int c = tid <= E ? cnt[tid] : 0, ns = (c + 31) / 32;
     int ic = c, is = ns;
     for (int o = 1; o < 64; o <<= 1) {
         const int pc = __shfl_up(ic, o, 64), ps = __shfl_up(is, o, 64);
@@ -1644,11 +1643,11 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids
     }
     __syncthreads();
     for (int e = tid; e <= E; e += blockDim.x)
-        for (int j = 0; run * j < cnt[e]; ++j) {
+        for (int j = 0; 32 * j < cnt[e]; ++j) {
             const int u = sbase[e] + j;
             slot_expert[u] = e;
-            slot_start[u] = start[e] + run * j;
-            slot_count[u] = min(run, cnt[e] - run * j);
+            slot_start[u] = start[e] + 32 * j;
+            slot_count[u] = min(32, cnt[e] - 32 * j);
         }
 }
 
@@ -2017,7 +2016,7 @@ int prefill_alloc(Model &m, int M) {
     const auto &c = m.c;
     const int64_t H = c.hidden, F = c.moe_ff, E1 = m.E1, K = c.top_k;
     pf.max_picks = cap * (c.top_k + 1);
-    pf.max_slots = static_cast<int>(E1 + pf.max_picks / kPrefillRun + 1);
+    pf.max_slots = static_cast<int>(E1 + pf.max_picks / 32 + 1);
     bool ok = true;
     auto get = [&](size_t bytes) -> void * {
         void *p = nullptr;
@@ -2053,7 +2052,7 @@ int prefill_alloc(Model &m, int M) {
 }
 
 // The MoE block of layer `layer` on the M rows in pf.h with the routed logits in pf.logits [M][E + 1] (column E
-// filled here: the shared expert's gate logit): route each row, group the picks by expert (runs of at most kPrefillRun),
+// filled here: the shared expert's gate logit): route each row, group the picks by expert (runs of at most 32),
 // the experts' products, SwiGLU, down, and the combine into pf.out (no residual).
 int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     const auto &c = m.c;
@@ -2070,7 +2069,7 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
                            pf.h, M, pf.logits, m.E1);
     }
     hipLaunchKernelGGL(route_rows_kernel, dim3(wg4), dim3(256), 0, st, pf.logits, E, K, M, pf.ids, pf.w, pf.gate);
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, kPrefillRun, pf.start, pf.n_slots,
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, pf.start, pf.n_slots,
                        pf.slot_expert, pf.slot_start, pf.slot_count, pf.n_picks);
     hipLaunchKernelGGL(fill_picks_kernel, dim3(m.E1), dim3(256), 0, st, pf.ids, M, K, E, pf.start, pf.pick_token,
                        pf.pick_of);
@@ -2079,8 +2078,8 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
                    nullptr};
     const int picks = M * (K + 1);
     // gate|up with the SwiGLU and its quantization in the launch (matched tile pairs), then down
-    if (moe_run(m, L, true, kPrefillRun, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st, pf.act_m) != 0) return -1;
-    if (moe_run(m, L, false, kPrefillRun, pf.act_m, pf.gu, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
+    if (moe_run(m, L, true, 32, pf.act, pf.gu, sl, pf.gu, pf.max_slots, picks, st, pf.act_m) != 0) return -1;
+    if (moe_run(m, L, false, 32, pf.act_m, pf.gu, sl, pf.y, pf.max_slots, picks, st) != 0) return -1;
     combine_launch(pf.y, H, K, MixView{pf.gate, pf.w, pf.pick_of}, M, pf.out, nullptr, 0.0f, nullptr, 0, st, nullptr,
                    false);
     GV_CHECK_HIP(hipGetLastError());
