@@ -38,7 +38,7 @@ COPY_BYTES = 256 << 20
 # HBM bytes a launch of the dominant kernel moves, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes (KiB a dispatch)
 # scaled by what the same counters read for a copy of known size (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000); the
 # commands and figures are in profiles/moe_up_c4_m5_traffic.md
-PROFILED_TRAFFIC = {("moe_up", 5): (22561.7 * 2.000 + 90.0 * 1.000) * 1024}
+PROFILED_TRAFFIC = {("moe_up", 5): (22704.1 * 2.000 + 94.6 * 1.000) * 1024}
 Q4_ROW = lambda cols: cols // 16 * 9   # noqa: E731  bytes of a q4 row (engine/src/kernels.cpp:900-902)
 
 
