@@ -49,6 +49,8 @@ constexpr int kSortThreads = 1024;
 constexpr int kMaxCand = 16384;   // top-K candidates a row can keep (the full-vocabulary nucleus has no limit)
 constexpr int kList = 1024;       // elements a walk lists under its last level's prefix
 constexpr int kSampleRows = 64;   // rows gv_sample_rows takes at most
+constexpr int kFB = 48;        // the candidate path's bins of a chunk's summary (down to exp(-12) of its largest e)
+constexpr int kFCap = 4096;    // elements a row collects at most on the candidate path
 
 __host__ __device__ constexpr int level_shift(int l) { return l == 0 ? 21 : l == 1 ? 10 : 0; }
 __host__ __device__ constexpr int level_bins(int l) { return l == 2 ? 1024 : 2048; }
@@ -152,6 +154,9 @@ struct Ws {   // device arrays of R rows
     uint64_t *lst;        // [R][2][kList] (key << 32) | index
     int32_t *picks;       // [R] the rows' picks
     double *u;            // [R] the uniforms
+    struct FStat *fs;     // [R][kMaxChunks] the candidate path's chunk summaries
+    struct FRow *fr;      // [R] its row states
+    uint32_t *fbc;        // [R][kFB] its bins' collected elements
 };
 
 // ---------------------------------------------------------------- loads
@@ -962,6 +967,621 @@ __global__ __launch_bounds__(kPass) void textbook_finish(Rows rs, Ws ws, int k, 
     }
 }
 
+// ---------------------------------------------------------------- the candidate path (a nucleus of top_p < 1)
+// The walks above go to any depth of the sorted order. A nucleus of top_p < 1 ends where its mass reaches top_p:
+// with logits spread like a language model's (and C2's N(0, 3) at T 0.7) that is a few to a few thousand elements,
+// all at or above one logit. The candidate path finds such a logit from a binned summary of each chunk, collects
+// the elements at or above it (at most kFCap a row), sorts them in LDS and runs the reference's nucleus on them as
+// written, then checks that the kept prefix ended inside them; a row it cannot decide (more elements, a prefix
+// past them, a row whose largest value is not finite) is marked, and the caller takes the walks instead. Four
+// launches instead of eight, none with histogram atomics:
+//   fast_stats     a chunk's largest value m and its elements' counts and e-mass exp((l - m) / T) in bins of
+//                  floor(4 l / T) (an e ratio of exp(1/4) a bin), the kFB bins from the chunk's top bin down;
+//   fast_collect   the row's bins merged (a chunk's mass rescaled by exp((m - max) / T): an estimate), the first bin
+//                  from the top where the mass reaches top_p (a 1e-3 margin and one bin more) or the count reaches
+//                  K, the elements at or above it collected; every element's exact e summed a chunk, as the walks'
+//                  first pass does;
+//   fast_nucleus   a workgroup a row: the collected elements sorted (logit descending, index ascending), the
+//                  nucleus, its draw, and the kept prefix written back in order;
+//   fast_textbook  the textbook rule's decisions, and at a rejection the residual max(0, p - q) over the target's
+//                  kept prefix (p is 0 elsewhere) in index order.
+// A bin is a logit threshold (floor(4 l / T) does not decrease as l grows), so the collected elements are a top
+// part of the sorted order and equal logits are collected together.
+
+struct FStat {   // a chunk's summary
+    uint32_t key;      // its largest key
+    int32_t top;       // that value's bin
+    float mass;        // its elements' exp((l - m) / T), m its largest value
+    uint32_t unused;
+    uint32_t cnt[kFB];   // elements a bin, bin top - j at j
+    float w[kFB];        // their exp((l - m) / T)
+};
+
+struct FRow {
+    uint32_t n;        // elements collected (more than kFCap: the row is not decided here)
+    int32_t ok;        // the row is decided here
+    uint64_t last;     // the kept prefix's last element, (key << 32) | ~index: x is kept iff its own is at least this
+    uint32_t top_key;  // the row's largest key
+    uint32_t unused;
+};
+
+struct FastU {   // kernel arguments: a uniform a row, the acceptance uniforms, the residual's
+    double u[64];
+    float acc[32];
+    float res;
+};
+
+__device__ inline int fbin(float l, float s) { return static_cast<int>(fminf(fmaxf(floorf(l * s), -1.0e9f), 1.0e9f)); }
+__device__ inline uint64_t comp_of(float l, uint32_t x) {
+    return (static_cast<uint64_t>(fkey(l)) << 32) | (0xFFFFFFFFu - x);
+}
+__device__ inline uint32_t comp_index(uint64_t c) { return 0xFFFFFFFFu - static_cast<uint32_t>(c); }
+
+// a[0, P) sorted descending (P a power of two; every thread of the workgroup, which holds whole waves). Pair i of a
+// stage of stride s <= 64 has both elements in [128 (i / 64), + 128): a wave's 64 consecutive pairs keep the same
+// 128 elements from one such stage to the next, so between two of them the wave only waits for its own LDS writes;
+// a workgroup barrier follows every other stage, and the last.
+__device__ void bitonic_desc(uint64_t *a, int P) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    for (int size = 2; size <= P; size <<= 1)
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int i = tid; i < P / 2; i += nthr) {
+                const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t x = a[lo], y = a[hi];
+                if ((x < y) == desc) {
+                    a[lo] = y;
+                    a[hi] = x;
+                }
+            }
+            const int next = stride > 1 ? stride / 2 : size;
+            if (stride <= 64 && next <= 64 && !(stride == 1 && size == P)) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            } else {
+                __syncthreads();
+            }
+        }
+}
+
+// grid (S, R), kPass threads
+__global__ __launch_bounds__(kPass) void fast_stats(Rows rs, Ws ws, float T) {
+    __shared__ uint32_t scnt[kFB];
+    __shared__ float sw[kFB];
+    __shared__ uint64_t red[kPass / 64];
+    __shared__ float redm[kPass / 64];
+    const int w = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const float *row = rs.row(r);
+    const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
+    float v[kLoads];
+    preload(row, c0, c1, v);
+    if (tid < kFB) {
+        scnt[tid] = 0u;
+        sw[tid] = 0.0f;
+    }
+    if (w == 0 && tid < kFB) ws.fbc[r * kFB + tid] = 0u;   // (the collect pass counts from here)
+    uint64_t best = 0;
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u)
+        if (c0 + u * kPass + tid < c1) best = max(best, comp_of(v[u], static_cast<uint32_t>(c0 + u * kPass + tid)));
+    for (int o = 32; o > 0; o >>= 1) best = max(best, static_cast<uint64_t>(__shfl_xor(best, o, 64)));
+    if (lane == 0) red[tid >> 6] = best;
+    __syncthreads();   // (also publishes the zeroed bins)
+    best = max(max(red[0], red[1]), max(red[2], red[3]));
+    const float mc = key_val(static_cast<uint32_t>(best >> 32)), s4 = 4.0f / T;
+    const int top = fbin(mc, s4);
+    float mass = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+        if (c0 + u * kPass + tid >= c1) continue;
+        const float e = e_of(v[u], mc, T);
+        mass += e;
+        const int b = top - fbin(v[u], s4);   // (>= 0 unless a value is NaN)
+        if (static_cast<unsigned>(b) < static_cast<unsigned>(kFB)) {
+            atomicAdd(&scnt[b], 1u);
+            atomicAdd(&sw[b], e);
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) mass += __shfl_xor(mass, o, 64);
+    if (lane == 0) redm[tid >> 6] = mass;
+    __syncthreads();
+    FStat &o = ws.fs[r * kMaxChunks + w];
+    if (tid < kFB) {
+        o.cnt[tid] = scnt[tid];
+        o.w[tid] = sw[tid];
+    }
+    if (tid == 0) {
+        o.key = static_cast<uint32_t>(best >> 32);
+        o.top = top;
+        o.mass = (redm[0] + redm[1]) + (redm[2] + redm[3]);
+    }
+}
+
+// grid (S, R), kPass threads. MASS: the full-vocabulary nucleus (top_p < 1); else the top-K candidates.
+template <bool MASS>
+__global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, float top_p, int K) {
+    __shared__ float sscale[kMaxChunks];
+    __shared__ int soff[kMaxChunks];
+    __shared__ uint32_t sq_c[4][64];
+    __shared__ double sq_w[4][64];
+    __shared__ uint32_t s_start[kFB], s_end[kFB], lcnt[kFB], lbase[kFB], lcur[kFB];
+    __shared__ double tmp_d[16];
+    __shared__ uint32_t tmp_u[16];
+    __shared__ uint32_t s_key;
+    __shared__ int s_top, s_first;
+    __shared__ double s_tot;
+    const int w = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, S = rs.S;
+    const float *row = rs.row(r);
+    const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
+    float v[kLoads];
+    preload(row, c0, c1, v);
+    const FStat *st = ws.fs + r * kMaxChunks;
+    if (tid < 64) {   // the row's largest key, its top bin and e-mass (a lane a chunk)
+        const uint32_t k = lane < S ? st[lane].key : 0u;
+        const int tp = lane < S ? st[lane].top : INT_MIN;
+        const float m = lane < S ? st[lane].mass : 0.0f;
+        uint32_t mk = k;
+        int mt = tp;
+        for (int o = 32; o > 0; o >>= 1) {
+            mk = max(mk, static_cast<uint32_t>(__shfl_xor(mk, o, 64)));
+            mt = max(mt, __shfl_xor(mt, o, 64));
+        }
+        const float M = key_val(mk);
+        const float sc = lane < S ? expf(__fdiv_rn(__fsub_rn(key_val(k), M), T)) : 0.0f;
+        double tot = static_cast<double>(m) * static_cast<double>(sc);
+        for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+        if (lane < S) {
+            sscale[lane] = sc;
+            soff[lane] = mt - tp;
+        }
+        if (lane == 0) {
+            s_key = mk;
+            s_top = mt;
+            s_tot = tot;
+            s_first = INT_MAX;
+        }
+    }
+    __syncthreads();
+    const float M = key_val(s_key);
+    // the row's bin j (from its top): every chunk's bin j - (its offset), thread j + 64 h taking chunks h, h + 4, ..
+    // (their loads all issued at once), the four quarters added in LDS
+    double bw = 0.0;
+    uint32_t bc = 0;
+    {
+        const int j = tid & 63, h = tid >> 6;
+        uint32_t cc[kMaxChunks / 4];
+        float ww[kMaxChunks / 4];
+#pragma unroll
+        for (int q = 0; q < kMaxChunks / 4; ++q) {
+            const int c = min(4 * q + h, S - 1), jj = min(max(j - soff[c], 0), kFB - 1);
+            cc[q] = st[c].cnt[jj];
+            ww[q] = MASS ? st[c].w[jj] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < kMaxChunks / 4; ++q) {
+            const int c = 4 * q + h, jl = j - soff[min(c, S - 1)];
+            const bool in = c < S && j < kFB && jl >= 0 && jl < kFB;
+            bc += in ? cc[q] : 0u;
+            if (MASS) bw += in ? static_cast<double>(ww[q]) * static_cast<double>(sscale[c]) : 0.0;
+        }
+        sq_c[h][j] = bc;
+        sq_w[h][j] = bw;
+        __syncthreads();
+        bc = tid < kFB ? (sq_c[0][tid] + sq_c[1][tid]) + (sq_c[2][tid] + sq_c[3][tid]) : 0u;
+        bw = tid < kFB ? (sq_w[0][tid] + sq_w[1][tid]) + (sq_w[2][tid] + sq_w[3][tid]) : 0.0;
+    }
+    bool hit;
+    uint32_t ctot;
+    const uint32_t cex = block_excl_scan(bc, tmp_u, ctot);
+    if (MASS) {
+        double wtot;
+        const double wex = block_excl_scan(bw, tmp_d, wtot);
+        hit = tid < kFB && wex + bw >= static_cast<double>(top_p) * s_tot * (1.0 + 1e-3);
+    } else {
+        hit = tid < kFB && cex + bc >= static_cast<uint32_t>(K);
+    }
+    if (hit) atomicMin(&s_first, tid);
+    if (tid < kFB) {   // bin j's elements go to [cex, cex + bc) of the row's list (the counts are whole for j <= jc)
+        s_start[tid] = cex;
+        s_end[tid] = cex + bc;
+        lcnt[tid] = 0u;
+        lcur[tid] = 0u;
+    }
+    __syncthreads();
+    const bool ok = isfinite(M) && s_first != INT_MAX;
+    const int jc = MASS ? min(s_first + 1, kFB - 1) : s_first;
+    const int thr = ok ? s_top - jc : INT_MAX;   // collected: row bin s_top - fbin(l) <= jc
+    const float s4 = 4.0f / T;
+    double part = 0.0;
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+        if (c0 + u * kPass + tid >= c1) continue;
+        const int b = fbin(v[u], s4);
+        if (b >= thr) atomicAdd(&lcnt[s_top - b], 1u);
+        if (MASS) part += static_cast<double>(e_of(v[u], M, T));
+    }
+    __syncthreads();
+    if (tid <= jc && ok && lcnt[tid]) lbase[tid] = atomicAdd(&ws.fbc[r * kFB + tid], lcnt[tid]);
+    __syncthreads();
+    uint64_t *cand = ws.cand + static_cast<int64_t>(r) * kMaxCand;
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+        const int i = c0 + u * kPass + tid;
+        const int b = fbin(v[u], s4);
+        if (i >= c1 || b < thr) continue;
+        const int j = s_top - b;
+        const uint32_t at = s_start[j] + lbase[j] + atomicAdd(&lcur[j], 1u);
+        if (at < static_cast<uint32_t>(kFCap)) cand[at] = comp_of(v[u], static_cast<uint32_t>(i));
+    }
+    if (MASS) {
+        const double cs = block_sum(part, tmp_d);
+        if (tid == 0) ws.psum[r * kMaxChunks + w] = cs;
+    }
+    if (w == 0 && tid == 0) {
+        ws.fr[r].ok = ok;
+        ws.fr[r].n = ok ? s_end[jc] : 0u;
+        ws.fr[r].top_key = s_key;
+    }
+}
+
+// Elements sorted by rank within their groups: in[g0, g1) is group g's, every key distinct; the element at i goes to
+// out[g0 + (how many of its group order before it)] (before: a greater key when DESC, a smaller one otherwise).
+// find(i) gives i's group bounds. Every thread of the workgroup; the caller synchronises after.
+template <bool DESC, typename Find>
+__device__ inline void rank_place(const uint64_t *in, uint64_t *out, int n, Find find) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t c = in[i];
+        uint32_t g0, g1;
+        find(i, c, g0, g1);
+        uint32_t rk[8] = {};   // (eight loads in flight)
+        uint32_t j = g0;
+        for (; j + 8 <= g1; j += 8)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) rk[q] += DESC ? in[j + q] > c : in[j + q] < c;
+        for (; j < g1; ++j) rk[0] += DESC ? in[j] > c : in[j] < c;
+        out[g0 + ((rk[0] + rk[1]) + (rk[2] + rk[3])) + ((rk[4] + rk[5]) + (rk[6] + rk[7]))] = c;
+    }
+}
+
+// A workgroup a row: the reference's nucleus (sampler.cpp:31-49) on the collected elements, which arrive grouped by
+// bin, the bins in the sorted order: e_i = exp((l_i - max) / T); sum = every element's e (the chunks' sums in order);
+// keep = the first i (in the sorted order) where the running sum over sum reaches top_p; kept = e_0 + .. +
+// e_{keep-1}; the draw of u[row]: the first i < keep where kept u - (e_0 + .. + e_i) <= 0. One scan over the grouped
+// elements gives the running sum at every bin's end, which does not depend on the order inside the bins; only the bin
+// where top_p is reached and the bin where the draw lands are put in order (by rank) and scanned again. A row whose
+// prefix does not end inside the collected elements is marked undecided.
+constexpr int kSeg = kFCap / kSortThreads;   // consecutive elements a thread scans
+
+// inclusive running sums of v over positions [0, m) (m <= kFCap, thread t taking t kSeg ..); cl[j]: through position
+// t kSeg + j (tmp: LDS of 16 doubles); the total
+__device__ inline double seg_scan(const double (&v)[kSeg], double (&cl)[kSeg], double *tmp) {
+    double loc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+        loc += v[j];
+        cl[j] = loc;
+    }
+    double tot;
+    const double ex = block_excl_scan(loc, tmp, tot);
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) cl[j] += ex;
+    return tot;
+}
+
+// in[g, g + m) put in descending order into out[0, m) by rank (keys distinct); every thread; the caller synchronises
+__device__ inline void rank_sort_desc(const uint64_t *in, int g, int m, uint64_t *out) {
+    for (int i = threadIdx.x; i < m; i += blockDim.x) {
+        const uint64_t c = in[g + i];
+        uint32_t rk[8] = {};   // (eight loads in flight)
+        int j = 0;
+        for (; j + 8 <= m; j += 8)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) rk[q] += in[g + j + q] > c;
+        for (; j < m; ++j) rk[0] += in[g + j] > c;
+        out[((rk[0] + rk[1]) + (rk[2] + rk[3])) + ((rk[4] + rk[5]) + (rk[6] + rk[7]))] = c;
+    }
+}
+
+__global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, float T, float top_p, FastU fu) {
+    extern __shared__ uint64_t lds[];   // [kFCap] the collected elements (by bin), [kFCap] doubles: the running e
+                                        // sums, [kFCap] the top-p bin sorted, [kFCap] the draw's bin sorted
+    uint64_t *in = lds, *sk = lds + 2 * kFCap, *sd = lds + 3 * kFCap;
+    double *cum = reinterpret_cast<double *>(lds + kFCap);
+    __shared__ uint32_t s_start[kFB + 1];
+    __shared__ double tmp_d[16];
+    __shared__ double e_part[kMaxChunks];
+    __shared__ int s_bk, s_bd, s_t, s_td;
+    __shared__ double s_sum;
+    const int r = blockIdx.x, tid = threadIdx.x;
+    FRow &fr = ws.fr[r];
+    const int n = static_cast<int>(fr.n);
+    if (!fr.ok || n <= 0 || n > kFCap || !(top_p < 1.0f)) {
+        if (tid == 0) fr.ok = 0;
+        return;
+    }
+    uint64_t *cand = ws.cand + static_cast<int64_t>(r) * kMaxCand;
+    const float mx = key_val(fr.top_key);
+    if (tid < 64) {   // the bins' starts (wave 0)
+        const uint32_t c = tid < kFB ? ws.fbc[r * kFB + tid] : 0u;
+        const uint32_t incl = wave_incl_scan(c);
+        if (tid < kFB) s_start[tid] = incl - c;
+        if (tid == kFB - 1) s_start[kFB] = incl;
+    }
+    if (tid < rs.S) e_part[tid] = ws.psum[r * kMaxChunks + tid];
+    if (tid == 0) {
+        s_t = INT_MAX;
+        s_td = INT_MAX;
+    }
+    const int i0 = tid * kSeg;
+    double v[kSeg], cl[kSeg];
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+        const uint64_t c = i0 + j < n ? cand[i0 + j] : 0ull;
+        if (i0 + j < n) in[i0 + j] = c;
+        v[j] = i0 + j < n ? static_cast<double>(e_of(key_val(static_cast<uint32_t>(c >> 32)), mx, T)) : 0.0;
+    }
+    (void)seg_scan(v, cl, tmp_d);   // (its barriers publish the starts, e_part and in)
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j)
+        if (i0 + j < n) cum[i0 + j] = cl[j];
+    if (tid == 0) {
+        double t = 0.0;   // the row's e sum, chunks in order
+        for (int c = 0; c < rs.S; ++c) t += e_part[c];
+        s_sum = t;
+    }
+    __syncthreads();
+    const double sum = s_sum, target = static_cast<double>(top_p);
+    auto end_of = [&](int b) { return cum[s_start[b + 1] - 1]; };   // (a nonempty bin)
+    auto before = [&](int b) { return s_start[b] ? cum[s_start[b] - 1] : 0.0; };
+    if (tid < 64) {   // the bin where the running sum reaches top_p
+        const bool hit = tid < kFB && s_start[tid + 1] > s_start[tid] && end_of(tid) / sum >= target;
+        const uint64_t m = __ballot(hit);
+        if (tid == 0) s_bk = m ? __builtin_ctzll(m) : -1;
+    }
+    __syncthreads();
+    const int bk = s_bk;
+    if (bk < 0) {   // the prefix goes on past the collected elements
+        if (tid == 0) fr.ok = 0;
+        return;
+    }
+    const int gk = static_cast<int>(s_start[bk]), mk = static_cast<int>(s_start[bk + 1]) - gk;
+    rank_sort_desc(in, gk, mk, sk);
+    __syncthreads();
+    const double cb = before(bk);
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j)
+        v[j] = i0 + j < mk ? static_cast<double>(e_of(key_val(static_cast<uint32_t>(sk[i0 + j] >> 32)), mx, T)) : 0.0;
+    (void)seg_scan(v, cl, tmp_d);
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j)
+        if (i0 + j < mk && (cb + cl[j]) / sum >= target) {
+            atomicMin(&s_t, i0 + j);
+            break;
+        }
+    __syncthreads();
+    const int t = s_t;
+    if (t == INT_MAX) {   // (rounding: the bin's end in its sorted order fell short)
+        if (tid == 0) fr.ok = 0;
+        return;
+    }
+    const int keep = gk + t + 1;
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j)
+        if (i0 + j == t) s_sum = cb + cl[j];   // (every thread has read s_sum)
+    __syncthreads();
+    const double kept = s_sum, rr = kept * fu.u[r];
+    if (tid < 64) {   // the draw's bin: the first before bk whose end reaches rr, else bk
+        const bool hit = tid < bk && s_start[tid + 1] > s_start[tid] && rr - end_of(tid) <= 0.0;
+        const uint64_t m = __ballot(hit);
+        if (tid == 0) s_bd = m ? __builtin_ctzll(m) : bk;
+    }
+    __syncthreads();
+    const int bd = s_bd;
+    uint64_t pick_c;
+    if (bd == bk) {
+#pragma unroll
+        for (int j = 0; j < kSeg; ++j)
+            if (i0 + j <= t && rr - (cb + cl[j]) <= 0.0) {
+                atomicMin(&s_td, i0 + j);
+                break;
+            }
+        __syncthreads();
+        pick_c = sk[s_td != INT_MAX ? s_td : t];   // rounding past the end: the last kept
+    } else {
+        const int gd = static_cast<int>(s_start[bd]), md = static_cast<int>(s_start[bd + 1]) - gd;
+        rank_sort_desc(in, gd, md, sd);
+        __syncthreads();
+        const double cbd = before(bd);
+#pragma unroll
+        for (int j = 0; j < kSeg; ++j)
+            v[j] = i0 + j < md ? static_cast<double>(e_of(key_val(static_cast<uint32_t>(sd[i0 + j] >> 32)), mx, T))
+                               : 0.0;
+        (void)seg_scan(v, cl, tmp_d);
+#pragma unroll
+        for (int j = 0; j < kSeg; ++j)
+            if (i0 + j < md && rr - (cbd + cl[j]) <= 0.0) {
+                atomicMin(&s_td, i0 + j);
+                break;
+            }
+        __syncthreads();
+        if (s_td != INT_MAX) {
+            pick_c = sd[s_td];
+        } else {   // (rounding: the bin's end in its sorted order fell short) the next bin's first element
+            int b2 = bd + 1;
+            while (s_start[b2 + 1] == s_start[b2]) ++b2;   // (a nonempty bin at or before bk follows)
+            pick_c = sk[0];
+            if (b2 != bk) {
+                if (tid == 0) sd[0] = 0ull;
+                __syncthreads();
+                for (int i = static_cast<int>(s_start[b2]) + tid; i < static_cast<int>(s_start[b2 + 1]); i += blockDim.x)
+                    atomicMax(reinterpret_cast<unsigned long long *>(&sd[0]), static_cast<unsigned long long>(in[i]));
+                __syncthreads();
+                pick_c = sd[0];
+            }
+        }
+    }
+    if (tid == 0) {
+        const int32_t pick = static_cast<int32_t>(comp_index(pick_c));
+        RowInfo &info = ws.info[r];
+        info.mx = mx;
+        info.sum = sum;
+        info.keep = static_cast<uint32_t>(keep);
+        info.kept = kept;
+        info.pick = pick;
+        ws.picks[r] = pick;
+        fr.last = sk[t];
+    }
+    // the kept prefix for the residual: the bins before bk stay as collected, then bk's first t + 1 in order
+    for (int i = tid; i <= t; i += blockDim.x) cand[gk + i] = sk[i];
+}
+
+// The textbook rule over the candidate path's nuclei (target rows 0..k, draft rows k+1..2k; one workgroup): as
+// textbook_finish, with p(x) and q(x) read from the kept prefixes. At a rejection the target's kept prefix (p is 0
+// elsewhere) is put in index order by 256 buckets of indices and ranks within them, its residuals summed by one scan.
+// st[0] = emitted, or 0 when a row was not decided here (out untouched).
+constexpr int kBuckets = 256;
+constexpr int kRankMax = 512;   // a bucket of more elements is sorted by the bitonic network instead
+
+__global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, int k, float T, FastU fu,
+                                                              int32_t *__restrict__ out, int *__restrict__ st) {
+    extern __shared__ uint64_t lds[];   // [kFCap] (index << 32) | position by bucket, [kFCap] in index order,
+                                        // [kFCap] doubles: the residuals by position
+    uint64_t *grp = lds, *ord = lds + kFCap;
+    double *res = reinterpret_cast<double *>(lds + 2 * kFCap);
+    __shared__ uint32_t bcnt[kBuckets], bstart[kBuckets + 1], bcur[kBuckets];
+    __shared__ uint32_t tmp_u[16];
+    __shared__ double tmp_d[16];
+    __shared__ int s_rej, s_first, s_last, s_big;
+    const int tid = threadIdx.x, nthr = blockDim.x, R = 2 * k + 1;
+    if (tid < 64) {
+        const uint64_t bad = __ballot(tid < R && ws.fr[min(tid, R - 1)].ok == 0);
+        if (tid == 0) s_rej = bad ? -1 : INT_MAX;
+    }
+    if (tid < kBuckets) {
+        bcnt[tid] = 0u;
+        bcur[tid] = 0u;
+    }
+    __syncthreads();
+    if (s_rej < 0) {
+        if (tid == 0) st[0] = 0;
+        return;
+    }
+    if (tid < k) {   // draft i stands with probability min(1, p_i(d) / q_i(d))
+        const int i = tid, d = ws.picks[k + 1 + i];
+        const RowInfo &P = ws.info[i], &Q = ws.info[k + 1 + i];
+        const float lq = rs.row(k + 1 + i)[d], lp = rs.row(i)[d];
+        const double qd = static_cast<double>(e_of(lq, Q.mx, T)) / Q.kept;
+        const bool in_p = comp_of(lp, static_cast<uint32_t>(d)) >= ws.fr[i].last;
+        const double pd = in_p ? static_cast<double>(e_of(lp, P.mx, T)) / P.kept : 0.0;
+        if (!(static_cast<double>(fu.acc[i]) * qd < pd)) atomicMin(&s_rej, i);
+    }
+    __syncthreads();
+    const int rej = s_rej;
+    if (rej == INT_MAX) {   // every draft stood: the bonus, target row k's draw
+        for (int i = tid; i < k; i += nthr) out[i] = ws.picks[k + 1 + i];
+        if (tid == 0) {
+            out[k] = ws.picks[k];
+            st[0] = k + 1;
+        }
+        return;
+    }
+    const RowInfo &P = ws.info[rej], &Q = ws.info[k + 1 + rej];
+    const int keep = static_cast<int>(P.keep);
+    const uint64_t *pc = ws.cand + static_cast<int64_t>(rej) * kMaxCand;
+    const float *tq = rs.row(k + 1 + rej);
+    const uint64_t lastq = ws.fr[k + 1 + rej].last;
+    const float bscale = static_cast<float>(kBuckets) / static_cast<float>(rs.V);
+    auto bucket = [&](uint32_t x) { return min(static_cast<int>(static_cast<float>(x) * bscale), kBuckets - 1); };
+    for (int j = tid; j < keep; j += nthr) {   // max(0, p - q) of the kept prefix's element j; its bucket counted
+        const uint64_t c = pc[j];
+        const uint32_t x = comp_index(c);
+        const float lq = tq[x];
+        const double p = static_cast<double>(e_of(key_val(static_cast<uint32_t>(c >> 32)), P.mx, T)) / P.kept;
+        const double q = comp_of(lq, x) >= lastq ? static_cast<double>(e_of(lq, Q.mx, T)) / Q.kept : 0.0;
+        res[j] = fmax(0.0, p - q);
+        ord[j] = (static_cast<uint64_t>(x) << 32) | static_cast<uint32_t>(j);
+        atomicAdd(&bcnt[bucket(x)], 1u);
+    }
+    __syncthreads();
+    {
+        const uint32_t c = tid < kBuckets ? bcnt[tid] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan(c, tmp_u, tot);
+        if (tid < kBuckets) bstart[tid] = ex;
+        if (tid == 0) {
+            bstart[kBuckets] = tot;
+            s_big = 0;
+        }
+        __syncthreads();
+        if (c > static_cast<uint32_t>(kRankMax)) s_big = 1;
+    }
+    for (int j = tid; j < keep; j += nthr) {   // grouped by bucket
+        const uint64_t o = ord[j];
+        const int b = bucket(static_cast<uint32_t>(o >> 32));
+        grp[bstart[b] + atomicAdd(&bcur[b], 1u)] = o;
+    }
+    __syncthreads();
+    if (!s_big) {
+        rank_place<false>(grp, ord, keep, [&](int, uint64_t c, uint32_t &g0, uint32_t &g1) {
+            const int b = bucket(static_cast<uint32_t>(c >> 32));
+            g0 = bstart[b];
+            g1 = bstart[b + 1];
+        });
+        __syncthreads();
+    } else {   // (index ascending: ~index descending)
+        int Pn = 1;
+        while (Pn < keep) Pn <<= 1;
+        for (int j = tid; j < Pn; j += nthr)
+            ord[j] = j < keep ? (grp[j] ^ 0xFFFFFFFF00000000ull) : 0ull;
+        __syncthreads();
+        bitonic_desc(ord, Pn);
+        for (int j = tid; j < keep; j += nthr) ord[j] ^= 0xFFFFFFFF00000000ull;
+        __syncthreads();
+    }
+    const int i0 = tid * kSeg;
+    double rv[kSeg], cl[kSeg];
+    double loc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+        rv[j] = i0 + j < keep ? res[static_cast<uint32_t>(ord[i0 + j])] : 0.0;
+        loc += rv[j];
+        cl[j] = loc;
+    }
+    double total;
+    const double ex = block_excl_scan(loc, tmp_d, total);
+    int pick;
+    if (!(total > 0.0)) {
+        pick = ws.picks[rej];   // no residual mass: the target row's own draw
+    } else {
+        const double goal = static_cast<double>(fu.res) * total;
+        if (tid == 0) {
+            s_first = INT_MAX;
+            s_last = -1;
+        }
+        __syncthreads();
+        int last = -1;
+#pragma unroll
+        for (int j = 0; j < kSeg; ++j)
+            if (rv[j] > 0.0) last = i0 + j;
+        if (last >= 0) atomicMax(&s_last, last);
+#pragma unroll
+        for (int j = 0; j < kSeg; ++j)
+            if (rv[j] > 0.0 && cl[j] + ex >= goal) {
+                atomicMin(&s_first, i0 + j);
+                break;
+            }
+        __syncthreads();
+        const int at = s_first != INT_MAX ? s_first : s_last;   // rounding past the end: the last positive weight
+        pick = static_cast<int>(ord[at] >> 32);
+    }
+    for (int i = tid; i < rej; i += nthr) out[i] = ws.picks[k + 1 + i];
+    if (tid == 0) {
+        out[rej] = pick;
+        st[0] = rej + 1;
+    }
+}
+
 // ---------------------------------------------------------------- host side
 struct Workspace {
     void *p = nullptr;
@@ -1018,6 +1638,9 @@ size_t ws_bytes(int R, size_t io) {
     b += align256(16 * static_cast<size_t>(R) + 4 * static_cast<size_t>(R));
     b += align256(static_cast<size_t>(R) * kMaxCand * 8);
     b += align256(static_cast<size_t>(R) * 2 * kList * 8);
+    b += align256(sizeof(FStat) * kMaxChunks * R);
+    b += align256(sizeof(FRow) * R);
+    b += align256(4 * static_cast<size_t>(kFB) * R);
     b += align256(8 * static_cast<size_t>(R) + io);
     return b;
 }
@@ -1042,6 +1665,12 @@ Carved carve(void *base, int R) {
     p += align256(static_cast<size_t>(R) * kMaxCand * 8);
     w.lst = reinterpret_cast<uint64_t *>(p);
     p += align256(static_cast<size_t>(R) * 2 * kList * 8);
+    w.fs = reinterpret_cast<FStat *>(p);
+    p += align256(sizeof(FStat) * kMaxChunks * R);
+    w.fr = reinterpret_cast<FRow *>(p);
+    p += align256(sizeof(FRow) * R);
+    w.fbc = reinterpret_cast<uint32_t *>(p);
+    p += align256(4 * static_cast<size_t>(kFB) * R);
     c.io = p;
     w.u = reinterpret_cast<double *>(p);
     return c;
@@ -1223,14 +1852,40 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
     for (int i = 0; i < k; ++i) hacc[i] = greedy ? 0.0f : u_acc[i];
     *reinterpret_cast<uint32_t *>(hacc + 32) = 0u;   // the finishing count
     const hipStream_t st = stream();
+    const Rows rs = make_rows(target, k + 1, draft, ld, V);
+    int32_t *hout = reinterpret_cast<int32_t *>(hacc + 33);
+    if (!greedy && top_p < 1.0f && rs.S <= kMaxChunks) {
+        // the candidate path, its uniforms as kernel arguments; a row it does not decide sends the call to the walks
+        FastU fu{};
+        for (int r = 0; r < R; ++r) fu.u[r] = hu[r];
+        for (int i = 0; i < k; ++i) fu.acc[i] = u_acc[i];
+        fu.res = u_res;
+        const dim3 grid(rs.S, R), block(kPass);
+        hipLaunchKernelGGL(fast_stats, grid, block, 0, st, rs, c.ws, temperature);
+        hipLaunchKernelGGL(fast_collect<true>, grid, block, 0, st, rs, c.ws, temperature, top_p, 0);
+        static int granted_n = 0, granted_t = 0;
+        const size_t lds_n = static_cast<size_t>(kFCap) * 32, lds_t = static_cast<size_t>(kFCap) * 24;
+        if (lds_grant(reinterpret_cast<const void *>(&fast_nucleus), lds_n, granted_n) != 0 ||
+            lds_grant(reinterpret_cast<const void *>(&fast_textbook), lds_t, granted_t) != 0)
+            return -1;
+        hipLaunchKernelGGL(fast_nucleus, dim3(R), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, fu);
+        hipLaunchKernelGGL(fast_textbook, dim3(1), dim3(kSortThreads), lds_t, st, rs, c.ws, k, temperature, fu, dout,
+                           dst);
+        GV_CHECK_HIP(hipGetLastError());
+        GV_CHECK_HIP(hipMemcpyAsync(hout, dout, 33 * 4, hipMemcpyDeviceToHost, st));
+        GV_CHECK_HIP(hipStreamSynchronize(st));
+        const int emitted = hout[32];
+        if (emitted > 0) {
+            for (int i = 0; i < emitted; ++i) out[i] = hout[i];
+            return emitted;
+        }
+    }
     GV_CHECK_HIP(hipMemcpyAsync(c.io, pin, io, hipMemcpyHostToDevice, st));
     const float Tn = greedy ? 0.0f : temperature;
-    const Rows rs = make_rows(target, k + 1, draft, ld, V);
     if (nuclei(rs, R, Tn, top_p, 0, 0, c.ws, st) != 0) return -1;
     hipLaunchKernelGGL(textbook_finish, dim3(greedy ? 1 : rs.S), dim3(kPass), 0, st, rs, c.ws, k, greedy, temperature,
                        dacc, u_res, rsum, ddone, dout, dst);
     GV_CHECK_HIP(hipGetLastError());
-    int32_t *hout = reinterpret_cast<int32_t *>(hacc + 33);
     GV_CHECK_HIP(hipMemcpyAsync(hout, dout, 33 * 4, hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
     const int emitted = hout[32];
