@@ -135,6 +135,7 @@ SIGNATURES = {
                                    _c.c_int, _P, _P, _P]),
     "gv_accept_match_ex": (_c.c_int, [_P, _c.c_int64, _c.c_int, _P, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
                                       _c.c_int, _P, _P, _c.c_int, _c.c_float, _P, _c.c_int, _P, _P]),
+    "gv_sampler_paths": (_c.c_int, [_P, _P]),
     "gv_accept_textbook": (_c.c_int, [_P, _P, _c.c_int64, _c.c_int, _c.c_int, _c.c_float, _c.c_float, _c.c_int,
                                       _P, _P, _c.c_float, _P]),
 }
@@ -349,6 +350,13 @@ def accept_textbook(target, draft, temperature, top_p, greedy, u_draft=None, u_a
                                    ua.ctypes.data_as(_P), float(u_res), out.ctypes.data_as(_P))
     check(-1 if rc < 0 else 0, "gv_accept_textbook")
     return out[:rc].copy()
+
+
+def sampler_paths():
+    """(calls the textbook rule's candidate path decided, calls that ran the full walks) since the library loaded"""
+    a, b = _c.c_int64(0), _c.c_int64(0)
+    check(_lib().gv_sampler_paths(_c.byref(a), _c.byref(b)), "gv_sampler_paths")
+    return a.value, b.value
 
 
 class Pack:

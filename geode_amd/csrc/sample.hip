@@ -28,6 +28,7 @@
 // sequential sums in the last bits (~1e-15 relative), which moves a decision only when a uniform or top_p falls that
 // close to a boundary; expf is the device's (within 1 ulp of glibc's).
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <vector>
@@ -1612,6 +1613,8 @@ struct Pinned {
     }
 };
 
+std::atomic<int64_t> g_path_candidate{0}, g_path_walks{0};   // gv_accept_textbook calls by path
+
 Workspace &ws_mem() {
     static Workspace w;
     return w;
@@ -1734,6 +1737,13 @@ int nuclei(const Rows &rs, int R, float T, float top_p, int top_k, int cap, cons
 using namespace gv;
 
 extern "C" {
+
+int gv_sampler_paths(int64_t *candidate, int64_t *walks) {
+    GV_REQUIRE(candidate && walks, "gv_sampler_paths: null argument");
+    *candidate = g_path_candidate.load(std::memory_order_relaxed);
+    *walks = g_path_walks.load(std::memory_order_relaxed);
+    return 0;
+}
 
 int gv_sample_rows(const float *logits, int64_t ld, int rows, int V, float temperature, float top_p, int top_k,
                    int cap, const double *u, int32_t *out) {
@@ -1869,17 +1879,19 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
             lds_grant(reinterpret_cast<const void *>(&fast_textbook), lds_t, granted_t) != 0)
             return -1;
         hipLaunchKernelGGL(fast_nucleus, dim3(R), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, fu);
-        hipLaunchKernelGGL(fast_textbook, dim3(1), dim3(kSortThreads), lds_t, st, rs, c.ws, k, temperature, fu, dout,
-                           dst);
+        // (the results straight into the pinned buffer: no copy launch)
+        hipLaunchKernelGGL(fast_textbook, dim3(1), dim3(kSortThreads), lds_t, st, rs, c.ws, k, temperature, fu, hout,
+                           hout + 32);
         GV_CHECK_HIP(hipGetLastError());
-        GV_CHECK_HIP(hipMemcpyAsync(hout, dout, 33 * 4, hipMemcpyDeviceToHost, st));
         GV_CHECK_HIP(hipStreamSynchronize(st));
         const int emitted = hout[32];
         if (emitted > 0) {
             for (int i = 0; i < emitted; ++i) out[i] = hout[i];
+            g_path_candidate.fetch_add(1, std::memory_order_relaxed);
             return emitted;
         }
     }
+    g_path_walks.fetch_add(1, std::memory_order_relaxed);
     GV_CHECK_HIP(hipMemcpyAsync(c.io, pin, io, hipMemcpyHostToDevice, st));
     const float Tn = greedy ? 0.0f : temperature;
     if (nuclei(rs, R, Tn, top_p, 0, 0, c.ws, st) != 0) return -1;

@@ -1,0 +1,108 @@
+"""The textbook rule's two paths on the GPU against the oracle (po.accept_textbook): the candidate path (a nucleus of
+top_p < 1 decided among the elements above one logit) and the full walks it hands a call to when a row's prefix does
+not end among them. Each case checks the emitted tokens exactly and which path served the call (gv_sampler_paths).
+
+Cases: C2's trial shape; small, ragged and one-chunk vocabularies; k = 1 and k = 31 (63 rows); a tiny top_p (one
+kept token); a peaked and a flat temperature; coarse logits (ties inside the collected bins); a rejection with no
+residual mass (draft = target, u_acc = 1: the target row's own draw); rows whose nucleus spans most of the
+vocabulary and top_p = 1 (the walks)."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gv():
+    import geode_amd
+
+    geode_amd.init(0)
+    return geode_amd
+
+
+def _trial(seed, k, V, sigma=3.0, noise=0.5, grid=None):
+    target = po.normal(seed, (k + 1) * V, sigma).reshape(k + 1, V)
+    draft = target[:k] + po.normal(seed + 1, k * V, noise).reshape(k, V)
+    if grid:
+        target = (np.round(target / grid) * grid).astype(np.float32)
+        draft = (np.round(draft / grid) * grid).astype(np.float32)
+    rng = np.random.default_rng(seed + 2)
+    return target, draft, rng.random(k).astype(np.float32), rng.random(k).astype(np.float32), np.float32(rng.random())
+
+
+def _run(gv, target, draft, T, top_p, ud, ua, ur):
+    c0, w0 = gv.sampler_paths()
+    got = gv.accept_textbook(target, draft, T, top_p, False, ud, ua, ur)
+    c1, w1 = gv.sampler_paths()
+    want = po.accept_textbook(target, draft, T, top_p, False, ud, ua, ur)
+    assert list(got) == list(want), (list(got), list(want))
+    assert (c1 - c0) + (w1 - w0) == 1
+    return "candidate" if c1 > c0 else "walks"
+
+
+def _rejections(gv, target, draft, T, top_p, ud, ur):
+    """every draft position rejected in turn (the residual draw), then all accepted (the bonus)"""
+    k = draft.shape[0]
+    paths = set()
+    for first in range(min(k, 4) + 1):
+        ua = np.zeros(k, np.float32)
+        if first < k:
+            ua[first] = np.float32(0.999999)
+        paths.add(_run(gv, target, draft, T, top_p, ud, ua, ur))
+    return paths
+
+
+@pytest.mark.parametrize("seed", [5, 6, 7])
+def test_c2_shape_takes_the_candidate_path(gv, seed):
+    target, draft, ud, ua, ur = _trial(seed * 10, 4, 151936)
+    assert _run(gv, target, draft, 0.7, 0.95, ud, ua, ur) == "candidate"
+    assert _rejections(gv, target, draft, 0.7, 0.95, ud, ur) == {"candidate"}
+
+
+@pytest.mark.parametrize("V", [1000, 4096, 4097, 12289, 50000])
+def test_small_and_ragged_vocabularies(gv, V):
+    target, draft, ud, _, ur = _trial(300 + V, 4, V)
+    assert _rejections(gv, target, draft, 0.7, 0.95, ud, ur) == {"candidate"}
+
+
+@pytest.mark.parametrize("k", [1, 31])
+def test_chain_lengths(gv, k):
+    target, draft, ud, ua, ur = _trial(400 + k, k, 20000)
+    assert _run(gv, target, draft, 0.7, 0.95, ud, ua, ur) == "candidate"
+    ua[:] = 0.0   # every draft stands: the bonus from row k
+    assert _run(gv, target, draft, 0.7, 0.95, ud, ua, ur) == "candidate"
+
+
+def test_tiny_top_p(gv):
+    target, draft, ud, _, ur = _trial(500, 4, 151936)
+    assert _rejections(gv, target, draft, 0.7, 1e-4, ud, ur) == {"candidate"}
+
+
+@pytest.mark.parametrize("T", [0.05, 2.0])
+def test_temperatures(gv, T):
+    target, draft, ud, _, ur = _trial(600, 4, 151936)
+    _rejections(gv, target, draft, T, 0.95, ud, ur)   # (either path; the tokens must match)
+
+
+def test_ties_inside_the_collected_bins(gv):
+    """logits on a 1/8 grid: equal values straddle the top-p prefix's end and the draws, taken in index order"""
+    target, draft, ud, _, ur = _trial(700, 4, 151936, grid=0.125)
+    assert _rejections(gv, target, draft, 0.7, 0.95, ud, ur) == {"candidate"}
+
+
+def test_rejection_without_residual_mass(gv):
+    """draft = target and u_acc = 1: q(d) = p(d) and the first draft is rejected with max(0, p - q) = 0 everywhere,
+    so the emitted token is the target row's own draw"""
+    target, _, ud, _, ur = _trial(800, 4, 151936)
+    draft = target[:4].copy()
+    ua = np.ones(4, np.float32)
+    assert _run(gv, target, draft, 0.7, 0.95, ud, ua, ur) == "candidate"
+
+
+def test_flat_rows_and_top_p_one_take_the_walks(gv):
+    target, draft, ud, _, ur = _trial(900, 4, 151936, sigma=1.0)   # T = 1 on N(0, 1): most of the vocabulary
+    assert _rejections(gv, target, draft, 1.0, 0.95, ud, ur) == {"walks"}
+    target, draft, ud, _, ur = _trial(901, 4, 151936)
+    assert _rejections(gv, target, draft, 0.7, 1.0, ud, ur) == {"walks"}
