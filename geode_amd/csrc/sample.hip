@@ -1046,6 +1046,16 @@ __device__ void bitonic_desc(uint64_t *a, int P) {
         }
 }
 
+// one LDS atomic a wave: the lowest (highest) pos among the lanes where hit holds, pos rising with the lane
+__device__ inline void wave_min_hit(bool hit, int pos, int *dst) {
+    const uint64_t b = __ballot(hit);
+    if (b && (threadIdx.x & 63) == __builtin_ctzll(b)) atomicMin(dst, pos);
+}
+__device__ inline void wave_max_hit(bool hit, int pos, int *dst) {
+    const uint64_t b = __ballot(hit);
+    if (b && (threadIdx.x & 63) == 63 - __builtin_clzll(b)) atomicMax(dst, pos);
+}
+
 // grid (S, R), kPass threads
 __global__ __launch_bounds__(kPass) void fast_stats(Rows rs, Ws ws, float T) {
     __shared__ uint32_t scnt[kFB];
@@ -1182,7 +1192,7 @@ __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, f
     } else {
         hit = tid < kFB && cex + bc >= static_cast<uint32_t>(K);
     }
-    if (hit) atomicMin(&s_first, tid);
+    wave_min_hit(hit, tid, &s_first);
     if (tid < kFB) {   // bin j's elements go to [cex, cex + bc) of the row's list (the counts are whole for j <= jc)
         s_start[tid] = cex;
         s_end[tid] = cex + bc;
@@ -1270,18 +1280,87 @@ __device__ inline double seg_scan(const double (&v)[kSeg], double (&cl)[kSeg], d
     return tot;
 }
 
-// in[g, g + m) put in descending order into out[0, m) by rank (keys distinct); every thread; the caller synchronises
-__device__ inline void rank_sort_desc(const uint64_t *in, int g, int m, uint64_t *out) {
-    for (int i = threadIdx.x; i < m; i += blockDim.x) {
-        const uint64_t c = in[g + i];
-        uint32_t rk[8] = {};   // (eight loads in flight)
-        int j = 0;
-        for (; j + 8 <= m; j += 8)
+// how many of in[j0 + G i] < in[j1] exceed c (eight loads in flight)
+__device__ inline uint32_t count_above(const uint64_t *in, int j0, int j1, int G, uint64_t c) {
+    uint32_t rk[8] = {};
+    int j = j0;
+    for (; j + 7 * G < j1; j += 8 * G)
 #pragma unroll
-            for (int q = 0; q < 8; ++q) rk[q] += in[g + j + q] > c;
-        for (; j < m; ++j) rk[0] += in[g + j] > c;
-        out[((rk[0] + rk[1]) + (rk[2] + rk[3])) + ((rk[4] + rk[5]) + (rk[6] + rk[7]))] = c;
+        for (int q = 0; q < 8; ++q) rk[q] += in[j + q * G] > c;
+    for (; j < j1; j += G) rk[0] += in[j] > c;
+    return ((rk[0] + rk[1]) + (rk[2] + rk[3])) + ((rk[4] + rk[5]) + (rk[6] + rk[7]));
+}
+
+
+// in[g, g + m) put in descending order into out[0, m) by rank (keys distinct); every thread of the workgroup; the
+// caller synchronises. Up to half the threads' count of elements: G adjacent lanes an element, lane q counting the
+// others at q, q + G, .. (adjacent words for adjacent lanes: no LDS bank conflicts), their counts added across them.
+__device__ inline void rank_sort_desc(const uint64_t *in, int g, int m, uint64_t *out) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    if (2 * m <= nthr) {
+        int lg = 1;   // G = 2^lg lanes an element
+        while ((2 << lg) * m <= nthr && lg < 6) ++lg;
+        const int G = 1 << lg, i = tid >> lg, q = tid & (G - 1);
+        const uint64_t c = i < m ? in[g + i] : 0ull;
+        uint32_t rk = i < m ? count_above(in, g + q, g + m, G, c) : 0u;
+        for (int o = 1; o < G; o <<= 1) rk += __shfl_xor(rk, o, 64);
+        if (i < m && q == 0) out[rk] = c;
+        return;
     }
+    for (int i = tid; i < m; i += nthr) {
+        const uint64_t c = in[g + i];
+        out[count_above(in, g, g + m, 1, c)] = c;
+    }
+}
+
+// The first position p < m where pred(base + v(0) + .. + v(p)) holds, into s_pos (INT_MAX: none), the running sum
+// there into s_cum; every thread of the workgroup, synchronised on return. Up to 512 positions one wave scans them
+// (eight a lane); more (up to kFCap) the workgroup.
+template <typename Val, typename Pred>
+__device__ void first_reach(int m, double base, Val val, Pred pred, double *tmp, int &s_pos, double &s_cum) {
+    const int tid = threadIdx.x;
+    if (tid == 0) s_pos = INT_MAX;
+    if (m <= 512) {
+        if (tid < 64) {
+            double cl[8], loc = 0.0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                loc += 8 * tid + j < m ? val(8 * tid + j) : 0.0;
+                cl[j] = loc;
+            }
+            const double ex = base + wave_incl_scan(loc) - loc;
+            int hit = -1;
+            double at = 0.0;
+#pragma unroll
+            for (int j = 7; j >= 0; --j)
+                if (8 * tid + j < m && pred(ex + cl[j])) {
+                    hit = j;
+                    at = ex + cl[j];
+                }
+            const uint64_t bal = __ballot(hit >= 0);
+            if (bal && tid == __builtin_ctzll(bal)) {
+                s_pos = 8 * tid + hit;
+                s_cum = at;
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    const int i0 = tid * kSeg;
+    double v[kSeg], cl[kSeg];
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) v[j] = i0 + j < m ? val(i0 + j) : 0.0;
+    (void)seg_scan(v, cl, tmp);
+    int hit = INT_MAX;
+#pragma unroll
+    for (int j = kSeg - 1; j >= 0; --j)
+        if (i0 + j < m && pred(base + cl[j])) hit = i0 + j;
+    wave_min_hit(hit != INT_MAX, hit, &s_pos);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j)
+        if (i0 + j == s_pos) s_cum = base + cl[j];
+    __syncthreads();
 }
 
 __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, float T, float top_p, FastU fu) {
@@ -1293,7 +1372,7 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
     __shared__ double tmp_d[16];
     __shared__ double e_part[kMaxChunks];
     __shared__ int s_bk, s_bd, s_t, s_td;
-    __shared__ double s_sum;
+    __shared__ double s_sum, s_kept, s_dcum;
     const int r = blockIdx.x, tid = threadIdx.x;
     FRow &fr = ws.fr[r];
     const int n = static_cast<int>(fr.n);
@@ -1310,10 +1389,6 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
         if (tid == kFB - 1) s_start[kFB] = incl;
     }
     if (tid < rs.S) e_part[tid] = ws.psum[r * kMaxChunks + tid];
-    if (tid == 0) {
-        s_t = INT_MAX;
-        s_td = INT_MAX;
-    }
     const int i0 = tid * kSeg;
     double v[kSeg], cl[kSeg];
 #pragma unroll
@@ -1349,29 +1424,17 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
     const int gk = static_cast<int>(s_start[bk]), mk = static_cast<int>(s_start[bk + 1]) - gk;
     rank_sort_desc(in, gk, mk, sk);
     __syncthreads();
-    const double cb = before(bk);
-#pragma unroll
-    for (int j = 0; j < kSeg; ++j)
-        v[j] = i0 + j < mk ? static_cast<double>(e_of(key_val(static_cast<uint32_t>(sk[i0 + j] >> 32)), mx, T)) : 0.0;
-    (void)seg_scan(v, cl, tmp_d);
-#pragma unroll
-    for (int j = 0; j < kSeg; ++j)
-        if (i0 + j < mk && (cb + cl[j]) / sum >= target) {
-            atomicMin(&s_t, i0 + j);
-            break;
-        }
-    __syncthreads();
+    auto e_sorted = [&](const uint64_t *a) {
+        return [=](int p) { return static_cast<double>(e_of(key_val(static_cast<uint32_t>(a[p] >> 32)), mx, T)); };
+    };
+    first_reach(mk, before(bk), e_sorted(sk), [=](double c) { return c / sum >= target; }, tmp_d, s_t, s_kept);
     const int t = s_t;
     if (t == INT_MAX) {   // (rounding: the bin's end in its sorted order fell short)
         if (tid == 0) fr.ok = 0;
         return;
     }
     const int keep = gk + t + 1;
-#pragma unroll
-    for (int j = 0; j < kSeg; ++j)
-        if (i0 + j == t) s_sum = cb + cl[j];   // (every thread has read s_sum)
-    __syncthreads();
-    const double kept = s_sum, rr = kept * fu.u[r];
+    const double kept = s_kept, rr = kept * fu.u[r];
     if (tid < 64) {   // the draw's bin: the first before bk whose end reaches rr, else bk
         const bool hit = tid < bk && s_start[tid + 1] > s_start[tid] && rr - end_of(tid) <= 0.0;
         const uint64_t m = __ballot(hit);
@@ -1380,32 +1443,15 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
     __syncthreads();
     const int bd = s_bd;
     uint64_t pick_c;
+    const auto drawn = [=](double c) { return rr - c <= 0.0; };
     if (bd == bk) {
-#pragma unroll
-        for (int j = 0; j < kSeg; ++j)
-            if (i0 + j <= t && rr - (cb + cl[j]) <= 0.0) {
-                atomicMin(&s_td, i0 + j);
-                break;
-            }
-        __syncthreads();
+        first_reach(t + 1, before(bk), e_sorted(sk), drawn, tmp_d, s_td, s_dcum);
         pick_c = sk[s_td != INT_MAX ? s_td : t];   // rounding past the end: the last kept
     } else {
         const int gd = static_cast<int>(s_start[bd]), md = static_cast<int>(s_start[bd + 1]) - gd;
         rank_sort_desc(in, gd, md, sd);
         __syncthreads();
-        const double cbd = before(bd);
-#pragma unroll
-        for (int j = 0; j < kSeg; ++j)
-            v[j] = i0 + j < md ? static_cast<double>(e_of(key_val(static_cast<uint32_t>(sd[i0 + j] >> 32)), mx, T))
-                               : 0.0;
-        (void)seg_scan(v, cl, tmp_d);
-#pragma unroll
-        for (int j = 0; j < kSeg; ++j)
-            if (i0 + j < md && rr - (cbd + cl[j]) <= 0.0) {
-                atomicMin(&s_td, i0 + j);
-                break;
-            }
-        __syncthreads();
+        first_reach(md, before(bd), e_sorted(sd), drawn, tmp_d, s_td, s_dcum);
         if (s_td != INT_MAX) {
             pick_c = sd[s_td];
         } else {   // (rounding: the bin's end in its sorted order fell short) the next bin's first element
@@ -1561,17 +1607,15 @@ __global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, in
             s_last = -1;
         }
         __syncthreads();
-        int last = -1;
+        int last = -1, first = INT_MAX;
 #pragma unroll
         for (int j = 0; j < kSeg; ++j)
             if (rv[j] > 0.0) last = i0 + j;
-        if (last >= 0) atomicMax(&s_last, last);
 #pragma unroll
-        for (int j = 0; j < kSeg; ++j)
-            if (rv[j] > 0.0 && cl[j] + ex >= goal) {
-                atomicMin(&s_first, i0 + j);
-                break;
-            }
+        for (int j = kSeg - 1; j >= 0; --j)
+            if (rv[j] > 0.0 && cl[j] + ex >= goal) first = i0 + j;
+        wave_max_hit(last >= 0, last, &s_last);
+        wave_min_hit(first != INT_MAX, first, &s_first);
         __syncthreads();
         const int at = s_first != INT_MAX ? s_first : s_last;   // rounding past the end: the last positive weight
         pick = static_cast<int>(ord[at] >> 32);
