@@ -1071,7 +1071,6 @@ __global__ __launch_bounds__(kPass) void fast_stats(Rows rs, Ws ws, float T) {
         scnt[tid] = 0u;
         sw[tid] = 0.0f;
     }
-    if (w == 0 && tid < kFB) ws.fbc[r * kFB + tid] = 0u;   // (the collect pass counts from here)
     uint64_t best = 0;
 #pragma unroll
     for (int u = 0; u < kLoads; ++u)
@@ -1114,9 +1113,9 @@ template <bool MASS>
 __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, float top_p, int K) {
     __shared__ float sscale[kMaxChunks];
     __shared__ int soff[kMaxChunks];
-    __shared__ uint32_t sq_c[4][64];
+    __shared__ uint32_t sq_c[4][64], sq_b[4][64];
     __shared__ double sq_w[4][64];
-    __shared__ uint32_t s_start[kFB], s_end[kFB], lcnt[kFB], lbase[kFB], lcur[kFB];
+    __shared__ uint32_t s_start[kFB], s_end[kFB], lcur[kFB];
     __shared__ double tmp_d[16];
     __shared__ uint32_t tmp_u[16];
     __shared__ uint32_t s_key;
@@ -1156,9 +1155,10 @@ __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, f
     __syncthreads();
     const float M = key_val(s_key);
     // the row's bin j (from its top): every chunk's bin j - (its offset), thread j + 64 h taking chunks h, h + 4, ..
-    // (their loads all issued at once), the four quarters added in LDS
+    // (their loads all issued at once), the four quarters added in LDS; also the counts of the chunks before this one
+    // (this chunk's first slot in each bin after the bin's start)
     double bw = 0.0;
-    uint32_t bc = 0;
+    uint32_t bc = 0, bb = 0;
     {
         const int j = tid & 63, h = tid >> 6;
         uint32_t cc[kMaxChunks / 4];
@@ -1174,12 +1174,15 @@ __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, f
             const int c = 4 * q + h, jl = j - soff[min(c, S - 1)];
             const bool in = c < S && j < kFB && jl >= 0 && jl < kFB;
             bc += in ? cc[q] : 0u;
+            bb += in && c < w ? cc[q] : 0u;
             if (MASS) bw += in ? static_cast<double>(ww[q]) * static_cast<double>(sscale[c]) : 0.0;
         }
         sq_c[h][j] = bc;
+        sq_b[h][j] = bb;
         sq_w[h][j] = bw;
         __syncthreads();
         bc = tid < kFB ? (sq_c[0][tid] + sq_c[1][tid]) + (sq_c[2][tid] + sq_c[3][tid]) : 0u;
+        bb = tid < kFB ? (sq_b[0][tid] + sq_b[1][tid]) + (sq_b[2][tid] + sq_b[3][tid]) : 0u;
         bw = tid < kFB ? (sq_w[0][tid] + sq_w[1][tid]) + (sq_w[2][tid] + sq_w[3][tid]) : 0.0;
     }
     bool hit;
@@ -1193,10 +1196,9 @@ __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, f
         hit = tid < kFB && cex + bc >= static_cast<uint32_t>(K);
     }
     wave_min_hit(hit, tid, &s_first);
-    if (tid < kFB) {   // bin j's elements go to [cex, cex + bc) of the row's list (the counts are whole for j <= jc)
-        s_start[tid] = cex;
+    if (tid < kFB) {   // bin j's elements go to [cex, cex + bc) of the row's list (the counts are whole for j <= jc),
+        s_start[tid] = cex + bb;   // this chunk's from cex + bb
         s_end[tid] = cex + bc;
-        lcnt[tid] = 0u;
         lcur[tid] = 0u;
     }
     __syncthreads();
@@ -1205,34 +1207,29 @@ __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, f
     const int thr = ok ? s_top - jc : INT_MAX;   // collected: row bin s_top - fbin(l) <= jc
     const float s4 = 4.0f / T;
     double part = 0.0;
-#pragma unroll
-    for (int u = 0; u < kLoads; ++u) {
-        if (c0 + u * kPass + tid >= c1) continue;
-        const int b = fbin(v[u], s4);
-        if (b >= thr) atomicAdd(&lcnt[s_top - b], 1u);
-        if (MASS) part += static_cast<double>(e_of(v[u], M, T));
-    }
-    __syncthreads();
-    if (tid <= jc && ok && lcnt[tid]) lbase[tid] = atomicAdd(&ws.fbc[r * kFB + tid], lcnt[tid]);
-    __syncthreads();
     uint64_t *cand = ws.cand + static_cast<int64_t>(r) * kMaxCand;
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
         const int i = c0 + u * kPass + tid;
+        if (i >= c1) continue;
+        if (MASS) part += static_cast<double>(e_of(v[u], M, T));
         const int b = fbin(v[u], s4);
-        if (i >= c1 || b < thr) continue;
+        if (b < thr) continue;
         const int j = s_top - b;
-        const uint32_t at = s_start[j] + lbase[j] + atomicAdd(&lcur[j], 1u);
+        const uint32_t at = s_start[j] + atomicAdd(&lcur[j], 1u);
         if (at < static_cast<uint32_t>(kFCap)) cand[at] = comp_of(v[u], static_cast<uint32_t>(i));
     }
     if (MASS) {
         const double cs = block_sum(part, tmp_d);
         if (tid == 0) ws.psum[r * kMaxChunks + w] = cs;
     }
-    if (w == 0 && tid == 0) {
-        ws.fr[r].ok = ok;
-        ws.fr[r].n = ok ? s_end[jc] : 0u;
-        ws.fr[r].top_key = s_key;
+    if (w == 0) {   // the row's bins' counts, for the nucleus
+        if (tid < kFB) ws.fbc[r * kFB + tid] = ok && tid <= jc ? s_end[tid] - (s_start[tid] - bb) : 0u;
+        if (tid == 0) {
+            ws.fr[r].ok = ok;
+            ws.fr[r].n = ok ? s_end[jc] : 0u;
+            ws.fr[r].top_key = s_key;
+        }
     }
 }
 
