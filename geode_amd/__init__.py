@@ -353,7 +353,8 @@ def accept_textbook(target, draft, temperature, top_p, greedy, u_draft=None, u_a
 
 
 def sampler_paths():
-    """(calls the textbook rule's candidate path decided, calls that ran the full walks) since the library loaded"""
+    """(sampling calls of the acceptance rules the candidate path decided, calls that ran the full walks) since the
+    library loaded"""
     a, b = _c.c_int64(0), _c.c_int64(0)
     check(_lib().gv_sampler_paths(_c.byref(a), _c.byref(b)), "gv_sampler_paths")
     return a.value, b.value

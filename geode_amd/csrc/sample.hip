@@ -144,6 +144,14 @@ struct Rows {   // rows [0, R1) of x1, then rows of x2, ld floats apart; a row i
     }
 };
 
+struct FRow {
+    uint32_t n;        // elements collected (more than kFCap: the row is not decided here)
+    int32_t ok;        // the row is decided here
+    uint64_t last;     // the kept prefix's last element, (key << 32) | ~index: x is kept iff its own is at least this
+    uint32_t top_key;  // the row's largest key
+    int32_t jc;        // the last bin collected (from the top)
+};
+
 struct Ws {   // device arrays of R rows
     RowInfo *info;        // [R]
     uint32_t *pmax;       // [R][kMaxChunks] a chunk's largest key
@@ -733,13 +741,22 @@ __global__ __launch_bounds__(kSortThreads) void cand_nucleus(Rows rs, Ws ws, flo
 
 // ---------------------------------------------------------------- acceptance
 // sample-and-match over the sampled rows (geode.cpp:331-350): out = the stood drafts then the first sampled token
-// that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}
+// that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}. fr
+// (the candidate path's rows, or null): a row it did not decide gives res = {0, 0}.
 __global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ picks, const int32_t *__restrict__ batch,
                                                    int n, const int32_t *__restrict__ stop, int n_stop,
-                                                   int32_t *__restrict__ out, int *__restrict__ res) {
+                                                   int32_t *__restrict__ out, int *__restrict__ res,
+                                                   const FRow *__restrict__ fr) {
     __shared__ int32_t pick[32], next[32];
     __shared__ int stopped[32];
     const int t = threadIdx.x;
+    if (fr && __ballot(t < n && fr[min(t, n - 1)].ok == 0)) {
+        if (t == 0) {
+            res[0] = 0;
+            res[1] = 0;
+        }
+        return;
+    }
     if (t < n) {
         pick[t] = picks[t];
         next[t] = t + 1 < n ? batch[t + 1] : -1;
@@ -998,13 +1015,6 @@ struct FStat {   // a chunk's summary
     float w[kFB];        // their exp((l - m) / T)
 };
 
-struct FRow {
-    uint32_t n;        // elements collected (more than kFCap: the row is not decided here)
-    int32_t ok;        // the row is decided here
-    uint64_t last;     // the kept prefix's last element, (key << 32) | ~index: x is kept iff its own is at least this
-    uint32_t top_key;  // the row's largest key
-    uint32_t unused;
-};
 
 struct FastU {   // kernel arguments: a uniform a row, the acceptance uniforms, the residual's
     double u[64];
@@ -1229,6 +1239,7 @@ __global__ __launch_bounds__(kPass) void fast_collect(Rows rs, Ws ws, float T, f
             ws.fr[r].ok = ok;
             ws.fr[r].n = ok ? s_end[jc] : 0u;
             ws.fr[r].top_key = s_key;
+            ws.fr[r].jc = jc;
         }
     }
 }
@@ -1360,20 +1371,22 @@ __device__ void first_reach(int m, double base, Val val, Pred pred, double *tmp,
     __syncthreads();
 }
 
-__global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, float T, float top_p, FastU fu) {
+template <bool MASS>
+__global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, float T, float top_p, int K, FastU fu) {
     extern __shared__ uint64_t lds[];   // [kFCap] the collected elements (by bin), [kFCap] doubles: the running e
-                                        // sums, [kFCap] the top-p bin sorted, [kFCap] the draw's bin sorted
-    uint64_t *in = lds, *sk = lds + 2 * kFCap, *sd = lds + 3 * kFCap;
+                                        // sums, [kFCap] the bins put in order, each at its own place
+    uint64_t *in = lds, *srt = lds + 2 * kFCap;
     double *cum = reinterpret_cast<double *>(lds + kFCap);
     __shared__ uint32_t s_start[kFB + 1];
     __shared__ double tmp_d[16];
     __shared__ double e_part[kMaxChunks];
     __shared__ int s_bk, s_bd, s_t, s_td;
     __shared__ double s_sum, s_kept, s_dcum;
+    __shared__ unsigned long long s_max;
     const int r = blockIdx.x, tid = threadIdx.x;
     FRow &fr = ws.fr[r];
-    const int n = static_cast<int>(fr.n);
-    if (!fr.ok || n <= 0 || n > kFCap || !(top_p < 1.0f)) {
+    const int n = static_cast<int>(fr.n), jc = fr.jc;
+    if (!fr.ok || n <= 0 || n > kFCap || (MASS ? !(top_p < 1.0f) : n < K)) {
         if (tid == 0) fr.ok = 0;
         return;
     }
@@ -1385,55 +1398,72 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
         if (tid < kFB) s_start[tid] = incl - c;
         if (tid == kFB - 1) s_start[kFB] = incl;
     }
-    if (tid < rs.S) e_part[tid] = ws.psum[r * kMaxChunks + tid];
+    if (MASS && tid < rs.S) e_part[tid] = ws.psum[r * kMaxChunks + tid];
+    for (int i = tid; i < n; i += blockDim.x) in[i] = cand[i];
+    __syncthreads();
+    // the top K (count mode): the bins before the last one, then the last one's first K - (its start) in order
+    const int Kc = MASS ? n : K, gj = static_cast<int>(s_start[jc]);
+    if (!MASS) {
+        rank_sort_desc(in, gj, static_cast<int>(s_start[jc + 1]) - gj, srt + gj);
+        __syncthreads();
+    }
+    auto e_at = [=](uint64_t c) { return static_cast<double>(e_of(key_val(static_cast<uint32_t>(c >> 32)), mx, T)); };
     const int i0 = tid * kSeg;
     double v[kSeg], cl[kSeg];
 #pragma unroll
     for (int j = 0; j < kSeg; ++j) {
-        const uint64_t c = i0 + j < n ? cand[i0 + j] : 0ull;
-        if (i0 + j < n) in[i0 + j] = c;
-        v[j] = i0 + j < n ? static_cast<double>(e_of(key_val(static_cast<uint32_t>(c >> 32)), mx, T)) : 0.0;
+        const int p = i0 + j;
+        v[j] = p < Kc ? e_at(!MASS && p >= gj ? srt[p] : in[p]) : 0.0;
     }
-    (void)seg_scan(v, cl, tmp_d);   // (its barriers publish the starts, e_part and in)
+    const double tot = seg_scan(v, cl, tmp_d);
 #pragma unroll
     for (int j = 0; j < kSeg; ++j)
-        if (i0 + j < n) cum[i0 + j] = cl[j];
-    if (tid == 0) {
+        if (i0 + j < Kc) cum[i0 + j] = cl[j];
+    if (MASS && tid == 0) {
         double t = 0.0;   // the row's e sum, chunks in order
         for (int c = 0; c < rs.S; ++c) t += e_part[c];
         s_sum = t;
     }
     __syncthreads();
-    const double sum = s_sum, target = static_cast<double>(top_p);
-    auto end_of = [&](int b) { return cum[s_start[b + 1] - 1]; };   // (a nonempty bin)
+    const double sum = MASS ? s_sum : tot, target = static_cast<double>(top_p);
+    auto live = [&](int b) { return s_start[b + 1] > s_start[b] && static_cast<int>(s_start[b]) < Kc; };
+    auto end_of = [&](int b) { return cum[min(static_cast<int>(s_start[b + 1]), Kc) - 1]; };   // (a live bin)
     auto before = [&](int b) { return s_start[b] ? cum[s_start[b] - 1] : 0.0; };
+    auto sorted_e = [=](int g) { return [=](int p) { return e_at(srt[g + p]); }; };
     if (tid < 64) {   // the bin where the running sum reaches top_p
-        const bool hit = tid < kFB && s_start[tid + 1] > s_start[tid] && end_of(tid) / sum >= target;
+        const bool hit = top_p < 1.0f && tid < kFB && live(tid) && end_of(tid) / sum >= target;
         const uint64_t m = __ballot(hit);
         if (tid == 0) s_bk = m ? __builtin_ctzll(m) : -1;
     }
     __syncthreads();
-    const int bk = s_bk;
-    if (bk < 0) {   // the prefix goes on past the collected elements
-        if (tid == 0) fr.ok = 0;
-        return;
+    int bk = s_bk, t;
+    double kept;
+    if (bk < 0) {
+        if (MASS) {   // the prefix goes on past the collected elements
+            if (tid == 0) fr.ok = 0;
+            return;
+        }
+        bk = jc;   // (count mode: top_p 1, or never reached: the whole top K kept)
+        t = Kc - 1 - gj;
+        kept = cum[Kc - 1];
+    } else {
+        const int gk = static_cast<int>(s_start[bk]), mk = min(static_cast<int>(s_start[bk + 1]), Kc) - gk;
+        if (MASS || bk != jc) {
+            rank_sort_desc(in, gk, static_cast<int>(s_start[bk + 1]) - gk, srt + gk);
+            __syncthreads();
+        }
+        first_reach(mk, before(bk), sorted_e(gk), [=](double c) { return c / sum >= target; }, tmp_d, s_t, s_kept);
+        if (s_t == INT_MAX) {   // (rounding: the bin's end in its sorted order fell short)
+            if (tid == 0) fr.ok = 0;
+            return;
+        }
+        t = s_t;
+        kept = s_kept;
     }
-    const int gk = static_cast<int>(s_start[bk]), mk = static_cast<int>(s_start[bk + 1]) - gk;
-    rank_sort_desc(in, gk, mk, sk);
-    __syncthreads();
-    auto e_sorted = [&](const uint64_t *a) {
-        return [=](int p) { return static_cast<double>(e_of(key_val(static_cast<uint32_t>(a[p] >> 32)), mx, T)); };
-    };
-    first_reach(mk, before(bk), e_sorted(sk), [=](double c) { return c / sum >= target; }, tmp_d, s_t, s_kept);
-    const int t = s_t;
-    if (t == INT_MAX) {   // (rounding: the bin's end in its sorted order fell short)
-        if (tid == 0) fr.ok = 0;
-        return;
-    }
-    const int keep = gk + t + 1;
-    const double kept = s_kept, rr = kept * fu.u[r];
+    const int gk = static_cast<int>(s_start[bk]), keep = gk + t + 1;
+    const double rr = kept * fu.u[r];
     if (tid < 64) {   // the draw's bin: the first before bk whose end reaches rr, else bk
-        const bool hit = tid < bk && s_start[tid + 1] > s_start[tid] && rr - end_of(tid) <= 0.0;
+        const bool hit = tid < bk && live(tid) && rr - end_of(tid) <= 0.0;
         const uint64_t m = __ballot(hit);
         if (tid == 0) s_bd = m ? __builtin_ctzll(m) : bk;
     }
@@ -1442,26 +1472,27 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
     uint64_t pick_c;
     const auto drawn = [=](double c) { return rr - c <= 0.0; };
     if (bd == bk) {
-        first_reach(t + 1, before(bk), e_sorted(sk), drawn, tmp_d, s_td, s_dcum);
-        pick_c = sk[s_td != INT_MAX ? s_td : t];   // rounding past the end: the last kept
-    } else {
+        first_reach(t + 1, before(bk), sorted_e(gk), drawn, tmp_d, s_td, s_dcum);
+        pick_c = srt[gk + (s_td != INT_MAX ? s_td : t)];   // rounding past the end: the last kept
+    } else {   // (bd < bk <= jc: a whole bin)
         const int gd = static_cast<int>(s_start[bd]), md = static_cast<int>(s_start[bd + 1]) - gd;
-        rank_sort_desc(in, gd, md, sd);
+        rank_sort_desc(in, gd, md, srt + gd);
         __syncthreads();
-        first_reach(md, before(bd), e_sorted(sd), drawn, tmp_d, s_td, s_dcum);
+        first_reach(md, before(bd), sorted_e(gd), drawn, tmp_d, s_td, s_dcum);
         if (s_td != INT_MAX) {
-            pick_c = sd[s_td];
-        } else {   // (rounding: the bin's end in its sorted order fell short) the next bin's first element
+            pick_c = srt[gd + s_td];
+        } else {   // (rounding: the bin's end in its sorted order fell short) the next live bin's first element
             int b2 = bd + 1;
-            while (s_start[b2 + 1] == s_start[b2]) ++b2;   // (a nonempty bin at or before bk follows)
-            pick_c = sk[0];
-            if (b2 != bk) {
-                if (tid == 0) sd[0] = 0ull;
+            while (!live(b2)) ++b2;   // (bk is live)
+            if (b2 == bk) {
+                pick_c = srt[gk];
+            } else {
+                if (tid == 0) s_max = 0ull;
                 __syncthreads();
                 for (int i = static_cast<int>(s_start[b2]) + tid; i < static_cast<int>(s_start[b2 + 1]); i += blockDim.x)
-                    atomicMax(reinterpret_cast<unsigned long long *>(&sd[0]), static_cast<unsigned long long>(in[i]));
+                    atomicMax(&s_max, static_cast<unsigned long long>(in[i]));
                 __syncthreads();
-                pick_c = sd[0];
+                pick_c = s_max;
             }
         }
     }
@@ -1474,10 +1505,10 @@ __global__ __launch_bounds__(kSortThreads) void fast_nucleus(Rows rs, Ws ws, flo
         info.kept = kept;
         info.pick = pick;
         ws.picks[r] = pick;
-        fr.last = sk[t];
+        fr.last = srt[gk + t];
     }
-    // the kept prefix for the residual: the bins before bk stay as collected, then bk's first t + 1 in order
-    for (int i = tid; i <= t; i += blockDim.x) cand[gk + i] = sk[i];
+    if (MASS)   // the kept prefix for the residual: the bins before bk stay as collected, then bk's first t + 1
+        for (int i = tid; i <= t; i += blockDim.x) cand[gk + i] = srt[gk + i];
 }
 
 // The textbook rule over the candidate path's nuclei (target rows 0..k, draft rows k+1..2k; one workgroup): as
@@ -1654,7 +1685,7 @@ struct Pinned {
     }
 };
 
-std::atomic<int64_t> g_path_candidate{0}, g_path_walks{0};   // gv_accept_textbook calls by path
+std::atomic<int64_t> g_path_candidate{0}, g_path_walks{0};   // the acceptance rules' sampling calls by path
 
 Workspace &ws_mem() {
     static Workspace w;
@@ -1865,8 +1896,37 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
         GV_CHECK_HIP(hipGetLastError());
     }
     const Rows rs = make_rows(logits, n, nullptr, ld, V);
+    const int K = top_k > 0 ? std::min(top_k, V) : (cap > 0 ? std::min(cap, V) : V);
+    if (temperature > 0.0f && K < V && K <= kFCap && rs.S <= kMaxChunks) {
+        // the candidate path over the top K; a row it does not decide sends the call to the walks (the penalty
+        // already applied)
+        FastU fu{};
+        for (int i = 0; i < n; ++i) fu.u[i] = u[i];
+        const dim3 grid(rs.S, n), block(kPass);
+        static int granted_n = 0;
+        const size_t lds_n = static_cast<size_t>(kFCap) * 24;
+        if (lds_grant(reinterpret_cast<const void *>(&fast_nucleus<false>), lds_n, granted_n) != 0) return -1;
+        hipLaunchKernelGGL(fast_stats, grid, block, 0, st, rs, c.ws, temperature);
+        hipLaunchKernelGGL(fast_collect<false>, grid, block, 0, st, rs, c.ws, temperature, top_p, K);
+        hipLaunchKernelGGL(fast_nucleus<false>, dim3(n), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, K,
+                           fu);
+        hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, dbatch, n, dstop, n_stop, dout, dres,
+                           static_cast<const FRow *>(c.ws.fr));
+        GV_CHECK_HIP(hipGetLastError());
+        GV_CHECK_HIP(hipMemcpyAsync(hint, dout, 36 * 4, hipMemcpyDeviceToHost, st));
+        GV_CHECK_HIP(hipStreamSynchronize(st));
+        const int emitted = hint[32];
+        if (emitted > 0) {
+            for (int i = 0; i < emitted; ++i) out[i] = hint[i];
+            if (kept) *kept = hint[33];
+            g_path_candidate.fetch_add(1, std::memory_order_relaxed);
+            return emitted;
+        }
+    }
+    if (temperature > 0.0f) g_path_walks.fetch_add(1, std::memory_order_relaxed);
     if (nuclei(rs, n, temperature, top_p, top_k, cap, c.ws, st) != 0) return -1;
-    hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, dbatch, n, dstop, n_stop, dout, dres);
+    hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, dbatch, n, dstop, n_stop, dout, dres,
+                       static_cast<const FRow *>(nullptr));
     GV_CHECK_HIP(hipGetLastError());
     GV_CHECK_HIP(hipMemcpyAsync(hint, dout, 36 * 4, hipMemcpyDeviceToHost, st));
     GV_CHECK_HIP(hipStreamSynchronize(st));
@@ -1915,11 +1975,12 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
         hipLaunchKernelGGL(fast_stats, grid, block, 0, st, rs, c.ws, temperature);
         hipLaunchKernelGGL(fast_collect<true>, grid, block, 0, st, rs, c.ws, temperature, top_p, 0);
         static int granted_n = 0, granted_t = 0;
-        const size_t lds_n = static_cast<size_t>(kFCap) * 32, lds_t = static_cast<size_t>(kFCap) * 24;
-        if (lds_grant(reinterpret_cast<const void *>(&fast_nucleus), lds_n, granted_n) != 0 ||
+        const size_t lds_n = static_cast<size_t>(kFCap) * 24, lds_t = static_cast<size_t>(kFCap) * 24;
+        if (lds_grant(reinterpret_cast<const void *>(&fast_nucleus<true>), lds_n, granted_n) != 0 ||
             lds_grant(reinterpret_cast<const void *>(&fast_textbook), lds_t, granted_t) != 0)
             return -1;
-        hipLaunchKernelGGL(fast_nucleus, dim3(R), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, fu);
+        hipLaunchKernelGGL(fast_nucleus<true>, dim3(R), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, 0,
+                           fu);
         // (the results straight into the pinned buffer: no copy launch)
         hipLaunchKernelGGL(fast_textbook, dim3(1), dim3(kSortThreads), lds_t, st, rs, c.ws, k, temperature, fu, hout,
                            hout + 32);

@@ -378,9 +378,10 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
  * accepted drafts then the extra token; returns their count (or -1). */
 int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int V, int k, float temperature,
                        float top_p, int greedy, const float *u_draft, const float *u_acc, float u_res, int32_t *out);
-/* How many gv_accept_textbook calls the candidate path decided (a nucleus of top_p < 1 found among the elements above
- * one logit, its rows' prefixes ending inside them) and how many ran the full walks, since the library loaded. No
- * reference counterpart: for tests and measurement, to tell which path served a call. */
+/* How many sampling calls of the acceptance rules (gv_accept_textbook; gv_accept_match(_ex) at T > 0) the candidate
+ * path decided (each row's nucleus found among the elements above one logit: a top_p < 1 prefix of the full
+ * vocabulary, or the top_k / cap candidates) and how many ran the full walks, since the library loaded. No reference
+ * counterpart: for tests and measurement, to tell which path served a call. */
 int gv_sampler_paths(int64_t *candidate, int64_t *walks);
 
 #ifdef __cplusplus
