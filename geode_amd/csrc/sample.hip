@@ -349,6 +349,7 @@ __device__ void hist_chunk(int c0, int c1, const float (&v)[kLoads], uint32_t pr
 
 // pass 0: a chunk's largest key and the lowest index holding it; the row's histograms and counters zeroed for the
 // passes after it (a share each workgroup)
+template <bool ZERO>
 __global__ __launch_bounds__(kPass) void max_pass(Rows rs, Ws ws) {
     __shared__ uint64_t red[kPass / 64];
     const int w = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(kPass) void max_pass(Rows rs, Ws ws) {
     const int c0 = w * rs.C, c1 = min(rs.V, c0 + rs.C);
     float v[kLoads];
     preload(row, c0, c1, v);
-    {
+    if (ZERO) {
         uint32_t *h = reinterpret_cast<uint32_t *>(ws.h + r * kHists);
         constexpr int words = static_cast<int>(sizeof(LevelHist) * kHists / 4);
         for (int i = w * kPass + tid; i < words; i += rs.S * kPass) h[i] = 0u;
@@ -1655,6 +1656,35 @@ __global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, in
     }
 }
 
+// The textbook rule when greedy (target rows 0..k, draft rows k+1..2k; one workgroup, their chunks' maxima done):
+// each row's first argmax from its chunks' (a wave a row), then target row i's argmax is emitted while draft row i's
+// agrees, and target row k's when all do (the bonus). st[0] = emitted.
+__global__ __launch_bounds__(kSortThreads) void greedy_finish(Ws ws, int S, int k, int32_t *__restrict__ out,
+                                                              int *__restrict__ st) {
+    __shared__ int32_t pick[64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, R = 2 * k + 1;
+    for (int r = wave; r < R; r += blockDim.x >> 6) {
+        uint64_t best = 0;
+        if (lane < S)
+            best = (static_cast<uint64_t>(ws.pmax[r * kMaxChunks + lane]) << 32) |
+                   (0xFFFFFFFFu - static_cast<uint32_t>(ws.pidx[r * kMaxChunks + lane]));
+        for (int o = 32; o > 0; o >>= 1) best = max(best, static_cast<uint64_t>(__shfl_xor(best, o, 64)));
+        if (lane == 0) pick[r] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    int emitted = 0;
+    for (int i = 0; i < k; ++i) {
+        out[emitted++] = pick[i];
+        if (pick[i] != pick[k + 1 + i]) {
+            st[0] = emitted;
+            return;
+        }
+    }
+    out[emitted++] = pick[k];
+    st[0] = emitted;
+}
+
 // ---------------------------------------------------------------- host side
 struct Workspace {
     void *p = nullptr;
@@ -1775,12 +1805,13 @@ int launch_cand_nucleus(const Rows &rs, const Ws &ws, int R, float T, float top_
 int nuclei(const Rows &rs, int R, float T, float top_p, int top_k, int cap, const Ws &ws, hipStream_t st) {
     GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
     const dim3 grid(rs.S, R), block(kPass);
-    hipLaunchKernelGGL(max_pass, grid, block, 0, st, rs, ws);
     if (T <= 0.0f) {
+        hipLaunchKernelGGL(max_pass<false>, grid, block, 0, st, rs, ws);
         hipLaunchKernelGGL(argmax_reduce, dim3(R), dim3(64), 0, st, ws, rs.S);
         GV_CHECK_HIP(hipGetLastError());
         return 0;
     }
+    hipLaunchKernelGGL(max_pass<true>, grid, block, 0, st, rs, ws);
     const int K = top_k > 0 ? std::min(top_k, rs.V) : (cap > 0 ? std::min(cap, rs.V) : rs.V);
     if (K < rs.V) {   // the top-K candidates: a count walk to the K-th, collected, sorted, the nucleus as written
         GV_REQUIRE(K <= kMaxCand, "sampler: at most 16384 top-k candidates (top_k or cap); 0 takes the whole vocabulary");
@@ -1965,6 +1996,16 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
     const hipStream_t st = stream();
     const Rows rs = make_rows(target, k + 1, draft, ld, V);
     int32_t *hout = reinterpret_cast<int32_t *>(hacc + 33);
+    if (greedy) {   // the chunks' maxima, then the first argmaxes and the decisions, straight into the pinned buffer
+        GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
+        hipLaunchKernelGGL(max_pass<false>, dim3(rs.S, R), dim3(kPass), 0, st, rs, c.ws);
+        hipLaunchKernelGGL(greedy_finish, dim3(1), dim3(kSortThreads), 0, st, c.ws, rs.S, k, hout, hout + 32);
+        GV_CHECK_HIP(hipGetLastError());
+        GV_CHECK_HIP(hipStreamSynchronize(st));
+        const int emitted = hout[32];
+        for (int i = 0; i < emitted; ++i) out[i] = hout[i];
+        return emitted;
+    }
     if (!greedy && top_p < 1.0f && rs.S <= kMaxChunks) {
         // the candidate path, its uniforms as kernel arguments; a row it does not decide sends the call to the walks
         FastU fu{};
