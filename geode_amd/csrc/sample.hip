@@ -12,6 +12,11 @@
 //                                                   max(0, p - q) by inverse CDF in index order; a bonus from p_k
 //                                                   when every draft stands.
 //
+// Two paths. The candidate path (fast_*) decides a nucleus of top_p < 1, or the top-K candidates, among the elements
+// at or above one logit: binned chunk summaries, the elements above the row's threshold bin collected grouped by bin,
+// only the bins where the prefix ends and where the draw lands put in order (its comment below). A row it cannot
+// decide goes to the walks, which decide any row:
+//
 // The sorted order of a row (logit descending, index ascending) is walked without sorting the row: a walk finds the
 // element where the running weight of that order first reaches a target, by three histogram levels of an
 // order-preserving 32-bit key (bits 31..21, 20..10, 9..0), each level a pass of S workgroups a row over the
