@@ -911,10 +911,12 @@ __global__ __launch_bounds__(512) void mixout_kernel(const MixOutArgs a) {
     else if (a.route_role) mixout_route(a, reinterpret_cast<float *>(mix_lds));
 }
 
-// The experts' products on the matrix cores, a workgroup per (slot, row tiles): UP takes gate_up [2F x H] against
-// the post-norm rows of the slot's tokens, DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each
-// pick's rows go to out [pick][rows].
-constexpr int kMoeFlush = 4;   // tiles whose partial sums an expert workgroup holds at once
+// The experts' products on the matrix cores: UP takes gate_up [2F x H] against the post-norm rows of a slot's tokens,
+// DOWN takes down [H x F] against the slot's picks' SwiGLU rows; each pick's rows go to out [pick][rows]. The grid is
+// one round of resident workgroups; the slots' units (row tiles, or matched tile pairs with SW) are laid end to end
+// and each workgroup takes an equal run of them, so a workgroup spans one or two slots (each part loading its
+// slot's rows once) and the chip ends the launch together.
+constexpr int kMoeFlush = 8;   // tiles whose partial sums an expert workgroup holds at once
 
 // The SwiGLU of a matched gate / up tile pair's sums for F tile p (gs, us: the lane's rows 4 lg .. 4 lg + 3 of its
 // column; x their globals g0, g1), m = silu(gate) x up (swiglu_quant_kernel's arithmetic), quantized per 16-value
@@ -976,58 +978,56 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
                                                         const float *__restrict__ globals, int half_rows,
                                                         const _Float16 *__restrict__ act, int64_t act_stride,
                                                         const float *__restrict__ gu, const Slots sl,
-                                                        float *__restrict__ out, int tiles_per_wg, int E1,
-                                                        int max_picks, _Float16 *__restrict__ sw_out,
-                                                        int64_t sw_stride) {
+                                                        float *__restrict__ out, int E1, int max_picks,
+                                                        _Float16 *__restrict__ sw_out, int64_t sw_stride) {
     static_assert(!SW || (UP && kMoeFlush % 2 == 0), "pairs: the up products, whole pairs a flush");
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
-    const int u = blockIdx.x;
-    if (u >= *sl.n_slots) return;
-    const int e = sl.expert[u], start = sl.start[u], cnt = sl.count[u];
-    if (e < 0 || e >= E1 || cnt < 1 || cnt > kMaxRows || start < 0 || start + cnt > max_picks) return;   // no slot
-    const int64_t ntiles = tiles_rows(rows);
-    const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
-    if constexpr (SW) {
-        const int npair = static_cast<int>(ntiles / 2), ppw = tiles_per_wg / 2;
-        const int P0 = static_cast<int>(blockIdx.y) * ppw, P1 = min(P0 + ppw, npair);
-        if (P0 >= npair) return;
-        mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
-            codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
-            K / kSuperK, 0, 2 * (P1 - P0), cnt,
-            [&](int j) { return act + static_cast<int64_t>(sl.pick_token[start + j]) * act_stride; },
-            [](int64_t, int, float) {}, part_lds, tab,
-            [&](int i) -> int64_t { return (i & 1) ? npair + P0 + (i >> 1) : P0 + (i >> 1); }, NoHook{}, NoHook{},
-            flush_with([&](int i0, int i1, const f4 *part, int W) {   // a pair and column tile a wave: sums in wave order
-                for (int o = threadIdx.x; o < (i1 - i0) / 2 * NTT * 64; o += blockDim.x) {
-                    const int q = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
-                    f4 gs = part[((2 * q * W) * NTT + tt) * 64 + ll], us = part[(((2 * q + 1) * W) * NTT + tt) * 64 + ll];
-                    for (int w2 = 1; w2 < W; ++w2) {
-                        gs += part[(((2 * q) * W + w2) * NTT + tt) * 64 + ll];
-                        us += part[(((2 * q + 1) * W + w2) * NTT + tt) * 64 + ll];
+    // (32-bit and uniform: slots x units stay far below 2^31 / the grid)
+    const int ntiles = static_cast<int>(tiles_rows(rows)), npair = ntiles / 2, U = SW ? npair : ntiles;   // units a slot
+    const int total = __builtin_amdgcn_readfirstlane(*sl.n_slots) * U, G = static_cast<int>(gridDim.x);
+    const int x0 = static_cast<int>(blockIdx.x) * total / G, x1 = (static_cast<int>(blockIdx.x) + 1) * total / G;
+    for (int x = x0; x < x1;) {   // (the same sequence in every thread)
+        const int u = x / U, p0 = x - u * U, p1 = min(U, p0 + (x1 - x));
+        x += p1 - p0;
+        const int e = sl.expert[u], start = sl.start[u], cnt = sl.count[u];
+        if (e < 0 || e >= E1 || cnt < 1 || cnt > kMaxRows || start < 0 || start + cnt > max_picks) continue;   // no slot
+        const float g0 = globals[e * 3], g1 = globals[e * 3 + 1], g2 = globals[e * 3 + 2];
+        if constexpr (SW) {   // pairs [p0, p1): gate tile p, up tile npair + p
+            const int P0 = static_cast<int>(p0);
+            mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
+                codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
+                K / kSuperK, 0, static_cast<int>(2 * (p1 - p0)), cnt,
+                [&](int j) { return act + static_cast<int64_t>(sl.pick_token[start + j]) * act_stride; },
+                [](int64_t, int, float) {}, part_lds, tab,
+                [&](int i) -> int64_t { return (i & 1) ? npair + P0 + (i >> 1) : P0 + (i >> 1); }, NoHook{}, NoHook{},
+                flush_with([&](int i0, int i1, const f4 *part, int W) {   // a pair and column tile a wave: sums in wave order
+                    for (int o = threadIdx.x; o < (i1 - i0) / 2 * NTT * 64; o += blockDim.x) {
+                        const int q = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+                        f4 gs = part[((2 * q * W) * NTT + tt) * 64 + ll], us = part[(((2 * q + 1) * W) * NTT + tt) * 64 + ll];
+                        for (int w2 = 1; w2 < W; ++w2) {
+                            gs += part[(((2 * q) * W + w2) * NTT + tt) * 64 + ll];
+                            us += part[(((2 * q + 1) * W + w2) * NTT + tt) * 64 + ll];
+                        }
+                        const int j = tt * 16 + ll % 16;
+                        swiglu_pair_out(gs, us, g0, g1, P0 + (i0 >> 1) + q, j < cnt, sw_out + (start + j) * sw_stride);
                     }
-                    const int j = tt * 16 + ll % 16;
-                    swiglu_pair_out(gs, us, g0, g1, P0 + (i0 >> 1) + q, j < cnt, sw_out + (start + j) * sw_stride);
-                }
-            }));
-        return;
+                }));
+        } else {   // tiles [p0, p1)
+            mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
+                codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
+                K / kSuperK, 0, static_cast<int>(p1 - p0), cnt,
+                [&](int j) {   // UP: the row's act16 operands; DOWN: the pick's SwiGLU operands
+                    const int64_t src = UP ? sl.pick_token[start + j] : start + j;
+                    return act + src * act_stride;
+                },
+                [&](int64_t row, int j, float v) {
+                    const float gl = UP ? (row < half_rows ? g0 : g1) : g2;
+                    out[static_cast<int64_t>(start + j) * rows + row] = v * gl;
+                },
+                part_lds, tab, TileRun{p0});
+        }
     }
-    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * tiles_per_wg;
-    const int64_t t1 = t0 + tiles_per_wg < ntiles ? t0 + tiles_per_wg : ntiles;
-    if (t0 >= ntiles) return;
-    mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
-        codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
-        K / kSuperK, 0, static_cast<int>(t1 - t0),
-        cnt,
-        [&](int j) {   // UP: the row's act16 operands; DOWN: the pick's SwiGLU operands
-            const int64_t src = UP ? sl.pick_token[start + j] : start + j;
-            return act + src * act_stride;
-        },
-        [&](int64_t row, int j, float v) {
-            const float gl = UP ? (row < half_rows ? g0 : g1) : g2;
-            out[static_cast<int64_t>(start + j) * rows + row] = v * gl;
-        },
-        part_lds, tab, TileRun{t0});
 }
 
 // ---------------------------------------------------------------- the decode MoE
@@ -1404,22 +1404,17 @@ struct MoeArgs {
 
 template <int KW, int NTT, int WMAX, bool UP, bool SW>
 int launch_moe_raw(const MoeArgs &a, int waves, hipStream_t st) {
-    const int64_t ntiles = tiles_rows(a.rows);
-    // the slots' tiles over about four times as many workgroups as the chip holds at once (each workgroup loads its
-    // rows' activations once for all its tiles, so longer runs a workgroup read them fewer times); SW: whole pairs
-    const int64_t resident = 256 * std::max(1, 8 / waves);
-    int per = static_cast<int>(
-        std::min<int64_t>(ntiles, std::max<int64_t>(kMoeFlush, (ntiles * a.slots + 4 * resident - 1) / (4 * resident))));
-    if (SW) per += per % 2;
-    const int tiles = static_cast<int>((ntiles + per - 1) / per);
+    // one round of resident workgroups (2 waves a SIMD at these kernels' register use), the slots' units split
+    // evenly among them on the device (the slot count is the route's)
+    const int G = 256 * std::max(1, 8 / waves);
     const size_t lds = static_cast<size_t>(kMoeFlush) * waves * NTT * 1024;   // the waves' partial sums
     static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP, SW>), 76 * 1024, granted) != 0)
+    if (lds_grant(reinterpret_cast<const void *>(&moe_mfma_kernel<KW, NTT, WMAX, UP, SW>), std::max<size_t>(lds, 76 * 1024),
+                  granted) != 0)
         return -1;
-    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP, SW>), dim3(a.slots, tiles), dim3(64 * waves), lds, st,
-                       a.codes, a.scales, a.code_stride, a.scale_stride, a.rows, static_cast<int>(a.cols), a.globals,
-                       a.F, a.act, act_halves(a.cols), a.gu, a.sl, a.out, per, a.E1, a.max_picks, a.sw_out,
-                       act_halves(a.F));
+    hipLaunchKernelGGL((moe_mfma_kernel<KW, NTT, WMAX, UP, SW>), dim3(G), dim3(64 * waves), lds, st, a.codes, a.scales,
+                       a.code_stride, a.scale_stride, a.rows, static_cast<int>(a.cols), a.globals, a.F, a.act,
+                       act_halves(a.cols), a.gu, a.sl, a.out, a.E1, a.max_picks, a.sw_out, act_halves(a.F));
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }
