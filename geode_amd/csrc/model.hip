@@ -1013,7 +1013,23 @@ __global__ __launch_bounds__(64 * WMAX) void moe_mfma_kernel(const uint8_t *__re
                         swiglu_pair_out(gs, us, g0, g1, P0 + (i0 >> 1) + q, j < cnt, sw_out + (start + j) * sw_stride);
                     }
                 }));
-        } else {   // tiles [p0, p1)
+        } else if constexpr (!UP) {   // down, tiles [p0, p1): a lane's four sums are four consecutive rows of its
+                                      // pick's output, one 16-byte store (rows a multiple of 16)
+            mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
+                codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
+                K / kSuperK, 0, p1 - p0, cnt, [&](int j) { return act + static_cast<int64_t>(start + j) * act_stride; },
+                [](int64_t, int, float) {}, part_lds, tab, TileRun{p0}, NoHook{}, NoHook{},
+                flush_with([&](int i0, int i1, const f4 *part, int W) {   // a tile and column tile a lane: wave order
+                    for (int o = threadIdx.x; o < (i1 - i0) * NTT * 64; o += blockDim.x) {
+                        const int i = o / (NTT * 64), tt = (o / 64) % NTT, ll = o % 64;
+                        f4 sum = part[((i * W) * NTT + tt) * 64 + ll];
+                        for (int w2 = 1; w2 < W; ++w2) sum += part[((i * W + w2) * NTT + tt) * 64 + ll];
+                        const int j = tt * 16 + ll % 16;
+                        const int64_t row = static_cast<int64_t>(p0 + i0 + i) * kTileR + 4 * (ll / 16);
+                        if (j < cnt) *reinterpret_cast<f4 *>(out + static_cast<int64_t>(start + j) * rows + row) = sum * g2;
+                    }
+                }));
+        } else {   // up, tiles [p0, p1)
             mfma_tiles<KW, NTT, kSplitK, 0, 3, false, kMoeFlush>(
                 codes + static_cast<size_t>(e) * code_stride, scales + static_cast<size_t>(e) * scale_stride, rows,
                 K / kSuperK, 0, static_cast<int>(p1 - p0), cnt,
