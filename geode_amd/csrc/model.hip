@@ -1559,7 +1559,7 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStre
 // the shared expert's gate logit of each row: the bf16 row . h in the router's eight-sum order; a wave a row
 __global__ __launch_bounds__(256) void gate_rows_kernel(const uint16_t *__restrict__ wrow, int H,
                                                         const float *__restrict__ h, int M, float *__restrict__ logits,
-                                                        int E1, _Float16 *__restrict__ act, int64_t act_stride) {
+                                                        int E1) {
     // LDS: the gate row as fp32 [H], then the waves' rows [4][H]. Every global load is issued before the first store
     // to the LDS (the gate row 8 values a thread, the wave's row 4 values a lane, 2048 values a pass), then the eight
     // fixed-order chains run from the LDS.
@@ -1594,17 +1594,6 @@ __global__ __launch_bounds__(256) void gate_rows_kernel(const uint16_t *__restri
     }
     __syncthreads();
     if (t >= M) return;
-    // the row's operands for the expert products (quantize_act_kernel's arithmetic, no norm: act16_group of each
-    // 8-value group, the lane pair of a 16-value block adjacent), from the LDS copy
-    for (int g0 = 0; g0 < H / 8; g0 += 64) {
-        const int g = g0 + lane;
-        const bool live = g < H / 8;
-        float v[8];
-        const float4 x0 = *reinterpret_cast<const float4 *>(hs + min(g, H / 8 - 1) * 8);
-        const float4 x1 = *reinterpret_cast<const float4 *>(hs + min(g, H / 8 - 1) * 8 + 4);
-        v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w, v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
-        act16_group(v, g, live, act + static_cast<int64_t>(t) * act_stride);
-    }
     float a = 0.0f;
     if (lane < 8)
         for (int c0 = lane; c0 < H; c0 += 8 * 16) {   // 16 steps' operands read ahead of their sums
@@ -2081,13 +2070,14 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     const int H = c.hidden, E = c.n_experts, K = c.top_k, F = c.moe_ff;
     Prefill &pf = m.pf;
     LayerW &L = m.layers[static_cast<size_t>(layer)];
-    const int wg4 = (M + 3) / 4;   // (the rows' operands for the products quantized in gate_rows_kernel)
+    if (quantize_act(pf.h, H, M, H, nullptr, 0.0f, pf.act, act_halves(H), nullptr, 0, st) != 0) return -1;
+    const int wg4 = (M + 3) / 4;
     {
         const size_t lds = static_cast<size_t>(5) * H * 4;   // the gate row and the 4 waves' rows as fp32
         static int granted = 0;
         if (lds_grant(reinterpret_cast<const void *>(&gate_rows_kernel), lds, granted) != 0) return -1;
         hipLaunchKernelGGL(gate_rows_kernel, dim3(wg4), dim3(256), lds, st, L.router + static_cast<int64_t>(E) * H, H,
-                           pf.h, M, pf.logits, m.E1, pf.act, act_halves(H));
+                           pf.h, M, pf.logits, m.E1);
     }
     hipLaunchKernelGGL(route_rows_kernel, dim3(wg4), dim3(256), 0, st, pf.logits, E, K, M, pf.ids, pf.w, pf.gate);
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, pf.start, pf.n_slots,
