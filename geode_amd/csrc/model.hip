@@ -1546,10 +1546,11 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStre
             }
         }
     } else {
-        a.groups = (a.H / kTileR + waves * kMoeDnTiles - 1) / (waves * kMoeDnTiles);
+        // a wave a workgroup (its tiles need no other wave): the finest grain, so that the CUs' shares even out
+        a.groups = (a.H / kTileR + kMoeDnTiles - 1) / kMoeDnTiles;
         const dim3 grid(static_cast<unsigned>(slots * a.groups));
-        if (kwd == 16) hipLaunchKernelGGL(moe_down_kernel<16>, grid, dim3(64 * waves), 0, st, a);
-        else hipLaunchKernelGGL(moe_down_kernel<4>, grid, dim3(64 * waves), 0, st, a);
+        if (kwd == 16) hipLaunchKernelGGL(moe_down_kernel<16>, grid, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL(moe_down_kernel<4>, grid, dim3(64), 0, st, a);
     }
     GV_CHECK_HIP(hipGetLastError());
     return 0;
