@@ -1246,6 +1246,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
         float *xr = x + static_cast<int64_t>(t) * H + gc * 8;
         const float *xs = residual ? xr : zero + gc * 8;   // (no residual: the block's output alone, x + 0)
         const float4 xa = *reinterpret_cast<const float4 *>(xs), xb = *reinterpret_cast<const float4 *>(xs + 4);
+        float wkv[8];   // the picks' weights, with the rows (not a round trip after them)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) wkv[u] = mix.weight[t * K + min(u, K - 1)];
         __builtin_amdgcn_sched_barrier(0);
         float o[8];
         {
@@ -1256,7 +1259,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
         // rank order, skipping zero weights
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const float wk = u < K ? mix.weight[t * K + u] : 0.0f;
+            const float wk = u < K ? wkv[u] : 0.0f;
             if (wk == 0.0f) continue;   // uniform
             const float yv[8] = {ya[u].x, ya[u].y, ya[u].z, ya[u].w, yb[u].x, yb[u].y, yb[u].z, yb[u].w};
 #pragma unroll
