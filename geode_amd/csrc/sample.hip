@@ -749,10 +749,10 @@ __global__ __launch_bounds__(kSortThreads) void cand_nucleus(Rows rs, Ws ws, flo
 // sample-and-match over the sampled rows (geode.cpp:331-350): out = the stood drafts then the first sampled token
 // that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}. fr
 // (the candidate path's rows, or null): a row it did not decide gives res = {0, 0}.
-__global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ picks, const int32_t *__restrict__ batch,
-                                                   int n, const int32_t *__restrict__ stop, int n_stop,
-                                                   int32_t *__restrict__ out, int *__restrict__ res,
-                                                   const FRow *__restrict__ fr) {
+template <typename BatchAt, typename StopAt>
+__device__ inline void match_body(const int32_t *__restrict__ picks, BatchAt batch_at, int n, StopAt stop_at,
+                                  int n_stop, int32_t *__restrict__ out, int *__restrict__ res,
+                                  const FRow *__restrict__ fr) {
     __shared__ int32_t pick[32], next[32];
     __shared__ int stopped[32];
     const int t = threadIdx.x;
@@ -765,13 +765,15 @@ __global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ p
     }
     if (t < n) {
         pick[t] = picks[t];
-        next[t] = t + 1 < n ? batch[t + 1] : -1;
+        next[t] = t + 1 < n ? batch_at(t + 1) : -1;
         stopped[t] = 0;
     }
     __syncthreads();
-    for (int j = t; j < n_stop; j += blockDim.x)   // which rows sampled a stop token
+    for (int j = t; j < n_stop; j += blockDim.x) {   // which rows sampled a stop token
+        const int32_t sj = stop_at(j);
         for (int i = 0; i < n; ++i)
-            if (stop[j] == pick[i]) stopped[i] = 1;
+            if (sj == pick[i]) stopped[i] = 1;
+    }
     __syncthreads();
     if (t != 0) return;
     int emitted = 0, kept = 1;
@@ -785,6 +787,25 @@ __global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ p
     }
     res[0] = emitted;
     res[1] = kept;
+}
+
+__global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ picks, const int32_t *__restrict__ batch,
+                                                   int n, const int32_t *__restrict__ stop, int n_stop,
+                                                   int32_t *__restrict__ out, int *__restrict__ res,
+                                                   const FRow *__restrict__ fr) {
+    match_body(picks, [&](int i) { return batch[i]; }, n, [&](int j) { return stop[j]; }, n_stop, out, res, fr);
+}
+
+// the same with the batch and up to 32 stop tokens as kernel arguments (no input copy)
+struct MatchIn {
+    int32_t batch[32];
+    int32_t stop[32];
+};
+__global__ __launch_bounds__(64) void match_args_kernel(const int32_t *__restrict__ picks, MatchIn in, int n,
+                                                        int n_stop, int32_t *__restrict__ out, int *__restrict__ res,
+                                                        const FRow *__restrict__ fr) {
+    match_body(picks, [&](int i) { return in.batch[i]; }, n, [&](int j) { return in.stop[j]; }, n_stop, out, res,
+               fr);
 }
 
 // The presence penalty of the generate loop (geode.cpp:236-255) on the verified rows, in place: row i (a workgroup)
@@ -1923,6 +1944,49 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
     if (n_stop) std::copy(stop, stop + n_stop, hint + 101);
     if (n_seen_dev) std::copy(seen, seen + n_seen_dev, hint + 101 + n_stop);
     const hipStream_t st = stream();
+    const Rows rs = make_rows(logits, n, nullptr, ld, V);
+    const int K = top_k > 0 ? std::min(top_k, V) : (cap > 0 ? std::min(cap, V) : V);
+    const bool candidate = temperature > 0.0f && K < V && K <= kFCap && rs.S <= kMaxChunks;
+    static int granted_n = 0;
+    const size_t lds_n = static_cast<size_t>(kFCap) * 24;
+    if (candidate && lds_grant(reinterpret_cast<const void *>(&fast_nucleus<false>), lds_n, granted_n) != 0) return -1;
+    auto launch_candidate = [&](const FastU &fu) {
+        const dim3 grid(rs.S, n), block(kPass);
+        hipLaunchKernelGGL(fast_stats, grid, block, 0, st, rs, c.ws, temperature);
+        hipLaunchKernelGGL(fast_collect<false>, grid, block, 0, st, rs, c.ws, temperature, top_p, K);
+        hipLaunchKernelGGL(fast_nucleus<false>, dim3(n), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, K,
+                           fu);
+    };
+    FastU fu{};
+    if (temperature > 0.0f)
+        for (int i = 0; i < n; ++i) fu.u[i] = u[i];
+    if ((candidate || temperature <= 0.0f) && !penalize && n_stop <= 32) {
+        // no penalty and few stop tokens: every input as kernel arguments and the results straight into the pinned
+        // buffer, no copy either way (greedy: the chunks' maxima and the first argmaxes)
+        MatchIn in{};
+        std::copy(batch, batch + n, in.batch);
+        if (n_stop) std::copy(stop, stop + n_stop, in.stop);
+        if (candidate) {
+            launch_candidate(fu);
+        } else {
+            GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
+            hipLaunchKernelGGL(max_pass<false>, dim3(rs.S, n), dim3(kPass), 0, st, rs, c.ws);
+            hipLaunchKernelGGL(argmax_reduce, dim3(n), dim3(64), 0, st, c.ws, rs.S);
+        }
+        hipLaunchKernelGGL(match_args_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, in, n, n_stop, hint, hint + 32,
+                           candidate ? static_cast<const FRow *>(c.ws.fr) : nullptr);
+        GV_CHECK_HIP(hipGetLastError());
+        GV_CHECK_HIP(hipStreamSynchronize(st));
+        const int emitted = hint[32];
+        if (emitted > 0) {
+            for (int i = 0; i < emitted; ++i) out[i] = hint[i];
+            if (kept) *kept = hint[33];
+            if (candidate) g_path_candidate.fetch_add(1, std::memory_order_relaxed);
+            return emitted;
+        }
+        // (a row the candidate path did not decide: the walks below, from the copied inputs)
+        std::copy(batch, batch + n, hint + 36);
+    }
     GV_CHECK_HIP(hipMemcpyAsync(c.io, pin, io, hipMemcpyHostToDevice, st));
     int32_t *dout = dint, *dres = dint + 32, *dbatch = dint + 36, *dfresh = dint + 68, *dstop = dint + 101;
     int32_t *dseen = dstop + n_stop;
@@ -1931,21 +1995,10 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
                            presence_penalty);
         GV_CHECK_HIP(hipGetLastError());
     }
-    const Rows rs = make_rows(logits, n, nullptr, ld, V);
-    const int K = top_k > 0 ? std::min(top_k, V) : (cap > 0 ? std::min(cap, V) : V);
-    if (temperature > 0.0f && K < V && K <= kFCap && rs.S <= kMaxChunks) {
+    if (candidate && (penalize || n_stop > 32)) {
         // the candidate path over the top K; a row it does not decide sends the call to the walks (the penalty
         // already applied)
-        FastU fu{};
-        for (int i = 0; i < n; ++i) fu.u[i] = u[i];
-        const dim3 grid(rs.S, n), block(kPass);
-        static int granted_n = 0;
-        const size_t lds_n = static_cast<size_t>(kFCap) * 24;
-        if (lds_grant(reinterpret_cast<const void *>(&fast_nucleus<false>), lds_n, granted_n) != 0) return -1;
-        hipLaunchKernelGGL(fast_stats, grid, block, 0, st, rs, c.ws, temperature);
-        hipLaunchKernelGGL(fast_collect<false>, grid, block, 0, st, rs, c.ws, temperature, top_p, K);
-        hipLaunchKernelGGL(fast_nucleus<false>, dim3(n), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, K,
-                           fu);
+        launch_candidate(fu);
         hipLaunchKernelGGL(match_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, dbatch, n, dstop, n_stop, dout, dres,
                            static_cast<const FRow *>(c.ws.fr));
         GV_CHECK_HIP(hipGetLastError());

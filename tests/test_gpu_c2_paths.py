@@ -8,7 +8,7 @@ Textbook rule: C2's trial shape; small, ragged and one-chunk vocabularies; k = 1
 no residual mass (draft = target, u_acc = 1: the target row's own draw); rows whose nucleus spans most of the
 vocabulary and top_p = 1 (the walks). Sample-and-match: C2's rows at the reference's cap of 1024, top_k 1, 50 and
 3000 (top_p 1), ties at the cut, a peaked temperature with a presence penalty (the walks, the penalty applied once),
-a cap above the candidate path's 4096 (the walks)."""
+a cap above the candidate path's 4096 (the walks), stop lists of 3 and 40 tokens."""
 import numpy as np
 import pytest
 
@@ -181,3 +181,21 @@ def test_match_large_cap_takes_the_walks(gv):
     x, u, _ = _match_case(1600)
     batch = np.array([7, 1, 2, 3, 4], np.int32)
     assert _match(gv, x, batch, 0.7, 0.95, 0, 8192, u) == "walks"
+
+
+@pytest.mark.parametrize("n_stop", [3, 40])
+def test_match_stop_lists_on_the_candidate_path(gv, n_stop):
+    """stop tokens with no penalty: up to 32 go to the launch as kernel arguments (no copies), more through the copied
+    inputs; a draft that is a stop token never stands, on both"""
+    x, u, rng = _match_case(1700 + n_stop)
+    samples = [po.sample(x[i], 0.7, 0.95, 0, 1024, u[i]) for i in range(5)]
+    batch = np.array([7] + samples[:4], np.int32)
+    stop = np.concatenate([[samples[1]], rng.choice(x.shape[1], size=n_stop - 1, replace=False)]).astype(np.int32)
+    none = np.zeros(0, np.int32)
+    c0, w0 = gv.sampler_paths()
+    want, wk, _ = po.accept_match_ex(x, batch, 0.7, 0.95, 0, 1024, u, none, 0.0, stop)
+    got, gk, _ = gv.accept_match_ex(x, batch, 0.7, 0.95, 0, 1024, u, none, 0.0, stop)
+    c1, w1 = gv.sampler_paths()
+    assert list(got) == list(want) and gk == wk, (list(got), list(want))
+    assert (c1, w1) == (c0 + 1, w0)
+    assert wk <= 2   # (row 1's sample is a stop token: its draft cannot stand)
