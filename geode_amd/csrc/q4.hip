@@ -280,6 +280,67 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
     if (tc >= 0) trace(tc, 3);
 }
 
+// The skinny product at 17..32 rows over two K ranges in one launch (each range's activations fill the waves'
+// registers, as in two gemv_q4_kernel launches, the second accumulating): the workgroup runs the first range's tiles,
+// keeps their partial sums in LDS, runs the second's, then writes (y + s0 x global) + s1 x global (accumulate), or
+// s0 x global + s1 x global: the two launches' sums in their order.
+template <int KW, int WMAX>
+__global__ __launch_bounds__(64 * WMAX) void gemv_q4_2pass_kernel(Q4 w, const _Float16 *__restrict__ act,
+                                                                  int64_t act_stride, int M, int sc_step,
+                                                                  int tiles_per_wg, GemvOut out) {
+    extern __shared__ f4 part_lds[];
+    __shared__ uint2 tab[256];
+    const int64_t ntiles = tiles_rows(w.rows);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tiles_per_wg;
+    if (t0 >= ntiles) return;
+    const int nt = static_cast<int>(std::min<int64_t>(tiles_per_wg, ntiles - t0));
+    const int W = blockDim.x / 64, o0 = threadIdx.x;
+    f4 *part1 = part_lds + static_cast<size_t>(tiles_per_wg) * W * 2 * 64;
+    auto item = [&](int o, int64_t &row0, int &j) {
+        const int i = o / 128, tt = (o / 64) % 2, ll = o % 64;
+        row0 = (t0 + i) * kTileR + 4 * (ll / 16);
+        j = tt * 16 + ll % 16;
+    };
+    float old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto prefetch = [&] {
+        if (!out.accumulate) return;   // uniform
+        int64_t row0;
+        int j;
+        item(min(o0, nt * 128 - 1), row0, j);
+        const float *p = out.y + min(j, M - 1) * out.ldy;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) old[r] = p[min(row0 + r, w.rows - 1)];   // (clamped: always a valid address)
+    };
+    const int nsc = static_cast<int>(w.cols / kSuperK);
+    mfma_tiles<KW, 2, kKeepParts, 0, 3, false>(w.codes, w.scales, w.rows, nsc, 0, nt, M,
+                                                [&](int j) { return act + j * act_stride; },
+                                                [](int64_t, int, float) {}, part_lds, tab, TileRun{t0}, prefetch);
+    mfma_tiles<KW, 2, kKeepParts, 0, 3, false>(w.codes, w.scales, w.rows, nsc, sc_step, nt, M,
+                                                [&](int j) { return act + j * act_stride; },
+                                                [](int64_t, int, float) {}, part1, tab, TileRun{t0});
+    for (int o = o0; o < nt * 128; o += blockDim.x) {   // each range's waves' partial sums in wave order
+        const int i = o / 128, tt = (o / 64) % 2, ll = o % 64;
+        f4 s0 = part_lds[((i * W + 0) * 2 + tt) * 64 + ll], s1 = part1[((i * W + 0) * 2 + tt) * 64 + ll];
+        for (int w2 = 1; w2 < W; ++w2) {
+            s0 += part_lds[((i * W + w2) * 2 + tt) * 64 + ll];
+            s1 += part1[((i * W + w2) * 2 + tt) * 64 + ll];
+        }
+        int64_t row0;
+        int j;
+        item(o, row0, j);
+        if (j >= M) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = row0 + r;
+            if (row >= w.rows) break;
+            float *p = out.y + j * out.ldy + row;
+            const float first = out.scaled(row, s0[r]);
+            const float v = out.accumulate ? (o == o0 ? old[r] : *p) + first : first;
+            *p = v + out.scaled(row, s1[r]);
+        }
+    }
+}
+
 // The skinny product over many row tiles a workgroup at 17..32 rows (two 16-column tiles: a K range's activations
 // take half the registers, so the kept-parts form above holds only 4 tiles' partial sums and each workgroup reloads
 // the rows' activations every 4 tiles): the waves' sums put every kGemvFlush tiles (mfma_tiles FLUSH), the same
@@ -512,6 +573,20 @@ int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const G
     const int nsc = static_cast<int>(w.cols / kSuperK);
     // K ranges whose activations fit the waves' registers: one launch up to 4096 (2048 for 17..32 rows) values,
     // later ranges adding to the first's sums
+    if (ntt == 2 && nsc == 32) {   // two ranges of 2048 in one launch (kept parts, up to two tiles a workgroup)
+        int waves, kw;
+        const int64_t ntiles = tiles_rows(w.rows);
+        if (mfma_split(16 * kSuperK, 2, waves, kw) && kw == 8 && waves == 8 && tiles_per_wg(ntiles, waves, 2) <= 2) {
+            const int64_t per = tiles_per_wg(ntiles, waves, 2), wg = (ntiles + per - 1) / per;
+            const size_t lds = static_cast<size_t>(2 * per) * waves * 2 * 1024;
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_2pass_kernel<8, 8>), lds, granted) != 0) return -1;
+            hipLaunchKernelGGL((gemv_q4_2pass_kernel<8, 8>), dim3(static_cast<unsigned>(wg)), dim3(64 * waves), lds, st,
+                               w, act, act_stride, M, 16, static_cast<int>(per), out);
+            GV_CHECK_HIP(hipGetLastError());
+            return 0;
+        }
+    }
     for (int sc0 = 0, part = 0; sc0 < nsc; ++part) {
         int n = std::min(nsc - sc0, ntt == 1 ? 32 : 16);
         int waves, kw;
