@@ -801,6 +801,28 @@ struct MatchIn {
     int32_t batch[32];
     int32_t stop[32];
 };
+
+// greedy (T <= 0): each row's first argmax from its chunks' maxima (max_pass), then the decisions; one wave
+__global__ __launch_bounds__(64) void greedy_match_kernel(Ws ws, int S, MatchIn in, int n, int n_stop,
+                                                          int32_t *__restrict__ out, int *__restrict__ res) {
+    __shared__ int32_t pk[32];
+    __shared__ uint64_t cm[32 * kMaxChunks];
+    const int lane = threadIdx.x;
+    for (int i = lane; i < n * S; i += 64) {   // (every row's chunk maxima, their loads independent)
+        const int r = i / S, c = i - r * S;
+        cm[r * kMaxChunks + c] = (static_cast<uint64_t>(ws.pmax[r * kMaxChunks + c]) << 32) |
+                                 (0xFFFFFFFFu - static_cast<uint32_t>(ws.pidx[r * kMaxChunks + c]));
+    }
+    __syncthreads();
+    for (int r = 0; r < n; ++r) {
+        uint64_t b = lane < S ? cm[r * kMaxChunks + lane] : 0ull;
+        for (int o = 32; o > 0; o >>= 1) b = max(b, static_cast<uint64_t>(__shfl_xor(b, o, 64)));
+        if (lane == 0) pk[r] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(b));
+    }
+    __syncthreads();
+    match_body(pk, [&](int i) { return in.batch[i]; }, n, [&](int j) { return in.stop[j]; }, n_stop, out, res,
+               static_cast<const FRow *>(nullptr));
+}
 __global__ __launch_bounds__(64) void match_args_kernel(const int32_t *__restrict__ picks, MatchIn in, int n,
                                                         int n_stop, int32_t *__restrict__ out, int *__restrict__ res,
                                                         const FRow *__restrict__ fr) {
@@ -1968,13 +1990,13 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
         if (n_stop) std::copy(stop, stop + n_stop, in.stop);
         if (candidate) {
             launch_candidate(fu);
+            hipLaunchKernelGGL(match_args_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, in, n, n_stop, hint, hint + 32,
+                               static_cast<const FRow *>(c.ws.fr));
         } else {
             GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
             hipLaunchKernelGGL(max_pass<false>, dim3(rs.S, n), dim3(kPass), 0, st, rs, c.ws);
-            hipLaunchKernelGGL(argmax_reduce, dim3(n), dim3(64), 0, st, c.ws, rs.S);
+            hipLaunchKernelGGL(greedy_match_kernel, dim3(1), dim3(64), 0, st, c.ws, rs.S, in, n, n_stop, hint, hint + 32);
         }
-        hipLaunchKernelGGL(match_args_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, in, n, n_stop, hint, hint + 32,
-                           candidate ? static_cast<const FRow *>(c.ws.fr) : nullptr);
         GV_CHECK_HIP(hipGetLastError());
         GV_CHECK_HIP(hipStreamSynchronize(st));
         const int emitted = hint[32];
