@@ -34,6 +34,7 @@
 // close to a boundary; expf is the device's (within 1 ulp of glibc's).
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <climits>
 #include <cmath>
 #include <vector>
@@ -746,13 +747,23 @@ __global__ __launch_bounds__(kSortThreads) void cand_nucleus(Rows rs, Ws ws, flo
 }
 
 // ---------------------------------------------------------------- acceptance
+// A call's results written into pinned host memory, then its sequence number `seq` to *done (null: none): the host
+// polls that word instead of waiting for the stream. The calling thread's result stores come first in program order,
+// and the system-scope fence makes them visible before the word; a workgroup whose other threads stored results
+// fences in each of them and meets at a barrier first.
+__device__ inline void post_seq(uint32_t *done, uint32_t seq) {
+    if (!done) return;
+    __threadfence_system();
+    __hip_atomic_store(done, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // sample-and-match over the sampled rows (geode.cpp:331-350): out = the stood drafts then the first sampled token
-// that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}. fr
-// (the candidate path's rows, or null): a row it did not decide gives res = {0, 0}.
+// that is no draft; a draft stands only if it is no stop token either (stop[0..n_stop)); res = {emitted, kept}, then
+// seq to *done (post_seq). fr (the candidate path's rows, or null): a row it did not decide gives res = {0, 0}.
 template <typename BatchAt, typename StopAt>
 __device__ inline void match_body(const int32_t *__restrict__ picks, BatchAt batch_at, int n, StopAt stop_at,
                                   int n_stop, int32_t *__restrict__ out, int *__restrict__ res,
-                                  const FRow *__restrict__ fr) {
+                                  const FRow *__restrict__ fr, uint32_t *done, uint32_t seq) {
     __shared__ int32_t pick[32], next[32];
     __shared__ int stopped[32];
     const int t = threadIdx.x;
@@ -760,6 +771,7 @@ __device__ inline void match_body(const int32_t *__restrict__ picks, BatchAt bat
         if (t == 0) {
             res[0] = 0;
             res[1] = 0;
+            post_seq(done, seq);
         }
         return;
     }
@@ -787,13 +799,15 @@ __device__ inline void match_body(const int32_t *__restrict__ picks, BatchAt bat
     }
     res[0] = emitted;
     res[1] = kept;
+    post_seq(done, seq);
 }
 
 __global__ __launch_bounds__(64) void match_kernel(const int32_t *__restrict__ picks, const int32_t *__restrict__ batch,
                                                    int n, const int32_t *__restrict__ stop, int n_stop,
                                                    int32_t *__restrict__ out, int *__restrict__ res,
                                                    const FRow *__restrict__ fr) {
-    match_body(picks, [&](int i) { return batch[i]; }, n, [&](int j) { return stop[j]; }, n_stop, out, res, fr);
+    match_body(picks, [&](int i) { return batch[i]; }, n, [&](int j) { return stop[j]; }, n_stop, out, res, fr, nullptr,
+               0u);
 }
 
 // the same with the batch and up to 32 stop tokens as kernel arguments (no input copy)
@@ -804,7 +818,8 @@ struct MatchIn {
 
 // greedy (T <= 0): each row's first argmax from its chunks' maxima (max_pass), then the decisions; one wave
 __global__ __launch_bounds__(64) void greedy_match_kernel(Ws ws, int S, MatchIn in, int n, int n_stop,
-                                                          int32_t *__restrict__ out, int *__restrict__ res) {
+                                                          int32_t *__restrict__ out, int *__restrict__ res,
+                                                          uint32_t *done, uint32_t seq) {
     __shared__ int32_t pk[32];
     __shared__ uint64_t cm[32 * kMaxChunks];
     const int lane = threadIdx.x;
@@ -821,13 +836,13 @@ __global__ __launch_bounds__(64) void greedy_match_kernel(Ws ws, int S, MatchIn 
     }
     __syncthreads();
     match_body(pk, [&](int i) { return in.batch[i]; }, n, [&](int j) { return in.stop[j]; }, n_stop, out, res,
-               static_cast<const FRow *>(nullptr));
+               static_cast<const FRow *>(nullptr), done, seq);
 }
 __global__ __launch_bounds__(64) void match_args_kernel(const int32_t *__restrict__ picks, MatchIn in, int n,
                                                         int n_stop, int32_t *__restrict__ out, int *__restrict__ res,
-                                                        const FRow *__restrict__ fr) {
+                                                        const FRow *__restrict__ fr, uint32_t *done, uint32_t seq) {
     match_body(picks, [&](int i) { return in.batch[i]; }, n, [&](int j) { return in.stop[j]; }, n_stop, out, res,
-               fr);
+               fr, done, seq);
 }
 
 // The presence penalty of the generate loop (geode.cpp:236-255) on the verified rows, in place: row i (a workgroup)
@@ -1568,7 +1583,8 @@ constexpr int kBuckets = 256;
 constexpr int kRankMax = 512;   // a bucket of more elements is sorted by the bitonic network instead
 
 __global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, int k, float T, FastU fu,
-                                                              int32_t *__restrict__ out, int *__restrict__ st) {
+                                                              int32_t *__restrict__ out, int *__restrict__ st,
+                                                              uint32_t *done, uint32_t seq) {
     extern __shared__ uint64_t lds[];   // [kFCap] (index << 32) | position by bucket, [kFCap] in index order,
                                         // [kFCap] doubles: the residuals by position
     uint64_t *grp = lds, *ord = lds + kFCap;
@@ -1586,9 +1602,23 @@ __global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, in
         bcnt[tid] = 0u;
         bcur[tid] = 0u;
     }
+    // the results: out[0, n - 1) the stood drafts, out[n - 1] = last, st[0] = n, then the posting (post_seq)
+    auto emit = [&](int n, int32_t last) {
+        for (int i = tid; i < n - 1; i += nthr) out[i] = ws.picks[k + 1 + i];
+        __threadfence_system();
+        __syncthreads();
+        if (tid == 0) {
+            out[n - 1] = last;
+            st[0] = n;
+            post_seq(done, seq);
+        }
+    };
     __syncthreads();
     if (s_rej < 0) {
-        if (tid == 0) st[0] = 0;
+        if (tid == 0) {
+            st[0] = 0;
+            post_seq(done, seq);
+        }
         return;
     }
     if (tid < k) {   // draft i stands with probability min(1, p_i(d) / q_i(d))
@@ -1603,11 +1633,7 @@ __global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, in
     __syncthreads();
     const int rej = s_rej;
     if (rej == INT_MAX) {   // every draft stood: the bonus, target row k's draw
-        for (int i = tid; i < k; i += nthr) out[i] = ws.picks[k + 1 + i];
-        if (tid == 0) {
-            out[k] = ws.picks[k];
-            st[0] = k + 1;
-        }
+        emit(k + 1, ws.picks[k]);
         return;
     }
     const RowInfo &P = ws.info[rej], &Q = ws.info[k + 1 + rej];
@@ -1697,18 +1723,14 @@ __global__ __launch_bounds__(kSortThreads) void fast_textbook(Rows rs, Ws ws, in
         const int at = s_first != INT_MAX ? s_first : s_last;   // rounding past the end: the last positive weight
         pick = static_cast<int>(ord[at] >> 32);
     }
-    for (int i = tid; i < rej; i += nthr) out[i] = ws.picks[k + 1 + i];
-    if (tid == 0) {
-        out[rej] = pick;
-        st[0] = rej + 1;
-    }
+    emit(rej + 1, pick);
 }
 
 // The textbook rule when greedy (target rows 0..k, draft rows k+1..2k; one workgroup, their chunks' maxima done):
 // each row's first argmax from its chunks' (a wave a row), then target row i's argmax is emitted while draft row i's
-// agrees, and target row k's when all do (the bonus). st[0] = emitted.
+// agrees, and target row k's when all do (the bonus). st[0] = emitted, then seq to *done (post_seq).
 __global__ __launch_bounds__(kSortThreads) void greedy_finish(Ws ws, int S, int k, int32_t *__restrict__ out,
-                                                              int *__restrict__ st) {
+                                                              int *__restrict__ st, uint32_t *done, uint32_t seq) {
     __shared__ int32_t pick[64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, R = 2 * k + 1;
     for (int r = wave; r < R; r += blockDim.x >> 6) {
@@ -1726,11 +1748,13 @@ __global__ __launch_bounds__(kSortThreads) void greedy_finish(Ws ws, int S, int 
         out[emitted++] = pick[i];
         if (pick[i] != pick[k + 1 + i]) {
             st[0] = emitted;
+            post_seq(done, seq);
             return;
         }
     }
     out[emitted++] = pick[k];
     st[0] = emitted;
+    post_seq(done, seq);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1748,7 +1772,8 @@ struct Workspace {
     }
 };
 
-// pinned host memory for a call's inputs and results (one copy each way)
+// pinned host memory for a call's inputs and results (one copy each way, or the results written by the kernels),
+// coherent: the kernels' system-scope stores reach the host while the stream still runs
 struct Pinned {
     void *p = nullptr;
     size_t n = 0;
@@ -1757,13 +1782,44 @@ struct Pinned {
         if (p) (void)hipHostFree(p);
         p = nullptr;
         n = 0;
-        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) return nullptr;
+        if (hipHostMalloc(&p, want, hipHostMallocCoherent) != hipSuccess) return nullptr;
         n = want;
         return p;
     }
 };
 
 std::atomic<int64_t> g_path_candidate{0}, g_path_walks{0};   // the acceptance rules' sampling calls by path
+
+// A call's sequence number (never 0), its word in pinned memory cleared for it before the launches
+std::atomic<uint32_t> g_seq{0};
+uint32_t next_seq(uint32_t *done) {
+    uint32_t s = g_seq.fetch_add(1, std::memory_order_relaxed) + 1;
+    if (s == 0) s = g_seq.fetch_add(1, std::memory_order_relaxed) + 1;
+    __atomic_store_n(done, 0u, __ATOMIC_RELAXED);
+    return s;
+}
+
+// Waits until the call's last kernel has posted seq at *done (post_seq: its results in the same pinned buffer are
+// visible by then), polling the word: the stream wait returns several microseconds after the kernel is done. Once the
+// wait has lasted kQueryAfterUs, the stream is queried every 1024 polls, so a failed launch or a fault ends the wait
+// with its error, and a stream that finished without posting is an error too. (Queries from the start cost a short
+// call ~10 us: measured 31-35 us a greedy textbook trial against 17 us.)
+constexpr int64_t kQueryAfterUs = 10000;
+int wait_posted(const uint32_t *done, uint32_t seq, hipStream_t st) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t n = 1;; ++n) {
+        if (__atomic_load_n(done, __ATOMIC_ACQUIRE) == seq) return 0;
+        if ((n & 1023u) != 0) continue;
+        if (std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() <
+            kQueryAfterUs)
+            continue;
+        const hipError_t e = hipStreamQuery(st);
+        if (e == hipErrorNotReady) continue;
+        GV_CHECK_HIP(e);
+        if (__atomic_load_n(done, __ATOMIC_ACQUIRE) == seq) return 0;
+        GV_REQUIRE(false, "sampler: the stream finished without the call's posted results");
+    }
+}
 
 Workspace &ws_mem() {
     static Workspace w;
@@ -1988,17 +2044,20 @@ int gv_accept_match_ex(float *logits, int64_t ld, int V, const int32_t *batch, i
         MatchIn in{};
         std::copy(batch, batch + n, in.batch);
         if (n_stop) std::copy(stop, stop + n_stop, in.stop);
+        uint32_t *done = reinterpret_cast<uint32_t *>(hint + 34);
+        const uint32_t seq = next_seq(done);
         if (candidate) {
             launch_candidate(fu);
             hipLaunchKernelGGL(match_args_kernel, dim3(1), dim3(64), 0, st, c.ws.picks, in, n, n_stop, hint, hint + 32,
-                               static_cast<const FRow *>(c.ws.fr));
+                               static_cast<const FRow *>(c.ws.fr), done, seq);
         } else {
             GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
             hipLaunchKernelGGL(max_pass<false>, dim3(rs.S, n), dim3(kPass), 0, st, rs, c.ws);
-            hipLaunchKernelGGL(greedy_match_kernel, dim3(1), dim3(64), 0, st, c.ws, rs.S, in, n, n_stop, hint, hint + 32);
+            hipLaunchKernelGGL(greedy_match_kernel, dim3(1), dim3(64), 0, st, c.ws, rs.S, in, n, n_stop, hint, hint + 32,
+                               done, seq);
         }
         GV_CHECK_HIP(hipGetLastError());
-        GV_CHECK_HIP(hipStreamSynchronize(st));
+        if (wait_posted(done, seq, st) != 0) return -1;
         const int emitted = hint[32];
         if (emitted > 0) {
             for (int i = 0; i < emitted; ++i) out[i] = hint[i];
@@ -2054,8 +2113,9 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
     GV_REQUIRE(target && draft && out && k >= 1 && k <= 31 && V >= 1 && ld >= V, "gv_accept_textbook: bad arguments");
     GV_REQUIRE(greedy || (u_draft && u_acc && temperature > 0.0f), "gv_accept_textbook: uniforms and T > 0 needed");
     const int R = 2 * k + 1;
-    // io: [R] uniforms, then rsum[kMaxChunks] (double), u_acc[32] (float), done, out[32], st (uint32 / int32)
-    const size_t io = 8 * static_cast<size_t>(R) + 8 * kMaxChunks + 4 * 32 + 4 + 4 * 33;
+    // io: [R] uniforms, then rsum[kMaxChunks] (double), u_acc[32] (float), done, out[32], st (uint32 / int32), and
+    // the posted sequence word (host side only)
+    const size_t io = 8 * static_cast<size_t>(R) + 8 * kMaxChunks + 4 * 32 + 4 + 4 * 33 + 4;
     void *base = ws_mem().get(ws_bytes(R, io));
     auto *pin = static_cast<char *>(pinned().get(io));
     GV_REQUIRE(base && pin, "gv_accept_textbook: out of memory");
@@ -2076,12 +2136,15 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
     const hipStream_t st = stream();
     const Rows rs = make_rows(target, k + 1, draft, ld, V);
     int32_t *hout = reinterpret_cast<int32_t *>(hacc + 33);
+    uint32_t *done = reinterpret_cast<uint32_t *>(hout + 33);
     if (greedy) {   // the chunks' maxima, then the first argmaxes and the decisions, straight into the pinned buffer
         GV_REQUIRE(rs.S <= kMaxChunks, "sampler: a vocabulary of at most 262,144 tokens");
+        const uint32_t seq = next_seq(done);
         hipLaunchKernelGGL(max_pass<false>, dim3(rs.S, R), dim3(kPass), 0, st, rs, c.ws);
-        hipLaunchKernelGGL(greedy_finish, dim3(1), dim3(kSortThreads), 0, st, c.ws, rs.S, k, hout, hout + 32);
+        hipLaunchKernelGGL(greedy_finish, dim3(1), dim3(kSortThreads), 0, st, c.ws, rs.S, k, hout, hout + 32, done,
+                           seq);
         GV_CHECK_HIP(hipGetLastError());
-        GV_CHECK_HIP(hipStreamSynchronize(st));
+        if (wait_posted(done, seq, st) != 0) return -1;
         const int emitted = hout[32];
         for (int i = 0; i < emitted; ++i) out[i] = hout[i];
         return emitted;
@@ -2100,13 +2163,14 @@ int gv_accept_textbook(const float *target, const float *draft, int64_t ld, int 
         if (lds_grant(reinterpret_cast<const void *>(&fast_nucleus<true>), lds_n, granted_n) != 0 ||
             lds_grant(reinterpret_cast<const void *>(&fast_textbook), lds_t, granted_t) != 0)
             return -1;
+        const uint32_t seq = next_seq(done);
         hipLaunchKernelGGL(fast_nucleus<true>, dim3(R), dim3(kSortThreads), lds_n, st, rs, c.ws, temperature, top_p, 0,
                            fu);
         // (the results straight into the pinned buffer: no copy launch)
         hipLaunchKernelGGL(fast_textbook, dim3(1), dim3(kSortThreads), lds_t, st, rs, c.ws, k, temperature, fu, hout,
-                           hout + 32);
+                           hout + 32, done, seq);
         GV_CHECK_HIP(hipGetLastError());
-        GV_CHECK_HIP(hipStreamSynchronize(st));
+        if (wait_posted(done, seq, st) != 0) return -1;
         const int emitted = hout[32];
         if (emitted > 0) {
             for (int i = 0; i < emitted; ++i) out[i] = hout[i];
