@@ -15,7 +15,8 @@ OBJ = os.path.join(ROOT, "geode_amd", "_build")
 LIB = os.path.join(ROOT, "geode_amd", "libgeode_verify.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-SOURCES = ["misc.hip", "q4.hip", "capi.hip", "model.hip", "sample.hip", "state.hip", "pack.hip", "gdn.hip", "mtp.hip"]
+SOURCES = ["misc.hip", "q4.hip", "capi.hip", "model.hip", "sample.hip", "state.hip", "pack.hip", "gdn.hip", "mtp.hip",
+           "prefill.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

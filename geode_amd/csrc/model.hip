@@ -18,6 +18,7 @@
 #include "layer_common.hpp"
 #include "mfma_gemv.hpp"
 #include "model.hpp"
+#include "prefill_common.hpp"
 
 namespace gv {
 
@@ -1560,60 +1561,14 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStre
 }
 
 // ---------------------------------------------------------------- prefill MoE (C5): many rows
-// the shared expert's gate logit of each row: the bf16 row . h in the router's eight-sum order; a wave a row
+// the shared expert's gate logit of each row (gate_row_logit); a wave a row
 __global__ __launch_bounds__(256) void gate_rows_kernel(const uint16_t *__restrict__ wrow, int H,
                                                         const float *__restrict__ h, int M, float *__restrict__ logits,
                                                         int E1) {
-    // LDS: the gate row as fp32 [H], then the waves' rows [4][H]. Every global load is issued before the first store
-    // to the LDS (the gate row 8 values a thread, the wave's row 4 values a lane, 2048 values a pass), then the eight
-    // fixed-order chains run from the LDS.
     extern __shared__ float gr_lds[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = blockIdx.x * 4 + wave;
-    float *ws = gr_lds, *hs = gr_lds + H + wave * H;
-    const float *hr = h + static_cast<int64_t>(min(t, M - 1)) * H;
-    for (int p0 = 0; p0 < H; p0 += 2048) {
-        uint4 wv = make_uint4(0, 0, 0, 0);
-        const int iw = p0 + static_cast<int>(threadIdx.x) * 8;
-        if (iw < H) wv = *reinterpret_cast<const uint4 *>(wrow + iw);
-        float4 hv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int ih = min(p0 + u * 256 + lane * 4, H - 4);
-            hv[u] = *reinterpret_cast<const float4 *>(hr + ih);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (iw < H) {
-            const uint32_t wu[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                ws[iw + 2 * k] = __uint_as_float(wu[k] << 16);
-                ws[iw + 2 * k + 1] = __uint_as_float(wu[k] & 0xFFFF0000u);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int ih = p0 + u * 256 + lane * 4;
-            if (ih < H) *reinterpret_cast<float4 *>(hs + ih) = hv[u];
-        }
-    }
-    __syncthreads();
-    if (t >= M) return;
-    float a = 0.0f;
-    if (lane < 8)
-        for (int c0 = lane; c0 < H; c0 += 8 * 16) {   // 16 steps' operands read ahead of their sums
-            float hv[16], wv[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                hv[u] = hs[c0 + 8 * u];
-                wv[u] = ws[c0 + 8 * u];
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) a = __fadd_rn(a, __fmul_rn(wv[u], hv[u]));
-        }
-    const float s1 = __fadd_rn(a, __shfl_down(a, 4, 64));   // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7))
-    const float s2 = __fadd_rn(s1, __shfl_down(s1, 1, 64));
-    const float s3 = __fadd_rn(s2, __shfl_down(s2, 2, 64));
-    if (lane == 0) logits[static_cast<int64_t>(t) * E1 + E1 - 1] = s3;
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const float s3 = gate_row_logit(wrow, H, h, M, t, gr_lds);
+    if (t < M && lane == 0) logits[static_cast<int64_t>(t) * E1 + E1 - 1] = s3;
 }
 
 // route_topk of every row (route_row), a wave a row
@@ -1666,53 +1621,12 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids
         }
 }
 
-// The picks of expert blockIdx.x in (token, rank) order, by ordered compaction over ids [M][K]: their rows and,
-// per (row, rank), where the pick went; the shared expert (E) takes row t at start + t.
-constexpr int kFillBatch = 16;
+// The picks of expert blockIdx.x (fill_expert_picks)
 __global__ __launch_bounds__(256) void fill_picks_kernel(const int *__restrict__ ids, int M, int K, int E,
                                                          const int *__restrict__ start, int *__restrict__ pick_token,
                                                          int *__restrict__ pick_of) {
     __shared__ int wt[kFillBatch][4];
-    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int s0 = start[e];
-    if (e == E) {
-        for (int t = tid; t < M; t += blockDim.x) {
-            pick_token[s0 + t] = t;
-            pick_of[t * (K + 1) + K] = s0 + t;
-        }
-        return;
-    }
-    // kFillBatch chunks of 256 ids at a time: every id of the batch loaded at once, each chunk's matches counted per
-    // wave, one barrier, then each match placed after the earlier chunks' and waves' (the same order as one chunk at
-    // a time)
-    int base = 0;
-    for (int c0 = 0; c0 < M * K; c0 += kFillBatch * 256) {
-        int idv[kFillBatch];
-#pragma unroll
-        for (int u = 0; u < kFillBatch; ++u) idv[u] = ids[min(c0 + u * 256 + tid, M * K - 1)];
-        uint64_t bal[kFillBatch];
-#pragma unroll
-        for (int u = 0; u < kFillBatch; ++u) {
-            bal[u] = __ballot(c0 + u * 256 + tid < M * K && idv[u] == e);
-            if (lane == 0) wt[u][wave] = __popcll(bal[u]);
-        }
-        __syncthreads();
-        int run = base;
-#pragma unroll
-        for (int u = 0; u < kFillBatch; ++u) {
-            int wb = run;
-            for (int w2 = 0; w2 < wave; ++w2) wb += wt[u][w2];
-            if ((bal[u] >> lane) & 1ull) {
-                const int i = c0 + u * 256 + tid;
-                const int p = s0 + wb + __popcll(bal[u] & ((1ull << lane) - 1ull)), t = i / K, k = i % K;
-                pick_token[p] = t;
-                pick_of[t * (K + 1) + k] = p;
-            }
-            run += wt[u][0] + wt[u][1] + wt[u][2] + wt[u][3];
-        }
-        base = run;
-        __syncthreads();   // (wt is the next batch's)
-    }
+    fill_expert_picks(ids, M, K, E, static_cast<int>(blockIdx.x), start[blockIdx.x], pick_token, pick_of, wt);
 }
 
 GemvOut qkv_out(const Model &m, const LayerW &L) {
@@ -2074,21 +1988,29 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     const int H = c.hidden, E = c.n_experts, K = c.top_k, F = c.moe_ff;
     Prefill &pf = m.pf;
     LayerW &L = m.layers[static_cast<size_t>(layer)];
-    if (quantize_act(pf.h, H, M, H, nullptr, 0.0f, pf.act, act_halves(H), nullptr, 0, st) != 0) return -1;
-    const int wg4 = (M + 3) / 4;
-    {
-        const size_t lds = static_cast<size_t>(5) * H * 4;   // the gate row and the 4 waves' rows as fp32
-        static int granted = 0;
-        if (lds_grant(reinterpret_cast<const void *>(&gate_rows_kernel), lds, granted) != 0) return -1;
-        hipLaunchKernelGGL(gate_rows_kernel, dim3(wg4), dim3(256), lds, st, L.router + static_cast<int64_t>(E) * H, H,
-                           pf.h, M, pf.logits, m.E1);
+    if (m.fused) {   // two launches (prefill.hip), the same outputs as the five below
+        if (prefill_front(L.router + static_cast<int64_t>(E) * H, H, pf.h, M, E, K, pf.logits, pf.act, act_halves(H),
+                          pf.ids, pf.w, pf.gate, st) != 0 ||
+            prefill_group(pf.ids, M, K, E, pf.start, pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count,
+                          pf.n_picks, pf.pick_token, pf.pick_of, st) != 0)
+            return -1;
+    } else {
+        if (quantize_act(pf.h, H, M, H, nullptr, 0.0f, pf.act, act_halves(H), nullptr, 0, st) != 0) return -1;
+        const int wg4 = (M + 3) / 4;
+        {
+            const size_t lds = static_cast<size_t>(5) * H * 4;   // the gate row and the 4 waves' rows as fp32
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&gate_rows_kernel), lds, granted) != 0) return -1;
+            hipLaunchKernelGGL(gate_rows_kernel, dim3(wg4), dim3(256), lds, st, L.router + static_cast<int64_t>(E) * H,
+                               H, pf.h, M, pf.logits, m.E1);
+        }
+        hipLaunchKernelGGL(route_rows_kernel, dim3(wg4), dim3(256), 0, st, pf.logits, E, K, M, pf.ids, pf.w, pf.gate);
+        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, pf.start, pf.n_slots,
+                           pf.slot_expert, pf.slot_start, pf.slot_count, pf.n_picks);
+        hipLaunchKernelGGL(fill_picks_kernel, dim3(m.E1), dim3(256), 0, st, pf.ids, M, K, E, pf.start, pf.pick_token,
+                           pf.pick_of);
+        GV_CHECK_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(route_rows_kernel, dim3(wg4), dim3(256), 0, st, pf.logits, E, K, M, pf.ids, pf.w, pf.gate);
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, pf.ids, M, K, E, pf.start, pf.n_slots,
-                       pf.slot_expert, pf.slot_start, pf.slot_count, pf.n_picks);
-    hipLaunchKernelGGL(fill_picks_kernel, dim3(m.E1), dim3(256), 0, st, pf.ids, M, K, E, pf.start, pf.pick_token,
-                       pf.pick_of);
-    GV_CHECK_HIP(hipGetLastError());
     const Slots sl{pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count, pf.pick_token, pf.n_picks, nullptr,
                    nullptr};
     const int picks = M * (K + 1);

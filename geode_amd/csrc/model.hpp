@@ -195,6 +195,12 @@ int gdn_get_state(const Model &m, const LayerW &L, int slot, float *conv, float 
 // the verify step's launches (model.hip): one kernel class of layer l for M rows, and a layer's classes in order
 int run_class(Model &m, int cls, int l, int M, hipStream_t st);
 const int *layer_classes(int &count);
+// the prefill MoE's work before the experts' products in two launches (prefill.hip): the rows' shared-expert gate,
+// route and operands, then the picks grouped by expert and placed
+int prefill_front(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, _Float16 *act,
+                  int64_t act_stride, int *ids, float *w, float *gate, hipStream_t st);
+int prefill_group(const int *ids, int M, int K, int E, int *start, int *n_slots, int *slot_expert, int *slot_start,
+                  int *slot_count, int *n_picks, int *pick_token, int *pick_of, hipStream_t st);
 // the MTP layer's buffers (mtp.hip), at gv_model_create
 int mtp_alloc(Model &m);
 void mtp_free(Model &m);      // the draft head

@@ -55,6 +55,28 @@ def test_c5_prefill_moe_at_its_shape(gv):
         gm.close()
 
 
+@pytest.mark.parametrize("shape", [dict(), dict(n_experts=100, top_k=6)], ids=["e256k8", "e100k6"])
+@pytest.mark.parametrize("M", [18, 37, 512, 1000])
+def test_c5_fused_front_matches_the_separate_launches(gv, shape, M):
+    """the prefill MoE's two launches before the products (the rows' shared-expert gate, route and operands as roles
+    of one launch, then the picks grouped and placed: prefill.hip) against the five separate ones
+    (gv_model_set_fused(m, 0)): the block's output, routed ids and weights bit for bit. M from just past the decode
+    path's rows (max_rows 17) to 1,000 (a ragged last group of four rows; two batches of picks to place)."""
+    cfg = dict(C5, **shape)
+    gm = gv.VerifyModel(cfg)
+    try:
+        gm.randomize(44, 0.02, 0.0221, 0)
+        h = _f16_valued(45 + M, M * cfg["hidden"]).reshape(M, cfg["hidden"])
+        lg = po.normal(46 + M, M * cfg["n_experts"], 1.0).reshape(M, cfg["n_experts"])
+        fused = gm.moe(0, h, lg)
+        gm.set_fused(0)
+        apart = gm.moe(0, h, lg)
+        for a, b in zip(fused, apart):   # (output, ids, weights)
+            assert a.dtype == b.dtype and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        gm.close()
+
+
 # ---------------------------------------------------------------- the NPU plugin's calls
 def _open(gv):
     lib = gv.lib
