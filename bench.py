@@ -89,7 +89,9 @@ def algorithmic_bytes(cls, c, M, uniq_per_layer, ctx):
 
 
 def step_bytes(c, M, uniq_per_layer, ctx):
-    """algorithmic bytes of one whole verify step (BASELINE.md section 2 / SURVEY.md 8(d))"""
+    """algorithmic bytes of one whole verify step: per layer the q|k|v, o and router weights, the norm weights, the
+    touched routed experts' and the shared expert's weights and the KV cache read; then the lm_head and the rows'
+    embeddings"""
     tot = 0
     for u in uniq_per_layer:
         tot += algorithmic_bytes("qkv", c, M, [u], ctx) + algorithmic_bytes("o_proj", c, M, [u], ctx)
@@ -415,7 +417,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the verify step on one GPU only: the step of one sequence does not shard "
-              "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
+              "(independent sequences go one a GPU); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args)
