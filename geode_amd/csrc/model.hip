@@ -1988,7 +1988,7 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     const int H = c.hidden, E = c.n_experts, K = c.top_k, F = c.moe_ff;
     Prefill &pf = m.pf;
     LayerW &L = m.layers[static_cast<size_t>(layer)];
-    if (m.fused) {   // two launches (prefill.hip), the same outputs as the five below
+    if (m.fused && H <= kPrefillFrontMaxH) {   // two launches (prefill.hip), the same outputs as the five below
         if (prefill_front(L.router + static_cast<int64_t>(E) * H, H, pf.h, M, E, K, pf.logits, pf.act, act_halves(H),
                           pf.ids, pf.w, pf.gate, st) != 0 ||
             prefill_group(pf.ids, M, K, E, pf.start, pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count,

@@ -107,8 +107,8 @@ __global__ __launch_bounds__(256) void group_fill_kernel(const int *__restrict__
 
 int prefill_front(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, _Float16 *act,
                   int64_t act_stride, int *ids, float *w, float *gate, hipStream_t st) {
-    GV_REQUIRE(M > 0 && H % 16 == 0 && H <= 8192 && E >= 1 && E + 1 <= 257 && K >= 1 && K <= 16 && K <= E,
-               "prefill front: M > 0, hidden a multiple of 16 up to 8192, 1 <= top_k <= 16, top_k <= experts <= 256");
+    GV_REQUIRE(M > 0 && H % 16 == 0 && H <= kPrefillFrontMaxH && E >= 1 && E + 1 <= 257 && K >= 1 && K <= 16 && K <= E,
+               "prefill front: M > 0, hidden a multiple of 16 up to 4096, 1 <= top_k <= 16, top_k <= experts <= 256");
     const int g = (M + 3) / 4;
     const size_t lds = std::max(static_cast<size_t>(5) * H * 4, static_cast<size_t>(4) * (E + 4) * 4);
     static int granted = 0;
