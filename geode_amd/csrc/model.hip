@@ -1505,8 +1505,8 @@ int moe_up_threads(const gv_model_config &c) {
 // variant; route_small's bounds: at most 8 picks a row, 256 experts; not a replay of one launch alone); otherwise the
 // fused launch keeps its route workgroup
 inline bool up_routes(const Model &m, bool mixout) {
-    return mixout && m.route_in_up && m.moe_dec && !m.replaying && m.c.top_k <= 8 && m.c.n_experts <= 256 &&
-           moe_up_threads(m.c) >= 64;
+    return (mixout || m.block_up_routes) && m.route_in_up && m.moe_dec && !m.replaying && m.c.top_k <= 8 &&
+           m.c.n_experts <= 256 && moe_up_threads(m.c) >= 64;
 }
 
 int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStream_t st) {
@@ -2807,8 +2807,13 @@ int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
     if (rc == 0 && given)                                  // the routed logits as given
         rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, pf.logits, static_cast<size_t>(m.E1) * 4,
                               static_cast<size_t>(E) * 4, M, hipMemcpyDeviceToDevice, st) == hipSuccess ? 0 : -1;
+    // at most kMaxRowsMixOut rows: the experts' up launch routes them from the logits (moe_up_kernel's route: the
+    // route launch's ids, weights and slots), no route launch
+    m.block_up_routes = M <= kMaxRowsMixOut;
+    const bool up_route = up_routes(m, false);
     for (int cls : {GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN})
-        if (rc == 0) rc = launch_class(m, cls, layer, M, st);
+        if (rc == 0 && !(cls == GV_K_ROUTE && up_route)) rc = launch_class(m, cls, layer, M, st);
+    m.block_up_routes = false;
     if (rc == 0) rc = launch_class(m, GV_K_COMBINE, layer, M, st);   // the block's output, no residual
     m.moe_only = false;
     return rc;
