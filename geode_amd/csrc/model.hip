@@ -1825,10 +1825,11 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         const int shared_dg = shared_only ? (m.E1 - 1) / kRouterRows : -1;
         const int n_dg = shared_only ? std::min(M, TG) + 1 : std::max((m.E1 + kRouterRows - 1) / kRouterRows, std::min(M, TG));
         const int wgs = n_dg * ((M + TG - 1) / TG);
+        const float *xr = m.moe_only && m.block_h ? m.block_h : m.x;   // (the MoE block's rows as given)
         if (H <= 2048) {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<1>), router_lds(H), granted) != 0) return -1;
-            hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
+            hipLaunchKernelGGL(router_kernel<1>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, xr,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
                                m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
                                m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg,
@@ -1836,7 +1837,7 @@ int launch_class(Model &m, int cls, int l, int M, hipStream_t st) {
         } else {
             static int granted = 0;
             if (lds_grant(reinterpret_cast<const void *>(&router_kernel<2>), router_lds(H), granted) != 0) return -1;
-            hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, m.x,
+            hipLaunchKernelGGL(router_kernel<2>, dim3(wgs), dim3(256), router_lds(H), st, L.router, m.E1, H, xr,
                                m.moe_only ? nullptr : L.post_norm, c.eps, m.sp, m.rlogits, m.act_h, abH,
                                m.route_in_router && !m.moe_only ? 1 : 0, c.n_experts, c.top_k, m.route + l,
                                m.route_ids + static_cast<int64_t>(l) * c.max_rows * c.top_k, m.counter, n_dg,
@@ -2799,10 +2800,11 @@ int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
     const int H = c.hidden, E = c.n_experts;
     if (M > c.max_rows) return moe_prefill(m, layer, M, st);
     Prefill &pf = m.pf;
-    GV_CHECK_HIP(hipMemcpyAsync(m.x, pf.h, static_cast<size_t>(M) * H * 4, hipMemcpyDeviceToDevice, st));
     m.moe_only = true;
     m.router_shared_only = given;
+    m.block_h = pf.h;   // (the router reads the rows where they are; the combine writes the block's output to x)
     int rc = launch_class(m, GV_K_ROUTER, layer, M, st);   // the shared expert's gate logit and the operands
+    m.block_h = nullptr;
     m.router_shared_only = false;
     if (rc == 0 && given)                                  // the routed logits as given
         rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, pf.logits, static_cast<size_t>(m.E1) * 4,

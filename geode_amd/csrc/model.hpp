@@ -135,6 +135,7 @@ struct Model {
     bool route_in_up = true;       // (fused) the experts' up launch routes the rows itself (gv_model_set_fused 2: off)
     bool router_shared_only = false;   // the MoE block's router launch with the routed logits given (gv_model_moe)
     bool block_up_routes = false;      // the MoE block's experts' up launch routes the rows itself (no route launch)
+    const float *block_h = nullptr;    // the MoE block's input rows, which its router reads in place of x
     int *ctr = nullptr;            // [n_layers][kFlagsPerLayer] the fused launches' flags (each launch clears its own)
     int *err = nullptr;            // set by a fused launch whose wait ran out (read back by gv_verify)
     uint64_t *trace = nullptr;     // gv_model_trace's stamps [GV_K_COUNT][8192 workgroups][8] (allocated when on)
