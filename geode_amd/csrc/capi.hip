@@ -43,7 +43,7 @@ int use_act_mode(int exact) {
     GV_CHECK_HIP(hipStreamSynchronize(stream()));
     GV_CHECK_HIP(hipDeviceSynchronize());
     if (act_mode_set_model(exact) != 0 || act_mode_set_q4(exact) != 0 || act_mode_set_gdn(exact) != 0 ||
-        act_mode_set_mtp(exact) != 0)
+        act_mode_set_mtp(exact) != 0 || act_mode_set_prefill(exact) != 0)
         return -1;
     GV_CHECK_HIP(hipDeviceSynchronize());
     rt().act_exact = exact;

@@ -62,6 +62,7 @@ int act_mode_set_model(int exact);
 int act_mode_set_q4(int exact);
 int act_mode_set_gdn(int exact);
 int act_mode_set_mtp(int exact);
+int act_mode_set_prefill(int exact);
 int use_act_mode(int exact);
 int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const GemvOut &out, hipStream_t st);
 // C1's dense FFN pieces: fp16 rows to operands; gate and up with the SwiGLU and its quantization (M <= 8)

@@ -105,6 +105,8 @@ __global__ __launch_bounds__(256) void group_fill_kernel(const int *__restrict__
 
 }  // namespace
 
+GV_ACT_MODE_SETTER(act_mode_set_prefill)
+
 int prefill_front(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, _Float16 *act,
                   int64_t act_stride, int *ids, float *w, float *gate, hipStream_t st) {
     GV_REQUIRE(M > 0 && H % 16 == 0 && H <= kPrefillFrontMaxH && E >= 1 && E + 1 <= 257 && K >= 1 && K <= 16 && K <= E,
