@@ -1990,10 +1990,10 @@ int moe_prefill(Model &m, int layer, int M, hipStream_t st) {
     Prefill &pf = m.pf;
     LayerW &L = m.layers[static_cast<size_t>(layer)];
     if (m.fused && H <= kPrefillFrontMaxH) {   // two launches (prefill.hip), the same outputs as the five below
-        if (prefill_front(L.router + static_cast<int64_t>(E) * H, H, pf.h, M, E, K, pf.logits, pf.act, act_halves(H),
-                          pf.ids, pf.w, pf.gate, st) != 0 ||
-            prefill_group(pf.ids, M, K, E, pf.start, pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count,
-                          pf.n_picks, pf.pick_token, pf.pick_of, st) != 0)
+        if (prefill_route(pf.logits, M, E, K, pf.ids, pf.w, st) != 0 ||
+            prefill_rest(L.router + static_cast<int64_t>(E) * H, H, pf.h, M, E, K, pf.logits, pf.gate, pf.act,
+                         act_halves(H), pf.ids, pf.start, pf.n_slots, pf.slot_expert, pf.slot_start, pf.slot_count,
+                         pf.n_picks, pf.pick_token, pf.pick_of, st) != 0)
             return -1;
     } else {
         if (quantize_act(pf.h, H, M, H, nullptr, 0.0f, pf.act, act_halves(H), nullptr, 0, st) != 0) return -1;

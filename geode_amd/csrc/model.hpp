@@ -197,14 +197,14 @@ int gdn_get_state(const Model &m, const LayerW &L, int slot, float *conv, float 
 // the verify step's launches (model.hip): one kernel class of layer l for M rows, and a layer's classes in order
 int run_class(Model &m, int cls, int l, int M, hipStream_t st);
 const int *layer_classes(int &count);
-// the prefill MoE's work before the experts' products in two launches (prefill.hip): the rows' shared-expert gate,
-// route and operands, then the picks grouped by expert and placed; hidden sizes up to kPrefillFrontMaxH (the gate
-// role's LDS, 20 bytes a hidden value, and the launch's own within a workgroup's 160 KB)
+// the prefill MoE's work before the experts' products in two launches (prefill.hip): the rows' routes, then the
+// picks grouped by expert and placed with the shared expert's gate and the rows' operands as roles of one launch;
+// hidden sizes up to kPrefillFrontMaxH (the gate role's LDS, 20 bytes a hidden value, within a workgroup's 160 KB)
 constexpr int kPrefillFrontMaxH = 4096;
-int prefill_front(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, _Float16 *act,
-                  int64_t act_stride, int *ids, float *w, float *gate, hipStream_t st);
-int prefill_group(const int *ids, int M, int K, int E, int *start, int *n_slots, int *slot_expert, int *slot_start,
-                  int *slot_count, int *n_picks, int *pick_token, int *pick_of, hipStream_t st);
+int prefill_route(const float *logits, int M, int E, int K, int *ids, float *w, hipStream_t st);
+int prefill_rest(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, float *gate,
+                 _Float16 *act, int64_t act_stride, const int *ids, int *start, int *n_slots, int *slot_expert,
+                 int *slot_start, int *slot_count, int *n_picks, int *pick_token, int *pick_of, hipStream_t st);
 // the MTP layer's buffers (mtp.hip), at gv_model_create
 int mtp_alloc(Model &m);
 void mtp_free(Model &m);      // the draft head
