@@ -2803,7 +2803,14 @@ int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
     m.moe_only = true;
     m.router_shared_only = given;
     m.block_h = pf.h;   // (the router reads the rows where they are; the combine writes the block's output to x)
-    int rc = launch_class(m, GV_K_ROUTER, layer, M, st);   // the shared expert's gate logit and the operands
+    // the shared expert's gate logit and the operands: with the routed logits given and at most kMaxRowsMixOut
+    // rows, prefill.hip's gate and operand roles (the router launch's values); else the router launch
+    int rc;
+    if (given && m.fused && M <= kMaxRowsMixOut && H <= kPrefillFrontMaxH)
+        rc = prefill_gate_ops(m.layers[static_cast<size_t>(layer)].router + static_cast<int64_t>(E) * H, H, pf.h, M, E,
+                              m.rlogits, pf.gate, m.act_h, act_halves(H), st);
+    else
+        rc = launch_class(m, GV_K_ROUTER, layer, M, st);
     m.block_h = nullptr;
     m.router_shared_only = false;
     if (rc == 0 && given)                                  // the routed logits as given

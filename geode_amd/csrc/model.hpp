@@ -205,6 +205,9 @@ int prefill_route(const float *logits, int M, int E, int K, int *ids, float *w, 
 int prefill_rest(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, float *gate,
                  _Float16 *act, int64_t act_stride, const int *ids, int *start, int *n_slots, int *slot_expert,
                  int *slot_start, int *slot_count, int *n_picks, int *pick_token, int *pick_of, hipStream_t st);
+// the same launch's gate and operand roles alone (the MoE block at up to 8 rows with its routed logits given)
+int prefill_gate_ops(const uint16_t *gate_row, int H, const float *h, int M, int E, float *logits, float *gate,
+                     _Float16 *act, int64_t act_stride, hipStream_t st);
 // the MTP layer's buffers (mtp.hip), at gv_model_create
 int mtp_alloc(Model &m);
 void mtp_free(Model &m);      // the draft head

@@ -79,18 +79,18 @@ __device__ void group_fill(const int *__restrict__ ids, int M, int K, int E, int
     fill_expert_picks(ids, M, K, E, e, start, o.pick_token, o.pick_of, wt);
 }
 
-// Three roles after the routes, g = ceil(M / 4), 256 threads:
+// Three roles after the routes, g = ceil(M / 4), G = E + 1 (or 0: no grouping), 256 threads:
 //   workgroups [0, g)                  the shared expert's gate logits (gate_row_logit, 4 rows a workgroup) to
 //                                      logits [t][E] and sigmoid(logit) to gate [t] (route_rows' arithmetic,
 //                                      model.cpp:4021-4065);
-//   workgroups [g, g + E + 1)          expert b - g's picks grouped and placed (group_fill);
-//   workgroups [g + E + 1, ... + M)    row t's operands for the products (norm_quant_row without a norm,
+//   workgroups [g, g + G)              expert b - g's picks grouped and placed (group_fill);
+//   workgroups [g + G, g + G + M)      row t's operands for the products (norm_quant_row without a norm,
 //                                      quantize_act's).
 __global__ __launch_bounds__(256) void prefill_rest_kernel(const uint16_t *__restrict__ wrow, int H,
                                                            const float *__restrict__ h, int M, int E, int K,
                                                            float *__restrict__ logits, float *__restrict__ gate,
                                                            _Float16 *__restrict__ act, int64_t act_stride,
-                                                           const int *__restrict__ ids, const GroupOut o) {
+                                                           const int *__restrict__ ids, const GroupOut o, int G) {
     extern __shared__ float pf_lds[];
     __shared__ double red[16];
     const int g = (M + 3) / 4, b = static_cast<int>(blockIdx.x);
@@ -102,10 +102,10 @@ __global__ __launch_bounds__(256) void prefill_rest_kernel(const uint16_t *__res
             logits[static_cast<int64_t>(t) * (E + 1) + E] = sg;
             gate[t] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-sg)));
         }
-    } else if (b < g + E + 1) {
+    } else if (b < g + G) {
         group_fill(ids, M, K, E, b - g, o);
     } else {
-        const int t = b - g - E - 1;
+        const int t = b - g - G;
         norm_quant_row(h + static_cast<int64_t>(t) * H, H, nullptr, 0.0f, act + static_cast<int64_t>(t) * act_stride,
                        nullptr, red);
     }
@@ -114,6 +114,8 @@ __global__ __launch_bounds__(256) void prefill_rest_kernel(const uint16_t *__res
 }  // namespace
 
 GV_ACT_MODE_SETTER(act_mode_set_prefill)
+
+static int g_rest_granted = 0;   // prefill_rest_kernel's dynamic LDS grant (both of its host entries)
 
 int prefill_route(const float *logits, int M, int E, int K, int *ids, float *w, hipStream_t st) {
     GV_REQUIRE(M > 0 && E >= 1 && E + 1 <= 257 && K >= 1 && K <= 16 && K <= E,
@@ -127,15 +129,29 @@ int prefill_route(const float *logits, int M, int E, int K, int *ids, float *w, 
 int prefill_rest(const uint16_t *gate_row, int H, const float *h, int M, int E, int K, float *logits, float *gate,
                  _Float16 *act, int64_t act_stride, const int *ids, int *start, int *n_slots, int *slot_expert,
                  int *slot_start, int *slot_count, int *n_picks, int *pick_token, int *pick_of, hipStream_t st) {
+    GV_REQUIRE(ids && start && n_slots && slot_expert && slot_start && slot_count && n_picks && pick_token && pick_of,
+               "prefill: the grouping's arrays");
     GV_REQUIRE(M > 0 && H % 16 == 0 && H <= kPrefillFrontMaxH && E >= 1 && E + 1 <= 257 && K >= 1 && K <= 16,
                "prefill: M > 0, hidden a multiple of 16 up to 4096, 1 <= top_k <= 16, experts <= 256");
     const int g = (M + 3) / 4;
     const size_t lds = static_cast<size_t>(5) * H * 4;   // the gate role's: the gate row and 4 rows as fp32
-    static int granted = 0;
-    if (lds_grant(reinterpret_cast<const void *>(&prefill_rest_kernel), lds, granted) != 0) return -1;
+    if (lds_grant(reinterpret_cast<const void *>(&prefill_rest_kernel), lds, g_rest_granted) != 0) return -1;
     const GroupOut o{start, n_slots, slot_expert, slot_start, slot_count, n_picks, pick_token, pick_of};
     hipLaunchKernelGGL(prefill_rest_kernel, dim3(static_cast<unsigned>(g + E + 1 + M)), dim3(256), lds, st, gate_row,
-                       H, h, M, E, K, logits, gate, act, act_stride, ids, o);
+                       H, h, M, E, K, logits, gate, act, act_stride, ids, o, E + 1);
+    GV_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+int prefill_gate_ops(const uint16_t *gate_row, int H, const float *h, int M, int E, float *logits, float *gate,
+                     _Float16 *act, int64_t act_stride, hipStream_t st) {
+    GV_REQUIRE(M > 0 && H % 16 == 0 && H <= kPrefillFrontMaxH && E >= 1 && E + 1 <= 257,
+               "gate and operands: M > 0, hidden a multiple of 16 up to 4096, experts <= 256");
+    const int g = (M + 3) / 4;
+    const size_t lds = static_cast<size_t>(5) * H * 4;
+    if (lds_grant(reinterpret_cast<const void *>(&prefill_rest_kernel), lds, g_rest_granted) != 0) return -1;
+    hipLaunchKernelGGL(prefill_rest_kernel, dim3(static_cast<unsigned>(g + M)), dim3(256), lds, st, gate_row, H, h, M,
+                       E, 0, logits, gate, act, act_stride, static_cast<const int *>(nullptr), GroupOut{}, 0);
     GV_CHECK_HIP(hipGetLastError());
     return 0;
 }

@@ -57,13 +57,13 @@ def test_c5_prefill_moe_at_its_shape(gv):
 
 @pytest.mark.parametrize("shape", [dict(), dict(n_experts=100, top_k=6), dict(exact=1)],
                          ids=["e256k8", "e100k6", "exact"])
-@pytest.mark.parametrize("M", [18, 37, 512, 1000])
+@pytest.mark.parametrize("M", [5, 8, 18, 37, 512, 1000])
 def test_c5_fused_front_matches_the_separate_launches(gv, shape, M):
-    """the prefill MoE's two launches before the products (the rows' shared-expert gate, route and operands as roles
-    of one launch, then the picks grouped and placed: prefill.hip) against the five separate ones
+    """the MoE block's launches before the experts' products (prefill.hip) against the separate ones
     (gv_model_set_fused(m, 0)): the block's output, routed ids and weights bit for bit, in both arithmetic modes (the
-    exact path's operands are the fp32 rows). M from just past the decode path's rows (max_rows 17) to 1,000 (a
-    ragged last group of four rows; two batches of picks to place)."""
+    exact path's operands are the fp32 rows). Past the decode path's rows (max_rows 17), up to 1,000 (a ragged last
+    group of four rows; two batches of picks to place): the routes, then the grouping with the shared expert's gate
+    and the operands, against five launches; at 5 and 8 rows: the gate and operand roles against the router launch."""
     cfg = dict(C5, **shape)
     gm = gv.VerifyModel(cfg)
     try:
