@@ -1525,7 +1525,7 @@ int moe_dec(const Model &m, const LayerW &L, int M, bool up, bool route, hipStre
     const int64_t l = &L - &m.layers[0];
     a.sl = route_slots(m.route + l);
     a.E1 = m.E1, a.max_picks = m.max_picks;
-    a.logits = m.rlogits, a.E = m.c.n_experts, a.K = m.c.top_k;
+    a.logits = m.block_logits ? m.block_logits : m.rlogits, a.E = m.c.n_experts, a.K = m.c.top_k;
     a.rs = m.route + l;
     a.ids_out = m.route_ids + l * m.c.max_rows * m.c.top_k;
     a.sp = m.sp;
@@ -2803,25 +2803,30 @@ int moe_block(Model &m, int layer, int M, bool given, hipStream_t st) {
     m.moe_only = true;
     m.router_shared_only = given;
     m.block_h = pf.h;   // (the router reads the rows where they are; the combine writes the block's output to x)
-    // the shared expert's gate logit and the operands: with the routed logits given and at most kMaxRowsMixOut
-    // rows, prefill.hip's gate and operand roles (the router launch's values); else the router launch
-    int rc;
-    if (given && m.fused && M <= kMaxRowsMixOut && H <= kPrefillFrontMaxH)
-        rc = prefill_gate_ops(m.layers[static_cast<size_t>(layer)].router + static_cast<int64_t>(E) * H, H, pf.h, M, E,
-                              m.rlogits, pf.gate, m.act_h, act_halves(H), st);
-    else
-        rc = launch_class(m, GV_K_ROUTER, layer, M, st);
-    m.block_h = nullptr;
-    m.router_shared_only = false;
-    if (rc == 0 && given)                                  // the routed logits as given
-        rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, pf.logits, static_cast<size_t>(m.E1) * 4,
-                              static_cast<size_t>(E) * 4, M, hipMemcpyDeviceToDevice, st) == hipSuccess ? 0 : -1;
     // at most kMaxRowsMixOut rows: the experts' up launch routes them from the logits (moe_up_kernel's route: the
     // route launch's ids, weights and slots), no route launch
     m.block_up_routes = M <= kMaxRowsMixOut;
     const bool up_route = up_routes(m, false);
+    // the shared expert's gate logit and the operands: with the routed logits given and routed by the up launch,
+    // prefill.hip's gate and operand roles (the router launch's values), the gate logit into the given rows' column
+    // E so that the up launch routes from those rows (no copy); else the router launch, then the given logits copied
+    // into its rows
+    const bool lean = given && up_route && m.fused && H <= kPrefillFrontMaxH;
+    int rc;
+    if (lean)
+        rc = prefill_gate_ops(m.layers[static_cast<size_t>(layer)].router + static_cast<int64_t>(E) * H, H, pf.h, M, E,
+                              pf.logits, pf.gate, m.act_h, act_halves(H), st);
+    else
+        rc = launch_class(m, GV_K_ROUTER, layer, M, st);
+    m.block_h = nullptr;
+    m.router_shared_only = false;
+    if (rc == 0 && given && !lean)                         // the routed logits as given
+        rc = hipMemcpy2DAsync(m.rlogits, static_cast<size_t>(m.E1) * 4, pf.logits, static_cast<size_t>(m.E1) * 4,
+                              static_cast<size_t>(E) * 4, M, hipMemcpyDeviceToDevice, st) == hipSuccess ? 0 : -1;
+    m.block_logits = lean ? pf.logits : nullptr;
     for (int cls : {GV_K_ROUTE, GV_K_MOE_UP, GV_K_SWIGLU, GV_K_MOE_DOWN})
         if (rc == 0 && !(cls == GV_K_ROUTE && up_route)) rc = launch_class(m, cls, layer, M, st);
+    m.block_logits = nullptr;
     m.block_up_routes = false;
     if (rc == 0) rc = launch_class(m, GV_K_COMBINE, layer, M, st);   // the block's output, no residual
     m.moe_only = false;

@@ -136,6 +136,7 @@ struct Model {
     bool router_shared_only = false;   // the MoE block's router launch with the routed logits given (gv_model_moe)
     bool block_up_routes = false;      // the MoE block's experts' up launch routes the rows itself (no route launch)
     const float *block_h = nullptr;    // the MoE block's input rows, which its router reads in place of x
+    const float *block_logits = nullptr;   // the MoE block's given logits rows, which its up launch routes from
     int *ctr = nullptr;            // [n_layers][kFlagsPerLayer] the fused launches' flags (each launch clears its own)
     int *err = nullptr;            // set by a fused launch whose wait ran out (read back by gv_verify)
     uint64_t *trace = nullptr;     // gv_model_trace's stamps [GV_K_COUNT][8192 workgroups][8] (allocated when on)
