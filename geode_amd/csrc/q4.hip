@@ -223,12 +223,22 @@ int quantize_act(const float *x, int64_t ldx, int M, int cols, const float *norm
 // PACK: at most 8 rows, their hi and lo halves in the MFMA's two column halves (mfma_tiles)
 // NT > 0 (a launch of at most NT tiles a workgroup): the tile loop straight-line, every tile's loads issued before
 // the first tile is computed (NT <= the ring's depth); 0: the ring of three over any number of tiles
-template <int KW, int NTT, int WMAX, bool PACK, int NT = 0>
+// RSPLIT: the M rows in gridDim.y groups of ceil(M / gridDim.y), group blockIdx.y's rows by this workgroup (each row's
+// sums as in a launch of its group alone)
+template <int KW, int NTT, int WMAX, bool PACK, int NT = 0, bool RSPLIT = false>
 __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16 *__restrict__ act,
                                                             int64_t act_stride, int M, int sc0, int tiles_per_wg,
                                                             GemvOut out) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
+    if constexpr (RSPLIT) {
+        const int mh = (M + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
+        const int r0 = static_cast<int>(blockIdx.y) * mh;
+        if (r0 >= M) return;   // (uniform)
+        act += static_cast<int64_t>(r0) * act_stride;
+        out.y += static_cast<int64_t>(r0) * out.ldy;
+        M = min(mh, M - r0);
+    }
     const int tc = out.trace_cls;
     if (tc >= 0) trace(tc, 0);
     const int64_t ntiles = tiles_rows(w.rows);
@@ -571,6 +581,24 @@ int gemv_q4(const Q4 &w, const _Float16 *act, int64_t act_stride, int M, const G
     GV_REQUIRE(w.cols % kSuperK == 0 && w.cols <= kMaxActCols, "gemv_q4: cols must be a multiple of 128, at most 16384");
     const int ntt = M <= 16 ? 1 : 2;
     const int nsc = static_cast<int>(w.cols / kSuperK);
+    if (ntt == 2 && nsc == 32) {   // 17..32 rows over K = 4096 (the tree's output projection), a few tiles: the rows in
+                                   // two groups of at most 16, each over the whole K in one range (the sums of an
+                                   // M <= 16 launch), both groups in one launch: twice the workgroups, each loading
+                                   // half the rows' operands
+        int waves, kw;
+        const int64_t ntiles = tiles_rows(w.rows);
+        if (mfma_split(32 * kSuperK, 1, waves, kw) && kw == 16 && waves == 8 && tiles_per_wg(ntiles, waves, 1) == 1) {
+            static int granted = 0;
+            if (lds_grant(reinterpret_cast<const void *>(&gemv_q4_kernel<16, 1, 8, false, 0, true>), 76 * 1024,
+                          granted) != 0)
+                return -1;
+            hipLaunchKernelGGL((gemv_q4_kernel<16, 1, 8, false, 0, true>), dim3(static_cast<unsigned>(ntiles), 2),
+                               dim3(64 * waves), static_cast<size_t>(waves) * 1024, st, w, act, act_stride, M, 0, 1,
+                               out);
+            GV_CHECK_HIP(hipGetLastError());
+            return 0;
+        }
+    }
     // K ranges whose activations fit the waves' registers: one launch up to 4096 (2048 for 17..32 rows) values,
     // later ranges adding to the first's sums
     if (ntt == 2 && nsc == 32) {   // two ranges of 2048 in one launch (kept parts, up to two tiles a workgroup)

@@ -103,9 +103,11 @@ def _rowptrs(a):
     return (ctypes.c_void_p * a.shape[0])(*[a[i].ctypes.data for i in range(a.shape[0])])
 
 
-@pytest.mark.parametrize("rows,cols,n", [(256, 512, 1), (1024, 2048, 5), (520, 6144, 37)])
+@pytest.mark.parametrize("rows,cols,n", [(256, 512, 1), (1024, 2048, 5), (520, 6144, 37), (2048, 4096, 17),
+                                         (256, 4096, 32)])
 def test_npu_gemm(gv, rows, cols, n):
-    """gnpu_gemm's contract (npu_api.h:42-44): ys[t] = W xs[t], fp32 rows in and out; n past 32 rows in batches"""
+    """gnpu_gemm's contract (npu_api.h:42-44): ys[t] = W xs[t], fp32 rows in and out; n past 32 rows in batches;
+    17..32 rows over K = 4096 (the rows in two groups of one launch)"""
     lib, h = _open(gv)
     try:
         wq, g = po.q4_random(50 + rows, rows, cols, 0.02)
