@@ -104,10 +104,10 @@ def _rowptrs(a):
 
 
 @pytest.mark.parametrize("rows,cols,n", [(256, 512, 1), (1024, 2048, 5), (520, 6144, 37), (2048, 4096, 17),
-                                         (256, 4096, 32)])
+                                         (256, 4096, 32), (9216, 2048, 17), (9000, 2048, 25)])
 def test_npu_gemm(gv, rows, cols, n):
     """gnpu_gemm's contract (npu_api.h:42-44): ys[t] = W xs[t], fp32 rows in and out; n past 32 rows in batches;
-    17..32 rows over K = 4096 (the rows in two groups of one launch)"""
+    17..32 rows over K = 4096 (the rows in two groups of one launch) and over K = 2048 (a ragged last tile)"""
     lib, h = _open(gv)
     try:
         wq, g = po.q4_random(50 + rows, rows, cols, 0.02)
