@@ -231,12 +231,13 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
                                                             GemvOut out) {
     extern __shared__ f4 part_lds[];
     __shared__ uint2 tab[256];
+    int r0 = 0;   // the first row of the workgroup's group (its outputs' row index offset; out itself is left as
+                  // passed: a copy of it would go to scratch, its segment arrays being indexed at run time)
     if constexpr (RSPLIT) {
         const int mh = (M + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
-        const int r0 = static_cast<int>(blockIdx.y) * mh;
+        r0 = static_cast<int>(blockIdx.y) * mh;
         if (r0 >= M) return;   // (uniform)
         act += static_cast<int64_t>(r0) * act_stride;
-        out.y += static_cast<int64_t>(r0) * out.ldy;
         M = min(mh, M - r0);
     }
     const int tc = out.trace_cls;
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
         int64_t row0;
         int j;
         item(min(o0, nt * NTT * 64 - 1), row0, j);
-        const float *p = out.y + min(j, M - 1) * out.ldy;
+        const float *p = out.y + (r0 + min(j, M - 1)) * out.ldy;
 #pragma unroll
         for (int r = 0; r < 4; ++r) old[r] = p[min(row0 + r, w.rows - 1)];   // (clamped: always a valid address)
     };
@@ -283,8 +284,8 @@ __global__ __launch_bounds__(64 * WMAX) void gemv_q4_kernel(Q4 w, const _Float16
         for (int r = 0; r < 4; ++r) {
             const int64_t row = row0 + r;
             if (row >= w.rows) break;
-            if (o == o0 && out.accumulate) out.y[j * out.ldy + row] = old[r] + out.scaled(row, sum[r]);
-            else out.put(row, j, sum[r]);
+            if (o == o0 && out.accumulate) out.y[(r0 + j) * out.ldy + row] = old[r] + out.scaled(row, sum[r]);
+            else out.put(row, r0 + j, sum[r]);
         }
     }
     if (tc >= 0) trace(tc, 3);
